@@ -1,0 +1,1665 @@
+// backend.hip - the C ABI of include/silvic_rocm.h on one MI355X (gfx950).
+//
+// One context owns one device, one stream (default priority) and the training data in its own layout:
+//   - slabs: runs of up to 128 non-trivial features stored as W-byte rows (W = 32, 64 or 128), the layout the
+//     histogram kernel reads (a scattered row of a 128-feature slab is one 128-byte line);
+//   - column-major bins (one byte per row per feature), which partition and add_tree read;
+//   - gradients, packed quantized gradients, two partition buffers and the per-leaf histogram pool.
+// Host code mirrors silvic-core's Backend, Learner and Trainer (file:line beside each function); every
+// histogram, subtraction, split scan, partition, quantization and score update runs on the device.
+
+#include "../../include/silvic_rocm.h"
+#include "kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+using namespace srocm;
+
+struct Failure : std::runtime_error {
+    int kind;
+    Failure(int k, const std::string &m) : std::runtime_error(m), kind(k) {}
+};
+
+[[noreturn]] void fail(int kind, const std::string &m) { throw Failure(kind, m); }
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) fail(SROCM_ERR_DEVICE, std::string("hip ") + what + ": " + hipGetErrorString(e));
+}
+
+void launch_check(const char *what) { hip_check(hipGetLastError(), what); }
+
+template <typename T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : p(o.p), n(o.n) {
+        o.p = nullptr;
+        o.n = 0;
+    }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        release();
+        p = o.p;
+        n = o.n;
+        o.p = nullptr;
+        o.n = 0;
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void alloc(size_t count) {
+        if (p && count <= n) return;
+        release();
+        hip_check(hipMalloc(reinterpret_cast<void **>(&p), std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc");
+        n = count;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+template <typename T>
+struct Pinned {
+    T *p = nullptr;
+    size_t n = 0;
+    Pinned() = default;
+    Pinned(const Pinned &) = delete;
+    Pinned &operator=(const Pinned &) = delete;
+    ~Pinned() { release(); }
+    void alloc(size_t count) {
+        if (p && count <= n) return;
+        release();
+        hip_check(hipHostMalloc(reinterpret_cast<void **>(&p), std::max<size_t>(count, 1) * sizeof(T), hipHostMallocDefault),
+                  "hipHostMalloc");
+        n = count;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------------------------------------
+// Host restatements the driver needs (quantize.rs, split.rs, tree.rs)
+// ---------------------------------------------------------------------------------------------------------
+
+inline uint32_t mix32_h(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352dU;
+    x ^= x >> 15;
+    x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return x;
+}
+
+inline float uniform_h(uint32_t seed, uint32_t stream, uint32_t iteration, uint64_t row) {
+    uint32_t row_hash = mix32_h(static_cast<uint32_t>(row) ^ mix32_h(static_cast<uint32_t>(row >> 32)));
+    uint32_t h = mix32_h(seed ^ mix32_h(stream ^ mix32_h(iteration ^ row_hash)));
+    return static_cast<float>(h >> 8) * (1.0f / 16777216.0f);
+}
+
+inline int64_t sat_i64_h(double x) {
+    if (std::isnan(x)) return 0;
+    if (x >= 9223372036854775807.0) return std::numeric_limits<int64_t>::max();
+    if (x <= -9223372036854775808.0) return std::numeric_limits<int64_t>::min();
+    return static_cast<int64_t>(x);
+}
+
+inline double positive_or_one(double v) { return (v > 0.0 && std::isfinite(v)) ? v : 1.0; }
+
+// quantize.rs:56-84
+srocm_quant_spec make_quant_spec(double max_abs_grad, double max_hess, bool constant_hessian, double constant,
+                                 uint32_t num_bins, bool stochastic, uint32_t seed, uint32_t iteration) {
+    srocm_quant_spec s{};
+    s.grad_max_q = static_cast<int32_t>(num_bins / 2);
+    s.hess_max_q = static_cast<int32_t>(num_bins);
+    s.grad_scale = positive_or_one(max_abs_grad / static_cast<double>(s.grad_max_q));
+    s.hess_scale = constant_hessian ? positive_or_one(constant) : positive_or_one(max_hess / static_cast<double>(s.hess_max_q));
+    s.inv_grad_scale = static_cast<float>(1.0 / s.grad_scale);
+    s.inv_hess_scale = static_cast<float>(1.0 / s.hess_scale);
+    s.constant_hessian = constant_hessian;
+    s.stochastic = stochastic;
+    s.seed = seed;
+    s.iteration = iteration;
+    return s;
+}
+
+// quantize.rs:153-159
+float fixed_point_scale(double max_abs) {
+    if (!std::isfinite(max_abs) || max_abs <= 0.0) return 1.0f;
+    int32_t e = 30 - static_cast<int32_t>(sat_i64_h(std::ceil(std::log2(max_abs))));
+    e = std::clamp(e, -126, 127);
+    return std::ldexp(1.0f, e);
+}
+
+// split.rs:145-154, 190-192
+inline double leaf_output_h(double g, double h, double l1, double l2) {
+    double reg = std::fmax(std::fabs(g) - l1, 0.0);
+    double sign = static_cast<double>(static_cast<int>(g > 0.0) - static_cast<int>(g < 0.0));
+    return -(sign * reg) / (h + l2);
+}
+
+inline int total_cmp_f(float a, float b) {
+    int32_t x, y;
+    std::memcpy(&x, &a, 4);
+    std::memcpy(&y, &b, 4);
+    x ^= static_cast<int32_t>(static_cast<uint32_t>(x >> 31) >> 1);
+    y ^= static_cast<int32_t>(static_cast<uint32_t>(y >> 31) >> 1);
+    return (x > y) - (x < y);
+}
+
+constexpr double K_EPS_H = static_cast<double>(1e-15f);
+constexpr double ZERO_THRESHOLD = static_cast<double>(1e-35f);  // tree.rs:13
+inline double nan_to_zero(double v) { return std::isnan(v) ? 0.0 : v; }
+inline double round_to_zero(double v) { return std::fabs(v) > ZERO_THRESHOLD ? v : 0.0; }
+
+// tree.rs:46-203, thresholds as bins
+struct HostTree {
+    uint32_t num_leaves = 1;
+    std::vector<int32_t> split_feature, left_child, right_child;
+    std::vector<uint32_t> threshold_bin;
+    std::vector<uint8_t> default_left;
+    std::vector<float> split_gain;
+    std::vector<double> internal_value, internal_weight;
+    std::vector<int64_t> internal_count;
+    std::vector<double> leaf_value{0.0}, leaf_weight{0.0};
+    std::vector<int64_t> leaf_count{0};
+    std::vector<int32_t> leaf_parent{-1}, leaf_depth{0};
+
+    // tree.rs:143-177
+    uint32_t split(uint32_t leaf, int32_t feature, uint32_t threshold, bool dl, double lv, double rv, int64_t lc,
+                   int64_t rc, double lw, double rw, float gain) {
+        int32_t node = static_cast<int32_t>(num_leaves - 1);
+        uint32_t new_leaf = num_leaves;
+        int32_t parent = leaf_parent[leaf];
+        if (parent >= 0) {
+            if (left_child[parent] == ~static_cast<int32_t>(leaf)) left_child[parent] = node;
+            else right_child[parent] = node;
+        }
+        split_feature.push_back(feature);
+        split_gain.push_back(gain);
+        threshold_bin.push_back(threshold);
+        default_left.push_back(dl ? 1 : 0);
+        left_child.push_back(~static_cast<int32_t>(leaf));
+        right_child.push_back(~static_cast<int32_t>(new_leaf));
+        internal_weight.push_back(leaf_weight[leaf]);
+        internal_value.push_back(leaf_value[leaf]);
+        internal_count.push_back(lc + rc);
+        leaf_value[leaf] = nan_to_zero(lv);
+        leaf_weight[leaf] = lw;
+        leaf_count[leaf] = lc;
+        leaf_value.push_back(nan_to_zero(rv));
+        leaf_weight.push_back(rw);
+        leaf_count.push_back(rc);
+        leaf_parent[leaf] = node;
+        leaf_parent.push_back(node);
+        int32_t depth = leaf_depth[leaf] + 1;
+        leaf_depth[leaf] = depth;
+        leaf_depth.push_back(depth);
+        ++num_leaves;
+        return new_leaf;
+    }
+    void shrink(double rate) {  // tree.rs:180-185
+        for (double &v : leaf_value) v = round_to_zero(v * rate);
+        for (double &v : internal_value) v = round_to_zero(v * rate);
+    }
+    void add_bias(double bias) {  // tree.rs:188-193
+        for (double &v : leaf_value) v = round_to_zero(v + bias);
+        for (double &v : internal_value) v = round_to_zero(v + bias);
+    }
+};
+
+// ---------------------------------------------------------------------------------------------------------
+// The context
+// ---------------------------------------------------------------------------------------------------------
+
+constexpr uint32_t MAX_SLAB_FEATURES = 128;
+constexpr uint32_t HIST_MIN_ROWS = 4096;   // rows per histogram workgroup before another one is used
+constexpr uint64_t ROW_BLOCK = 256;
+
+struct Slab {
+    uint32_t width = 0;
+    std::vector<uint32_t> feats;  // feature ids
+    DevBuf<uint8_t> bins;         // [rows][width]
+    DevBuf<uint32_t> col_offset, col_bins;
+};
+
+struct DevData {
+    uint64_t rows = 0;
+    DevBuf<uint8_t> col;  // [nt feature][rows]
+    DevBuf<float> scores;
+};
+
+struct Profile {
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> hist_events, part_events;
+    double hist_launches = 0, hist_builds = 0, hist_rows = 0, hist_bins = 0, hist_bytes = 0, part_launches = 0, part_rows = 0;
+    double hist_ms = 0, part_ms = 0;
+    std::vector<hipEvent_t> pool;
+};
+
+struct GrowLeaf {
+    srocm_leaf_range range{};
+    double ug = 0.0, uh = 0.0;
+    int64_t count = 0;
+    int slot = -1;  // device histogram slot, -1: none
+    std::vector<uint8_t> splittable;
+    bool has_best = false;
+    SplitOut best{};
+};
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string error;
+    std::string device_name;
+    uint32_t cus = 256;
+    bool loaded = false;
+
+    // layout
+    uint32_t nf = 0;
+    std::vector<srocm_feature> feats;
+    uint64_t total_bins = 0;
+    std::vector<std::vector<int32_t>> group_col_nt;
+    std::vector<int32_t> feat_nt;
+    std::vector<uint32_t> nt_feat;
+    std::vector<Slab> slabs;
+    uint64_t rows = 0, row_offset = 0;
+    uint32_t max_width = 32;
+
+    DevData train;
+    std::vector<DevData> valid;
+    DevBuf<float> label, weight, grad, hess;
+    bool has_weight = false;
+    std::vector<float> h_label_v, h_weight_v;
+    DevBuf<int32_t> packed, partial;
+    DevBuf<uint32_t> part, part2, block_left, scalars;
+    DevBuf<FeatDev> dfeats;
+    uint32_t part_len = 0;
+    std::vector<uint8_t> used;
+    uint32_t objective = SROCM_OBJ_REGRESSION;
+    double sigmoid = 1.0;
+    int64_t max_quant = 1;
+    bool quantized_once = false;
+
+    Pinned<float> h_scores, h_grad, h_hess;
+    Pinned<int64_t> h_hist;
+    Pinned<uint32_t> h_u32;
+    Pinned<uint8_t> h_result;
+    Pinned<uint8_t> h_stage;  // per-split uploads (jobs, evaluate flags), rewritten only after a sync
+
+    std::vector<DevBuf<int64_t>> slots;
+    std::vector<int> spare;
+    DevBuf<ScanJob> d_jobs;
+    DevBuf<FeatCand> d_cands;
+    DevBuf<SplitOut> d_split;
+    DevBuf<uint8_t> d_splittable, d_eval;
+    DevBuf<DevNode> d_nodes;
+    DevBuf<float> d_leaf_values;
+    DevBuf<LeafJob> d_leaf_jobs;
+    DevBuf<unsigned long long> d_leaf_out;
+
+    Profile prof;
+
+    ~Context() {
+        for (auto &e : prof.hist_events) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        for (auto &e : prof.part_events) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        for (auto e : prof.pool) (void)hipEventDestroy(e);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void sync() { hip_check(hipStreamSynchronize(stream), "stream synchronize"); }
+
+    void require_loaded() const {
+        if (!loaded) fail(SROCM_ERR_DEVICE, "rocm backend used before load");
+    }
+
+    hipEvent_t event() {
+        if (!prof.pool.empty()) {
+            hipEvent_t e = prof.pool.back();
+            prof.pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        hip_check(hipEventCreate(&e), "hipEventCreate");
+        return e;
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // load (cpu.rs:707-746 checks; device layout)
+    // ------------------------------------------------------------------------------------------------
+
+    void load(const srocm_dataset *t, const srocm_dataset *const *v, uint32_t nv, const srocm_objective *obj) {
+        if (!t || !obj) fail(SROCM_ERR_DATA, "load needs a training set and an objective");
+        if (t->num_rows > 0xFFFFFFFFull) fail(SROCM_ERR_UNSUPPORTED, std::to_string(t->num_rows) + " rows on one rank; the limit is 2^32 - 1");
+        if (obj->kind == SROCM_OBJ_LAMBDARANK) {
+            // gradients arrive through srocm_set_gradients
+        } else if (obj->kind != SROCM_OBJ_REGRESSION && obj->kind != SROCM_OBJ_BINARY) {
+            fail(SROCM_ERR_CONFIG, "unknown objective");
+        }
+        auto check_layout = [&](const srocm_dataset *d) {
+            if (d->num_groups != t->num_groups || d->num_features != t->num_features)
+                fail(SROCM_ERR_DATA, "validation set binned with a different layout than the training set");
+            for (uint32_t g = 0; g < d->num_groups; ++g)
+                if (!d->groups[g].data && d->num_rows) fail(SROCM_ERR_DATA, "group without data");
+        };
+        for (uint32_t i = 0; i < nv; ++i) check_layout(v[i]);
+        loaded = false;
+        nf = t->num_features;
+        feats.assign(t->features, t->features + nf);
+        total_bins = t->total_bins;
+        rows = t->num_rows;
+        row_offset = t->row_offset;
+        objective = obj->kind;
+        sigmoid = obj->sigmoid;
+        // feature checks (cpu.rs:178-223) and the column-major order of non-trivial features
+        feat_nt.assign(nf, -1);
+        nt_feat.clear();
+        group_col_nt.assign(t->num_groups, {});
+        for (uint32_t g = 0; g < t->num_groups; ++g) group_col_nt[g].assign(t->groups[g].row_stride, -1);
+        uint64_t bins_seen = 0;
+        for (uint32_t f = 0; f < nf; ++f) {
+            const srocm_feature &m = feats[f];
+            if (m.num_bins == 0) continue;
+            if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
+            if (m.kind != SROCM_BINS_NUMERICAL && m.kind != SROCM_BINS_CATEGORICAL) fail(SROCM_ERR_DATA, "bad feature kind");
+            if (m.group >= t->num_groups) fail(SROCM_ERR_DATA, "feature in a missing group");
+            const srocm_group &g = t->groups[m.group];
+            if (m.column >= g.row_stride || m.hist_offset < g.hist_offset ||
+                m.hist_offset - g.hist_offset + m.num_bins > g.total_bins || m.hist_offset + m.num_bins > total_bins)
+                fail(SROCM_ERR_DATA, "feature " + std::to_string(f) + " lies outside its group's bins or row");
+            feat_nt[f] = static_cast<int32_t>(nt_feat.size());
+            group_col_nt[m.group][m.column] = feat_nt[f];
+            nt_feat.push_back(f);
+            bins_seen += m.num_bins;
+        }
+        (void)bins_seen;
+        // slabs: consecutive non-trivial features, up to 128 per slab
+        slabs.clear();
+        max_width = 32;
+        for (size_t i = 0; i < nt_feat.size(); i += MAX_SLAB_FEATURES) {
+            Slab s;
+            size_t end = std::min(nt_feat.size(), i + MAX_SLAB_FEATURES);
+            s.feats.assign(nt_feat.begin() + static_cast<long>(i), nt_feat.begin() + static_cast<long>(end));
+            uint32_t n = static_cast<uint32_t>(s.feats.size());
+            s.width = n <= 32 ? 32 : (n <= 64 ? 64 : 128);
+            max_width = std::max(max_width, s.width);
+            slabs.push_back(std::move(s));
+        }
+        // device buffers
+        train = DevData{};
+        upload_bins(t, train, true);
+        valid.clear();
+        for (uint32_t i = 0; i < nv; ++i) {
+            DevData d;
+            upload_bins(v[i], d, false);
+            valid.push_back(std::move(d));
+        }
+        label.alloc(rows);
+        h_label_v.assign(t->label, t->label + rows);
+        hip_check(hipMemcpy(label.p, t->label, rows * sizeof(float), hipMemcpyHostToDevice), "upload label");
+        has_weight = t->weight != nullptr;
+        h_weight_v.clear();
+        if (has_weight) {
+            weight.alloc(rows);
+            h_weight_v.assign(t->weight, t->weight + rows);
+            hip_check(hipMemcpy(weight.p, t->weight, rows * sizeof(float), hipMemcpyHostToDevice), "upload weight");
+        }
+        grad.alloc(rows);
+        hess.alloc(rows);
+        packed.alloc(rows);
+        part.alloc(rows);
+        part2.alloc(rows);
+        block_left.alloc(cus * 4 + 16);
+        scalars.alloc(16);
+        partial.alloc(static_cast<size_t>(cus) * 256 * max_width * 2);
+        std::vector<FeatDev> fd(nf);
+        for (uint32_t f = 0; f < nf; ++f) fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin};
+        dfeats.alloc(nf);
+        hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
+        for (auto &s : slabs) {
+            std::vector<uint32_t> off(s.width, 0), nb(s.width, 0);
+            for (size_t c = 0; c < s.feats.size(); ++c) {
+                off[c] = feats[s.feats[c]].hist_offset;
+                nb[c] = feats[s.feats[c]].num_bins;
+            }
+            s.col_offset.alloc(s.width);
+            s.col_bins.alloc(s.width);
+            hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
+            hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
+        }
+        used.assign(nf, 1);
+        part_len = 0;
+        max_quant = 1;
+        quantized_once = false;
+        slots.clear();
+        spare.clear();
+        sync();
+        loaded = true;
+    }
+
+    // Repacks a dataset's groups into slab rows (training set) and column-major bins, on the device.
+    void upload_bins(const srocm_dataset *d, DevData &out, bool with_slabs) {
+        out.rows = d->num_rows;
+        uint64_t n = d->num_rows;
+        out.col.alloc(std::max<uint64_t>(1, nt_feat.size() * n));
+        out.scores.alloc(std::max<uint64_t>(n, 1));
+        hip_check(hipMemsetAsync(out.scores.p, 0, std::max<uint64_t>(n, 1) * sizeof(float), stream), "zero scores");
+        if (with_slabs)
+            for (auto &s : slabs) {
+                s.bins.alloc(std::max<uint64_t>(1, n * s.width));
+                hip_check(hipMemsetAsync(s.bins.p, 0, std::max<uint64_t>(1, n * s.width), stream), "zero slab");
+            }
+        if (n == 0) return;
+        DevBuf<uint8_t> staging;
+        for (uint32_t g = 0; g < d->num_groups; ++g) {
+            const srocm_group &grp = d->groups[g];
+            uint64_t bytes = n * grp.row_stride;
+            staging.alloc(bytes);
+            hip_check(hipMemcpyAsync(staging.p, grp.data, bytes, hipMemcpyHostToDevice, stream), "upload group");
+            for (uint32_t c = 0; c < grp.row_stride; ++c) {
+                int32_t nt = group_col_nt[g][c];
+                if (nt < 0) continue;
+                uint32_t f = nt_feat[nt];
+                uint8_t *slab_bins = nullptr;
+                uint32_t width = 0, slab_col = 0;
+                if (with_slabs) {
+                    uint32_t s = static_cast<uint32_t>(nt) / MAX_SLAB_FEATURES;
+                    slab_bins = slabs[s].bins.p;
+                    width = slabs[s].width;
+                    slab_col = static_cast<uint32_t>(nt) % MAX_SLAB_FEATURES;
+                }
+                (void)f;
+                repack(staging.p, grp.row_stride, c, n, out.col.p + static_cast<size_t>(nt) * n, slab_bins, width, slab_col);
+            }
+            sync();  // staging is reused
+        }
+    }
+
+    void repack(const uint8_t *src, uint32_t stride, uint32_t column, uint64_t n, uint8_t *col, uint8_t *slab,
+                uint32_t width, uint32_t slab_col);
+
+    // ------------------------------------------------------------------------------------------------
+    // gradients, quantization, partition reset
+    // ------------------------------------------------------------------------------------------------
+
+    std::pair<double, double> read_maxima() {
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p + 1, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream), "read maxima");
+        sync();
+        float g, h;
+        std::memcpy(&g, &h_u32.p[0], 4);
+        std::memcpy(&h, &h_u32.p[1], 4);
+        return {static_cast<double>(g), static_cast<double>(h)};
+    }
+
+    uint32_t grid_rows(uint64_t n) const { return static_cast<uint32_t>(std::min<uint64_t>(std::max<uint64_t>(div_up(n, 256), 1), cus * 8ull)); }
+
+    std::pair<double, double> compute_gradients();
+
+    std::pair<double, double> set_gradients(const float *g, const float *h, uint64_t n) {
+        require_loaded();
+        if (n != rows) fail(SROCM_ERR_DEVICE, "gradient arrays of " + std::to_string(n) + " rows, expected " + std::to_string(rows));
+        hip_check(hipMemcpyAsync(grad.p, g, n * 4, hipMemcpyHostToDevice, stream), "upload grad");
+        hip_check(hipMemcpyAsync(hess.p, h, n * 4, hipMemcpyHostToDevice, stream), "upload hess");
+        hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
+        k_max_abs<<<grid_rows(n), 256, 0, stream>>>(grad.p, hess.p, n, scalars.p + 1);
+        launch_check("k_max_abs");
+        return read_maxima();
+    }
+
+    void quantize(const srocm_quant_spec &s) {
+        require_loaded();
+        QuantDev q{s.inv_grad_scale, s.inv_hess_scale, s.grad_max_q, s.hess_max_q, s.constant_hessian, s.stochastic, s.seed, s.iteration};
+        if (rows) {
+            k_quantize<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, q);
+            launch_check("k_quantize");
+        }
+        max_quant = std::max(s.grad_max_q, s.hess_max_q);
+        quantized_once = true;
+    }
+
+    uint32_t reset_partition(const srocm_bag &bag) {
+        require_loaded();
+        if (rows == 0) {
+            part_len = 0;
+            return 0;
+        }
+        k_iota<<<grid_rows(rows), 256, 0, stream>>>(part.p, rows);
+        launch_check("k_iota");
+        if (bag.kind == SROCM_BAG_ALL) {
+            part_len = static_cast<uint32_t>(rows);
+            return part_len;
+        }
+        if (bag.kind != SROCM_BAG_BERNOULLI) fail(SROCM_ERR_CONFIG, "unknown bag kind");
+        // a stable compaction: the in-bag rows, ascending (cpu.rs:816-823)
+        PartArgs a = part_args(0, static_cast<uint32_t>(rows));
+        a.col = nullptr;
+        a.bag_seed = bag.seed;
+        a.bag_round = bag.round;
+        a.row_offset = row_offset;
+        a.fraction = bag.fraction;
+        run_partition(a, static_cast<uint32_t>(rows));
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read bag count");
+        sync();
+        part_len = h_u32.p[0];
+        return part_len;
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // histograms
+    // ------------------------------------------------------------------------------------------------
+
+    uint32_t flush_rows() const { return static_cast<uint32_t>(32767 / std::max<int64_t>(max_quant, 1)); }
+
+    uint32_t hist_groups(uint64_t n) const {
+        uint32_t want = div_up(std::max<uint64_t>(n, 1), HIST_MIN_ROWS);
+        return std::max<uint32_t>(1, std::min<uint32_t>(want, cus));
+    }
+
+    // The histogram of rows part[begin..+count] (or the `side` child of that range split at *dev_left) into
+    // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
+    void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
+                     int64_t *parent, uint64_t bins_used) {
+        uint32_t grid = hist_groups(count);
+        for (auto &s : slabs) {
+            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
+            hipEvent_t e0 = nullptr, e1 = nullptr;
+            if (prof.on) {
+                e0 = event();
+                e1 = event();
+                hip_check(hipEventRecord(e0, stream), "event");
+            }
+            switch (s.width) {
+            case 32: k_hist<32><<<grid, 1024, 0, stream>>>(a); break;
+            case 64: k_hist<64><<<grid, 1024, 0, stream>>>(a); break;
+            default: k_hist<128><<<grid, 1024, 0, stream>>>(a); break;
+            }
+            launch_check("k_hist");
+            if (prof.on) {
+                hip_check(hipEventRecord(e1, stream), "event");
+                prof.hist_events.emplace_back(e0, e1);
+                prof.hist_launches += 1;
+            }
+            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
+            k_hist_reduce<<<div_up(256ull * s.width, 256), 256, 0, stream>>>(r);
+            launch_check("k_hist_reduce");
+        }
+        if (prof.on) {
+            prof.hist_builds += 1;
+            if (!dev_left) {
+                prof.hist_rows += count;
+                prof.hist_bins += static_cast<double>(count) * static_cast<double>(bins_used);
+            }
+        }
+    }
+
+    uint64_t used_columns() const {
+        uint64_t n = 0;
+        for (uint32_t f = 0; f < nf; ++f)
+            if (used[f] && feats[f].num_bins) ++n;
+        return n;
+    }
+
+    void check_range(srocm_leaf_range leaf) const {
+        uint64_t end = static_cast<uint64_t>(leaf.begin) + leaf.count;
+        if (end > part_len)
+            fail(SROCM_ERR_DEVICE, "leaf rows " + std::to_string(leaf.begin) + ".." + std::to_string(end) +
+                                       " outside the partition of " + std::to_string(part_len) + " rows");
+    }
+
+    DevBuf<int64_t> tmp_hist;
+
+    void histogram_to_host(double *out) {
+        hip_check(hipMemcpyAsync(h_hist.p, tmp_hist.p, 2 * total_bins * sizeof(int64_t), hipMemcpyDeviceToHost, stream), "read histogram");
+    }
+
+    void histogram(srocm_leaf_range leaf, int quantized, double *out, size_t len) {
+        require_loaded();
+        check_range(leaf);
+        if (!quantized) fail(SROCM_ERR_UNSUPPORTED, "float-mode histograms run on the cpu backend only");
+        if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
+        if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
+        tmp_hist.alloc(2 * total_bins);
+        h_hist.alloc(2 * total_bins);
+        if (leaf.count == 0) {
+            std::fill(out, out + len, 0.0);
+            return;
+        }
+        launch_hist(leaf.begin, leaf.count, nullptr, 0, tmp_hist.p, nullptr, used_columns());
+        histogram_to_host(out);
+        sync();
+        for (size_t i = 0; i < len; ++i) out[i] = static_cast<double>(h_hist.p[i]);
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // partition
+    // ------------------------------------------------------------------------------------------------
+
+    PartArgs part_args(uint32_t begin, uint32_t count) {
+        PartArgs a{};
+        a.src = part.p;
+        a.dst = part2.p;
+        a.block_left = block_left.p;
+        a.dev_left = scalars.p;
+        a.begin = begin;
+        a.count = count;
+        uint32_t per = div_up(count, cus * 4ull);
+        per = std::max<uint32_t>(256, (per + 255) / 256 * 256);
+        a.per_block = per;
+        return a;
+    }
+
+    void run_partition(const PartArgs &a, uint32_t count) {
+        uint32_t grid = std::max<uint32_t>(1, div_up(count, a.per_block));
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (prof.on) {
+            e0 = event();
+            e1 = event();
+            hip_check(hipEventRecord(e0, stream), "event");
+        }
+        k_part_count<<<grid, 256, 0, stream>>>(a);
+        launch_check("k_part_count");
+        k_part_scatter<<<grid, 256, 0, stream>>>(a);
+        launch_check("k_part_scatter");
+        k_copy_u32<<<std::max<uint32_t>(1, std::min<uint32_t>(div_up(count, 256), cus * 8)), 256, 0, stream>>>(part2.p, part.p, a.begin, count);
+        launch_check("k_copy_u32");
+        if (prof.on) {
+            hip_check(hipEventRecord(e1, stream), "event");
+            prof.part_events.emplace_back(e0, e1);
+            prof.part_launches += 1;
+            prof.part_rows += count;
+        }
+    }
+
+    // Enqueues the stable partition of `leaf` by `split`; the left count lands in scalars[0].
+    void enqueue_partition(srocm_leaf_range leaf, const srocm_bin_split &split) {
+        if (split.group >= group_col_nt.size()) fail(SROCM_ERR_DEVICE, "split on missing group " + std::to_string(split.group));
+        if (split.column >= group_col_nt[split.group].size() || group_col_nt[split.group][split.column] < 0)
+            fail(SROCM_ERR_DEVICE, "split on a column without a feature");
+        int32_t nt = group_col_nt[split.group][split.column];
+        if (leaf.count == 0) {
+            hip_check(hipMemsetAsync(scalars.p, 0, 4, stream), "zero left");
+            return;
+        }
+        PartArgs a = part_args(leaf.begin, leaf.count);
+        a.col = train.col.p + static_cast<size_t>(nt) * rows;
+        std::memcpy(a.left_bins, split.left_bins, sizeof(a.left_bins));
+        run_partition(a, leaf.count);
+    }
+
+    uint32_t partition(srocm_leaf_range leaf, const srocm_bin_split &split) {
+        require_loaded();
+        check_range(leaf);
+        enqueue_partition(leaf, split);
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
+        sync();
+        return h_u32.p[0];
+    }
+
+    uint32_t partition_and_histogram(srocm_leaf_range leaf, const srocm_bin_split &split, uint32_t side, int quantized,
+                                     double *out, size_t len) {
+        require_loaded();
+        check_range(leaf);
+        if (!quantized) fail(SROCM_ERR_UNSUPPORTED, "float-mode histograms run on the cpu backend only");
+        if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
+        if (side > 1) fail(SROCM_ERR_DEVICE, "bad side");
+        tmp_hist.alloc(2 * total_bins);
+        h_hist.alloc(2 * total_bins);
+        enqueue_partition(leaf, split);
+        if (leaf.count) launch_hist(leaf.begin, leaf.count, scalars.p, side, tmp_hist.p, nullptr, used_columns());
+        else hip_check(hipMemsetAsync(tmp_hist.p, 0, 2 * total_bins * 8, stream), "zero histogram");
+        histogram_to_host(out);
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
+        sync();
+        for (size_t i = 0; i < len; ++i) out[i] = static_cast<double>(h_hist.p[i]);
+        return h_u32.p[0];
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // leaf sums, add_tree, scores
+    // ------------------------------------------------------------------------------------------------
+
+    void leaf_sums(const srocm_leaf_range *leaves, uint32_t n, float gs, float hs, int64_t *out) {
+        require_loaded();
+        for (uint32_t i = 0; i < n; ++i) check_range(leaves[i]);
+        if (n == 0) return;
+        std::vector<LeafJob> jobs(n);
+        uint32_t maxc = 0;
+        for (uint32_t i = 0; i < n; ++i) {
+            jobs[i] = LeafJob{leaves[i].begin, leaves[i].count, i};
+            maxc = std::max(maxc, leaves[i].count);
+        }
+        d_leaf_jobs.alloc(n);
+        d_leaf_out.alloc(2 * n);
+        hip_check(hipMemcpyAsync(d_leaf_jobs.p, jobs.data(), n * sizeof(LeafJob), hipMemcpyHostToDevice, stream), "upload leaves");
+        hip_check(hipMemsetAsync(d_leaf_out.p, 0, 2 * n * 8, stream), "zero sums");
+        uint32_t chunk = 8192;
+        dim3 grid(std::max<uint32_t>(1, div_up(maxc, chunk)), n);
+        k_leaf_sums<<<grid, 256, 0, stream>>>(grad.p, hess.p, part.p, d_leaf_jobs.p, gs, hs, d_leaf_out.p, chunk);
+        launch_check("k_leaf_sums");
+        Pinned<unsigned long long> h;
+        h.alloc(2 * n);
+        hip_check(hipMemcpyAsync(h.p, d_leaf_out.p, 2 * n * 8, hipMemcpyDeviceToHost, stream), "read sums");
+        sync();
+        for (uint32_t i = 0; i < 2 * n; ++i) out[i] = static_cast<int64_t>(h.p[i]);
+    }
+
+    void add_tree(const srocm_device_node *nodes, uint32_t nn, const float *lv, uint32_t nl) {
+        require_loaded();
+        if (nl == 0 || nl != nn + 1) fail(SROCM_ERR_DEVICE, "tree with " + std::to_string(nn) + " nodes and " + std::to_string(nl) + " leaves");
+        std::vector<DevNode> dn(nn);
+        for (uint32_t k = 0; k < nn; ++k) {
+            const srocm_device_node &n = nodes[k];
+            if (n.split.group >= group_col_nt.size() || n.split.column >= group_col_nt[n.split.group].size() ||
+                group_col_nt[n.split.group][n.split.column] < 0)
+                fail(SROCM_ERR_DEVICE, "malformed device tree");
+            for (int32_t c : {n.left, n.right}) {
+                bool bad = c >= 0 ? (static_cast<uint32_t>(c) <= k || static_cast<uint32_t>(c) >= nn) : (static_cast<uint32_t>(~c) >= nl);
+                if (bad) fail(SROCM_ERR_DEVICE, "malformed device tree");
+            }
+            std::memcpy(dn[k].left_bins, n.split.left_bins, sizeof(dn[k].left_bins));
+            dn[k].feature = static_cast<uint32_t>(group_col_nt[n.split.group][n.split.column]);
+            dn[k].left = n.left;
+            dn[k].right = n.right;
+            dn[k].pad = 0;
+        }
+        d_nodes.alloc(std::max<uint32_t>(nn, 1));
+        d_leaf_values.alloc(nl);
+        if (nn) hip_check(hipMemcpyAsync(d_nodes.p, dn.data(), nn * sizeof(DevNode), hipMemcpyHostToDevice, stream), "upload tree");
+        hip_check(hipMemcpyAsync(d_leaf_values.p, lv, nl * sizeof(float), hipMemcpyHostToDevice, stream), "upload leaves");
+        auto apply = [&](DevData &d) {
+            if (d.rows == 0) return;
+            if (nn == 0) k_add_const<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, lv[0]);
+            else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p);
+            launch_check("k_add_tree");
+        };
+        apply(train);
+        for (auto &v : valid) apply(v);
+        sync();  // the host tree arrays may be reused
+    }
+
+    DevData &dataset(uint32_t i) {
+        if (i == 0) return train;
+        if (i - 1 >= valid.size()) fail(SROCM_ERR_DEVICE, "no dataset " + std::to_string(i));
+        return valid[i - 1];
+    }
+
+    void init_scores(uint32_t i, double value) {
+        require_loaded();
+        DevData &d = dataset(i);
+        if (d.rows) {
+            k_fill_f32<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, static_cast<float>(value));
+            launch_check("k_fill_f32");
+        }
+    }
+
+    void scores(uint32_t i, float *out, size_t len) {
+        require_loaded();
+        DevData &d = dataset(i);
+        if (len != d.rows) fail(SROCM_ERR_DEVICE, "scores buffer of " + std::to_string(len) + " values, expected " + std::to_string(d.rows));
+        if (len) hip_check(hipMemcpyAsync(out, d.scores.p, len * 4, hipMemcpyDeviceToHost, stream), "read scores");
+        sync();
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // device split search (split.rs:919-961)
+    // ------------------------------------------------------------------------------------------------
+
+    void ensure_scan(uint32_t jobs) {
+        d_jobs.alloc(jobs);
+        d_cands.alloc(static_cast<size_t>(jobs) * nf);
+        d_split.alloc(jobs);
+        d_splittable.alloc(static_cast<size_t>(jobs) * nf);
+        d_eval.alloc(nf);
+        h_result.alloc(jobs * (sizeof(SplitOut) + nf) + 64);
+        h_stage.alloc(jobs * sizeof(ScanJob) + nf + 64);
+    }
+
+    // Uploads `n` scan jobs and (when given) the evaluate flags through the pinned staging buffer.
+    void upload_jobs(const ScanJob *jobs, uint32_t n, const uint8_t *evaluate) {
+        std::memcpy(h_stage.p, jobs, n * sizeof(ScanJob));
+        hip_check(hipMemcpyAsync(d_jobs.p, h_stage.p, n * sizeof(ScanJob), hipMemcpyHostToDevice, stream), "upload jobs");
+        if (evaluate) {
+            uint8_t *ev = h_stage.p + n * sizeof(ScanJob);
+            std::memcpy(ev, evaluate, nf);
+            hip_check(hipMemcpyAsync(d_eval.p, ev, nf, hipMemcpyHostToDevice, stream), "upload evaluate");
+        }
+    }
+
+    static SplitCfgDev cfg_dev(const srocm_split_config &c) {
+        return SplitCfgDev{c.min_data_in_leaf, c.min_sum_hessian_in_leaf, c.lambda_l1, c.lambda_l2, c.min_gain_to_split};
+    }
+
+    void check_numerical(const uint8_t *evaluate) const {
+        for (uint32_t f = 0; f < nf; ++f)
+            if (evaluate[f] && feats[f].num_bins && feats[f].kind == SROCM_BINS_CATEGORICAL)
+                fail(SROCM_ERR_UNSUPPORTED, "categorical split search runs on the cpu backend only");
+    }
+
+    // Enqueues the scan and select of `jobs` (already uploaded to d_jobs) and the readback of their results.
+    void enqueue_scan(uint32_t njobs, const srocm_split_config &cfg, double sg, double sh) {
+        dim3 grid(div_up(nf, 4), njobs);
+        k_split_scan<<<grid, 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, cfg_dev(cfg), sg, sh);
+        launch_check("k_split_scan");
+        k_split_select<<<njobs, 256, 0, stream>>>(d_jobs.p, nf, cfg_dev(cfg), sg, sh, d_split.p, d_splittable.p);
+        launch_check("k_split_select");
+        hip_check(hipMemcpyAsync(h_result.p, d_split.p, njobs * sizeof(SplitOut), hipMemcpyDeviceToHost, stream), "read splits");
+        hip_check(hipMemcpyAsync(h_result.p + njobs * sizeof(SplitOut), d_splittable.p, static_cast<size_t>(njobs) * nf,
+                                 hipMemcpyDeviceToHost, stream), "read splittable");
+    }
+
+    SplitOut result_split(uint32_t j) const {
+        SplitOut o;
+        std::memcpy(&o, h_result.p + j * sizeof(SplitOut), sizeof(SplitOut));
+        return o;
+    }
+    const uint8_t *result_splittable(uint32_t njobs, uint32_t j) const { return h_result.p + njobs * sizeof(SplitOut) + static_cast<size_t>(j) * nf; }
+
+    // split.rs:919-961 on a host histogram over an explicit feature table (no loaded dataset needed)
+    void find_best_split(const double *hist, size_t len, const srocm_feature *features, uint32_t num_features,
+                         const uint8_t *evaluate, const srocm_sums &sums, double sg, double sh,
+                         const srocm_split_config &cfg, srocm_split_info *out, uint8_t *splittable) {
+        std::vector<FeatDev> fd(num_features);
+        for (uint32_t f = 0; f < num_features; ++f) {
+            const srocm_feature &m = features[f];
+            if (evaluate[f] && m.num_bins && m.kind == SROCM_BINS_CATEGORICAL)
+                fail(SROCM_ERR_UNSUPPORTED, "categorical split search runs on the cpu backend only");
+            if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
+            if (m.num_bins && static_cast<uint64_t>(m.hist_offset) + m.num_bins > len / 2)
+                fail(SROCM_ERR_DEVICE, "feature " + std::to_string(f) + " lies outside the histogram");
+            fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin};
+        }
+        std::vector<int64_t> units(len);
+        for (size_t i = 0; i < len; ++i) units[i] = static_cast<int64_t>(hist[i]);
+        DevBuf<int64_t> dh;
+        DevBuf<FeatDev> dfd;
+        DevBuf<ScanJob> dj;
+        DevBuf<FeatCand> dc;
+        DevBuf<SplitOut> dso;
+        DevBuf<uint8_t> dsp, dev;
+        dh.alloc(std::max<size_t>(len, 1));
+        dfd.alloc(std::max<uint32_t>(num_features, 1));
+        dj.alloc(1);
+        dc.alloc(std::max<uint32_t>(num_features, 1));
+        dso.alloc(1);
+        dsp.alloc(std::max<uint32_t>(num_features, 1));
+        dev.alloc(std::max<uint32_t>(num_features, 1));
+        if (len) hip_check(hipMemcpyAsync(dh.p, units.data(), len * 8, hipMemcpyHostToDevice, stream), "upload histogram");
+        if (num_features) {
+            hip_check(hipMemcpyAsync(dfd.p, fd.data(), num_features * sizeof(FeatDev), hipMemcpyHostToDevice, stream), "upload features");
+            hip_check(hipMemcpyAsync(dev.p, evaluate, num_features, hipMemcpyHostToDevice, stream), "upload evaluate");
+        }
+        ScanJob job{dh.p, sums.grad, sums.hess, sums.count, dc.p};
+        hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
+        if (num_features) {
+            dim3 grid(div_up(num_features, 4), 1);
+            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh);
+            launch_check("k_split_scan");
+        }
+        k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
+        launch_check("k_split_select");
+        SplitOut o;
+        hip_check(hipMemcpyAsync(&o, dso.p, sizeof(o), hipMemcpyDeviceToHost, stream), "read split");
+        if (num_features) hip_check(hipMemcpyAsync(splittable, dsp.p, num_features, hipMemcpyDeviceToHost, stream), "read splittable");
+        sync();
+        to_info(o, out);
+    }
+
+    static void to_info(const SplitOut &o, srocm_split_info *out) {
+        std::memset(out, 0, sizeof(*out));
+        out->found = o.found;
+        if (!o.found) return;
+        out->feature = o.feature;
+        out->gain = o.gain;
+        out->threshold = o.threshold;
+        out->default_left = o.default_left;
+        out->left = srocm_sums{o.left_grad, o.left_hess, o.left_count};
+        out->right = srocm_sums{o.right_grad, o.right_hess, o.right_count};
+        out->left_output = o.left_output;
+        out->right_output = o.right_output;
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // Learner::grow on the device (learner.rs:121-352)
+    // ------------------------------------------------------------------------------------------------
+
+    int take_slot() {
+        if (!spare.empty()) {
+            int s = spare.back();
+            spare.pop_back();
+            return s;
+        }
+        slots.emplace_back();
+        slots.back().alloc(2 * total_bins);
+        return static_cast<int>(slots.size() - 1);
+    }
+    void give_slot(int s) {
+        if (s >= 0) spare.push_back(s);
+    }
+
+    void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves);
+    void set_job_counts(int64_t parent_count);
+
+    void copy_tree(const HostTree &t, const std::vector<GrowLeaf> &leaves, srocm_grown_tree *out) const {
+        if (out->capacity_leaves < t.num_leaves) fail(SROCM_ERR_DEVICE, "grown tree has more leaves than the output holds");
+        out->num_leaves = t.num_leaves;
+        uint32_t ni = t.num_leaves - 1;
+        auto cp = [](auto *dst, const auto &v, size_t n) {
+            if (dst) std::copy(v.begin(), v.begin() + static_cast<long>(n), dst);
+        };
+        cp(out->split_feature, t.split_feature, ni);
+        cp(out->threshold_bin, t.threshold_bin, ni);
+        cp(out->default_left, t.default_left, ni);
+        cp(out->left_child, t.left_child, ni);
+        cp(out->right_child, t.right_child, ni);
+        cp(out->split_gain, t.split_gain, ni);
+        cp(out->internal_value, t.internal_value, ni);
+        cp(out->internal_weight, t.internal_weight, ni);
+        cp(out->internal_count, t.internal_count, ni);
+        cp(out->leaf_value, t.leaf_value, t.num_leaves);
+        cp(out->leaf_weight, t.leaf_weight, t.num_leaves);
+        cp(out->leaf_count, t.leaf_count, t.num_leaves);
+        cp(out->leaf_parent, t.leaf_parent, t.num_leaves);
+        cp(out->leaf_depth, t.leaf_depth, t.num_leaves);
+        if (out->leaf_range)
+            for (uint32_t i = 0; i < t.num_leaves && i < leaves.size(); ++i) out->leaf_range[i] = leaves[i].range;
+    }
+
+    // ------------------------------------------------------------------------------------------------
+    // boosting (boosting.rs:83-324)
+    // ------------------------------------------------------------------------------------------------
+
+    double init_score_value = 0.0;
+    uint32_t trees_added = 0;
+
+    double boost_init(const srocm_train_params &p);
+    uint32_t boost(const srocm_train_params &p, uint32_t first, uint32_t count, srocm_grown_tree *trees);
+
+    // profiling
+    void profile(int enable) {
+        settle_profile();
+        prof.on = enable != 0;
+        prof.hist_launches = prof.hist_builds = prof.hist_rows = prof.hist_bins = prof.hist_bytes = prof.part_launches = prof.part_rows = 0;
+        prof.hist_ms = prof.part_ms = 0;
+    }
+    void settle_profile() {
+        sync();
+        for (auto &e : prof.hist_events) {
+            float ms = 0;
+            hip_check(hipEventElapsedTime(&ms, e.first, e.second), "event elapsed");
+            prof.hist_ms += ms;
+            prof.pool.push_back(e.first);
+            prof.pool.push_back(e.second);
+        }
+        prof.hist_events.clear();
+        for (auto &e : prof.part_events) {
+            float ms = 0;
+            hip_check(hipEventElapsedTime(&ms, e.first, e.second), "event elapsed");
+            prof.part_ms += ms;
+            prof.pool.push_back(e.first);
+            prof.pool.push_back(e.second);
+        }
+        prof.part_events.clear();
+    }
+};
+
+__global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint32_t column, uint64_t n,
+                         uint8_t *__restrict__ col, uint8_t *__restrict__ slab, uint32_t width, uint32_t slab_col) {
+    for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x) {
+        uint8_t b = src[r * stride + column];
+        col[r] = b;
+        if (slab) slab[r * width + slab_col] = b;
+    }
+}
+
+void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint64_t n, uint8_t *col, uint8_t *slab,
+                     uint32_t width, uint32_t slab_col) {
+    k_repack<<<grid_rows(n), 256, 0, stream>>>(src, stride, column, n, col, slab, width, slab_col);
+    launch_check("k_repack");
+}
+
+// objective/binary.rs:27-50 on the host (f64 with the C library's exp, stored as f32), objective/regression.rs
+// on the device; maxima as cpu.rs:774-778.
+std::pair<double, double> Context::compute_gradients() {
+    require_loaded();
+    if (objective == SROCM_OBJ_REGRESSION) {
+        hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
+        if (rows) {
+            k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, has_weight ? weight.p : nullptr, grad.p,
+                                                                   hess.p, rows, scalars.p + 1);
+            launch_check("k_grad_regression");
+        }
+        return read_maxima();
+    }
+    if (objective != SROCM_OBJ_BINARY) fail(SROCM_ERR_UNSUPPORTED, "this objective's gradients come through srocm_set_gradients");
+    h_scores.alloc(rows);
+    h_grad.alloc(rows);
+    h_hess.alloc(rows);
+    if (rows) hip_check(hipMemcpyAsync(h_scores.p, train.scores.p, rows * 4, hipMemcpyDeviceToHost, stream), "read scores");
+    sync();
+    unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> ts;
+    std::vector<double> mg(threads, 0.0), mh(threads, 0.0);
+    uint64_t chunk = (rows + threads - 1) / threads;
+    const float *lab = h_label_v.data();
+    const float *w = has_weight ? h_weight_v.data() : nullptr;
+    double sig = sigmoid;
+    for (unsigned t = 0; t < threads; ++t) {
+        uint64_t b = t * chunk, e = std::min<uint64_t>(rows, b + chunk);
+        if (b >= e) break;
+        ts.emplace_back([&, t, b, e] {
+            double m1 = 0.0, m2 = 0.0;
+            for (uint64_t r = b; r < e; ++r) {
+                double sign = lab[r] > 0.0f ? 1.0 : -1.0;
+                double response = -sign * sig / (1.0 + std::exp(sign * sig * static_cast<double>(h_scores.p[r])));
+                double abs_response = std::fabs(response);
+                double wr = w ? static_cast<double>(w[r]) : 1.0;
+                float g = static_cast<float>(response * wr);
+                float h = static_cast<float>(abs_response * (sig - abs_response) * wr);
+                h_grad.p[r] = g;
+                h_hess.p[r] = h;
+                m1 = std::fmax(m1, static_cast<double>(std::fabs(g)));
+                m2 = std::fmax(m2, static_cast<double>(std::fabs(h)));
+            }
+            mg[t] = m1;
+            mh[t] = m2;
+        });
+    }
+    for (auto &t : ts) t.join();
+    double max_g = 0.0, max_h = 0.0;
+    for (unsigned t = 0; t < threads; ++t) {
+        max_g = std::fmax(max_g, mg[t]);
+        max_h = std::fmax(max_h, mh[t]);
+    }
+    if (rows) {
+        hip_check(hipMemcpyAsync(grad.p, h_grad.p, rows * 4, hipMemcpyHostToDevice, stream), "upload grad");
+        hip_check(hipMemcpyAsync(hess.p, h_hess.p, rows * 4, hipMemcpyHostToDevice, stream), "upload hess");
+    }
+    return {max_g, max_h};
+}
+
+__global__ void k_job_counts(ScanJob *jobs, const uint32_t *dev_left, int64_t parent_count) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        int64_t left = static_cast<int64_t>(*dev_left);
+        jobs[0].count = left;
+        jobs[1].count = parent_count - left;
+    }
+}
+
+void Context::set_job_counts(int64_t parent_count) {
+    k_job_counts<<<1, 64, 0, stream>>>(d_jobs.p, scalars.p, parent_count);
+    launch_check("k_job_counts");
+}
+
+// learner.rs:121-352 with histograms, subtraction, split search and partition on the device and one
+// readback per split (the left count and both children's best splits).
+void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits,
+                   std::vector<GrowLeaf> &leaves) {
+    require_loaded();
+    if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
+    check_range(spec.root);
+    const srocm_split_config &cfg = spec.cfg;
+    std::vector<uint8_t> mask(spec.feature_mask, spec.feature_mask + nf);
+    check_numerical(mask.data());
+    auto depth_allows = [&](int32_t d) { return spec.max_depth <= 0 || d < spec.max_depth; };  // learner.rs:178-180
+    auto may_split = [&](int32_t d, int64_t l, int64_t r) {                                      // learner.rs:172-175
+        int64_t min_pair = 2 * cfg.min_data_in_leaf;
+        return depth_allows(d) && (l >= min_pair || r >= min_pair);
+    };
+    // every slot back to the pool
+    spare.clear();
+    for (size_t i = 0; i < slots.size(); ++i) spare.push_back(static_cast<int>(i));
+    tree = HostTree{};
+    splits.clear();
+    leaves.assign(1, GrowLeaf{});
+    leaves[0].range = spec.root;
+    leaves[0].count = spec.root_count;
+    leaves[0].splittable.assign(nf, 1);
+    ensure_scan(2);
+    int32_t sums_feature = -1;
+    for (uint32_t f = 0; f < nf; ++f)
+        if (feats[f].num_bins) {
+            sums_feature = static_cast<int32_t>(f);
+            break;
+        }
+    const uint64_t all_columns = nt_feat.size();
+    if (sums_feature >= 0 && may_split(0, spec.root_count, 0)) {
+        int slot = take_slot();
+        launch_hist(spec.root.begin, spec.root.count, nullptr, 0, slots[slot].p, nullptr, all_columns);
+        const srocm_feature &m = feats[sums_feature];
+        h_hist.alloc(2 * static_cast<size_t>(m.num_bins));
+        hip_check(hipMemcpyAsync(h_hist.p, slots[slot].p + 2 * static_cast<size_t>(m.hist_offset), 2 * m.num_bins * 8,
+                                 hipMemcpyDeviceToHost, stream), "read sums feature");
+        sync();
+        double sg = 0.0, sh = 0.0;  // split.rs:101-108
+        for (uint32_t b = 0; b < m.num_bins; ++b) {
+            sg = sg + static_cast<double>(h_hist.p[2 * b]);
+            sh = sh + static_cast<double>(h_hist.p[2 * b + 1]);
+        }
+        leaves[0].ug = sg;
+        leaves[0].uh = sh;
+        leaves[0].slot = slot;
+        ScanJob job{slots[slot].p, sg, sh, spec.root_count, d_cands.p};
+        upload_jobs(&job, 1, mask.data());
+        enqueue_scan(1, cfg, spec.grad_scale, spec.hess_scale);
+        sync();
+        leaves[0].best = result_split(0);
+        leaves[0].has_best = leaves[0].best.found != 0;
+        leaves[0].splittable.assign(result_splittable(1, 0), result_splittable(1, 0) + nf);
+    }
+    std::vector<uint8_t> evaluate(nf);
+    while (tree.num_leaves < spec.num_leaves) {
+        // learner.rs:418-429 best_leaf
+        int best = -1;
+        double best_gain = 0.0;
+        for (size_t i = 0; i < leaves.size(); ++i) {
+            if (!leaves[i].has_best) continue;
+            if (best < 0 || leaves[i].best.gain > best_gain) {
+                best = static_cast<int>(i);
+                best_gain = leaves[i].best.gain;
+            }
+        }
+        if (best < 0 || !(best_gain > 0.0)) break;
+        // learner.rs:249-352 split_leaf
+        uint32_t index = static_cast<uint32_t>(best);
+        SplitOut info = leaves[index].best;
+        leaves[index].has_best = false;
+        const srocm_feature &meta = feats[info.feature];
+        srocm_bin_split bs{};  // learner.rs:432-452
+        for (uint32_t b = 0; b <= info.threshold; ++b) bs.left_bins[b / 32] |= 1u << (b % 32);
+        if (info.default_left && meta.nan_bin) bs.left_bins[(meta.num_bins - 1) / 32] |= 1u << ((meta.num_bins - 1) % 32);
+        bs.group = meta.group;
+        bs.column = meta.column;
+        srocm_leaf_range parent_range = leaves[index].range;
+        int64_t parent_count = leaves[index].count;
+        bool may_search = leaves[index].slot >= 0 && tree.num_leaves + 1 < spec.num_leaves &&
+                          depth_allows(tree.leaf_depth[index] + 1);
+        uint32_t built_side = info.left_count <= info.right_count ? 0u : 1u;
+        for (uint32_t f = 0; f < nf; ++f) evaluate[f] = mask[f] && leaves[index].splittable[f];
+        enqueue_partition(parent_range, bs);
+        int parent_slot = leaves[index].slot;
+        int built_slot = -1;
+        if (may_search) {
+            built_slot = take_slot();
+            uint64_t used_cols = 0;
+            for (uint32_t f = 0; f < nf; ++f)
+                if (evaluate[f] && feats[f].num_bins) ++used_cols;
+            launch_hist(parent_range.begin, parent_range.count, scalars.p, built_side, slots[built_slot].p, slots[parent_slot].p, used_cols);
+            // both children, with their exact counts from the device-side left count
+            ScanJob jobs[2];
+            double lug = info.left_grad, luh = info.left_hess, rug = info.right_grad, ruh = info.right_hess;
+            jobs[0] = ScanJob{slots[built_side == 0 ? built_slot : parent_slot].p, lug, luh, 0, d_cands.p};
+            jobs[1] = ScanJob{slots[built_side == 0 ? parent_slot : built_slot].p, rug, ruh, 0, d_cands.p + nf};
+            upload_jobs(jobs, 2, evaluate.data());
+            set_job_counts(parent_count);
+            enqueue_scan(2, cfg, spec.grad_scale, spec.hess_scale);
+        }
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
+        sync();
+        uint32_t left_local = h_u32.p[0];
+        int64_t left_count = left_local;
+        int64_t right_count = parent_count - left_count;
+        if (left_count <= 0 || right_count <= 0)
+            fail(SROCM_ERR_INTERNAL, "split of leaf " + std::to_string(index) + " on feature " + std::to_string(info.feature) + " sends " +
+                                         std::to_string(left_count) + " rows left and " + std::to_string(right_count) + " right");
+        if (prof.on && may_search) {
+            uint64_t used_cols = 0;
+            for (uint32_t f = 0; f < nf; ++f)
+                if (evaluate[f] && feats[f].num_bins) ++used_cols;
+            double built_rows = built_side == 0 ? static_cast<double>(left_count) : static_cast<double>(right_count);
+            prof.hist_rows += built_rows;
+            prof.hist_bins += built_rows * static_cast<double>(used_cols);
+        }
+        float gain32 = static_cast<float>(info.gain + cfg.min_gain_to_split);
+        uint32_t right_index = tree.split(index, info.feature, info.threshold, info.default_left != 0, info.left_output, info.right_output,
+                                          left_count, right_count, info.left_hess * spec.hess_scale, info.right_hess * spec.hess_scale, gain32);
+        if (right_index != leaves.size()) fail(SROCM_ERR_INTERNAL, "tree numbered the new leaf unexpectedly");
+        splits.push_back(bs);
+        GrowLeaf left, right;
+        left.range = srocm_leaf_range{parent_range.begin, left_local};
+        left.ug = info.left_grad;
+        left.uh = info.left_hess;
+        left.count = left_count;
+        right.range = srocm_leaf_range{parent_range.begin + left_local, parent_range.count - left_local};
+        right.ug = info.right_grad;
+        right.uh = info.right_hess;
+        right.count = right_count;
+        int32_t depth = tree.leaf_depth[index];
+        bool searched = may_split(depth, left_count, right_count);
+        if (may_search && searched) {
+            int built_leaf_slot = built_slot, other_leaf_slot = parent_slot;
+            GrowLeaf &lb = built_side == 0 ? left : right;
+            GrowLeaf &lo = built_side == 0 ? right : left;
+            lb.slot = built_leaf_slot;
+            lo.slot = other_leaf_slot;
+            for (int side = 0; side < 2; ++side) {
+                GrowLeaf &l = side == 0 ? left : right;
+                l.best = result_split(side);
+                l.has_best = l.best.found != 0;
+                l.splittable.assign(result_splittable(2, side), result_splittable(2, side) + nf);
+            }
+        } else {
+            give_slot(parent_slot);
+            give_slot(built_slot);
+        }
+        leaves[index] = std::move(left);
+        leaves.push_back(std::move(right));
+    }
+}
+
+
+// boosting.rs:100-108 and objective/mod.rs:92-109
+double Context::boost_init(const srocm_train_params &p) {
+    require_loaded();
+    double score = 0.0;
+    if (p.boost_from_average && objective != SROCM_OBJ_LAMBDARANK) {
+        double sum_label = 0.0, sum_weight = 0.0;
+        const float *lab = h_label_v.data();
+        if (objective == SROCM_OBJ_BINARY) {  // binary.rs:11-25
+            if (has_weight) {
+                for (uint64_t i = 0; i < rows; ++i) {
+                    float pos = lab[i] > 0.0f ? 1.0f : 0.0f;
+                    sum_label = sum_label + static_cast<double>(pos * h_weight_v[i]);
+                    sum_weight = sum_weight + static_cast<double>(h_weight_v[i]);
+                }
+            } else {
+                for (uint64_t i = 0; i < rows; ++i) sum_label += lab[i] > 0.0f ? 1.0 : 0.0;
+                sum_weight = static_cast<double>(rows);
+            }
+            double pr = std::clamp(sum_label / sum_weight, K_EPS_H, 1.0 - K_EPS_H);
+            score = std::log(pr / (1.0 - pr)) / p.sigmoid;
+        } else {  // regression.rs:60-67
+            if (has_weight) {
+                for (uint64_t i = 0; i < rows; ++i) {
+                    sum_label = sum_label + static_cast<double>(lab[i] * h_weight_v[i]);
+                    sum_weight = sum_weight + static_cast<double>(h_weight_v[i]);
+                }
+            } else {
+                for (uint64_t i = 0; i < rows; ++i) sum_label += static_cast<double>(lab[i]);
+                sum_weight = static_cast<double>(rows);
+            }
+            score = sum_label / sum_weight;
+        }
+        score = std::fabs(score) > K_EPS_H ? score : 0.0;
+    }
+    for (uint32_t d = 0; d <= valid.size(); ++d) init_scores(d, score);
+    sync();
+    init_score_value = score;
+    trees_added = 0;
+    return score;
+}
+
+// split.rs:966-985 feature_mask
+static void feature_mask(const std::vector<srocm_feature> &feats, double fraction, uint32_t seed, uint32_t iteration,
+                         std::vector<uint8_t> &mask) {
+    std::vector<uint32_t> usable;
+    for (uint32_t f = 0; f < feats.size(); ++f)
+        if (feats[f].num_bins) usable.push_back(f);
+    mask.assign(feats.size(), 0);
+    if (fraction >= 1.0) {
+        for (uint32_t f : usable) mask[f] = 1;
+        return;
+    }
+    size_t count = std::max<size_t>(static_cast<size_t>(sat_i64_h(static_cast<double>(usable.size()) * fraction + 0.5)),
+                                    std::min<size_t>(usable.size(), 1));
+    std::vector<std::pair<float, uint32_t>> keyed;
+    for (uint32_t f : usable) keyed.emplace_back(uniform_h(seed, 3u, iteration, f), f);
+    std::sort(keyed.begin(), keyed.end(), [](const auto &a, const auto &b) {
+        int c = total_cmp_f(a.first, b.first);
+        if (c != 0) return c < 0;
+        return a.second < b.second;
+    });
+    for (size_t i = 0; i < count && i < keyed.size(); ++i) mask[keyed[i].second] = 1;
+}
+
+// boosting.rs:227-324 train_one_iter / add, `count` times
+uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t count, srocm_grown_tree *trees) {
+    require_loaded();
+    if (objective == SROCM_OBJ_LAMBDARANK) fail(SROCM_ERR_UNSUPPORTED, "lambdarank gradients stay on the host; drive the backend ops");
+    bool constant_hessian = objective == SROCM_OBJ_REGRESSION && !has_weight;  // objective/mod.rs:84-89
+    uint32_t done = 0;
+    HostTree tree;
+    std::vector<srocm_bin_split> splits;
+    std::vector<GrowLeaf> leaves;
+    std::vector<uint8_t> mask;
+    for (uint32_t it = first; it < first + count; ++it) {
+        auto [mg, mh] = compute_gradients();
+        srocm_quant_spec spec = make_quant_spec(mg, mh, constant_hessian, 1.0, p.num_grad_quant_bins, p.stochastic_rounding != 0,
+                                                p.data_random_seed, it);
+        quantize(spec);
+        srocm_bag bag{};
+        if (p.bagging_fraction < 1.0 && p.bagging_freq > 0) {
+            bag.kind = SROCM_BAG_BERNOULLI;
+            bag.seed = p.bagging_seed;
+            bag.round = it / p.bagging_freq;
+            bag.fraction = p.bagging_fraction;
+        }
+        uint32_t local_rows = reset_partition(bag);
+        feature_mask(feats, p.feature_fraction, p.feature_fraction_seed, it, mask);
+        srocm_grow_spec gs{};
+        gs.cfg = p.cfg;
+        gs.num_leaves = p.num_leaves;
+        gs.max_depth = p.max_depth;
+        gs.grad_scale = spec.grad_scale;
+        gs.hess_scale = spec.hess_scale;
+        gs.feature_mask = mask.data();
+        gs.root = srocm_leaf_range{0, local_rows};
+        gs.root_count = local_rows;
+        grow(gs, tree, splits, leaves);
+        if (tree.num_leaves == 1) {  // boosting.rs:301-310
+            if (trees_added == 0) {
+                HostTree c;
+                c.leaf_value[0] = init_score_value;
+                copy_tree(c, {}, &trees[done]);
+                ++done;
+                ++trees_added;
+            }
+            break;
+        }
+        if (p.quant_train_renew_leaf) {  // learner.rs:376-404
+            float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
+            std::vector<srocm_leaf_range> ranges(leaves.size());
+            for (size_t i = 0; i < leaves.size(); ++i) ranges[i] = leaves[i].range;
+            std::vector<int64_t> sums(2 * leaves.size());
+            leaf_sums(ranges.data(), static_cast<uint32_t>(ranges.size()), gsc, hsc, sums.data());
+            for (size_t l = 0; l < leaves.size(); ++l) {
+                double sum_grad = static_cast<double>(sums[2 * l]) / static_cast<double>(gsc);
+                double sum_hess = static_cast<double>(sums[2 * l + 1]) / static_cast<double>(hsc);
+                tree.leaf_value[l] = round_to_zero(leaf_output_h(sum_grad, sum_hess, p.cfg.lambda_l1, p.cfg.lambda_l2));
+                tree.leaf_weight[l] = sum_hess;
+            }
+        }
+        // boosting.rs:313-324
+        tree.shrink(p.learning_rate);
+        std::vector<srocm_device_node> nodes(splits.size());
+        for (size_t k = 0; k < nodes.size(); ++k) {
+            nodes[k].split = splits[k];
+            nodes[k].left = tree.left_child[k];
+            nodes[k].right = tree.right_child[k];
+        }
+        std::vector<float> lv(tree.leaf_value.size());
+        for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i]);
+        if (trees_added == 0 && init_score_value != 0.0) {
+            tree.add_bias(init_score_value);
+            for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i] - init_score_value);  // replay.rs:38-40
+        }
+        add_tree(nodes.data(), static_cast<uint32_t>(nodes.size()), lv.data(), static_cast<uint32_t>(lv.size()));
+        if (trees) copy_tree(tree, leaves, &trees[done]);
+        ++done;
+        ++trees_added;
+    }
+    return done;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------------------
+
+thread_local std::string g_create_error;
+
+template <typename F>
+int guard(void *ctx, F &&body) {
+    Context *c = static_cast<Context *>(ctx);
+    if (!c) return SROCM_ERR_DEVICE;
+    try {
+        body(*c);
+        c->error.clear();
+        return SROCM_OK;
+    } catch (const Failure &f) {
+        c->error = f.what();
+        return f.kind;
+    } catch (const std::bad_alloc &) {
+        c->error = "host out of memory";
+        return SROCM_ERR_DEVICE;
+    } catch (const std::exception &e) {
+        c->error = e.what();
+        return SROCM_ERR_INTERNAL;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int srocm_is_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    for (int i = 0; i < n; ++i) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) return 1;
+    }
+    return 0;
+}
+
+int srocm_create(int ordinal, void **out) {
+    if (!out) return SROCM_ERR_DEVICE;
+    *out = nullptr;
+    try {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n <= 0) fail(SROCM_ERR_DEVICE, "rocm: no HIP device is available");
+        int dev = ordinal < 0 ? 0 : ordinal;
+        if (dev >= n) fail(SROCM_ERR_DEVICE, "rocm: device " + std::to_string(dev) + " of " + std::to_string(n));
+        hipDeviceProp_t prop;
+        hip_check(hipGetDeviceProperties(&prop, dev), "device properties");
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            fail(SROCM_ERR_DEVICE, std::string("rocm: device is ") + prop.gcnArchName + ", this build targets gfx950");
+        hip_check(hipSetDevice(dev), "set device");
+        auto c = std::make_unique<Context>();
+        c->device = dev;
+        c->cus = static_cast<uint32_t>(prop.multiProcessorCount);
+        c->device_name = prop.name;
+        hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "create stream");
+        c->h_u32.alloc(64);
+        *out = c.release();
+        g_create_error.clear();
+        return SROCM_OK;
+    } catch (const Failure &f) {
+        g_create_error = f.what();
+        return f.kind;
+    } catch (const std::exception &e) {
+        g_create_error = e.what();
+        return SROCM_ERR_INTERNAL;
+    }
+}
+
+void srocm_destroy(void *ctx) {
+    Context *c = static_cast<Context *>(ctx);
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    delete c;
+}
+
+const char *srocm_last_error(const void *ctx) {
+    if (!ctx) return g_create_error.c_str();
+    return static_cast<const Context *>(ctx)->error.c_str();
+}
+
+int srocm_name(void *ctx, char *buf, size_t len) {
+    return guard(ctx, [&](Context &c) {
+        std::string n = c.device_name + " (rocm, " + std::to_string(c.cus) + " CUs)";
+        if (buf && len) {
+            std::strncpy(buf, n.c_str(), len - 1);
+            buf[len - 1] = 0;
+        }
+    });
+}
+
+int srocm_load(void *ctx, const srocm_dataset *train, const srocm_dataset *const *valid, uint32_t num_valid,
+               const srocm_objective *objective) {
+    return guard(ctx, [&](Context &c) {
+        hip_check(hipSetDevice(c.device), "set device");
+        c.load(train, valid, num_valid, objective);
+    });
+}
+
+int srocm_init_scores(void *ctx, uint32_t dataset, double value) {
+    return guard(ctx, [&](Context &c) {
+        c.init_scores(dataset, value);
+        c.sync();
+    });
+}
+
+int srocm_compute_gradients(void *ctx, double *max_abs_grad, double *max_hess) {
+    return guard(ctx, [&](Context &c) {
+        auto [g, h] = c.compute_gradients();
+        c.sync();
+        if (max_abs_grad) *max_abs_grad = g;
+        if (max_hess) *max_hess = h;
+    });
+}
+
+int srocm_set_gradients(void *ctx, const float *grad, const float *hess, uint64_t n, double *max_abs_grad, double *max_hess) {
+    return guard(ctx, [&](Context &c) {
+        auto [g, h] = c.set_gradients(grad, hess, n);
+        if (max_abs_grad) *max_abs_grad = g;
+        if (max_hess) *max_hess = h;
+    });
+}
+
+int srocm_quantize(void *ctx, const srocm_quant_spec *spec) {
+    return guard(ctx, [&](Context &c) {
+        if (!spec) fail(SROCM_ERR_DEVICE, "null quantization spec");
+        c.quantize(*spec);
+        c.sync();
+    });
+}
+
+int srocm_reset_partition(void *ctx, const srocm_bag *bag, uint32_t *count) {
+    return guard(ctx, [&](Context &c) {
+        srocm_bag all{};
+        uint32_t n = c.reset_partition(bag ? *bag : all);
+        c.sync();
+        if (count) *count = n;
+    });
+}
+
+int srocm_set_histogram_features(void *ctx, const uint8_t *used, uint32_t num_features) {
+    return guard(ctx, [&](Context &c) {
+        c.require_loaded();
+        for (uint32_t f = 0; f < c.nf; ++f) c.used[f] = (!used || f >= num_features) ? 1 : used[f];
+    });
+}
+
+int srocm_histogram(void *ctx, srocm_leaf_range leaf, int quantized, double *out, size_t len) {
+    return guard(ctx, [&](Context &c) { c.histogram(leaf, quantized, out, len); });
+}
+
+int srocm_partition(void *ctx, srocm_leaf_range leaf, const srocm_bin_split *split, uint32_t *left) {
+    return guard(ctx, [&](Context &c) {
+        if (!split) fail(SROCM_ERR_DEVICE, "null split");
+        uint32_t l = c.partition(leaf, *split);
+        if (left) *left = l;
+    });
+}
+
+int srocm_partition_and_histogram(void *ctx, srocm_leaf_range leaf, const srocm_bin_split *split, uint32_t side,
+                                  int quantized, double *out, size_t len, uint32_t *left) {
+    return guard(ctx, [&](Context &c) {
+        if (!split) fail(SROCM_ERR_DEVICE, "null split");
+        uint32_t l = c.partition_and_histogram(leaf, *split, side, quantized, out, len);
+        if (left) *left = l;
+    });
+}
+
+int srocm_leaf_sums(void *ctx, const srocm_leaf_range *leaves, uint32_t num_leaves, float grad_scale, float hess_scale,
+                    int64_t *out) {
+    return guard(ctx, [&](Context &c) { c.leaf_sums(leaves, num_leaves, grad_scale, hess_scale, out); });
+}
+
+int srocm_add_tree(void *ctx, const srocm_device_node *nodes, uint32_t num_nodes, const float *leaf_values,
+                   uint32_t num_leaf_values) {
+    return guard(ctx, [&](Context &c) { c.add_tree(nodes, num_nodes, leaf_values, num_leaf_values); });
+}
+
+int srocm_scores(void *ctx, uint32_t dataset, float *out, size_t len) {
+    return guard(ctx, [&](Context &c) { c.scores(dataset, out, len); });
+}
+
+int srocm_find_best_split(void *ctx, const double *hist, size_t len, const srocm_feature *features,
+                          uint32_t num_features, const uint8_t *evaluate, const srocm_sums *sums, double grad_scale,
+                          double hess_scale, const srocm_split_config *cfg, srocm_split_info *out,
+                          uint8_t *splittable) {
+    return guard(ctx, [&](Context &c) {
+        if ((!hist && len) || (!features && num_features) || (!evaluate && num_features) || !sums || !cfg || !out ||
+            (!splittable && num_features))
+            fail(SROCM_ERR_DEVICE, "null argument");
+        c.find_best_split(hist, len, features, num_features, evaluate, *sums, grad_scale, hess_scale, *cfg, out, splittable);
+    });
+}
+
+int srocm_grow(void *ctx, const srocm_grow_spec *spec, srocm_grown_tree *out) {
+    return guard(ctx, [&](Context &c) {
+        if (!spec || !out || !spec->feature_mask) fail(SROCM_ERR_DEVICE, "null argument");
+        HostTree tree;
+        std::vector<srocm_bin_split> splits;
+        std::vector<GrowLeaf> leaves;
+        c.grow(*spec, tree, splits, leaves);
+        c.copy_tree(tree, leaves, out);
+    });
+}
+
+int srocm_boost_init(void *ctx, const srocm_train_params *params, double *init_score) {
+    return guard(ctx, [&](Context &c) {
+        if (!params) fail(SROCM_ERR_CONFIG, "null parameters");
+        double s = c.boost_init(*params);
+        if (init_score) *init_score = s;
+    });
+}
+
+int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iteration, uint32_t count,
+                srocm_grown_tree *trees, uint32_t *trained) {
+    return guard(ctx, [&](Context &c) {
+        if (!params) fail(SROCM_ERR_CONFIG, "null parameters");
+        if (params->num_leaves < 2) fail(SROCM_ERR_CONFIG, "num_leaves must be at least 2");
+        if (params->num_grad_quant_bins < 2 || params->num_grad_quant_bins > 64 || params->num_grad_quant_bins % 2)
+            fail(SROCM_ERR_CONFIG, "num_grad_quant_bins must be even and in 2..=64");
+        uint32_t n = c.boost(*params, first_iteration, count, trees);
+        if (trained) *trained = n;
+    });
+}
+
+int srocm_profile(void *ctx, int enable) {
+    return guard(ctx, [&](Context &c) { c.profile(enable); });
+}
+
+int srocm_profile_read(void *ctx, double *out8) {
+    return guard(ctx, [&](Context &c) {
+        c.settle_profile();
+        const Profile &p = c.prof;
+        // algorithmic bytes of the builds: rows x (used columns x 1 B bin + 4 B packed gradients + 4 B row id)
+        // plus the 2 x total_bins x 4 B histogram write per build
+        double bytes = p.hist_bins + 8.0 * p.hist_rows + p.hist_builds * 8.0 * static_cast<double>(c.total_bins);
+        double v[8] = {p.hist_launches, p.hist_ms, p.hist_rows, p.hist_bins, bytes, p.part_launches, p.part_ms, p.part_rows};
+        if (out8) std::copy(v, v + 8, out8);
+    });
+}
+
+}  // extern "C"

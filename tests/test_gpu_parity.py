@@ -1,0 +1,279 @@
+"""Parity of the HIP backend with the oracle, through the C ABI, on an MI355X.
+
+Integer work (quantization, histograms, partitions, leaf sums) must match bit for bit; split decisions, tree
+arrays and leaf values must be identical; scores must agree within 1e-6 relative (the f32 adds are the same, so
+they match exactly in practice). Every test prints the case it runs before touching the GPU.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+import silvic_amd
+from silvic_amd import _abi, bin_split, device_node
+from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients
+from tests.split_cases import config, numerical_cases, quantized_cases, sums
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def quantized_setup(rocm, data, grad, hess, seed=1, iteration=0, num_bins=4):
+    """Loads `data`, hands both sides the same gradients and quantizes them; returns (spec, oracle packed)."""
+    rocm.load(data)
+    mg, mh = rocm.set_gradients(grad, hess)
+    assert mg == float(np.abs(grad).max()) and mh == float(np.abs(hess).max())
+    spec = oracle.quant_spec(mg, mh, None, num_bins, True, seed, iteration)
+    rocm.quantize(spec)
+    packed = oracle.quantize(spec, grad, hess, data.row_offset)
+    return spec, packed
+
+
+def binary_gradients(data, seed=0):
+    rng = np.random.default_rng(seed)
+    scores = (rng.standard_normal(data.num_rows) * 0.5).astype(np.float32)
+    g, h, _, _ = oracle.gradients(_abi.OBJ_BINARY, scores, data.label)
+    return g, h
+
+
+@pytest.mark.parametrize("rows,cols", [(5_000, 28), (300_000, 128), (120_000, 136)])
+def test_root_and_leaf_histograms_bit_exact(rocm, rows, cols):
+    say("histogram", rows, cols)
+    data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=11)
+    g, h = binary_gradients(data)
+    spec, packed = quantized_setup(rocm, data, g, h)
+    n = rocm.reset_partition()
+    assert n == rows
+    root = rocm.histogram((0, rows))
+    expected = oracle.histogram(data, packed, 4, np.arange(rows, dtype=np.uint32))
+    assert np.array_equal(root, expected)
+    # a leaf: partition the root on a feature, then both children and sub-ranges (which pin the row order)
+    f = 5
+    meta = data.features[f]
+    split = bin_split(meta.group, meta.column, list(range(0, meta.num_bins // 2)) + [meta.num_bins - 1])
+    left = rocm.partition((0, rows), split)
+    o_rows, o_left = oracle.partition(data, np.arange(rows, dtype=np.uint32), split)
+    assert left == o_left
+    for b, c in [(0, left), (left, rows - left), (0, min(777, left)), (left + 13, min(1000, rows - left - 13))]:
+        got = rocm.histogram((b, c))
+        want = oracle.histogram(data, packed, 4, o_rows[b:b + c])
+        assert np.array_equal(got, want), (b, c)
+
+
+def test_partition_and_histogram_fused(rocm):
+    say("partition_and_histogram")
+    data = silvic_amd.synthetic(2, rows=200_000, cols=64, seed=3)
+    g, h = binary_gradients(data, 1)
+    spec, packed = quantized_setup(rocm, data, g, h)
+    rocm.reset_partition()
+    meta = data.features[40]
+    split = bin_split(meta.group, meta.column, range(0, 100))
+    o_rows, o_left = oracle.partition(data, np.arange(200_000, dtype=np.uint32), split)
+    for side in (0, 1):
+        rocm.reset_partition()
+        left, hist = rocm.partition_and_histogram((0, 200_000), split, side)
+        assert left == o_left
+        b, c = (0, o_left) if side == 0 else (o_left, 200_000 - o_left)
+        assert np.array_equal(hist, oracle.histogram(data, packed, 4, o_rows[b:b + c]))
+
+
+def test_bagged_partition_is_ascending_and_exact(rocm):
+    say("bagging")
+    data = silvic_amd.synthetic(2, rows=100_000, cols=32, seed=5)
+    g, h = binary_gradients(data, 2)
+    spec, packed = quantized_setup(rocm, data, g, h)
+    bag = _abi.Bag(_abi.BAG_BERNOULLI, 4, 1, 0, 0.7)
+    n = rocm.reset_partition(bag)
+    rows = np.array([r for r in range(100_000) if oracle.lib().oracle_in_bag(4, 1, r, 0.7)], np.uint32)
+    assert n == len(rows)
+    for b, c in [(0, n), (0, 1000), (n - 500, 500)]:
+        assert np.array_equal(rocm.histogram((b, c)), oracle.histogram(data, packed, 4, rows[b:b + c]))
+
+
+def test_reference_backend_cases(rocm):
+    # cpu.rs:1014-1179 on the device: histograms over a bag, stable partition, add_tree, leaf sums
+    say("cpu.rs cases")
+    data = cpu_dataset(50_000)
+    grad, hess = cpu_gradients(50_000)
+    rocm.load(data)
+    rocm.set_gradients(grad, hess)
+    spec = oracle.quant_spec(1.5, 0.75, None, 16, True, 9, 3)
+    rocm.quantize(spec)
+    packed = oracle.quantize(spec, grad, hess, data.row_offset)
+    n = rocm.reset_partition(_abi.Bag(_abi.BAG_BERNOULLI, 4, 1, 0, 0.7))
+    part = np.array([r for r in range(50_000) if oracle.lib().oracle_in_bag(4, 1, 100 + r, 0.7)], np.uint32)
+    assert n == len(part)
+    got = rocm.histogram((1000, 30_000))
+    assert np.array_equal(got, oracle.histogram(data, packed, 16, part[1000:31_000]))
+    rocm.reset_partition()
+    split = bin_split(0, 0, [1, 2, 4])
+    left = rocm.partition((500, 25_000), split)
+    o_rows, o_left = oracle.partition(data, np.arange(500, 25_500, dtype=np.uint32), split)
+    assert left == o_left
+    sums = rocm.leaf_sums([(500, left), (500 + left, 25_000 - left)], 1024.0, 256.0)
+    full = np.arange(50_000, dtype=np.uint32)
+    full[500:25_500] = o_rows
+    want = oracle.leaf_sums(grad, hess, full, [(500, left), (500 + left, 25_000 - left)], 1024.0, 256.0)
+    assert np.array_equal(sums, want)
+    tsplit = bin_split(1, 0, [0, 1])
+    rocm.init_scores(0, 1.0)
+    rocm.add_tree([device_node(tsplit, ~0, ~1)], [0.5, -0.25])
+    assert np.array_equal(rocm.scores(0), np.where(data.bin(2) < 2, 1.5, 0.75).astype(np.float32))
+
+
+def test_errors_are_reported_not_crashes(rocm):
+    say("errors")
+    data = cpu_dataset(1000)
+    rocm.load(data)
+    g, h = cpu_gradients(1000)
+    rocm.set_gradients(g, h)
+    rocm.quantize(oracle.quant_spec(1.0, 1.0, None, 4, True, 1, 0))
+    rocm.reset_partition()
+    with pytest.raises(_abi.DeviceError):
+        rocm.histogram((900, 200))
+    with pytest.raises(_abi.SilvicError) as e:
+        rocm.histogram((0, 10), quantized=False)
+    assert e.value.kind == "unsupported"
+    with pytest.raises(_abi.DeviceError):
+        rocm.add_tree([device_node(bin_split(0, 0, [0]), 0, ~1)], [0.0, 1.0])
+    with pytest.raises(_abi.DeviceError):
+        rocm.partition((0, 10), bin_split(7, 0, [0]))
+    assert rocm.histogram((0, 0)).sum() == 0
+
+
+def compare_split(d, o, name):
+    assert bool(d.found) == bool(o.found), name
+    if not o.found:
+        return
+    assert d.feature == o.feature, name
+    assert (d.threshold, d.default_left) == (o.threshold, o.default_left), name
+    assert d.gain == o.gain, (name, d.gain, o.gain)
+    for side in ("left", "right"):
+        ds, os_ = getattr(d, side), getattr(o, side)
+        assert (ds.grad, ds.hess, ds.count) == (os_.grad, os_.hess, os_.count), (name, side)
+    assert d.left_output == o.left_output and d.right_output == o.right_output, name
+
+
+def test_split_search_matches_the_oracle_bit_for_bit(rocm):
+    say("split search: 400 numerical cases")
+    for name, hist, rows, meta, cfg in numerical_cases():
+        s = sums(hist, rows)
+        # histograms hold integer units on the device path: scale the reference's real-valued cases
+        units = np.round(hist * 64.0)
+        s = (units[0::2].sum(), units[1::2].sum(), s[2])
+        o, ospl = oracle.find_best_split(units, [meta], [1], s, 1.0 / 64, 1.0 / 64, cfg)
+        d, dspl = rocm.find_best_split(units, [meta], [1], s, 1.0 / 64, 1.0 / 64, cfg)
+        compare_split(d, o, name)
+        assert np.array_equal(dspl, ospl), name
+    say("split search: quantized-scale cases")
+    for case, units, rows, meta in quantized_cases():
+        s = (units[0::2].sum(), units[1::2].sum(), int(rows.sum()))
+        o, _ = oracle.find_best_split(units, [meta], [1], s, 0.37, 0.125, config())
+        d, _ = rocm.find_best_split(units, [meta], [1], s, 0.37, 0.125, config())
+        compare_split(d, o, case)
+
+
+def test_split_search_over_a_real_histogram(rocm):
+    say("split search on a config-2 histogram")
+    data = silvic_amd.synthetic(2, rows=200_000, cols=128, seed=9)
+    g, h = binary_gradients(data, 4)
+    spec, packed = quantized_setup(rocm, data, g, h)
+    hist = oracle.histogram(data, packed, 4, np.arange(200_000, dtype=np.uint32))
+    f0 = data.features[0]
+    s = (hist[2 * f0.hist_offset:2 * (f0.hist_offset + f0.num_bins):2].sum(),
+         hist[2 * f0.hist_offset + 1:2 * (f0.hist_offset + f0.num_bins):2].sum(), 200_000)
+    for ev_seed in range(4):
+        ev = np.random.default_rng(ev_seed).random(len(data.features)) < (1.0 if ev_seed == 0 else 0.5)
+        for kw in ({}, dict(lambda_l1=0.5, lambda_l2=2.0), dict(min_data_in_leaf=5000)):
+            cfg = oracle.split_config(**kw)
+            o, ospl = oracle.find_best_split(hist, data.features, ev, s, spec.grad_scale, spec.hess_scale, cfg)
+            d, dspl = rocm.find_best_split(hist, data.features, ev, s, spec.grad_scale, spec.hess_scale, cfg)
+            compare_split(d, o, (ev_seed, kw))
+            assert np.array_equal(dspl, ospl)
+
+
+def compare_trees(d, o, name, exact_values=True):
+    assert d["num_leaves"] == o["num_leaves"], name
+    for k in ("split_feature", "threshold_bin", "left_child", "right_child", "internal_count", "leaf_count",
+              "leaf_depth"):
+        assert np.array_equal(d[k], o[k]), (name, k)
+    dl = (o["decision_type"] & 2) != 0
+    assert np.array_equal(d["default_left"].astype(bool), dl), name
+    assert np.array_equal(d["split_gain"], o["split_gain"]), name
+    for k in ("leaf_value", "leaf_weight", "internal_value", "internal_weight"):
+        if exact_values:
+            assert np.array_equal(d[k], o[k]), (name, k, np.abs(d[k] - o[k]).max())
+        else:
+            np.testing.assert_allclose(d[k], o[k], rtol=1e-6, atol=0, err_msg=f"{name} {k}")
+
+
+@pytest.mark.parametrize("rows,cols,leaves", [(20_000, 16, 31), (400_000, 128, 255)])
+def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves):
+    say("grow", rows, cols, leaves)
+    data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=21)
+    g, h = binary_gradients(data, 7)
+    p = oracle.default_params(num_leaves=leaves)
+    o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
+    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed)
+    n = rocm.reset_partition()
+    mask = oracle.feature_mask(data.features, 1.0, 2, 0)
+    d = rocm.grow(p.cfg, leaves, -1, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
+    o = dict(o_tree)
+    o["leaf_value"] = o_tree["leaf_value"]
+    compare_trees(d, o, "grow")
+    assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+
+
+def test_learner_cases_on_the_device(rocm):
+    # learner.rs:690-740 on numerical features: max_depth, zero-gradient rows
+    say("learner cases")
+    data, bins = learner_dataset(0, 6000)
+    data.features[2].kind = _abi.BINS_NUMERICAL
+    g, h = learner_gradients(0, 6000, bins, zeros=True)
+    for kw in (dict(max_depth=2), dict(min_data_in_leaf=0, min_sum_hessian_in_leaf=0.0, num_leaves=31)):
+        p = oracle.default_params(num_leaves=kw.get("num_leaves", 8), min_data_in_leaf=kw.get("min_data_in_leaf", 20),
+                                  min_sum_hessian_in_leaf=kw.get("min_sum_hessian_in_leaf", 1e-3),
+                                  max_depth=kw.get("max_depth", -1))
+        o_tree, o_ranges, _ = oracle.grow_tree(data, g, h, p, renew=False)
+        spec, _ = quantized_setup(rocm, data, g, h)
+        n = rocm.reset_partition()
+        d = rocm.grow(p.cfg, p.num_leaves, p.max_depth, spec.grad_scale, spec.hess_scale, np.ones(3, bool),
+                      (0, n), n)
+        compare_trees(d, o_tree, kw)
+
+
+def boost_both(data, params, rounds):
+    o = oracle.train(data, oracle.default_params(num_iterations=rounds, **params))
+    t = silvic_amd.Trainer(dict(params_to_lightgbm(params), num_iterations=rounds, device_type="rocm"), data)
+    t.step(rounds)
+    return o, t
+
+
+def params_to_lightgbm(params):
+    out = dict(params)
+    if "objective" in out:
+        out["objective"] = {_abi.OBJ_REGRESSION: "regression", _abi.OBJ_BINARY: "binary"}[out["objective"]]
+    return out
+
+
+@pytest.mark.parametrize("config,rows,cols,params,rounds", [
+    (1, 100_000, 28, dict(num_leaves=31), 20),
+    (2, 200_000, 128, dict(objective=_abi.OBJ_BINARY, num_leaves=255), 6),
+    (2, 100_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, bagging_fraction=0.8, bagging_freq=2,
+                          feature_fraction=0.7, lambda_l2=1.0), 8),
+])
+def test_boosting_matches_the_oracle(config, rows, cols, params, rounds):
+    say("boost", config, rows, cols, params, rounds)
+    data = silvic_amd.synthetic(config, rows=rows, cols=cols, seed=13)
+    o, t = boost_both(data, params, rounds)
+    assert len(t.trees) == len(o.trees) == rounds
+    assert t.init_score == o.init_score
+    for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+        compare_trees(d, ot, f"tree {i}", exact_values=False)
+    s = t.backend.scores(0)
+    np.testing.assert_allclose(s, o.scores, rtol=1e-6, atol=1e-6)
+    assert np.array_equal(s, o.scores), "scores are the same f32 adds"
+    t.backend.close()
