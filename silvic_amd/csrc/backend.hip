@@ -234,7 +234,7 @@ struct HostTree {
 // ---------------------------------------------------------------------------------------------------------
 
 constexpr uint32_t MAX_SLAB_FEATURES = 128;
-constexpr uint32_t HIST_MIN_ROWS = 4096;   // rows per histogram workgroup before another one is used
+constexpr uint32_t HIST_MIN_ROWS = 2048;   // rows per histogram workgroup before another one is used
 constexpr uint64_t ROW_BLOCK = 256;
 
 struct Slab {

@@ -210,11 +210,17 @@ __device__ __forceinline__ void hist_split(uint32_t n, uint32_t max_groups, uint
     if (groups == 0) groups = 1;
 }
 
+// Loads are branch-free: row positions past the range are clamped to its last row and their gradients
+// zeroed, so the compiler issues every load of a step back to back instead of one masked load at a time. A
+// wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
+// step, and hands them out with a shuffle.
 template <int W>
 __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
-    constexpr int DW = W / 4;         // dwords per row
-    constexpr int RPW = WAVE / DW;    // rows per wave step
-    constexpr int UNROLL = 8;         // wave steps in flight
+    constexpr int DW = W / 4;                 // dwords per row
+    constexpr int RPW = WAVE / DW;            // rows per wave step
+    // row ids of one step fit one wave-wide load; at W = 128 the 64 accumulator registers leave room for 8
+    constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
+    constexpr uint32_t STEP = 16u * RPW * UNROLL;          // rows per block step (16 waves)
     constexpr int SLOTS = 256 * W / 1024;
     __shared__ int32_t lds[256 * W];
 
@@ -240,24 +246,29 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
 
     for (uint32_t chunk = start; chunk < end; chunk += a.flush_rows) {
         uint32_t cend = chunk + a.flush_rows < end ? chunk + a.flush_rows : end;
-        for (uint32_t base = chunk + wave * RPW * UNROLL; base < cend; base += 16u * RPW * UNROLL) {
+        uint32_t last = cend - 1;
+        uint32_t base = chunk + wave * RPW * UNROLL;
+        uint32_t cidx = rows[min(base + lane, last)];
+        for (; base < cend; base += STEP) {
+            uint32_t r[UNROLL];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) r[u] = __shfl(cidx, u * RPW + rsub);
+            cidx = rows[min(base + STEP + lane, last)];
             uint32_t dw[UNROLL];
             int32_t g[UNROLL];
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
-                uint32_t i = base + u * RPW + rsub;
-                bool ok = i < cend;
-                uint32_t r = ok ? rows[i] : 0u;
-                g[u] = ok ? a.gh[r] : 0;
-                dw[u] = ok ? bins32[(size_t)r * DW + d] : 0u;
+                g[u] = a.gh[r[u]];
+                dw[u] = bins32[(size_t)r[u] * DW + d];
             }
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
+                int32_t gv = base + u * RPW + rsub < cend ? g[u] : 0;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     uint32_t x = (k + rot) & 3u;
                     uint32_t b = (dw[u] >> (8u * x)) & 255u;
-                    atomicAdd(&lds[b * W + 4u * d + x], g[u]);
+                    atomicAdd(&lds[b * W + 4u * d + x], gv);
                 }
             }
         }
