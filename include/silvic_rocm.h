@@ -251,6 +251,10 @@ int srocm_compute_gradients(void *ctx, double *max_abs_grad, double *max_hess);
 int srocm_set_gradients(void *ctx, const float *grad, const float *hess, uint64_t n, double *max_abs_grad,
                         double *max_hess);
 
+/* Reads back the training gradients and hessians the last srocm_compute_gradients / srocm_set_gradients left
+ * on the device (no counterpart in the trait: for callers that check or reuse them on the host). */
+int srocm_gradients(void *ctx, float *grad, float *hess, size_t len);
+
 /* Backend::quantize (mod.rs:134-135). */
 int srocm_quantize(void *ctx, const srocm_quant_spec *spec);
 

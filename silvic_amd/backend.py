@@ -97,6 +97,14 @@ class RocmBackend:
                                                   C.byref(g), C.byref(h)))
         return g.value, h.value
 
+    def gradients(self):
+        """The training gradients and hessians on the device (float32 arrays)."""
+        n = self._datasets[0].num_rows
+        g = np.zeros(n, np.float32)
+        h = np.zeros(n, np.float32)
+        self._check(self._lib.srocm_gradients(self._h, _p(g, C.c_float), _p(h, C.c_float), n))
+        return g, h
+
     def quantize(self, spec):
         self._check(self._lib.srocm_quantize(self._h, C.byref(spec)))
 

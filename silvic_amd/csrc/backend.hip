@@ -302,7 +302,6 @@ struct Context {
     int64_t max_quant = 1;
     bool quantized_once = false;
 
-    Pinned<float> h_scores, h_grad, h_hess;
     Pinned<int64_t> h_hist;
     Pinned<uint32_t> h_u32;
     Pinned<uint8_t> h_result;
@@ -1044,64 +1043,21 @@ void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint6
     launch_check("k_repack");
 }
 
-// objective/binary.rs:27-50 on the host (f64 with the C library's exp, stored as f32), objective/regression.rs
-// on the device; maxima as cpu.rs:774-778.
+// objective/regression.rs:70-93 and objective/binary.rs:27-50 on the device; maxima as cpu.rs:774-778.
 std::pair<double, double> Context::compute_gradients() {
     require_loaded();
-    if (objective == SROCM_OBJ_REGRESSION) {
-        hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
-        if (rows) {
-            k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, has_weight ? weight.p : nullptr, grad.p,
-                                                                   hess.p, rows, scalars.p + 1);
-            launch_check("k_grad_regression");
-        }
-        return read_maxima();
-    }
-    if (objective != SROCM_OBJ_BINARY) fail(SROCM_ERR_UNSUPPORTED, "this objective's gradients come through srocm_set_gradients");
-    h_scores.alloc(rows);
-    h_grad.alloc(rows);
-    h_hess.alloc(rows);
-    if (rows) hip_check(hipMemcpyAsync(h_scores.p, train.scores.p, rows * 4, hipMemcpyDeviceToHost, stream), "read scores");
-    sync();
-    unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-    std::vector<std::thread> ts;
-    std::vector<double> mg(threads, 0.0), mh(threads, 0.0);
-    uint64_t chunk = (rows + threads - 1) / threads;
-    const float *lab = h_label_v.data();
-    const float *w = has_weight ? h_weight_v.data() : nullptr;
-    double sig = sigmoid;
-    for (unsigned t = 0; t < threads; ++t) {
-        uint64_t b = t * chunk, e = std::min<uint64_t>(rows, b + chunk);
-        if (b >= e) break;
-        ts.emplace_back([&, t, b, e] {
-            double m1 = 0.0, m2 = 0.0;
-            for (uint64_t r = b; r < e; ++r) {
-                double sign = lab[r] > 0.0f ? 1.0 : -1.0;
-                double response = -sign * sig / (1.0 + std::exp(sign * sig * static_cast<double>(h_scores.p[r])));
-                double abs_response = std::fabs(response);
-                double wr = w ? static_cast<double>(w[r]) : 1.0;
-                float g = static_cast<float>(response * wr);
-                float h = static_cast<float>(abs_response * (sig - abs_response) * wr);
-                h_grad.p[r] = g;
-                h_hess.p[r] = h;
-                m1 = std::fmax(m1, static_cast<double>(std::fabs(g)));
-                m2 = std::fmax(m2, static_cast<double>(std::fabs(h)));
-            }
-            mg[t] = m1;
-            mh[t] = m2;
-        });
-    }
-    for (auto &t : ts) t.join();
-    double max_g = 0.0, max_h = 0.0;
-    for (unsigned t = 0; t < threads; ++t) {
-        max_g = std::fmax(max_g, mg[t]);
-        max_h = std::fmax(max_h, mh[t]);
-    }
+    if (objective != SROCM_OBJ_REGRESSION && objective != SROCM_OBJ_BINARY)
+        fail(SROCM_ERR_UNSUPPORTED, "this objective's gradients come through srocm_set_gradients");
+    hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
     if (rows) {
-        hip_check(hipMemcpyAsync(grad.p, h_grad.p, rows * 4, hipMemcpyHostToDevice, stream), "upload grad");
-        hip_check(hipMemcpyAsync(hess.p, h_hess.p, rows * 4, hipMemcpyHostToDevice, stream), "upload hess");
+        const float *w = has_weight ? weight.p : nullptr;
+        if (objective == SROCM_OBJ_REGRESSION)
+            k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, scalars.p + 1);
+        else
+            k_grad_binary<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, sigmoid, scalars.p + 1);
+        launch_check("k_grad");
     }
-    return {max_g, max_h};
+    return read_maxima();
 }
 
 __global__ void k_job_counts(ScanJob *jobs, const uint32_t *dev_left, int64_t parent_count) {
@@ -1541,6 +1497,18 @@ int srocm_set_gradients(void *ctx, const float *grad, const float *hess, uint64_
         auto [g, h] = c.set_gradients(grad, hess, n);
         if (max_abs_grad) *max_abs_grad = g;
         if (max_hess) *max_hess = h;
+    });
+}
+
+int srocm_gradients(void *ctx, float *grad, float *hess, size_t len) {
+    return guard(ctx, [&](Context &c) {
+        c.require_loaded();
+        if (len != c.rows) fail(SROCM_ERR_DEVICE, "gradient buffers of " + std::to_string(len) + " values, expected " + std::to_string(c.rows));
+        if (len) {
+            hip_check(hipMemcpyAsync(grad, c.grad.p, len * 4, hipMemcpyDeviceToHost, c.stream), "read grad");
+            hip_check(hipMemcpyAsync(hess, c.hess.p, len * 4, hipMemcpyDeviceToHost, c.stream), "read hess");
+        }
+        c.sync();
     });
 }
 

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "exp_f64.hpp"
+
 namespace srocm {
 
 constexpr double K_EPSILON = static_cast<double>(1e-15f);  // split.rs:37 (a float literal widened)
@@ -129,6 +131,28 @@ __global__ void k_grad_regression(const float *__restrict__ scores, const float 
                 g = residual;
                 h = 1.0f;
             }
+            grad[r] = g;
+            hess[r] = h;
+        }
+        block_max_abs(g, maxima);
+        block_max_abs(h, maxima + 1);
+    }
+}
+
+// objective/binary.rs:27-50: f64 logloss gradients with an exp equal to the C library's, stored as f32
+__global__ void k_grad_binary(const float *__restrict__ scores, const float *__restrict__ label,
+                              const float *__restrict__ weight, float *__restrict__ grad, float *__restrict__ hess,
+                              uint64_t n, double sigmoid, uint32_t *maxima) {
+    for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x; base < n; base += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t r = base + threadIdx.x;
+        float g = 0.0f, h = 0.0f;
+        if (r < n) {
+            double sign = label[r] > 0.0f ? 1.0 : -1.0;
+            double response = -sign * sigmoid / (1.0 + srocm_exp::exp(sign * sigmoid * static_cast<double>(scores[r])));
+            double abs_response = __builtin_fabs(response);
+            double w = weight ? static_cast<double>(weight[r]) : 1.0;
+            g = static_cast<float>(response * w);
+            h = static_cast<float>(abs_response * (sigmoid - abs_response) * w);
             grad[r] = g;
             hess[r] = h;
         }

@@ -124,6 +124,53 @@ def test_reference_backend_cases(rocm):
     assert np.array_equal(rocm.scores(0), np.where(data.bin(2) < 2, 1.5, 0.75).astype(np.float32))
 
 
+def test_binary_gradients_are_the_oracles_bit_for_bit(rocm):
+    # objective/binary.rs:27-50 on the device (exp restated bit-exactly) vs the oracle (C library exp)
+    say("binary gradients")
+    data = silvic_amd.synthetic(2, rows=400_000, cols=16, seed=17)
+    rocm.load(data, objective=_abi.OBJ_BINARY, sigmoid=1.0)
+    # diverse scores: a 255-leaf tree with leaf values over [-40, 40] on top of a constant
+    rocm.init_scores(0, 0.3)
+    rng = np.random.default_rng(5)
+    nodes = []
+    for k in range(127):
+        meta = data.features[k % 16]
+        left = 2 * k + 1 if 2 * k + 1 < 127 else ~(2 * k + 1 - 127)
+        right = 2 * k + 2 if 2 * k + 2 < 127 else ~(2 * k + 2 - 127)
+        nodes.append(device_node(bin_split(meta.group, meta.column, range(int(rng.integers(1, meta.num_bins)))),
+                                 left, right))
+    leaf_values = (rng.uniform(-40, 40, 128)).astype(np.float32)
+    rocm.add_tree(nodes, leaf_values)
+    scores = rocm.scores(0)
+    assert len(np.unique(scores)) > 50
+    mg, mh = rocm.compute_gradients()
+    g, h = rocm.gradients()
+    og, oh, omg, omh = oracle.gradients(_abi.OBJ_BINARY, scores, data.label, sigmoid=1.0)
+    assert np.array_equal(g.view(np.uint32), og.view(np.uint32))
+    assert np.array_equal(h.view(np.uint32), oh.view(np.uint32))
+    assert (mg, mh) == (omg, omh)
+    for sig in (0.5, 2.0):
+        rocm.load(data, objective=_abi.OBJ_BINARY, sigmoid=sig)
+        rocm.init_scores(0, 0.0)
+        rocm.add_tree(nodes, leaf_values)
+        rocm.compute_gradients()
+        g, h = rocm.gradients()
+        og, oh, _, _ = oracle.gradients(_abi.OBJ_BINARY, rocm.scores(0), data.label, sigmoid=sig)
+        assert np.array_equal(g.view(np.uint32), og.view(np.uint32)), sig
+        assert np.array_equal(h.view(np.uint32), oh.view(np.uint32)), sig
+
+
+def test_regression_gradients_are_exact(rocm):
+    say("regression gradients")
+    data = silvic_amd.synthetic(1, rows=100_000, seed=3)
+    rocm.load(data)
+    rocm.init_scores(0, 0.25)
+    mg, mh = rocm.compute_gradients()
+    g, h = rocm.gradients()
+    og, oh, omg, omh = oracle.gradients(_abi.OBJ_REGRESSION, np.full(100_000, 0.25, np.float32), data.label)
+    assert np.array_equal(g, og) and np.array_equal(h, oh) and (mg, mh) == (omg, omh)
+
+
 def test_errors_are_reported_not_crashes(rocm):
     say("errors")
     data = cpu_dataset(1000)
