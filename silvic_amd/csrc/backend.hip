@@ -307,12 +307,6 @@ struct Context {
     Pinned<uint8_t> h_result;
     Pinned<uint8_t> h_stage;  // per-split uploads (jobs, evaluate flags), rewritten only after a sync
 
-    std::vector<DevBuf<int64_t>> slots;
-    std::vector<int> spare;
-    DevBuf<ScanJob> d_jobs;
-    DevBuf<FeatCand> d_cands;
-    DevBuf<SplitOut> d_split;
-    DevBuf<uint8_t> d_splittable, d_eval;
     DevBuf<DevNode> d_nodes;
     DevBuf<float> d_leaf_values;
     DevBuf<LeafJob> d_leaf_jobs;
@@ -442,6 +436,8 @@ struct Context {
         for (uint32_t f = 0; f < nf; ++f) fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin};
         dfeats.alloc(nf);
         hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
+        d_feat_nt.alloc(nf);
+        hip_check(hipMemcpy(d_feat_nt.p, feat_nt.data(), nf * sizeof(int32_t), hipMemcpyHostToDevice), "upload features");
         for (auto &s : slabs) {
             std::vector<uint32_t> off(s.width, 0), nb(s.width, 0);
             for (size_t c = 0; c < s.feats.size(); ++c) {
@@ -457,8 +453,8 @@ struct Context {
         part_len = 0;
         max_quant = 1;
         quantized_once = false;
-        slots.clear();
-        spare.clear();
+        grow_capacity = 0;
+        pool.release();
         sync();
         loaded = true;
     }
@@ -583,11 +579,12 @@ struct Context {
 
     // The histogram of rows part[begin..+count] (or the `side` child of that range split at *dev_left) into
     // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
+    // With `plan`, the leaf is the plan's built child and out/parent are its slots in `pool` (count: an upper bound).
     void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
-                     int64_t *parent, uint64_t bins_used) {
+                     int64_t *parent, uint64_t bins_used, const Plan *plan = nullptr) {
         uint32_t grid = hist_groups(count);
         for (auto &s : slabs) {
-            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
+            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS, plan, part2.p};
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (prof.on) {
                 e0 = event();
@@ -605,11 +602,12 @@ struct Context {
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
+            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width,
+                         plan, pool.p, 2 * total_bins};
             k_hist_reduce<<<div_up(256ull * s.width, 256), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
-        if (prof.on) {
+        if (prof.on && !plan) {
             prof.hist_builds += 1;
             if (!dev_left) {
                 prof.hist_rows += count;
@@ -668,14 +666,15 @@ struct Context {
         a.dev_left = scalars.p;
         a.begin = begin;
         a.count = count;
-        uint32_t per = div_up(count, cus * 4ull);
-        per = std::max<uint32_t>(256, (per + 255) / 256 * 256);
-        a.per_block = per;
+        a.rows = rows;
+        a.buf0 = part.p;
+        a.buf1 = part2.p;
         return a;
     }
 
+    // `count` is the rows to partition, or (with a plan) an upper bound of them.
     void run_partition(const PartArgs &a, uint32_t count) {
-        uint32_t grid = std::max<uint32_t>(1, div_up(count, a.per_block));
+        uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(cus, div_up(count, 1024)));
         hipEvent_t e0 = nullptr, e1 = nullptr;
         if (prof.on) {
             e0 = event();
@@ -686,13 +685,16 @@ struct Context {
         launch_check("k_part_count");
         k_part_scatter<<<grid, 256, 0, stream>>>(a);
         launch_check("k_part_scatter");
-        k_copy_u32<<<std::max<uint32_t>(1, std::min<uint32_t>(div_up(count, 256), cus * 8)), 256, 0, stream>>>(part2.p, part.p, a.begin, count);
-        launch_check("k_copy_u32");
+        if (!a.plan) {  // the trait's partition is in place: bring the range back into the first buffer
+            k_copy_u32<<<std::max<uint32_t>(1, std::min<uint32_t>(div_up(count, 256), cus * 8)), 256, 0, stream>>>(part2.p, part.p, a.begin,
+                                                                                                            count, nullptr);
+            launch_check("k_copy_u32");
+        }
         if (prof.on) {
             hip_check(hipEventRecord(e1, stream), "event");
             prof.part_events.emplace_back(e0, e1);
             prof.part_launches += 1;
-            prof.part_rows += count;
+            if (!a.plan) prof.part_rows += count;
         }
     }
 
@@ -830,27 +832,6 @@ struct Context {
     // device split search (split.rs:919-961)
     // ------------------------------------------------------------------------------------------------
 
-    void ensure_scan(uint32_t jobs) {
-        d_jobs.alloc(jobs);
-        d_cands.alloc(static_cast<size_t>(jobs) * nf);
-        d_split.alloc(jobs);
-        d_splittable.alloc(static_cast<size_t>(jobs) * nf);
-        d_eval.alloc(nf);
-        h_result.alloc(jobs * (sizeof(SplitOut) + nf) + 64);
-        h_stage.alloc(jobs * sizeof(ScanJob) + nf + 64);
-    }
-
-    // Uploads `n` scan jobs and (when given) the evaluate flags through the pinned staging buffer.
-    void upload_jobs(const ScanJob *jobs, uint32_t n, const uint8_t *evaluate) {
-        std::memcpy(h_stage.p, jobs, n * sizeof(ScanJob));
-        hip_check(hipMemcpyAsync(d_jobs.p, h_stage.p, n * sizeof(ScanJob), hipMemcpyHostToDevice, stream), "upload jobs");
-        if (evaluate) {
-            uint8_t *ev = h_stage.p + n * sizeof(ScanJob);
-            std::memcpy(ev, evaluate, nf);
-            hip_check(hipMemcpyAsync(d_eval.p, ev, nf, hipMemcpyHostToDevice, stream), "upload evaluate");
-        }
-    }
-
     static SplitCfgDev cfg_dev(const srocm_split_config &c) {
         return SplitCfgDev{c.min_data_in_leaf, c.min_sum_hessian_in_leaf, c.lambda_l1, c.lambda_l2, c.min_gain_to_split};
     }
@@ -860,25 +841,6 @@ struct Context {
             if (evaluate[f] && feats[f].num_bins && feats[f].kind == SROCM_BINS_CATEGORICAL)
                 fail(SROCM_ERR_UNSUPPORTED, "categorical split search runs on the cpu backend only");
     }
-
-    // Enqueues the scan and select of `jobs` (already uploaded to d_jobs) and the readback of their results.
-    void enqueue_scan(uint32_t njobs, const srocm_split_config &cfg, double sg, double sh) {
-        dim3 grid(div_up(nf, 4), njobs);
-        k_split_scan<<<grid, 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, cfg_dev(cfg), sg, sh);
-        launch_check("k_split_scan");
-        k_split_select<<<njobs, 256, 0, stream>>>(d_jobs.p, nf, cfg_dev(cfg), sg, sh, d_split.p, d_splittable.p);
-        launch_check("k_split_select");
-        hip_check(hipMemcpyAsync(h_result.p, d_split.p, njobs * sizeof(SplitOut), hipMemcpyDeviceToHost, stream), "read splits");
-        hip_check(hipMemcpyAsync(h_result.p + njobs * sizeof(SplitOut), d_splittable.p, static_cast<size_t>(njobs) * nf,
-                                 hipMemcpyDeviceToHost, stream), "read splittable");
-    }
-
-    SplitOut result_split(uint32_t j) const {
-        SplitOut o;
-        std::memcpy(&o, h_result.p + j * sizeof(SplitOut), sizeof(SplitOut));
-        return o;
-    }
-    const uint8_t *result_splittable(uint32_t njobs, uint32_t j) const { return h_result.p + njobs * sizeof(SplitOut) + static_cast<size_t>(j) * nf; }
 
     // split.rs:919-961 on a host histogram over an explicit feature table (no loaded dataset needed)
     void find_best_split(const double *hist, size_t len, const srocm_feature *features, uint32_t num_features,
@@ -918,7 +880,7 @@ struct Context {
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             dim3 grid(div_up(num_features, 4), 1);
-            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh);
+            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, nullptr);
             launch_check("k_split_scan");
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
@@ -948,22 +910,87 @@ struct Context {
     // Learner::grow on the device (learner.rs:121-352)
     // ------------------------------------------------------------------------------------------------
 
-    int take_slot() {
-        if (!spare.empty()) {
-            int s = spare.back();
-            spare.pop_back();
-            return s;
-        }
-        slots.emplace_back();
-        slots.back().alloc(2 * total_bins);
-        return static_cast<int>(slots.size() - 1);
+    // ------------------------------------------------------------------------------------------------
+    // Learner::grow on the device (learner.rs:121-352)
+    // ------------------------------------------------------------------------------------------------
+
+    DevBuf<int64_t> pool;             // histogram slots, 2 * total_bins i64 each
+    DevBuf<Plan> d_plan;
+    DevBuf<GrowCtl> d_ctl;
+    DevBuf<DLeaf> d_leaves;
+    DevBuf<uint8_t> d_splittable, d_eval, d_mask;
+    DevBuf<int32_t> d_free, d_feat_nt;
+    DevBuf<ScanJob> d_jobs;
+    DevBuf<FeatCand> d_cands;
+    struct TreeBufs {
+        DevBuf<int32_t> split_feature, left_child, right_child, leaf_parent, leaf_depth;
+        DevBuf<uint32_t> threshold_bin;
+        DevBuf<uint8_t> default_left;
+        DevBuf<float> split_gain;
+        DevBuf<double> internal_value, internal_weight, leaf_value, leaf_weight;
+        DevBuf<int64_t> internal_count, leaf_count;
+    } dtree;
+    uint32_t grow_capacity = 0;
+
+    void ensure_grow(uint32_t L) {
+        if (grow_capacity >= L && pool.p) return;
+        uint32_t S = L + 2;
+        pool.alloc(static_cast<size_t>(S) * 2 * total_bins);
+        d_plan.alloc(1);
+        d_ctl.alloc(1);
+        d_leaves.alloc(L);
+        d_splittable.alloc(static_cast<size_t>(L) * nf);
+        d_eval.alloc(nf);
+        d_mask.alloc(nf);
+        d_free.alloc(S);
+        d_jobs.alloc(2);
+        d_cands.alloc(2 * static_cast<size_t>(nf));
+        dtree.split_feature.alloc(L);
+        dtree.left_child.alloc(L);
+        dtree.right_child.alloc(L);
+        dtree.leaf_parent.alloc(L);
+        dtree.leaf_depth.alloc(L);
+        dtree.threshold_bin.alloc(L);
+        dtree.default_left.alloc(L);
+        dtree.split_gain.alloc(L);
+        dtree.internal_value.alloc(L);
+        dtree.internal_weight.alloc(L);
+        dtree.leaf_value.alloc(L);
+        dtree.leaf_weight.alloc(L);
+        dtree.internal_count.alloc(L);
+        dtree.leaf_count.alloc(L);
+        grow_capacity = L;
     }
-    void give_slot(int s) {
-        if (s >= 0) spare.push_back(s);
+
+    GrowState grow_state(const srocm_grow_spec &spec) {
+        GrowState g{};
+        g.ctl = d_ctl.p;
+        g.plan = d_plan.p;
+        g.leaves = d_leaves.p;
+        g.splittable = d_splittable.p;
+        g.free_slots = d_free.p;
+        g.jobs = d_jobs.p;
+        g.cands = d_cands.p;
+        g.evaluate = d_eval.p;
+        g.mask = d_mask.p;
+        g.feats = dfeats.p;
+        g.feat_nt = d_feat_nt.p;
+        g.tree = TreeDev{dtree.split_feature.p, dtree.threshold_bin.p, dtree.default_left.p, dtree.left_child.p,
+                         dtree.right_child.p, dtree.split_gain.p, dtree.internal_value.p, dtree.internal_weight.p,
+                         dtree.internal_count.p, dtree.leaf_value.p, dtree.leaf_weight.p, dtree.leaf_count.p,
+                         dtree.leaf_parent.p, dtree.leaf_depth.p};
+        g.pool = pool.p;
+        g.slot_stride = 2 * total_bins;
+        g.nf = nf;
+        g.num_leaves = spec.num_leaves;
+        g.max_depth = spec.max_depth;
+        g.cfg = cfg_dev(spec.cfg);
+        g.sg = spec.grad_scale;
+        g.sh = spec.hess_scale;
+        return g;
     }
 
     void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves);
-    void set_job_counts(int64_t parent_count);
 
     void copy_tree(const HostTree &t, const std::vector<GrowLeaf> &leaves, srocm_grown_tree *out) const {
         if (out->capacity_leaves < t.num_leaves) fail(SROCM_ERR_DEVICE, "grown tree has more leaves than the output holds");
@@ -1060,175 +1087,130 @@ std::pair<double, double> Context::compute_gradients() {
     return read_maxima();
 }
 
-__global__ void k_job_counts(ScanJob *jobs, const uint32_t *dev_left, int64_t parent_count) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        int64_t left = static_cast<int64_t>(*dev_left);
-        jobs[0].count = left;
-        jobs[1].count = parent_count - left;
-    }
-}
-
-void Context::set_job_counts(int64_t parent_count) {
-    k_job_counts<<<1, 64, 0, stream>>>(d_jobs.p, scalars.p, parent_count);
-    launch_check("k_job_counts");
-}
-
-// learner.rs:121-352 with histograms, subtraction, split search and partition on the device and one
-// readback per split (the left count and both children's best splits).
+// learner.rs:121-352 on the device: every split step is enqueued without waiting; the device picks the leaf,
+// partitions, histograms the smaller child, subtracts, searches both children and updates the tree. The host reads
+// the finished tree once.
 void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits,
                    std::vector<GrowLeaf> &leaves) {
     require_loaded();
     if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
     check_range(spec.root);
-    const srocm_split_config &cfg = spec.cfg;
+    if (spec.num_leaves < 1) fail(SROCM_ERR_CONFIG, "num_leaves must be positive");
+    const uint32_t L = spec.num_leaves;
     std::vector<uint8_t> mask(spec.feature_mask, spec.feature_mask + nf);
     check_numerical(mask.data());
-    auto depth_allows = [&](int32_t d) { return spec.max_depth <= 0 || d < spec.max_depth; };  // learner.rs:178-180
-    auto may_split = [&](int32_t d, int64_t l, int64_t r) {                                      // learner.rs:172-175
-        int64_t min_pair = 2 * cfg.min_data_in_leaf;
-        return depth_allows(d) && (l >= min_pair || r >= min_pair);
-    };
-    // every slot back to the pool
-    spare.clear();
-    for (size_t i = 0; i < slots.size(); ++i) spare.push_back(static_cast<int>(i));
-    tree = HostTree{};
-    splits.clear();
-    leaves.assign(1, GrowLeaf{});
-    leaves[0].range = spec.root;
-    leaves[0].count = spec.root_count;
-    leaves[0].splittable.assign(nf, 1);
-    ensure_scan(2);
+    ensure_grow(L);
     int32_t sums_feature = -1;
     for (uint32_t f = 0; f < nf; ++f)
         if (feats[f].num_bins) {
             sums_feature = static_cast<int32_t>(f);
             break;
         }
-    const uint64_t all_columns = nt_feat.size();
-    if (sums_feature >= 0 && may_split(0, spec.root_count, 0)) {
-        int slot = take_slot();
-        launch_hist(spec.root.begin, spec.root.count, nullptr, 0, slots[slot].p, nullptr, all_columns);
-        const srocm_feature &m = feats[sums_feature];
-        h_hist.alloc(2 * static_cast<size_t>(m.num_bins));
-        hip_check(hipMemcpyAsync(h_hist.p, slots[slot].p + 2 * static_cast<size_t>(m.hist_offset), 2 * m.num_bins * 8,
-                                 hipMemcpyDeviceToHost, stream), "read sums feature");
-        sync();
-        double sg = 0.0, sh = 0.0;  // split.rs:101-108
-        for (uint32_t b = 0; b < m.num_bins; ++b) {
-            sg = sg + static_cast<double>(h_hist.p[2 * b]);
-            sh = sh + static_cast<double>(h_hist.p[2 * b + 1]);
+    const srocm_split_config &cfg = spec.cfg;
+    auto depth_allows = [&](int32_t d) { return spec.max_depth <= 0 || d < spec.max_depth; };
+    bool root_searched = sums_feature >= 0 && depth_allows(0) && spec.root_count >= 2 * cfg.min_data_in_leaf;
+    GrowState g = grow_state(spec);
+    g.sums_feature = sums_feature < 0 ? 0u : static_cast<uint32_t>(sums_feature);
+    h_stage.alloc(nf + 64);
+    std::memcpy(h_stage.p, mask.data(), nf);
+    hip_check(hipMemcpyAsync(d_mask.p, h_stage.p, nf, hipMemcpyHostToDevice, stream), "upload mask");
+    k_grow_init<<<1, 256, 0, stream>>>(g, spec.root.begin, spec.root.count, spec.root_count, L + 2, root_searched ? 1u : 0u);
+    launch_check("k_grow_init");
+    uint64_t used_root = 0;
+    for (uint32_t f = 0; f < nf; ++f)
+        if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
+    if (root_searched) {
+        // the root histogram goes into slot 0, the first one k_grow_init takes off the free list
+        launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
+        k_root_prep<<<1, 256, 0, stream>>>(g);
+        launch_check("k_root_prep");
+        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr);
+        launch_check("k_split_scan");
+        k_root_select<<<1, 256, 0, stream>>>(g);
+        launch_check("k_root_select");
+        // split steps: each is a no-op once the tree has stopped
+        PartArgs pa = part_args(0, 0);
+        pa.plan = d_plan.p;
+        pa.colbase = train.col.p;
+        for (uint32_t s = 0; s + 1 < L; ++s) {
+            run_partition(pa, spec.root.count);
+            launch_hist(0, spec.root.count, nullptr, 0, nullptr, nullptr, 0, d_plan.p);
+            k_split_scan<<<dim3(div_up(nf, 4), 2), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, d_plan.p);
+            launch_check("k_split_scan");
+            k_apply<<<1, 256, 0, stream>>>(g);
+            launch_check("k_apply");
         }
-        leaves[0].ug = sg;
-        leaves[0].uh = sh;
-        leaves[0].slot = slot;
-        ScanJob job{slots[slot].p, sg, sh, spec.root_count, d_cands.p};
-        upload_jobs(&job, 1, mask.data());
-        enqueue_scan(1, cfg, spec.grad_scale, spec.hess_scale);
-        sync();
-        leaves[0].best = result_split(0);
-        leaves[0].has_best = leaves[0].best.found != 0;
-        leaves[0].splittable.assign(result_splittable(1, 0), result_splittable(1, 0) + nf);
     }
-    std::vector<uint8_t> evaluate(nf);
-    while (tree.num_leaves < spec.num_leaves) {
-        // learner.rs:418-429 best_leaf
-        int best = -1;
-        double best_gain = 0.0;
-        for (size_t i = 0; i < leaves.size(); ++i) {
-            if (!leaves[i].has_best) continue;
-            if (best < 0 || leaves[i].best.gain > best_gain) {
-                best = static_cast<int>(i);
-                best_gain = leaves[i].best.gain;
-            }
-        }
-        if (best < 0 || !(best_gain > 0.0)) break;
-        // learner.rs:249-352 split_leaf
-        uint32_t index = static_cast<uint32_t>(best);
-        SplitOut info = leaves[index].best;
-        leaves[index].has_best = false;
-        const srocm_feature &meta = feats[info.feature];
-        srocm_bin_split bs{};  // learner.rs:432-452
-        for (uint32_t b = 0; b <= info.threshold; ++b) bs.left_bins[b / 32] |= 1u << (b % 32);
-        if (info.default_left && meta.nan_bin) bs.left_bins[(meta.num_bins - 1) / 32] |= 1u << ((meta.num_bins - 1) % 32);
-        bs.group = meta.group;
-        bs.column = meta.column;
-        srocm_leaf_range parent_range = leaves[index].range;
-        int64_t parent_count = leaves[index].count;
-        bool may_search = leaves[index].slot >= 0 && tree.num_leaves + 1 < spec.num_leaves &&
-                          depth_allows(tree.leaf_depth[index] + 1);
-        uint32_t built_side = info.left_count <= info.right_count ? 0u : 1u;
-        for (uint32_t f = 0; f < nf; ++f) evaluate[f] = mask[f] && leaves[index].splittable[f];
-        enqueue_partition(parent_range, bs);
-        int parent_slot = leaves[index].slot;
-        int built_slot = -1;
-        if (may_search) {
-            built_slot = take_slot();
-            uint64_t used_cols = 0;
-            for (uint32_t f = 0; f < nf; ++f)
-                if (evaluate[f] && feats[f].num_bins) ++used_cols;
-            launch_hist(parent_range.begin, parent_range.count, scalars.p, built_side, slots[built_slot].p, slots[parent_slot].p, used_cols);
-            // both children, with their exact counts from the device-side left count
-            ScanJob jobs[2];
-            double lug = info.left_grad, luh = info.left_hess, rug = info.right_grad, ruh = info.right_hess;
-            jobs[0] = ScanJob{slots[built_side == 0 ? built_slot : parent_slot].p, lug, luh, 0, d_cands.p};
-            jobs[1] = ScanJob{slots[built_side == 0 ? parent_slot : built_slot].p, rug, ruh, 0, d_cands.p + nf};
-            upload_jobs(jobs, 2, evaluate.data());
-            set_job_counts(parent_count);
-            enqueue_scan(2, cfg, spec.grad_scale, spec.hess_scale);
-        }
-        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
-        sync();
-        uint32_t left_local = h_u32.p[0];
-        int64_t left_count = left_local;
-        int64_t right_count = parent_count - left_count;
-        if (left_count <= 0 || right_count <= 0)
-            fail(SROCM_ERR_INTERNAL, "split of leaf " + std::to_string(index) + " on feature " + std::to_string(info.feature) + " sends " +
-                                         std::to_string(left_count) + " rows left and " + std::to_string(right_count) + " right");
-        if (prof.on && may_search) {
-            uint64_t used_cols = 0;
-            for (uint32_t f = 0; f < nf; ++f)
-                if (evaluate[f] && feats[f].num_bins) ++used_cols;
-            double built_rows = built_side == 0 ? static_cast<double>(left_count) : static_cast<double>(right_count);
-            prof.hist_rows += built_rows;
-            prof.hist_bins += built_rows * static_cast<double>(used_cols);
-        }
-        float gain32 = static_cast<float>(info.gain + cfg.min_gain_to_split);
-        uint32_t right_index = tree.split(index, info.feature, info.threshold, info.default_left != 0, info.left_output, info.right_output,
-                                          left_count, right_count, info.left_hess * spec.hess_scale, info.right_hess * spec.hess_scale, gain32);
-        if (right_index != leaves.size()) fail(SROCM_ERR_INTERNAL, "tree numbered the new leaf unexpectedly");
-        splits.push_back(bs);
-        GrowLeaf left, right;
-        left.range = srocm_leaf_range{parent_range.begin, left_local};
-        left.ug = info.left_grad;
-        left.uh = info.left_hess;
-        left.count = left_count;
-        right.range = srocm_leaf_range{parent_range.begin + left_local, parent_range.count - left_local};
-        right.ug = info.right_grad;
-        right.uh = info.right_hess;
-        right.count = right_count;
-        int32_t depth = tree.leaf_depth[index];
-        bool searched = may_split(depth, left_count, right_count);
-        if (may_search && searched) {
-            int built_leaf_slot = built_slot, other_leaf_slot = parent_slot;
-            GrowLeaf &lb = built_side == 0 ? left : right;
-            GrowLeaf &lo = built_side == 0 ? right : left;
-            lb.slot = built_leaf_slot;
-            lo.slot = other_leaf_slot;
-            for (int side = 0; side < 2; ++side) {
-                GrowLeaf &l = side == 0 ? left : right;
-                l.best = result_split(side);
-                l.has_best = l.best.found != 0;
-                l.splittable.assign(result_splittable(2, side), result_splittable(2, side) + nf);
-            }
-        } else {
-            give_slot(parent_slot);
-            give_slot(built_slot);
-        }
-        leaves[index] = std::move(left);
-        leaves.push_back(std::move(right));
+    if (root_searched) {  // every leaf's rows back in the first partition buffer
+        k_consolidate<<<dim3(std::max<uint32_t>(1, std::min<uint32_t>(div_up(spec.root.count, 256 * 8), cus)), L), 256, 0, stream>>>(
+            g, part2.p, part.p);
+        launch_check("k_consolidate");
+    }
+    // one readback: control block, leaves, tree arrays
+    size_t need = sizeof(GrowCtl) + static_cast<size_t>(L) * (sizeof(DLeaf) + 4 * 5 + 4 + 1 + 4 + 8 * 6);
+    h_result.alloc(need + 64);
+    uint8_t *hp = h_result.p;
+    auto rd = [&](void *dev, size_t bytes) {
+        hip_check(hipMemcpyAsync(hp, dev, bytes, hipMemcpyDeviceToHost, stream), "read tree");
+        uint8_t *at = hp;
+        hp += bytes;
+        return at;
+    };
+    const GrowCtl *hc = reinterpret_cast<const GrowCtl *>(rd(d_ctl.p, sizeof(GrowCtl)));
+    const DLeaf *hl = reinterpret_cast<const DLeaf *>(rd(d_leaves.p, L * sizeof(DLeaf)));
+    // 8-byte arrays first so every array stays aligned in the staging buffer
+    auto *iv = reinterpret_cast<const double *>(rd(dtree.internal_value.p, L * 8));
+    auto *iw = reinterpret_cast<const double *>(rd(dtree.internal_weight.p, L * 8));
+    auto *lv = reinterpret_cast<const double *>(rd(dtree.leaf_value.p, L * 8));
+    auto *lw = reinterpret_cast<const double *>(rd(dtree.leaf_weight.p, L * 8));
+    auto *ic = reinterpret_cast<const int64_t *>(rd(dtree.internal_count.p, L * 8));
+    auto *lcn = reinterpret_cast<const int64_t *>(rd(dtree.leaf_count.p, L * 8));
+    auto *sf = reinterpret_cast<const int32_t *>(rd(dtree.split_feature.p, L * 4));
+    auto *lc = reinterpret_cast<const int32_t *>(rd(dtree.left_child.p, L * 4));
+    auto *rc = reinterpret_cast<const int32_t *>(rd(dtree.right_child.p, L * 4));
+    auto *lp = reinterpret_cast<const int32_t *>(rd(dtree.leaf_parent.p, L * 4));
+    auto *ld = reinterpret_cast<const int32_t *>(rd(dtree.leaf_depth.p, L * 4));
+    auto *tb = reinterpret_cast<const uint32_t *>(rd(dtree.threshold_bin.p, L * 4));
+    auto *sgn = reinterpret_cast<const float *>(rd(dtree.split_gain.p, L * 4));
+    auto *dl = reinterpret_cast<const uint8_t *>(rd(dtree.default_left.p, L));
+    sync();
+    if (hc->error == 1) fail(SROCM_ERR_INTERNAL, "a split sent no rows to one side");
+    if (hc->error) fail(SROCM_ERR_INTERNAL, "no free histogram slot");
+    uint32_t n = hc->num_leaves;
+    tree = HostTree{};
+    tree.num_leaves = n;
+    uint32_t ni = n - 1;
+    tree.split_feature.assign(sf, sf + ni);
+    tree.left_child.assign(lc, lc + ni);
+    tree.right_child.assign(rc, rc + ni);
+    tree.threshold_bin.assign(tb, tb + ni);
+    tree.default_left.assign(dl, dl + ni);
+    tree.split_gain.assign(sgn, sgn + ni);
+    tree.internal_value.assign(iv, iv + ni);
+    tree.internal_weight.assign(iw, iw + ni);
+    tree.internal_count.assign(ic, ic + ni);
+    tree.leaf_value.assign(lv, lv + n);
+    tree.leaf_weight.assign(lw, lw + n);
+    tree.leaf_count.assign(lcn, lcn + n);
+    tree.leaf_parent.assign(lp, lp + n);
+    tree.leaf_depth.assign(ld, ld + n);
+    leaves.assign(n, GrowLeaf{});
+    for (uint32_t i = 0; i < n; ++i) leaves[i].range = srocm_leaf_range{hl[i].begin, hl[i].count};
+    splits.assign(ni, srocm_bin_split{});
+    for (uint32_t k = 0; k < ni; ++k) {  // learner.rs:432-452
+        const srocm_feature &m = feats[tree.split_feature[k]];
+        srocm_bin_split &bs = splits[k];
+        for (uint32_t b = 0; b <= tree.threshold_bin[k]; ++b) bs.left_bins[b / 32] |= 1u << (b % 32);
+        if (tree.default_left[k] && m.nan_bin) bs.left_bins[(m.num_bins - 1) / 32] |= 1u << ((m.num_bins - 1) % 32);
+        bs.group = m.group;
+        bs.column = m.column;
+    }
+    if (prof.on && root_searched) {
+        prof.hist_builds += 1.0 + hc->hist_builds;
+        prof.hist_rows += static_cast<double>(spec.root.count) + hc->hist_rows;
+        prof.hist_bins += static_cast<double>(spec.root.count) * static_cast<double>(used_root) + hc->hist_bins;
     }
 }
-
 
 // boosting.rs:100-108 and objective/mod.rs:92-109
 double Context::boost_init(const srocm_train_params &p) {
