@@ -64,18 +64,22 @@ def main():
     t0 = time.perf_counter()
     timed = trainer.step(args.steps)
     elapsed = time.perf_counter() - t0
-    prof = (C.c_double * 8)()
-    trainer.backend._check(lib.srocm_profile_read(h, prof))
+    prof = (C.c_double * 12)()
+    trainer.backend._check(lib.srocm_profile_read(h, prof, 12))
     trainer.backend._check(lib.srocm_profile(h, 0))
     if len(timed) != args.steps:
         log(f"training ended after {len(timed)} of {args.steps} timed iterations")
-    launches, hist_ms, hist_rows, hist_bins, hist_bytes, part_launches, part_ms, part_rows = list(prof)
+    (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
+     part_rows, _, _) = list(prof)
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
-    bins_per_s = hist_bins / (hist_ms / 1e3) if hist_ms else 0.0
-    achieved_gbps = (hist_bytes / launches) / (hist_ms / 1e3 / launches) / 1e9 if launches else 0.0
-    log(f"{steps} iterations in {elapsed:.3f}s; histogram: {launches:.0f} launches, {hist_ms:.1f} ms, "
-        f"{achieved_gbps:.0f} GB/s algorithmic; partition {part_launches:.0f} launches {part_ms:.1f} ms")
+    # every histogram is built by k_hist (roots) or k_step_rows (split steps, which also partition)
+    bins_per_s = hist_bins / ((hist_ms + step_ms) / 1e3) if hist_ms + step_ms else 0.0
+    step_gbps = step_bytes / (step_ms / 1e3) / 1e9 if step_ms else 0.0
+    root_gbps = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms else 0.0
+    log(f"{steps} iterations in {elapsed:.3f}s; k_step_rows: {step_launches:.0f} launches, {step_ms:.1f} ms, "
+        f"{step_gbps:.0f} GB/s algorithmic; k_hist (roots): {hist_launches:.0f} launches, {hist_ms:.1f} ms, "
+        f"{root_gbps:.0f} GB/s; {builds:.0f} histograms, {part_rows:.3g} rows partitioned")
 
     cpu = None
     if not args.no_cpu:
@@ -133,12 +137,15 @@ def main():
                                "num_grad_quant_bins=4", "rows": args.rows, "features": args.cols,
                    "num_leaves": args.leaves, "total_bins": data.total_bins, "parallelism": "single GPU"},
         "hist_bins_per_s": bins_per_s,
-        "hist_kernel_ms_per_step": hist_ms / steps,
-        "partition_ms_per_step": part_ms / steps,
-        "roofline": {"bound": "hbm", "achieved": achieved_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "k_hist<128>", "launches": launches,
-                     "avg_launch_us": hist_ms / launches * 1e3 if launches else None},
+        "step_kernel_ms_per_iter": step_ms / steps,
+        "root_hist_ms_per_iter": hist_ms / steps,
+        "roofline": {"bound": "hbm", "achieved": step_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": step_gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "k_step_rows<128> (split step: stable partition + built-child histogram)",
+                     "launches": step_launches, "avg_launch_us": step_ms / step_launches * 1e3 if step_launches else None,
+                     "bytes_per_launch": step_bytes / step_launches if step_launches else None,
+                     "root_k_hist": {"launches": hist_launches, "achieved": root_gbps,
+                                     "avg_launch_us": hist_ms / hist_launches * 1e3 if hist_launches else None}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -337,12 +337,19 @@ int srocm_boost_init(void *ctx, const srocm_train_params *params, double *init_s
 int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iteration, uint32_t count,
                 srocm_grown_tree *trees, uint32_t *trained);
 
-/* Per-kernel timing with HIP events on the backend's stream: enable (1) resets the counters. `out` receives
- * {histogram kernel launches (k_hist, one per slab per build), their total ms, rows histogrammed, row x
- * used-column bins, algorithmic histogram bytes (rows x (used columns + 8 B) + 8 B x total_bins per build),
- * partition launches, partition ms (count + scatter + copy), partition rows}. */
+/* Per-kernel timing with HIP events on the backend's stream, and algorithmic byte counts; no counterpart in the
+ * reference (a measurement hook). srocm_profile: enable (1) or disable (0); either resets the counters.
+ * srocm_profile_read writes min(len, SROCM_PROFILE_VALUES) values:
+ *   [0] k_hist launches (root and trait histograms, one per slab)   [1] their ms   [2] their algorithmic bytes
+ *   [3] k_step_rows launches (split steps: partition + built-child histogram)   [4] their ms
+ *   [5] their algorithmic bytes (9 B per partitioned row + used columns + 4 B per histogrammed row)
+ *   [6] histogram builds   [7] rows histogrammed   [8] rows x used columns   [9] rows partitioned
+ *   [10] trait partition launches   [11] their ms (count + scatter + copy back)
+ * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
+ * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
+#define SROCM_PROFILE_VALUES 12
 int srocm_profile(void *ctx, int enable);
-int srocm_profile_read(void *ctx, double *out8);
+int srocm_profile_read(void *ctx, double *out, uint32_t len);
 
 #ifdef __cplusplus
 }

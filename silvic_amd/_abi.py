@@ -166,7 +166,7 @@ _SIGNATURES = {
     "srocm_boost": (C.c_int, [_P, C.POINTER(TrainParams), C.c_uint32, C.c_uint32, C.POINTER(GrownTree),
                               C.POINTER(C.c_uint32)]),
     "srocm_profile": (C.c_int, [_P, C.c_int]),
-    "srocm_profile_read": (C.c_int, [_P, C.POINTER(C.c_double)]),
+    "srocm_profile_read": (C.c_int, [_P, C.POINTER(C.c_double), C.c_uint32]),
 }
 
 EXPORTS = tuple(_SIGNATURES)

@@ -242,6 +242,7 @@ struct Slab {
     std::vector<uint32_t> feats;  // feature ids
     DevBuf<uint8_t> bins;         // [rows][width]
     DevBuf<uint32_t> col_offset, col_bins;
+    uint64_t step_partial_off = 0;  // the slab's partials in the step partial buffer, in {g, h} pairs
 };
 
 struct DevData {
@@ -250,12 +251,19 @@ struct DevData {
     DevBuf<float> scores;
 };
 
+// Event timing of the histogram-building kernels and algorithmic byte counts (see srocm_profile_read).
 struct Profile {
     bool on = false;
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> hist_events, part_events;
-    double hist_launches = 0, hist_builds = 0, hist_rows = 0, hist_bins = 0, hist_bytes = 0, part_launches = 0, part_rows = 0;
-    double hist_ms = 0, part_ms = 0;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> hist_events, step_events, part_events;
+    double hist_launches = 0, hist_ms = 0, hist_bytes = 0;  // k_hist: root and trait histograms
+    double step_launches = 0, step_ms = 0, step_bytes = 0;  // k_step_rows: split steps
+    double builds = 0, rows = 0, bins = 0, part_rows = 0;
+    double part_launches = 0, part_ms = 0;                  // trait partitions
     std::vector<hipEvent_t> pool;
+    void reset() {
+        hist_launches = hist_ms = hist_bytes = step_launches = step_ms = step_bytes = 0;
+        builds = rows = bins = part_rows = part_launches = part_ms = 0;
+    }
 };
 
 struct GrowLeaf {
@@ -295,6 +303,11 @@ struct Context {
     DevBuf<int32_t> packed, partial;
     DevBuf<uint32_t> part, part2, block_left, scalars;
     DevBuf<FeatDev> dfeats;
+    DevBuf<ColGroup> d_cgs;
+    DevBuf<uint32_t> gcol_offset, gcol_bins;
+    DevBuf<int32_t> gcol_feat;
+    uint32_t ncg = 0;
+    uint64_t step_partial_pairs = 0;
     uint32_t part_len = 0;
     std::vector<uint8_t> used;
     uint32_t objective = SROCM_OBJ_REGRESSION;
@@ -320,6 +333,10 @@ struct Context {
             (void)hipEventDestroy(e.second);
         }
         for (auto &e : prof.part_events) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        for (auto &e : prof.step_events) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
         }
@@ -433,11 +450,11 @@ struct Context {
         scalars.alloc(16);
         partial.alloc(static_cast<size_t>(cus) * 256 * max_width * 2);
         std::vector<FeatDev> fd(nf);
-        for (uint32_t f = 0; f < nf; ++f) fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin};
+        for (uint32_t f = 0; f < nf; ++f)
+            fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin,
+                            feat_nt[f] < 0 ? 0u : static_cast<uint32_t>(feat_nt[f])};
         dfeats.alloc(nf);
         hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
-        d_feat_nt.alloc(nf);
-        hip_check(hipMemcpy(d_feat_nt.p, feat_nt.data(), nf * sizeof(int32_t), hipMemcpyHostToDevice), "upload features");
         for (auto &s : slabs) {
             std::vector<uint32_t> off(s.width, 0), nb(s.width, 0);
             for (size_t c = 0; c < s.feats.size(); ++c) {
@@ -448,6 +465,37 @@ struct Context {
             s.col_bins.alloc(s.width);
             hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
+        }
+        // groups of 8 slab columns for k_step_finish, and the global column arrays they index
+        {
+            std::vector<ColGroup> cg;
+            std::vector<uint32_t> goff, gbins;
+            std::vector<int32_t> gfeat;
+            uint64_t poff = 0;
+            for (auto &s : slabs) {
+                s.step_partial_off = poff;
+                uint32_t gbase = static_cast<uint32_t>(goff.size());
+                for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) cg.push_back(ColGroup{poff, s.width, c0, gbase + c0, 0});
+                for (uint32_t c = 0; c < s.width; ++c) {
+                    bool real = c < s.feats.size();
+                    goff.push_back(real ? feats[s.feats[c]].hist_offset : 0u);
+                    gbins.push_back(real ? feats[s.feats[c]].num_bins : 0u);
+                    gfeat.push_back(real ? static_cast<int32_t>(s.feats[c]) : -1);
+                }
+                poff += static_cast<uint64_t>(cus) * step_partial_stride(s.width);
+            }
+            ncg = static_cast<uint32_t>(cg.size());
+            step_partial_pairs = std::max<uint64_t>(poff, 1);
+            d_cgs.alloc(std::max<size_t>(cg.size(), 1));
+            gcol_offset.alloc(std::max<size_t>(goff.size(), 1));
+            gcol_bins.alloc(std::max<size_t>(goff.size(), 1));
+            gcol_feat.alloc(std::max<size_t>(goff.size(), 1));
+            if (!cg.empty()) {
+                hip_check(hipMemcpy(d_cgs.p, cg.data(), cg.size() * sizeof(ColGroup), hipMemcpyHostToDevice), "upload column groups");
+                hip_check(hipMemcpy(gcol_offset.p, goff.data(), goff.size() * 4, hipMemcpyHostToDevice), "upload columns");
+                hip_check(hipMemcpy(gcol_bins.p, gbins.data(), gbins.size() * 4, hipMemcpyHostToDevice), "upload columns");
+                hip_check(hipMemcpy(gcol_feat.p, gfeat.data(), gfeat.size() * 4, hipMemcpyHostToDevice), "upload columns");
+            }
         }
         used.assign(nf, 1);
         part_len = 0;
@@ -579,12 +627,11 @@ struct Context {
 
     // The histogram of rows part[begin..+count] (or the `side` child of that range split at *dev_left) into
     // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
-    // With `plan`, the leaf is the plan's built child and out/parent are its slots in `pool` (count: an upper bound).
     void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
-                     int64_t *parent, uint64_t bins_used, const Plan *plan = nullptr) {
+                     int64_t *parent, uint64_t bins_used) {
         uint32_t grid = hist_groups(count);
         for (auto &s : slabs) {
-            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS, plan, part2.p};
+            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS, nullptr, nullptr};
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (prof.on) {
                 e0 = event();
@@ -603,15 +650,16 @@ struct Context {
                 prof.hist_launches += 1;
             }
             ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width,
-                         plan, pool.p, 2 * total_bins};
+                         nullptr, nullptr, 0};
             k_hist_reduce<<<div_up(256ull * s.width, 256), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
-        if (prof.on && !plan) {
-            prof.hist_builds += 1;
-            if (!dev_left) {
-                prof.hist_rows += count;
-                prof.hist_bins += static_cast<double>(count) * static_cast<double>(bins_used);
+        if (prof.on) {
+            prof.builds += 1;
+            if (!dev_left) {  // rows known on the host: rows x (used columns + 4 B gradients + 4 B row id) + the output
+                prof.rows += count;
+                prof.bins += static_cast<double>(count) * static_cast<double>(bins_used);
+                prof.hist_bytes += static_cast<double>(count) * (static_cast<double>(bins_used) + 8.0) + 16.0 * static_cast<double>(total_bins);
             }
         }
     }
@@ -854,7 +902,7 @@ struct Context {
             if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
             if (m.num_bins && static_cast<uint64_t>(m.hist_offset) + m.num_bins > len / 2)
                 fail(SROCM_ERR_DEVICE, "feature " + std::to_string(f) + " lies outside the histogram");
-            fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin};
+            fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin, 0u};
         }
         std::vector<int64_t> units(len);
         for (size_t i = 0; i < len; ++i) units[i] = static_cast<int64_t>(hist[i]);
@@ -910,18 +958,19 @@ struct Context {
     // Learner::grow on the device (learner.rs:121-352)
     // ------------------------------------------------------------------------------------------------
 
-    // ------------------------------------------------------------------------------------------------
-    // Learner::grow on the device (learner.rs:121-352)
-    // ------------------------------------------------------------------------------------------------
-
     DevBuf<int64_t> pool;             // histogram slots, 2 * total_bins i64 each
     DevBuf<Plan> d_plan;
     DevBuf<GrowCtl> d_ctl;
     DevBuf<DLeaf> d_leaves;
     DevBuf<uint8_t> d_splittable, d_eval, d_mask;
-    DevBuf<int32_t> d_free, d_feat_nt;
+    DevBuf<LeafKey> d_keys;
     DevBuf<ScanJob> d_jobs;
     DevBuf<FeatCand> d_cands;
+    // split steps (k_step_rows, k_step_finish)
+    DevBuf<int32_t> step_partial;            // per slab: [cus][256 * W] {g, h}
+    DevBuf<unsigned long long> tile_status;  // per partition tile
+    DevBuf<uint32_t> fin_counts;             // [ncg] chunk counters, then the column-group counter
+    uint64_t epochs_used = 0;
     struct TreeBufs {
         DevBuf<int32_t> split_feature, left_child, right_child, leaf_parent, leaf_depth;
         DevBuf<uint32_t> threshold_bin;
@@ -934,16 +983,15 @@ struct Context {
 
     void ensure_grow(uint32_t L) {
         if (grow_capacity >= L && pool.p) return;
-        uint32_t S = L + 2;
-        pool.alloc(static_cast<size_t>(S) * 2 * total_bins);
+        pool.alloc(static_cast<size_t>(L) * 2 * total_bins);  // a slot per leaf
+        d_keys.alloc(L);
         d_plan.alloc(1);
         d_ctl.alloc(1);
         d_leaves.alloc(L);
         d_splittable.alloc(static_cast<size_t>(L) * nf);
         d_eval.alloc(nf);
         d_mask.alloc(nf);
-        d_free.alloc(S);
-        d_jobs.alloc(2);
+        d_jobs.alloc(1);
         d_cands.alloc(2 * static_cast<size_t>(nf));
         dtree.split_feature.alloc(L);
         dtree.left_child.alloc(L);
@@ -959,7 +1007,19 @@ struct Context {
         dtree.leaf_weight.alloc(L);
         dtree.internal_count.alloc(L);
         dtree.leaf_count.alloc(L);
+        step_partial.alloc(2 * step_partial_pairs);
+        tile_status.alloc(div_up(rows, STEP_TILE) + 1);
+        fin_counts.alloc(ncg + 1);
+        reset_step_state();
         grow_capacity = L;
+    }
+
+    // Tile status words carry the step's epoch; the counters are returned to zero by the kernels themselves.
+    void reset_step_state() {
+        hip_check(hipMemsetAsync(d_ctl.p, 0, sizeof(GrowCtl), stream), "zero grow control");
+        hip_check(hipMemsetAsync(tile_status.p, 0, tile_status.n * sizeof(unsigned long long), stream), "zero tile status");
+        hip_check(hipMemsetAsync(fin_counts.p, 0, fin_counts.n * sizeof(uint32_t), stream), "zero step counters");
+        epochs_used = 0;
     }
 
     GrowState grow_state(const srocm_grow_spec &spec) {
@@ -968,13 +1028,12 @@ struct Context {
         g.plan = d_plan.p;
         g.leaves = d_leaves.p;
         g.splittable = d_splittable.p;
-        g.free_slots = d_free.p;
+        g.keys = d_keys.p;
         g.jobs = d_jobs.p;
         g.cands = d_cands.p;
         g.evaluate = d_eval.p;
         g.mask = d_mask.p;
         g.feats = dfeats.p;
-        g.feat_nt = d_feat_nt.p;
         g.tree = TreeDev{dtree.split_feature.p, dtree.threshold_bin.p, dtree.default_left.p, dtree.left_child.p,
                          dtree.right_child.p, dtree.split_gain.p, dtree.internal_value.p, dtree.internal_weight.p,
                          dtree.internal_count.p, dtree.leaf_value.p, dtree.leaf_weight.p, dtree.leaf_count.p,
@@ -1031,27 +1090,23 @@ struct Context {
     void profile(int enable) {
         settle_profile();
         prof.on = enable != 0;
-        prof.hist_launches = prof.hist_builds = prof.hist_rows = prof.hist_bins = prof.hist_bytes = prof.part_launches = prof.part_rows = 0;
-        prof.hist_ms = prof.part_ms = 0;
+        prof.reset();
     }
     void settle_profile() {
         sync();
-        for (auto &e : prof.hist_events) {
-            float ms = 0;
-            hip_check(hipEventElapsedTime(&ms, e.first, e.second), "event elapsed");
-            prof.hist_ms += ms;
-            prof.pool.push_back(e.first);
-            prof.pool.push_back(e.second);
-        }
-        prof.hist_events.clear();
-        for (auto &e : prof.part_events) {
-            float ms = 0;
-            hip_check(hipEventElapsedTime(&ms, e.first, e.second), "event elapsed");
-            prof.part_ms += ms;
-            prof.pool.push_back(e.first);
-            prof.pool.push_back(e.second);
-        }
-        prof.part_events.clear();
+        auto settle = [&](std::vector<std::pair<hipEvent_t, hipEvent_t>> &events, double &total) {
+            for (auto &e : events) {
+                float ms = 0;
+                hip_check(hipEventElapsedTime(&ms, e.first, e.second), "event elapsed");
+                total += ms;
+                prof.pool.push_back(e.first);
+                prof.pool.push_back(e.second);
+            }
+            events.clear();
+        };
+        settle(prof.hist_events, prof.hist_ms);
+        settle(prof.step_events, prof.step_ms);
+        settle(prof.part_events, prof.part_ms);
     }
 };
 
@@ -1111,16 +1166,18 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     bool root_searched = sums_feature >= 0 && depth_allows(0) && spec.root_count >= 2 * cfg.min_data_in_leaf;
     GrowState g = grow_state(spec);
     g.sums_feature = sums_feature < 0 ? 0u : static_cast<uint32_t>(sums_feature);
+    if (epochs_used + L > (1ull << 29)) reset_step_state();  // tile status epochs are 30 bits wide
+    epochs_used += L;
     h_stage.alloc(nf + 64);
     std::memcpy(h_stage.p, mask.data(), nf);
     hip_check(hipMemcpyAsync(d_mask.p, h_stage.p, nf, hipMemcpyHostToDevice, stream), "upload mask");
-    k_grow_init<<<1, 256, 0, stream>>>(g, spec.root.begin, spec.root.count, spec.root_count, L + 2, root_searched ? 1u : 0u);
+    k_grow_init<<<1, 64, 0, stream>>>(g, spec.root.begin, spec.root.count, spec.root_count, root_searched ? 1u : 0u);
     launch_check("k_grow_init");
     uint64_t used_root = 0;
     for (uint32_t f = 0; f < nf; ++f)
         if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
     if (root_searched) {
-        // the root histogram goes into slot 0, the first one k_grow_init takes off the free list
+        // the root histogram goes into slot 0
         launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
         k_root_prep<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_prep");
@@ -1129,16 +1186,32 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         k_root_select<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_select");
         // split steps: each is a no-op once the tree has stopped
-        PartArgs pa = part_args(0, 0);
-        pa.plan = d_plan.p;
-        pa.colbase = train.col.p;
+        FinishArgs fa{step_partial.p, d_cgs.p, gcol_offset.p, gcol_bins.p, gcol_feat.p, fin_counts.p, fin_counts.p + ncg, ncg, cus};
         for (uint32_t s = 0; s + 1 < L; ++s) {
-            run_partition(pa, spec.root.count);
-            launch_hist(0, spec.root.count, nullptr, 0, nullptr, nullptr, 0, d_plan.p);
-            k_split_scan<<<dim3(div_up(nf, 4), 2), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, d_plan.p);
-            launch_check("k_split_scan");
-            k_apply<<<1, 256, 0, stream>>>(g);
-            launch_check("k_apply");
+            hipEvent_t e0 = nullptr, e1 = nullptr;
+            if (prof.on) {
+                e0 = event();
+                e1 = event();
+                hip_check(hipEventRecord(e0, stream), "event");
+            }
+            for (size_t si = 0; si < slabs.size(); ++si) {
+                const Slab &sl = slabs[si];
+                StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
+                            tile_status.p, d_plan.p, d_ctl.p, flush_rows(), cus, si == 0 ? 1u : 0u};
+                switch (sl.width) {
+                case 32: k_step_rows<32><<<cus, 1024, 0, stream>>>(sa); break;
+                case 64: k_step_rows<64><<<cus, 1024, 0, stream>>>(sa); break;
+                default: k_step_rows<128><<<cus, 1024, 0, stream>>>(sa); break;
+                }
+                launch_check("k_step_rows");
+            }
+            if (prof.on) {
+                hip_check(hipEventRecord(e1, stream), "event");
+                prof.step_events.emplace_back(e0, e1);
+                prof.step_launches += static_cast<double>(slabs.size());
+            }
+            k_step_finish<<<dim3(ncg, FIN_CHUNKS), 1024, 0, stream>>>(g, fa);
+            launch_check("k_step_finish");
         }
     }
     if (root_searched) {  // every leaf's rows back in the first partition buffer
@@ -1175,7 +1248,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     auto *dl = reinterpret_cast<const uint8_t *>(rd(dtree.default_left.p, L));
     sync();
     if (hc->error == 1) fail(SROCM_ERR_INTERNAL, "a split sent no rows to one side");
-    if (hc->error) fail(SROCM_ERR_INTERNAL, "no free histogram slot");
+    if (hc->error == 3) fail(SROCM_ERR_INTERNAL, "a partition tile waited too long for an earlier tile's count");
+    if (hc->error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc->error));
     uint32_t n = hc->num_leaves;
     tree = HostTree{};
     tree.num_leaves = n;
@@ -1205,10 +1279,14 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         bs.group = m.group;
         bs.column = m.column;
     }
-    if (prof.on && root_searched) {
-        prof.hist_builds += 1.0 + hc->hist_builds;
-        prof.hist_rows += static_cast<double>(spec.root.count) + hc->hist_rows;
-        prof.hist_bins += static_cast<double>(spec.root.count) * static_cast<double>(used_root) + hc->hist_bins;
+    if (prof.on && root_searched) {  // the root histogram was counted by launch_hist
+        prof.builds += hc->hist_builds;
+        prof.rows += hc->hist_rows;
+        prof.bins += hc->hist_bins;
+        prof.part_rows += hc->part_rows;
+        // partition: 4 B row id read, 1 B split bin, 4 B row id write per parent row; histogram: the built
+        // child's used columns and 4 B packed gradients per row
+        prof.step_bytes += 9.0 * hc->part_rows + hc->hist_bins + 4.0 * hc->hist_rows;
     }
 }
 
@@ -1600,15 +1678,13 @@ int srocm_profile(void *ctx, int enable) {
     return guard(ctx, [&](Context &c) { c.profile(enable); });
 }
 
-int srocm_profile_read(void *ctx, double *out8) {
+int srocm_profile_read(void *ctx, double *out, uint32_t len) {
     return guard(ctx, [&](Context &c) {
         c.settle_profile();
         const Profile &p = c.prof;
-        // algorithmic bytes of the builds: rows x (used columns x 1 B bin + 4 B packed gradients + 4 B row id)
-        // plus the 2 x total_bins x 4 B histogram write per build
-        double bytes = p.hist_bins + 8.0 * p.hist_rows + p.hist_builds * 8.0 * static_cast<double>(c.total_bins);
-        double v[8] = {p.hist_launches, p.hist_ms, p.hist_rows, p.hist_bins, bytes, p.part_launches, p.part_ms, p.part_rows};
-        if (out8) std::copy(v, v + 8, out8);
+        double v[SROCM_PROFILE_VALUES] = {p.hist_launches, p.hist_ms, p.hist_bytes, p.step_launches, p.step_ms, p.step_bytes,
+                                          p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms};
+        if (out) std::copy(v, v + std::min<uint32_t>(len, SROCM_PROFILE_VALUES), out);
     });
 }
 

@@ -225,6 +225,11 @@ struct Plan {
     int64_t parent_count;
     uint32_t used_columns;    // evaluated non-trivial features (the histogram's used columns)
     uint32_t src_buf;         // partition buffer holding the leaf's rows; its children go to the other one
+    uint32_t src_rev;         // the leaf's rows are stored in reverse order
+    uint32_t epoch;           // tags this step's partition tile status words
+    uint32_t ticket;          // next partition tile to hand out (0 at the start of the step)
+    uint32_t pad_;
+    double child_ug[2], child_uh[2];  // the children's sums in histogram units (left, right)
 };
 
 struct HistArgs {
@@ -721,7 +726,11 @@ struct FeatCand {
     double left_grad, left_hess;
     int64_t left_count;
     double left_units_g, left_units_h;
+    uint32_t col;         // the feature's column-major index (its bins for the partition)
+    uint32_t nan_idx;     // its NaN bin, or NO_BIN
 };
+
+constexpr uint32_t NO_BIN = 0xffffffffu;
 
 struct Grown {
     uint32_t bin;
@@ -730,27 +739,113 @@ struct Grown {
     double gain;
 };
 
+// Wave-wide inclusive scans with DPP row operations (gfx9: row_shr within rows of 16 lanes, then row_bcast:15
+// and row_bcast:31 across rows): each step is a VALU move, not an LDS permute.
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+// The value of the lane the DPP step reads (0 where the step has no source or leaves the lane unwritten).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, true));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    uint32_t lo = dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(v));
+    uint32_t hi = dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t bits_of(double x) { return __builtin_bit_cast(uint64_t, x); }
+__device__ __forceinline__ double double_of(uint64_t x) { return __builtin_bit_cast(double, x); }
+
+// Whether step CTRL/ROW_MASK gives `lane` a source lane (the steps of an inclusive scan, in order).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ bool dpp_has_source(uint32_t lane) {
+    const uint32_t row = lane >> 4, in_row = lane & 15u;
+    if (CTRL >= DPP_ROW_SHR1 && CTRL <= DPP_ROW_SHR1 + 14) return in_row >= static_cast<uint32_t>(CTRL - 0x110);
+    return (ROW_MASK >> row) & 1u;
+}
+
+// Inclusive sums over the wave of three exact (integer-valued) quantities.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void scan_add_step(double &g, double &h, int64_t &c) {
+    g += double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(g)));
+    h += double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(h)));
+    c += static_cast<int64_t>(dpp_u64<CTRL, ROW_MASK>(static_cast<uint64_t>(c)));
+}
+
+// A run of candidates in scan order: whether it holds the stopping candidate, and its best candidate before
+// the stop (highest gain, the first on ties; -1 when none). A run combines with the run after it: that run
+// counts only when no stop came before it.
+struct ScanRun {
+    uint32_t stopped;
+    double gain;
+    int32_t k;
+};
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void scan_run_step(ScanRun &r, uint32_t lane) {
+    ScanRun a;
+    a.stopped = dpp_u32<CTRL, ROW_MASK>(r.stopped);
+    a.gain = double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(r.gain)));
+    a.k = static_cast<int32_t>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(r.k)));
+    if (!dpp_has_source<CTRL, ROW_MASK>(lane)) return;
+    // a precedes r
+    if (a.stopped) {
+        r = a;
+    } else if (!(r.k >= 0 && (a.k < 0 || r.gain > a.gain))) {
+        r.gain = a.gain;
+        r.k = a.k;
+    }
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t lane) {
+    uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
+    uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // One scan direction over `n` bins of a feature's histogram slice `h` (i64 {g,h} pairs): element k is bin
 // t0 + step * k. Lane l holds elements 4l..4l+3. Returns whether a candidate beat min_gain_shift.
+// split.rs:420-462: candidates run until the first one where the other side is too small while the growing side
+// is not (excluded); each has the gain of its two sides, -inf when the growing side is too small; the best is
+// the first maximum (split.rs:508-531); all of it as one ordered wave scan.
 __device__ bool wave_scan(const Ctx &c, const SplitCfgDev &cfg, const int64_t *h, int t0, int step, int n, Grown &out) {
-    const int lane = threadIdx.x & 63;
+    const uint32_t lane = threadIdx.x & 63u;
     double pg[4], ph[4];
     int64_t pc[4];
     double lg = 0.0, lh = 0.0;
     int64_t lc = 0;
+    double gu[4], hu[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        int k = 4 * lane + j;
-        double gu = 0.0, hu = 0.0;
-        int64_t ci = 0;
-        if (k < n) {
-            int t = t0 + step * k;
-            gu = static_cast<double>(h[2 * t]);
-            hu = static_cast<double>(h[2 * t + 1]);
-            ci = sat_i64(hu * c.scale_hess * c.cnt_factor + 0.5);  // split.rs:196-198, 236-238
-        }
-        lg += gu;
-        lh += hu;
+        int k = 4 * static_cast<int>(lane) + j;
+        int t = t0 + step * (k < n ? k : 0);
+        gu[j] = k < n ? static_cast<double>(h[2 * t]) : 0.0;
+        hu[j] = k < n ? static_cast<double>(h[2 * t + 1]) : 0.0;
+    }
+    // per-bin counts (split.rs:196-198, 236-238): `(x + 0.5) as i64`; one conversion when the wave's are all in u32
+    double xc[4];
+    bool small = true;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int k = 4 * static_cast<int>(lane) + j;
+        xc[j] = k < n ? hu[j] * c.scale_hess * c.cnt_factor + 0.5 : 0.0;
+        small = small && xc[j] >= 0.0 && xc[j] < 4294967296.0;
+    }
+    int64_t cis[4];
+    if (__all(small)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cis[j] = static_cast<int64_t>(static_cast<uint32_t>(xc[j]));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cis[j] = sat_i64(xc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int64_t ci = cis[j];
+        lg += gu[j];
+        lh += hu[j];
         lc += ci;
         pg[j] = lg;
         ph[j] = lh;
@@ -759,71 +854,57 @@ __device__ bool wave_scan(const Ctx &c, const SplitCfgDev &cfg, const int64_t *h
     // exclusive prefix of the lane totals over the wave (exact: integer-valued)
     double eg = lg, eh = lh;
     int64_t ec = lc;
-    for (int o = 1; o < 64; o <<= 1) {
-        double ag = __shfl_up(eg, o);
-        double ah = __shfl_up(eh, o);
-        int64_t ac = __shfl_up(ec, o);
-        if (lane >= o) {
-            eg += ag;
-            eh += ah;
-            ec += ac;
-        }
-    }
+    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
     eg -= lg;
     eh -= lh;
     ec -= lc;
     const int64_t min_count = cfg.min_data_in_leaf > 1 ? cfg.min_data_in_leaf : 1;
     const double min_hess = cfg.min_sum_hessian_in_leaf;
-    // split.rs:420-444: the first candidate where the other side is too small while the growing one is not
-    int stop = n;
+    ScanRun run = {0u, -__builtin_inf(), -1};
+    double gains[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        int k = 4 * lane + j;
+        int k = 4 * static_cast<int>(lane) + j;
         pg[j] += eg;
         ph[j] += eh;
         pc[j] += ec;
-        if (k < n) {
+        gains[j] = -__builtin_inf();
+        if (k < n && !run.stopped) {
             double hh = K_EPSILON + ph[j] * c.scale_hess;
             bool skip = pc[j] < min_count || hh < min_hess || ph[j] <= 0.0;
             bool other_small = c.num_data - pc[j] < min_count || c.sum_hess - hh < min_hess || c.units_hess - ph[j] <= 0.0;
-            if (other_small && !skip && k < stop) stop = k;
+            if (other_small && !skip) {
+                run.stopped = 1u;
+            } else {
+                double gg = pg[j] * c.scale_grad;
+                double gain = leaf_gain(c.sum_grad - gg, c.sum_hess - hh, cfg.lambda_l1, cfg.lambda_l2) +
+                              leaf_gain(gg, hh, cfg.lambda_l1, cfg.lambda_l2);
+                gains[j] = (skip || gain != gain) ? -__builtin_inf() : gain;  // NaN never wins (split.rs:508-531)
+                if (run.k < 0 || gains[j] > run.gain) {
+                    run.gain = gains[j];
+                    run.k = k;
+                }
+            }
         }
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        int s = __shfl_xor(stop, o);
-        stop = s < stop ? s : stop;
-    }
-    // split.rs:447-462 gains, split.rs:508-531 first maximum
-    double gains[4];
-    double m = -__builtin_inf();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int k = 4 * lane + j;
-        gains[j] = -__builtin_inf();
-        if (k < stop) {
-            double hh = K_EPSILON + ph[j] * c.scale_hess;
-            bool skip = pc[j] < min_count || hh < min_hess || ph[j] <= 0.0;
-            double gg = pg[j] * c.scale_grad;
-            double gain = leaf_gain(c.sum_grad - gg, c.sum_hess - hh, cfg.lambda_l1, cfg.lambda_l2) +
-                          leaf_gain(gg, hh, cfg.lambda_l1, cfg.lambda_l2);
-            gains[j] = skip ? -__builtin_inf() : gain;
-            m = max_num(m, gains[j]);
-        }
-    }
-    for (int o = 32; o >= 1; o >>= 1) m = max_num(m, __shfl_xor(m, o));
-    if (!(m > c.min_gain_shift)) return false;
-    int first = 1 << 30;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int k = 4 * lane + j;
-        if (k < stop && gains[j] == m && k < first) first = k;
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        int s = __shfl_xor(first, o);
-        first = s < first ? s : first;
-    }
-    int owner = first >> 2, jj = first & 3;
-    double og = 0.0, oh = 0.0, ogain = 0.0;
+    scan_run_step<DPP_ROW_SHR1, 0xf>(run, lane);
+    scan_run_step<DPP_ROW_SHR2, 0xf>(run, lane);
+    scan_run_step<DPP_ROW_SHR4, 0xf>(run, lane);
+    scan_run_step<DPP_ROW_SHR8, 0xf>(run, lane);
+    scan_run_step<DPP_ROW_BCAST15, 0xa>(run, lane);
+    scan_run_step<DPP_ROW_BCAST31, 0xc>(run, lane);
+    const int32_t first = __builtin_amdgcn_readlane(run.k, 63);
+    const double best = double_of(readlane_u64(bits_of(run.gain), 63));
+    // NaN gains never become the best; an all -inf run fails here as in the reference's comparison
+    if (first < 0 || !(best > c.min_gain_shift)) return false;
+    const uint32_t owner = static_cast<uint32_t>(first) >> 2;
+    const int jj = first & 3;
+    double og = 0.0, oh = 0.0;
     int64_t oc = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -831,18 +912,18 @@ __device__ bool wave_scan(const Ctx &c, const SplitCfgDev &cfg, const int64_t *h
             og = pg[j];
             oh = ph[j];
             oc = pc[j];
-            ogain = gains[j];
         }
-    out.ug = __shfl(og, owner);
-    out.uh = __shfl(oh, owner);
-    out.count = __shfl(oc, owner);
-    out.gain = __shfl(ogain, owner);
+    out.ug = double_of(readlane_u64(bits_of(og), owner));
+    out.uh = double_of(readlane_u64(bits_of(oh), owner));
+    out.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
+    out.gain = best;
     out.bin = static_cast<uint32_t>(t0 + step * first);
     return true;
 }
 
 struct FeatDev {
     uint32_t num_bins, hist_offset, kind, nan_bin;
+    uint32_t col;  // column-major index among the non-trivial features
 };
 
 struct ScanJob {
@@ -860,6 +941,78 @@ __device__ __forceinline__ int64_t job_count(const ScanJob &job, const Plan *pla
     return j == 0 ? left : plan->parent_count - left;
 }
 
+// split.rs:584-620 find_numerical, in two parts so that a feature's two scan directions can run on two waves.
+// Direction 0 is the reverse scan (split.rs:557-567: missing values go left); direction 1, only for a feature with
+// a NaN bin and more than two bins, the forward scan over the bins before the NaN bin (split.rs:571-580).
+__device__ __forceinline__ bool scan_searched(const Ctx &c, const FeatDev &m, bool evaluate) {
+    return c.valid && evaluate && m.num_bins >= 2 && m.kind == 1;
+}
+__device__ __forceinline__ bool scan_two_way(const FeatDev &m) { return m.nan_bin && m.num_bins > 2; }
+
+// One direction's scan of a searched feature (wave-wide). Returns whether it found a candidate.
+__device__ __forceinline__ bool scan_direction(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist,
+                                               int dir, Grown &out) {
+    const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
+    const int nb = static_cast<int>(m.num_bins);
+    if (scan_two_way(m)) {
+        const int last = nb - 2;
+        return dir == 0 ? wave_scan(c, cfg, h, last, -1, last, out) : wave_scan(c, cfg, h, 0, 1, last + 1, out);
+    }
+    return dir == 0 ? wave_scan(c, cfg, h, nb - 1, -1, nb - 1, out) : false;
+}
+
+// The feature's candidate from its scans' results (rf/rg reverse, ff/fg forward).
+__device__ FeatCand feature_candidate(const Ctx &c, const FeatDev &m, bool rf, const Grown &rg, bool ff, const Grown &fg) {
+    FeatCand r = {};
+    bool have = false;
+    r.splittable = rf || ff;
+    double output_gain = -__builtin_inf();
+    if (rf) {  // split.rs:557-567 reverse_best
+        double right_hess = K_EPSILON + rg.uh * c.scale_hess;
+        r.best_gain = rg.gain;
+        r.threshold = rg.bin - 1;
+        r.left_grad = c.sum_grad - rg.ug * c.scale_grad;
+        r.left_hess = c.sum_hess - right_hess;
+        r.left_count = c.num_data - rg.count;
+        r.left_units_g = c.units_grad - rg.ug;
+        r.left_units_h = c.units_hess - rg.uh;
+        r.default_left = scan_two_way(m) ? 1 : (m.nan_bin ? 0 : 1);
+        output_gain = rg.gain - c.min_gain_shift;
+        have = true;
+    }
+    if (ff && fg.gain > output_gain + c.min_gain_shift) {  // split.rs:571-580 forward_best
+        r.best_gain = fg.gain;
+        r.threshold = fg.bin;
+        r.left_grad = fg.ug * c.scale_grad;
+        r.left_hess = K_EPSILON + fg.uh * c.scale_hess;
+        r.left_count = fg.count;
+        r.left_units_g = fg.ug;
+        r.left_units_h = fg.uh;
+        r.default_left = 0;
+        have = true;
+    }
+    if (have) {
+        r.found = 1;
+        r.gain = r.best_gain - c.min_gain_shift;
+        r.col = m.col;
+        r.nan_idx = m.nan_bin ? m.num_bins - 1 : NO_BIN;
+    }
+    return r;
+}
+
+// split.rs:584-620 find_numerical for one feature of one leaf, by one wave; lane 0's result is the candidate.
+__device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool evaluate) {
+    Grown rg = {}, fg = {};
+    bool rf = false, ff = false;
+    if (scan_searched(c, m, evaluate)) {
+        rf = scan_direction(c, cfg, m, hist, 0, rg);
+        if (scan_two_way(m)) ff = scan_direction(c, cfg, m, hist, 1, fg);
+    } else {
+        return FeatCand{};
+    }
+    return feature_candidate(c, m, rf, rg, ff, fg);
+}
+
 __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
                                                     SplitCfgDev cfg, double sg, double sh, const Plan *plan) {
@@ -867,69 +1020,9 @@ __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ 
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (f >= num_features) return;
-    const int lane = threadIdx.x & 63;
-    FeatCand r = {};
-    FeatDev m = feats[f];
     Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job_count(job, plan, blockIdx.y));
-    if (c.valid && evaluate[f] && m.num_bins != 0 && m.kind == 1) {
-        const int64_t *h = job.hist + 2 * static_cast<size_t>(m.hist_offset);
-        int nb = static_cast<int>(m.num_bins);
-        bool have = false;
-        // split.rs:584-620 find_numerical
-        if (m.nan_bin && nb > 2) {
-            int last = nb - 2;
-            Grown rg, fg;
-            bool rf = wave_scan(c, cfg, h, last, -1, last, rg);
-            bool ff = wave_scan(c, cfg, h, 0, 1, last + 1, fg);
-            r.splittable = rf || ff;
-            double output_gain = -__builtin_inf();
-            if (rf) {  // split.rs:557-567 reverse_best
-                double right_hess = K_EPSILON + rg.uh * c.scale_hess;
-                r.best_gain = rg.gain;
-                r.threshold = rg.bin - 1;
-                r.left_grad = c.sum_grad - rg.ug * c.scale_grad;
-                r.left_hess = c.sum_hess - right_hess;
-                r.left_count = c.num_data - rg.count;
-                r.left_units_g = c.units_grad - rg.ug;
-                r.left_units_h = c.units_hess - rg.uh;
-                r.default_left = 1;
-                output_gain = rg.gain - c.min_gain_shift;
-                have = true;
-            }
-            if (ff && fg.gain > output_gain + c.min_gain_shift) {  // split.rs:571-580 forward_best
-                r.best_gain = fg.gain;
-                r.threshold = fg.bin;
-                r.left_grad = fg.ug * c.scale_grad;
-                r.left_hess = K_EPSILON + fg.uh * c.scale_hess;
-                r.left_count = fg.count;
-                r.left_units_g = fg.ug;
-                r.left_units_h = fg.uh;
-                r.default_left = 0;
-                have = true;
-            }
-        } else if (nb >= 2) {
-            Grown rg;
-            bool rf = wave_scan(c, cfg, h, nb - 1, -1, nb - 1, rg);
-            r.splittable = rf;
-            if (rf) {
-                double right_hess = K_EPSILON + rg.uh * c.scale_hess;
-                r.best_gain = rg.gain;
-                r.threshold = rg.bin - 1;
-                r.left_grad = c.sum_grad - rg.ug * c.scale_grad;
-                r.left_hess = c.sum_hess - right_hess;
-                r.left_count = c.num_data - rg.count;
-                r.left_units_g = c.units_grad - rg.ug;
-                r.left_units_h = c.units_hess - rg.uh;
-                r.default_left = m.nan_bin ? 0 : 1;
-                have = true;
-            }
-        }
-        if (have) {
-            r.found = 1;
-            r.gain = r.best_gain - c.min_gain_shift;
-        }
-    }
-    if (lane == 0) job.out[f] = r;
+    FeatCand r = scan_feature(c, cfg, feats[f], job.hist, evaluate[f] != 0);
+    if ((threadIdx.x & 63) == 0) job.out[f] = r;
 }
 
 // The leaf's SplitInfo (split.rs:631-651 finish) and splittable flags from the per-feature candidates: the
@@ -943,23 +1036,47 @@ struct SplitOut {
     double right_grad, right_hess;
     int64_t right_count;
     double left_output, right_output;
+    uint32_t col, nan_idx;  // the feature's column-major index and NaN bin (NO_BIN: none)
 };
 
 // The best split over the per-feature candidates of `job` (highest gain, NaN as -inf, ties to the lower feature,
-// split.rs:866-880) as the leaf's SplitOut (split.rs:631-651 finish), and its splittable flags. Block-wide (256).
+// split.rs:866-880) as the leaf's SplitOut (split.rs:631-651 finish), and its splittable flags. Block-wide (up
+// to 1024 threads).
 // (gain, feature) order of split.rs:866-880 for reductions: a beats b on higher gain, then lower feature; -1 is
 // "no candidate".
 __device__ __forceinline__ bool cand_better(double ga, int fa, double gb, int fb) {
     return fa >= 0 && (fb < 0 || ga > gb || (ga == gb && fa < fb));
 }
 
+// split.rs:631-651 finish: the leaf's SplitInfo from its best feature's candidate.
+__device__ __forceinline__ SplitOut split_out(const FeatCand &c, int f, const Ctx &x, const SplitCfgDev &cfg) {
+    SplitOut o = {};
+    o.found = 1;
+    o.feature = f;
+    o.gain = c.best_gain - x.min_gain_shift;
+    o.threshold = c.threshold;
+    o.default_left = c.default_left;
+    o.left_grad = c.left_units_g;
+    o.left_hess = c.left_units_h;
+    o.left_count = c.left_count;
+    o.right_grad = x.units_grad - c.left_units_g;
+    o.right_hess = x.units_hess - c.left_units_h;
+    o.right_count = x.num_data - c.left_count;
+    o.left_output = leaf_output(c.left_grad, c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
+    o.right_output = leaf_output(x.sum_grad - c.left_grad, x.sum_hess - c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
+    o.col = c.col;
+    o.nan_idx = c.nan_idx;
+    return o;
+}
+
 __device__ void select_split(const ScanJob &job, int64_t count, uint32_t num_features, const SplitCfgDev &cfg, double sg,
                              double sh, SplitOut *out, uint8_t *splittable) {
-    __shared__ double wgain[4];
-    __shared__ int wfeat[4];
+    __shared__ double wgain[16];
+    __shared__ int wfeat[16];
+    const uint32_t nw = blockDim.x >> 6;
     double best = 0.0;
     int bf = -1;
-    for (uint32_t f = threadIdx.x; f < num_features; f += 256) {
+    for (uint32_t f = threadIdx.x; f < num_features; f += blockDim.x) {
         const FeatCand &c = job.out[f];
         splittable[f] = static_cast<uint8_t>(c.splittable);
         if (!c.found) continue;
@@ -983,30 +1100,13 @@ __device__ void select_split(const ScanJob &job, int64_t count, uint32_t num_fea
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
+        for (uint32_t w = 1; w < nw; ++w)
             if (cand_better(wgain[w], wfeat[w], best, bf)) {
                 best = wgain[w];
                 bf = wfeat[w];
             }
         SplitOut o = {};
-        int f = bf;
-        if (f >= 0) {
-            const FeatCand &c = job.out[f];
-            Ctx x = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, count);
-            o.found = 1;
-            o.feature = f;
-            o.gain = c.best_gain - x.min_gain_shift;
-            o.threshold = c.threshold;
-            o.default_left = c.default_left;
-            o.left_grad = c.left_units_g;
-            o.left_hess = c.left_units_h;
-            o.left_count = c.left_count;
-            o.right_grad = x.units_grad - c.left_units_g;
-            o.right_hess = x.units_hess - c.left_units_h;
-            o.right_count = x.num_data - c.left_count;
-            o.left_output = leaf_output(c.left_grad, c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
-            o.right_output = leaf_output(x.sum_grad - c.left_grad, x.sum_hess - c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
-        }
+        if (bf >= 0) o = split_out(job.out[bf], bf, make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, count), cfg);
         *out = o;
     }
     __syncthreads();
@@ -1032,8 +1132,20 @@ struct DLeaf {
     int32_t slot;            // histogram slot, -1: none
     uint32_t has_best;
     uint32_t buf;            // partition buffer holding the rows
+    uint32_t rev;            // the rows are stored last-first (right children of a split step)
+    int32_t depth;
+    int32_t parent;          // the internal node above, -1 for the root
+    uint32_t is_left;        // the leaf is its parent's left child
     uint32_t pad_;
+    double value, weight;    // the leaf's output and hessian weight in the tree
     SplitOut best;
+};
+
+// A leaf's best gain for the choice of the next leaf to split (learner.rs:418-429); `has` is 0 without one.
+struct LeafKey {
+    double gain;
+    uint32_t has;
+    uint32_t pad_;
 };
 
 struct TreeDev {
@@ -1052,25 +1164,29 @@ struct TreeDev {
 struct GrowCtl {
     uint32_t num_leaves;     // the tree's leaves so far
     uint32_t done;           // no further split this tree
-    uint32_t error;          // an invariant failed (a child without rows, no free histogram slot)
-    int32_t free_top;        // entries on the free-slot stack
+    uint32_t error;          // an invariant failed: 1 a child without rows, 3 a partition tile's look-back gave up
+    uint32_t pad0_;
     double hist_rows;        // rows histogrammed (built children), and rows x evaluated features
     double hist_bins;
     double hist_builds;      // child histograms built
+    double part_rows;        // rows partitioned by the split steps
+    uint32_t epoch;          // split steps planned so far (kept across trees; tags tile status words)
+    uint32_t pad_;
 };
 
+// Histogram slots: the root's is slot 0 and the child built by the step that creates leaf n goes to slot n, so
+// a tree of L leaves needs L slots and none is reused within a tree; the other child keeps its parent's slot.
 struct GrowState {
     GrowCtl *ctl;
     Plan *plan;
     DLeaf *leaves;
+    LeafKey *keys;           // [leaf]
     uint8_t *splittable;     // [leaf][nf]
-    int32_t *free_slots;
-    ScanJob *jobs;           // [2]
+    ScanJob *jobs;           // [1]: the root's search
     FeatCand *cands;         // [2][nf]
     uint8_t *evaluate;       // [nf]
     const uint8_t *mask;     // [nf], the tree's feature mask
     const FeatDev *feats;
-    const int32_t *feat_nt;  // feature -> column-major index
     TreeDev tree;
     int64_t *pool;
     uint64_t slot_stride;
@@ -1082,140 +1198,102 @@ struct GrowState {
 
 __device__ __forceinline__ bool depth_allows(const GrowState &g, int32_t d) { return g.max_depth <= 0 || d < g.max_depth; }
 
-// learner.rs:418-429 best_leaf, then learner.rs:249-290: the next step's plan. Block-wide.
-__device__ void plan_next(const GrowState &g) {
-    __shared__ double bgain[4];
-    __shared__ int bidx[4];
-    GrowCtl *ctl = g.ctl;
-    uint32_t n = ctl->num_leaves;
-    bool stop = ctl->done || ctl->error || n >= g.num_leaves;
-    double best = 0.0;
-    int bi = -1;
-    if (!stop)
-        for (uint32_t i = threadIdx.x; i < n; i += 256) {  // leaves ascend within a thread: ties keep the first
-            const DLeaf &l = g.leaves[i];
-            if (!l.has_best) continue;
-            if (bi < 0 || l.best.gain > best) {
-                best = l.best.gain;
-                bi = static_cast<int>(i);
-            }
-        }
-    for (int o = 32; o >= 1; o >>= 1) {
-        double og = __shfl_xor(best, o);
-        int oi = __shfl_xor(bi, o);
-        if (cand_better(og, oi, best, bi)) {
-            best = og;
-            bi = oi;
-        }
-    }
-    if ((threadIdx.x & 63) == 0) {
-        bgain[threadIdx.x >> 6] = best;
-        bidx[threadIdx.x >> 6] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-        for (int w = 1; w < 4; ++w)
-            if (cand_better(bgain[w], bidx[w], bgain[0], bidx[0])) {
-                bgain[0] = bgain[w];
-                bidx[0] = bidx[w];
-            }
-    __syncthreads();
-    int index = bidx[0];
-    bool go = !stop && index >= 0 && bgain[0] > 0.0;
-    __syncthreads();
-    if (!go) {
-        if (threadIdx.x == 0) {
-            g.plan->active = 0;
-            ctl->done = 1;
-        }
-        return;
-    }
-    DLeaf &leaf = g.leaves[index];
-    const SplitOut &info = leaf.best;
-    __shared__ uint32_t used_w[4];
+// learner.rs:249-290 for leaf `next` (held in LDS by the caller): the step's plan, the evaluated features
+// (learner.rs:262-265: the tree's mask and the leaf's splittable flags) and the leaf's key cleared. `n` is
+// the tree's leaf count; the step will create leaf n. Block-wide.
+__device__ void plan_leaf(const GrowState &g, uint32_t next, const DLeaf &leaf, uint32_t n) {
+    __shared__ uint32_t used_w[16];
+    const uint32_t nw = blockDim.x >> 6;
+    const uint8_t *row = g.splittable + static_cast<size_t>(next) * g.nf;
     uint32_t used = 0;
-    for (uint32_t f = threadIdx.x; f < g.nf; f += 256) {
-        uint8_t e = static_cast<uint8_t>(g.mask[f] && g.splittable[(size_t)index * g.nf + f]);
+    for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) {
+        uint8_t e = static_cast<uint8_t>(g.mask[f] && row[f]);
         g.evaluate[f] = e;
-        used += (e && g.feats[f].num_bins) ? 1u : 0u;
+        used += e;  // a splittable feature has bins
     }
     for (int o = 32; o >= 1; o >>= 1) used += __shfl_xor(used, o);
     if ((threadIdx.x & 63) == 0) used_w[threadIdx.x >> 6] = used;
     __syncthreads();
     if (threadIdx.x == 0) {
+        const SplitOut &info = leaf.best;
         Plan &p = *g.plan;
-        FeatDev m = g.feats[info.feature];
         p.active = 1;
-        p.index = static_cast<uint32_t>(index);
+        p.index = next;
         p.begin = leaf.begin;
         p.count = leaf.count;
         p.parent_count = leaf.cnt;
         p.src_buf = leaf.buf;
-        p.col = static_cast<uint32_t>(g.feat_nt[info.feature]);
+        p.src_rev = leaf.rev;
+        p.epoch = ++g.ctl->epoch;
+        p.ticket = 0;
+        p.left = 0;
+        p.col = info.col;
         // learner.rs:432-452: bins 0..=threshold, and the NaN bin when missing values go left
-        uint32_t words[8];
+        const uint32_t upto = info.threshold + 1;
+        const bool nan_left = info.default_left && info.nan_idx != NO_BIN;
+#pragma unroll
         for (uint32_t w = 0; w < 8; ++w) {
             uint32_t lo = 32 * w;
-            uint32_t upto = info.threshold + 1;  // bins below `upto` go left
-            words[w] = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
+            uint32_t word = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
+            if (nan_left && (info.nan_idx >> 5) == w) word |= 1u << (info.nan_idx & 31u);
+            p.left_bins[w] = word;
         }
-        if (info.default_left && m.nan_bin) words[(m.num_bins - 1) >> 5] |= 1u << ((m.num_bins - 1) & 31u);
-        for (uint32_t w = 0; w < 8; ++w) p.left_bins[w] = words[w];
-        p.used_columns = used_w[0] + used_w[1] + used_w[2] + used_w[3];
+        uint32_t used_all = 0;
+        for (uint32_t w = 0; w < nw; ++w) used_all += used_w[w];
+        p.used_columns = used_all;
         p.built_side = info.left_count <= info.right_count ? 0u : 1u;
-        p.may_search = leaf.slot >= 0 && n + 1 < g.num_leaves && depth_allows(g, g.tree.leaf_depth[index] + 1);
+        p.may_search = leaf.slot >= 0 && n + 1 < g.num_leaves && depth_allows(g, leaf.depth + 1);
         p.parent_slot = leaf.slot;
-        p.built_slot = -1;
-        if (p.may_search) {
-            if (ctl->free_top <= 0) {
-                ctl->error = 2;
-                p.may_search = 0;
-            } else {
-                p.built_slot = g.free_slots[--ctl->free_top];
-            }
-        }
-        if (p.may_search) {
-            int64_t *built = g.pool + (size_t)p.built_slot * g.slot_stride;
-            int64_t *parent = g.pool + (size_t)p.parent_slot * g.slot_stride;
-            // jobs: the left child, then the right; their exact counts come from the partition
-            g.jobs[0] = ScanJob{p.built_side == 0 ? built : parent, info.left_grad, info.left_hess, 0, g.cands};
-            g.jobs[1] = ScanJob{p.built_side == 0 ? parent : built, info.right_grad, info.right_hess, 0, g.cands + g.nf};
-        }
-        leaf.has_best = 0;
+        p.built_slot = p.may_search ? static_cast<int32_t>(n) : -1;
+        p.child_ug[0] = info.left_grad;
+        p.child_uh[0] = info.left_hess;
+        p.child_ug[1] = info.right_grad;
+        p.child_uh[1] = info.right_hess;
+        g.keys[next].has = 0;
+        g.leaves[next].has_best = 0;
     }
     __syncthreads();
 }
 
-// Copies the rows of every leaf that ended in the second partition buffer back into the first. grid: (x, leaves).
+// Brings every leaf's rows into the first partition buffer in ascending order: copied from the second buffer
+// (reversed when stored last-first), or reversed in place. grid: (x, leaves).
 __global__ void k_consolidate(GrowState g, const uint32_t *__restrict__ buf1, uint32_t *__restrict__ buf0) {
     if (blockIdx.y >= g.ctl->num_leaves) return;
     const DLeaf &l = g.leaves[blockIdx.y];
-    if (!l.buf) return;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < l.count; i += gridDim.x * blockDim.x)
-        buf0[l.begin + i] = buf1[l.begin + i];
+    const uint32_t b = l.begin, n = l.count;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    if (l.buf) {
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+            buf0[b + i] = buf1[l.rev ? b + n - 1 - i : b + i];
+    } else if (l.rev) {
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n / 2; i += stride) {
+            uint32_t x = buf0[b + i], y = buf0[b + n - 1 - i];
+            buf0[b + i] = y;
+            buf0[b + n - 1 - i] = x;
+        }
+    }
 }
 
-// The tree at its start: one leaf holding the root rows; slot 0 for its histogram when it is searched.
-__global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_count, int64_t root_cnt, uint32_t slots,
-                            uint32_t searched) {
-    for (uint32_t i = threadIdx.x; i < slots; i += blockDim.x) g.free_slots[i] = static_cast<int32_t>(slots - 1 - i);
-    __syncthreads();
+// The tree at its start: one leaf holding the root rows, its histogram in slot 0 when it is searched.
+__global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_count, int64_t root_cnt, uint32_t searched) {
     if (threadIdx.x == 0) {
         GrowCtl &c = *g.ctl;
         c.num_leaves = 1;
         c.done = 0;
         c.error = 0;
-        c.free_top = static_cast<int32_t>(slots);
         c.hist_rows = 0.0;
         c.hist_bins = 0.0;
         c.hist_builds = 0.0;
+        c.part_rows = 0.0;
         g.plan->active = 0;
         DLeaf l = {};
         l.begin = root_begin;
         l.count = root_count;
         l.cnt = root_cnt;
-        l.slot = searched ? g.free_slots[--c.free_top] : -1;
+        l.slot = searched ? 0 : -1;
+        l.parent = -1;
         g.leaves[0] = l;
+        g.keys[0] = LeafKey{0.0, 0u, 0u};
         g.tree.leaf_value[0] = 0.0;
         g.tree.leaf_weight[0] = 0.0;
         g.tree.leaf_count[0] = 0;
@@ -1242,116 +1320,697 @@ __global__ void k_root_prep(GrowState g) {
     }
 }
 
+// The root's best split (learner.rs:157-163), then the first step's plan when the root splits (best_leaf over
+// the one leaf: a positive gain, learner.rs:418-429).
 __global__ __launch_bounds__(256) void k_root_select(GrowState g) {
     ScanJob job = g.jobs[0];
     __shared__ SplitOut o;
+    __shared__ DLeaf leaf;
     select_split(job, job.count, g.nf, g.cfg, g.sg, g.sh, &o, g.splittable);
     if (threadIdx.x == 0) {
-        g.leaves[0].best = o;
-        g.leaves[0].has_best = o.found ? 1u : 0u;
+        leaf = g.leaves[0];
+        leaf.best = o;
+        leaf.has_best = o.found ? 1u : 0u;
+        g.leaves[0] = leaf;
+        g.keys[0] = LeafKey{o.gain, leaf.has_best, 0u};
     }
     __syncthreads();
-    plan_next(g);
+    bool go = o.found && o.gain > 0.0 && 1 < g.num_leaves;
+    if (!go) {
+        if (threadIdx.x == 0) g.ctl->done = 1;
+        return;
+    }
+    plan_leaf(g, 0, leaf, 1);
 }
 
-// learner.rs:294-352: apply the planned split with the exact left count, set up the children (their best splits
-// when searched), free unused histogram slots, then plan the next step. One block.
-__global__ __launch_bounds__(256) void k_apply(GrowState g) {
-    const Plan &p = *g.plan;
-    if (!p.active) return;
-    __shared__ int searched;
+// The end of a split step, by one block of 1024 threads (learner.rs:294-352, then learner.rs:418-429 and
+// 249-290): both children's best splits from their per-feature candidates (half a block each, split.rs:866-880),
+// the planned split applied to the tree and the leaf table (tree.rs:143-177), then the next leaf chosen and
+// planned. The leaf table, the candidates and the leaf keys are read once, together.
+__device__ void finish_step(const GrowState &g) {
+    __shared__ double s_gain[16];
+    __shared__ int s_feat[16];
+    __shared__ FeatCand s_win[2];
+    __shared__ SplitOut s_out[2];
+    __shared__ DLeaf s_leaf[3];  // the two children, then the next leaf when it is neither
+    __shared__ uint32_t s_searched, s_go, s_next, s_ok;
+    __shared__ int s_first[16];
+    __shared__ double s_kgain[16];
+    __shared__ int s_kidx[16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const Plan &P = *g.plan;
     GrowCtl *ctl = g.ctl;
-    const uint32_t index = p.index;
-    const uint32_t new_leaf = ctl->num_leaves;
-    const int64_t left = static_cast<int64_t>(p.left);
-    const int64_t right = p.parent_count - left;
-    if (threadIdx.x == 0) {
-        const SplitOut info = g.leaves[index].best;
-        searched = 0;
+    const uint32_t n = ctl->num_leaves;  // leaves before the step; it creates leaf n
+    const uint32_t index = P.index;
+    const int64_t left = static_cast<int64_t>(P.left);
+    const int64_t right = P.parent_count - left;
+    const bool may_search = P.may_search != 0;
+    // this thread's leaf keys, for the choice of the next leaf (leaves ascend within a thread)
+    // (read up front with everything else)
+    LeafKey key_own[1];
+    key_own[0] = tid < n ? g.keys[tid] : LeafKey{0.0, 0u, 0u};
+
+    // -- both children's best splits: half h (512 threads) takes child h
+    const uint32_t half = tid >> 9, ht = tid & 511u;
+    if (may_search) {
+        const FeatCand *cands = g.cands + static_cast<size_t>(half) * g.nf;
+        uint8_t *row = g.splittable + static_cast<size_t>(half == 0 ? index : n) * g.nf;
+        double best = 0.0;
+        int bf = -1;
+        FeatCand bc = {};
+        for (uint32_t f = ht; f < g.nf; f += 512u) {
+            FeatCand c = cands[f];
+            row[f] = static_cast<uint8_t>(c.splittable);
+            if (!c.found) continue;
+            double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+            if (cand_better(gv, static_cast<int>(f), best, bf)) {
+                best = gv;
+                bf = static_cast<int>(f);
+                bc = c;
+            }
+        }
+        double wb = best;
+        int wf = bf;
+        for (int o = 32; o >= 1; o >>= 1) {
+            double og = __shfl_xor(wb, o);
+            int of = __shfl_xor(wf, o);
+            if (cand_better(og, of, wb, wf)) {
+                wb = og;
+                wf = of;
+            }
+        }
+        if (lane == 0) {
+            s_gain[wave] = wb;
+            s_feat[wave] = wf;
+        }
+        __syncthreads();
+        if (ht == 0) {
+            for (uint32_t w = half * 8 + 1; w < half * 8 + 8; ++w)
+                if (cand_better(s_gain[w], s_feat[w], wb, wf)) {
+                    wb = s_gain[w];
+                    wf = s_feat[w];
+                }
+            s_feat[half * 8] = wf;
+        }
+        __syncthreads();
+        if (bf >= 0 && bf == s_feat[half * 8]) s_win[half] = bc;
+        __syncthreads();
+        if (ht == 0) {
+            SplitOut o = {};
+            const int wf2 = s_feat[half * 8];
+            if (wf2 >= 0) {
+                int64_t cnt = half == 0 ? left : right;
+                o = split_out(s_win[half], wf2, make_ctx(g.cfg, g.sg, g.sh, P.child_ug[half], P.child_uh[half], cnt), g.cfg);
+            }
+            s_out[half] = o;
+        }
+    }
+
+    // -- apply the split (tree.rs:143-177) and set up the children (learner.rs:294-352)
+    if (tid == 0) {
+        const DLeaf pl = g.leaves[index];
+        const SplitOut &info = pl.best;
+        uint32_t searched = 0;
         if (left <= 0 || right <= 0) {
             ctl->error = 1;
         } else {
-            // tree.rs:143-177 Tree::split
             const TreeDev &t = g.tree;
-            int32_t node = static_cast<int32_t>(new_leaf) - 1;
-            int32_t parent = t.leaf_parent[index];
-            if (parent >= 0) {
-                if (t.left_child[parent] == ~static_cast<int32_t>(index)) t.left_child[parent] = node;
-                else t.right_child[parent] = node;
+            const int32_t node = static_cast<int32_t>(n) - 1;
+            if (pl.parent >= 0) {
+                if (pl.is_left) t.left_child[pl.parent] = node;
+                else t.right_child[pl.parent] = node;
             }
             t.split_feature[node] = info.feature;
             t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
             t.threshold_bin[node] = info.threshold;
             t.default_left[node] = static_cast<uint8_t>(info.default_left);
             t.left_child[node] = ~static_cast<int32_t>(index);
-            t.right_child[node] = ~static_cast<int32_t>(new_leaf);
-            t.internal_weight[node] = t.leaf_weight[index];
-            t.internal_value[node] = t.leaf_value[index];
+            t.right_child[node] = ~static_cast<int32_t>(n);
+            t.internal_weight[node] = pl.weight;
+            t.internal_value[node] = pl.value;
             t.internal_count[node] = left + right;
-            double lv = info.left_output, rv = info.right_output;
-            t.leaf_value[index] = lv != lv ? 0.0 : lv;
-            t.leaf_weight[index] = info.left_hess * g.sh;
-            t.leaf_count[index] = left;
-            t.leaf_value[new_leaf] = rv != rv ? 0.0 : rv;
-            t.leaf_weight[new_leaf] = info.right_hess * g.sh;
-            t.leaf_count[new_leaf] = right;
-            t.leaf_parent[index] = node;
-            t.leaf_parent[new_leaf] = node;
-            int32_t depth = t.leaf_depth[index] + 1;
-            t.leaf_depth[index] = depth;
-            t.leaf_depth[new_leaf] = depth;
-            // the children (learner.rs:320-334)
+            const int32_t depth = pl.depth + 1;
             DLeaf l = {}, r = {};
-            l.begin = p.begin;
-            l.count = p.left;
+            l.begin = P.begin;
+            l.count = P.left;
+            r.begin = P.begin + P.left;
+            r.count = P.count - P.left;
             l.ug = info.left_grad;
             l.uh = info.left_hess;
-            l.cnt = left;
-            l.slot = -1;
-            l.buf = 1u - p.src_buf;
-            r.buf = 1u - p.src_buf;
-            r.begin = p.begin + p.left;
-            r.count = p.count - p.left;
             r.ug = info.right_grad;
             r.uh = info.right_hess;
+            l.cnt = left;
             r.cnt = right;
-            r.slot = -1;
-            int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
-            bool s = p.may_search && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
-            if (p.may_search) {  // the built child's histogram was made, searched or not
-                double built_rows = p.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
+            l.buf = r.buf = 1u - P.src_buf;
+            l.rev = 0;  // the split step writes the left child first-first and the right child last-first
+            r.rev = 1;
+            l.depth = r.depth = depth;
+            l.parent = r.parent = node;
+            l.is_left = 1;
+            r.is_left = 0;
+            double lv = info.left_output, rv = info.right_output;
+            l.value = lv != lv ? 0.0 : lv;
+            r.value = rv != rv ? 0.0 : rv;
+            l.weight = info.left_hess * g.sh;
+            r.weight = info.right_hess * g.sh;
+            t.leaf_value[index] = l.value;
+            t.leaf_weight[index] = l.weight;
+            t.leaf_count[index] = left;
+            t.leaf_value[n] = r.value;
+            t.leaf_weight[n] = r.weight;
+            t.leaf_count[n] = right;
+            t.leaf_parent[index] = node;
+            t.leaf_parent[n] = node;
+            t.leaf_depth[index] = depth;
+            t.leaf_depth[n] = depth;
+            const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
+            const bool sr = may_search && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
+            l.slot = r.slot = -1;
+            if (sr) {
+                l.slot = P.built_side == 0 ? P.built_slot : P.parent_slot;
+                r.slot = P.built_side == 0 ? P.parent_slot : P.built_slot;
+            }
+            if (may_search) {  // the built child's histogram was made, searched or not
+                double built_rows = P.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
                 ctl->hist_rows += built_rows;
-                ctl->hist_bins += built_rows * static_cast<double>(p.used_columns);
+                ctl->hist_bins += built_rows * static_cast<double>(P.used_columns);
                 ctl->hist_builds += 1.0;
             }
-            if (s) {
-                l.slot = p.built_side == 0 ? p.built_slot : p.parent_slot;
-                r.slot = p.built_side == 0 ? p.parent_slot : p.built_slot;
-            } else {
-                if (p.parent_slot >= 0) g.free_slots[ctl->free_top++] = p.parent_slot;
-                if (p.built_slot >= 0) g.free_slots[ctl->free_top++] = p.built_slot;
-            }
-            g.leaves[index] = l;
-            g.leaves[new_leaf] = r;
-            ctl->num_leaves = new_leaf + 1;
-            searched = s ? 1 : 0;
+            ctl->part_rows += static_cast<double>(P.count);
+            ctl->num_leaves = n + 1;
+            s_leaf[0] = l;
+            s_leaf[1] = r;
+            searched = sr ? 1u : 0u;
+        }
+        s_searched = searched;
+        s_ok = (left > 0 && right > 0) ? 1u : 0u;
+    }
+    __syncthreads();
+    const bool ok = s_ok != 0;
+    if (tid < 2 && ok) {
+        DLeaf &c = s_leaf[tid];
+        c.has_best = 0;
+        if (s_searched) {
+            c.best = s_out[tid];
+            c.has_best = s_out[tid].found ? 1u : 0u;
         }
     }
     __syncthreads();
-    if (searched) {
-        __shared__ SplitOut o;
-        for (uint32_t j = 0; j < 2; ++j) {
-            ScanJob job = g.jobs[j];
-            uint32_t who = j == 0 ? index : new_leaf;
-            select_split(job, j == 0 ? left : right, g.nf, g.cfg, g.sg, g.sh, &o, g.splittable + (size_t)who * g.nf);
-            if (threadIdx.x == 0) {
-                g.leaves[who].best = o;
-                g.leaves[who].has_best = o.found ? 1u : 0u;
+
+    // -- best_leaf (learner.rs:418-429) over leaves 0..=n, the children's keys replacing the split leaf's and
+    // adding leaf n: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
+    // otherwise the first highest gain among the rest (a NaN later never wins). `first` is 2 * leaf + (NaN).
+    int first = 1 << 30;
+    double kg = 0.0;
+    int ki = -1;
+    if (ok) {
+        for (uint32_t i = tid; i <= n; i += blockDim.x) {
+            LeafKey k;
+            if (i == index || i == n) {
+                const DLeaf &c = s_leaf[i == index ? 0 : 1];
+                k = LeafKey{c.best.gain, c.has_best, 0u};
+            } else {
+                k = i == tid ? key_own[0] : g.keys[i];
             }
-            __syncthreads();
+            if (!k.has) continue;
+            const bool nan = k.gain != k.gain;
+            const int code = 2 * static_cast<int>(i) + (nan ? 1 : 0);
+            if (code < first) first = code;
+            if (nan) continue;
+            if (cand_better(k.gain, static_cast<int>(i), kg, ki)) {
+                kg = k.gain;
+                ki = static_cast<int>(i);
+            }
         }
     }
-    plan_next(g);
+    for (int o = 32; o >= 1; o >>= 1) {
+        int of = __shfl_xor(first, o);
+        first = of < first ? of : first;
+        double og = __shfl_xor(kg, o);
+        int oi = __shfl_xor(ki, o);
+        if (cand_better(og, oi, kg, ki)) {
+            kg = og;
+            ki = oi;
+        }
+    }
+    if (lane == 0) {
+        s_first[wave] = first;
+        s_kgain[wave] = kg;
+        s_kidx[wave] = ki;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t nw = blockDim.x >> 6;
+        for (uint32_t w = 1; w < nw; ++w) {
+            if (s_first[w] < first) first = s_first[w];
+            if (cand_better(s_kgain[w], s_kidx[w], kg, ki)) {
+                kg = s_kgain[w];
+                ki = s_kidx[w];
+            }
+        }
+        const bool nan_first = first < (1 << 30) && (first & 1);
+        const bool go = ok && !ctl->done && n + 1 < g.num_leaves && !nan_first && ki >= 0 && kg > 0.0;
+        s_go = go ? 1u : 0u;
+        s_next = go ? static_cast<uint32_t>(ki) : 0u;
+        if (ok) {
+            g.leaves[index] = s_leaf[0];
+            g.leaves[n] = s_leaf[1];
+            g.keys[index] = LeafKey{s_leaf[0].best.gain, s_leaf[0].has_best, 0u};
+            g.keys[n] = LeafKey{s_leaf[1].best.gain, s_leaf[1].has_best, 0u};
+        }
+        if (go) {
+            const uint32_t next = static_cast<uint32_t>(ki);
+            if (next != index && next != n) s_leaf[2] = g.leaves[next];
+        } else {
+            g.plan->active = 0;
+            ctl->done = 1;
+        }
+    }
+    __syncthreads();
+    if (!s_go) return;
+    const uint32_t next = s_next;
+    plan_leaf(g, next, s_leaf[next == index ? 0 : (next == n ? 1 : 2)], n + 1);
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// A split step in two kernels (learner.rs:249-352 for the leaf the previous step planned).
+//
+// k_step_rows: the stable partition of the leaf's rows by the planned BinSplit (cpu.rs:556-599) in one pass,
+// fused with the built child's histogram. Tiles of STEP_TILE rows are handed out in order; a tile's left
+// count is published at once, its offset comes from a look-back over the earlier tiles' status words (no
+// second pass over the rows), its rows are scattered, then its rows of the built child (kept in LDS) are
+// histogrammed as k_hist does. Left rows are
+// written first-first from the range's start, right rows last-first from its end, so both children are
+// stable; a leaf stored last-first is read back to front by the next step and by k_consolidate. Launches for
+// a second or later slab only histogram.
+//
+// k_step_finish: adds the partials of the built child (a block per 8 columns and bin chunk), forms the sibling
+// by subtraction (learner.rs:356-371), scans the two children's features (the last chunk block of each column
+// group, a wave per feature and child), then the last column group selects both children's splits, applies
+// the step and plans the next (finish_step). Hand-offs are counters that the last arriving block resets; no
+// block ever waits for another in k_step_finish.
+// ---------------------------------------------------------------------------------------------------------
+
+constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: two per thread of a 1024-thread block
+// A split step's partials are 256 * W {g, h} pairs per workgroup, padded so that the same slot of consecutive
+// partials does not fall at a power-of-two distance (which maps it to the same memory channel and bank).
+constexpr uint32_t STEP_PARTIAL_PAD = 288;
+__host__ __device__ constexpr size_t step_partial_stride(uint32_t w) { return 256u * static_cast<size_t>(w) + STEP_PARTIAL_PAD; }
+constexpr uint32_t ST_AGG = 1, ST_INCL = 2;   // tile status: its own left count / lefts up to and including it
+constexpr uint32_t LOOKBACK_SPINS = 1u << 20; // ~0.1 s of polling before a step gives up with an error
+
+struct StepArgs {
+    const uint8_t *bins;         // slab rows: row r at bins + r * W
+    const int32_t *gh;           // packed quantized gradients per row
+    const uint8_t *colbase;      // column-major bins [feature][rows]
+    uint64_t rows;
+    uint32_t *buf0, *buf1;       // the partition buffers
+    int32_t *partial;            // this slab's partials: [max_groups][step_partial_stride(W)] {g, h}
+    unsigned long long *status;  // per-tile status words
+    Plan *plan;
+    GrowCtl *ctl;
+    uint32_t flush_rows;
+    uint32_t max_groups;         // == gridDim.x
+    uint32_t partition;          // 1: this launch partitions (the first slab's); 0: histogram only
+};
+
+__device__ __forceinline__ uint32_t step_groups(uint32_t count, uint32_t max_groups) {
+    uint32_t tiles = (count + STEP_TILE - 1) / STEP_TILE;
+    return tiles < max_groups ? tiles : max_groups;
+}
+
+__device__ __forceinline__ unsigned long long status_word(uint32_t epoch, uint32_t flag, uint32_t value) {
+    return (static_cast<unsigned long long>(((epoch & 0x3fffffffu) << 2) | flag) << 32) | value;
+}
+
+// Lefts in the tiles before `t`: wave-wide over up to 64 earlier tiles at a time, nearest first, summing
+// aggregates until an inclusive prefix. Tile 0 always publishes an inclusive one, and every earlier tile was
+// handed to a running block that publishes its aggregate before any wait, so the polling ends; a step that
+// still sees no status after LOOKBACK_SPINS polls flags an error instead of waiting on.
+__device__ uint32_t lookback(const unsigned long long *status, uint32_t t, uint32_t epoch, GrowCtl *ctl) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t want = epoch & 0x3fffffffu;
+    uint32_t prefix = 0, spins = 0;
+    int64_t hi = static_cast<int64_t>(t) - 1;
+    while (hi >= 0) {
+        const int64_t idx = hi - static_cast<int64_t>(lane);
+        unsigned long long w = 0;
+        if (idx >= 0) w = __hip_atomic_load(status + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t tag = static_cast<uint32_t>(w >> 32);
+        const bool ready = idx >= 0 && (tag >> 2) == want && (tag & 3u) != 0u;
+        const unsigned long long waiting = __ballot(idx >= 0 && !ready);
+        const unsigned long long incl = __ballot(ready && (tag & 3u) == ST_INCL);
+        const uint32_t first_incl = incl ? static_cast<uint32_t>(__builtin_ctzll(incl)) : 64u;
+        const uint32_t first_wait = waiting ? static_cast<uint32_t>(__builtin_ctzll(waiting)) : 64u;
+        if (first_wait < first_incl) {
+            if (++spins > LOOKBACK_SPINS) {
+                if (lane == 0) ctl->error = 3;
+                return prefix;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            continue;
+        }
+        const uint32_t take = first_incl < 64u ? first_incl + 1u : 64u;
+        uint32_t v = (lane < take && idx >= 0) ? static_cast<uint32_t>(w) : 0u;
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+        prefix += v;
+        if (first_incl < 64u) break;
+        hi -= 64;
+    }
+    return prefix;
+}
+
+// Adds the packed 16/16 LDS words of this thread's slots into its i32 sums (optionally zeroing them). Block-wide.
+template <int SLOTS>
+__device__ __forceinline__ void unpack_slots(int32_t *lds, uint32_t tid, int32_t (&accg)[SLOTS], int32_t (&acch)[SLOTS],
+                                             bool clear) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+        int32_t v = lds[tid + j * 1024];
+        if (clear) lds[tid + j * 1024] = 0;
+        int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
+        accg[j] += gq;
+        acch[j] += (v - gq) >> 16;
+    }
+    __syncthreads();
+}
+
+template <int W>
+__global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
+    constexpr int DW = W / 4;
+    constexpr int RPW = WAVE / DW;
+    constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
+    constexpr uint32_t STEP = 16u * RPW * UNROLL;
+    constexpr int SLOTS = 256 * W / 1024;
+    __shared__ int32_t lds[256 * W];
+    __shared__ uint32_t list[STEP_TILE];
+    __shared__ uint32_t wl[2][16];
+    __shared__ uint32_t s_tile, s_prefix;
+
+    Plan *plan = a.plan;
+    if (!plan->active) return;
+    const bool hist = plan->may_search != 0;
+    if (!hist && !a.partition) return;
+    const uint32_t begin = plan->begin, count = plan->count;
+    const uint32_t ntiles = (count + STEP_TILE - 1) / STEP_TILE;
+    const uint32_t groups = step_groups(count, a.max_groups);
+    if (blockIdx.x >= groups) return;
+    const uint32_t *src = plan->src_buf ? a.buf1 : a.buf0;
+    uint32_t *dst = plan->src_buf ? a.buf0 : a.buf1;
+    const bool rev = plan->src_rev != 0;
+    const uint8_t *col = a.colbase + static_cast<size_t>(plan->col) * a.rows;
+    uint32_t left_bins[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) left_bins[i] = plan->left_bins[i];
+    const uint32_t built_left = plan->built_side == 0 ? 1u : 0u;
+    const uint32_t epoch = plan->epoch;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    const uint32_t d = lane % DW, rsub = lane / DW;
+    const uint32_t rot = (lane & 31u) >> 3;
+    const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
+    int32_t accg[SLOTS], acch[SLOTS];
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
+    if (hist)
+        for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
+    uint32_t pending = 0;  // rows added to the packed LDS words since they were last unpacked
+
+    uint32_t next = blockIdx.x;  // histogram-only launches take tiles blockIdx.x, + groups, ...
+    for (;;) {
+        __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
+        if (tid == 0) s_tile = a.partition ? atomicAdd(&plan->ticket, 1u) : next;
+        __syncthreads();
+        const uint32_t t = s_tile;
+        next += groups;
+        if (t >= ntiles) break;
+        const uint32_t t0 = t * STEP_TILE;
+        const uint32_t valid = count - t0 < STEP_TILE ? count - t0 : STEP_TILE;
+        uint32_t row[2];
+        bool ok[2], left[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t i = t0 + j * 1024 + tid;
+            ok[j] = i < count;
+            uint32_t ic = ok[j] ? i : count - 1;
+            row[j] = src[rev ? begin + count - 1 - ic : begin + ic];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t b = col[row[j]];
+            left[j] = ok[j] && ((left_bins[b >> 5] >> (b & 31u)) & 1u);
+        }
+        uint32_t below[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            unsigned long long m = __ballot(left[j]);
+            below[j] = static_cast<uint32_t>(__popcll(m & below_mask));
+            if (lane == 0) wl[j][wave] = static_cast<uint32_t>(__popcll(m));
+        }
+        __syncthreads();
+        // lefts before each row of the tile (rows in order: sub-tile, wave, lane)
+        uint32_t sub0 = 0, sub1 = 0, before0 = 0, before1 = 0;
+        for (uint32_t w = 0; w < 16; ++w) {
+            uint32_t v0 = wl[0][w], v1 = wl[1][w];
+            sub0 += v0;
+            sub1 += v1;
+            if (w < wave) {
+                before0 += v0;
+                before1 += v1;
+            }
+        }
+        const uint32_t tile_left = sub0 + sub1;
+        uint32_t lrank[2] = {before0 + below[0], sub0 + before1 + below[1]};
+        if (a.partition && tid == 0)
+            __hip_atomic_store(a.status + t, status_word(epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (hist) {  // the tile's rows of the built child, in order
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t pos = j * 1024 + tid;
+                if (ok[j] && (left[j] ? 1u : 0u) == built_left) list[built_left ? lrank[j] : pos - lrank[j]] = row[j];
+            }
+        }
+        if (a.partition) {
+            if (wave == 0) {
+                uint32_t prefix = t == 0 ? 0u : lookback(a.status, t, epoch, a.ctl);
+                if (lane == 0) {
+                    if (t > 0)
+                        __hip_atomic_store(a.status + t, status_word(epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    s_prefix = prefix;
+                    if (t == ntiles - 1) plan->left = prefix + tile_left;
+                }
+            }
+            __syncthreads();
+            const uint32_t lp = s_prefix, rp = t0 - lp;  // lefts and rights before the tile
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (!ok[j]) continue;
+                if (left[j]) {
+                    uint32_t k = lp + lrank[j];
+                    if (k < count) dst[begin + k] = row[j];
+                } else {
+                    uint32_t k = rp + (j * 1024 + tid - lrank[j]);
+                    if (k < count) dst[begin + count - 1 - k] = row[j];
+                }
+            }
+        }
+        if (hist) {  // their histogram
+            const uint32_t nb = built_left ? tile_left : valid - tile_left;
+            __syncthreads();
+            uint32_t c0 = 0;
+            while (c0 < nb) {
+                if (pending >= a.flush_rows) {
+                    unpack_slots<SLOTS>(lds, tid, accg, acch, true);
+                    pending = 0;
+                }
+                uint32_t room = a.flush_rows - pending;
+                uint32_t c1 = nb - c0 < room ? nb : c0 + room;
+                const uint32_t last = c1 - 1;
+                for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
+                    uint32_t r[UNROLL];
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) r[u] = list[min(base + u * RPW + rsub, last)];
+                    uint32_t dw[UNROLL];
+                    int32_t gq[UNROLL];
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        gq[u] = a.gh[r[u]];
+                        dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
+                    }
+#pragma unroll
+                    for (int u = 0; u < UNROLL; ++u) {
+                        int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            uint32_t x = (k + rot) & 3u;
+                            uint32_t b = (dw[u] >> (8u * x)) & 255u;
+                            atomicAdd(&lds[b * W + 4u * d + x], gv);
+                        }
+                    }
+                }
+                pending += c1 - c0;
+                c0 = c1;
+            }
+        }
+    }
+    if (!hist) return;
+    unpack_slots<SLOTS>(lds, tid, accg, acch, false);
+    int2 *out = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) out[tid + j * 1024] = make_int2(accg[j], acch[j]);
+}
+
+// Four columns of one slab, reduced and scanned together by k_step_finish.
+struct ColGroup {
+    uint64_t partial;  // the slab's partials, in {g, h} pairs from the start of the step partial buffer
+    uint32_t width;    // the slab's W
+    uint32_t c0;       // first column of the group in the slab
+    uint32_t gcol;     // first column of the group in the global column arrays
+    uint32_t pad_;
+};
+
+constexpr uint32_t CG_COLS = 4;
+constexpr uint32_t FIN_CHUNKS = 8;  // gridDim.y of k_step_finish: bin chunks per column group at most
+
+struct FinishArgs {
+    const int32_t *partial;     // the step partial buffer
+    const ColGroup *cgs;        // [ncg]
+    const uint32_t *col_offset; // per global column: first bin of its feature in the flat histogram
+    const uint32_t *col_bins;   // per global column: the feature's bins (0 for padding)
+    const int32_t *col_feat;    // per global column: the feature, -1 for padding
+    uint32_t *cg_count;         // [ncg] chunk blocks done; returned to 0 by the last one
+    uint32_t *done_count;       // column groups done; returned to 0 by the last one
+    uint32_t ncg;
+    uint32_t max_groups;        // k_step_rows' grid
+};
+
+// Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
+// which then sees the global stores every arriving block made before arriving; that block returns the counter
+// to 0. Each thread first waits for its own stores to reach L2, so thread 0's release fence (an L2 write-back,
+// waited for before the increment) covers the whole block, and its acquire fence covers the last block's reads.
+__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) {
+    __shared__ uint32_t s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __builtin_amdgcn_s_waitcnt(0);
+        bool last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target - 1u;
+        if (last) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        s_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return s_last != 0;
+}
+
+// Bin chunks of a column group for `groups` partials: up to 64 partials, each thread sums at most 8 of them
+// (one round of loads); beyond, 8 chunks.
+__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups) {
+    return groups <= 8 ? 1u : (groups <= 16 ? 2u : (groups <= 32 ? 4u : 8u));
+}
+
+// grid: (ncg, FIN_CHUNKS), 1024 threads.
+__global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a) {
+    __shared__ int64_t red[1024][2];
+    __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
+    __shared__ uint32_t s_found[2][CG_COLS][2];
+    const Plan &p = *g.plan;
+    if (!p.active) return;
+    if (!p.may_search) {  // no histogram: apply and plan
+        if (blockIdx.x == 0 && blockIdx.y == 0) finish_step(g);
+        return;
+    }
+    const uint32_t groups = step_groups(p.count, a.max_groups);
+    const uint32_t chunks = finish_chunks(groups);
+    if (blockIdx.y >= chunks) return;
+    const uint32_t tid = threadIdx.x;
+    const ColGroup cg = a.cgs[blockIdx.x];
+    // what the group's scans need, read now: wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
+    const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
+    const int32_t sf = a.col_feat[cg.gcol + scol];
+    FeatDev sm = {};
+    bool sev = false;
+    if (sf >= 0) {
+        sm = g.feats[sf];
+        sev = g.evaluate[sf] != 0;
+    }
+    int64_t *built = g.pool + static_cast<size_t>(p.built_slot) * g.slot_stride;
+    int64_t *parent = g.pool + static_cast<size_t>(p.parent_slot) * g.slot_stride;
+
+    // (bin, column) slots of this chunk: S = 1024 / chunks; `ways` threads per slot sum interleaved partials
+    const uint32_t nbins = 256u / chunks, S = nbins * CG_COLS, bin0 = blockIdx.y * nbins;
+    const uint32_t ways = 1024u / S;
+    const size_t pstride = step_partial_stride(cg.width);
+    const int2 *part = reinterpret_cast<const int2 *>(a.partial) + cg.partial + cg.c0;
+    {
+        const uint32_t s = tid % S, q = tid / S;
+        const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
+        const int2 *src = part + static_cast<size_t>(bin) * cg.width + cc;
+        int64_t sg = 0, sh = 0;
+        for (uint32_t w = q; w < groups; w += 8u * ways) {
+            int2 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                uint32_t wk = w + k * ways;
+                v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
+                if (wk >= groups) v[k] = make_int2(0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                sg += v[k].x;
+                sh += v[k].y;
+            }
+        }
+        if (ways > 1u) {
+            red[tid][0] = sg;
+            red[tid][1] = sh;
+            __syncthreads();
+            if (q == 0)
+                for (uint32_t k = 1; k < ways; ++k) {
+                    sg += red[tid + k * S][0];
+                    sh += red[tid + k * S][1];
+                }
+        }
+        const uint32_t gc = cg.gcol + cc;
+        if (q == 0 && bin < a.col_bins[gc]) {
+            size_t o = 2 * (static_cast<size_t>(a.col_offset[gc]) + bin);
+            built[o] = sg;
+            built[o + 1] = sh;
+            parent[o] -= sg;
+            parent[o + 1] -= sh;
+        }
+    }
+    if (!arrive_last(&a.cg_count[blockIdx.x], chunks)) return;
+    // the group's features, both children, both directions (split.rs:584-620)
+    const int64_t cnt = child == 0 ? static_cast<int64_t>(p.left) : p.parent_count - static_cast<int64_t>(p.left);
+    const Ctx c = make_ctx(g.cfg, g.sg, g.sh, p.child_ug[child], p.child_uh[child], cnt);
+    const int64_t *hist = child == p.built_side ? built : parent;
+    const bool searched = sf >= 0 && scan_searched(c, sm, sev);
+    if (searched && (dir == 0 || scan_two_way(sm))) {
+        Grown r = {};
+        bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
+        if ((tid & 63u) == 0) {
+            s_grown[child][scol][dir] = r;
+            s_found[child][scol][dir] = found ? 1u : 0u;
+        }
+    }
+    __syncthreads();
+    if (sf >= 0 && dir == 0 && (tid & 63u) == 0) {
+        FeatCand r = {};
+        if (searched)
+            r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
+                                  scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
+        g.cands[static_cast<size_t>(child) * g.nf + sf] = r;
+    }
+    if (!arrive_last(a.done_count, a.ncg)) return;
+    finish_step(g);
 }
 
 }  // namespace srocm
