@@ -304,7 +304,6 @@ struct Context {
     DevBuf<uint32_t> part, part2, block_left, scalars;
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
-    DevBuf<uint32_t> gcol_offset, gcol_bins;
     DevBuf<int32_t> gcol_feat;
     uint32_t ncg = 0;
     uint64_t step_partial_pairs = 0;
@@ -466,34 +465,32 @@ struct Context {
             hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
         }
-        // groups of 8 slab columns for k_step_finish, and the global column arrays they index
+        // groups of CG_COLS slab columns for k_step_finish, and the feature of every slab column
         {
             std::vector<ColGroup> cg;
-            std::vector<uint32_t> goff, gbins;
             std::vector<int32_t> gfeat;
             uint64_t poff = 0;
             for (auto &s : slabs) {
                 s.step_partial_off = poff;
-                uint32_t gbase = static_cast<uint32_t>(goff.size());
-                for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) cg.push_back(ColGroup{poff, s.width, c0, gbase + c0, 0});
-                for (uint32_t c = 0; c < s.width; ++c) {
-                    bool real = c < s.feats.size();
-                    goff.push_back(real ? feats[s.feats[c]].hist_offset : 0u);
-                    gbins.push_back(real ? feats[s.feats[c]].num_bins : 0u);
-                    gfeat.push_back(real ? static_cast<int32_t>(s.feats[c]) : -1);
+                uint32_t gbase = static_cast<uint32_t>(gfeat.size());
+                for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) {
+                    ColGroup x{poff, s.width, c0, gbase + c0, 0, {}, {}};
+                    for (uint32_t k = 0; k < CG_COLS; ++k) {
+                        bool real = c0 + k < s.feats.size();
+                        x.offset[k] = real ? feats[s.feats[c0 + k]].hist_offset : 0u;
+                        x.bins[k] = real ? feats[s.feats[c0 + k]].num_bins : 0u;
+                    }
+                    cg.push_back(x);
                 }
+                for (uint32_t c = 0; c < s.width; ++c) gfeat.push_back(c < s.feats.size() ? static_cast<int32_t>(s.feats[c]) : -1);
                 poff += static_cast<uint64_t>(cus) * step_partial_stride(s.width);
             }
             ncg = static_cast<uint32_t>(cg.size());
             step_partial_pairs = std::max<uint64_t>(poff, 1);
             d_cgs.alloc(std::max<size_t>(cg.size(), 1));
-            gcol_offset.alloc(std::max<size_t>(goff.size(), 1));
-            gcol_bins.alloc(std::max<size_t>(goff.size(), 1));
-            gcol_feat.alloc(std::max<size_t>(goff.size(), 1));
+            gcol_feat.alloc(std::max<size_t>(gfeat.size(), 1));
             if (!cg.empty()) {
                 hip_check(hipMemcpy(d_cgs.p, cg.data(), cg.size() * sizeof(ColGroup), hipMemcpyHostToDevice), "upload column groups");
-                hip_check(hipMemcpy(gcol_offset.p, goff.data(), goff.size() * 4, hipMemcpyHostToDevice), "upload columns");
-                hip_check(hipMemcpy(gcol_bins.p, gbins.data(), gbins.size() * 4, hipMemcpyHostToDevice), "upload columns");
                 hip_check(hipMemcpy(gcol_feat.p, gfeat.data(), gfeat.size() * 4, hipMemcpyHostToDevice), "upload columns");
             }
         }
@@ -1186,7 +1183,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         k_root_select<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_select");
         // split steps: each is a no-op once the tree has stopped
-        FinishArgs fa{step_partial.p, d_cgs.p, gcol_offset.p, gcol_bins.p, gcol_feat.p, fin_counts.p, fin_counts.p + ncg, ncg, cus};
+        FinishArgs fa{step_partial.p, d_cgs.p, gcol_feat.p, fin_counts.p, fin_counts.p + ncg, ncg, cus, flush_rows()};
         for (uint32_t s = 0; s + 1 < L; ++s) {
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (prof.on) {
@@ -1197,7 +1194,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
             for (size_t si = 0; si < slabs.size(); ++si) {
                 const Slab &sl = slabs[si];
                 StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
-                            tile_status.p, d_plan.p, d_ctl.p, flush_rows(), cus, si == 0 ? 1u : 0u};
+                            sl.col_bins.p, tile_status.p, d_plan.p, d_ctl.p, flush_rows(), cus, si == 0 ? 1u : 0u};
                 switch (sl.width) {
                 case 32: k_step_rows<32><<<cus, 1024, 0, stream>>>(sa); break;
                 case 64: k_step_rows<64><<<cus, 1024, 0, stream>>>(sa); break;

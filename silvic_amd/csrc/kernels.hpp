@@ -1343,21 +1343,70 @@ __global__ __launch_bounds__(256) void k_root_select(GrowState g) {
     plan_leaf(g, 0, leaf, 1);
 }
 
-// The end of a split step, by one block of 1024 threads (learner.rs:294-352, then learner.rs:418-429 and
-// 249-290): both children's best splits from their per-feature candidates (half a block each, split.rs:866-880),
-// the planned split applied to the tree and the leaf table (tree.rs:143-177), then the next leaf chosen and
-// planned. The leaf table, the candidates and the leaf keys are read once, together.
+// Wave-wide all-reductions through the DPP scan steps; every lane ends with the result.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void best_step(double &g, int &i, uint32_t lane) {
+    double og = double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(g)));
+    int oi = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(i)));
+    if (dpp_has_source<CTRL, ROW_MASK>(lane) && cand_better(og, oi, g, i)) {
+        g = og;
+        i = oi;
+    }
+}
+// The best (gain, index) pair: higher gain, then the lower index; index < 0 is "none".
+__device__ __forceinline__ void wave_best(double &g, int &i) {
+    const uint32_t lane = threadIdx.x & 63u;
+    best_step<DPP_ROW_SHR1, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR2, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR4, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR8, 0xf>(g, i, lane);
+    best_step<DPP_ROW_BCAST15, 0xa>(g, i, lane);
+    best_step<DPP_ROW_BCAST31, 0xc>(g, i, lane);
+    i = __builtin_amdgcn_readlane(i, 63);
+    g = double_of(readlane_u64(bits_of(g), 63));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void min_step(int &v, uint32_t lane) {
+    int o = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(v)));
+    if (dpp_has_source<CTRL, ROW_MASK>(lane) && o < v) v = o;
+}
+__device__ __forceinline__ int wave_min(int v) {
+    const uint32_t lane = threadIdx.x & 63u;
+    min_step<DPP_ROW_SHR1, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR2, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR4, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR8, 0xf>(v, lane);
+    min_step<DPP_ROW_BCAST15, 0xa>(v, lane);
+    min_step<DPP_ROW_BCAST31, 0xc>(v, lane);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ double readlane_f64(double v, uint32_t lane) { return double_of(readlane_u64(bits_of(v), lane)); }
+
+// A feature candidate as held by lane `owner`, broadcast to the wave.
+__device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
+    FeatCand r;
+    r.found = __builtin_amdgcn_readlane(c.found, owner);
+    r.splittable = __builtin_amdgcn_readlane(c.splittable, owner);
+    r.gain = readlane_f64(c.gain, owner);
+    r.best_gain = readlane_f64(c.best_gain, owner);
+    r.threshold = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.threshold), owner));
+    r.default_left = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.default_left), owner));
+    r.left_grad = readlane_f64(c.left_grad, owner);
+    r.left_hess = readlane_f64(c.left_hess, owner);
+    r.left_count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(c.left_count), owner));
+    r.left_units_g = readlane_f64(c.left_units_g, owner);
+    r.left_units_h = readlane_f64(c.left_units_h, owner);
+    r.col = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.col), owner));
+    r.nan_idx = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.nan_idx), owner));
+    return r;
+}
+
+// The end of a split step, by one wave (learner.rs:294-352, then learner.rs:418-429 and 249-290): both children's
+// best splits from their per-feature candidates (split.rs:866-880), the planned split applied to the tree and the
+// leaf table (tree.rs:143-177), then the next leaf chosen and planned. Values every lane computes alike are kept
+// uniform; lane 0 writes the scalars.
 __device__ void finish_step(const GrowState &g) {
-    __shared__ double s_gain[16];
-    __shared__ int s_feat[16];
-    __shared__ FeatCand s_win[2];
-    __shared__ SplitOut s_out[2];
-    __shared__ DLeaf s_leaf[3];  // the two children, then the next leaf when it is neither
-    __shared__ uint32_t s_searched, s_go, s_next, s_ok;
-    __shared__ int s_first[16];
-    __shared__ double s_kgain[16];
-    __shared__ int s_kidx[16];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
     const Plan &P = *g.plan;
     GrowCtl *ctl = g.ctl;
     const uint32_t n = ctl->num_leaves;  // leaves before the step; it creates leaf n
@@ -1365,157 +1414,136 @@ __device__ void finish_step(const GrowState &g) {
     const int64_t left = static_cast<int64_t>(P.left);
     const int64_t right = P.parent_count - left;
     const bool may_search = P.may_search != 0;
-    // this thread's leaf keys, for the choice of the next leaf (leaves ascend within a thread)
-    // (read up front with everything else)
-    LeafKey key_own[1];
-    key_own[0] = tid < n ? g.keys[tid] : LeafKey{0.0, 0u, 0u};
+    const DLeaf pl = g.leaves[index];
+    const SplitOut &info = pl.best;
+    // read up front: this lane's leaf keys (leaves lane + 64 j, j < 4) and mask flags (features lane + 64 k, k < 32)
+    LeafKey kp[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t i = lane + 64u * j;
+        kp[j] = i < n ? g.keys[i] : LeafKey{0.0, 0u, 0u};
+    }
+    uint32_t mbits = 0;
+    for (uint32_t k = 0, f = lane; k < 32 && f < g.nf; ++k, f += 64u) mbits |= (g.mask[f] != 0 ? 1u : 0u) << k;
+    uint32_t sbits[2] = {0u, 0u};  // the children's splittable flags for the same features
 
-    // -- both children's best splits: half h (512 threads) takes child h
-    const uint32_t half = tid >> 9, ht = tid & 511u;
+    // -- both children's best splits (every lane holds features lane, lane + 64, ...)
+    SplitOut out[2] = {};
     if (may_search) {
-        const FeatCand *cands = g.cands + static_cast<size_t>(half) * g.nf;
-        uint8_t *row = g.splittable + static_cast<size_t>(half == 0 ? index : n) * g.nf;
-        double best = 0.0;
-        int bf = -1;
-        FeatCand bc = {};
-        for (uint32_t f = ht; f < g.nf; f += 512u) {
-            FeatCand c = cands[f];
-            row[f] = static_cast<uint8_t>(c.splittable);
-            if (!c.found) continue;
-            double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
-            if (cand_better(gv, static_cast<int>(f), best, bf)) {
-                best = gv;
-                bf = static_cast<int>(f);
-                bc = c;
-            }
-        }
-        double wb = best;
-        int wf = bf;
-        for (int o = 32; o >= 1; o >>= 1) {
-            double og = __shfl_xor(wb, o);
-            int of = __shfl_xor(wf, o);
-            if (cand_better(og, of, wb, wf)) {
-                wb = og;
-                wf = of;
-            }
-        }
-        if (lane == 0) {
-            s_gain[wave] = wb;
-            s_feat[wave] = wf;
-        }
-        __syncthreads();
-        if (ht == 0) {
-            for (uint32_t w = half * 8 + 1; w < half * 8 + 8; ++w)
-                if (cand_better(s_gain[w], s_feat[w], wb, wf)) {
-                    wb = s_gain[w];
-                    wf = s_feat[w];
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ++ch) {
+            const FeatCand *cands = g.cands + static_cast<size_t>(ch) * g.nf;
+            uint8_t *row = g.splittable + static_cast<size_t>(ch == 0 ? index : n) * g.nf;
+            double best = 0.0;
+            int bf = -1;
+            FeatCand bc = {};
+            for (uint32_t k = 0, f = lane; f < g.nf; ++k, f += 64u) {
+                FeatCand c = cands[f];
+                row[f] = static_cast<uint8_t>(c.splittable);
+                if (k < 32) sbits[ch] |= (c.splittable ? 1u : 0u) << k;
+                if (!c.found) continue;
+                double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+                if (cand_better(gv, static_cast<int>(f), best, bf)) {
+                    best = gv;
+                    bf = static_cast<int>(f);
+                    bc = c;
                 }
-            s_feat[half * 8] = wf;
-        }
-        __syncthreads();
-        if (bf >= 0 && bf == s_feat[half * 8]) s_win[half] = bc;
-        __syncthreads();
-        if (ht == 0) {
-            SplitOut o = {};
-            const int wf2 = s_feat[half * 8];
-            if (wf2 >= 0) {
-                int64_t cnt = half == 0 ? left : right;
-                o = split_out(s_win[half], wf2, make_ctx(g.cfg, g.sg, g.sh, P.child_ug[half], P.child_uh[half], cnt), g.cfg);
             }
-            s_out[half] = o;
+            double wb = best;
+            int wf = bf;
+            wave_best(wb, wf);
+            if (wf >= 0) {
+                const FeatCand c = readlane_cand(bc, static_cast<uint32_t>(wf) & 63u);
+                const int64_t cnt = ch == 0 ? left : right;
+                out[ch] = split_out(c, wf, make_ctx(g.cfg, g.sg, g.sh, P.child_ug[ch], P.child_uh[ch], cnt), g.cfg);
+            }
         }
     }
 
     // -- apply the split (tree.rs:143-177) and set up the children (learner.rs:294-352)
-    if (tid == 0) {
-        const DLeaf pl = g.leaves[index];
-        const SplitOut &info = pl.best;
-        uint32_t searched = 0;
-        if (left <= 0 || right <= 0) {
+    const bool ok = left > 0 && right > 0;
+    if (!ok) {
+        if (lane == 0) {
             ctl->error = 1;
-        } else {
-            const TreeDev &t = g.tree;
-            const int32_t node = static_cast<int32_t>(n) - 1;
-            if (pl.parent >= 0) {
-                if (pl.is_left) t.left_child[pl.parent] = node;
-                else t.right_child[pl.parent] = node;
-            }
-            t.split_feature[node] = info.feature;
-            t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
-            t.threshold_bin[node] = info.threshold;
-            t.default_left[node] = static_cast<uint8_t>(info.default_left);
-            t.left_child[node] = ~static_cast<int32_t>(index);
-            t.right_child[node] = ~static_cast<int32_t>(n);
-            t.internal_weight[node] = pl.weight;
-            t.internal_value[node] = pl.value;
-            t.internal_count[node] = left + right;
-            const int32_t depth = pl.depth + 1;
-            DLeaf l = {}, r = {};
-            l.begin = P.begin;
-            l.count = P.left;
-            r.begin = P.begin + P.left;
-            r.count = P.count - P.left;
-            l.ug = info.left_grad;
-            l.uh = info.left_hess;
-            r.ug = info.right_grad;
-            r.uh = info.right_hess;
-            l.cnt = left;
-            r.cnt = right;
-            l.buf = r.buf = 1u - P.src_buf;
-            l.rev = 0;  // the split step writes the left child first-first and the right child last-first
-            r.rev = 1;
-            l.depth = r.depth = depth;
-            l.parent = r.parent = node;
-            l.is_left = 1;
-            r.is_left = 0;
-            double lv = info.left_output, rv = info.right_output;
-            l.value = lv != lv ? 0.0 : lv;
-            r.value = rv != rv ? 0.0 : rv;
-            l.weight = info.left_hess * g.sh;
-            r.weight = info.right_hess * g.sh;
-            t.leaf_value[index] = l.value;
-            t.leaf_weight[index] = l.weight;
-            t.leaf_count[index] = left;
-            t.leaf_value[n] = r.value;
-            t.leaf_weight[n] = r.weight;
-            t.leaf_count[n] = right;
-            t.leaf_parent[index] = node;
-            t.leaf_parent[n] = node;
-            t.leaf_depth[index] = depth;
-            t.leaf_depth[n] = depth;
-            const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
-            const bool sr = may_search && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
-            l.slot = r.slot = -1;
-            if (sr) {
-                l.slot = P.built_side == 0 ? P.built_slot : P.parent_slot;
-                r.slot = P.built_side == 0 ? P.parent_slot : P.built_slot;
-            }
-            if (may_search) {  // the built child's histogram was made, searched or not
-                double built_rows = P.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
-                ctl->hist_rows += built_rows;
-                ctl->hist_bins += built_rows * static_cast<double>(P.used_columns);
-                ctl->hist_builds += 1.0;
-            }
-            ctl->part_rows += static_cast<double>(P.count);
-            ctl->num_leaves = n + 1;
-            s_leaf[0] = l;
-            s_leaf[1] = r;
-            searched = sr ? 1u : 0u;
+            g.plan->active = 0;
+            ctl->done = 1;
         }
-        s_searched = searched;
-        s_ok = (left > 0 && right > 0) ? 1u : 0u;
+        return;
     }
-    __syncthreads();
-    const bool ok = s_ok != 0;
-    if (tid < 2 && ok) {
-        DLeaf &c = s_leaf[tid];
-        c.has_best = 0;
-        if (s_searched) {
-            c.best = s_out[tid];
-            c.has_best = s_out[tid].found ? 1u : 0u;
+    const int32_t node = static_cast<int32_t>(n) - 1;
+    const int32_t depth = pl.depth + 1;
+    DLeaf l = {}, r = {};
+    l.begin = P.begin;
+    l.count = P.left;
+    r.begin = P.begin + P.left;
+    r.count = P.count - P.left;
+    l.ug = info.left_grad;
+    l.uh = info.left_hess;
+    r.ug = info.right_grad;
+    r.uh = info.right_hess;
+    l.cnt = left;
+    r.cnt = right;
+    l.buf = r.buf = 1u - P.src_buf;
+    l.rev = 0;  // the split step writes the left child first-first and the right child last-first
+    r.rev = 1;
+    l.depth = r.depth = depth;
+    l.parent = r.parent = node;
+    l.is_left = 1;
+    r.is_left = 0;
+    const double lv = info.left_output, rv = info.right_output;
+    l.value = lv != lv ? 0.0 : lv;
+    r.value = rv != rv ? 0.0 : rv;
+    l.weight = info.left_hess * g.sh;
+    r.weight = info.right_hess * g.sh;
+    const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
+    const bool searched = may_search && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
+    l.slot = r.slot = -1;
+    if (searched) {
+        l.slot = P.built_side == 0 ? P.built_slot : P.parent_slot;
+        r.slot = P.built_side == 0 ? P.parent_slot : P.built_slot;
+        l.best = out[0];
+        r.best = out[1];
+        l.has_best = out[0].found ? 1u : 0u;
+        r.has_best = out[1].found ? 1u : 0u;
+    }
+    if (lane == 0) {
+        const TreeDev &t = g.tree;
+        if (pl.parent >= 0) {
+            if (pl.is_left) t.left_child[pl.parent] = node;
+            else t.right_child[pl.parent] = node;
         }
+        t.split_feature[node] = info.feature;
+        t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
+        t.threshold_bin[node] = info.threshold;
+        t.default_left[node] = static_cast<uint8_t>(info.default_left);
+        t.left_child[node] = ~static_cast<int32_t>(index);
+        t.right_child[node] = ~static_cast<int32_t>(n);
+        t.internal_weight[node] = pl.weight;
+        t.internal_value[node] = pl.value;
+        t.internal_count[node] = left + right;
+        t.leaf_value[index] = l.value;
+        t.leaf_weight[index] = l.weight;
+        t.leaf_count[index] = left;
+        t.leaf_value[n] = r.value;
+        t.leaf_weight[n] = r.weight;
+        t.leaf_count[n] = right;
+        t.leaf_parent[index] = node;
+        t.leaf_parent[n] = node;
+        t.leaf_depth[index] = depth;
+        t.leaf_depth[n] = depth;
+        if (may_search) {  // the built child's histogram was made, searched or not
+            double built_rows = P.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
+            ctl->hist_rows += built_rows;
+            ctl->hist_bins += built_rows * static_cast<double>(P.used_columns);
+            ctl->hist_builds += 1.0;
+        }
+        ctl->part_rows += static_cast<double>(P.count);
+        ctl->num_leaves = n + 1;
+        g.leaves[index] = l;
+        g.leaves[n] = r;
+        g.keys[index] = LeafKey{l.best.gain, l.has_best, 0u};
+        g.keys[n] = LeafKey{r.best.gain, r.has_best, 0u};
     }
-    __syncthreads();
 
     // -- best_leaf (learner.rs:418-429) over leaves 0..=n, the children's keys replacing the split leaf's and
     // adding leaf n: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
@@ -1523,73 +1551,88 @@ __device__ void finish_step(const GrowState &g) {
     int first = 1 << 30;
     double kg = 0.0;
     int ki = -1;
-    if (ok) {
-        for (uint32_t i = tid; i <= n; i += blockDim.x) {
-            LeafKey k;
-            if (i == index || i == n) {
-                const DLeaf &c = s_leaf[i == index ? 0 : 1];
-                k = LeafKey{c.best.gain, c.has_best, 0u};
-            } else {
-                k = i == tid ? key_own[0] : g.keys[i];
-            }
-            if (!k.has) continue;
-            const bool nan = k.gain != k.gain;
-            const int code = 2 * static_cast<int>(i) + (nan ? 1 : 0);
-            if (code < first) first = code;
-            if (nan) continue;
-            if (cand_better(k.gain, static_cast<int>(i), kg, ki)) {
-                kg = k.gain;
-                ki = static_cast<int>(i);
-            }
+    auto consider = [&](uint32_t i, LeafKey k) {
+        if (i == index) k = LeafKey{l.best.gain, l.has_best, 0u};
+        else if (i == n) k = LeafKey{r.best.gain, r.has_best, 0u};
+        if (!k.has) return;
+        const bool nan = k.gain != k.gain;
+        const int code = 2 * static_cast<int>(i) + (nan ? 1 : 0);
+        if (code < first) first = code;
+        if (nan) return;
+        if (cand_better(k.gain, static_cast<int>(i), kg, ki)) {
+            kg = k.gain;
+            ki = static_cast<int>(i);
         }
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        int of = __shfl_xor(first, o);
-        first = of < first ? of : first;
-        double og = __shfl_xor(kg, o);
-        int oi = __shfl_xor(ki, o);
-        if (cand_better(og, oi, kg, ki)) {
-            kg = og;
-            ki = oi;
-        }
-    }
-    if (lane == 0) {
-        s_first[wave] = first;
-        s_kgain[wave] = kg;
-        s_kidx[wave] = ki;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t nw = blockDim.x >> 6;
-        for (uint32_t w = 1; w < nw; ++w) {
-            if (s_first[w] < first) first = s_first[w];
-            if (cand_better(s_kgain[w], s_kidx[w], kg, ki)) {
-                kg = s_kgain[w];
-                ki = s_kidx[w];
-            }
-        }
-        const bool nan_first = first < (1 << 30) && (first & 1);
-        const bool go = ok && !ctl->done && n + 1 < g.num_leaves && !nan_first && ki >= 0 && kg > 0.0;
-        s_go = go ? 1u : 0u;
-        s_next = go ? static_cast<uint32_t>(ki) : 0u;
-        if (ok) {
-            g.leaves[index] = s_leaf[0];
-            g.leaves[n] = s_leaf[1];
-            g.keys[index] = LeafKey{s_leaf[0].best.gain, s_leaf[0].has_best, 0u};
-            g.keys[n] = LeafKey{s_leaf[1].best.gain, s_leaf[1].has_best, 0u};
-        }
-        if (go) {
-            const uint32_t next = static_cast<uint32_t>(ki);
-            if (next != index && next != n) s_leaf[2] = g.leaves[next];
-        } else {
+    };
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j)
+        if (lane + 64u * j <= n) consider(lane + 64u * j, kp[j]);
+    for (uint32_t i = lane + 256u; i <= n; i += 64u) consider(i, g.keys[i]);
+    first = wave_min(first);
+    wave_best(kg, ki);
+    const bool nan_first = first < (1 << 30) && (first & 1);
+    const bool go = !ctl->done && n + 1 < g.num_leaves && !nan_first && ki >= 0 && kg > 0.0;
+    if (!go) {
+        if (lane == 0) {
             g.plan->active = 0;
             ctl->done = 1;
         }
+        return;
     }
-    __syncthreads();
-    if (!s_go) return;
-    const uint32_t next = s_next;
-    plan_leaf(g, next, s_leaf[next == index ? 0 : (next == n ? 1 : 2)], n + 1);
+    const uint32_t next = static_cast<uint32_t>(ki);
+    const DLeaf nl = next == index ? l : (next == n ? r : g.leaves[next]);
+
+    // -- plan the next step (learner.rs:249-290): evaluated features (the tree's mask and the leaf's splittable
+    // flags, learner.rs:262-265; the flags of a new child were written by this lane above)
+    const uint8_t *row = g.splittable + static_cast<size_t>(next) * g.nf;
+    const bool child_next = searched && (next == index || next == n);
+    const uint32_t cbits = next == index ? sbits[0] : sbits[1];
+    uint32_t used = 0;
+    for (uint32_t k = 0, f = lane; f < g.nf; ++k, f += 64u) {
+        const bool m = k < 32 ? ((mbits >> k) & 1u) : (g.mask[f] != 0);
+        const bool sp = (k < 32 && child_next) ? ((cbits >> k) & 1u) : (row[f] != 0);
+        const bool e = m && sp;
+        g.evaluate[f] = static_cast<uint8_t>(e);
+        used += static_cast<uint32_t>(__popcll(__ballot(e)));
+    }
+    if (lane == 0) {
+        const SplitOut &ni = nl.best;
+        const uint32_t nn = n + 1;  // the tree's leaves after this step; the next step creates leaf nn
+        Plan &p = *g.plan;
+        p.active = 1;
+        p.index = next;
+        p.begin = nl.begin;
+        p.count = nl.count;
+        p.parent_count = nl.cnt;
+        p.src_buf = nl.buf;
+        p.src_rev = nl.rev;
+        p.epoch = ctl->epoch + 1;
+        ctl->epoch = ctl->epoch + 1;
+        p.ticket = 0;
+        p.left = 0;
+        p.col = ni.col;
+        // learner.rs:432-452: bins 0..=threshold, and the NaN bin when missing values go left
+        const uint32_t upto = ni.threshold + 1;
+        const bool nan_left = ni.default_left && ni.nan_idx != NO_BIN;
+#pragma unroll
+        for (uint32_t w = 0; w < 8; ++w) {
+            uint32_t lo = 32 * w;
+            uint32_t word = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
+            if (nan_left && (ni.nan_idx >> 5) == w) word |= 1u << (ni.nan_idx & 31u);
+            p.left_bins[w] = word;
+        }
+        p.used_columns = used;
+        p.built_side = ni.left_count <= ni.right_count ? 0u : 1u;
+        p.may_search = nl.slot >= 0 && nn + 1 < g.num_leaves && depth_allows(g, nl.depth + 1);
+        p.parent_slot = nl.slot;
+        p.built_slot = p.may_search ? static_cast<int32_t>(nn) : -1;
+        p.child_ug[0] = ni.left_grad;
+        p.child_uh[0] = ni.left_hess;
+        p.child_ug[1] = ni.right_grad;
+        p.child_uh[1] = ni.right_hess;
+        g.keys[next].has = 0;
+        g.leaves[next].has_best = 0;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1612,6 +1655,7 @@ __device__ void finish_step(const GrowState &g) {
 // ---------------------------------------------------------------------------------------------------------
 
 constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: two per thread of a 1024-thread block
+constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
 // A split step's partials are 256 * W {g, h} pairs per workgroup, padded so that the same slot of consecutive
 // partials does not fall at a power-of-two distance (which maps it to the same memory channel and bank).
 constexpr uint32_t STEP_PARTIAL_PAD = 288;
@@ -1625,7 +1669,8 @@ struct StepArgs {
     const uint8_t *colbase;      // column-major bins [feature][rows]
     uint64_t rows;
     uint32_t *buf0, *buf1;       // the partition buffers
-    int32_t *partial;            // this slab's partials: [max_groups][step_partial_stride(W)] {g, h}
+    int32_t *partial;            // this slab's partials, step_partial_stride(W) elements apart (see step_packed)
+    const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
     unsigned long long *status;  // per-tile status words
     Plan *plan;
     GrowCtl *ctl;
@@ -1633,6 +1678,14 @@ struct StepArgs {
     uint32_t max_groups;         // == gridDim.x
     uint32_t partition;          // 1: this launch partitions (the first slab's); 0: histogram only
 };
+
+// Whether a step's partials are the packed 16/16 LDS words (one i32 per slot): when every workgroup takes a
+// single tile (so its sums never outgrow 16 bits); otherwise {g, h} i32 pairs. The same in both kernels.
+// Packed partials are column-group major ([group][256 bins][4 columns]) so that a group's bins are contiguous;
+// pair partials are slot major ([bin][W columns]).
+__device__ __forceinline__ bool step_packed(uint32_t count, uint32_t max_groups, uint32_t flush_rows) {
+    return (count + STEP_TILE - 1) / STEP_TILE <= max_groups && flush_rows >= STEP_TILE;
+}
 
 __device__ __forceinline__ uint32_t step_groups(uint32_t count, uint32_t max_groups) {
     uint32_t tiles = (count + STEP_TILE - 1) / STEP_TILE;
@@ -1716,6 +1769,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     const uint32_t ntiles = (count + STEP_TILE - 1) / STEP_TILE;
     const uint32_t groups = step_groups(count, a.max_groups);
     if (blockIdx.x >= groups) return;
+    const bool packed = step_packed(count, a.max_groups, a.flush_rows);  // then one tile per workgroup
     const uint32_t *src = plan->src_buf ? a.buf1 : a.buf0;
     uint32_t *dst = plan->src_buf ? a.buf0 : a.buf1;
     const bool rev = plan->src_rev != 0;
@@ -1856,12 +1910,56 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 c0 = c1;
             }
         }
+        if (packed) break;
     }
     if (!hist) return;
+    // the partial: slots of used bins only (slot = bin * W + column; this thread's column is tid % W)
+    const uint32_t col_bins = a.col_bins[tid % W];
+    if (packed) {
+        // task k: column c = k % W and bins 4q..4q+3 (q = k / W); rows of LDS read across the wave, then a 4x4
+        // transpose in each quad of lanes (the group's 4 columns) so that lane c % 4 holds bin 4q + c % 4 of all
+        // four columns and the quad stores 64 contiguous bytes.
+        __syncthreads();
+        int4 *out = reinterpret_cast<int4 *>(a.partial + static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
+        const uint32_t c4 = tid & 3u;
+#pragma unroll
+        for (int it = 0; it < SLOTS / 4; ++it) {
+            const uint32_t k = tid + 1024u * it, c = k % W, q = k / W;
+            int32_t v0 = lds[(4 * q + 0) * W + c], v1 = lds[(4 * q + 1) * W + c];
+            int32_t v2 = lds[(4 * q + 2) * W + c], v3 = lds[(4 * q + 3) * W + c];
+            // butterfly transpose over the quad: at level b a lane keeps the elements whose index bit b matches its
+            // own and swaps the other two with lane c4 ^ b; every choice is one select on a lane bit
+            {
+                const bool hi = (c4 & 1u) != 0;
+                const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v1, 0xB1, 0xf, 0xf, false);
+                const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v2 : v3, 0xB1, 0xf, 0xf, false);
+                const int32_t n0 = hi ? t0 : v0, n1 = hi ? v1 : t0, n2 = hi ? t1 : v2, n3 = hi ? v3 : t1;
+                v0 = n0;
+                v1 = n1;
+                v2 = n2;
+                v3 = n3;
+            }
+            {
+                const bool hi = (c4 & 2u) != 0;
+                const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v2, 0x4E, 0xf, 0xf, false);
+                const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v1 : v3, 0x4E, 0xf, 0xf, false);
+                const int32_t n0 = hi ? t0 : v0, n1 = hi ? t1 : v1, n2 = hi ? v2 : t0, n3 = hi ? v3 : t1;
+                v0 = n0;
+                v1 = n1;
+                v2 = n2;
+                v3 = n3;
+            }
+            int32_t o[4] = {v0, v1, v2, v3};  // o[j]: column (c & ~3) + j at bin 4q + c4
+            (void)col_bins;
+            out[(c / CG_COLS) * 256 + 4 * q + c4] = make_int4(o[0], o[1], o[2], o[3]);
+        }
+        return;
+    }
     unpack_slots<SLOTS>(lds, tid, accg, acch, false);
     int2 *out = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
 #pragma unroll
-    for (int j = 0; j < SLOTS; ++j) out[tid + j * 1024] = make_int2(accg[j], acch[j]);
+    for (int j = 0; j < SLOTS; ++j)
+        if ((tid + j * 1024) / W < col_bins) out[tid + j * 1024] = make_int2(accg[j], acch[j]);
 }
 
 // Four columns of one slab, reduced and scanned together by k_step_finish.
@@ -1871,21 +1969,21 @@ struct ColGroup {
     uint32_t c0;       // first column of the group in the slab
     uint32_t gcol;     // first column of the group in the global column arrays
     uint32_t pad_;
+    uint32_t offset[4];  // per column: its feature's first bin in the flat histogram
+    uint32_t bins[4];    // per column: the feature's bins (0 for padding)
 };
 
-constexpr uint32_t CG_COLS = 4;
 constexpr uint32_t FIN_CHUNKS = 8;  // gridDim.y of k_step_finish: bin chunks per column group at most
 
 struct FinishArgs {
     const int32_t *partial;     // the step partial buffer
     const ColGroup *cgs;        // [ncg]
-    const uint32_t *col_offset; // per global column: first bin of its feature in the flat histogram
-    const uint32_t *col_bins;   // per global column: the feature's bins (0 for padding)
     const int32_t *col_feat;    // per global column: the feature, -1 for padding
     uint32_t *cg_count;         // [ncg] chunk blocks done; returned to 0 by the last one
     uint32_t *done_count;       // column groups done; returned to 0 by the last one
     uint32_t ncg;
     uint32_t max_groups;        // k_step_rows' grid
+    uint32_t flush_rows;        // as given to k_step_rows
 };
 
 // Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
@@ -1910,25 +2008,28 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
     return s_last != 0;
 }
 
-// Bin chunks of a column group for `groups` partials: up to 64 partials, each thread sums at most 8 of them
-// (one round of loads); beyond, 8 chunks.
-__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups) {
+// Bin chunks of a column group for `groups` partials, so that each thread adds at most 8 of them (one round of
+// loads) where it can: packed partials are added a bin (four columns) per thread, pairs a slot per thread.
+__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups, bool packed) {
+    if (packed) return groups <= 32 ? 1u : (groups <= 64 ? 2u : (groups <= 128 ? 4u : 8u));
     return groups <= 8 ? 1u : (groups <= 16 ? 2u : (groups <= 32 ? 4u : 8u));
 }
 
 // grid: (ncg, FIN_CHUNKS), 1024 threads.
 __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a) {
-    __shared__ int64_t red[1024][2];
+    __shared__ int64_t red8[1024][8];  // partial sums on their way to stripe 0 (the first two words for pairs)
+    int64_t(*red)[8] = red8;
     __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
     __shared__ uint32_t s_found[2][CG_COLS][2];
     const Plan &p = *g.plan;
     if (!p.active) return;
     if (!p.may_search) {  // no histogram: apply and plan
-        if (blockIdx.x == 0 && blockIdx.y == 0) finish_step(g);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) finish_step(g);
         return;
     }
     const uint32_t groups = step_groups(p.count, a.max_groups);
-    const uint32_t chunks = finish_chunks(groups);
+    const bool packed = step_packed(p.count, a.max_groups, a.flush_rows);
+    const uint32_t chunks = finish_chunks(groups, packed);
     if (blockIdx.y >= chunks) return;
     const uint32_t tid = threadIdx.x;
     const ColGroup cg = a.cgs[blockIdx.x];
@@ -1948,24 +2049,83 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
     const uint32_t nbins = 256u / chunks, S = nbins * CG_COLS, bin0 = blockIdx.y * nbins;
     const uint32_t ways = 1024u / S;
     const size_t pstride = step_partial_stride(cg.width);
-    const int2 *part = reinterpret_cast<const int2 *>(a.partial) + cg.partial + cg.c0;
-    {
-        const uint32_t s = tid % S, q = tid / S;
-        const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
-        const int2 *src = part + static_cast<size_t>(bin) * cg.width + cc;
-        int64_t sg = 0, sh = 0;
-        for (uint32_t w = q; w < groups; w += 8u * ways) {
-            int2 v[8];
+    if (packed) {  // a thread per (bin, partial stripe) adds the bin's four columns
+        const uint32_t pways = 1024u / nbins;
+        const uint32_t bin = bin0 + tid % nbins, q = tid / nbins;
+        const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin;
+        const size_t stride4 = pstride / 4;
+        int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
+        for (uint32_t w = q; w < groups; w += 8u * pways) {
+            int4 v[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                uint32_t wk = w + k * ways;
-                v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
-                if (wk >= groups) v[k] = make_int2(0, 0);
+                uint32_t wk = w + k * pways;
+                v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
+                if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
             }
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                sg += v[k].x;
-                sh += v[k].y;
+                const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
+                    sg[c] += gq;
+                    sh[c] += (x[c] - gq) >> 16;
+                }
+            }
+        }
+        // stripes q > 0 hand their sums to stripe 0 through LDS
+        if (pways > 1u) {
+            int64_t *r8 = reinterpret_cast<int64_t *>(red8);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                r8[tid * 8 + 2 * c] = sg[c];
+                r8[tid * 8 + 2 * c + 1] = sh[c];
+            }
+            __syncthreads();
+            if (q == 0)
+                for (uint32_t k = 1; k < pways; ++k) {
+                    const int64_t *o8 = r8 + (tid + k * nbins) * 8;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        sg[c] += o8[2 * c];
+                        sh[c] += o8[2 * c + 1];
+                    }
+                }
+        }
+        if (q == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (bin < cg.bins[c]) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                    built[o] = sg[c];
+                    built[o + 1] = sh[c];
+                    parent[o] -= sg[c];
+                    parent[o + 1] -= sh[c];
+                }
+            }
+        }
+    } else {
+        const uint32_t s = tid % S, q = tid / S;
+        const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
+        const bool used = bin < cg.bins[cc];
+        const size_t at = static_cast<size_t>(bin) * cg.width + cg.c0 + cc;  // the slot within a partial
+        int64_t sg = 0, sh = 0;
+        if (used) {
+            const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + at;
+            for (uint32_t w = q; w < groups; w += 8u * ways) {
+                int2 v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    uint32_t wk = w + k * ways;
+                    v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
+                    if (wk >= groups) v[k] = make_int2(0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    sg += v[k].x;
+                    sh += v[k].y;
+                }
             }
         }
         if (ways > 1u) {
@@ -1978,9 +2138,8 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
                     sh += red[tid + k * S][1];
                 }
         }
-        const uint32_t gc = cg.gcol + cc;
-        if (q == 0 && bin < a.col_bins[gc]) {
-            size_t o = 2 * (static_cast<size_t>(a.col_offset[gc]) + bin);
+        if (q == 0 && used) {
+            const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
             built[o] = sg;
             built[o + 1] = sh;
             parent[o] -= sg;
@@ -2010,7 +2169,7 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
         g.cands[static_cast<size_t>(child) * g.nf + sf] = r;
     }
     if (!arrive_last(a.done_count, a.ncg)) return;
-    finish_step(g);
+    if (tid < 64) finish_step(g);
 }
 
 }  // namespace srocm
