@@ -1749,176 +1749,190 @@ __device__ __forceinline__ void unpack_slots(int32_t *lds, uint32_t tid, int32_t
     __syncthreads();
 }
 
+// The step's plan as one workgroup of k_step_rows sees it.
+struct StepView {
+    Plan *plan;
+    uint32_t begin, count, ntiles, groups;
+    const uint32_t *src;
+    uint32_t *dst;
+    bool rev, hist, partition;
+    const uint8_t *col;
+    uint32_t built_left;  // 1: the left child is histogrammed
+    uint32_t epoch;
+};
+
+struct StepShared {
+    uint32_t list[STEP_TILE];  // the tile's rows of the built child
+    uint32_t wl[2][16];        // left counts per (sub-tile, wave)
+    uint32_t left_bins[8];     // the split's bins that go left
+    uint32_t tile, prefix;
+};
+
+// One partition tile: its rows read in the leaf's order, its left count published, its offset from the look-back,
+// its rows scattered (left first-first, right last-first), and its rows of the built child left in sh.list in
+// order. Returns that row count. Block-wide.
+__device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs &a, uint32_t t, StepShared &sh) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    const uint32_t t0 = t * STEP_TILE;
+    const uint32_t valid = v.count - t0 < STEP_TILE ? v.count - t0 : STEP_TILE;
+    uint32_t row[2];
+    bool ok[2], left[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t i = t0 + j * 1024 + tid;
+        ok[j] = i < v.count;
+        uint32_t ic = ok[j] ? i : v.count - 1;
+        row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t b = v.col[row[j]];
+        left[j] = ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
+    }
+    uint32_t below[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        unsigned long long m = __ballot(left[j]);
+        below[j] = static_cast<uint32_t>(__popcll(m & below_mask));
+        if (lane == 0) sh.wl[j][wave] = static_cast<uint32_t>(__popcll(m));
+    }
+    __syncthreads();
+    // lefts before each row of the tile (rows in order: sub-tile, wave, lane)
+    uint32_t sub0 = 0, sub1 = 0, before0 = 0, before1 = 0;
+    for (uint32_t w = 0; w < 16; ++w) {
+        uint32_t v0 = sh.wl[0][w], v1 = sh.wl[1][w];
+        sub0 += v0;
+        sub1 += v1;
+        if (w < wave) {
+            before0 += v0;
+            before1 += v1;
+        }
+    }
+    const uint32_t tile_left = sub0 + sub1;
+    uint32_t lrank[2] = {before0 + below[0], sub0 + before1 + below[1]};
+    if (v.partition && tid == 0)
+        __hip_atomic_store(a.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    if (v.hist) {  // the tile's rows of the built child, in order
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t pos = j * 1024 + tid;
+            if (ok[j] && (left[j] ? 1u : 0u) == v.built_left) sh.list[v.built_left ? lrank[j] : pos - lrank[j]] = row[j];
+        }
+    }
+    if (v.partition) {
+        if (wave == 0) {
+            uint32_t prefix = t == 0 ? 0u : lookback(a.status, t, v.epoch, a.ctl);
+            if (lane == 0) {
+                if (t > 0)
+                    __hip_atomic_store(a.status + t, status_word(v.epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                sh.prefix = prefix;
+                if (t == v.ntiles - 1) v.plan->left = prefix + tile_left;
+            }
+        }
+        __syncthreads();
+        const uint32_t lp = sh.prefix, rp = t0 - lp;  // lefts and rights before the tile
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (!ok[j]) continue;
+            if (left[j]) {
+                uint32_t k = lp + lrank[j];
+                if (k < v.count) v.dst[v.begin + k] = row[j];
+            } else {
+                uint32_t k = rp + (j * 1024 + tid - lrank[j]);
+                if (k < v.count) v.dst[v.begin + v.count - 1 - k] = row[j];
+            }
+        }
+    }
+    const uint32_t nb = v.built_left ? tile_left : valid - tile_left;
+    __syncthreads();  // the list is complete
+    return nb;
+}
+
+// The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
+// lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free.
+template <int W, int UNROLL>
+__device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
+                                          const uint32_t *bins32) {
+    constexpr int DW = W / 4;
+    constexpr int RPW = WAVE / DW;
+    constexpr uint32_t STEP = 16u * RPW * UNROLL;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t d = lane % DW, rsub = lane / DW;
+    const uint32_t rot = (lane & 31u) >> 3;
+    const uint32_t last = c1 - 1;
+    for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
+        uint32_t r[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) r[u] = list[min(base + u * RPW + rsub, last)];
+        uint32_t dw[UNROLL];
+        int32_t gq[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            gq[u] = gh[r[u]];
+            dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t x = (k + rot) & 3u;
+                uint32_t b = (dw[u] >> (8u * x)) & 255u;
+                atomicAdd(&lds[b * W + 4u * d + x], gv);
+            }
+        }
+    }
+}
+
 template <int W>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     constexpr int DW = W / 4;
     constexpr int RPW = WAVE / DW;
+    // multi-tile workgroups keep 2 * SLOTS accumulator registers: at W = 128 that leaves room for 8 rows per lane
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
-    constexpr uint32_t STEP = 16u * RPW * UNROLL;
     constexpr int SLOTS = 256 * W / 1024;
     __shared__ int32_t lds[256 * W];
-    __shared__ uint32_t list[STEP_TILE];
-    __shared__ uint32_t wl[2][16];
-    __shared__ uint32_t s_tile, s_prefix;
+    __shared__ StepShared sh;
 
     Plan *plan = a.plan;
     if (!plan->active) return;
-    const bool hist = plan->may_search != 0;
-    if (!hist && !a.partition) return;
-    const uint32_t begin = plan->begin, count = plan->count;
-    const uint32_t ntiles = (count + STEP_TILE - 1) / STEP_TILE;
-    const uint32_t groups = step_groups(count, a.max_groups);
-    if (blockIdx.x >= groups) return;
-    const bool packed = step_packed(count, a.max_groups, a.flush_rows);  // then one tile per workgroup
-    const uint32_t *src = plan->src_buf ? a.buf1 : a.buf0;
-    uint32_t *dst = plan->src_buf ? a.buf0 : a.buf1;
-    const bool rev = plan->src_rev != 0;
-    const uint8_t *col = a.colbase + static_cast<size_t>(plan->col) * a.rows;
-    uint32_t left_bins[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) left_bins[i] = plan->left_bins[i];
-    const uint32_t built_left = plan->built_side == 0 ? 1u : 0u;
-    const uint32_t epoch = plan->epoch;
-
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint64_t below_mask = (1ull << lane) - 1ull;
-    const uint32_t d = lane % DW, rsub = lane / DW;
-    const uint32_t rot = (lane & 31u) >> 3;
+    StepView v;
+    v.plan = plan;
+    v.hist = plan->may_search != 0;
+    v.partition = a.partition != 0;
+    if (!v.hist && !v.partition) return;
+    v.begin = plan->begin;
+    v.count = plan->count;
+    v.ntiles = (v.count + STEP_TILE - 1) / STEP_TILE;
+    v.groups = step_groups(v.count, a.max_groups);
+    if (blockIdx.x >= v.groups) return;
+    const bool packed = step_packed(v.count, a.max_groups, a.flush_rows);  // then one tile per workgroup
+    v.src = plan->src_buf ? a.buf1 : a.buf0;
+    v.dst = plan->src_buf ? a.buf0 : a.buf1;
+    v.rev = plan->src_rev != 0;
+    v.col = a.colbase + static_cast<size_t>(plan->col) * a.rows;
+    v.built_left = plan->built_side == 0 ? 1u : 0u;
+    v.epoch = plan->epoch;
+    const uint32_t tid = threadIdx.x;
+    if (tid < 8) sh.left_bins[tid] = plan->left_bins[tid];  // visible after the first barrier below
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
-    int32_t accg[SLOTS], acch[SLOTS];
-#pragma unroll
-    for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
-    if (hist)
+    if (v.hist)
         for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
-    uint32_t pending = 0;  // rows added to the packed LDS words since they were last unpacked
 
-    uint32_t next = blockIdx.x;  // histogram-only launches take tiles blockIdx.x, + groups, ...
-    for (;;) {
-        __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
-        if (tid == 0) s_tile = a.partition ? atomicAdd(&plan->ticket, 1u) : next;
-        __syncthreads();
-        const uint32_t t = s_tile;
-        next += groups;
-        if (t >= ntiles) break;
-        const uint32_t t0 = t * STEP_TILE;
-        const uint32_t valid = count - t0 < STEP_TILE ? count - t0 : STEP_TILE;
-        uint32_t row[2];
-        bool ok[2], left[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            uint32_t i = t0 + j * 1024 + tid;
-            ok[j] = i < count;
-            uint32_t ic = ok[j] ? i : count - 1;
-            row[j] = src[rev ? begin + count - 1 - ic : begin + ic];
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            uint32_t b = col[row[j]];
-            left[j] = ok[j] && ((left_bins[b >> 5] >> (b & 31u)) & 1u);
-        }
-        uint32_t below[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            unsigned long long m = __ballot(left[j]);
-            below[j] = static_cast<uint32_t>(__popcll(m & below_mask));
-            if (lane == 0) wl[j][wave] = static_cast<uint32_t>(__popcll(m));
-        }
-        __syncthreads();
-        // lefts before each row of the tile (rows in order: sub-tile, wave, lane)
-        uint32_t sub0 = 0, sub1 = 0, before0 = 0, before1 = 0;
-        for (uint32_t w = 0; w < 16; ++w) {
-            uint32_t v0 = wl[0][w], v1 = wl[1][w];
-            sub0 += v0;
-            sub1 += v1;
-            if (w < wave) {
-                before0 += v0;
-                before1 += v1;
-            }
-        }
-        const uint32_t tile_left = sub0 + sub1;
-        uint32_t lrank[2] = {before0 + below[0], sub0 + before1 + below[1]};
-        if (a.partition && tid == 0)
-            __hip_atomic_store(a.status + t, status_word(epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        if (hist) {  // the tile's rows of the built child, in order
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                uint32_t pos = j * 1024 + tid;
-                if (ok[j] && (left[j] ? 1u : 0u) == built_left) list[built_left ? lrank[j] : pos - lrank[j]] = row[j];
-            }
-        }
-        if (a.partition) {
-            if (wave == 0) {
-                uint32_t prefix = t == 0 ? 0u : lookback(a.status, t, epoch, a.ctl);
-                if (lane == 0) {
-                    if (t > 0)
-                        __hip_atomic_store(a.status + t, status_word(epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    s_prefix = prefix;
-                    if (t == ntiles - 1) plan->left = prefix + tile_left;
-                }
-            }
-            __syncthreads();
-            const uint32_t lp = s_prefix, rp = t0 - lp;  // lefts and rights before the tile
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if (!ok[j]) continue;
-                if (left[j]) {
-                    uint32_t k = lp + lrank[j];
-                    if (k < count) dst[begin + k] = row[j];
-                } else {
-                    uint32_t k = rp + (j * 1024 + tid - lrank[j]);
-                    if (k < count) dst[begin + count - 1 - k] = row[j];
-                }
-            }
-        }
-        if (hist) {  // their histogram
-            const uint32_t nb = built_left ? tile_left : valid - tile_left;
-            __syncthreads();
-            uint32_t c0 = 0;
-            while (c0 < nb) {
-                if (pending >= a.flush_rows) {
-                    unpack_slots<SLOTS>(lds, tid, accg, acch, true);
-                    pending = 0;
-                }
-                uint32_t room = a.flush_rows - pending;
-                uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                const uint32_t last = c1 - 1;
-                for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
-                    uint32_t r[UNROLL];
-#pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) r[u] = list[min(base + u * RPW + rsub, last)];
-                    uint32_t dw[UNROLL];
-                    int32_t gq[UNROLL];
-#pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        gq[u] = a.gh[r[u]];
-                        dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
-                    }
-#pragma unroll
-                    for (int u = 0; u < UNROLL; ++u) {
-                        int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            uint32_t x = (k + rot) & 3u;
-                            uint32_t b = (dw[u] >> (8u * x)) & 255u;
-                            atomicAdd(&lds[b * W + 4u * d + x], gv);
-                        }
-                    }
-                }
-                pending += c1 - c0;
-                c0 = c1;
-            }
-        }
-        if (packed) break;
-    }
-    if (!hist) return;
-    // the partial: slots of used bins only (slot = bin * W + column; this thread's column is tid % W)
-    const uint32_t col_bins = a.col_bins[tid % W];
     if (packed) {
-        // task k: column c = k % W and bins 4q..4q+3 (q = k / W); rows of LDS read across the wave, then a 4x4
-        // transpose in each quad of lanes (the group's 4 columns) so that lane c % 4 holds bin 4q + c % 4 of all
-        // four columns and the quad stores 64 contiguous bytes.
+        // one tile; the partial is the LDS words themselves, written column-group major: task k takes column
+        // c = k % W and bins 4q..4q+3 (q = k / W), reads LDS across the wave, and a butterfly transpose in each
+        // quad of lanes (the group's 4 columns) leaves lane c % 4 with bin 4q + c % 4 of all four columns, so the
+        // quad stores 64 contiguous bytes
+        __syncthreads();
+        if (tid == 0) sh.tile = v.partition ? atomicAdd(&plan->ticket, 1u) : blockIdx.x;
+        __syncthreads();
+        const uint32_t nb = step_tile(v, a, sh.tile, sh);
+        if (!v.hist) return;
+        hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         __syncthreads();
         int4 *out = reinterpret_cast<int4 *>(a.partial + static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
         const uint32_t c4 = tid & 3u;
@@ -1927,8 +1941,8 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
             const uint32_t k = tid + 1024u * it, c = k % W, q = k / W;
             int32_t v0 = lds[(4 * q + 0) * W + c], v1 = lds[(4 * q + 1) * W + c];
             int32_t v2 = lds[(4 * q + 2) * W + c], v3 = lds[(4 * q + 3) * W + c];
-            // butterfly transpose over the quad: at level b a lane keeps the elements whose index bit b matches its
-            // own and swaps the other two with lane c4 ^ b; every choice is one select on a lane bit
+            // at level b a lane keeps the elements whose index bit b matches its own and swaps the other two with
+            // lane c4 ^ b; every choice is one select on a lane bit
             {
                 const bool hi = (c4 & 1u) != 0;
                 const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v1, 0xB1, 0xf, 0xf, false);
@@ -1949,13 +1963,42 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 v2 = n2;
                 v3 = n3;
             }
-            int32_t o[4] = {v0, v1, v2, v3};  // o[j]: column (c & ~3) + j at bin 4q + c4
-            (void)col_bins;
-            out[(c / CG_COLS) * 256 + 4 * q + c4] = make_int4(o[0], o[1], o[2], o[3]);
+            out[(c / CG_COLS) * 256 + 4 * q + c4] = make_int4(v0, v1, v2, v3);  // column (c & ~3) + j at bin 4q + c4
         }
         return;
     }
+
+    // several tiles per workgroup: the packed words are unpacked into i32 sums every flush_rows rows
+    int32_t accg[SLOTS], acch[SLOTS];
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
+    uint32_t pending = 0;  // rows added to the packed LDS words since they were last unpacked
+    uint32_t next = blockIdx.x;  // histogram-only launches take tiles blockIdx.x, + groups, ...
+    for (;;) {
+        __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
+        if (tid == 0) sh.tile = v.partition ? atomicAdd(&plan->ticket, 1u) : next;
+        __syncthreads();
+        const uint32_t t = sh.tile;
+        next += v.groups;
+        if (t >= v.ntiles) break;
+        const uint32_t nb = step_tile(v, a, t, sh);
+        if (!v.hist) continue;
+        uint32_t c0 = 0;
+        while (c0 < nb) {
+            if (pending >= a.flush_rows) {
+                unpack_slots<SLOTS>(lds, tid, accg, acch, true);
+                pending = 0;
+            }
+            uint32_t room = a.flush_rows - pending;
+            uint32_t c1 = nb - c0 < room ? nb : c0 + room;
+            hist_list<W, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+            pending += c1 - c0;
+            c0 = c1;
+        }
+    }
+    if (!v.hist) return;
     unpack_slots<SLOTS>(lds, tid, accg, acch, false);
+    const uint32_t col_bins = a.col_bins[tid % W];  // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W
     int2 *out = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j)
@@ -2054,6 +2097,15 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
         const uint32_t bin = bin0 + tid % nbins, q = tid / nbins;
         const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin;
         const size_t stride4 = pstride / 4;
+        // the parent's sums of the bin's four columns, read with the partials
+        int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q == 0 && bin < cg.bins[c]) {
+                const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                pg[c] = parent[o];
+                ph[c] = parent[o + 1];
+            }
         int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
         for (uint32_t w = q; w < groups; w += 8u * pways) {
             int4 v[8];
@@ -2074,22 +2126,21 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
                 }
             }
         }
-        // stripes q > 0 hand their sums to stripe 0 through LDS
+        // stripes q > 0 hand their sums to stripe 0 through LDS ([value][thread]: conflict-free)
         if (pways > 1u) {
             int64_t *r8 = reinterpret_cast<int64_t *>(red8);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                r8[tid * 8 + 2 * c] = sg[c];
-                r8[tid * 8 + 2 * c + 1] = sh[c];
+                r8[(2 * c) * 1024 + tid] = sg[c];
+                r8[(2 * c + 1) * 1024 + tid] = sh[c];
             }
             __syncthreads();
             if (q == 0)
                 for (uint32_t k = 1; k < pways; ++k) {
-                    const int64_t *o8 = r8 + (tid + k * nbins) * 8;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        sg[c] += o8[2 * c];
-                        sh[c] += o8[2 * c + 1];
+                        sg[c] += r8[(2 * c) * 1024 + tid + k * nbins];
+                        sh[c] += r8[(2 * c + 1) * 1024 + tid + k * nbins];
                     }
                 }
         }
@@ -2100,8 +2151,8 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
                     const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
                     built[o] = sg[c];
                     built[o + 1] = sh[c];
-                    parent[o] -= sg[c];
-                    parent[o + 1] -= sh[c];
+                    parent[o] = pg[c] - sg[c];
+                    parent[o + 1] = ph[c] - sh[c];
                 }
             }
         }
