@@ -337,6 +337,11 @@ int srocm_boost_init(void *ctx, const srocm_train_params *params, double *init_s
 int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iteration, uint32_t count,
                 srocm_grown_tree *trees, uint32_t *trained);
 
+/* Reads back the first `len` row ids of the backend's partition (the order srocm_reset_partition,
+ * srocm_partition and srocm_grow left them in; a grown tree's leaves hold their rows' ranges). No counterpart in
+ * the trait: for callers that check or reuse the row order on the host. `len` is at most the training rows. */
+int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
+
 /* Per-kernel timing with HIP events on the backend's stream, and algorithmic byte counts; no counterpart in the
  * reference (a measurement hook). srocm_profile: enable (1) or disable (0); either resets the counters.
  * srocm_profile_read writes min(len, SROCM_PROFILE_VALUES) values:

@@ -146,6 +146,7 @@ _SIGNATURES = {
     "srocm_set_gradients": (C.c_int, [_P, C.POINTER(C.c_float), C.POINTER(C.c_float), C.c_uint64,
                                       C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "srocm_gradients": (C.c_int, [_P, C.POINTER(C.c_float), C.POINTER(C.c_float), C.c_size_t]),
+    "srocm_partition_rows": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_size_t]),
     "srocm_quantize": (C.c_int, [_P, C.POINTER(QuantSpec)]),
     "srocm_reset_partition": (C.c_int, [_P, C.POINTER(Bag), C.POINTER(C.c_uint32)]),
     "srocm_set_histogram_features": (C.c_int, [_P, C.POINTER(C.c_uint8), C.c_uint32]),

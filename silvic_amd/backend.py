@@ -105,6 +105,13 @@ class RocmBackend:
         self._check(self._lib.srocm_gradients(self._h, _p(g, C.c_float), _p(h, C.c_float), n))
         return g, h
 
+    def partition_rows(self, count=None):
+        """The backend's partition (row ids in leaf-range order), its first `count` entries (default: all rows)."""
+        n = self._datasets[0].num_rows if count is None else int(count)
+        out = np.zeros(n, np.uint32)
+        self._check(self._lib.srocm_partition_rows(self._h, _p(out, C.c_uint32), n))
+        return out
+
     def quantize(self, spec):
         self._check(self._lib.srocm_quantize(self._h, C.byref(spec)))
 

@@ -1569,6 +1569,16 @@ int srocm_gradients(void *ctx, float *grad, float *hess, size_t len) {
     });
 }
 
+int srocm_partition_rows(void *ctx, uint32_t *out, size_t len) {
+    return guard(ctx, [&](Context &c) {
+        c.require_loaded();
+        if (len > c.rows) fail(SROCM_ERR_DEVICE, "partition read of " + std::to_string(len) + " rows, the training set has " + std::to_string(c.rows));
+        if (len && !out) fail(SROCM_ERR_DEVICE, "null output");
+        if (len) hip_check(hipMemcpyAsync(out, c.part.p, len * 4, hipMemcpyDeviceToHost, c.stream), "read partition");
+        c.sync();
+    });
+}
+
 int srocm_quantize(void *ctx, const srocm_quant_spec *spec) {
     return guard(ctx, [&](Context &c) {
         if (!spec) fail(SROCM_ERR_DEVICE, "null quantization spec");

@@ -257,14 +257,17 @@ def compare_trees(d, o, name, exact_values=True):
             np.testing.assert_allclose(d[k], o[k], rtol=1e-6, atol=0, err_msg=f"{name} {k}")
 
 
-@pytest.mark.parametrize("rows,cols,leaves", [(20_000, 16, 31), (400_000, 128, 255)])
-def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves):
-    say("grow", rows, cols, leaves)
+# (rows, features, leaves, gradient bins): the 700k-row root partitions in several tiles per workgroup; 300
+# features span three slabs; 32 gradient bins keep every workgroup's sums in {g, h} pairs.
+@pytest.mark.parametrize("rows,cols,leaves,qbins", [(20_000, 16, 31, 4), (400_000, 128, 255, 4), (700_000, 8, 63, 4),
+                                                    (60_000, 300, 63, 4), (150_000, 40, 63, 32)])
+def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves, qbins):
+    say("grow", rows, cols, leaves, qbins)
     data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=21)
     g, h = binary_gradients(data, 7)
-    p = oracle.default_params(num_leaves=leaves)
+    p = oracle.default_params(num_leaves=leaves, num_grad_quant_bins=qbins)
     o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
-    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed)
+    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed, num_bins=qbins)
     n = rocm.reset_partition()
     mask = oracle.feature_mask(data.features, 1.0, 2, 0)
     d = rocm.grow(p.cfg, leaves, -1, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
@@ -272,6 +275,8 @@ def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves):
     o["leaf_value"] = o_tree["leaf_value"]
     compare_trees(d, o, "grow")
     assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+    # the stable partition, row for row (cpu.rs:556-599)
+    assert np.array_equal(rocm.partition_rows(n), o_part[:n])
 
 
 def test_learner_cases_on_the_device(rocm):
