@@ -18,10 +18,45 @@ sys.path.insert(0, ROOT)
 
 METRIC = "histogram bins/s + boosting iters/s at 10M×128 int8-quantized; % HBM peak"
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "split_step_traffic_10Mx128.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a
+    copy kernel of known size), for the default workload; None when the summary is absent."""
+    import re
+
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch " + re.escape(kernel) + r": (\d+)$", text, re.M)
+    return float(m.group(1)) if m else None
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def copy_calibration(nbytes):
+    """Four device-to-device copies of `nbytes` through the HIP runtime (its copy kernel reads and writes each byte
+    once): the reference point for FETCH_SIZE / WRITE_SIZE counters."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    src, dst = C.c_void_p(), C.c_void_p()
+    for buf in (src, dst):
+        if hip.hipMalloc(C.byref(buf), C.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    if hip.hipMemset(src, 1, C.c_size_t(nbytes)) != 0:
+        raise RuntimeError("hipMemset failed")
+    for _ in range(4):
+        if hip.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copy calibration: 4 x {nbytes} B device-to-device")
 
 
 def main():
@@ -34,6 +69,9 @@ def main():
     ap.add_argument("--leaves", type=int, default=255)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of oracle work for the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="first run 4 device-to-device copies of MB MiB (the runtime's copy kernel): known bytes for "
+                         "scaling hardware memory counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported (the path is single-GPU; "
@@ -46,6 +84,9 @@ def main():
 
     import silvic_amd
     from silvic_amd import _abi
+
+    if args.calibrate_copy:
+        copy_calibration(args.calibrate_copy << 20)
 
     t0 = time.perf_counter()
     data = silvic_amd.synthetic(2, rows=args.rows, cols=args.cols, seed=7)
@@ -76,6 +117,8 @@ def main():
     # every histogram is built by k_hist (roots) or k_step_rows (split steps, which also partition)
     bins_per_s = hist_bins / ((hist_ms + step_ms) / 1e3) if hist_ms + step_ms else 0.0
     step_gbps = step_bytes / (step_ms / 1e3) / 1e9 if step_ms else 0.0
+    default_workload = (args.rows, args.cols, args.leaves) == (10_000_000, 128, 255)
+    traffic = measured_traffic("k_step_rows<128>") if default_workload else None
     root_gbps = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms else 0.0
     log(f"{steps} iterations in {elapsed:.3f}s; k_step_rows: {step_launches:.0f} launches, {step_ms:.1f} ms, "
         f"{step_gbps:.0f} GB/s algorithmic; k_hist (roots): {hist_launches:.0f} launches, {hist_ms:.1f} ms, "
@@ -140,7 +183,8 @@ def main():
         "step_kernel_ms_per_iter": step_ms / steps,
         "root_hist_ms_per_iter": hist_ms / steps,
         "roofline": {"bound": "hbm", "achieved": step_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": step_gbps / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": step_gbps / HBM_PEAK_GBPS, "traffic": traffic,
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,
                      "kernel": "k_step_rows<128> (split step: stable partition + built-child histogram)",
                      "launches": step_launches, "avg_launch_us": step_ms / step_launches * 1e3 if step_launches else None,
                      "bytes_per_launch": step_bytes / step_launches if step_launches else None,
