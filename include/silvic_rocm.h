@@ -163,8 +163,10 @@ typedef struct srocm_sums {
     int64_t count;
 } srocm_sums;
 
-/* SplitInfo (crates/silvic-core/src/split.rs:120-132) for a numerical rule (SplitRule::Numerical):
- * bins 0..=threshold go left, the NaN bin goes left iff default_left. */
+/* SplitInfo (crates/silvic-core/src/split.rs:120-132). SplitRule::Numerical (categorical == 0): bins
+ * 0..=threshold go left, the NaN bin goes left iff default_left. SplitRule::Categorical (categorical == 1): the
+ * num_cat_bins bins cat_bins[0..num_cat_bins) go left, in the rule's order (split.rs:114-116); threshold and
+ * default_left are 0. */
 typedef struct srocm_split_info {
     int32_t found;        /* 0: the leaf has no split (Option::None) */
     int32_t feature;
@@ -175,6 +177,9 @@ typedef struct srocm_split_info {
     srocm_sums right;
     double left_output;
     double right_output;
+    uint32_t categorical;
+    uint32_t num_cat_bins;
+    uint32_t cat_bins[256];
 } srocm_split_info;
 
 /* One tree grown on the device (Learner::grow, crates/silvic-core/src/learner.rs:121-169): LightGBM tree
@@ -201,6 +206,9 @@ typedef struct srocm_grown_tree {
     int32_t *leaf_parent;
     int32_t *leaf_depth;
     srocm_leaf_range *leaf_range;
+    /* per internal node, 8 words: the bins that go left (BinSplit::left_bins); a categorical node has
+     * threshold_bin 0 and default_left 0. May be null. */
+    uint32_t *left_bins;
 } srocm_grown_tree;
 
 /* TreeSpec (crates/silvic-core/src/learner.rs:42-54) plus the learner's own parameters. */

@@ -91,6 +91,7 @@ def lib():
             "oracle_model_scores": (None, [C.c_void_p, P(C.c_float), C.c_uint64]),
             "oracle_model_times": (None, [C.c_void_p, P(C.c_double)]),
             "oracle_model_hist_bins": (C.c_double, [C.c_void_p]),
+            "oracle_model_tree_left_bins": (None, [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32)]),
             "oracle_grow_tree": (C.c_void_p, [P(_abi.Dataset), P(C.c_float), P(C.c_float), P(Params), C.c_int]),
             "oracle_model_leaf_ranges": (None, [C.c_void_p, P(_abi.LeafRange)]),
             "oracle_model_partition": (None, [C.c_void_p, P(C.c_uint32)]),
@@ -267,6 +268,9 @@ class Model:
                      C.c_int64, C.c_double, C.c_double, C.c_int64, C.c_int32]
             L.oracle_model_tree(handle, t, *[ptr(v, ty) for v, ty in zip(a.values(), types)])
             a["num_leaves"] = nl
+            lb = np.zeros(8 * max(ni, 1), np.uint32)
+            L.oracle_model_tree_left_bins(handle, t, ptr(lb, C.c_uint32))
+            a["left_bins"] = lb[: 8 * ni].reshape(-1, 8)
             self.trees.append(a)
         self.scores = np.zeros(num_rows, np.float32)
         L.oracle_model_scores(handle, ptr(self.scores, C.c_float), num_rows)

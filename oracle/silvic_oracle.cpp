@@ -1471,6 +1471,7 @@ struct Learner {
 
 struct Model {
     std::vector<Tree> trees;
+    std::vector<std::vector<srocm_bin_split>> splits;  // per tree, per internal node: the bins that go left
     std::vector<srocm_leaf_range> leaf_ranges;  // of the last tree grown by grow_tree
     std::vector<uint32_t> partition;
     double init_score = 0.0;
@@ -1517,6 +1518,7 @@ Model *train(const srocm_dataset *d, const oracle_params *p) {
                 Tree t;
                 t.leaf_value[0] = init;
                 model->trees.push_back(t);
+                model->splits.emplace_back();
             }
             break;
         }
@@ -1538,6 +1540,7 @@ Model *train(const srocm_dataset *d, const oracle_params *p) {
         }
         backend.add_tree(nodes, leaf_values);
         model->trees.push_back(std::move(grown.tree));
+        model->splits.push_back(grown.splits);
     }
     backend.times[T_TOTAL] = std::chrono::duration<double>(Clock::now() - start).count();
     std::copy(backend.times, backend.times + T_COUNT, model->times);
@@ -1575,6 +1578,7 @@ Model *grow_tree(const srocm_dataset *d, const float *grad, const float *hess, c
     model->leaf_ranges = g.leaves;
     model->partition = backend.partition;
     model->trees.push_back(std::move(g.tree));
+    model->splits.push_back(g.splits);
     model->scores.assign(d->num_rows, 0.0f);
     return model.release();
 }
@@ -1781,5 +1785,11 @@ void oracle_model_partition(const void *model, uint32_t *out) {
 }
 
 double oracle_model_hist_bins(const void *model) { return static_cast<const Model *>(model)->hist_bins; }
+
+void oracle_model_tree_left_bins(const void *model, uint32_t tree, uint32_t *out) {
+    const Model *m = static_cast<const Model *>(model);
+    const auto &sp = m->splits.at(tree);
+    for (size_t k = 0; k < sp.size(); ++k) std::copy(sp[k].left_bins, sp[k].left_bins + 8, out + 8 * k);
+}
 
 }  // extern "C"

@@ -151,6 +151,8 @@ void oracle_model_leaf_ranges(const void *model, srocm_leaf_range *out);
 void oracle_model_partition(const void *model, uint32_t *out);
 /* Sum over histogram builds of rows x used feature columns (the "bins" work unit). */
 double oracle_model_hist_bins(const void *model);
+/* per internal node of tree `tree`, 8 words: the bins that go left (the BinSplit the learner handed the backend) */
+void oracle_model_tree_left_bins(const void *model, uint32_t tree, uint32_t *out);
 
 #ifdef __cplusplus
 }

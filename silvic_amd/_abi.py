@@ -100,7 +100,8 @@ class Sums(C.Structure):
 class SplitInfo(C.Structure):
     _fields_ = [("found", C.c_int32), ("feature", C.c_int32), ("gain", C.c_double), ("threshold", C.c_uint32),
                 ("default_left", C.c_uint32), ("left", Sums), ("right", Sums), ("left_output", C.c_double),
-                ("right_output", C.c_double)]
+                ("right_output", C.c_double), ("categorical", C.c_uint32), ("num_cat_bins", C.c_uint32),
+                ("cat_bins", C.c_uint32 * 256)]
 
 
 class GrownTree(C.Structure):
@@ -112,7 +113,7 @@ class GrownTree(C.Structure):
                 ("internal_count", C.POINTER(C.c_int64)), ("leaf_value", C.POINTER(C.c_double)),
                 ("leaf_weight", C.POINTER(C.c_double)), ("leaf_count", C.POINTER(C.c_int64)),
                 ("leaf_parent", C.POINTER(C.c_int32)), ("leaf_depth", C.POINTER(C.c_int32)),
-                ("leaf_range", C.POINTER(LeafRange))]
+                ("leaf_range", C.POINTER(LeafRange)), ("left_bins", C.POINTER(C.c_uint32))]
 
 
 class GrowSpec(C.Structure):

@@ -199,7 +199,7 @@ def new_tree(capacity):
         "internal_count": np.zeros(ni, np.int64), "leaf_value": np.zeros(capacity, np.float64),
         "leaf_weight": np.zeros(capacity, np.float64), "leaf_count": np.zeros(capacity, np.int64),
         "leaf_parent": np.zeros(capacity, np.int32), "leaf_depth": np.zeros(capacity, np.int32),
-        "leaf_range": np.zeros(2 * capacity, np.uint32),
+        "leaf_range": np.zeros(2 * capacity, np.uint32), "left_bins": np.zeros(8 * ni, np.uint32),
     }
     types = {np.int32: C.c_int32, np.uint32: C.c_uint32, np.uint8: C.c_uint8, np.float32: C.c_float,
              np.float64: C.c_double, np.int64: C.c_int64}
@@ -215,6 +215,8 @@ def tree_dict(t, keep):
     for k, v in keep.items():
         if k == "leaf_range":
             out[k] = v[: 2 * n].reshape(-1, 2).copy()
+        elif k == "left_bins":
+            out[k] = v[: 8 * ni].reshape(-1, 8).copy()
         elif k.startswith("leaf_"):
             out[k] = v[:n].copy()
         else:

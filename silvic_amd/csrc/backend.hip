@@ -185,6 +185,7 @@ struct HostTree {
     std::vector<double> leaf_value{0.0}, leaf_weight{0.0};
     std::vector<int64_t> leaf_count{0};
     std::vector<int32_t> leaf_parent{-1}, leaf_depth{0};
+    std::vector<uint32_t> left_bins;  // [node][8]: the bins that go left
 
     // tree.rs:143-177
     uint32_t split(uint32_t leaf, int32_t feature, uint32_t threshold, bool dl, double lv, double rv, int64_t lc,
@@ -878,13 +879,8 @@ struct Context {
     // ------------------------------------------------------------------------------------------------
 
     static SplitCfgDev cfg_dev(const srocm_split_config &c) {
-        return SplitCfgDev{c.min_data_in_leaf, c.min_sum_hessian_in_leaf, c.lambda_l1, c.lambda_l2, c.min_gain_to_split};
-    }
-
-    void check_numerical(const uint8_t *evaluate) const {
-        for (uint32_t f = 0; f < nf; ++f)
-            if (evaluate[f] && feats[f].num_bins && feats[f].kind == SROCM_BINS_CATEGORICAL)
-                fail(SROCM_ERR_UNSUPPORTED, "categorical split search runs on the cpu backend only");
+        return SplitCfgDev{c.min_data_in_leaf, c.min_sum_hessian_in_leaf, c.lambda_l1, c.lambda_l2, c.min_gain_to_split,
+                           c.max_cat_to_onehot, c.max_cat_threshold, c.cat_l2, c.cat_smooth, c.min_data_per_group};
     }
 
     // split.rs:919-961 on a host histogram over an explicit feature table (no loaded dataset needed)
@@ -894,8 +890,6 @@ struct Context {
         std::vector<FeatDev> fd(num_features);
         for (uint32_t f = 0; f < num_features; ++f) {
             const srocm_feature &m = features[f];
-            if (evaluate[f] && m.num_bins && m.kind == SROCM_BINS_CATEGORICAL)
-                fail(SROCM_ERR_UNSUPPORTED, "categorical split search runs on the cpu backend only");
             if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
             if (m.num_bins && static_cast<uint64_t>(m.hist_offset) + m.num_bins > len / 2)
                 fail(SROCM_ERR_DEVICE, "feature " + std::to_string(f) + " lies outside the histogram");
@@ -908,7 +902,8 @@ struct Context {
         DevBuf<ScanJob> dj;
         DevBuf<FeatCand> dc;
         DevBuf<SplitOut> dso;
-        DevBuf<uint8_t> dsp, dev;
+        DevBuf<uint8_t> dsp, dev, dorder;
+        dorder.alloc(static_cast<size_t>(std::max<uint32_t>(num_features, 1)) * 256);
         dh.alloc(std::max<size_t>(len, 1));
         dfd.alloc(std::max<uint32_t>(num_features, 1));
         dj.alloc(1);
@@ -925,7 +920,7 @@ struct Context {
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             dim3 grid(div_up(num_features, 4), 1);
-            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, nullptr);
+            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, nullptr, dorder.p);
             launch_check("k_split_scan");
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
@@ -935,6 +930,11 @@ struct Context {
         if (num_features) hip_check(hipMemcpyAsync(splittable, dsp.p, num_features, hipMemcpyDeviceToHost, stream), "read splittable");
         sync();
         to_info(o, out);
+        if (o.found && o.rule == RULE_SORTED) {  // the rule's bins in order (split.rs:114-116)
+            uint8_t order[256];
+            hip_check(hipMemcpy(order, dorder.p + static_cast<size_t>(o.feature) * 256, 256, hipMemcpyDeviceToHost), "read categories");
+            for (uint32_t i = 0; i < o.cat_count && i < 256; ++i) out->cat_bins[i] = order[i];
+        }
     }
 
     static void to_info(const SplitOut &o, srocm_split_info *out) {
@@ -949,6 +949,13 @@ struct Context {
         out->right = srocm_sums{o.right_grad, o.right_hess, o.right_count};
         out->left_output = o.left_output;
         out->right_output = o.right_output;
+        if (o.rule != RULE_NUMERICAL) {
+            out->categorical = 1;
+            out->num_cat_bins = o.cat_count;
+            uint32_t k = 0;  // one-hot: the single bin of the mask
+            for (uint32_t b = 0; b < 256 && k < o.cat_count; ++b)
+                if ((o.cat_mask[b >> 5] >> (b & 31)) & 1u) out->cat_bins[k++] = b;
+        }
     }
 
     // ------------------------------------------------------------------------------------------------
@@ -975,6 +982,7 @@ struct Context {
         DevBuf<float> split_gain;
         DevBuf<double> internal_value, internal_weight, leaf_value, leaf_weight;
         DevBuf<int64_t> internal_count, leaf_count;
+        DevBuf<uint32_t> left_bins;
     } dtree;
     uint32_t grow_capacity = 0;
 
@@ -1004,6 +1012,7 @@ struct Context {
         dtree.leaf_weight.alloc(L);
         dtree.internal_count.alloc(L);
         dtree.leaf_count.alloc(L);
+        dtree.left_bins.alloc(static_cast<size_t>(L) * 8);
         step_partial.alloc(2 * step_partial_pairs);
         tile_status.alloc(div_up(rows, STEP_TILE) + 1);
         fin_counts.alloc(ncg + 1);
@@ -1034,7 +1043,7 @@ struct Context {
         g.tree = TreeDev{dtree.split_feature.p, dtree.threshold_bin.p, dtree.default_left.p, dtree.left_child.p,
                          dtree.right_child.p, dtree.split_gain.p, dtree.internal_value.p, dtree.internal_weight.p,
                          dtree.internal_count.p, dtree.leaf_value.p, dtree.leaf_weight.p, dtree.leaf_count.p,
-                         dtree.leaf_parent.p, dtree.leaf_depth.p};
+                         dtree.leaf_parent.p, dtree.leaf_depth.p, dtree.left_bins.p};
         g.pool = pool.p;
         g.slot_stride = 2 * total_bins;
         g.nf = nf;
@@ -1069,6 +1078,7 @@ struct Context {
         cp(out->leaf_count, t.leaf_count, t.num_leaves);
         cp(out->leaf_parent, t.leaf_parent, t.num_leaves);
         cp(out->leaf_depth, t.leaf_depth, t.num_leaves);
+        cp(out->left_bins, t.left_bins, static_cast<size_t>(ni) * 8);
         if (out->leaf_range)
             for (uint32_t i = 0; i < t.num_leaves && i < leaves.size(); ++i) out->leaf_range[i] = leaves[i].range;
     }
@@ -1150,7 +1160,6 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     if (spec.num_leaves < 1) fail(SROCM_ERR_CONFIG, "num_leaves must be positive");
     const uint32_t L = spec.num_leaves;
     std::vector<uint8_t> mask(spec.feature_mask, spec.feature_mask + nf);
-    check_numerical(mask.data());
     ensure_grow(L);
     int32_t sums_feature = -1;
     for (uint32_t f = 0; f < nf; ++f)
@@ -1178,7 +1187,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
         k_root_prep<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_prep");
-        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr);
+        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, nullptr);
         launch_check("k_split_scan");
         k_root_select<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_select");
@@ -1217,7 +1226,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_check("k_consolidate");
     }
     // one readback: control block, leaves, tree arrays
-    size_t need = sizeof(GrowCtl) + static_cast<size_t>(L) * (sizeof(DLeaf) + 4 * 5 + 4 + 1 + 4 + 8 * 6);
+    size_t need = sizeof(GrowCtl) + static_cast<size_t>(L) * (sizeof(DLeaf) + 4 * 5 + 4 + 1 + 4 + 8 * 6 + 32);
     h_result.alloc(need + 64);
     uint8_t *hp = h_result.p;
     auto rd = [&](void *dev, size_t bytes) {
@@ -1242,6 +1251,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     auto *ld = reinterpret_cast<const int32_t *>(rd(dtree.leaf_depth.p, L * 4));
     auto *tb = reinterpret_cast<const uint32_t *>(rd(dtree.threshold_bin.p, L * 4));
     auto *sgn = reinterpret_cast<const float *>(rd(dtree.split_gain.p, L * 4));
+    auto *lb = reinterpret_cast<const uint32_t *>(rd(dtree.left_bins.p, static_cast<size_t>(L) * 32));
     auto *dl = reinterpret_cast<const uint8_t *>(rd(dtree.default_left.p, L));
     sync();
     if (hc->error == 1) fail(SROCM_ERR_INTERNAL, "a split sent no rows to one side");
@@ -1267,12 +1277,12 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     tree.leaf_depth.assign(ld, ld + n);
     leaves.assign(n, GrowLeaf{});
     for (uint32_t i = 0; i < n; ++i) leaves[i].range = srocm_leaf_range{hl[i].begin, hl[i].count};
+    tree.left_bins.assign(lb, lb + static_cast<size_t>(ni) * 8);
     splits.assign(ni, srocm_bin_split{});
-    for (uint32_t k = 0; k < ni; ++k) {  // learner.rs:432-452
+    for (uint32_t k = 0; k < ni; ++k) {  // learner.rs:432-452, as the device planned each split
         const srocm_feature &m = feats[tree.split_feature[k]];
         srocm_bin_split &bs = splits[k];
-        for (uint32_t b = 0; b <= tree.threshold_bin[k]; ++b) bs.left_bins[b / 32] |= 1u << (b % 32);
-        if (tree.default_left[k] && m.nan_bin) bs.left_bins[(m.num_bins - 1) / 32] |= 1u << ((m.num_bins - 1) % 32);
+        std::copy(lb + 8 * static_cast<size_t>(k), lb + 8 * static_cast<size_t>(k) + 8, bs.left_bins);
         bs.group = m.group;
         bs.column = m.column;
     }

@@ -675,6 +675,9 @@ __global__ void k_add_const(float *__restrict__ scores, uint64_t rows, float v) 
 struct SplitCfgDev {
     int64_t min_data_in_leaf;
     double min_sum_hessian_in_leaf, lambda_l1, lambda_l2, min_gain_to_split;
+    uint64_t max_cat_to_onehot, max_cat_threshold;
+    double cat_l2, cat_smooth;
+    int64_t min_data_per_group;
 };
 
 struct Ctx {
@@ -728,9 +731,14 @@ struct FeatCand {
     double left_units_g, left_units_h;
     uint32_t col;         // the feature's column-major index (its bins for the partition)
     uint32_t nan_idx;     // its NaN bin, or NO_BIN
+    uint32_t rule;        // RULE_NUMERICAL, RULE_ONEHOT or RULE_SORTED
+    uint32_t cat_forward; // sorted categorical: the run went from the low end of the sorted order
+    uint32_t cat_count;   // categorical: bins going left
+    uint32_t cat_mask[8]; // categorical: the bins going left
 };
 
 constexpr uint32_t NO_BIN = 0xffffffffu;
+constexpr uint32_t RULE_NUMERICAL = 0, RULE_ONEHOT = 1, RULE_SORTED = 2;  // split.rs:112-117, 694-844
 
 struct Grown {
     uint32_t bin;
@@ -804,6 +812,77 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t lane) {
     uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
+
+// (gain, feature) order of split.rs:866-880 for reductions: a beats b on higher gain, then lower feature; -1 is
+// "no candidate".
+__device__ __forceinline__ bool cand_better(double ga, int fa, double gb, int fb) {
+    return fa >= 0 && (fb < 0 || ga > gb || (ga == gb && fa < fb));
+}
+
+// Wave-wide all-reductions through the DPP scan steps; every lane ends with the result.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void best_step(double &g, int &i, uint32_t lane) {
+    double og = double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(g)));
+    int oi = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(i)));
+    if (dpp_has_source<CTRL, ROW_MASK>(lane) && cand_better(og, oi, g, i)) {
+        g = og;
+        i = oi;
+    }
+}
+// The best (gain, index) pair: higher gain, then the lower index; index < 0 is "none".
+__device__ __forceinline__ void wave_best(double &g, int &i) {
+    const uint32_t lane = threadIdx.x & 63u;
+    best_step<DPP_ROW_SHR1, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR2, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR4, 0xf>(g, i, lane);
+    best_step<DPP_ROW_SHR8, 0xf>(g, i, lane);
+    best_step<DPP_ROW_BCAST15, 0xa>(g, i, lane);
+    best_step<DPP_ROW_BCAST31, 0xc>(g, i, lane);
+    i = __builtin_amdgcn_readlane(i, 63);
+    g = double_of(readlane_u64(bits_of(g), 63));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void min_step(int &v, uint32_t lane) {
+    int o = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(v)));
+    if (dpp_has_source<CTRL, ROW_MASK>(lane) && o < v) v = o;
+}
+__device__ __forceinline__ int wave_min(int v) {
+    const uint32_t lane = threadIdx.x & 63u;
+    min_step<DPP_ROW_SHR1, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR2, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR4, 0xf>(v, lane);
+    min_step<DPP_ROW_SHR8, 0xf>(v, lane);
+    min_step<DPP_ROW_BCAST15, 0xa>(v, lane);
+    min_step<DPP_ROW_BCAST31, 0xc>(v, lane);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ double readlane_f64(double v, uint32_t lane) { return double_of(readlane_u64(bits_of(v), lane)); }
+
+// A feature candidate as held by lane `owner`, broadcast to the wave.
+__device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
+    FeatCand r;
+    r.found = __builtin_amdgcn_readlane(c.found, owner);
+    r.splittable = __builtin_amdgcn_readlane(c.splittable, owner);
+    r.gain = readlane_f64(c.gain, owner);
+    r.best_gain = readlane_f64(c.best_gain, owner);
+    r.threshold = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.threshold), owner));
+    r.default_left = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.default_left), owner));
+    r.left_grad = readlane_f64(c.left_grad, owner);
+    r.left_hess = readlane_f64(c.left_hess, owner);
+    r.left_count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(c.left_count), owner));
+    r.left_units_g = readlane_f64(c.left_units_g, owner);
+    r.left_units_h = readlane_f64(c.left_units_h, owner);
+    r.col = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.col), owner));
+    r.nan_idx = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.nan_idx), owner));
+    r.rule = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.rule), owner));
+    r.cat_forward = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.cat_forward), owner));
+    r.cat_count = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.cat_count), owner));
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+        r.cat_mask[w] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.cat_mask[w]), owner));
+    return r;
+}
+
 
 // One scan direction over `n` bins of a feature's histogram slice `h` (i64 {g,h} pairs): element k is bin
 // t0 + step * k. Lane l holds elements 4l..4l+3. Returns whether a candidate beat min_gain_shift.
@@ -945,7 +1024,7 @@ __device__ __forceinline__ int64_t job_count(const ScanJob &job, const Plan *pla
 // Direction 0 is the reverse scan (split.rs:557-567: missing values go left); direction 1, only for a feature with
 // a NaN bin and more than two bins, the forward scan over the bins before the NaN bin (split.rs:571-580).
 __device__ __forceinline__ bool scan_searched(const Ctx &c, const FeatDev &m, bool evaluate) {
-    return c.valid && evaluate && m.num_bins >= 2 && m.kind == 1;
+    return c.valid && evaluate && m.num_bins >= 2 && (m.kind == 1 || m.kind == 2);
 }
 __device__ __forceinline__ bool scan_two_way(const FeatDev &m) { return m.nan_bin && m.num_bins > 2; }
 
@@ -1000,28 +1079,324 @@ __device__ FeatCand feature_candidate(const Ctx &c, const FeatDev &m, bool rf, c
     return r;
 }
 
-// split.rs:584-620 find_numerical for one feature of one leaf, by one wave; lane 0's result is the candidate.
-__device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool evaluate) {
-    Grown rg = {}, fg = {};
-    bool rf = false, ff = false;
-    if (scan_searched(c, m, evaluate)) {
-        rf = scan_direction(c, cfg, m, hist, 0, rg);
-        if (scan_two_way(m)) ff = scan_direction(c, cfg, m, hist, 1, fg);
-    } else {
-        return FeatCand{};
+// ---------------------------------------------------------------------------------------------------------
+// Categorical features (split.rs:694-844): one-hot for at most max_cat_to_onehot bins, otherwise the bins with
+// enough rows sorted by their smoothed gradient ratio and scanned from both ends. One wave per feature.
+// ---------------------------------------------------------------------------------------------------------
+
+// split.rs:243-258 check for a growing side (rows, hessian, hessian units) against the other side:
+// 0 skip the candidate (Continue), 1 stop the scan (Break), 2 evaluate it.
+__device__ __forceinline__ int side_check(const Ctx &c, const SplitCfgDev &cfg, int64_t cnt, double hess, double units_h,
+                                          int64_t other_cnt, double other_hess) {
+    if (cnt < cfg.min_data_in_leaf || cnt <= 0 || hess < cfg.min_sum_hessian_in_leaf || units_h <= 0.0) return 0;
+    if (other_cnt < cfg.min_data_in_leaf || other_cnt <= 0) return 1;
+    if (other_hess < cfg.min_sum_hessian_in_leaf || c.units_hess - units_h <= 0.0) return 1;
+    return 2;
+}
+
+__device__ __forceinline__ int64_t bin_rows(const Ctx &c, double units_h) {  // split.rs:236-238 bin_count
+    return sat_i64(units_h * c.scale_hess * c.cnt_factor + 0.5);
+}
+
+__device__ __forceinline__ void mask_set(uint32_t (&mask)[8], uint32_t bin) {
+#pragma unroll
+    for (uint32_t w = 0; w < 8; ++w)
+        if ((bin >> 5) == w) mask[w] |= 1u << (bin & 31u);
+}
+
+// split.rs:695-736 find_onehot: every bin 1..num_bins on its own against the rest; the first strict maximum above
+// min_gain_shift (NaN never counts). Lane l takes bins 1 + l + 64 j.
+__device__ FeatCand onehot_scan(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist) {
+    const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
+    const uint32_t lane = threadIdx.x & 63u;
+    const int nb = static_cast<int>(m.num_bins);
+    double bg = 0.0, bu_g = 0.0, bu_h = 0.0;
+    int bt = -1;
+    int64_t bcnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 1 + static_cast<int>(lane) + 64 * j;
+        if (t >= nb) continue;
+        const double ug = static_cast<double>(h[2 * t]), uh = static_cast<double>(h[2 * t + 1]);
+        const int64_t cnt = bin_rows(c, uh);
+        const double raw_hess = uh * c.scale_hess;
+        const int64_t other_cnt = c.num_data - cnt;
+        const double other_hess = c.sum_hess - raw_hess - K_EPSILON;
+        if (side_check(c, cfg, cnt, raw_hess, uh, other_cnt, other_hess) != 2) continue;
+        const double grad = ug * c.scale_grad;
+        const double gain = leaf_gain(c.sum_grad - grad, other_hess, cfg.lambda_l1, cfg.lambda_l2) +
+                            leaf_gain(grad, raw_hess + K_EPSILON, cfg.lambda_l1, cfg.lambda_l2);
+        if (gain != gain || gain <= c.min_gain_shift) continue;
+        if (bt < 0 || gain > bg) {
+            bg = gain;
+            bt = t;
+            bu_g = ug;
+            bu_h = uh;
+            bcnt = cnt;
+        }
     }
+    const bool any = __ballot(bt >= 0) != 0;
+    double wg = bg;
+    int wt = bt;
+    wave_best(wg, wt);
+    FeatCand r = {};
+    r.splittable = any ? 1 : 0;
+    if (wt >= 0) {
+        const uint32_t owner = static_cast<uint32_t>(wt - 1) & 63u;
+        const double ug = readlane_f64(bu_g, owner), uh = readlane_f64(bu_h, owner);
+        const int64_t cnt = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(bcnt), owner));
+        r.found = 1;
+        r.best_gain = wg;
+        r.gain = wg - c.min_gain_shift;
+        r.threshold = static_cast<uint32_t>(wt);
+        r.left_grad = ug * c.scale_grad;
+        r.left_hess = uh * c.scale_hess + K_EPSILON;
+        r.left_count = cnt;
+        r.left_units_g = ug;
+        r.left_units_h = uh;
+        r.col = m.col;
+        r.nan_idx = NO_BIN;
+        r.rule = RULE_ONEHOT;
+        r.cat_count = 1;
+        mask_set(r.cat_mask, static_cast<uint32_t>(wt));
+    }
+    return r;
+}
+
+// A wave's LDS for the sorted categorical scan.
+struct CatScratch {
+    unsigned long long key[256];  // total-order bits of each bin's ratio (bin-indexed)
+    uint32_t order[256];          // the sorted bins
+    uint8_t eligible[256];        // the bin has at least cat_smooth rows
+};
+
+// f64 total order (split.rs:754 total_cmp) as an unsigned integer order. A ratio that is NaN (0 / 0 with
+// cat_smooth = 0) orders by its sign bit; the reference computes it on x86-64, whose invalid-operation result is the
+// default NaN with the sign set, so the device's NaN is replaced by that one.
+__device__ __forceinline__ unsigned long long total_order_bits(double x) {
+    unsigned long long b = x != x ? 0xfff8000000000000ull : __builtin_bit_cast(unsigned long long, x);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+// One run of split.rs:795-843 SortedScan::run over the first `steps` positions of the sorted order, from the low
+// end (forward) or the high end. Positions i = lane + 64 j; the stateful min_data_per_group walk is uniform.
+// Returns whether a candidate passed; (gain, pos) the best, and its left sums.
+__device__ bool sorted_run(const Ctx &c, const SplitCfgDev &cfg, const int64_t *h, const CatScratch &sc, int used,
+                           int steps, bool forward, double l2, bool &splittable, double &best_gain, int &best_pos,
+                           double &lug, double &luh, int64_t &lcnt) {
+    const uint32_t lane = threadIdx.x & 63u;
+    double pg[4], ph[4];
+    int64_t pc[4], ci[4];
+    double lg = 0.0, lh = 0.0;
+    int64_t lc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = static_cast<int>(lane) * 4 + j;  // contiguous positions per lane: the prefix below is in order
+        double gu = 0.0, hu = 0.0;
+        int64_t cn = 0;
+        if (i < steps) {
+            const uint32_t t = sc.order[forward ? i : used - 1 - i];
+            gu = static_cast<double>(h[2 * t]);
+            hu = static_cast<double>(h[2 * t + 1]);
+            cn = bin_rows(c, hu);
+        }
+        ci[j] = cn;
+        lg += gu;
+        lh += hu;
+        lc += cn;
+        pg[j] = lg;
+        ph[j] = lh;
+        pc[j] = lc;
+    }
+    double eg = lg, eh = lh;
+    int64_t ec = lc;
+    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
+    eg -= lg;
+    eh -= lh;
+    ec -= lc;
+    // per position: 1 skip (Continue), 2 stop (Break, or the other side below min_data_per_group), 0 candidate
+    uint32_t flags = 0;  // 2 bits per position j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        pg[j] += eg;
+        ph[j] += eh;
+        pc[j] += ec;
+        const int i = static_cast<int>(lane) * 4 + j;
+        if (i >= steps) continue;
+        const double lhess = K_EPSILON + ph[j] * c.scale_hess;
+        const int64_t rcnt = c.num_data - pc[j];
+        const double rhess = c.sum_hess - lhess;
+        const int chk = side_check(c, cfg, pc[j], lhess, ph[j], rcnt, rhess);
+        uint32_t f = chk == 0 ? 1u : (chk == 1 || rcnt < cfg.min_data_per_group ? 2u : 0u);
+        flags |= f << (2 * j);
+    }
+    // the walk (split.rs:806-823): rows since the last evaluated candidate must reach min_data_per_group
+    uint32_t mine = 0;  // bit j: this lane's position 4 lane + j is evaluated
+    int64_t group = 0;
+    for (int i = 0; i < steps; ++i) {
+        const uint32_t src = static_cast<uint32_t>(i) >> 2, jj = static_cast<uint32_t>(i) & 3u;
+        const int64_t cij = jj == 0 ? ci[0] : (jj == 1 ? ci[1] : (jj == 2 ? ci[2] : ci[3]));
+        group += static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(cij), src));
+        const uint32_t f = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(flags), src)) >> (2 * jj)) & 3u;
+        if (f == 1u) continue;
+        if (f == 2u) break;
+        if (group < cfg.min_data_per_group) continue;
+        group = 0;
+        if (lane == src) mine |= 1u << jj;
+    }
+    double bg = 0.0;
+    int bp = -1;
+    double b_g = 0.0, b_h = 0.0;
+    int64_t b_c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (!((mine >> j) & 1u)) continue;
+        const double lgrad = pg[j] * c.scale_grad;
+        const double lhess = K_EPSILON + ph[j] * c.scale_hess;
+        const double rhess = c.sum_hess - lhess;
+        const double gain = leaf_gain(lgrad, lhess, cfg.lambda_l1, l2) + leaf_gain(c.sum_grad - lgrad, rhess, cfg.lambda_l1, l2);
+        if (gain != gain || gain <= c.min_gain_shift) continue;
+        if (bp < 0 || gain > bg) {
+            bg = gain;
+            bp = static_cast<int>(lane) * 4 + j;
+            b_g = pg[j];
+            b_h = ph[j];
+            b_c = pc[j];
+        }
+    }
+    splittable = splittable || (__ballot(bp >= 0) != 0);
+    double wg = bg;
+    int wp = bp;
+    wave_best(wg, wp);
+    if (wp < 0) return false;
+    const uint32_t owner = static_cast<uint32_t>(wp) >> 2;
+    best_gain = wg;
+    best_pos = wp;
+    lug = readlane_f64(b_g, owner);
+    luh = readlane_f64(b_h, owner);
+    lcnt = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(b_c), owner));
+    return true;
+}
+
+// split.rs:740-784: sorted categorical. `order_out` (when given) receives the left bins in the rule's order.
+__device__ FeatCand sorted_scan(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist,
+                                CatScratch &sc, uint8_t *order_out) {
+    const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
+    const uint32_t lane = threadIdx.x & 63u;
+    const int nb = static_cast<int>(m.num_bins < 256 ? m.num_bins : 256);
+    // split.rs:740-760: bins with at least cat_smooth (estimated) rows, by (g / (h + cat_smooth), bin)
+    bool ok[4];
+    unsigned long long key[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 1 + static_cast<int>(lane) + 64 * j;
+        ok[j] = false;
+        key[j] = 0;
+        if (t < nb) {
+            const double gu = static_cast<double>(h[2 * t]), hu = static_cast<double>(h[2 * t + 1]);
+            ok[j] = static_cast<double>(bin_rows(c, hu)) >= cfg.cat_smooth;
+            key[j] = total_order_bits((gu * c.scale_grad) / (hu * c.scale_hess + cfg.cat_smooth));
+        }
+        if (t < 256) {
+            sc.key[t] = key[j];
+            sc.eligible[t] = ok[j] ? 1 : 0;
+        }
+    }
+    if (lane == 0) sc.eligible[0] = 0;
+    int used = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) used += __popcll(__ballot(ok[j]));
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // rank = eligible bins before this one in (key, bin) order
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 1 + static_cast<int>(lane) + 64 * j;
+        int rank = 0;
+        if (ok[j])
+            for (int u = 1; u < nb; ++u) {
+                const unsigned long long ku = sc.key[u];
+                rank += (sc.eligible[u] && (ku < key[j] || (ku == key[j] && u < t))) ? 1 : 0;
+            }
+        __builtin_amdgcn_wave_barrier();
+        if (ok[j]) sc.order[rank] = static_cast<uint32_t>(t);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    FeatCand r = {};
+    const int max_num_cat = static_cast<int>(cfg.max_cat_threshold < static_cast<uint64_t>((used + 1) / 2)
+                                                 ? cfg.max_cat_threshold : static_cast<uint64_t>((used + 1) / 2));
+    const int steps = used < max_num_cat ? used : max_num_cat;
+    const double l2 = cfg.lambda_l2 + cfg.cat_l2;
+    bool splittable = false;
+    double fg = 0.0, bgn = 0.0, flg = 0.0, flh = 0.0, blg = 0.0, blh = 0.0;
+    int fp = -1, bpz = -1;
+    int64_t flc = 0, blc = 0;
+    const bool ff = steps > 0 && sorted_run(c, cfg, h, sc, used, steps, true, l2, splittable, fg, fp, flg, flh, flc);
+    const bool bf = steps > 0 && sorted_run(c, cfg, h, sc, used, steps, false, l2, splittable, bgn, bpz, blg, blh, blc);
+    r.splittable = splittable ? 1 : 0;
+    if (!ff && !bf) return r;
+    const bool fwd = ff && !(bf && bgn > fg);  // split.rs:775-781: the backward run replaces only a lower gain
+    const double gain = fwd ? fg : bgn;
+    const int pos = fwd ? fp : bpz;
+    const double ug = fwd ? flg : blg, uh = fwd ? flh : blh;
+    r.found = 1;
+    r.best_gain = gain;
+    r.gain = gain - c.min_gain_shift;
+    r.threshold = static_cast<uint32_t>(pos);
+    r.left_grad = ug * c.scale_grad;
+    r.left_hess = K_EPSILON + uh * c.scale_hess;
+    r.left_count = fwd ? flc : blc;
+    r.left_units_g = ug;
+    r.left_units_h = uh;
+    r.col = m.col;
+    r.nan_idx = NO_BIN;
+    r.rule = RULE_SORTED;
+    r.cat_forward = fwd ? 1u : 0u;
+    r.cat_count = static_cast<uint32_t>(pos + 1);
+    for (int k = 0; k <= pos; ++k) {
+        const uint32_t t = sc.order[fwd ? k : used - 1 - k];
+        mask_set(r.cat_mask, t);
+        if (order_out && lane == 0) order_out[k] = static_cast<uint8_t>(t);
+    }
+    return r;
+}
+
+// The candidate of a categorical feature (split.rs:847-862).
+__device__ __forceinline__ FeatCand categorical_candidate(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m,
+                                                          const int64_t *hist, CatScratch &sc, uint8_t *order_out) {
+    if (m.num_bins <= cfg.max_cat_to_onehot) return onehot_scan(c, cfg, m, hist);
+    return sorted_scan(c, cfg, m, hist, sc, order_out);
+}
+
+// split.rs:584-620 find_numerical (or a categorical search) for one feature of one leaf, by one wave.
+__device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool evaluate,
+                                 CatScratch &sc, uint8_t *order_out) {
+    if (!scan_searched(c, m, evaluate)) return FeatCand{};
+    if (m.kind == 2) return categorical_candidate(c, cfg, m, hist, sc, order_out);
+    Grown rg = {}, fg = {};
+    bool rf = scan_direction(c, cfg, m, hist, 0, rg);
+    bool ff = scan_two_way(m) ? scan_direction(c, cfg, m, hist, 1, fg) : false;
     return feature_candidate(c, m, rf, rg, ff, fg);
 }
 
 __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
-                                                    SplitCfgDev cfg, double sg, double sh, const Plan *plan) {
+                                                    SplitCfgDev cfg, double sg, double sh, const Plan *plan,
+                                                    uint8_t *cat_order /* [feature][256] or null */) {
+    __shared__ CatScratch cats[4];
     if (plan && (!plan->active || !plan->may_search)) return;
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (f >= num_features) return;
     Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job_count(job, plan, blockIdx.y));
-    FeatCand r = scan_feature(c, cfg, feats[f], job.hist, evaluate[f] != 0);
+    FeatCand r = scan_feature(c, cfg, feats[f], job.hist, evaluate[f] != 0, cats[threadIdx.x >> 6],
+                              cat_order ? cat_order + static_cast<size_t>(f) * 256 : nullptr);
     if ((threadIdx.x & 63) == 0) job.out[f] = r;
 }
 
@@ -1037,17 +1412,14 @@ struct SplitOut {
     int64_t right_count;
     double left_output, right_output;
     uint32_t col, nan_idx;  // the feature's column-major index and NaN bin (NO_BIN: none)
+    uint32_t rule;          // RULE_*: categorical rules send exactly the bins of cat_mask left
+    uint32_t cat_count;
+    uint32_t cat_mask[8];
 };
 
 // The best split over the per-feature candidates of `job` (highest gain, NaN as -inf, ties to the lower feature,
 // split.rs:866-880) as the leaf's SplitOut (split.rs:631-651 finish), and its splittable flags. Block-wide (up
 // to 1024 threads).
-// (gain, feature) order of split.rs:866-880 for reductions: a beats b on higher gain, then lower feature; -1 is
-// "no candidate".
-__device__ __forceinline__ bool cand_better(double ga, int fa, double gb, int fb) {
-    return fa >= 0 && (fb < 0 || ga > gb || (ga == gb && fa < fb));
-}
-
 // split.rs:631-651 finish: the leaf's SplitInfo from its best feature's candidate.
 __device__ __forceinline__ SplitOut split_out(const FeatCand &c, int f, const Ctx &x, const SplitCfgDev &cfg) {
     SplitOut o = {};
@@ -1062,10 +1434,18 @@ __device__ __forceinline__ SplitOut split_out(const FeatCand &c, int f, const Ct
     o.right_grad = x.units_grad - c.left_units_g;
     o.right_hess = x.units_hess - c.left_units_h;
     o.right_count = x.num_data - c.left_count;
-    o.left_output = leaf_output(c.left_grad, c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
-    o.right_output = leaf_output(x.sum_grad - c.left_grad, x.sum_hess - c.left_hess, cfg.lambda_l1, cfg.lambda_l2);
+    const double l2 = c.rule == RULE_SORTED ? cfg.lambda_l2 + cfg.cat_l2 : cfg.lambda_l2;  // split.rs:667-680
+    o.left_output = leaf_output(c.left_grad, c.left_hess, cfg.lambda_l1, l2);
+    o.right_output = leaf_output(x.sum_grad - c.left_grad, x.sum_hess - c.left_hess, cfg.lambda_l1, l2);
     o.col = c.col;
     o.nan_idx = c.nan_idx;
+    o.rule = c.rule;
+    o.cat_count = c.cat_count;
+    for (int w = 0; w < 8; ++w) o.cat_mask[w] = c.cat_mask[w];
+    if (c.rule != RULE_NUMERICAL) {
+        o.threshold = 0;
+        o.default_left = 0;
+    }
     return o;
 }
 
@@ -1125,6 +1505,17 @@ __global__ __launch_bounds__(256) void k_split_select(const ScanJob *__restrict_
 // -> split scan of both children -> k_apply, which updates the tree and the leaves and plans the next step.
 // ---------------------------------------------------------------------------------------------------------
 
+// learner.rs:432-452 bin_split: word w of the bins that go left; numerical: bins 0..=threshold and the NaN bin when
+// missing values go left; categorical: the rule's bins.
+__device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_t w) {
+    if (info.rule != RULE_NUMERICAL) return info.cat_mask[w];
+    const uint32_t upto = info.threshold + 1;
+    const uint32_t lo = 32 * w;
+    uint32_t word = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
+    if (info.default_left && info.nan_idx != NO_BIN && (info.nan_idx >> 5) == w) word |= 1u << (info.nan_idx & 31u);
+    return word;
+}
+
 struct DLeaf {
     uint32_t begin, count;   // rows in the partition
     double ug, uh;           // sums in histogram units
@@ -1159,6 +1550,7 @@ struct TreeDev {
     double *leaf_value, *leaf_weight;
     int64_t *leaf_count;
     int32_t *leaf_parent, *leaf_depth;
+    uint32_t *left_bins;  // [node][8]: the bins that go left (BinSplit::left_bins)
 };
 
 struct GrowCtl {
@@ -1228,16 +1620,8 @@ __device__ void plan_leaf(const GrowState &g, uint32_t next, const DLeaf &leaf, 
         p.ticket = 0;
         p.left = 0;
         p.col = info.col;
-        // learner.rs:432-452: bins 0..=threshold, and the NaN bin when missing values go left
-        const uint32_t upto = info.threshold + 1;
-        const bool nan_left = info.default_left && info.nan_idx != NO_BIN;
 #pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) {
-            uint32_t lo = 32 * w;
-            uint32_t word = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
-            if (nan_left && (info.nan_idx >> 5) == w) word |= 1u << (info.nan_idx & 31u);
-            p.left_bins[w] = word;
-        }
+        for (uint32_t w = 0; w < 8; ++w) p.left_bins[w] = left_bins_word(info, w);
         uint32_t used_all = 0;
         for (uint32_t w = 0; w < nw; ++w) used_all += used_w[w];
         p.used_columns = used_all;
@@ -1341,64 +1725,6 @@ __global__ __launch_bounds__(256) void k_root_select(GrowState g) {
         return;
     }
     plan_leaf(g, 0, leaf, 1);
-}
-
-// Wave-wide all-reductions through the DPP scan steps; every lane ends with the result.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void best_step(double &g, int &i, uint32_t lane) {
-    double og = double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(g)));
-    int oi = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(i)));
-    if (dpp_has_source<CTRL, ROW_MASK>(lane) && cand_better(og, oi, g, i)) {
-        g = og;
-        i = oi;
-    }
-}
-// The best (gain, index) pair: higher gain, then the lower index; index < 0 is "none".
-__device__ __forceinline__ void wave_best(double &g, int &i) {
-    const uint32_t lane = threadIdx.x & 63u;
-    best_step<DPP_ROW_SHR1, 0xf>(g, i, lane);
-    best_step<DPP_ROW_SHR2, 0xf>(g, i, lane);
-    best_step<DPP_ROW_SHR4, 0xf>(g, i, lane);
-    best_step<DPP_ROW_SHR8, 0xf>(g, i, lane);
-    best_step<DPP_ROW_BCAST15, 0xa>(g, i, lane);
-    best_step<DPP_ROW_BCAST31, 0xc>(g, i, lane);
-    i = __builtin_amdgcn_readlane(i, 63);
-    g = double_of(readlane_u64(bits_of(g), 63));
-}
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void min_step(int &v, uint32_t lane) {
-    int o = static_cast<int>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(v)));
-    if (dpp_has_source<CTRL, ROW_MASK>(lane) && o < v) v = o;
-}
-__device__ __forceinline__ int wave_min(int v) {
-    const uint32_t lane = threadIdx.x & 63u;
-    min_step<DPP_ROW_SHR1, 0xf>(v, lane);
-    min_step<DPP_ROW_SHR2, 0xf>(v, lane);
-    min_step<DPP_ROW_SHR4, 0xf>(v, lane);
-    min_step<DPP_ROW_SHR8, 0xf>(v, lane);
-    min_step<DPP_ROW_BCAST15, 0xa>(v, lane);
-    min_step<DPP_ROW_BCAST31, 0xc>(v, lane);
-    return __builtin_amdgcn_readlane(v, 63);
-}
-__device__ __forceinline__ double readlane_f64(double v, uint32_t lane) { return double_of(readlane_u64(bits_of(v), lane)); }
-
-// A feature candidate as held by lane `owner`, broadcast to the wave.
-__device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
-    FeatCand r;
-    r.found = __builtin_amdgcn_readlane(c.found, owner);
-    r.splittable = __builtin_amdgcn_readlane(c.splittable, owner);
-    r.gain = readlane_f64(c.gain, owner);
-    r.best_gain = readlane_f64(c.best_gain, owner);
-    r.threshold = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.threshold), owner));
-    r.default_left = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.default_left), owner));
-    r.left_grad = readlane_f64(c.left_grad, owner);
-    r.left_hess = readlane_f64(c.left_hess, owner);
-    r.left_count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(c.left_count), owner));
-    r.left_units_g = readlane_f64(c.left_units_g, owner);
-    r.left_units_h = readlane_f64(c.left_units_h, owner);
-    r.col = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.col), owner));
-    r.nan_idx = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(c.nan_idx), owner));
-    return r;
 }
 
 // The end of a split step, by one wave (learner.rs:294-352, then learner.rs:418-429 and 249-290): both children's
@@ -1513,6 +1839,8 @@ __device__ void finish_step(const GrowState &g) {
             else t.right_child[pl.parent] = node;
         }
         t.split_feature[node] = info.feature;
+#pragma unroll
+        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = P.left_bins[w];
         t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
         t.threshold_bin[node] = info.threshold;
         t.default_left[node] = static_cast<uint8_t>(info.default_left);
@@ -1611,16 +1939,8 @@ __device__ void finish_step(const GrowState &g) {
         p.ticket = 0;
         p.left = 0;
         p.col = ni.col;
-        // learner.rs:432-452: bins 0..=threshold, and the NaN bin when missing values go left
-        const uint32_t upto = ni.threshold + 1;
-        const bool nan_left = ni.default_left && ni.nan_idx != NO_BIN;
 #pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) {
-            uint32_t lo = 32 * w;
-            uint32_t word = upto >= lo + 32 ? 0xffffffffu : (upto > lo ? (1u << (upto - lo)) - 1u : 0u);
-            if (nan_left && (ni.nan_idx >> 5) == w) word |= 1u << (ni.nan_idx & 31u);
-            p.left_bins[w] = word;
-        }
+        for (uint32_t w = 0; w < 8; ++w) p.left_bins[w] = left_bins_word(ni, w);
         p.used_columns = used;
         p.built_side = ni.left_count <= ni.right_count ? 0u : 1u;
         p.may_search = nl.slot >= 0 && nn + 1 < g.num_leaves && depth_allows(g, nl.depth + 1);
@@ -2061,6 +2381,9 @@ __device__ __forceinline__ uint32_t finish_chunks(uint32_t groups, bool packed) 
 // grid: (ncg, FIN_CHUNKS), 1024 threads.
 __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a) {
     __shared__ int64_t red8[1024][8];  // partial sums on their way to stripe 0 (the first two words for pairs)
+    static_assert(8 * sizeof(CatScratch) <= sizeof(red8), "categorical scratch reuses the reduction buffer");
+    // per (column, child) wave of a categorical scan; the scans start after the reduction's last barrier
+    CatScratch *cats = reinterpret_cast<CatScratch *>(red8);
     int64_t(*red)[8] = red8;
     __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
     __shared__ uint32_t s_found[2][CG_COLS][2];
@@ -2203,7 +2526,11 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
     const Ctx c = make_ctx(g.cfg, g.sg, g.sh, p.child_ug[child], p.child_uh[child], cnt);
     const int64_t *hist = child == p.built_side ? built : parent;
     const bool searched = sf >= 0 && scan_searched(c, sm, sev);
-    if (searched && (dir == 0 || scan_two_way(sm))) {
+    const bool categorical = sm.kind == 2;
+    if (searched && categorical && dir == 0) {  // one wave per categorical feature and child
+        FeatCand r = categorical_candidate(c, g.cfg, sm, hist, cats[wave & 7u], nullptr);
+        if ((tid & 63u) == 0) g.cands[static_cast<size_t>(child) * g.nf + sf] = r;
+    } else if (searched && !categorical && (dir == 0 || scan_two_way(sm))) {
         Grown r = {};
         bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
         if ((tid & 63u) == 0) {
@@ -2212,7 +2539,7 @@ __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a)
         }
     }
     __syncthreads();
-    if (sf >= 0 && dir == 0 && (tid & 63u) == 0) {
+    if (sf >= 0 && dir == 0 && (tid & 63u) == 0 && !(searched && categorical)) {
         FeatCand r = {};
         if (searched)
             r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],

@@ -142,8 +142,29 @@ CONFIGS = {
 }
 
 
-def synthetic(config, rows=None, cols=None, seed=7, max_bin=None):
-    """Configuration ``config`` (1-5) as a binned dataset, generated natively; ``rows``/``cols`` shrink it."""
+def as_categorical(data, features):
+    """``data`` with the numerical ``features`` turned categorical: the NaN bin (or none) becomes bin 0, the bin of
+    silvic's categorical mappers for negative / missing / unseen values (data/bin_mapper.rs), and value bin b becomes
+    category bin b + 1. The bin count is unchanged when the feature has a NaN bin. Modifies ``data`` in place."""
+    for j in features:
+        m = data.features[j]
+        if m.kind != _abi.BINS_NUMERICAL or not m.num_bins:
+            raise ValueError(f"feature {j} is not a numerical feature with bins")
+        if not m.nan_bin:
+            raise ValueError(f"feature {j} has no NaN bin to become the categorical bin 0")
+        g = data.groups[m.group]
+        col = g.data.reshape(data.num_rows, g.row_stride)[:, m.column]
+        nan = m.num_bins - 1
+        col[:] = np.where(col == nan, 0, col.astype(np.int32) + 1).astype(np.uint8)
+        m.kind = _abi.BINS_CATEGORICAL
+        m.nan_bin = False
+        m.bounds = None
+    return data
+
+
+def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=False):
+    """Configuration ``config`` (1-5) as a binned dataset, generated natively; ``rows``/``cols`` shrink it.
+    ``categorical``: config 2's integer features (the last quarter) as categorical features (see as_categorical)."""
     lib = _abi.load_synth()
     drows, dcols, dbin, _ = CONFIGS[config]
     rows = drows if rows is None else rows
@@ -176,4 +197,10 @@ def synthetic(config, rows=None, cols=None, seed=7, max_bin=None):
         total = int(lib.synth_total_bins(h))
     finally:
         lib.synth_free(h)
-    return BinnedDataset(rows, features, groups, total, label)
+    data = BinnedDataset(rows, features, groups, total, label)
+    if categorical:
+        if config != 2:
+            raise ValueError("categorical features are defined for configuration 2")
+        ints = [j for j in range(3 * cols // 4, cols) if features[j].num_bins and features[j].nan_bin]
+        as_categorical(data, ints)
+    return data

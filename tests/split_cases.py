@@ -122,3 +122,35 @@ def quantized_cases():
             units += [rng.below(9) - 4.0, 2.0 * n]
         out.append((case, np.array(units, np.float64), rows, numerical(num_bins, case % 2 == 0)))
     return out
+
+
+def categorical_cases():
+    """split.rs:1252-1349 one-hot and sorted categorical cases, sorted cases under the default categorical
+    parameters with larger bins, and split.rs:1414-1471's zero-hessian bins with cat_smooth 0 (a 0/0 ratio):
+    (name, hist, rows, meta, cfg)."""
+    out = []
+    rng = Lcg(3)
+    for case in range(200):
+        num_bins = 2 + rng.below(3)
+        hist, rows = random_hist(rng, num_bins, 1.0)
+        out.append((f"one-hot {case}", hist, rows, categorical(num_bins), config()))
+    rng = Lcg(5)
+    for case in range(200):
+        num_bins = 6 + rng.below(12)
+        hist, rows = random_hist(rng, num_bins, 1.0)
+        cfg = config(min_data_per_group=1, cat_smooth=1.0, max_cat_threshold=4)
+        out.append((f"sorted {case}", hist, rows, categorical(num_bins), cfg))
+    rng = Lcg(13)
+    for case in range(100):
+        num_bins = 20 + rng.below(200)
+        rows = np.array([rng.below(300) for _ in range(num_bins)], np.int64)
+        hist = []
+        for n in rows:
+            hist += [(rng.next() - 0.45) * n, n * 1.0]
+        out.append((f"sorted default {case}", np.array(hist, np.float64), rows, categorical(num_bins), config()))
+    zero = np.array([0.0, 0.0, -3.0, 2.0, 0.0, 0.0, 4.0, 2.0, 0.0, 0.0, 1.0, 1.0, 0.0, 0.0, 0.0, 0.0])
+    for nb in (3, 8):
+        h = zero[: 2 * nb]
+        cfg = config(min_data_in_leaf=0, min_sum_hessian_in_leaf=0.0, min_data_per_group=0, cat_smooth=0.0)
+        out.append((f"zero hessian {nb}", h, h[1::2].astype(np.int64), categorical(nb), cfg))
+    return out

@@ -12,7 +12,7 @@ import oracle
 import silvic_amd
 from silvic_amd import _abi, bin_split, device_node
 from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients
-from tests.split_cases import config, numerical_cases, quantized_cases, sums
+from tests.split_cases import categorical_cases, config, numerical_cases, quantized_cases, sums
 
 pytestmark = pytest.mark.gpu
 
@@ -202,6 +202,21 @@ def compare_split(d, o, name):
         ds, os_ = getattr(d, side), getattr(o, side)
         assert (ds.grad, ds.hess, ds.count) == (os_.grad, os_.hess, os_.count), (name, side)
     assert d.left_output == o.left_output and d.right_output == o.right_output, name
+    assert bool(d.categorical) == bool(o.categorical), name
+    if o.categorical:
+        assert d.num_cat_bins == o.num_cat_bins, name
+        assert list(d.cat_bins[: d.num_cat_bins]) == list(o.cat_bins[: o.num_cat_bins]), name
+
+
+def test_categorical_split_search_matches_the_oracle_bit_for_bit(rocm):
+    say("split search: one-hot, sorted and zero-hessian categorical cases")
+    for name, hist, rows, meta, cfg in categorical_cases():
+        units = np.round(hist * 64.0)
+        s = (units[0::2].sum(), units[1::2].sum(), int(rows.sum()))
+        o, ospl = oracle.find_best_split(units, [meta], [1], s, 1.0 / 64, 1.0 / 64, cfg)
+        d, dspl = rocm.find_best_split(units, [meta], [1], s, 1.0 / 64, 1.0 / 64, cfg)
+        compare_split(d, o, name)
+        assert np.array_equal(dspl, ospl), name
 
 
 def test_split_search_matches_the_oracle_bit_for_bit(rocm):
@@ -279,6 +294,30 @@ def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves, qbins):
     assert np.array_equal(rocm.partition_rows(n), o_part[:n])
 
 
+# categorical columns: the default parameters search sorted categorical rules (21 bins > max_cat_to_onehot 4);
+# max_cat_to_onehot 32 searches one-hot rules; cat_smooth 0 with min_data_per_group 1 ranks raw ratios.
+@pytest.mark.parametrize("rows,cols,leaves,kw", [(200_000, 28, 63, {}), (300_000, 12, 255, dict(max_cat_to_onehot=32)),
+                                                 (60_000, 16, 31, dict(cat_smooth=0.0, min_data_per_group=1,
+                                                                       max_cat_threshold=8))])
+def test_categorical_tree_matches_the_oracle(rocm, rows, cols, leaves, kw):
+    say("categorical grow", rows, cols, leaves, kw)
+    data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=23, categorical=True)
+    assert any(f.kind == _abi.BINS_CATEGORICAL for f in data.features)
+    g, h = binary_gradients(data, 9)
+    p = oracle.default_params(num_leaves=leaves, **kw)
+    o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
+    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed)
+    n = rocm.reset_partition()
+    mask = oracle.feature_mask(data.features, 1.0, 2, 0)
+    d = rocm.grow(p.cfg, leaves, -1, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
+    compare_trees(d, o_tree, "categorical grow")
+    cat_nodes = (o_tree["decision_type"] & 1) != 0
+    assert cat_nodes.any(), "the case must split on a categorical feature"
+    assert np.array_equal(d["left_bins"], o_tree["left_bins"])
+    assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+    assert np.array_equal(rocm.partition_rows(n), o_part[:n])
+
+
 def test_learner_cases_on_the_device(rocm):
     # learner.rs:690-740 on numerical features: max_depth, zero-gradient rows
     say("learner cases")
@@ -316,10 +355,12 @@ def params_to_lightgbm(params):
     (2, 200_000, 128, dict(objective=_abi.OBJ_BINARY, num_leaves=255), 6),
     (2, 100_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, bagging_fraction=0.8, bagging_freq=2,
                           feature_fraction=0.7, lambda_l2=1.0), 8),
+    (2, 120_000, 28, dict(objective=_abi.OBJ_BINARY, num_leaves=63, categorical=True), 6),
 ])
 def test_boosting_matches_the_oracle(config, rows, cols, params, rounds):
     say("boost", config, rows, cols, params, rounds)
-    data = silvic_amd.synthetic(config, rows=rows, cols=cols, seed=13)
+    categorical = bool(params.pop("categorical", False))
+    data = silvic_amd.synthetic(config, rows=rows, cols=cols, seed=13, categorical=categorical)
     o, t = boost_both(data, params, rounds)
     assert len(t.trees) == len(o.trees) == rounds
     assert t.init_score == o.init_score

@@ -35,6 +35,38 @@ def test_leaves_match_the_partition_and_their_sums():
         assert abs(tree["leaf_weight"][leaf] - H) <= 1e-6 * H
 
 
+def test_left_bin_masks_route_every_row_to_its_leaf():
+    # learner.rs:459-485 apply_split: a numerical node sends bins 0..=threshold (and the NaN bin iff default_left)
+    # left, a categorical node exactly its rule's bins; walking each row down the masks must reach the leaf whose
+    # range holds it
+    data, bins = learner_dataset(0, 3000)
+    g, h = learner_gradients(0, 3000, bins)
+    tree, ranges, part = oracle.grow_tree(data, g, h, learner_params())
+    masks = tree["left_bins"]
+    for node, f in enumerate(tree["split_feature"]):
+        meta = data.features[f]
+        cat = (tree["decision_type"][node] & 1) != 0
+        assert cat == (meta.kind == _abi.BINS_CATEGORICAL)
+        left = [b for b in range(256) if (masks[node][b >> 5] >> (b & 31)) & 1]
+        if cat:
+            assert tree["threshold_bin"][node] == 0 and 0 < len(left) < meta.num_bins
+        else:
+            want = list(range(tree["threshold_bin"][node] + 1))
+            if meta.nan_bin and (tree["decision_type"][node] & 2):
+                want.append(meta.num_bins - 1)
+            assert left == want
+    leaf_of = np.empty(3000, np.int64)
+    for leaf, (b, c) in enumerate(ranges):
+        leaf_of[part[b:b + c]] = leaf
+    for r in range(3000):
+        node = 0
+        while node >= 0:
+            b = int(bins[r, tree["split_feature"][node]])
+            go_left = (masks[node][b >> 5] >> (b & 31)) & 1
+            node = tree["left_child"][node] if go_left else tree["right_child"][node]
+        assert ~node == leaf_of[r]
+
+
 def test_max_depth_limits_growth():
     # learner.rs:690-699
     data, bins = learner_dataset(0, 3000)
