@@ -105,13 +105,13 @@ def main():
     t0 = time.perf_counter()
     timed = trainer.step(args.steps)
     elapsed = time.perf_counter() - t0
-    prof = (C.c_double * 12)()
-    trainer.backend._check(lib.srocm_profile_read(h, prof, 12))
+    prof = (C.c_double * 15)()
+    trainer.backend._check(lib.srocm_profile_read(h, prof, 15))
     trainer.backend._check(lib.srocm_profile(h, 0))
     if len(timed) != args.steps:
         log(f"training ended after {len(timed)} of {args.steps} timed iterations")
     (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
-     part_rows, _, _) = list(prof)
+     part_rows, _, _, grow_steps, expansions, kept) = list(prof)
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
     # every histogram is built by k_hist (roots) or k_step_rows (split steps, which also partition)
@@ -122,7 +122,8 @@ def main():
     root_gbps = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms else 0.0
     log(f"{steps} iterations in {elapsed:.3f}s; k_step_rows: {step_launches:.0f} launches, {step_ms:.1f} ms, "
         f"{step_gbps:.0f} GB/s algorithmic; k_hist (roots): {hist_launches:.0f} launches, {hist_ms:.1f} ms, "
-        f"{root_gbps:.0f} GB/s; {builds:.0f} histograms, {part_rows:.3g} rows partitioned")
+        f"{root_gbps:.0f} GB/s; {builds:.0f} histograms, {part_rows:.3g} rows partitioned; {grow_steps:.0f} split "
+        f"steps expanded {expansions:.0f} leaves for {kept:.0f} kept splits")
 
     cpu = None
     if not args.no_cpu:

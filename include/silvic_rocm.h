@@ -358,9 +358,10 @@ int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
  *   [5] their algorithmic bytes (9 B per partitioned row + used columns + 4 B per histogrammed row)
  *   [6] histogram builds   [7] rows histogrammed   [8] rows x used columns   [9] rows partitioned
  *   [10] trait partition launches   [11] their ms (count + scatter + copy back)
+ *   [12] device-growth split steps   [13] leaves they expanded   [14] of those, splits the trees kept
  * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
  * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
-#define SROCM_PROFILE_VALUES 12
+#define SROCM_PROFILE_VALUES 15
 int srocm_profile(void *ctx, int enable);
 int srocm_profile_read(void *ctx, double *out, uint32_t len);
 

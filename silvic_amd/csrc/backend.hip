@@ -260,10 +260,12 @@ struct Profile {
     double step_launches = 0, step_ms = 0, step_bytes = 0;  // k_step_rows: split steps
     double builds = 0, rows = 0, bins = 0, part_rows = 0;
     double part_launches = 0, part_ms = 0;                  // trait partitions
+    double steps = 0, expansions = 0, splits = 0;           // device growth: split steps, leaves expanded, kept
     std::vector<hipEvent_t> pool;
     void reset() {
         hist_launches = hist_ms = hist_bytes = step_launches = step_ms = step_bytes = 0;
         builds = rows = bins = part_rows = part_launches = part_ms = 0;
+        steps = expansions = splits = 0;
     }
 };
 
@@ -484,7 +486,7 @@ struct Context {
                     cg.push_back(x);
                 }
                 for (uint32_t c = 0; c < s.width; ++c) gfeat.push_back(c < s.feats.size() ? static_cast<int32_t>(s.feats[c]) : -1);
-                poff += static_cast<uint64_t>(cus) * step_partial_stride(s.width);
+                poff += static_cast<uint64_t>(cus + JMAX) * step_partial_stride(s.width);
             }
             ncg = static_cast<uint32_t>(cg.size());
             step_partial_pairs = std::max<uint64_t>(poff, 1);
@@ -629,7 +631,7 @@ struct Context {
                      int64_t *parent, uint64_t bins_used) {
         uint32_t grid = hist_groups(count);
         for (auto &s : slabs) {
-            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS, nullptr, nullptr};
+            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (prof.on) {
                 e0 = event();
@@ -647,8 +649,7 @@ struct Context {
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width,
-                         nullptr, nullptr, 0};
+            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
             k_hist_reduce<<<div_up(256ull * s.width, 256), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
@@ -712,13 +713,10 @@ struct Context {
         a.dev_left = scalars.p;
         a.begin = begin;
         a.count = count;
-        a.rows = rows;
-        a.buf0 = part.p;
-        a.buf1 = part2.p;
         return a;
     }
 
-    // `count` is the rows to partition, or (with a plan) an upper bound of them.
+    // `count` is the rows to partition.
     void run_partition(const PartArgs &a, uint32_t count) {
         uint32_t grid = std::max<uint32_t>(1, std::min<uint32_t>(cus, div_up(count, 1024)));
         hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -731,16 +729,15 @@ struct Context {
         launch_check("k_part_count");
         k_part_scatter<<<grid, 256, 0, stream>>>(a);
         launch_check("k_part_scatter");
-        if (!a.plan) {  // the trait's partition is in place: bring the range back into the first buffer
-            k_copy_u32<<<std::max<uint32_t>(1, std::min<uint32_t>(div_up(count, 256), cus * 8)), 256, 0, stream>>>(part2.p, part.p, a.begin,
-                                                                                                            count, nullptr);
-            launch_check("k_copy_u32");
-        }
+        // the trait's partition is in place: bring the range back into the first buffer
+        k_copy_u32<<<std::max<uint32_t>(1, std::min<uint32_t>(div_up(count, 256), cus * 8)), 256, 0, stream>>>(part2.p, part.p, a.begin,
+                                                                                                        count);
+        launch_check("k_copy_u32");
         if (prof.on) {
             hip_check(hipEventRecord(e1, stream), "event");
             prof.part_events.emplace_back(e0, e1);
             prof.part_launches += 1;
-            if (!a.plan) prof.part_rows += count;
+            prof.part_rows += count;
         }
     }
 
@@ -920,7 +917,7 @@ struct Context {
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             dim3 grid(div_up(num_features, 4), 1);
-            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, nullptr, dorder.p);
+            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p);
             launch_check("k_split_scan");
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
@@ -963,18 +960,26 @@ struct Context {
     // ------------------------------------------------------------------------------------------------
 
     DevBuf<int64_t> pool;             // histogram slots, 2 * total_bins i64 each
-    DevBuf<Plan> d_plan;
+    DevBuf<StepPlan> d_plans;         // [2], by step parity
     DevBuf<GrowCtl> d_ctl;
-    DevBuf<DLeaf> d_leaves;
+    DevBuf<TLeaf> d_tl;               // the speculative tree's leaves
+    DevBuf<TKey> d_tk;
+    DevBuf<int32_t> d_leaf_t;
+    DevBuf<uint8_t> d_leaf_left;
     DevBuf<uint8_t> d_splittable, d_eval, d_mask;
-    DevBuf<LeafKey> d_keys;
     DevBuf<ScanJob> d_jobs;
     DevBuf<FeatCand> d_cands;
+    DevBuf<RowRun> d_runs;            // end of a tree: runs of rows to bring into ascending order
+    DevBuf<MergeJob> d_merges;        // end of a tree: leaves whose expansion was dropped
+    DevBuf<uint32_t> d_starts;
+    Pinned<uint8_t> h_fix;            // staging of the runs and merges (rewritten only after a sync)
+    Pinned<GrowCtl> h_ctl;
     // split steps (k_step_rows, k_step_finish)
-    DevBuf<int32_t> step_partial;            // per slab: [cus][256 * W] {g, h}
+    DevBuf<int32_t> step_partial;            // per slab: [cus + JMAX][256 * W] {g, h}
     DevBuf<unsigned long long> tile_status;  // per partition tile
-    DevBuf<uint32_t> fin_counts;             // [ncg] chunk counters, then the column-group counter
+    DevBuf<uint32_t> fin_counts;             // [JMAX][ncg] item counters, [JMAX] job counters, the job counter
     uint64_t epochs_used = 0;
+    uint32_t last_steps = 0;                 // split steps of the last tree (the first guess for the next)
     struct TreeBufs {
         DevBuf<int32_t> split_feature, left_child, right_child, leaf_parent, leaf_depth;
         DevBuf<uint32_t> threshold_bin;
@@ -986,18 +991,24 @@ struct Context {
     } dtree;
     uint32_t grow_capacity = 0;
 
+    uint32_t k1_groups() const { return cus + JMAX; }  // k_step_rows' grid
+    uint32_t k2_blocks() const { return cus; }         // k_step_finish's grid: one 1024-thread block per CU fits
+
     void ensure_grow(uint32_t L) {
         if (grow_capacity >= L && pool.p) return;
-        pool.alloc(static_cast<size_t>(L) * 2 * total_bins);  // a slot per leaf
-        d_keys.alloc(L);
-        d_plan.alloc(1);
+        const uint32_t tcap = grow_tcap(L), nslots = tcap / 2 + 1;
+        pool.alloc(static_cast<size_t>(nslots) * 2 * total_bins);
+        d_plans.alloc(2);
         d_ctl.alloc(1);
-        d_leaves.alloc(L);
-        d_splittable.alloc(static_cast<size_t>(L) * nf);
+        d_tl.alloc(tcap);
+        d_tk.alloc(tcap);
+        d_leaf_t.alloc(L);
+        d_leaf_left.alloc(L);
+        d_splittable.alloc(static_cast<size_t>(tcap) * nf);
         d_eval.alloc(nf);
         d_mask.alloc(nf);
         d_jobs.alloc(1);
-        d_cands.alloc(2 * static_cast<size_t>(nf));
+        d_cands.alloc(static_cast<size_t>(JMAX) * 2 * nf);
         dtree.split_feature.alloc(L);
         dtree.left_child.alloc(L);
         dtree.right_child.alloc(L);
@@ -1014,8 +1025,8 @@ struct Context {
         dtree.leaf_count.alloc(L);
         dtree.left_bins.alloc(static_cast<size_t>(L) * 8);
         step_partial.alloc(2 * step_partial_pairs);
-        tile_status.alloc(div_up(rows, STEP_TILE) + 1);
-        fin_counts.alloc(ncg + 1);
+        tile_status.alloc(div_up(rows, STEP_TILE) + JMAX + 1);
+        fin_counts.alloc(static_cast<size_t>(JMAX) * ncg + JMAX + 1);
         reset_step_state();
         grow_capacity = L;
     }
@@ -1031,10 +1042,12 @@ struct Context {
     GrowState grow_state(const srocm_grow_spec &spec) {
         GrowState g{};
         g.ctl = d_ctl.p;
-        g.plan = d_plan.p;
-        g.leaves = d_leaves.p;
+        g.plans = d_plans.p;
+        g.tl = d_tl.p;
+        g.tk = d_tk.p;
+        g.leaf_t = d_leaf_t.p;
+        g.leaf_left = d_leaf_left.p;
         g.splittable = d_splittable.p;
-        g.keys = d_keys.p;
         g.jobs = d_jobs.p;
         g.cands = d_cands.p;
         g.evaluate = d_eval.p;
@@ -1048,10 +1061,15 @@ struct Context {
         g.slot_stride = 2 * total_bins;
         g.nf = nf;
         g.num_leaves = spec.num_leaves;
+        g.tcap = grow_tcap(spec.num_leaves);
+        g.nslots = g.tcap / 2 + 1;
         g.max_depth = spec.max_depth;
         g.cfg = cfg_dev(spec.cfg);
         g.sg = spec.grad_scale;
         g.sh = spec.hess_scale;
+        g.target_groups = cus;
+        g.ncg = ncg;
+        g.flush_rows = flush_rows();
         return g;
     }
 
@@ -1149,15 +1167,18 @@ std::pair<double, double> Context::compute_gradients() {
     return read_maxima();
 }
 
-// learner.rs:121-352 on the device: every split step is enqueued without waiting; the device picks the leaf,
-// partitions, histograms the smaller child, subtracts, searches both children and updates the tree. The host reads
-// the finished tree once.
+// learner.rs:121-352 on the device: split steps are enqueued without waiting; the device replays the reference's
+// leaf order, expands leaves (speculatively beyond the next one), partitions, histograms the smaller children,
+// subtracts, searches the children and writes the tree. The host checks for the end of the tree once per batch of
+// steps (sized by the last tree's step count), reads the finished tree, and enqueues the final row order.
 void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits,
                    std::vector<GrowLeaf> &leaves) {
     require_loaded();
     if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
     check_range(spec.root);
     if (spec.num_leaves < 1) fail(SROCM_ERR_CONFIG, "num_leaves must be positive");
+    if (spec.num_leaves > GROW_MAX_LEAVES)
+        fail(SROCM_ERR_UNSUPPORTED, "device growth takes num_leaves up to " + std::to_string(GROW_MAX_LEAVES));
     const uint32_t L = spec.num_leaves;
     std::vector<uint8_t> mask(spec.feature_mask, spec.feature_mask + nf);
     ensure_grow(L);
@@ -1182,68 +1203,99 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     uint64_t used_root = 0;
     for (uint32_t f = 0; f < nf; ++f)
         if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
+    h_ctl.alloc(1);
+    auto read_ctl = [&]() {
+        hip_check(hipMemcpyAsync(h_ctl.p, d_ctl.p, sizeof(GrowCtl), hipMemcpyDeviceToHost, stream), "read grow control");
+        sync();
+        return *h_ctl.p;
+    };
+    GrowCtl hc{};
     if (root_searched) {
         // the root histogram goes into slot 0
         launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
         k_root_prep<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_prep");
-        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, nullptr);
+        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr);
         launch_check("k_split_scan");
-        k_root_select<<<1, 256, 0, stream>>>(g);
+        k_root_select<<<1, 1024, 0, stream>>>(g);
         launch_check("k_root_select");
-        // split steps: each is a no-op once the tree has stopped
-        FinishArgs fa{step_partial.p, d_cgs.p, gcol_feat.p, fin_counts.p, fin_counts.p + ncg, ncg, cus, flush_rows()};
-        for (uint32_t s = 0; s + 1 < L; ++s) {
-            hipEvent_t e0 = nullptr, e1 = nullptr;
-            if (prof.on) {
-                e0 = event();
-                e1 = event();
-                hip_check(hipEventRecord(e0, stream), "event");
-            }
-            for (size_t si = 0; si < slabs.size(); ++si) {
-                const Slab &sl = slabs[si];
-                StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
-                            sl.col_bins.p, tile_status.p, d_plan.p, d_ctl.p, flush_rows(), cus, si == 0 ? 1u : 0u};
-                switch (sl.width) {
-                case 32: k_step_rows<32><<<cus, 1024, 0, stream>>>(sa); break;
-                case 64: k_step_rows<64><<<cus, 1024, 0, stream>>>(sa); break;
-                default: k_step_rows<128><<<cus, 1024, 0, stream>>>(sa); break;
+        // split steps: each is a no-op once the tree is complete; each commits at least one split
+        uint32_t s = 0, batch = std::max<uint32_t>(2, last_steps ? last_steps : 8);
+        const uint32_t max_steps = L;
+        for (;;) {
+            const uint32_t end = std::min(max_steps, s + batch);
+            for (; s < end; ++s) {
+                const uint32_t parity = s & 1u;
+                hipEvent_t e0 = nullptr, e1 = nullptr;
+                if (prof.on) {
+                    e0 = event();
+                    e1 = event();
+                    hip_check(hipEventRecord(e0, stream), "event");
                 }
-                launch_check("k_step_rows");
+                for (size_t si = 0; si < slabs.size(); ++si) {
+                    const Slab &sl = slabs[si];
+                    StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
+                                sl.col_bins.p, tile_status.p, d_plans.p + parity, d_ctl.p, flush_rows(), si == 0 ? 1u : 0u};
+                    switch (sl.width) {
+                    case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 64: k_step_rows<64><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    default: k_step_rows<128><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    }
+                    launch_check("k_step_rows");
+                }
+                if (prof.on) {
+                    hip_check(hipEventRecord(e1, stream), "event");
+                    prof.step_events.emplace_back(e0, e1);
+                    prof.step_launches += static_cast<double>(slabs.size());
+                }
+                uint32_t *fc = fin_counts.p;
+                FinishArgs fa{step_partial.p, d_cgs.p, gcol_feat.p, fc, fc + static_cast<size_t>(JMAX) * ncg,
+                              fc + static_cast<size_t>(JMAX) * ncg + JMAX, d_plans.p + parity, d_plans.p + (parity ^ 1u)};
+                k_step_finish<<<k2_blocks(), 1024, 0, stream>>>(g, fa);
+                launch_check("k_step_finish");
             }
-            if (prof.on) {
-                hip_check(hipEventRecord(e1, stream), "event");
-                prof.step_events.emplace_back(e0, e1);
-                prof.step_launches += static_cast<double>(slabs.size());
-            }
-            k_step_finish<<<dim3(ncg, FIN_CHUNKS), 1024, 0, stream>>>(g, fa);
-            launch_check("k_step_finish");
+            hc = read_ctl();
+            if (hc.done) break;
+            if (s >= max_steps) fail(SROCM_ERR_INTERNAL, "the device learner did not finish the tree");
+            batch = 2;
         }
+        last_steps = hc.steps;
+    } else {
+        hc = read_ctl();
     }
-    if (root_searched) {  // every leaf's rows back in the first partition buffer
-        k_consolidate<<<dim3(std::max<uint32_t>(1, std::min<uint32_t>(div_up(spec.root.count, 256 * 8), cus)), L), 256, 0, stream>>>(
-            g, part2.p, part.p);
-        launch_check("k_consolidate");
+    if (hc.error == 1) {
+        const uint32_t *e = hc.err_info;
+        fail(SROCM_ERR_INTERNAL, "a split sent no rows to one side (step job " + std::to_string(e[0]) + ", leaf " +
+                                     std::to_string(e[1]) + ", " + std::to_string(e[3]) + " of " + std::to_string(e[2]) +
+                                     " rows left, " + std::to_string(e[4]) + " tiles on " + std::to_string(e[5]) +
+                                     (e[6] ? " workgroups, packed)" : " workgroups)"));
     }
-    // one readback: control block, leaves, tree arrays
-    size_t need = sizeof(GrowCtl) + static_cast<size_t>(L) * (sizeof(DLeaf) + 4 * 5 + 4 + 1 + 4 + 8 * 6 + 32);
-    h_result.alloc(need + 64);
+    if (hc.error == 3) fail(SROCM_ERR_INTERNAL, "a partition tile waited too long for an earlier tile's count");
+    if (hc.error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc.error));
+    const uint32_t n = hc.num_leaves, ni = n - 1, ntent = hc.ntent;
+    // one readback: speculative leaves, committed leaves and the tree arrays
+    auto padded = [](size_t bytes) { return (bytes + 7) & ~static_cast<size_t>(7); };
+    // what is read below: the speculative leaves, six 8-byte, eight 4-byte and one 1-byte array of L, the masks
+    const size_t need = padded(static_cast<size_t>(ntent) * sizeof(TLeaf)) + 6 * padded(static_cast<size_t>(L) * 8) +
+                        8 * padded(static_cast<size_t>(L) * 4) + padded(static_cast<size_t>(L) * 32) + padded(L);
+    h_result.alloc(need);
     uint8_t *hp = h_result.p;
+    const uint8_t *hend = h_result.p + need;
     auto rd = [&](void *dev, size_t bytes) {
+        if (hp + bytes > hend) fail(SROCM_ERR_INTERNAL, "tree readback outgrew its staging");
         hip_check(hipMemcpyAsync(hp, dev, bytes, hipMemcpyDeviceToHost, stream), "read tree");
         uint8_t *at = hp;
-        hp += bytes;
+        hp += padded(bytes);
         return at;
     };
-    const GrowCtl *hc = reinterpret_cast<const GrowCtl *>(rd(d_ctl.p, sizeof(GrowCtl)));
-    const DLeaf *hl = reinterpret_cast<const DLeaf *>(rd(d_leaves.p, L * sizeof(DLeaf)));
-    // 8-byte arrays first so every array stays aligned in the staging buffer
+    const TLeaf *tl = reinterpret_cast<const TLeaf *>(rd(d_tl.p, ntent * sizeof(TLeaf)));
     auto *iv = reinterpret_cast<const double *>(rd(dtree.internal_value.p, L * 8));
     auto *iw = reinterpret_cast<const double *>(rd(dtree.internal_weight.p, L * 8));
     auto *lv = reinterpret_cast<const double *>(rd(dtree.leaf_value.p, L * 8));
     auto *lw = reinterpret_cast<const double *>(rd(dtree.leaf_weight.p, L * 8));
     auto *ic = reinterpret_cast<const int64_t *>(rd(dtree.internal_count.p, L * 8));
     auto *lcn = reinterpret_cast<const int64_t *>(rd(dtree.leaf_count.p, L * 8));
+    auto *lt = reinterpret_cast<const int32_t *>(rd(d_leaf_t.p, L * 4));
     auto *sf = reinterpret_cast<const int32_t *>(rd(dtree.split_feature.p, L * 4));
     auto *lc = reinterpret_cast<const int32_t *>(rd(dtree.left_child.p, L * 4));
     auto *rc = reinterpret_cast<const int32_t *>(rd(dtree.right_child.p, L * 4));
@@ -1254,13 +1306,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     auto *lb = reinterpret_cast<const uint32_t *>(rd(dtree.left_bins.p, static_cast<size_t>(L) * 32));
     auto *dl = reinterpret_cast<const uint8_t *>(rd(dtree.default_left.p, L));
     sync();
-    if (hc->error == 1) fail(SROCM_ERR_INTERNAL, "a split sent no rows to one side");
-    if (hc->error == 3) fail(SROCM_ERR_INTERNAL, "a partition tile waited too long for an earlier tile's count");
-    if (hc->error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc->error));
-    uint32_t n = hc->num_leaves;
     tree = HostTree{};
     tree.num_leaves = n;
-    uint32_t ni = n - 1;
     tree.split_feature.assign(sf, sf + ni);
     tree.left_child.assign(lc, lc + ni);
     tree.right_child.assign(rc, rc + ni);
@@ -1275,9 +1322,13 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     tree.leaf_count.assign(lcn, lcn + n);
     tree.leaf_parent.assign(lp, lp + n);
     tree.leaf_depth.assign(ld, ld + n);
-    leaves.assign(n, GrowLeaf{});
-    for (uint32_t i = 0; i < n; ++i) leaves[i].range = srocm_leaf_range{hl[i].begin, hl[i].count};
     tree.left_bins.assign(lb, lb + static_cast<size_t>(ni) * 8);
+    leaves.assign(n, GrowLeaf{});
+    for (uint32_t i = 0; i < n; ++i) {
+        const int32_t k = lt[i];
+        if (k < 0 || static_cast<uint32_t>(k) >= ntent) fail(SROCM_ERR_INTERNAL, "device learner lost a leaf");
+        leaves[i].range = srocm_leaf_range{tl[k].begin, tl[k].count};
+    }
     splits.assign(ni, srocm_bin_split{});
     for (uint32_t k = 0; k < ni; ++k) {  // learner.rs:432-452, as the device planned each split
         const srocm_feature &m = feats[tree.split_feature[k]];
@@ -1286,14 +1337,76 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         bs.group = m.group;
         bs.column = m.column;
     }
+
+    // the final row order (cpu.rs:556-599 keeps every leaf ascending): each unexpanded speculative leaf's rows into
+    // the first buffer in ascending order, then each leaf whose expansion was dropped merged from its runs
+    std::vector<RowRun> runs;
+    for (uint32_t k = 0; k < ntent; ++k)
+        if (tl[k].state == T_LEAF && tl[k].count && (tl[k].buf || tl[k].rev))
+            runs.push_back(RowRun{tl[k].begin, tl[k].count, tl[k].buf, tl[k].rev});
+    std::vector<MergeJob> merges;
+    std::vector<uint32_t> starts;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t k = static_cast<uint32_t>(lt[i]);
+        if (tl[k].state != T_EXPANDED) continue;
+        MergeJob m{tl[k].begin, tl[k].count, static_cast<uint32_t>(starts.size()), 0};
+        std::vector<uint32_t> stack{k};  // the unexpanded leaves below k, in row order (left child first)
+        while (!stack.empty()) {
+            const uint32_t x = stack.back();
+            stack.pop_back();
+            if (x >= ntent) fail(SROCM_ERR_INTERNAL, "device learner lost a leaf");
+            if (tl[x].state == T_EXPANDED) {
+                stack.push_back(static_cast<uint32_t>(tl[x].kid) + 1);
+                stack.push_back(static_cast<uint32_t>(tl[x].kid));
+            } else if (tl[x].count) {
+                starts.push_back(tl[x].begin - m.begin);
+                ++m.runs;
+            }
+        }
+        starts.push_back(m.count);
+        if (m.runs > 1) merges.push_back(m);
+        else starts.resize(m.first);
+    }
+    if (!runs.empty() || !merges.empty()) {
+        const size_t rb = runs.size() * sizeof(RowRun), mb = merges.size() * sizeof(MergeJob), sb = starts.size() * 4;
+        h_fix.alloc(rb + mb + sb + 64);
+        std::memcpy(h_fix.p, runs.data(), rb);
+        std::memcpy(h_fix.p + rb, merges.data(), mb);
+        std::memcpy(h_fix.p + rb + mb, starts.data(), sb);
+        uint32_t longest = 1;
+        if (!runs.empty()) {
+            d_runs.alloc(runs.size());
+            hip_check(hipMemcpyAsync(d_runs.p, h_fix.p, rb, hipMemcpyHostToDevice, stream), "upload runs");
+            for (const RowRun &r : runs) longest = std::max(longest, r.count);
+            k_consolidate<<<dim3(std::min<uint32_t>(div_up(longest, 256 * 4), 64), static_cast<uint32_t>(runs.size())), 256, 0, stream>>>(
+                d_runs.p, part2.p, part.p);
+            launch_check("k_consolidate");
+        }
+        if (!merges.empty()) {
+            d_merges.alloc(merges.size());
+            d_starts.alloc(starts.size());
+            hip_check(hipMemcpyAsync(d_merges.p, h_fix.p + rb, mb, hipMemcpyHostToDevice, stream), "upload merges");
+            hip_check(hipMemcpyAsync(d_starts.p, h_fix.p + rb + mb, sb, hipMemcpyHostToDevice, stream), "upload merges");
+            longest = 1;
+            for (const MergeJob &m : merges) longest = std::max(longest, m.count);
+            dim3 grid(std::min<uint32_t>(div_up(longest, 256 * 4), 64), static_cast<uint32_t>(merges.size()));
+            k_merge_runs<<<grid, 256, 0, stream>>>(d_merges.p, d_starts.p, part.p, part2.p);
+            launch_check("k_merge_runs");
+            k_copy_back<<<grid, 256, 0, stream>>>(d_merges.p, part2.p, part.p);
+            launch_check("k_copy_back");
+        }
+    }
     if (prof.on && root_searched) {  // the root histogram was counted by launch_hist
-        prof.builds += hc->hist_builds;
-        prof.rows += hc->hist_rows;
-        prof.bins += hc->hist_bins;
-        prof.part_rows += hc->part_rows;
+        prof.builds += hc.hist_builds;
+        prof.rows += hc.hist_rows;
+        prof.bins += hc.hist_bins;
+        prof.part_rows += hc.part_rows;
         // partition: 4 B row id read, 1 B split bin, 4 B row id write per parent row; histogram: the built
         // child's used columns and 4 B packed gradients per row
-        prof.step_bytes += 9.0 * hc->part_rows + hc->hist_bins + 4.0 * hc->hist_rows;
+        prof.step_bytes += 9.0 * hc.part_rows + hc.hist_bins + 4.0 * hc.hist_rows;
+        prof.expansions += hc.expansions;
+        prof.splits += static_cast<double>(ni);
+        prof.steps += hc.steps;
     }
 }
 
@@ -1700,7 +1813,8 @@ int srocm_profile_read(void *ctx, double *out, uint32_t len) {
         c.settle_profile();
         const Profile &p = c.prof;
         double v[SROCM_PROFILE_VALUES] = {p.hist_launches, p.hist_ms, p.hist_bytes, p.step_launches, p.step_ms, p.step_bytes,
-                                          p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms};
+                                          p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms,
+                                          p.steps, p.expansions, p.splits};
         if (out) std::copy(v, v + std::min<uint32_t>(len, SROCM_PROFILE_VALUES), out);
     });
 }

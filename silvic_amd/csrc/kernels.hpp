@@ -210,28 +210,6 @@ __global__ void k_iota(uint32_t *__restrict__ out, uint64_t n) {
 // histogram `partial[wg][bin * W + column] = {g, h}`; k_hist_reduce adds the partials.
 // ---------------------------------------------------------------------------------------------------------
 
-// The split one step of a device-driven tree applies (learner.rs:249-352), written by the step before it and read
-// by the step's partition, histogram and search kernels. `active` is 0 once the tree has stopped growing.
-struct Plan {
-    uint32_t active;          // this step splits a leaf
-    uint32_t may_search;      // the children get a histogram and a split search (learner.rs:266-268)
-    uint32_t index;           // the leaf split; it becomes the left child
-    uint32_t begin, count;    // its rows in the partition
-    uint32_t col;             // column-major index of the split feature
-    uint32_t built_side;      // 0: the left child is histogrammed, 1: the right (learner.rs:271-275)
-    int32_t parent_slot, built_slot;
-    uint32_t left;            // rows going left, written by the partition
-    uint32_t left_bins[8];
-    int64_t parent_count;
-    uint32_t used_columns;    // evaluated non-trivial features (the histogram's used columns)
-    uint32_t src_buf;         // partition buffer holding the leaf's rows; its children go to the other one
-    uint32_t src_rev;         // the leaf's rows are stored in reverse order
-    uint32_t epoch;           // tags this step's partition tile status words
-    uint32_t ticket;          // next partition tile to hand out (0 at the start of the step)
-    uint32_t pad_;
-    double child_ug[2], child_uh[2];  // the children's sums in histogram units (left, right)
-};
-
 struct HistArgs {
     const uint8_t *bins;      // slab rows: row r at bins + r * W
     const uint32_t *rows;     // partition buffer; the leaf's rows start at `begin`
@@ -242,27 +220,7 @@ struct HistArgs {
     uint32_t flush_rows;
     uint32_t max_groups;      // == gridDim.x
     uint32_t min_rows_per_group;
-    const Plan *plan;         // when non-null, the leaf is the plan's built child (and nothing to do unless searched)
-    const uint32_t *rows2;    // the second partition buffer, where a plan's children may live
 };
-
-// The leaf range of a histogram launch: from the plan when there is one. Returns false when there is nothing to do.
-__device__ __forceinline__ bool hist_range(const Plan *plan, const uint32_t *dev_left, uint32_t begin, uint32_t count,
-                                           uint32_t side, const uint32_t *&dl, uint32_t &b, uint32_t &c, uint32_t &s) {
-    if (plan) {
-        if (!plan->active || !plan->may_search) return false;
-        dl = &plan->left;
-        b = plan->begin;
-        c = plan->count;
-        s = plan->built_side;
-    } else {
-        dl = dev_left;
-        b = begin;
-        c = count;
-        s = side;
-    }
-    return true;
-}
 
 // The rows of the leaf after resolving a device-side left count; identical in every kernel that calls it.
 __device__ __forceinline__ void leaf_rows(const uint32_t *dev_left, uint32_t begin, uint32_t count, uint32_t side,
@@ -309,11 +267,8 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     constexpr int SLOTS = 256 * W / 1024;
     __shared__ int32_t lds[256 * W];
 
-    const uint32_t *dl;
-    uint32_t b0, c0, s0;
-    if (!hist_range(a.plan, a.dev_left, a.begin, a.count, a.side, dl, b0, c0, s0)) return;
     uint32_t lb, n;
-    leaf_rows(dl, b0, c0, s0, lb, n);
+    leaf_rows(a.dev_left, a.begin, a.count, a.side, lb, n);
     uint32_t groups, per;
     hist_split(n, a.max_groups, a.min_rows_per_group, groups, per);
     if (blockIdx.x >= groups) return;
@@ -327,7 +282,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
-    const uint32_t *rows = (a.plan && !a.plan->src_buf ? a.rows2 : a.rows) + lb;
+    const uint32_t *rows = a.rows + lb;
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     uint32_t start = blockIdx.x * per;
     uint32_t end = start + per < n ? start + per : n;
@@ -390,21 +345,11 @@ struct ReduceArgs {
     uint32_t begin, count, side;
     uint32_t max_groups, min_rows_per_group;
     uint32_t width;     // W
-    const Plan *plan;   // when non-null: out/parent are the plan's built/parent slots of `pool`
-    int64_t *pool;
-    uint64_t slot_stride;
 };
 
 __global__ void k_hist_reduce(ReduceArgs a) {
-    const uint32_t *dl;
-    uint32_t b0, c0, s0;
-    if (!hist_range(a.plan, a.dev_left, a.begin, a.count, a.side, dl, b0, c0, s0)) return;
-    if (a.plan) {
-        a.out = a.pool + (size_t)a.plan->built_slot * a.slot_stride;
-        a.parent = a.pool + (size_t)a.plan->parent_slot * a.slot_stride;
-    }
     uint32_t lb, n;
-    leaf_rows(dl, b0, c0, s0, lb, n);
+    leaf_rows(a.dev_left, a.begin, a.count, a.side, lb, n);
     uint32_t groups, per;
     hist_split(n, a.max_groups, a.min_rows_per_group, groups, per);
     uint32_t slots = 256u * a.width;
@@ -448,10 +393,6 @@ struct PartArgs {
     uint32_t bag_seed, bag_round;
     uint64_t row_offset;
     double fraction;
-    Plan *plan;            // when non-null: range, split column and mask from the plan; the left count goes there
-    const uint8_t *colbase;  // column-major bins of every feature ([feature][rows]) for the plan's column
-    uint64_t rows;
-    uint32_t *buf0, *buf1;   // the two partition buffers; the plan reads its leaf from one and writes the other
 };
 
 // Rows per block for `count` rows over the launch's blocks: a multiple of 256, the same in both passes.
@@ -459,20 +400,6 @@ __device__ __forceinline__ uint32_t part_per_block(uint32_t count, uint32_t bloc
     uint32_t per = (count + blocks - 1) / blocks;
     per = (per + 1023u) & ~1023u;
     return per < 1024u ? 1024u : per;
-}
-
-// Resolves the plan into the partition's range and predicate; false when the step does nothing.
-__device__ __forceinline__ bool part_resolve(PartArgs &a) {
-    if (!a.plan) return true;
-    if (!a.plan->active) return false;
-    a.begin = a.plan->begin;
-    a.count = a.plan->count;
-    a.src = a.plan->src_buf ? a.buf1 : a.buf0;
-    a.dst = a.plan->src_buf ? a.buf0 : a.buf1;
-    a.col = a.colbase + (size_t)a.plan->col * a.rows;
-    a.dev_left = &a.plan->left;
-    for (int i = 0; i < 8; ++i) a.left_bins[i] = a.plan->left_bins[i];
-    return true;
 }
 
 __device__ __forceinline__ bool part_left(const PartArgs &a, uint32_t row) {
@@ -487,7 +414,6 @@ __device__ __forceinline__ bool part_left(const PartArgs &a, uint32_t row) {
 // with every load of the tile issued before any is used (positions past the range are clamped and ignored).
 __global__ __launch_bounds__(256) void k_part_count(PartArgs a) {
     __shared__ uint32_t wsum[4];
-    if (!part_resolve(a)) return;
     const uint32_t per_block = part_per_block(a.count, gridDim.x);
     const uint32_t active = (a.count + per_block - 1) / per_block;
     if (blockIdx.x >= active && blockIdx.x > 0) return;
@@ -510,7 +436,6 @@ __global__ __launch_bounds__(256) void k_part_count(PartArgs a) {
 __global__ __launch_bounds__(256) void k_part_scatter(PartArgs a) {
     __shared__ uint32_t red[2][4];
     __shared__ uint32_t wl[4][4];  // [sub-tile][wave] left counts
-    if (!part_resolve(a)) return;
     const uint32_t per_block = part_per_block(a.count, gridDim.x);
     uint32_t active = (a.count + per_block - 1) / per_block;
     if (active == 0) active = 1;
@@ -587,13 +512,7 @@ __global__ __launch_bounds__(256) void k_part_scatter(PartArgs a) {
     }
 }
 
-__global__ void k_copy_u32(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, uint32_t begin, uint32_t n,
-                           const Plan *plan) {
-    if (plan) {
-        if (!plan->active) return;
-        begin = plan->begin;
-        n = plan->count;
-    }
+__global__ void k_copy_u32(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, uint32_t begin, uint32_t n) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         dst[begin + i] = src[begin + i];
 }
@@ -1012,14 +931,6 @@ struct ScanJob {
     FeatCand *out;        // [num_features]
 };
 
-// grid: (ceil(num_features / 4), num_jobs); 4 waves per block, a wave per feature.
-// The exact row count of job `j`: the job's own, or the plan's child counts (left, then right).
-__device__ __forceinline__ int64_t job_count(const ScanJob &job, const Plan *plan, uint32_t j) {
-    if (!plan) return job.count;
-    int64_t left = static_cast<int64_t>(plan->left);
-    return j == 0 ? left : plan->parent_count - left;
-}
-
 // split.rs:584-620 find_numerical, in two parts so that a feature's two scan directions can run on two waves.
 // Direction 0 is the reverse scan (split.rs:557-567: missing values go left); direction 1, only for a feature with
 // a NaN bin and more than two bins, the forward scan over the bins before the NaN bin (split.rs:571-580).
@@ -1385,16 +1296,16 @@ __device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const Fea
     return feature_candidate(c, m, rf, rg, ff, fg);
 }
 
+// grid: (ceil(num_features / 4), num_jobs); 4 waves per block, a wave per feature.
 __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
-                                                    SplitCfgDev cfg, double sg, double sh, const Plan *plan,
+                                                    SplitCfgDev cfg, double sg, double sh,
                                                     uint8_t *cat_order /* [feature][256] or null */) {
     __shared__ CatScratch cats[4];
-    if (plan && (!plan->active || !plan->may_search)) return;
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (f >= num_features) return;
-    Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job_count(job, plan, blockIdx.y));
+    Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job.count);
     FeatCand r = scan_feature(c, cfg, feats[f], job.hist, evaluate[f] != 0, cats[threadIdx.x >> 6],
                               cat_order ? cat_order + static_cast<size_t>(f) * 256 : nullptr);
     if ((threadIdx.x & 63) == 0) job.out[f] = r;
@@ -1500,9 +1411,17 @@ __global__ __launch_bounds__(256) void k_split_select(const ScanJob *__restrict_
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Device-driven growth (learner.rs:121-352): the leaf table, the tree arrays and the free list of histogram
-// slots live on the device; each split step is partition -> histogram of the built child -> reduce + subtract
-// -> split scan of both children -> k_apply, which updates the tree and the leaves and plans the next step.
+// Device-driven growth (learner.rs:121-352) with speculative expansion.
+//
+// The reference grows leaf-wise: each split takes the leaf with the highest best gain (learner.rs:418-429), and
+// a leaf's best split depends only on its own rows, its depth and its parent's splittable flags, never on when
+// the leaf is split. So one split step here expands several leaves at once: the leaf the reference splits next
+// (the blocker) and the highest-gain other leaves of the speculative tree. After each step, `advance` replays
+// the reference's order over the gains known so far: it commits expansions while the leaf the reference splits
+// next has been expanded (nodes and leaves get the reference's numbers), and plans the next step from the leaf
+// where it stopped. Expansions the order has not reached when the tree is complete are dropped: their rows are
+// merged back into ascending order (every leaf's rows are ascending, since the root's are and every partition
+// is stable).
 // ---------------------------------------------------------------------------------------------------------
 
 // learner.rs:432-452 bin_split: word w of the bins that go left; numerical: bins 0..=threshold and the NaN bin when
@@ -1516,7 +1435,46 @@ __device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_
     return word;
 }
 
-struct DLeaf {
+constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: two per thread of a 1024-thread block
+constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
+// A split step's partials: workgroup b of a slab owns step_partial_stride(W) {g, h} pairs from pair b * stride,
+// whether it writes 256 * W pairs or 256 * W packed words (a step can mix both). The stride is padded so that
+// the same slot of consecutive partials does not fall at a power-of-two distance (which maps it to the same
+// memory channel and bank).
+constexpr uint32_t STEP_PARTIAL_PAD = 288;
+__host__ __device__ constexpr size_t step_partial_stride(uint32_t w) { return 256u * static_cast<size_t>(w) + STEP_PARTIAL_PAD; }
+constexpr uint32_t ST_AGG = 1, ST_INCL = 2;   // tile status: its own left count / lefts up to and including it
+constexpr uint32_t LOOKBACK_SPINS = 1u << 20; // ~0.1 s of polling before a step gives up with an error
+
+// Bin chunks of a column group for `groups` partials, so that each thread adds at most 8 of them (one round of
+// loads) where it can: packed partials are added a bin (four columns) per thread, pairs a slot per thread.
+__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups, bool packed) {
+    if (packed) return groups <= 32 ? 1u : (groups <= 64 ? 2u : (groups <= 128 ? 4u : 8u));
+    return groups <= 8 ? 1u : (groups <= 16 ? 2u : (groups <= 32 ? 4u : 8u));
+}
+
+// Wave-wide sums of one value per lane: exclusive prefix and total.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(v, o);
+        if (lane >= static_cast<uint32_t>(o)) v += x;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_excl_sum(uint32_t v) { return wave_incl_sum(v) - v; }
+__device__ __forceinline__ uint32_t wave_total(uint32_t v) { return __shfl(wave_incl_sum(v), 63); }
+
+constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
+constexpr uint32_t SPEC_FLOOR = 4;         // speculative expansions a step may add whatever the budget
+constexpr uint32_t GROW_MAX_LEAVES = 512;  // num_leaves of a device-grown tree at most
+__host__ __device__ constexpr uint32_t grow_tcap(uint32_t num_leaves) { return 4 * num_leaves + 64; }
+constexpr uint32_t TCAP_MAX = 4 * GROW_MAX_LEAVES + 64;
+constexpr uint32_t T_LEAF = 0, T_PLANNED = 1, T_EXPANDED = 2;  // a speculative leaf's state
+
+// A leaf of the speculative tree: the committed leaves and the children of every expansion.
+struct TLeaf {
     uint32_t begin, count;   // rows in the partition
     double ug, uh;           // sums in histogram units
     int64_t cnt;             // exact row count
@@ -1525,17 +1483,19 @@ struct DLeaf {
     uint32_t buf;            // partition buffer holding the rows
     uint32_t rev;            // the rows are stored last-first (right children of a split step)
     int32_t depth;
-    int32_t parent;          // the internal node above, -1 for the root
-    uint32_t is_left;        // the leaf is its parent's left child
+    uint32_t state;          // T_LEAF, T_PLANNED (expanded by the running step), T_EXPANDED
+    int32_t kid;             // the children kid (left) and kid + 1 (right), once planned; -1 before
     uint32_t pad_;
-    double value, weight;    // the leaf's output and hessian weight in the tree
+    double value, weight;    // the leaf's output and hessian weight in the tree (from its parent's split)
     SplitOut best;
 };
 
-// A leaf's best gain for the choice of the next leaf to split (learner.rs:418-429); `has` is 0 without one.
-struct LeafKey {
-    double gain;
+// The part of a speculative leaf that advance reads for every leaf, kept apart for one coalesced load.
+struct TKey {
+    double gain;  // best gain, when `has`
     uint32_t has;
+    uint32_t state;
+    int32_t kid;
     uint32_t pad_;
 };
 
@@ -1553,97 +1513,96 @@ struct TreeDev {
     uint32_t *left_bins;  // [node][8]: the bins that go left (BinSplit::left_bins)
 };
 
-struct GrowCtl {
-    uint32_t num_leaves;     // the tree's leaves so far
-    uint32_t done;           // no further split this tree
-    uint32_t error;          // an invariant failed: 1 a child without rows, 3 a partition tile's look-back gave up
-    uint32_t pad0_;
-    double hist_rows;        // rows histogrammed (built children), and rows x evaluated features
-    double hist_bins;
-    double hist_builds;      // child histograms built
-    double part_rows;        // rows partitioned by the split steps
-    uint32_t epoch;          // split steps planned so far (kept across trees; tags tile status words)
-    uint32_t pad_;
+// One leaf expanded by a split step (learner.rs:249-290): written by advance, read by the step's kernels.
+struct JobPlan {
+    uint32_t t;                   // the speculative leaf expanded
+    uint32_t begin, count;        // its rows in the partition
+    uint32_t col;                 // column-major index of the split feature
+    uint32_t left_bins[8];
+    uint32_t built_side;          // 0: the left child is histogrammed, 1: the right (learner.rs:271-275)
+    uint32_t hist;                // the built child is histogrammed (learner.rs:266-268)
+    int32_t parent_slot, built_slot;
+    uint32_t src_buf, src_rev;    // the buffer holding the leaf's rows (its children go to the other) and order
+    uint32_t ntiles, tile_base;   // partition tiles and the first one's status word
+    uint32_t groups, group_base;  // k_step_rows workgroups, one partial each
+    uint32_t packed;              // the partials are packed 16/16 LDS words (one tile per workgroup)
+    uint32_t chunks;              // k_step_finish bin chunks per column group
+    uint32_t item_base, items;    // k_step_finish work items
+    uint32_t ticket;              // next partition tile to hand out
+    uint32_t left;                // rows going left, written by the last tile
+    int32_t kid;                  // the children's speculative leaves
+    int64_t parent_count;
+    double child_ug[2], child_uh[2];  // the children's sums in histogram units (left, right)
 };
 
-// Histogram slots: the root's is slot 0 and the child built by the step that creates leaf n goes to slot n, so
-// a tree of L leaves needs L slots and none is reused within a tree; the other child keeps its parent's slot.
+// A split step: the plan of step s is plans[s % 2], written by the step before it.
+struct StepPlan {
+    uint32_t njobs;
+    uint32_t total_groups;  // k_step_rows workgroups in use
+    uint32_t total_items;   // k_step_finish work items
+    uint32_t epoch;         // tags the step's tile status words
+    uint32_t item_ticket;   // next k_step_finish work item
+    uint32_t pad_[3];
+    JobPlan jobs[JMAX];
+};
+
+struct GrowCtl {
+    uint32_t num_leaves;   // committed leaves
+    uint32_t done;         // no further step this tree
+    uint32_t error;        // an invariant failed: 1 a child without rows, 3 a look-back gave up, 4 no room for a step
+    uint32_t ntent;        // speculative leaves in use
+    uint32_t next_slot;    // next free histogram slot
+    uint32_t pending;      // expanded leaves not yet committed
+    uint32_t epoch;        // split steps planned so far (kept across trees; tags tile status words)
+    uint32_t steps;        // split steps planned this tree
+    uint32_t expansions;   // leaves expanded this tree
+    uint32_t pad_;
+    uint32_t err_info[8];  // error 1: the job, its leaf, rows, left rows, tiles, workgroups, packed, jobs
+    double hist_rows;      // rows histogrammed (built children), and rows x evaluated features
+    double hist_bins;
+    double hist_builds;    // child histograms built
+    double part_rows;      // rows partitioned by the split steps
+};
+
+// Histogram slots: the root's is slot 0, each expansion that histograms takes the next free slot for its built
+// child, and the other child keeps its parent's slot (a slot is never reused within a tree).
 struct GrowState {
     GrowCtl *ctl;
-    Plan *plan;
-    DLeaf *leaves;
-    LeafKey *keys;           // [leaf]
-    uint8_t *splittable;     // [leaf][nf]
-    ScanJob *jobs;           // [1]: the root's search
-    FeatCand *cands;         // [2][nf]
-    uint8_t *evaluate;       // [nf]
-    const uint8_t *mask;     // [nf], the tree's feature mask
+    StepPlan *plans;          // [2]
+    TLeaf *tl;                // [tcap], 0 is the root
+    TKey *tk;                 // [tcap]
+    int32_t *leaf_t;          // [num_leaves]: each committed leaf's speculative leaf
+    uint8_t *leaf_left;       // [num_leaves]: the committed leaf is its parent's left child
+    uint8_t *splittable;      // [tcap][nf]
+    ScanJob *jobs;            // [1]: the root's search
+    FeatCand *cands;          // [JMAX][2][nf]
+    uint8_t *evaluate;        // [nf]: the root's evaluated features
+    const uint8_t *mask;      // [nf], the tree's feature mask
     const FeatDev *feats;
     TreeDev tree;
     int64_t *pool;
     uint64_t slot_stride;
     uint32_t nf, num_leaves, sums_feature;
+    uint32_t tcap, nslots;    // speculative leaves and histogram slots available
     int32_t max_depth;
     SplitCfgDev cfg;
     double sg, sh;
+    uint32_t target_groups;   // k_step_rows workgroups a step is spread over
+    uint32_t ncg;             // column groups of k_step_finish
+    uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
+    uint32_t pad_;
 };
 
 __device__ __forceinline__ bool depth_allows(const GrowState &g, int32_t d) { return g.max_depth <= 0 || d < g.max_depth; }
 
-// learner.rs:249-290 for leaf `next` (held in LDS by the caller): the step's plan, the evaluated features
-// (learner.rs:262-265: the tree's mask and the leaf's splittable flags) and the leaf's key cleared. `n` is
-// the tree's leaf count; the step will create leaf n. Block-wide.
-__device__ void plan_leaf(const GrowState &g, uint32_t next, const DLeaf &leaf, uint32_t n) {
-    __shared__ uint32_t used_w[16];
-    const uint32_t nw = blockDim.x >> 6;
-    const uint8_t *row = g.splittable + static_cast<size_t>(next) * g.nf;
-    uint32_t used = 0;
-    for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) {
-        uint8_t e = static_cast<uint8_t>(g.mask[f] && row[f]);
-        g.evaluate[f] = e;
-        used += e;  // a splittable feature has bins
-    }
-    for (int o = 32; o >= 1; o >>= 1) used += __shfl_xor(used, o);
-    if ((threadIdx.x & 63) == 0) used_w[threadIdx.x >> 6] = used;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const SplitOut &info = leaf.best;
-        Plan &p = *g.plan;
-        p.active = 1;
-        p.index = next;
-        p.begin = leaf.begin;
-        p.count = leaf.count;
-        p.parent_count = leaf.cnt;
-        p.src_buf = leaf.buf;
-        p.src_rev = leaf.rev;
-        p.epoch = ++g.ctl->epoch;
-        p.ticket = 0;
-        p.left = 0;
-        p.col = info.col;
-#pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) p.left_bins[w] = left_bins_word(info, w);
-        uint32_t used_all = 0;
-        for (uint32_t w = 0; w < nw; ++w) used_all += used_w[w];
-        p.used_columns = used_all;
-        p.built_side = info.left_count <= info.right_count ? 0u : 1u;
-        p.may_search = leaf.slot >= 0 && n + 1 < g.num_leaves && depth_allows(g, leaf.depth + 1);
-        p.parent_slot = leaf.slot;
-        p.built_slot = p.may_search ? static_cast<int32_t>(n) : -1;
-        p.child_ug[0] = info.left_grad;
-        p.child_uh[0] = info.left_hess;
-        p.child_ug[1] = info.right_grad;
-        p.child_uh[1] = info.right_hess;
-        g.keys[next].has = 0;
-        g.leaves[next].has_best = 0;
-    }
-    __syncthreads();
-}
+// Brings each listed run of rows into the first partition buffer in ascending order: copied from the second
+// buffer (reversed when stored last-first), or reversed in place. grid: (x, runs).
+struct RowRun {
+    uint32_t begin, count, buf, rev;
+};
 
-// Brings every leaf's rows into the first partition buffer in ascending order: copied from the second buffer
-// (reversed when stored last-first), or reversed in place. grid: (x, leaves).
-__global__ void k_consolidate(GrowState g, const uint32_t *__restrict__ buf1, uint32_t *__restrict__ buf0) {
-    if (blockIdx.y >= g.ctl->num_leaves) return;
-    const DLeaf &l = g.leaves[blockIdx.y];
+__global__ void k_consolidate(const RowRun *__restrict__ runs, const uint32_t *__restrict__ buf1, uint32_t *__restrict__ buf0) {
+    const RowRun l = runs[blockIdx.y];
     const uint32_t b = l.begin, n = l.count;
     const uint32_t stride = gridDim.x * blockDim.x;
     if (l.buf) {
@@ -1658,26 +1617,71 @@ __global__ void k_consolidate(GrowState g, const uint32_t *__restrict__ buf1, ui
     }
 }
 
+// A leaf whose expansion was dropped holds its rows as ascending runs (its speculative descendants' rows). Each
+// row's place in the leaf is its place in its run plus the rows below it in every other run (binary searches,
+// the rows of a leaf being distinct). Writes the merged leaf into the second buffer. grid: (x, leaves).
+struct MergeJob {
+    uint32_t begin, count;
+    uint32_t first, runs;  // the runs' starts (relative to begin) are starts[first, first + runs], then `count`
+};
+
+__global__ void k_merge_runs(const MergeJob *__restrict__ jobs, const uint32_t *__restrict__ starts,
+                             const uint32_t *__restrict__ buf0, uint32_t *__restrict__ buf1) {
+    const MergeJob m = jobs[blockIdx.y];
+    const uint32_t *s = starts + m.first;
+    const uint32_t *leaf = buf0 + m.begin;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < m.count; i += gridDim.x * blockDim.x) {
+        uint32_t p = 0;
+        while (p + 1 < m.runs && s[p + 1] <= i) ++p;
+        const uint32_t v = leaf[i];
+        uint32_t rank = i - s[p];
+        for (uint32_t q = 0; q < m.runs; ++q) {
+            if (q == p) continue;
+            uint32_t lo = s[q], hi = s[q + 1];  // rows of run q below v: the first position in it holding more
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (leaf[mid] < v) lo = mid + 1;
+                else hi = mid;
+            }
+            rank += lo - s[q];
+        }
+        buf1[m.begin + rank] = v;
+    }
+}
+
+__global__ void k_copy_back(const MergeJob *__restrict__ jobs, const uint32_t *__restrict__ buf1, uint32_t *__restrict__ buf0) {
+    const MergeJob m = jobs[blockIdx.y];
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < m.count; i += gridDim.x * blockDim.x)
+        buf0[m.begin + i] = buf1[m.begin + i];
+}
+
 // The tree at its start: one leaf holding the root rows, its histogram in slot 0 when it is searched.
 __global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_count, int64_t root_cnt, uint32_t searched) {
     if (threadIdx.x == 0) {
         GrowCtl &c = *g.ctl;
         c.num_leaves = 1;
-        c.done = 0;
+        c.done = searched ? 0u : 1u;
         c.error = 0;
+        c.ntent = 1;
+        c.next_slot = 1;
+        c.pending = 0;
+        c.steps = 0;
+        c.expansions = 0;
         c.hist_rows = 0.0;
         c.hist_bins = 0.0;
         c.hist_builds = 0.0;
         c.part_rows = 0.0;
-        g.plan->active = 0;
-        DLeaf l = {};
+        TLeaf l = {};
         l.begin = root_begin;
         l.count = root_count;
         l.cnt = root_cnt;
         l.slot = searched ? 0 : -1;
-        l.parent = -1;
-        g.leaves[0] = l;
-        g.keys[0] = LeafKey{0.0, 0u, 0u};
+        l.state = T_LEAF;
+        l.kid = -1;
+        g.tl[0] = l;
+        g.tk[0] = TKey{0.0, 0u, T_LEAF, -1, 0u};
+        g.leaf_t[0] = 0;
+        g.leaf_left[0] = 0;
         g.tree.leaf_value[0] = 0.0;
         g.tree.leaf_weight[0] = 0.0;
         g.tree.leaf_count[0] = 0;
@@ -1688,7 +1692,7 @@ __global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_coun
 
 // learner.rs:143-156: the root's sums from the sums feature's bins (split.rs:101-108), and its search job.
 __global__ void k_root_prep(GrowState g) {
-    const DLeaf &l = g.leaves[0];
+    const TLeaf &l = g.tl[0];
     const int64_t *h = g.pool + (size_t)l.slot * g.slot_stride;
     for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) g.evaluate[f] = g.mask[f];
     if (threadIdx.x == 0) {
@@ -1698,290 +1702,349 @@ __global__ void k_root_prep(GrowState g) {
             sg = sg + static_cast<double>(h[2 * ((size_t)m.hist_offset + b)]);
             sh = sh + static_cast<double>(h[2 * ((size_t)m.hist_offset + b) + 1]);
         }
-        g.leaves[0].ug = sg;
-        g.leaves[0].uh = sh;
+        g.tl[0].ug = sg;
+        g.tl[0].uh = sh;
         g.jobs[0] = ScanJob{h, sg, sh, l.cnt, g.cands};
     }
 }
 
-// The root's best split (learner.rs:157-163), then the first step's plan when the root splits (best_leaf over
-// the one leaf: a positive gain, learner.rs:418-429).
-__global__ __launch_bounds__(256) void k_root_select(GrowState g) {
-    ScanJob job = g.jobs[0];
-    __shared__ SplitOut o;
-    __shared__ DLeaf leaf;
-    select_split(job, job.count, g.nf, g.cfg, g.sg, g.sh, &o, g.splittable);
-    if (threadIdx.x == 0) {
-        leaf = g.leaves[0];
-        leaf.best = o;
-        leaf.has_best = o.found ? 1u : 0u;
-        g.leaves[0] = leaf;
-        g.keys[0] = LeafKey{o.gain, leaf.has_best, 0u};
-    }
-    __syncthreads();
-    bool go = o.found && o.gain > 0.0 && 1 < g.num_leaves;
-    if (!go) {
-        if (threadIdx.x == 0) g.ctl->done = 1;
-        return;
-    }
-    plan_leaf(g, 0, leaf, 1);
+// ---------------------------------------------------------------------------------------------------------
+// advance: the reference's order over the known gains, then the next step's plan. Block-wide (1024 threads);
+// `scratch` is LDS of at least sizeof(AdvShared) bytes.
+// ---------------------------------------------------------------------------------------------------------
+
+struct AdvShared {
+    double gain[TCAP_MAX];                // speculative leaves' best gains
+    uint32_t meta[TCAP_MAX];              // bit 0: has a best split; bits 1-2: state; bits 3..: kid + 1
+    uint16_t leaf_t[GROW_MAX_LEAVES];     // committed leaf -> speculative leaf, as the replay goes
+    int16_t pnode[GROW_MAX_LEAVES];       // committed leaf -> the internal node above it (-1: the root)
+    uint8_t is_left[GROW_MAX_LEAVES];     // committed leaf is its node's left child
+    uint8_t touched[GROW_MAX_LEAVES];     // committed leaf changed by this replay
+    uint16_t ck[GROW_MAX_LEAVES];         // commit c: the speculative leaf split (node n0 - 1 + c)
+    uint16_t cx[GROW_MAX_LEAVES];         // commit c: the leaf id split
+    int16_t cpn[GROW_MAX_LEAVES];         // commit c: the split leaf's node above
+    uint8_t cleft[GROW_MAX_LEAVES];       // commit c: the split leaf was its node's left child
+    uint16_t cand[TCAP_MAX];              // speculation candidates
+    uint16_t job_t[JMAX];
+    uint32_t ncand, ncommit, n, blocker, done, njobs;
+};
+
+__device__ __forceinline__ uint32_t key_meta(const TKey &k) {
+    return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
 }
 
-// The end of a split step, by one wave (learner.rs:294-352, then learner.rs:418-429 and 249-290): both children's
-// best splits from their per-feature candidates (split.rs:866-880), the planned split applied to the tree and the
-// leaf table (tree.rs:143-177), then the next leaf chosen and planned. Values every lane computes alike are kept
-// uniform; lane 0 writes the scalars.
-__device__ void finish_step(const GrowState &g) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const Plan &P = *g.plan;
-    GrowCtl *ctl = g.ctl;
-    const uint32_t n = ctl->num_leaves;  // leaves before the step; it creates leaf n
-    const uint32_t index = P.index;
-    const int64_t left = static_cast<int64_t>(P.left);
-    const int64_t right = P.parent_count - left;
-    const bool may_search = P.may_search != 0;
-    const DLeaf pl = g.leaves[index];
-    const SplitOut &info = pl.best;
-    // read up front: this lane's leaf keys (leaves lane + 64 j, j < 4) and mask flags (features lane + 64 k, k < 32)
-    LeafKey kp[4];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        const uint32_t i = lane + 64u * j;
-        kp[j] = i < n ? g.keys[i] : LeafKey{0.0, 0u, 0u};
-    }
-    uint32_t mbits = 0;
-    for (uint32_t k = 0, f = lane; k < 32 && f < g.nf; ++k, f += 64u) mbits |= (g.mask[f] != 0 ? 1u : 0u) << k;
-    uint32_t sbits[2] = {0u, 0u};  // the children's splittable flags for the same features
+// LDS writes of one lane made visible to the rest of its wave.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-    // -- both children's best splits (every lane holds features lane, lane + 64, ...)
-    SplitOut out[2] = {};
-    if (may_search) {
-#pragma unroll
-        for (uint32_t ch = 0; ch < 2; ++ch) {
-            const FeatCand *cands = g.cands + static_cast<size_t>(ch) * g.nf;
-            uint8_t *row = g.splittable + static_cast<size_t>(ch == 0 ? index : n) * g.nf;
-            double best = 0.0;
-            int bf = -1;
-            FeatCand bc = {};
-            for (uint32_t k = 0, f = lane; f < g.nf; ++k, f += 64u) {
-                FeatCand c = cands[f];
-                row[f] = static_cast<uint8_t>(c.splittable);
-                if (k < 32) sbits[ch] |= (c.splittable ? 1u : 0u) << k;
-                if (!c.found) continue;
-                double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
-                if (cand_better(gv, static_cast<int>(f), best, bf)) {
-                    best = gv;
-                    bf = static_cast<int>(f);
-                    bc = c;
+__device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
+    AdvShared &s = *reinterpret_cast<AdvShared *>(scratch);
+    GrowCtl *ctl = g.ctl;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, nt = blockDim.x;
+    if (ctl->done) return;
+    const uint32_t n0 = ctl->num_leaves, ntent = ctl->ntent, L = g.num_leaves;
+    const uint32_t pending0 = ctl->pending, slot0 = ctl->next_slot, epoch0 = ctl->epoch;
+    const uint32_t expansions0 = ctl->expansions, steps0 = ctl->steps;
+    __syncthreads();  // every thread has read the control block before thread 0 updates it
+    for (uint32_t k = tid; k < ntent; k += nt) {
+        const TKey key = g.tk[k];
+        s.gain[k] = key.gain;
+        s.meta[k] = key_meta(key);
+    }
+    for (uint32_t id = tid; id < n0; id += nt) {
+        s.leaf_t[id] = static_cast<uint16_t>(g.leaf_t[id]);
+        s.pnode[id] = static_cast<int16_t>(g.tree.leaf_parent[id]);
+        s.is_left[id] = g.leaf_left[id];
+        s.touched[id] = 0;
+    }
+    if (tid == 0) s.ncand = 0;
+    __syncthreads();
+
+    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave
+    if (tid < 64) {
+        uint32_t n = n0, nc = 0, blocker = 0;
+        bool done = false;
+        for (;;) {
+            if (n >= L) {
+                done = true;
+                break;
+            }
+            // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
+            // otherwise the first highest gain among the rest (a NaN later never wins); `first` is 2 * leaf + NaN
+            int first = 1 << 30;
+            double kg = 0.0;
+            int ki = -1;
+            for (uint32_t id = lane; id < n; id += 64u) {
+                const uint32_t k = s.leaf_t[id];
+                if (!(s.meta[k] & 1u)) continue;
+                const double gk = s.gain[k];
+                const bool nan = gk != gk;
+                const int code = 2 * static_cast<int>(id) + (nan ? 1 : 0);
+                if (code < first) first = code;
+                if (nan) continue;
+                if (cand_better(gk, static_cast<int>(id), kg, ki)) {
+                    kg = gk;
+                    ki = static_cast<int>(id);
                 }
             }
-            double wb = best;
-            int wf = bf;
-            wave_best(wb, wf);
-            if (wf >= 0) {
-                const FeatCand c = readlane_cand(bc, static_cast<uint32_t>(wf) & 63u);
-                const int64_t cnt = ch == 0 ? left : right;
-                out[ch] = split_out(c, wf, make_ctx(g.cfg, g.sg, g.sh, P.child_ug[ch], P.child_uh[ch], cnt), g.cfg);
+            first = wave_min(first);
+            wave_best(kg, ki);
+            const bool nan_first = first < (1 << 30) && (first & 1);
+            if (nan_first || ki < 0 || !(kg > 0.0)) {
+                done = true;
+                break;
             }
+            const uint32_t x = static_cast<uint32_t>(ki);
+            const uint32_t k = s.leaf_t[x];
+            const uint32_t m = s.meta[k];
+            if (((m >> 1) & 3u) != T_EXPANDED) {
+                blocker = k;
+                break;
+            }
+            const uint32_t kid = (m >> 3) - 1u;
+            if (lane == 0) {
+                const int16_t node = static_cast<int16_t>(n - 1);
+                s.ck[nc] = static_cast<uint16_t>(k);
+                s.cx[nc] = static_cast<uint16_t>(x);
+                s.cpn[nc] = s.pnode[x];
+                s.cleft[nc] = s.is_left[x];
+                s.leaf_t[x] = static_cast<uint16_t>(kid);
+                s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
+                s.pnode[x] = node;
+                s.pnode[n] = node;
+                s.is_left[x] = 1;
+                s.is_left[n] = 0;
+                s.touched[x] = 1;
+                s.touched[n] = 1;
+            }
+            wave_lds_sync();
+            ++nc;
+            ++n;
         }
-    }
-
-    // -- apply the split (tree.rs:143-177) and set up the children (learner.rs:294-352)
-    const bool ok = left > 0 && right > 0;
-    if (!ok) {
         if (lane == 0) {
-            ctl->error = 1;
-            g.plan->active = 0;
-            ctl->done = 1;
+            s.ncommit = nc;
+            s.n = n;
+            s.done = done ? 1u : 0u;
+            s.blocker = blocker;
         }
-        return;
     }
-    const int32_t node = static_cast<int32_t>(n) - 1;
-    const int32_t depth = pl.depth + 1;
-    DLeaf l = {}, r = {};
-    l.begin = P.begin;
-    l.count = P.left;
-    r.begin = P.begin + P.left;
-    r.count = P.count - P.left;
-    l.ug = info.left_grad;
-    l.uh = info.left_hess;
-    r.ug = info.right_grad;
-    r.uh = info.right_hess;
-    l.cnt = left;
-    r.cnt = right;
-    l.buf = r.buf = 1u - P.src_buf;
-    l.rev = 0;  // the split step writes the left child first-first and the right child last-first
-    r.rev = 1;
-    l.depth = r.depth = depth;
-    l.parent = r.parent = node;
-    l.is_left = 1;
-    r.is_left = 0;
-    const double lv = info.left_output, rv = info.right_output;
-    l.value = lv != lv ? 0.0 : lv;
-    r.value = rv != rv ? 0.0 : rv;
-    l.weight = info.left_hess * g.sh;
-    r.weight = info.right_hess * g.sh;
-    const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
-    const bool searched = may_search && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
-    l.slot = r.slot = -1;
-    if (searched) {
-        l.slot = P.built_side == 0 ? P.built_slot : P.parent_slot;
-        r.slot = P.built_side == 0 ? P.parent_slot : P.built_slot;
-        l.best = out[0];
-        r.best = out[1];
-        l.has_best = out[0].found ? 1u : 0u;
-        r.has_best = out[1].found ? 1u : 0u;
-    }
-    if (lane == 0) {
-        const TreeDev &t = g.tree;
-        if (pl.parent >= 0) {
-            if (pl.is_left) t.left_child[pl.parent] = node;
-            else t.right_child[pl.parent] = node;
-        }
+    __syncthreads();
+    const uint32_t nc = s.ncommit, n = s.n;
+    const bool done = s.done != 0;
+
+    // -- the commits applied to the tree (tree.rs:143-177): nodes, then the links into nodes split again
+    const TreeDev &t = g.tree;
+    for (uint32_t c = tid; c < nc; c += nt) {
+        const TLeaf &p = g.tl[s.ck[c]];
+        const SplitOut &info = p.best;
+        const uint32_t node = n0 - 1 + c;
         t.split_feature[node] = info.feature;
 #pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = P.left_bins[w];
+        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = left_bins_word(info, w);
         t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
         t.threshold_bin[node] = info.threshold;
         t.default_left[node] = static_cast<uint8_t>(info.default_left);
-        t.left_child[node] = ~static_cast<int32_t>(index);
-        t.right_child[node] = ~static_cast<int32_t>(n);
-        t.internal_weight[node] = pl.weight;
-        t.internal_value[node] = pl.value;
-        t.internal_count[node] = left + right;
-        t.leaf_value[index] = l.value;
-        t.leaf_weight[index] = l.weight;
-        t.leaf_count[index] = left;
-        t.leaf_value[n] = r.value;
-        t.leaf_weight[n] = r.weight;
-        t.leaf_count[n] = right;
-        t.leaf_parent[index] = node;
-        t.leaf_parent[n] = node;
-        t.leaf_depth[index] = depth;
-        t.leaf_depth[n] = depth;
-        if (may_search) {  // the built child's histogram was made, searched or not
-            double built_rows = P.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
-            ctl->hist_rows += built_rows;
-            ctl->hist_bins += built_rows * static_cast<double>(P.used_columns);
-            ctl->hist_builds += 1.0;
-        }
-        ctl->part_rows += static_cast<double>(P.count);
-        ctl->num_leaves = n + 1;
-        g.leaves[index] = l;
-        g.leaves[n] = r;
-        g.keys[index] = LeafKey{l.best.gain, l.has_best, 0u};
-        g.keys[n] = LeafKey{r.best.gain, r.has_best, 0u};
+        t.left_child[node] = ~static_cast<int32_t>(s.cx[c]);
+        t.right_child[node] = ~static_cast<int32_t>(n0 + c);
+        t.internal_weight[node] = p.weight;
+        t.internal_value[node] = p.value;
+        t.internal_count[node] = p.cnt;
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (uint32_t c = tid; c < nc; c += nt) {
+        const int32_t pn = s.cpn[c];
+        if (pn < 0) continue;
+        if (s.cleft[c]) t.left_child[pn] = static_cast<int32_t>(n0 - 1 + c);
+        else t.right_child[pn] = static_cast<int32_t>(n0 - 1 + c);
+    }
+    for (uint32_t id = tid; id < n; id += nt) {
+        if (!s.touched[id]) continue;
+        const uint32_t k = s.leaf_t[id];
+        const TLeaf &l = g.tl[k];
+        t.leaf_value[id] = l.value;
+        t.leaf_weight[id] = l.weight;
+        t.leaf_count[id] = l.cnt;
+        t.leaf_parent[id] = s.pnode[id];
+        t.leaf_depth[id] = l.depth;
+        g.leaf_t[id] = static_cast<int32_t>(k);
+        g.leaf_left[id] = s.is_left[id];
+    }
+    if (tid == 0) {
+        ctl->num_leaves = n;
+        ctl->pending = pending0 - nc;
+        if (done) ctl->done = 1;
+    }
+    if (done) return;
 
-    // -- best_leaf (learner.rs:418-429) over leaves 0..=n, the children's keys replacing the split leaf's and
-    // adding leaf n: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
-    // otherwise the first highest gain among the rest (a NaN later never wins). `first` is 2 * leaf + (NaN).
-    int first = 1 << 30;
-    double kg = 0.0;
-    int ki = -1;
-    auto consider = [&](uint32_t i, LeafKey k) {
-        if (i == index) k = LeafKey{l.best.gain, l.has_best, 0u};
-        else if (i == n) k = LeafKey{r.best.gain, r.has_best, 0u};
-        if (!k.has) return;
-        const bool nan = k.gain != k.gain;
-        const int code = 2 * static_cast<int>(i) + (nan ? 1 : 0);
-        if (code < first) first = code;
-        if (nan) return;
-        if (cand_better(k.gain, static_cast<int>(i), kg, ki)) {
-            kg = k.gain;
-            ki = static_cast<int>(i);
+    // -- speculation candidates: unexpanded leaves with a positive gain, the blocker aside
+    const uint32_t blocker = s.blocker;
+    for (uint32_t k = tid; k < ntent; k += nt) {
+        const uint32_t m = s.meta[k];
+        const double gk = s.gain[k];
+        if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && gk > 0.0 && k != blocker) {
+            const uint32_t at = atomicAdd(&s.ncand, 1u);
+            s.cand[at] = static_cast<uint16_t>(k);
         }
-    };
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
-        if (lane + 64u * j <= n) consider(lane + 64u * j, kp[j]);
-    for (uint32_t i = lane + 256u; i <= n; i += 64u) consider(i, g.keys[i]);
-    first = wave_min(first);
-    wave_best(kg, ki);
-    const bool nan_first = first < (1 << 30) && (first & 1);
-    const bool go = !ctl->done && n + 1 < g.num_leaves && !nan_first && ki >= 0 && kg > 0.0;
-    if (!go) {
-        if (lane == 0) {
-            g.plan->active = 0;
+    }
+    __syncthreads();
+    const uint32_t ncand = s.ncand;
+    const uint32_t R = L - n;  // splits left, this step's blocker included
+    const uint32_t pending = pending0 - nc;
+    uint32_t spec = R > pending + 1u + SPEC_FLOOR ? R - pending - 1u : SPEC_FLOOR;
+    if (spec > JMAX - 1) spec = JMAX - 1;
+    // room for this step and every later blocker (each commits, so at most R of them in all)
+    const uint32_t free_t = g.tcap - ntent, free_s = g.nslots - slot0;
+    const uint32_t room_t = free_t >= 2 * R ? (free_t - 2 * R) / 2 : 0u, room_s = free_s >= R ? free_s - R : 0u;
+    if (spec > room_t) spec = room_t;
+    if (spec > room_s) spec = room_s;
+    if (spec > ncand) spec = ncand;
+    // the spec highest gains (ties to the lower leaf); the blocker is job 0
+    for (uint32_t i = tid; i < ncand; i += nt) {
+        const uint32_t ki = s.cand[i];
+        const double gi = s.gain[ki];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ncand; ++j) {
+            const uint32_t kj = s.cand[j];
+            const double gj = s.gain[kj];
+            rank += (gj > gi || (gj == gi && kj < ki)) ? 1u : 0u;
+        }
+        if (rank < spec) s.job_t[1 + rank] = static_cast<uint16_t>(ki);
+    }
+    if (tid == 0) {
+        s.job_t[0] = static_cast<uint16_t>(blocker);
+        s.njobs = 1 + spec;
+    }
+    __syncthreads();
+    const uint32_t njobs = s.njobs;
+    if (free_t < 2 || free_s < 1) {  // no room even for the blocker: the sizes above make this unreachable
+        if (tid == 0) {
+            ctl->error = 4;
             ctl->done = 1;
         }
         return;
     }
-    const uint32_t next = static_cast<uint32_t>(ki);
-    const DLeaf nl = next == index ? l : (next == n ? r : g.leaves[next]);
 
-    // -- plan the next step (learner.rs:249-290): evaluated features (the tree's mask and the leaf's splittable
-    // flags, learner.rs:262-265; the flags of a new child were written by this lane above)
-    const uint8_t *row = g.splittable + static_cast<size_t>(next) * g.nf;
-    const bool child_next = searched && (next == index || next == n);
-    const uint32_t cbits = next == index ? sbits[0] : sbits[1];
-    uint32_t used = 0;
-    for (uint32_t k = 0, f = lane; f < g.nf; ++k, f += 64u) {
-        const bool m = k < 32 ? ((mbits >> k) & 1u) : (g.mask[f] != 0);
-        const bool sp = (k < 32 && child_next) ? ((cbits >> k) & 1u) : (row[f] != 0);
-        const bool e = m && sp;
-        g.evaluate[f] = static_cast<uint8_t>(e);
-        used += static_cast<uint32_t>(__popcll(__ballot(e)));
-    }
-    if (lane == 0) {
-        const SplitOut &ni = nl.best;
-        const uint32_t nn = n + 1;  // the tree's leaves after this step; the next step creates leaf nn
-        Plan &p = *g.plan;
-        p.active = 1;
-        p.index = next;
-        p.begin = nl.begin;
-        p.count = nl.count;
-        p.parent_count = nl.cnt;
-        p.src_buf = nl.buf;
-        p.src_rev = nl.rev;
-        p.epoch = ctl->epoch + 1;
-        ctl->epoch = ctl->epoch + 1;
-        p.ticket = 0;
-        p.left = 0;
-        p.col = ni.col;
+    // -- the jobs (learner.rs:249-290), one lane each; then prefix sums over the jobs on the same wave
+    if (tid < 64) {
+        const bool on = lane < njobs;
+        JobPlan J = {};
+        uint32_t hist = 0, ntiles = 0;
+        if (on) {
+            const uint32_t tt = s.job_t[lane];
+            const TLeaf &l = g.tl[tt];
+            const SplitOut &info = l.best;
+            J.t = tt;
+            J.begin = l.begin;
+            J.count = l.count;
+            J.col = info.col;
 #pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) p.left_bins[w] = left_bins_word(ni, w);
-        p.used_columns = used;
-        p.built_side = ni.left_count <= ni.right_count ? 0u : 1u;
-        p.may_search = nl.slot >= 0 && nn + 1 < g.num_leaves && depth_allows(g, nl.depth + 1);
-        p.parent_slot = nl.slot;
-        p.built_slot = p.may_search ? static_cast<int32_t>(nn) : -1;
-        p.child_ug[0] = ni.left_grad;
-        p.child_uh[0] = ni.left_hess;
-        p.child_ug[1] = ni.right_grad;
-        p.child_uh[1] = ni.right_hess;
-        g.keys[next].has = 0;
-        g.leaves[next].has_best = 0;
+            for (uint32_t w = 0; w < 8; ++w) J.left_bins[w] = left_bins_word(info, w);
+            J.built_side = info.left_count <= info.right_count ? 0u : 1u;
+            hist = (l.slot >= 0 && depth_allows(g, l.depth + 1)) ? 1u : 0u;
+            J.hist = hist;
+            J.parent_slot = l.slot;
+            J.src_buf = l.buf;
+            J.src_rev = l.rev;
+            ntiles = (l.count + STEP_TILE - 1) / STEP_TILE;
+            J.ntiles = ntiles;
+            J.parent_count = l.cnt;
+            J.child_ug[0] = info.left_grad;
+            J.child_uh[0] = info.left_hess;
+            J.child_ug[1] = info.right_grad;
+            J.child_uh[1] = info.right_hess;
+            J.kid = static_cast<int32_t>(ntent + 2 * lane);
+        }
+        // exclusive prefixes over lanes 0..njobs-1 (one wave)
+        const uint32_t hist_before = wave_excl_sum(hist);
+        const uint32_t tiles_before = wave_excl_sum(ntiles);
+        const uint32_t total_tiles = wave_total(ntiles);
+        uint32_t groups = 0;
+        if (on) {
+            uint64_t want = total_tiles ? static_cast<uint64_t>(ntiles) * g.target_groups / total_tiles : 1u;
+            groups = static_cast<uint32_t>(want < 1 ? 1 : (want > ntiles ? ntiles : want));
+            if (groups == 0) groups = 1;
+        }
+        const uint32_t groups_before = wave_excl_sum(groups);
+        const uint32_t total_groups = wave_total(groups);
+        uint32_t items = 0;
+        if (on) {
+            J.tile_base = tiles_before;
+            J.groups = groups;
+            J.group_base = groups_before;
+            J.packed = (ntiles <= groups && g.flush_rows >= STEP_TILE) ? 1u : 0u;
+            J.chunks = hist ? finish_chunks(groups, J.packed != 0) : 0u;
+            items = hist ? g.ncg * J.chunks : 1u;
+            J.items = items;
+            J.built_slot = hist ? static_cast<int32_t>(slot0 + hist_before) : -1;
+        }
+        const uint32_t items_before = wave_excl_sum(items);
+        const uint32_t total_items = wave_total(items);
+        const uint32_t nhist = wave_total(hist);
+        if (on) {
+            J.item_base = items_before;
+            J.ticket = 0;
+            J.left = 0;
+            next.jobs[lane] = J;
+            g.tl[J.t].state = T_PLANNED;
+            g.tl[J.t].kid = J.kid;
+            g.tk[J.t].state = T_PLANNED;
+            g.tk[J.t].kid = J.kid;
+        }
+        if (lane == 0) {
+            next.njobs = njobs;
+            next.total_groups = total_groups;
+            next.total_items = total_items;
+            next.epoch = epoch0 + 1;
+            next.item_ticket = 0;
+            ctl->epoch = epoch0 + 1;
+            ctl->ntent = ntent + 2 * njobs;
+            ctl->next_slot = slot0 + nhist;
+            ctl->pending = pending + njobs;
+            ctl->expansions = expansions0 + njobs;
+            ctl->steps = steps0 + 1;
+        }
     }
 }
 
-// ---------------------------------------------------------------------------------------------------------
-// A split step in two kernels (learner.rs:249-352 for the leaf the previous step planned).
-//
-// k_step_rows: the stable partition of the leaf's rows by the planned BinSplit (cpu.rs:556-599) in one pass,
-// fused with the built child's histogram. Tiles of STEP_TILE rows are handed out in order; a tile's left
-// count is published at once, its offset comes from a look-back over the earlier tiles' status words (no
-// second pass over the rows), its rows are scattered, then its rows of the built child (kept in LDS) are
-// histogrammed as k_hist does. Left rows are
-// written first-first from the range's start, right rows last-first from its end, so both children are
-// stable; a leaf stored last-first is read back to front by the next step and by k_consolidate. Launches for
-// a second or later slab only histogram.
-//
-// k_step_finish: adds the partials of the built child (a block per 8 columns and bin chunk), forms the sibling
-// by subtraction (learner.rs:356-371), scans the two children's features (the last chunk block of each column
-// group, a wave per feature and child), then the last column group selects both children's splits, applies
-// the step and plans the next (finish_step). Hand-offs are counters that the last arriving block resets; no
-// block ever waits for another in k_step_finish.
-// ---------------------------------------------------------------------------------------------------------
+// The root's best split (learner.rs:157-163), then the first step's plan. One block of 1024 threads.
+__global__ __launch_bounds__(1024) void k_root_select(GrowState g) {
+    __shared__ SplitOut o;
+    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
+    ScanJob job = g.jobs[0];
+    select_split(job, job.count, g.nf, g.cfg, g.sg, g.sh, &o, g.splittable);
+    if (threadIdx.x == 0) {
+        g.tl[0].best = o;
+        g.tl[0].has_best = o.found ? 1u : 0u;
+        g.tk[0].gain = o.gain;
+        g.tk[0].has = o.found ? 1u : 0u;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __threadfence();
+    advance(g, g.plans[0], scratch);
+}
 
-constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: two per thread of a 1024-thread block
-constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
-// A split step's partials are 256 * W {g, h} pairs per workgroup, padded so that the same slot of consecutive
-// partials does not fall at a power-of-two distance (which maps it to the same memory channel and bank).
-constexpr uint32_t STEP_PARTIAL_PAD = 288;
-__host__ __device__ constexpr size_t step_partial_stride(uint32_t w) { return 256u * static_cast<size_t>(w) + STEP_PARTIAL_PAD; }
-constexpr uint32_t ST_AGG = 1, ST_INCL = 2;   // tile status: its own left count / lefts up to and including it
-constexpr uint32_t LOOKBACK_SPINS = 1u << 20; // ~0.1 s of polling before a step gives up with an error
+// ---------------------------------------------------------------------------------------------------------
+// A split step in two kernels: every job of the step's plan (learner.rs:249-352 for each leaf it expands).
+//
+// k_step_rows: the stable partition of each job's rows by its BinSplit (cpu.rs:556-599) in one pass, fused with
+// its built child's histogram. A job's workgroups take its tiles of STEP_TILE rows in order; a tile's left
+// count is published at once, its offset comes from a look-back over the job's earlier tiles (no second pass
+// over the rows), its rows are scattered, then its rows of the built child (kept in LDS) are histogrammed as
+// k_hist does. Left rows are written first-first from the range's start, right rows last-first from its end, so
+// both children are stable; a leaf stored last-first is read back to front by the step that expands it and by
+// k_consolidate. Launches for a second or later slab only histogram.
+//
+// k_step_finish: work items (job, column group, bin chunk) handed out in order: each adds the job's partials of
+// its bins, writes the built child's histogram and forms the sibling by subtraction (learner.rs:356-371); the
+// last item of a column group scans its features for both children; the last group of a job selects both
+// children's splits (job_select); the last job runs advance. Hand-offs are counters that the last arriving
+// block resets; no block ever waits for another in k_step_finish.
+// ---------------------------------------------------------------------------------------------------------
 
 struct StepArgs {
     const uint8_t *bins;         // slab rows: row r at bins + r * W
@@ -1989,28 +2052,14 @@ struct StepArgs {
     const uint8_t *colbase;      // column-major bins [feature][rows]
     uint64_t rows;
     uint32_t *buf0, *buf1;       // the partition buffers
-    int32_t *partial;            // this slab's partials, step_partial_stride(W) elements apart (see step_packed)
+    int32_t *partial;            // this slab's partials, step_partial_stride(W) pairs apart, one per workgroup
     const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
     unsigned long long *status;  // per-tile status words
-    Plan *plan;
+    StepPlan *plan;              // this step's plan
     GrowCtl *ctl;
     uint32_t flush_rows;
-    uint32_t max_groups;         // == gridDim.x
     uint32_t partition;          // 1: this launch partitions (the first slab's); 0: histogram only
 };
-
-// Whether a step's partials are the packed 16/16 LDS words (one i32 per slot): when every workgroup takes a
-// single tile (so its sums never outgrow 16 bits); otherwise {g, h} i32 pairs. The same in both kernels.
-// Packed partials are column-group major ([group][256 bins][4 columns]) so that a group's bins are contiguous;
-// pair partials are slot major ([bin][W columns]).
-__device__ __forceinline__ bool step_packed(uint32_t count, uint32_t max_groups, uint32_t flush_rows) {
-    return (count + STEP_TILE - 1) / STEP_TILE <= max_groups && flush_rows >= STEP_TILE;
-}
-
-__device__ __forceinline__ uint32_t step_groups(uint32_t count, uint32_t max_groups) {
-    uint32_t tiles = (count + STEP_TILE - 1) / STEP_TILE;
-    return tiles < max_groups ? tiles : max_groups;
-}
 
 __device__ __forceinline__ unsigned long long status_word(uint32_t epoch, uint32_t flag, uint32_t value) {
     return (static_cast<unsigned long long>(((epoch & 0x3fffffffu) << 2) | flag) << 32) | value;
@@ -2069,9 +2118,10 @@ __device__ __forceinline__ void unpack_slots(int32_t *lds, uint32_t tid, int32_t
     __syncthreads();
 }
 
-// The step's plan as one workgroup of k_step_rows sees it.
+// A job of the step as one workgroup of k_step_rows sees it.
 struct StepView {
-    Plan *plan;
+    JobPlan *job;
+    unsigned long long *status;  // the job's tile status words
     uint32_t begin, count, ntiles, groups;
     const uint32_t *src;
     uint32_t *dst;
@@ -2132,7 +2182,7 @@ __device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs 
     const uint32_t tile_left = sub0 + sub1;
     uint32_t lrank[2] = {before0 + below[0], sub0 + before1 + below[1]};
     if (v.partition && tid == 0)
-        __hip_atomic_store(a.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
+        __hip_atomic_store(v.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     if (v.hist) {  // the tile's rows of the built child, in order
 #pragma unroll
@@ -2143,13 +2193,13 @@ __device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs 
     }
     if (v.partition) {
         if (wave == 0) {
-            uint32_t prefix = t == 0 ? 0u : lookback(a.status, t, v.epoch, a.ctl);
+            uint32_t prefix = t == 0 ? 0u : lookback(v.status, t, v.epoch, a.ctl);
             if (lane == 0) {
                 if (t > 0)
-                    __hip_atomic_store(a.status + t, status_word(v.epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
+                    __hip_atomic_store(v.status + t, status_word(v.epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 sh.prefix = prefix;
-                if (t == v.ntiles - 1) v.plan->left = prefix + tile_left;
+                if (t == v.ntiles - 1) v.job->left = prefix + tile_left;
             }
         }
         __syncthreads();
@@ -2217,27 +2267,33 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     __shared__ int32_t lds[256 * W];
     __shared__ StepShared sh;
 
-    Plan *plan = a.plan;
-    if (!plan->active) return;
+    if (a.ctl->done) return;
+    StepPlan &P = *a.plan;
+    if (blockIdx.x >= P.total_groups) return;
+    uint32_t j = 0;  // the workgroup's job: the last whose first workgroup is at or below it
+    for (uint32_t k = 1; k < P.njobs; ++k)
+        if (blockIdx.x >= P.jobs[k].group_base) j = k;
+    JobPlan &J = P.jobs[j];
     StepView v;
-    v.plan = plan;
-    v.hist = plan->may_search != 0;
+    v.job = &J;
+    v.hist = J.hist != 0;
     v.partition = a.partition != 0;
     if (!v.hist && !v.partition) return;
-    v.begin = plan->begin;
-    v.count = plan->count;
-    v.ntiles = (v.count + STEP_TILE - 1) / STEP_TILE;
-    v.groups = step_groups(v.count, a.max_groups);
-    if (blockIdx.x >= v.groups) return;
-    const bool packed = step_packed(v.count, a.max_groups, a.flush_rows);  // then one tile per workgroup
-    v.src = plan->src_buf ? a.buf1 : a.buf0;
-    v.dst = plan->src_buf ? a.buf0 : a.buf1;
-    v.rev = plan->src_rev != 0;
-    v.col = a.colbase + static_cast<size_t>(plan->col) * a.rows;
-    v.built_left = plan->built_side == 0 ? 1u : 0u;
-    v.epoch = plan->epoch;
+    v.status = a.status + J.tile_base;
+    v.begin = J.begin;
+    v.count = J.count;
+    v.ntiles = J.ntiles;
+    v.groups = J.groups;
+    const uint32_t gi = blockIdx.x - J.group_base;  // the workgroup within its job
+    const bool packed = J.packed != 0;  // then one tile per workgroup
+    v.src = J.src_buf ? a.buf1 : a.buf0;
+    v.dst = J.src_buf ? a.buf0 : a.buf1;
+    v.rev = J.src_rev != 0;
+    v.col = a.colbase + static_cast<size_t>(J.col) * a.rows;
+    v.built_left = J.built_side == 0 ? 1u : 0u;
+    v.epoch = P.epoch;
     const uint32_t tid = threadIdx.x;
-    if (tid < 8) sh.left_bins[tid] = plan->left_bins[tid];  // visible after the first barrier below
+    if (tid < 8) sh.left_bins[tid] = J.left_bins[tid];  // visible after the first barrier below
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     if (v.hist)
         for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
@@ -2248,13 +2304,13 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         // quad of lanes (the group's 4 columns) leaves lane c % 4 with bin 4q + c % 4 of all four columns, so the
         // quad stores 64 contiguous bytes
         __syncthreads();
-        if (tid == 0) sh.tile = v.partition ? atomicAdd(&plan->ticket, 1u) : blockIdx.x;
+        if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
         __syncthreads();
         const uint32_t nb = step_tile(v, a, sh.tile, sh);
         if (!v.hist) return;
         hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         __syncthreads();
-        int4 *out = reinterpret_cast<int4 *>(a.partial + static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
+        int4 *out = reinterpret_cast<int4 *>(a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
         const uint32_t c4 = tid & 3u;
 #pragma unroll
         for (int it = 0; it < SLOTS / 4; ++it) {
@@ -2293,10 +2349,10 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
     uint32_t pending = 0;  // rows added to the packed LDS words since they were last unpacked
-    uint32_t next = blockIdx.x;  // histogram-only launches take tiles blockIdx.x, + groups, ...
+    uint32_t next = gi;  // histogram-only launches take tiles gi, gi + groups, ...
     for (;;) {
         __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
-        if (tid == 0) sh.tile = v.partition ? atomicAdd(&plan->ticket, 1u) : next;
+        if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : next;
         __syncthreads();
         const uint32_t t = sh.tile;
         next += v.groups;
@@ -2336,19 +2392,6 @@ struct ColGroup {
     uint32_t bins[4];    // per column: the feature's bins (0 for padding)
 };
 
-constexpr uint32_t FIN_CHUNKS = 8;  // gridDim.y of k_step_finish: bin chunks per column group at most
-
-struct FinishArgs {
-    const int32_t *partial;     // the step partial buffer
-    const ColGroup *cgs;        // [ncg]
-    const int32_t *col_feat;    // per global column: the feature, -1 for padding
-    uint32_t *cg_count;         // [ncg] chunk blocks done; returned to 0 by the last one
-    uint32_t *done_count;       // column groups done; returned to 0 by the last one
-    uint32_t ncg;
-    uint32_t max_groups;        // k_step_rows' grid
-    uint32_t flush_rows;        // as given to k_step_rows
-};
-
 // Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
 // which then sees the global stores every arriving block made before arriving; that block returns the counter
 // to 0. Each thread first waits for its own stores to reach L2, so thread 0's release fence (an L2 write-back,
@@ -2371,183 +2414,307 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
     return s_last != 0;
 }
 
-// Bin chunks of a column group for `groups` partials, so that each thread adds at most 8 of them (one round of
-// loads) where it can: packed partials are added a bin (four columns) per thread, pairs a slot per thread.
-__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups, bool packed) {
-    if (packed) return groups <= 32 ? 1u : (groups <= 64 ? 2u : (groups <= 128 ? 4u : 8u));
-    return groups <= 8 ? 1u : (groups <= 16 ? 2u : (groups <= 32 ? 4u : 8u));
+struct FinishArgs {
+    const int32_t *partial;     // the step partial buffer
+    const ColGroup *cgs;        // [ncg]
+    const int32_t *col_feat;    // per global column: the feature, -1 for padding
+    uint32_t *cg_count;         // [JMAX][ncg] items done per (job, column group); returned to 0 by the last one
+    uint32_t *job_count;        // [JMAX] column groups done per job
+    uint32_t *all_count;        // jobs done
+    StepPlan *plan;             // this step's plan
+    StepPlan *next;             // the next step's
+};
+
+// The end of job j, by one wave (learner.rs:294-352): both children's best splits from their per-feature
+// candidates (split.rs:866-880), their leaves in the speculative tree, and the job's leaf marked expanded.
+// Values every lane computes alike are kept uniform; lane 0 writes the scalars.
+__device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
+    const uint32_t lane = threadIdx.x & 63u;
+    GrowCtl *ctl = g.ctl;
+    const TLeaf pl = g.tl[J.t];
+    const SplitOut &info = pl.best;
+    const int64_t left = static_cast<int64_t>(J.left);
+    const int64_t right = J.parent_count - left;
+    if (!(left > 0 && right > 0)) {
+        if (lane == 0) {
+            ctl->error = 1;
+            ctl->done = 1;
+            const uint32_t info[8] = {j, J.t, J.count, J.left, J.ntiles, J.groups, J.packed, 0u};
+            for (int k = 0; k < 8; ++k) ctl->err_info[k] = info[k];
+        }
+        return;
+    }
+    const int32_t kid = J.kid;
+    const int32_t depth = pl.depth + 1;
+    const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
+    const bool searched = J.hist && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
+    // the job's evaluated features (learner.rs:262-265), for the byte count
+    const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
+    uint32_t used = 0;
+    for (uint32_t f = lane; f < g.nf; f += 64u)
+        used += static_cast<uint32_t>(__popcll(__ballot(g.mask[f] != 0 && prow[f] != 0)));
+    SplitOut out[2] = {};
+    if (searched) {
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ++ch) {
+            const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
+            uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
+            double best = 0.0;
+            int bf = -1;
+            FeatCand bc = {};
+            for (uint32_t f = lane; f < g.nf; f += 64u) {
+                FeatCand c = cands[f];
+                row[f] = static_cast<uint8_t>(c.splittable);
+                if (!c.found) continue;
+                double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+                if (cand_better(gv, static_cast<int>(f), best, bf)) {
+                    best = gv;
+                    bf = static_cast<int>(f);
+                    bc = c;
+                }
+            }
+            double wb = best;
+            int wf = bf;
+            wave_best(wb, wf);
+            if (wf >= 0) {
+                const FeatCand c = readlane_cand(bc, static_cast<uint32_t>(wf) & 63u);
+                const int64_t cnt = ch == 0 ? left : right;
+                out[ch] = split_out(c, wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+            }
+        }
+    }
+    if (lane == 0) {
+        TLeaf l = {}, r = {};
+        l.begin = J.begin;
+        l.count = J.left;
+        r.begin = J.begin + J.left;
+        r.count = J.count - J.left;
+        l.ug = info.left_grad;
+        l.uh = info.left_hess;
+        r.ug = info.right_grad;
+        r.uh = info.right_hess;
+        l.cnt = left;
+        r.cnt = right;
+        l.buf = r.buf = 1u - J.src_buf;
+        l.rev = 0;  // the split step writes the left child first-first and the right child last-first
+        r.rev = 1;
+        l.depth = r.depth = depth;
+        l.state = r.state = T_LEAF;
+        l.kid = r.kid = -1;
+        const double lv = info.left_output, rv = info.right_output;
+        l.value = lv != lv ? 0.0 : lv;
+        r.value = rv != rv ? 0.0 : rv;
+        l.weight = info.left_hess * g.sh;
+        r.weight = info.right_hess * g.sh;
+        l.slot = r.slot = -1;
+        if (searched) {
+            l.slot = J.built_side == 0 ? J.built_slot : J.parent_slot;
+            r.slot = J.built_side == 0 ? J.parent_slot : J.built_slot;
+            l.best = out[0];
+            r.best = out[1];
+            l.has_best = out[0].found ? 1u : 0u;
+            r.has_best = out[1].found ? 1u : 0u;
+        }
+        g.tl[kid] = l;
+        g.tl[kid + 1] = r;
+        g.tk[kid] = TKey{l.best.gain, l.has_best, T_LEAF, -1, 0u};
+        g.tk[kid + 1] = TKey{r.best.gain, r.has_best, T_LEAF, -1, 0u};
+        g.tl[J.t].state = T_EXPANDED;
+        g.tk[J.t].state = T_EXPANDED;
+        if (J.hist) {  // the built child's histogram was made, searched or not
+            const double built_rows = J.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
+            atomicAdd(&ctl->hist_rows, built_rows);
+            atomicAdd(&ctl->hist_bins, built_rows * static_cast<double>(used));
+            atomicAdd(&ctl->hist_builds, 1.0);
+        }
+        atomicAdd(&ctl->part_rows, static_cast<double>(J.count));
+    }
 }
 
-// grid: (ncg, FIN_CHUNKS), 1024 threads.
+// Work items until none is left; grid: any number of 1024-thread blocks.
 __global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a) {
     __shared__ int64_t red8[1024][8];  // partial sums on their way to stripe 0 (the first two words for pairs)
     static_assert(8 * sizeof(CatScratch) <= sizeof(red8), "categorical scratch reuses the reduction buffer");
+    static_assert(sizeof(AdvShared) <= sizeof(red8), "advance's scratch reuses the reduction buffer");
     // per (column, child) wave of a categorical scan; the scans start after the reduction's last barrier
     CatScratch *cats = reinterpret_cast<CatScratch *>(red8);
     int64_t(*red)[8] = red8;
     __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
     __shared__ uint32_t s_found[2][CG_COLS][2];
-    const Plan &p = *g.plan;
-    if (!p.active) return;
-    if (!p.may_search) {  // no histogram: apply and plan
-        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) finish_step(g);
-        return;
-    }
-    const uint32_t groups = step_groups(p.count, a.max_groups);
-    const bool packed = step_packed(p.count, a.max_groups, a.flush_rows);
-    const uint32_t chunks = finish_chunks(groups, packed);
-    if (blockIdx.y >= chunks) return;
+    __shared__ uint32_t s_item;
+    if (g.ctl->done) return;
+    StepPlan &P = *a.plan;
     const uint32_t tid = threadIdx.x;
-    const ColGroup cg = a.cgs[blockIdx.x];
-    // what the group's scans need, read now: wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
-    const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
-    const int32_t sf = a.col_feat[cg.gcol + scol];
-    FeatDev sm = {};
-    bool sev = false;
-    if (sf >= 0) {
-        sm = g.feats[sf];
-        sev = g.evaluate[sf] != 0;
-    }
-    int64_t *built = g.pool + static_cast<size_t>(p.built_slot) * g.slot_stride;
-    int64_t *parent = g.pool + static_cast<size_t>(p.parent_slot) * g.slot_stride;
-
-    // (bin, column) slots of this chunk: S = 1024 / chunks; `ways` threads per slot sum interleaved partials
-    const uint32_t nbins = 256u / chunks, S = nbins * CG_COLS, bin0 = blockIdx.y * nbins;
-    const uint32_t ways = 1024u / S;
-    const size_t pstride = step_partial_stride(cg.width);
-    if (packed) {  // a thread per (bin, partial stripe) adds the bin's four columns
-        const uint32_t pways = 1024u / nbins;
-        const uint32_t bin = bin0 + tid % nbins, q = tid / nbins;
-        const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin;
-        const size_t stride4 = pstride / 4;
-        // the parent's sums of the bin's four columns, read with the partials
-        int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (q == 0 && bin < cg.bins[c]) {
-                const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                pg[c] = parent[o];
-                ph[c] = parent[o + 1];
+    for (;;) {
+        __syncthreads();  // the block is done with the previous item's LDS
+        if (tid == 0) s_item = atomicAdd(&P.item_ticket, 1u);
+        __syncthreads();
+        const uint32_t item = s_item;
+        if (item >= P.total_items) return;
+        uint32_t j = 0;  // the item's job: the last whose first item is at or below it
+        for (uint32_t k = 1; k < P.njobs; ++k)
+            if (item >= P.jobs[k].item_base) j = k;
+        const JobPlan &J = P.jobs[j];
+        if (J.hist) {
+            const uint32_t r = item - J.item_base, chunks = J.chunks;
+            const uint32_t cgi = r / chunks, chunk = r - cgi * chunks;
+            const ColGroup cg = a.cgs[cgi];
+            // what the group's scans need, read now: wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
+            const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
+            const int32_t sf = a.col_feat[cg.gcol + scol];
+            FeatDev sm = {};
+            bool sev = false;
+            if (sf >= 0) {
+                sm = g.feats[sf];
+                sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
             }
-        int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
-        for (uint32_t w = q; w < groups; w += 8u * pways) {
-            int4 v[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                uint32_t wk = w + k * pways;
-                v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
-                if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
-                    sg[c] += gq;
-                    sh[c] += (x[c] - gq) >> 16;
-                }
-            }
-        }
-        // stripes q > 0 hand their sums to stripe 0 through LDS ([value][thread]: conflict-free)
-        if (pways > 1u) {
-            int64_t *r8 = reinterpret_cast<int64_t *>(red8);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                r8[(2 * c) * 1024 + tid] = sg[c];
-                r8[(2 * c + 1) * 1024 + tid] = sh[c];
-            }
-            __syncthreads();
-            if (q == 0)
-                for (uint32_t k = 1; k < pways; ++k) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        sg[c] += r8[(2 * c) * 1024 + tid + k * nbins];
-                        sh[c] += r8[(2 * c + 1) * 1024 + tid + k * nbins];
+            int64_t *built = g.pool + static_cast<size_t>(J.built_slot) * g.slot_stride;
+            int64_t *parent = g.pool + static_cast<size_t>(J.parent_slot) * g.slot_stride;
+            const uint32_t groups = J.groups;
+            // (bin, column) slots of this chunk: S = 1024 / chunks; `ways` threads per slot sum interleaved partials
+            const uint32_t nbins = 256u / chunks, S = nbins * CG_COLS, bin0 = chunk * nbins;
+            const uint32_t ways = 1024u / S;
+            const size_t pstride = step_partial_stride(cg.width);
+            if (J.packed) {  // a thread per (bin, partial stripe) adds the bin's four columns
+                const uint32_t pways = 1024u / nbins;
+                const uint32_t bin = bin0 + tid % nbins, q = tid / nbins;
+                const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin +
+                                   static_cast<size_t>(J.group_base) * (pstride / 2);
+                const size_t stride4 = pstride / 2;  // a partial's pairs in int4 units
+                // the parent's sums of the bin's four columns, read with the partials
+                int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
+        #pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (q == 0 && bin < cg.bins[c]) {
+                        const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                        pg[c] = parent[o];
+                        ph[c] = parent[o + 1];
+                    }
+                int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
+                for (uint32_t w = q; w < groups; w += 8u * pways) {
+                    int4 v[8];
+        #pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        uint32_t wk = w + k * pways;
+                        v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
+                        if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
+                    }
+        #pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+        #pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
+                            sg[c] += gq;
+                            sh[c] += (x[c] - gq) >> 16;
+                        }
                     }
                 }
-        }
-        if (q == 0) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                if (bin < cg.bins[c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                    built[o] = sg[c];
-                    built[o + 1] = sh[c];
-                    parent[o] = pg[c] - sg[c];
-                    parent[o + 1] = ph[c] - sh[c];
+                // stripes q > 0 hand their sums to stripe 0 through LDS ([value][thread]: conflict-free)
+                if (pways > 1u) {
+                    int64_t *r8 = reinterpret_cast<int64_t *>(red8);
+        #pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        r8[(2 * c) * 1024 + tid] = sg[c];
+                        r8[(2 * c + 1) * 1024 + tid] = sh[c];
+                    }
+                    __syncthreads();
+                    if (q == 0)
+                        for (uint32_t k = 1; k < pways; ++k) {
+        #pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                sg[c] += r8[(2 * c) * 1024 + tid + k * nbins];
+                                sh[c] += r8[(2 * c + 1) * 1024 + tid + k * nbins];
+                            }
+                        }
+                }
+                if (q == 0) {
+        #pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        if (bin < cg.bins[c]) {
+                            const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                            built[o] = sg[c];
+                            built[o + 1] = sh[c];
+                            parent[o] = pg[c] - sg[c];
+                            parent[o + 1] = ph[c] - sh[c];
+                        }
+                    }
+                }
+            } else {
+                const uint32_t s = tid % S, q = tid / S;
+                const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
+                const bool used = bin < cg.bins[cc];
+                const size_t at = static_cast<size_t>(bin) * cg.width + cg.c0 + cc;  // the slot within a partial
+                int64_t sg = 0, sh = 0;
+                if (used) {
+                    const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + at +
+                                           static_cast<size_t>(J.group_base) * pstride;
+                    for (uint32_t w = q; w < groups; w += 8u * ways) {
+                        int2 v[8];
+        #pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            uint32_t wk = w + k * ways;
+                            v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
+                            if (wk >= groups) v[k] = make_int2(0, 0);
+                        }
+        #pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            sg += v[k].x;
+                            sh += v[k].y;
+                        }
+                    }
+                }
+                if (ways > 1u) {
+                    red[tid][0] = sg;
+                    red[tid][1] = sh;
+                    __syncthreads();
+                    if (q == 0)
+                        for (uint32_t k = 1; k < ways; ++k) {
+                            sg += red[tid + k * S][0];
+                            sh += red[tid + k * S][1];
+                        }
+                }
+                if (q == 0 && used) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
+                    built[o] = sg;
+                    built[o + 1] = sh;
+                    parent[o] -= sg;
+                    parent[o + 1] -= sh;
                 }
             }
-        }
-    } else {
-        const uint32_t s = tid % S, q = tid / S;
-        const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
-        const bool used = bin < cg.bins[cc];
-        const size_t at = static_cast<size_t>(bin) * cg.width + cg.c0 + cc;  // the slot within a partial
-        int64_t sg = 0, sh = 0;
-        if (used) {
-            const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + at;
-            for (uint32_t w = q; w < groups; w += 8u * ways) {
-                int2 v[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    uint32_t wk = w + k * ways;
-                    v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
-                    if (wk >= groups) v[k] = make_int2(0, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    sg += v[k].x;
-                    sh += v[k].y;
+            if (!arrive_last(&a.cg_count[j * g.ncg + cgi], chunks)) continue;
+            // the group's features, both children, both directions (split.rs:584-620)
+            const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
+            const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
+            const int64_t *hist = child == J.built_side ? built : parent;
+            const bool searched = sf >= 0 && scan_searched(c, sm, sev);
+            const bool categorical = sm.kind == 2;
+            FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + child) * g.nf;
+            if (searched && categorical && dir == 0) {  // one wave per categorical feature and child
+                FeatCand r = categorical_candidate(c, g.cfg, sm, hist, cats[wave & 7u], nullptr);
+                if ((tid & 63u) == 0) cands[sf] = r;
+            } else if (searched && !categorical && (dir == 0 || scan_two_way(sm))) {
+                Grown r = {};
+                bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
+                if ((tid & 63u) == 0) {
+                    s_grown[child][scol][dir] = r;
+                    s_found[child][scol][dir] = found ? 1u : 0u;
                 }
             }
-        }
-        if (ways > 1u) {
-            red[tid][0] = sg;
-            red[tid][1] = sh;
             __syncthreads();
-            if (q == 0)
-                for (uint32_t k = 1; k < ways; ++k) {
-                    sg += red[tid + k * S][0];
-                    sh += red[tid + k * S][1];
-                }
+            if (sf >= 0 && dir == 0 && (tid & 63u) == 0 && !(searched && categorical)) {
+                FeatCand r = {};
+                if (searched)
+                    r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
+                                          scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
+                cands[sf] = r;
+            }
+            if (!arrive_last(&a.job_count[j], g.ncg)) continue;
         }
-        if (q == 0 && used) {
-            const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
-            built[o] = sg;
-            built[o + 1] = sh;
-            parent[o] -= sg;
-            parent[o + 1] -= sh;
-        }
+        if (tid < 64) job_select(g, J, j);
+        if (!arrive_last(a.all_count, P.njobs)) continue;
+        advance(g, *a.next, red8);
     }
-    if (!arrive_last(&a.cg_count[blockIdx.x], chunks)) return;
-    // the group's features, both children, both directions (split.rs:584-620)
-    const int64_t cnt = child == 0 ? static_cast<int64_t>(p.left) : p.parent_count - static_cast<int64_t>(p.left);
-    const Ctx c = make_ctx(g.cfg, g.sg, g.sh, p.child_ug[child], p.child_uh[child], cnt);
-    const int64_t *hist = child == p.built_side ? built : parent;
-    const bool searched = sf >= 0 && scan_searched(c, sm, sev);
-    const bool categorical = sm.kind == 2;
-    if (searched && categorical && dir == 0) {  // one wave per categorical feature and child
-        FeatCand r = categorical_candidate(c, g.cfg, sm, hist, cats[wave & 7u], nullptr);
-        if ((tid & 63u) == 0) g.cands[static_cast<size_t>(child) * g.nf + sf] = r;
-    } else if (searched && !categorical && (dir == 0 || scan_two_way(sm))) {
-        Grown r = {};
-        bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
-        if ((tid & 63u) == 0) {
-            s_grown[child][scol][dir] = r;
-            s_found[child][scol][dir] = found ? 1u : 0u;
-        }
-    }
-    __syncthreads();
-    if (sf >= 0 && dir == 0 && (tid & 63u) == 0 && !(searched && categorical)) {
-        FeatCand r = {};
-        if (searched)
-            r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
-                                  scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
-        g.cands[static_cast<size_t>(child) * g.nf + sf] = r;
-    }
-    if (!arrive_last(a.done_count, a.ncg)) return;
-    if (tid < 64) finish_step(g);
 }
 
 }  // namespace srocm
