@@ -308,6 +308,8 @@ struct Context {
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
     DevBuf<int32_t> gcol_feat;
+    DevBuf<uint32_t> cat_feats;  // the categorical features of the slabs
+    uint32_t ncat = 0;
     uint32_t ncg = 0;
     uint64_t step_partial_pairs = 0;
     uint32_t part_len = 0;
@@ -496,6 +498,14 @@ struct Context {
                 hip_check(hipMemcpy(d_cgs.p, cg.data(), cg.size() * sizeof(ColGroup), hipMemcpyHostToDevice), "upload column groups");
                 hip_check(hipMemcpy(gcol_feat.p, gfeat.data(), gfeat.size() * 4, hipMemcpyHostToDevice), "upload columns");
             }
+            // the categorical features in the slabs, scanned by k_step_cat
+            std::vector<uint32_t> cats;
+            for (int32_t f : gfeat)
+                if (f >= 0 && feats[f].kind == SROCM_BINS_CATEGORICAL) cats.push_back(static_cast<uint32_t>(f));
+            ncat = static_cast<uint32_t>(cats.size());
+            cat_feats.alloc(std::max<size_t>(cats.size(), 1));
+            if (!cats.empty())
+                hip_check(hipMemcpy(cat_feats.p, cats.data(), cats.size() * 4, hipMemcpyHostToDevice), "upload categorical features");
         }
         used.assign(nf, 1);
         part_len = 0;
@@ -977,7 +987,7 @@ struct Context {
     // split steps (k_step_rows, k_step_finish)
     DevBuf<int32_t> step_partial;            // per slab: [cus + JMAX][256 * W] {g, h}
     DevBuf<unsigned long long> tile_status;  // per partition tile
-    DevBuf<uint32_t> fin_counts;             // [JMAX][ncg] item counters, [JMAX] job counters, the job counter
+    DevBuf<uint32_t> fin_counts;             // the jobs-selected counter of k_step_select
     uint64_t epochs_used = 0;
     uint32_t last_steps = 0;                 // split steps of the last tree (the first guess for the next)
     struct TreeBufs {
@@ -992,7 +1002,8 @@ struct Context {
     uint32_t grow_capacity = 0;
 
     uint32_t k1_groups() const { return cus + JMAX; }  // k_step_rows' grid
-    uint32_t k2_blocks() const { return cus; }         // k_step_finish's grid: one 1024-thread block per CU fits
+    uint32_t k2_blocks() const { return cus; }         // k_step_scan's grid: one 1024-thread block per CU
+    uint32_t reduce_blocks() const { return 8 * cus; } // k_step_reduce's grid
 
     void ensure_grow(uint32_t L) {
         if (grow_capacity >= L && pool.p) return;
@@ -1026,7 +1037,7 @@ struct Context {
         dtree.left_bins.alloc(static_cast<size_t>(L) * 8);
         step_partial.alloc(2 * step_partial_pairs);
         tile_status.alloc(div_up(rows, STEP_TILE) + JMAX + 1);
-        fin_counts.alloc(static_cast<size_t>(JMAX) * ncg + JMAX + 1);
+        fin_counts.alloc(1);
         reset_step_state();
         grow_capacity = L;
     }
@@ -1248,11 +1259,19 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     prof.step_events.emplace_back(e0, e1);
                     prof.step_launches += static_cast<double>(slabs.size());
                 }
-                uint32_t *fc = fin_counts.p;
-                FinishArgs fa{step_partial.p, d_cgs.p, gcol_feat.p, fc, fc + static_cast<size_t>(JMAX) * ncg,
-                              fc + static_cast<size_t>(JMAX) * ncg + JMAX, d_plans.p + parity, d_plans.p + (parity ^ 1u)};
-                k_step_finish<<<k2_blocks(), 1024, 0, stream>>>(g, fa);
-                launch_check("k_step_finish");
+                ReduceStepArgs ra{step_partial.p, d_cgs.p, d_plans.p + parity};
+                k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
+                launch_check("k_step_reduce");
+                ScanStepArgs sca{d_cgs.p, gcol_feat.p, cat_feats.p, ncat, d_plans.p + parity};
+                k_step_scan<<<k2_blocks(), 1024, 0, stream>>>(g, sca);
+                launch_check("k_step_scan");
+                if (ncat) {
+                    k_step_cat<<<std::min<uint32_t>(cus * 2, div_up(static_cast<uint64_t>(JMAX) * 2 * ncat, 4)), 256, 0, stream>>>(g, sca);
+                    launch_check("k_step_cat");
+                }
+                SelectArgs sa2{fin_counts.p, d_plans.p + parity, d_plans.p + (parity ^ 1u)};
+                k_step_select<<<JMAX, 512, 0, stream>>>(g, sa2);
+                launch_check("k_step_select");
             }
             hc = read_ctl();
             if (hc.done) break;

@@ -1446,11 +1446,12 @@ __host__ __device__ constexpr size_t step_partial_stride(uint32_t w) { return 25
 constexpr uint32_t ST_AGG = 1, ST_INCL = 2;   // tile status: its own left count / lefts up to and including it
 constexpr uint32_t LOOKBACK_SPINS = 1u << 20; // ~0.1 s of polling before a step gives up with an error
 
-// Bin chunks of a column group for `groups` partials, so that each thread adds at most 8 of them (one round of
-// loads) where it can: packed partials are added a bin (four columns) per thread, pairs a slot per thread.
-__device__ __forceinline__ uint32_t finish_chunks(uint32_t groups, bool packed) {
-    if (packed) return groups <= 32 ? 1u : (groups <= 64 ? 2u : (groups <= 128 ? 4u : 8u));
-    return groups <= 8 ? 1u : (groups <= 16 ? 2u : (groups <= 32 ? 4u : 8u));
+// Stripes of a job's `groups` partials that k_step_reduce adds on separate threads (combined through LDS), so that
+// a thread adds about 8 partials (one round of loads): a power of two up to 32.
+__device__ __forceinline__ uint32_t reduce_ways(uint32_t groups) {
+    uint32_t w = 1;
+    while (w < 32 && w * 8 < groups) w <<= 1;
+    return w;
 }
 
 // Wave-wide sums of one value per lane: exclusive prefix and total.
@@ -1526,8 +1527,9 @@ struct JobPlan {
     uint32_t ntiles, tile_base;   // partition tiles and the first one's status word
     uint32_t groups, group_base;  // k_step_rows workgroups, one partial each
     uint32_t packed;              // the partials are packed 16/16 LDS words (one tile per workgroup)
-    uint32_t chunks;              // k_step_finish bin chunks per column group
-    uint32_t item_base, items;    // k_step_finish work items
+    uint32_t ways;                // k_step_reduce stripes of the partials (reduce_ways)
+    uint32_t red_base, red_items; // k_step_reduce work items: per column group, `ways` (packed) or 4 * `ways`
+    uint32_t scan_base, scan_items;  // k_step_scan work items: a scan per column group (when histogrammed)
     uint32_t ticket;              // next partition tile to hand out
     uint32_t left;                // rows going left, written by the last tile
     int32_t kid;                  // the children's speculative leaves
@@ -1539,9 +1541,9 @@ struct JobPlan {
 struct StepPlan {
     uint32_t njobs;
     uint32_t total_groups;  // k_step_rows workgroups in use
-    uint32_t total_items;   // k_step_finish work items
+    uint32_t total_red;     // k_step_reduce work items
+    uint32_t total_scan;    // k_step_scan work items
     uint32_t epoch;         // tags the step's tile status words
-    uint32_t item_ticket;   // next k_step_finish work item
     uint32_t pad_[3];
     JobPlan jobs[JMAX];
 };
@@ -1724,6 +1726,9 @@ struct AdvShared {
     uint16_t cx[GROW_MAX_LEAVES];         // commit c: the leaf id split
     int16_t cpn[GROW_MAX_LEAVES];         // commit c: the split leaf's node above
     uint8_t cleft[GROW_MAX_LEAVES];       // commit c: the split leaf was its node's left child
+    double idg[GROW_MAX_LEAVES];          // committed leaf -> its speculative leaf's gain, as the replay goes
+    uint32_t idm[GROW_MAX_LEAVES];        // committed leaf -> its speculative leaf's meta
+    double cgain[TCAP_MAX];               // speculation candidates' gains
     uint16_t cand[TCAP_MAX];              // speculation candidates
     uint16_t job_t[JMAX];
     uint32_t ncand, ncommit, n, blocker, done, njobs;
@@ -1731,6 +1736,26 @@ struct AdvShared {
 
 __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
     return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
+}
+
+// This lane's part of best_leaf (learner.rs:418-429) over the committed leaves lane, lane + 64, ... below n: the
+// first leaf with a split as 2 * leaf + (its gain is NaN), and the first highest gain that is not NaN.
+__device__ __forceinline__ void lane_best(const AdvShared &s, uint32_t lane, uint32_t n, int &first, double &kg, int &ki) {
+    first = 1 << 30;
+    kg = 0.0;
+    ki = -1;
+    for (uint32_t id = lane; id < n; id += 64u) {
+        if (!(s.idm[id] & 1u)) continue;
+        const double gk = s.idg[id];
+        const bool nan = gk != gk;
+        const int code = 2 * static_cast<int>(id) + (nan ? 1 : 0);
+        if (code < first) first = code;
+        if (nan) continue;
+        if (cand_better(gk, static_cast<int>(id), kg, ki)) {
+            kg = gk;
+            ki = static_cast<int>(id);
+        }
+    }
 }
 
 // LDS writes of one lane made visible to the rest of its wave.
@@ -1762,35 +1787,31 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     }
     if (tid == 0) s.ncand = 0;
     __syncthreads();
+    for (uint32_t id = tid; id < n0; id += nt) {
+        const uint32_t k = s.leaf_t[id];
+        s.idg[id] = s.gain[k];
+        s.idm[id] = s.meta[k];
+    }
+    __syncthreads();
 
-    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave
+    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave: each lane keeps the best of
+    // its leaves and recomputes it when one of them changes
     if (tid < 64) {
         uint32_t n = n0, nc = 0, blocker = 0;
         bool done = false;
+        int lf, li;
+        double lg;
+        lane_best(s, lane, n, lf, lg, li);
         for (;;) {
             if (n >= L) {
                 done = true;
                 break;
             }
             // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
-            // otherwise the first highest gain among the rest (a NaN later never wins); `first` is 2 * leaf + NaN
-            int first = 1 << 30;
-            double kg = 0.0;
-            int ki = -1;
-            for (uint32_t id = lane; id < n; id += 64u) {
-                const uint32_t k = s.leaf_t[id];
-                if (!(s.meta[k] & 1u)) continue;
-                const double gk = s.gain[k];
-                const bool nan = gk != gk;
-                const int code = 2 * static_cast<int>(id) + (nan ? 1 : 0);
-                if (code < first) first = code;
-                if (nan) continue;
-                if (cand_better(gk, static_cast<int>(id), kg, ki)) {
-                    kg = gk;
-                    ki = static_cast<int>(id);
-                }
-            }
-            first = wave_min(first);
+            // otherwise the first highest gain among the rest (a NaN later never wins)
+            const int first = wave_min(lf);
+            double kg = lg;
+            int ki = li;
             wave_best(kg, ki);
             const bool nan_first = first < (1 << 30) && (first & 1);
             if (nan_first || ki < 0 || !(kg > 0.0)) {
@@ -1798,12 +1819,12 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
                 break;
             }
             const uint32_t x = static_cast<uint32_t>(ki);
-            const uint32_t k = s.leaf_t[x];
-            const uint32_t m = s.meta[k];
+            const uint32_t m = s.idm[x];
             if (((m >> 1) & 3u) != T_EXPANDED) {
-                blocker = k;
+                blocker = s.leaf_t[x];
                 break;
             }
+            const uint32_t k = s.leaf_t[x];
             const uint32_t kid = (m >> 3) - 1u;
             if (lane == 0) {
                 const int16_t node = static_cast<int16_t>(n - 1);
@@ -1819,10 +1840,15 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
                 s.is_left[n] = 0;
                 s.touched[x] = 1;
                 s.touched[n] = 1;
+                s.idg[x] = s.gain[kid];
+                s.idm[x] = s.meta[kid];
+                s.idg[n] = s.gain[kid + 1];
+                s.idm[n] = s.meta[kid + 1];
             }
             wave_lds_sync();
             ++nc;
             ++n;
+            if (lane == (x & 63u) || lane == ((n - 1u) & 63u)) lane_best(s, lane, n, lf, lg, li);
         }
         if (lane == 0) {
             s.ncommit = nc;
@@ -1888,6 +1914,7 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && gk > 0.0 && k != blocker) {
             const uint32_t at = atomicAdd(&s.ncand, 1u);
             s.cand[at] = static_cast<uint16_t>(k);
+            s.cgain[at] = gk;
         }
     }
     __syncthreads();
@@ -1905,11 +1932,11 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     // the spec highest gains (ties to the lower leaf); the blocker is job 0
     for (uint32_t i = tid; i < ncand; i += nt) {
         const uint32_t ki = s.cand[i];
-        const double gi = s.gain[ki];
+        const double gi = s.cgain[i];
         uint32_t rank = 0;
         for (uint32_t j = 0; j < ncand; ++j) {
+            const double gj = s.cgain[j];
             const uint32_t kj = s.cand[j];
-            const double gj = s.gain[kj];
             rank += (gj > gi || (gj == gi && kj < ki)) ? 1u : 0u;
         }
         if (rank < spec) s.job_t[1 + rank] = static_cast<uint16_t>(ki);
@@ -1970,22 +1997,25 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         }
         const uint32_t groups_before = wave_excl_sum(groups);
         const uint32_t total_groups = wave_total(groups);
-        uint32_t items = 0;
+        uint32_t red = 0, scan = 0;
         if (on) {
             J.tile_base = tiles_before;
             J.groups = groups;
             J.group_base = groups_before;
             J.packed = (ntiles <= groups && g.flush_rows >= STEP_TILE) ? 1u : 0u;
-            J.chunks = hist ? finish_chunks(groups, J.packed != 0) : 0u;
-            items = hist ? g.ncg * J.chunks : 1u;
-            J.items = items;
+            J.ways = reduce_ways(groups);
+            red = hist ? g.ncg * (J.packed ? J.ways : 4u * J.ways) : 0u;
+            scan = hist ? g.ncg : 0u;
+            J.red_items = red;
+            J.scan_items = scan;
             J.built_slot = hist ? static_cast<int32_t>(slot0 + hist_before) : -1;
         }
-        const uint32_t items_before = wave_excl_sum(items);
-        const uint32_t total_items = wave_total(items);
+        const uint32_t red_before = wave_excl_sum(red), scan_before = wave_excl_sum(scan);
+        const uint32_t total_red = wave_total(red), total_scan = wave_total(scan);
         const uint32_t nhist = wave_total(hist);
         if (on) {
-            J.item_base = items_before;
+            J.red_base = red_before;
+            J.scan_base = scan_before;
             J.ticket = 0;
             J.left = 0;
             next.jobs[lane] = J;
@@ -1997,9 +2027,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if (lane == 0) {
             next.njobs = njobs;
             next.total_groups = total_groups;
-            next.total_items = total_items;
+            next.total_red = total_red;
+            next.total_scan = total_scan;
             next.epoch = epoch0 + 1;
-            next.item_ticket = 0;
             ctl->epoch = epoch0 + 1;
             ctl->ntent = ntent + 2 * njobs;
             ctl->next_slot = slot0 + nhist;
@@ -2414,15 +2444,24 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
     return s_last != 0;
 }
 
-struct FinishArgs {
-    const int32_t *partial;     // the step partial buffer
+struct ScanStepArgs {
     const ColGroup *cgs;        // [ncg]
     const int32_t *col_feat;    // per global column: the feature, -1 for padding
-    uint32_t *cg_count;         // [JMAX][ncg] items done per (job, column group); returned to 0 by the last one
-    uint32_t *job_count;        // [JMAX] column groups done per job
-    uint32_t *all_count;        // jobs done
+    const uint32_t *cat_feats;  // the categorical features (k_step_cat)
+    uint32_t ncat;
+    StepPlan *plan;
+};
+
+struct SelectArgs {
+    uint32_t *all_count;        // jobs selected; returned to 0 by the last one
     StepPlan *plan;             // this step's plan
     StepPlan *next;             // the next step's
+};
+
+struct ReduceStepArgs {
+    const int32_t *partial;     // the step partial buffer
+    const ColGroup *cgs;        // [ncg]
+    StepPlan *plan;
 };
 
 // The end of job j, by one wave (learner.rs:294-352): both children's best splits from their per-feature
@@ -2461,25 +2500,22 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
             uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
             double best = 0.0;
             int bf = -1;
-            FeatCand bc = {};
             for (uint32_t f = lane; f < g.nf; f += 64u) {
-                FeatCand c = cands[f];
+                const FeatCand &c = cands[f];
                 row[f] = static_cast<uint8_t>(c.splittable);
                 if (!c.found) continue;
-                double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+                const double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
                 if (cand_better(gv, static_cast<int>(f), best, bf)) {
                     best = gv;
                     bf = static_cast<int>(f);
-                    bc = c;
                 }
             }
             double wb = best;
             int wf = bf;
             wave_best(wb, wf);
-            if (wf >= 0) {
-                const FeatCand c = readlane_cand(bc, static_cast<uint32_t>(wf) & 63u);
+            if (wf >= 0) {  // the winner, read once more where the scans left it
                 const int64_t cnt = ch == 0 ? left : right;
-                out[ch] = split_out(c, wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                out[ch] = split_out(cands[wf], wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
             }
         }
     }
@@ -2531,190 +2567,212 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
     }
 }
 
-// Work items until none is left; grid: any number of 1024-thread blocks.
-__global__ __launch_bounds__(1024) void k_step_finish(GrowState g, FinishArgs a) {
-    __shared__ int64_t red8[1024][8];  // partial sums on their way to stripe 0 (the first two words for pairs)
-    static_assert(8 * sizeof(CatScratch) <= sizeof(red8), "categorical scratch reuses the reduction buffer");
-    static_assert(sizeof(AdvShared) <= sizeof(red8), "advance's scratch reuses the reduction buffer");
-    // per (column, child) wave of a categorical scan; the scans start after the reduction's last barrier
-    CatScratch *cats = reinterpret_cast<CatScratch *>(red8);
-    int64_t(*red)[8] = red8;
-    __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
-    __shared__ uint32_t s_found[2][CG_COLS][2];
-    __shared__ uint32_t s_item;
+// The built child's histogram of each job from its workgroups' partials, and its sibling's by subtraction in place
+// of the parent's (learner.rs:356-371). Work items (job, column group, slot range) in a grid-stride loop: a
+// thread adds one stripe of the partials of its slot (a bin's four columns for packed partials, one {g, h} pair
+// otherwise) and the stripes meet in LDS. grid: any, 256 threads.
+__global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs a) {
+    __shared__ int64_t red[8][256];  // the stripes' sums, [value][thread]: conflict-free
     if (g.ctl->done) return;
-    StepPlan &P = *a.plan;
+    const StepPlan &P = *a.plan;
     const uint32_t tid = threadIdx.x;
-    for (;;) {
-        __syncthreads();  // the block is done with the previous item's LDS
-        if (tid == 0) s_item = atomicAdd(&P.item_ticket, 1u);
-        __syncthreads();
-        const uint32_t item = s_item;
-        if (item >= P.total_items) return;
+    for (uint32_t item = blockIdx.x; item < P.total_red; item += gridDim.x) {
         uint32_t j = 0;  // the item's job: the last whose first item is at or below it
         for (uint32_t k = 1; k < P.njobs; ++k)
-            if (item >= P.jobs[k].item_base) j = k;
+            if (item >= P.jobs[k].red_base) j = k;
         const JobPlan &J = P.jobs[j];
-        if (J.hist) {
-            const uint32_t r = item - J.item_base, chunks = J.chunks;
-            const uint32_t cgi = r / chunks, chunk = r - cgi * chunks;
-            const ColGroup cg = a.cgs[cgi];
-            // what the group's scans need, read now: wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
-            const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
-            const int32_t sf = a.col_feat[cg.gcol + scol];
-            FeatDev sm = {};
-            bool sev = false;
-            if (sf >= 0) {
-                sm = g.feats[sf];
-                sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
+        const uint32_t ways = J.ways, groups = J.groups;
+        const bool packed = J.packed != 0;
+        const uint32_t per_cg = packed ? ways : 4u * ways;
+        const uint32_t r = item - J.red_base, cgi = r / per_cg, sub = r - cgi * per_cg;
+        const ColGroup &cg = a.cgs[cgi];  // read in place: a column is picked per thread
+        int64_t *built = g.pool + static_cast<size_t>(J.built_slot) * g.slot_stride;
+        int64_t *parent = g.pool + static_cast<size_t>(J.parent_slot) * g.slot_stride;
+        const size_t pstride = step_partial_stride(cg.width);  // pairs from one partial to the next
+        const uint32_t ns = 256u / ways;                        // the item's slots
+        const uint32_t q = tid / ns;                            // this thread's stripe
+        if (packed) {
+            const uint32_t bin = sub * ns + tid % ns;
+            const size_t stride4 = pstride / 2;  // a partial's pairs in int4 units
+            const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin +
+                              static_cast<size_t>(J.group_base) * stride4;
+            int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
+            for (uint32_t w = q; w < groups; w += 8u * ways) {
+                int4 v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t wk = w + k * ways;
+                    v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
+                    if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
+                        sg[c] += gq;
+                        sh[c] += (x[c] - gq) >> 16;
+                    }
+                }
             }
-            int64_t *built = g.pool + static_cast<size_t>(J.built_slot) * g.slot_stride;
-            int64_t *parent = g.pool + static_cast<size_t>(J.parent_slot) * g.slot_stride;
-            const uint32_t groups = J.groups;
-            // (bin, column) slots of this chunk: S = 1024 / chunks; `ways` threads per slot sum interleaved partials
-            const uint32_t nbins = 256u / chunks, S = nbins * CG_COLS, bin0 = chunk * nbins;
-            const uint32_t ways = 1024u / S;
-            const size_t pstride = step_partial_stride(cg.width);
-            if (J.packed) {  // a thread per (bin, partial stripe) adds the bin's four columns
-                const uint32_t pways = 1024u / nbins;
-                const uint32_t bin = bin0 + tid % nbins, q = tid / nbins;
-                const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin +
-                                   static_cast<size_t>(J.group_base) * (pstride / 2);
-                const size_t stride4 = pstride / 2;  // a partial's pairs in int4 units
-                // the parent's sums of the bin's four columns, read with the partials
-                int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
-        #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (q == 0 && bin < cg.bins[c]) {
-                        const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                        pg[c] = parent[o];
-                        ph[c] = parent[o + 1];
-                    }
-                int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
-                for (uint32_t w = q; w < groups; w += 8u * pways) {
-                    int4 v[8];
-        #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        uint32_t wk = w + k * pways;
-                        v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
-                        if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
-                    }
-        #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-        #pragma unroll
+            if (ways > 1u) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    red[2 * c][tid] = sg[c];
+                    red[2 * c + 1][tid] = sh[c];
+                }
+                __syncthreads();
+                if (q == 0)
+                    for (uint32_t k = 1; k < ways; ++k) {
+#pragma unroll
                         for (int c = 0; c < 4; ++c) {
-                            int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
-                            sg[c] += gq;
-                            sh[c] += (x[c] - gq) >> 16;
+                            sg[c] += red[2 * c][tid + k * ns];
+                            sh[c] += red[2 * c + 1][tid + k * ns];
                         }
                     }
-                }
-                // stripes q > 0 hand their sums to stripe 0 through LDS ([value][thread]: conflict-free)
-                if (pways > 1u) {
-                    int64_t *r8 = reinterpret_cast<int64_t *>(red8);
-        #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        r8[(2 * c) * 1024 + tid] = sg[c];
-                        r8[(2 * c + 1) * 1024 + tid] = sh[c];
+            }
+            if (q == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (bin < cg.bins[c]) {
+                        const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                        const int64_t pg = parent[o], ph = parent[o + 1];
+                        built[o] = sg[c];
+                        built[o + 1] = sh[c];
+                        parent[o] = pg - sg[c];
+                        parent[o + 1] = ph - sh[c];
                     }
-                    __syncthreads();
-                    if (q == 0)
-                        for (uint32_t k = 1; k < pways; ++k) {
-        #pragma unroll
-                            for (int c = 0; c < 4; ++c) {
-                                sg[c] += r8[(2 * c) * 1024 + tid + k * nbins];
-                                sh[c] += r8[(2 * c + 1) * 1024 + tid + k * nbins];
-                            }
-                        }
-                }
-                if (q == 0) {
-        #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        if (bin < cg.bins[c]) {
-                            const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                            built[o] = sg[c];
-                            built[o + 1] = sh[c];
-                            parent[o] = pg[c] - sg[c];
-                            parent[o + 1] = ph[c] - sh[c];
-                        }
-                    }
-                }
-            } else {
-                const uint32_t s = tid % S, q = tid / S;
-                const uint32_t cc = s % CG_COLS, bin = bin0 + s / CG_COLS;
-                const bool used = bin < cg.bins[cc];
-                const size_t at = static_cast<size_t>(bin) * cg.width + cg.c0 + cc;  // the slot within a partial
-                int64_t sg = 0, sh = 0;
-                if (used) {
-                    const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + at +
-                                           static_cast<size_t>(J.group_base) * pstride;
-                    for (uint32_t w = q; w < groups; w += 8u * ways) {
-                        int2 v[8];
-        #pragma unroll
-                        for (int k = 0; k < 8; ++k) {
-                            uint32_t wk = w + k * ways;
-                            v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
-                            if (wk >= groups) v[k] = make_int2(0, 0);
-                        }
-        #pragma unroll
-                        for (int k = 0; k < 8; ++k) {
-                            sg += v[k].x;
-                            sh += v[k].y;
-                        }
-                    }
-                }
-                if (ways > 1u) {
-                    red[tid][0] = sg;
-                    red[tid][1] = sh;
-                    __syncthreads();
-                    if (q == 0)
-                        for (uint32_t k = 1; k < ways; ++k) {
-                            sg += red[tid + k * S][0];
-                            sh += red[tid + k * S][1];
-                        }
-                }
-                if (q == 0 && used) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
-                    built[o] = sg;
-                    built[o + 1] = sh;
-                    parent[o] -= sg;
-                    parent[o + 1] -= sh;
                 }
             }
-            if (!arrive_last(&a.cg_count[j * g.ncg + cgi], chunks)) continue;
-            // the group's features, both children, both directions (split.rs:584-620)
-            const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
-            const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
-            const int64_t *hist = child == J.built_side ? built : parent;
-            const bool searched = sf >= 0 && scan_searched(c, sm, sev);
-            const bool categorical = sm.kind == 2;
-            FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + child) * g.nf;
-            if (searched && categorical && dir == 0) {  // one wave per categorical feature and child
-                FeatCand r = categorical_candidate(c, g.cfg, sm, hist, cats[wave & 7u], nullptr);
-                if ((tid & 63u) == 0) cands[sf] = r;
-            } else if (searched && !categorical && (dir == 0 || scan_two_way(sm))) {
-                Grown r = {};
-                bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
-                if ((tid & 63u) == 0) {
-                    s_grown[child][scol][dir] = r;
-                    s_found[child][scol][dir] = found ? 1u : 0u;
+        } else {
+            const uint32_t slot = sub * ns + tid % ns, cc = slot % CG_COLS, bin = slot / CG_COLS;
+            const bool used = bin < cg.bins[cc];
+            int64_t sg = 0, sh = 0;
+            if (used) {
+                const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + static_cast<size_t>(bin) * cg.width + cg.c0 +
+                                  cc + static_cast<size_t>(J.group_base) * pstride;
+                for (uint32_t w = q; w < groups; w += 8u * ways) {
+                    int2 v[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const uint32_t wk = w + k * ways;
+                        v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
+                        if (wk >= groups) v[k] = make_int2(0, 0);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        sg += v[k].x;
+                        sh += v[k].y;
+                    }
                 }
             }
-            __syncthreads();
-            if (sf >= 0 && dir == 0 && (tid & 63u) == 0 && !(searched && categorical)) {
-                FeatCand r = {};
-                if (searched)
-                    r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
-                                          scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
-                cands[sf] = r;
+            if (ways > 1u) {
+                red[0][tid] = sg;
+                red[1][tid] = sh;
+                __syncthreads();
+                if (q == 0)
+                    for (uint32_t k = 1; k < ways; ++k) {
+                        sg += red[0][tid + k * ns];
+                        sh += red[1][tid + k * ns];
+                    }
             }
-            if (!arrive_last(&a.job_count[j], g.ncg)) continue;
+            if (q == 0 && used) {
+                const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
+                const int64_t pg = parent[o], ph = parent[o + 1];
+                built[o] = sg;
+                built[o + 1] = sh;
+                parent[o] = pg - sg;
+                parent[o + 1] = ph - sh;
+            }
         }
-        if (tid < 64) job_select(g, J, j);
-        if (!arrive_last(a.all_count, P.njobs)) continue;
-        advance(g, *a.next, red8);
+        __syncthreads();  // the LDS is free for the next item
     }
+}
+
+// Scan items (job, column group) in a grid-stride loop: the group's numerical features for both children, both
+// directions (split.rs:584-620), a wave per (feature, child, direction). Categorical features are k_step_cat's.
+// grid: any, 1024 threads.
+__global__ __launch_bounds__(1024) void k_step_scan(GrowState g, ScanStepArgs a) {
+    __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
+    __shared__ uint32_t s_found[2][CG_COLS][2];
+    if (g.ctl->done) return;
+    const StepPlan &P = *a.plan;
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t item = blockIdx.x; item < P.total_scan; item += gridDim.x) {
+        uint32_t j = 0;  // the item's job: the last whose first item is at or below it
+        for (uint32_t k = 1; k < P.njobs; ++k)
+            if (item >= P.jobs[k].scan_base) j = k;
+        const JobPlan &J = P.jobs[j];
+        const ColGroup &cg = a.cgs[item - J.scan_base];
+        // wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
+        const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
+        const int32_t sf = a.col_feat[cg.gcol + scol];
+        FeatDev sm = {};
+        bool sev = false;
+        if (sf >= 0) {
+            sm = g.feats[sf];
+            sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
+        }
+        const bool numerical = sf >= 0 && sm.kind != 2;
+        const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
+        const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
+        const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
+        const bool searched = numerical && scan_searched(c, sm, sev);
+        if (searched && (dir == 0 || scan_two_way(sm))) {
+            Grown r = {};
+            bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
+            if ((tid & 63u) == 0) {
+                s_grown[child][scol][dir] = r;
+                s_found[child][scol][dir] = found ? 1u : 0u;
+            }
+        }
+        __syncthreads();
+        if (numerical && dir == 0 && (tid & 63u) == 0) {
+            FeatCand r = {};
+            if (searched)
+                r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
+                                      scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
+            g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
+        }
+        __syncthreads();  // s_grown is free for the next item
+    }
+}
+
+// The categorical features' candidates of every job (split.rs:694-844): a wave per (job, feature, child) in a
+// grid-stride loop. grid: any, 256 threads.
+__global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
+    __shared__ CatScratch cats[4];
+    if (g.ctl->done) return;
+    const StepPlan &P = *a.plan;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t per_job = 2 * a.ncat, total = P.njobs * per_job;
+    for (uint32_t item = blockIdx.x * 4 + wave; item < total; item += gridDim.x * 4) {
+        const uint32_t j = item / per_job, r = item - j * per_job, child = r & 1u;
+        const JobPlan &J = P.jobs[j];
+        if (!J.hist) continue;
+        const uint32_t f = a.cat_feats[r >> 1];
+        const FeatDev sm = g.feats[f];
+        const bool sev = g.mask[f] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + f] != 0;
+        const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
+        const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
+        const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
+        FeatCand out = {};
+        if (scan_searched(c, sm, sev)) out = categorical_candidate(c, g.cfg, sm, hist, cats[wave], nullptr);
+        if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + f] = out;
+    }
+}
+
+// Block j selects both children of job j (job_select); the last block to finish runs advance. grid: JMAX blocks.
+__global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) {
+    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
+    if (g.ctl->done) return;
+    StepPlan &P = *a.plan;
+    const uint32_t j = blockIdx.x;
+    if (j >= P.njobs) return;
+    if (threadIdx.x < 64) job_select(g, P.jobs[j], j);
+    if (!arrive_last(a.all_count, P.njobs)) return;
+    advance(g, *a.next, scratch);
 }
 
 }  // namespace srocm
