@@ -974,7 +974,6 @@ struct Context {
     DevBuf<GrowCtl> d_ctl;
     DevBuf<TLeaf> d_tl;               // the speculative tree's leaves
     DevBuf<TKey> d_tk;
-    DevBuf<int32_t> d_leaf_t;
     DevBuf<uint8_t> d_leaf_left;
     DevBuf<uint8_t> d_splittable, d_eval, d_mask;
     DevBuf<ScanJob> d_jobs;
@@ -990,15 +989,21 @@ struct Context {
     DevBuf<uint32_t> fin_counts;             // the jobs-selected counter of k_step_select
     uint64_t epochs_used = 0;
     uint32_t last_steps = 0;                 // split steps of the last tree (the first guess for the next)
-    struct TreeBufs {
-        DevBuf<int32_t> split_feature, left_child, right_child, leaf_parent, leaf_depth;
-        DevBuf<uint32_t> threshold_bin;
-        DevBuf<uint8_t> default_left;
-        DevBuf<float> split_gain;
-        DevBuf<double> internal_value, internal_weight, leaf_value, leaf_weight;
-        DevBuf<int64_t> internal_count, leaf_count;
-        DevBuf<uint32_t> left_bins;
-    } dtree;
+    // The tree arrays and the committed leaves' speculative leaves, in one allocation so that a tree comes back in
+    // one copy: 8-byte arrays, then 4-byte arrays, the left-bin masks and the default-left flags, each padded to 8 B.
+    struct TreeLayout {
+        size_t iv, iw, lv, lw, ic, lc, leaf_t, sf, lch, rch, lp, ld, tb, sg, lb, dl, bytes;
+        explicit TreeLayout(uint32_t L = 0) {
+            size_t at = 0;
+            auto take = [&](size_t n) { size_t o = at; at += (n + 7) & ~static_cast<size_t>(7); return o; };
+            iv = take(8ull * L); iw = take(8ull * L); lv = take(8ull * L); lw = take(8ull * L); ic = take(8ull * L); lc = take(8ull * L);
+            leaf_t = take(4ull * L); sf = take(4ull * L); lch = take(4ull * L); rch = take(4ull * L); lp = take(4ull * L);
+            ld = take(4ull * L); tb = take(4ull * L); sg = take(4ull * L); lb = take(32ull * L); dl = take(L);
+            bytes = at;
+        }
+    };
+    DevBuf<uint8_t> dtree;
+    TreeLayout tree_layout;
     uint32_t grow_capacity = 0;
 
     uint32_t k1_groups() const { return cus + JMAX; }  // k_step_rows' grid
@@ -1013,28 +1018,14 @@ struct Context {
         d_ctl.alloc(1);
         d_tl.alloc(tcap);
         d_tk.alloc(tcap);
-        d_leaf_t.alloc(L);
         d_leaf_left.alloc(L);
         d_splittable.alloc(static_cast<size_t>(tcap) * nf);
         d_eval.alloc(nf);
         d_mask.alloc(nf);
         d_jobs.alloc(1);
         d_cands.alloc(static_cast<size_t>(JMAX) * 2 * nf);
-        dtree.split_feature.alloc(L);
-        dtree.left_child.alloc(L);
-        dtree.right_child.alloc(L);
-        dtree.leaf_parent.alloc(L);
-        dtree.leaf_depth.alloc(L);
-        dtree.threshold_bin.alloc(L);
-        dtree.default_left.alloc(L);
-        dtree.split_gain.alloc(L);
-        dtree.internal_value.alloc(L);
-        dtree.internal_weight.alloc(L);
-        dtree.leaf_value.alloc(L);
-        dtree.leaf_weight.alloc(L);
-        dtree.internal_count.alloc(L);
-        dtree.leaf_count.alloc(L);
-        dtree.left_bins.alloc(static_cast<size_t>(L) * 8);
+        tree_layout = TreeLayout(L);
+        dtree.alloc(tree_layout.bytes);
         step_partial.alloc(2 * step_partial_pairs);
         tile_status.alloc(div_up(rows, STEP_TILE) + JMAX + 1);
         fin_counts.alloc(1);
@@ -1056,7 +1047,9 @@ struct Context {
         g.plans = d_plans.p;
         g.tl = d_tl.p;
         g.tk = d_tk.p;
-        g.leaf_t = d_leaf_t.p;
+        const TreeLayout &tl = tree_layout;
+        uint8_t *tp = dtree.p;
+        g.leaf_t = reinterpret_cast<int32_t *>(tp + tl.leaf_t);
         g.leaf_left = d_leaf_left.p;
         g.splittable = d_splittable.p;
         g.jobs = d_jobs.p;
@@ -1064,10 +1057,13 @@ struct Context {
         g.evaluate = d_eval.p;
         g.mask = d_mask.p;
         g.feats = dfeats.p;
-        g.tree = TreeDev{dtree.split_feature.p, dtree.threshold_bin.p, dtree.default_left.p, dtree.left_child.p,
-                         dtree.right_child.p, dtree.split_gain.p, dtree.internal_value.p, dtree.internal_weight.p,
-                         dtree.internal_count.p, dtree.leaf_value.p, dtree.leaf_weight.p, dtree.leaf_count.p,
-                         dtree.leaf_parent.p, dtree.leaf_depth.p, dtree.left_bins.p};
+        g.tree = TreeDev{reinterpret_cast<int32_t *>(tp + tl.sf), reinterpret_cast<uint32_t *>(tp + tl.tb), tp + tl.dl,
+                         reinterpret_cast<int32_t *>(tp + tl.lch), reinterpret_cast<int32_t *>(tp + tl.rch),
+                         reinterpret_cast<float *>(tp + tl.sg), reinterpret_cast<double *>(tp + tl.iv),
+                         reinterpret_cast<double *>(tp + tl.iw), reinterpret_cast<int64_t *>(tp + tl.ic),
+                         reinterpret_cast<double *>(tp + tl.lv), reinterpret_cast<double *>(tp + tl.lw),
+                         reinterpret_cast<int64_t *>(tp + tl.lc), reinterpret_cast<int32_t *>(tp + tl.lp),
+                         reinterpret_cast<int32_t *>(tp + tl.ld), reinterpret_cast<uint32_t *>(tp + tl.lb)};
         g.pool = pool.p;
         g.slot_stride = 2 * total_bins;
         g.nf = nf;
@@ -1293,37 +1289,30 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     if (hc.error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc.error));
     const uint32_t n = hc.num_leaves, ni = n - 1, ntent = hc.ntent;
     // one readback: speculative leaves, committed leaves and the tree arrays
-    auto padded = [](size_t bytes) { return (bytes + 7) & ~static_cast<size_t>(7); };
-    // what is read below: the speculative leaves, six 8-byte, eight 4-byte and one 1-byte array of L, the masks
-    const size_t need = padded(static_cast<size_t>(ntent) * sizeof(TLeaf)) + 6 * padded(static_cast<size_t>(L) * 8) +
-                        8 * padded(static_cast<size_t>(L) * 4) + padded(static_cast<size_t>(L) * 32) + padded(L);
-    h_result.alloc(need);
-    uint8_t *hp = h_result.p;
-    const uint8_t *hend = h_result.p + need;
-    auto rd = [&](void *dev, size_t bytes) {
-        if (hp + bytes > hend) fail(SROCM_ERR_INTERNAL, "tree readback outgrew its staging");
-        hip_check(hipMemcpyAsync(hp, dev, bytes, hipMemcpyDeviceToHost, stream), "read tree");
-        uint8_t *at = hp;
-        hp += padded(bytes);
-        return at;
-    };
-    const TLeaf *tl = reinterpret_cast<const TLeaf *>(rd(d_tl.p, ntent * sizeof(TLeaf)));
-    auto *iv = reinterpret_cast<const double *>(rd(dtree.internal_value.p, L * 8));
-    auto *iw = reinterpret_cast<const double *>(rd(dtree.internal_weight.p, L * 8));
-    auto *lv = reinterpret_cast<const double *>(rd(dtree.leaf_value.p, L * 8));
-    auto *lw = reinterpret_cast<const double *>(rd(dtree.leaf_weight.p, L * 8));
-    auto *ic = reinterpret_cast<const int64_t *>(rd(dtree.internal_count.p, L * 8));
-    auto *lcn = reinterpret_cast<const int64_t *>(rd(dtree.leaf_count.p, L * 8));
-    auto *lt = reinterpret_cast<const int32_t *>(rd(d_leaf_t.p, L * 4));
-    auto *sf = reinterpret_cast<const int32_t *>(rd(dtree.split_feature.p, L * 4));
-    auto *lc = reinterpret_cast<const int32_t *>(rd(dtree.left_child.p, L * 4));
-    auto *rc = reinterpret_cast<const int32_t *>(rd(dtree.right_child.p, L * 4));
-    auto *lp = reinterpret_cast<const int32_t *>(rd(dtree.leaf_parent.p, L * 4));
-    auto *ld = reinterpret_cast<const int32_t *>(rd(dtree.leaf_depth.p, L * 4));
-    auto *tb = reinterpret_cast<const uint32_t *>(rd(dtree.threshold_bin.p, L * 4));
-    auto *sgn = reinterpret_cast<const float *>(rd(dtree.split_gain.p, L * 4));
-    auto *lb = reinterpret_cast<const uint32_t *>(rd(dtree.left_bins.p, static_cast<size_t>(L) * 32));
-    auto *dl = reinterpret_cast<const uint8_t *>(rd(dtree.default_left.p, L));
+    // one readback of the speculative leaves and one of the tree block
+    const TreeLayout &lay = tree_layout;
+    const size_t tl_bytes = (static_cast<size_t>(ntent) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7);
+    h_result.alloc(tl_bytes + lay.bytes);
+    hip_check(hipMemcpyAsync(h_result.p, d_tl.p, static_cast<size_t>(ntent) * sizeof(TLeaf), hipMemcpyDeviceToHost, stream), "read leaves");
+    hip_check(hipMemcpyAsync(h_result.p + tl_bytes, dtree.p, lay.bytes, hipMemcpyDeviceToHost, stream), "read tree");
+    const TLeaf *tl = reinterpret_cast<const TLeaf *>(h_result.p);
+    const uint8_t *hb = h_result.p + tl_bytes;
+    auto *iv = reinterpret_cast<const double *>(hb + lay.iv);
+    auto *iw = reinterpret_cast<const double *>(hb + lay.iw);
+    auto *lv = reinterpret_cast<const double *>(hb + lay.lv);
+    auto *lw = reinterpret_cast<const double *>(hb + lay.lw);
+    auto *ic = reinterpret_cast<const int64_t *>(hb + lay.ic);
+    auto *lcn = reinterpret_cast<const int64_t *>(hb + lay.lc);
+    auto *lt = reinterpret_cast<const int32_t *>(hb + lay.leaf_t);
+    auto *sf = reinterpret_cast<const int32_t *>(hb + lay.sf);
+    auto *lc = reinterpret_cast<const int32_t *>(hb + lay.lch);
+    auto *rc = reinterpret_cast<const int32_t *>(hb + lay.rch);
+    auto *lp = reinterpret_cast<const int32_t *>(hb + lay.lp);
+    auto *ld = reinterpret_cast<const int32_t *>(hb + lay.ld);
+    auto *tb = reinterpret_cast<const uint32_t *>(hb + lay.tb);
+    auto *sgn = reinterpret_cast<const float *>(hb + lay.sg);
+    auto *lb = reinterpret_cast<const uint32_t *>(hb + lay.lb);
+    auto *dl = reinterpret_cast<const uint8_t *>(hb + lay.dl);
     sync();
     tree = HostTree{};
     tree.num_leaves = n;

@@ -777,6 +777,49 @@ __device__ __forceinline__ int wave_min(int v) {
 }
 __device__ __forceinline__ double readlane_f64(double v, uint32_t lane) { return double_of(readlane_u64(bits_of(v), lane)); }
 
+// Branch-free all-reductions: a lane without a source in a DPP step reads the reduction's identity (the `old`
+// operand with bound_ctrl off), so every step is one move and one max or min.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_min_step(int v) {
+    const int o = __builtin_amdgcn_update_dpp(0x7fffffff, v, CTRL, ROW_MASK, 0xf, false);
+    return o < v ? o : v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = dpp_min_step<DPP_ROW_SHR1, 0xf>(v);
+    v = dpp_min_step<DPP_ROW_SHR2, 0xf>(v);
+    v = dpp_min_step<DPP_ROW_SHR4, 0xf>(v);
+    v = dpp_min_step<DPP_ROW_SHR8, 0xf>(v);
+    v = dpp_min_step<DPP_ROW_BCAST15, 0xa>(v);
+    v = dpp_min_step<DPP_ROW_BCAST31, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_max_step(double v) {  // v is never NaN
+    const uint64_t b = bits_of(v), id = bits_of(-__builtin_inf());
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(id)),
+                                                                          static_cast<int>(static_cast<uint32_t>(b)), CTRL, ROW_MASK, 0xf, false));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(id >> 32)),
+                                                                          static_cast<int>(static_cast<uint32_t>(b >> 32)), CTRL, ROW_MASK, 0xf, false));
+    const double o = double_of((static_cast<uint64_t>(hi) << 32) | lo);
+    return o > v ? o : v;
+}
+__device__ __forceinline__ double wave_max_f64(double v) {
+    v = dpp_max_step<DPP_ROW_SHR1, 0xf>(v);
+    v = dpp_max_step<DPP_ROW_SHR2, 0xf>(v);
+    v = dpp_max_step<DPP_ROW_SHR4, 0xf>(v);
+    v = dpp_max_step<DPP_ROW_SHR8, 0xf>(v);
+    v = dpp_max_step<DPP_ROW_BCAST15, 0xa>(v);
+    v = dpp_max_step<DPP_ROW_BCAST31, 0xc>(v);
+    return readlane_f64(v, 63);
+}
+// wave_best for gains that are never NaN: the highest gain, then the lowest index among the lanes holding it.
+__device__ __forceinline__ void wave_argmax(double &g, int &i) {
+    const double m = wave_max_f64(i >= 0 ? g : -__builtin_inf());
+    const int w = wave_min_i32(i >= 0 && g == m ? i : 0x7fffffff);
+    g = m;
+    i = w == 0x7fffffff ? -1 : w;
+}
+
 // A feature candidate as held by lane `owner`, broadcast to the wave.
 __device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
     FeatCand r;
@@ -1809,10 +1852,10 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             }
             // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
             // otherwise the first highest gain among the rest (a NaN later never wins)
-            const int first = wave_min(lf);
+            const int first = wave_min_i32(lf);
             double kg = lg;
             int ki = li;
-            wave_best(kg, ki);
+            wave_argmax(kg, ki);
             const bool nan_first = first < (1 << 30) && (first & 1);
             if (nan_first || ki < 0 || !(kg > 0.0)) {
                 done = true;
@@ -1934,6 +1977,7 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const uint32_t ki = s.cand[i];
         const double gi = s.cgain[i];
         uint32_t rank = 0;
+#pragma unroll 8
         for (uint32_t j = 0; j < ncand; ++j) {
             const double gj = s.cgain[j];
             const uint32_t kj = s.cand[j];
