@@ -325,6 +325,9 @@ struct Context {
     Pinned<uint8_t> h_stage;  // per-split uploads (jobs, evaluate flags), rewritten only after a sync
 
     DevBuf<DevNode> d_nodes;
+    Pinned<DevNode> h_nodes;
+    Pinned<float> h_lv;
+    DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
     DevBuf<LeafJob> d_leaf_jobs;
     DevBuf<unsigned long long> d_leaf_out;
@@ -824,10 +827,11 @@ struct Context {
         for (uint32_t i = 0; i < 2 * n; ++i) out[i] = static_cast<int64_t>(h.p[i]);
     }
 
-    void add_tree(const srocm_device_node *nodes, uint32_t nn, const float *lv, uint32_t nl) {
-        require_loaded();
+    // A tree's nodes, checked, into d_nodes (through pinned staging, rewritten only after a sync).
+    void upload_nodes(const srocm_device_node *nodes, uint32_t nn, uint32_t nl) {
         if (nl == 0 || nl != nn + 1) fail(SROCM_ERR_DEVICE, "tree with " + std::to_string(nn) + " nodes and " + std::to_string(nl) + " leaves");
-        std::vector<DevNode> dn(nn);
+        h_nodes.alloc(std::max<uint32_t>(nn, 1));
+        DevNode *dn = h_nodes.p;
         for (uint32_t k = 0; k < nn; ++k) {
             const srocm_device_node &n = nodes[k];
             if (n.split.group >= group_col_nt.size() || n.split.column >= group_col_nt[n.split.group].size() ||
@@ -844,18 +848,68 @@ struct Context {
             dn[k].pad = 0;
         }
         d_nodes.alloc(std::max<uint32_t>(nn, 1));
+        if (nn) hip_check(hipMemcpyAsync(d_nodes.p, dn, nn * sizeof(DevNode), hipMemcpyHostToDevice, stream), "upload tree");
+    }
+
+    void upload_leaf_values(const float *lv, uint32_t nl) {
+        h_lv.alloc(nl);
+        std::copy(lv, lv + nl, h_lv.p);
         d_leaf_values.alloc(nl);
-        if (nn) hip_check(hipMemcpyAsync(d_nodes.p, dn.data(), nn * sizeof(DevNode), hipMemcpyHostToDevice, stream), "upload tree");
-        hip_check(hipMemcpyAsync(d_leaf_values.p, lv, nl * sizeof(float), hipMemcpyHostToDevice, stream), "upload leaves");
-        auto apply = [&](DevData &d) {
-            if (d.rows == 0) return;
-            if (nn == 0) k_add_const<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, lv[0]);
-            else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p);
-            launch_check("k_add_tree");
-        };
-        apply(train);
-        for (auto &v : valid) apply(v);
-        sync();  // the host tree arrays may be reused
+        hip_check(hipMemcpyAsync(d_leaf_values.p, h_lv.p, nl * sizeof(float), hipMemcpyHostToDevice, stream), "upload leaves");
+    }
+
+    // scores += the uploaded tree's leaf values, through a walk per row, or (train, leaf_of) the leaves k_tree_leaves
+    // recorded
+    void apply_tree(DevData &d, uint32_t nn, float v0, bool from_leaf_of) {
+        if (d.rows == 0) return;
+        if (nn == 0) k_add_const<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, v0);
+        else if (from_leaf_of) k_add_leaf_values<<<grid_rows(d.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, d.scores.p, d.rows);
+        else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p);
+        launch_check("k_add_tree");
+    }
+
+    void add_tree(const srocm_device_node *nodes, uint32_t nn, const float *lv, uint32_t nl) {
+        require_loaded();
+        upload_nodes(nodes, nn, nl);
+        upload_leaf_values(lv, nl);
+        apply_tree(train, nn, lv[0], false);
+        for (auto &v : valid) apply_tree(v, nn, lv[0], false);
+        sync();  // the staging is rewritten by the next call
+    }
+
+    // The uploaded tree's leaf of every training row (leaf_of) and, when `sums` is set, the leaves' fixed-point
+    // gradient sums over the in-bag rows, as leaf_sums over the grown tree's leaves gives them.
+    void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums) {
+        leaf_of.alloc(rows);
+        TreeLeavesArgs a{};
+        a.colbins = train.col.p;
+        a.rows = rows;
+        a.nodes = d_nodes.p;
+        a.nn = nn;
+        a.nl = nl;
+        a.leaf_of = leaf_of.p;
+        if (sums) {
+            d_leaf_out.alloc(2 * nl);
+            hip_check(hipMemsetAsync(d_leaf_out.p, 0, 2 * nl * 8, stream), "zero sums");
+            a.grad = grad.p;
+            a.hess = hess.p;
+            a.gs = gs;
+            a.hs = hs;
+            a.sums = reinterpret_cast<unsigned long long *>(d_leaf_out.p);
+            a.bag = bag.kind == SROCM_BAG_BERNOULLI ? 1u : 0u;
+            a.bag_seed = bag.seed;
+            a.bag_round = bag.round;
+            a.row_offset = row_offset;
+            a.fraction = bag.fraction;
+        }
+        k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, 1024)), 256, 0, stream>>>(a);
+        launch_check("k_tree_leaves");
+        if (!sums) return;
+        Pinned<unsigned long long> h;
+        h.alloc(2 * nl);
+        hip_check(hipMemcpyAsync(h.p, d_leaf_out.p, 2 * nl * 8, hipMemcpyDeviceToHost, stream), "read sums");
+        sync();
+        for (uint32_t i = 0; i < 2 * nl; ++i) sums[i] = static_cast<int64_t>(h.p[i]);
     }
 
     DevData &dataset(uint32_t i) {
@@ -1080,7 +1134,10 @@ struct Context {
         return g;
     }
 
-    void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves);
+    // `final_order`: leave every leaf's rows ascending in the partition (the reference's order); without it the rows
+    // of each leaf are only grouped, which is all the boosting loop needs before the next tree resets them.
+    void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves,
+              bool final_order = true);
 
     void copy_tree(const HostTree &t, const std::vector<GrowLeaf> &leaves, srocm_grown_tree *out) const {
         if (out->capacity_leaves < t.num_leaves) fail(SROCM_ERR_DEVICE, "grown tree has more leaves than the output holds");
@@ -1179,7 +1236,7 @@ std::pair<double, double> Context::compute_gradients() {
 // subtracts, searches the children and writes the tree. The host checks for the end of the tree once per batch of
 // steps (sized by the last tree's step count), reads the finished tree, and enqueues the final row order.
 void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits,
-                   std::vector<GrowLeaf> &leaves) {
+                   std::vector<GrowLeaf> &leaves, bool final_order) {
     require_loaded();
     if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
     check_range(spec.root);
@@ -1349,12 +1406,12 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     // the final row order (cpu.rs:556-599 keeps every leaf ascending): each unexpanded speculative leaf's rows into
     // the first buffer in ascending order, then each leaf whose expansion was dropped merged from its runs
     std::vector<RowRun> runs;
-    for (uint32_t k = 0; k < ntent; ++k)
+    for (uint32_t k = 0; k < ntent && final_order; ++k)
         if (tl[k].state == T_LEAF && tl[k].count && (tl[k].buf || tl[k].rev))
             runs.push_back(RowRun{tl[k].begin, tl[k].count, tl[k].buf, tl[k].rev});
     std::vector<MergeJob> merges;
     std::vector<uint32_t> starts;
-    for (uint32_t i = 0; i < n; ++i) {
+    for (uint32_t i = 0; i < n && final_order; ++i) {
         const uint32_t k = static_cast<uint32_t>(lt[i]);
         if (tl[k].state != T_EXPANDED) continue;
         MergeJob m{tl[k].begin, tl[k].count, static_cast<uint32_t>(starts.size()), 0};
@@ -1515,7 +1572,8 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         gs.feature_mask = mask.data();
         gs.root = srocm_leaf_range{0, local_rows};
         gs.root_count = local_rows;
-        grow(gs, tree, splits, leaves);
+        const bool last = it + 1 == first + count;
+        grow(gs, tree, splits, leaves, last);
         if (tree.num_leaves == 1) {  // boosting.rs:301-310
             if (trees_added == 0) {
                 HostTree c;
@@ -1526,12 +1584,19 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             }
             break;
         }
-        if (p.quant_train_renew_leaf) {  // learner.rs:376-404
+        std::vector<srocm_device_node> nodes(splits.size());
+        for (size_t k = 0; k < nodes.size(); ++k) {
+            nodes[k].split = splits[k];
+            nodes[k].left = tree.left_child[k];
+            nodes[k].right = tree.right_child[k];
+        }
+        const uint32_t nn = static_cast<uint32_t>(nodes.size()), nl = tree.num_leaves;
+        upload_nodes(nodes.data(), nn, nl);
+        static_assert(GROW_MAX_LEAVES <= LEAVES_MAX_LDS, "k_tree_leaves takes every device-grown tree");
+        if (p.quant_train_renew_leaf) {  // learner.rs:376-404: the rows' leaves from one walk give the sums and the scores
             float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
-            std::vector<srocm_leaf_range> ranges(leaves.size());
-            for (size_t i = 0; i < leaves.size(); ++i) ranges[i] = leaves[i].range;
-            std::vector<int64_t> sums(2 * leaves.size());
-            leaf_sums(ranges.data(), static_cast<uint32_t>(ranges.size()), gsc, hsc, sums.data());
+            std::vector<int64_t> sums(2 * static_cast<size_t>(nl));
+            tree_leaves(nn, nl, bag, gsc, hsc, sums.data());
             for (size_t l = 0; l < leaves.size(); ++l) {
                 double sum_grad = static_cast<double>(sums[2 * l]) / static_cast<double>(gsc);
                 double sum_hess = static_cast<double>(sums[2 * l + 1]) / static_cast<double>(hsc);
@@ -1541,19 +1606,15 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         }
         // boosting.rs:313-324
         tree.shrink(p.learning_rate);
-        std::vector<srocm_device_node> nodes(splits.size());
-        for (size_t k = 0; k < nodes.size(); ++k) {
-            nodes[k].split = splits[k];
-            nodes[k].left = tree.left_child[k];
-            nodes[k].right = tree.right_child[k];
-        }
         std::vector<float> lv(tree.leaf_value.size());
         for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i]);
         if (trees_added == 0 && init_score_value != 0.0) {
             tree.add_bias(init_score_value);
             for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i] - init_score_value);  // replay.rs:38-40
         }
-        add_tree(nodes.data(), static_cast<uint32_t>(nodes.size()), lv.data(), static_cast<uint32_t>(lv.size()));
+        upload_leaf_values(lv.data(), nl);
+        apply_tree(train, nn, lv[0], p.quant_train_renew_leaf != 0);
+        for (auto &v : valid) apply_tree(v, nn, lv[0], false);
         if (trees) copy_tree(tree, leaves, &trees[done]);
         ++done;
         ++trees_added;

@@ -577,6 +577,80 @@ __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint64_t rows, c
     }
 }
 
+// Each row's leaf from a walk down the tree (nodes in LDS; four rows per thread in flight), in row order, and the
+// leaves' exact fixed-point sums rint(v * scale) of the in-bag rows' gradients: the sums k_leaf_sums makes over the
+// final partition (integers, so the order does not matter; cpu.rs:886-908). grid: any, 256 threads.
+struct TreeLeavesArgs {
+    const uint8_t *colbins;            // column-major bins [feature][rows]
+    uint64_t rows;
+    const DevNode *nodes;
+    uint32_t nn, nl;                   // internal nodes, leaves (nn >= 1, nl <= LEAVES_MAX_LDS)
+    uint16_t *leaf_of;                 // [rows]
+    const float *grad, *hess;          // null: no sums
+    float gs, hs;
+    unsigned long long *sums;          // [nl][2], zeroed before
+    uint32_t bag, bag_seed, bag_round; // bag != 0: only rows in the bag (quantize.rs:147-149) are summed
+    uint64_t row_offset;
+    double fraction;
+};
+constexpr uint32_t LEAVES_MAX_LDS = 512;  // the trees k_tree_leaves takes (device growth grows up to this)
+
+__global__ __launch_bounds__(256) void k_tree_leaves(TreeLeavesArgs a) {
+    __shared__ DevNode sn[LEAVES_MAX_LDS - 1];
+    __shared__ unsigned long long ls[LEAVES_MAX_LDS][2];
+    for (uint32_t k = threadIdx.x; k < a.nn; k += blockDim.x) sn[k] = a.nodes[k];
+    if (a.grad)
+        for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
+    __syncthreads();
+    const uint64_t stride = 4ull * gridDim.x * blockDim.x;
+    for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; base < a.rows; base += stride) {
+        uint64_t r[4];
+        int32_t nd[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            r[k] = base + static_cast<uint64_t>(k) * gridDim.x * blockDim.x;
+            nd[k] = r[k] < a.rows ? 0 : -1;
+        }
+        for (;;) {
+            uint32_t b[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) b[k] = nd[k] >= 0 ? a.colbins[static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]] : 0u;
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (nd[k] < 0) continue;
+                const DevNode &x = sn[nd[k]];
+                nd[k] = ((x.left_bins[b[k] >> 5] >> (b[k] & 31u)) & 1u) ? x.left : x.right;
+                any = any || nd[k] >= 0;
+            }
+            if (!any) break;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (r[k] >= a.rows) continue;
+            const uint32_t leaf = static_cast<uint32_t>(~nd[k]);
+            a.leaf_of[r[k]] = static_cast<uint16_t>(leaf);
+            if (!a.grad) continue;
+            if (a.bag && !(static_cast<double>(uniform(a.bag_seed, 2u, a.bag_round, a.row_offset + r[k])) < a.fraction)) continue;
+            atomicAdd(&ls[leaf][0], static_cast<unsigned long long>(to_fixed(a.grad[r[k]], a.gs)));
+            atomicAdd(&ls[leaf][1], static_cast<unsigned long long>(to_fixed(a.hess[r[k]], a.hs)));
+        }
+    }
+    if (!a.grad) return;
+    __syncthreads();
+    for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) {
+        if (ls[l][0]) atomicAdd(&a.sums[2 * l], ls[l][0]);
+        if (ls[l][1]) atomicAdd(&a.sums[2 * l + 1], ls[l][1]);
+    }
+}
+
+// scores[r] += the value of row r's leaf: the f32 add of k_add_tree, in row order.
+__global__ void k_add_leaf_values(const uint16_t *__restrict__ leaf_of, const float *__restrict__ leaf_values,
+                                  float *__restrict__ scores, uint64_t rows) {
+    for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
+        scores[r] += leaf_values[leaf_of[r]];
+}
+
 __global__ void k_add_const(float *__restrict__ scores, uint64_t rows, float v) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
         scores[r] += v;
