@@ -326,6 +326,7 @@ struct Context {
 
     DevBuf<DevNode> d_nodes;
     Pinned<DevNode> h_nodes;
+    Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
@@ -820,7 +821,7 @@ struct Context {
         dim3 grid(std::max<uint32_t>(1, div_up(maxc, chunk)), n);
         k_leaf_sums<<<grid, 256, 0, stream>>>(grad.p, hess.p, part.p, d_leaf_jobs.p, gs, hs, d_leaf_out.p, chunk);
         launch_check("k_leaf_sums");
-        Pinned<unsigned long long> h;
+        Pinned<unsigned long long> &h = h_sums;
         h.alloc(2 * n);
         hip_check(hipMemcpyAsync(h.p, d_leaf_out.p, 2 * n * 8, hipMemcpyDeviceToHost, stream), "read sums");
         sync();
@@ -905,7 +906,7 @@ struct Context {
         k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, 1024)), 256, 0, stream>>>(a);
         launch_check("k_tree_leaves");
         if (!sums) return;
-        Pinned<unsigned long long> h;
+        Pinned<unsigned long long> &h = h_sums;
         h.alloc(2 * nl);
         hip_check(hipMemcpyAsync(h.p, d_leaf_out.p, 2 * nl * 8, hipMemcpyDeviceToHost, stream), "read sums");
         sync();
@@ -1025,7 +1026,6 @@ struct Context {
 
     DevBuf<int64_t> pool;             // histogram slots, 2 * total_bins i64 each
     DevBuf<StepPlan> d_plans;         // [2], by step parity
-    DevBuf<GrowCtl> d_ctl;
     DevBuf<TLeaf> d_tl;               // the speculative tree's leaves
     DevBuf<TKey> d_tk;
     DevBuf<uint8_t> d_leaf_left;
@@ -1036,23 +1036,24 @@ struct Context {
     DevBuf<MergeJob> d_merges;        // end of a tree: leaves whose expansion was dropped
     DevBuf<uint32_t> d_starts;
     Pinned<uint8_t> h_fix;            // staging of the runs and merges (rewritten only after a sync)
-    Pinned<GrowCtl> h_ctl;
     // split steps (k_step_rows, k_step_finish)
     DevBuf<int32_t> step_partial;            // per slab: [cus + JMAX][256 * W] {g, h}
     DevBuf<unsigned long long> tile_status;  // per partition tile
     DevBuf<uint32_t> fin_counts;             // the jobs-selected counter of k_step_select
     uint64_t epochs_used = 0;
     uint32_t last_steps = 0;                 // split steps of the last tree (the first guess for the next)
-    // The tree arrays and the committed leaves' speculative leaves, in one allocation so that a tree comes back in
-    // one copy: 8-byte arrays, then 4-byte arrays, the left-bin masks and the default-left flags, each padded to 8 B.
+    // The control block, the tree arrays, the leaves' row ranges and the committed leaves' speculative leaves, in one
+    // allocation so that the check for the end of a tree brings the tree back with it: 8-byte arrays, then 4-byte
+    // arrays, the left-bin masks and the default-left flags, each padded to 8 B.
     struct TreeLayout {
-        size_t iv, iw, lv, lw, ic, lc, leaf_t, sf, lch, rch, lp, ld, tb, sg, lb, dl, bytes;
+        size_t ctl, iv, iw, lv, lw, ic, lc, leaf_t, sf, lch, rch, lp, ld, tb, sg, lr, lb, dl, bytes;
         explicit TreeLayout(uint32_t L = 0) {
             size_t at = 0;
             auto take = [&](size_t n) { size_t o = at; at += (n + 7) & ~static_cast<size_t>(7); return o; };
+            ctl = take(sizeof(GrowCtl));
             iv = take(8ull * L); iw = take(8ull * L); lv = take(8ull * L); lw = take(8ull * L); ic = take(8ull * L); lc = take(8ull * L);
             leaf_t = take(4ull * L); sf = take(4ull * L); lch = take(4ull * L); rch = take(4ull * L); lp = take(4ull * L);
-            ld = take(4ull * L); tb = take(4ull * L); sg = take(4ull * L); lb = take(32ull * L); dl = take(L);
+            ld = take(4ull * L); tb = take(4ull * L); sg = take(4ull * L); lr = take(8ull * L); lb = take(32ull * L); dl = take(L);
             bytes = at;
         }
     };
@@ -1069,7 +1070,6 @@ struct Context {
         const uint32_t tcap = grow_tcap(L), nslots = tcap / 2 + 1;
         pool.alloc(static_cast<size_t>(nslots) * 2 * total_bins);
         d_plans.alloc(2);
-        d_ctl.alloc(1);
         d_tl.alloc(tcap);
         d_tk.alloc(tcap);
         d_leaf_left.alloc(L);
@@ -1080,6 +1080,12 @@ struct Context {
         d_cands.alloc(static_cast<size_t>(JMAX) * 2 * nf);
         tree_layout = TreeLayout(L);
         dtree.alloc(tree_layout.bytes);
+        // host staging at its largest, so that no tree allocates pinned memory
+        h_result.alloc(((static_cast<size_t>(grow_tcap(L)) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7)) + tree_layout.bytes);
+        h_fix.alloc(static_cast<size_t>(grow_tcap(L)) * (sizeof(RowRun) + sizeof(MergeJob) + 8) + 64);
+        h_nodes.alloc(L);
+        h_lv.alloc(L);
+        h_sums.alloc(2 * static_cast<size_t>(L));
         step_partial.alloc(2 * step_partial_pairs);
         tile_status.alloc(div_up(rows, STEP_TILE) + JMAX + 1);
         fin_counts.alloc(1);
@@ -1089,7 +1095,7 @@ struct Context {
 
     // Tile status words carry the step's epoch; the counters are returned to zero by the kernels themselves.
     void reset_step_state() {
-        hip_check(hipMemsetAsync(d_ctl.p, 0, sizeof(GrowCtl), stream), "zero grow control");
+        hip_check(hipMemsetAsync(dtree.p + tree_layout.ctl, 0, sizeof(GrowCtl), stream), "zero grow control");
         hip_check(hipMemsetAsync(tile_status.p, 0, tile_status.n * sizeof(unsigned long long), stream), "zero tile status");
         hip_check(hipMemsetAsync(fin_counts.p, 0, fin_counts.n * sizeof(uint32_t), stream), "zero step counters");
         epochs_used = 0;
@@ -1097,12 +1103,12 @@ struct Context {
 
     GrowState grow_state(const srocm_grow_spec &spec) {
         GrowState g{};
-        g.ctl = d_ctl.p;
         g.plans = d_plans.p;
         g.tl = d_tl.p;
         g.tk = d_tk.p;
         const TreeLayout &tl = tree_layout;
         uint8_t *tp = dtree.p;
+        g.ctl = reinterpret_cast<GrowCtl *>(tp + tl.ctl);
         g.leaf_t = reinterpret_cast<int32_t *>(tp + tl.leaf_t);
         g.leaf_left = d_leaf_left.p;
         g.splittable = d_splittable.p;
@@ -1117,7 +1123,8 @@ struct Context {
                          reinterpret_cast<double *>(tp + tl.iw), reinterpret_cast<int64_t *>(tp + tl.ic),
                          reinterpret_cast<double *>(tp + tl.lv), reinterpret_cast<double *>(tp + tl.lw),
                          reinterpret_cast<int64_t *>(tp + tl.lc), reinterpret_cast<int32_t *>(tp + tl.lp),
-                         reinterpret_cast<int32_t *>(tp + tl.ld), reinterpret_cast<uint32_t *>(tp + tl.lb)};
+                         reinterpret_cast<int32_t *>(tp + tl.ld), reinterpret_cast<uint32_t *>(tp + tl.lb),
+                         reinterpret_cast<uint32_t *>(tp + tl.lr)};
         g.pool = pool.p;
         g.slot_stride = 2 * total_bins;
         g.nf = nf;
@@ -1267,11 +1274,15 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     uint64_t used_root = 0;
     for (uint32_t f = 0; f < nf; ++f)
         if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
-    h_ctl.alloc(1);
+    // the tree block comes back with every check for the end of the tree
+    const TreeLayout &lay = tree_layout;
+    const size_t tl_max = (static_cast<size_t>(grow_tcap(L)) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7);
+    h_result.alloc(tl_max + lay.bytes);
+    uint8_t *hb = h_result.p + tl_max;
     auto read_ctl = [&]() {
-        hip_check(hipMemcpyAsync(h_ctl.p, d_ctl.p, sizeof(GrowCtl), hipMemcpyDeviceToHost, stream), "read grow control");
+        hip_check(hipMemcpyAsync(hb, dtree.p, lay.bytes, hipMemcpyDeviceToHost, stream), "read tree");
         sync();
-        return *h_ctl.p;
+        return *reinterpret_cast<const GrowCtl *>(hb + lay.ctl);
     };
     GrowCtl hc{};
     if (root_searched) {
@@ -1299,7 +1310,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 for (size_t si = 0; si < slabs.size(); ++si) {
                     const Slab &sl = slabs[si];
                     StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
-                                sl.col_bins.p, tile_status.p, d_plans.p + parity, d_ctl.p, flush_rows(), si == 0 ? 1u : 0u};
+                                sl.col_bins.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
                     switch (sl.width) {
                     case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 64: k_step_rows<64><<<k1_groups(), 1024, 0, stream>>>(sa); break;
@@ -1345,15 +1356,6 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     if (hc.error == 3) fail(SROCM_ERR_INTERNAL, "a partition tile waited too long for an earlier tile's count");
     if (hc.error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc.error));
     const uint32_t n = hc.num_leaves, ni = n - 1, ntent = hc.ntent;
-    // one readback: speculative leaves, committed leaves and the tree arrays
-    // one readback of the speculative leaves and one of the tree block
-    const TreeLayout &lay = tree_layout;
-    const size_t tl_bytes = (static_cast<size_t>(ntent) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7);
-    h_result.alloc(tl_bytes + lay.bytes);
-    hip_check(hipMemcpyAsync(h_result.p, d_tl.p, static_cast<size_t>(ntent) * sizeof(TLeaf), hipMemcpyDeviceToHost, stream), "read leaves");
-    hip_check(hipMemcpyAsync(h_result.p + tl_bytes, dtree.p, lay.bytes, hipMemcpyDeviceToHost, stream), "read tree");
-    const TLeaf *tl = reinterpret_cast<const TLeaf *>(h_result.p);
-    const uint8_t *hb = h_result.p + tl_bytes;
     auto *iv = reinterpret_cast<const double *>(hb + lay.iv);
     auto *iw = reinterpret_cast<const double *>(hb + lay.iw);
     auto *lv = reinterpret_cast<const double *>(hb + lay.lv);
@@ -1370,7 +1372,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     auto *sgn = reinterpret_cast<const float *>(hb + lay.sg);
     auto *lb = reinterpret_cast<const uint32_t *>(hb + lay.lb);
     auto *dl = reinterpret_cast<const uint8_t *>(hb + lay.dl);
-    sync();
+    auto *lrg = reinterpret_cast<const uint32_t *>(hb + lay.lr);
     tree = HostTree{};
     tree.num_leaves = n;
     tree.split_feature.assign(sf, sf + ni);
@@ -1392,7 +1394,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     for (uint32_t i = 0; i < n; ++i) {
         const int32_t k = lt[i];
         if (k < 0 || static_cast<uint32_t>(k) >= ntent) fail(SROCM_ERR_INTERNAL, "device learner lost a leaf");
-        leaves[i].range = srocm_leaf_range{tl[k].begin, tl[k].count};
+        leaves[i].range = srocm_leaf_range{lrg[2 * i], lrg[2 * i + 1]};
     }
     splits.assign(ni, srocm_bin_split{});
     for (uint32_t k = 0; k < ni; ++k) {  // learner.rs:432-452, as the device planned each split
@@ -1405,13 +1407,18 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
 
     // the final row order (cpu.rs:556-599 keeps every leaf ascending): each unexpanded speculative leaf's rows into
     // the first buffer in ascending order, then each leaf whose expansion was dropped merged from its runs
+    const TLeaf *tl = reinterpret_cast<const TLeaf *>(h_result.p);
+    if (final_order && root_searched) {
+        hip_check(hipMemcpyAsync(h_result.p, d_tl.p, static_cast<size_t>(ntent) * sizeof(TLeaf), hipMemcpyDeviceToHost, stream), "read leaves");
+        sync();
+    }
     std::vector<RowRun> runs;
-    for (uint32_t k = 0; k < ntent && final_order; ++k)
+    for (uint32_t k = 0; k < ntent && final_order && root_searched; ++k)
         if (tl[k].state == T_LEAF && tl[k].count && (tl[k].buf || tl[k].rev))
             runs.push_back(RowRun{tl[k].begin, tl[k].count, tl[k].buf, tl[k].rev});
     std::vector<MergeJob> merges;
     std::vector<uint32_t> starts;
-    for (uint32_t i = 0; i < n && final_order; ++i) {
+    for (uint32_t i = 0; i < n && final_order && root_searched; ++i) {
         const uint32_t k = static_cast<uint32_t>(lt[i]);
         if (tl[k].state != T_EXPANDED) continue;
         MergeJob m{tl[k].begin, tl[k].count, static_cast<uint32_t>(starts.size()), 0};

@@ -1629,6 +1629,7 @@ struct TreeDev {
     int64_t *leaf_count;
     int32_t *leaf_parent, *leaf_depth;
     uint32_t *left_bins;  // [node][8]: the bins that go left (BinSplit::left_bins)
+    uint32_t *leaf_range; // [leaf][2]: the leaf's rows in the partition (begin, count)
 };
 
 // One leaf expanded by a split step (learner.rs:249-290): written by advance, read by the step's kernels.
@@ -1806,6 +1807,8 @@ __global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_coun
         g.tree.leaf_count[0] = 0;
         g.tree.leaf_parent[0] = -1;
         g.tree.leaf_depth[0] = 0;
+        g.tree.leaf_range[0] = root_begin;
+        g.tree.leaf_range[1] = root_count;
     }
 }
 
@@ -2013,6 +2016,8 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         t.leaf_count[id] = l.cnt;
         t.leaf_parent[id] = s.pnode[id];
         t.leaf_depth[id] = l.depth;
+        t.leaf_range[2 * id] = l.begin;
+        t.leaf_range[2 * id + 1] = l.count;
         g.leaf_t[id] = static_cast<int32_t>(k);
         g.leaf_left[id] = s.is_left[id];
     }
