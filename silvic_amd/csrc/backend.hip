@@ -664,7 +664,7 @@ struct Context {
                 prof.hist_launches += 1;
             }
             ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
-            k_hist_reduce<<<div_up(256ull * s.width, 256), 256, 0, stream>>>(r);
+            k_hist_reduce<<<div_up(256ull * s.width, 32), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
         if (prof.on) {
@@ -1062,7 +1062,7 @@ struct Context {
     uint32_t grow_capacity = 0;
 
     uint32_t k1_groups() const { return cus + JMAX; }  // k_step_rows' grid
-    uint32_t k2_blocks() const { return cus; }         // k_step_scan's grid: one 1024-thread block per CU
+    uint32_t scan_blocks() const { return 8 * cus; }   // k_step_scan's grid: four waves a block, a wave per item
     uint32_t reduce_blocks() const { return 8 * cus; } // k_step_reduce's grid
 
     void ensure_grow(uint32_t L) {
@@ -1327,7 +1327,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
                 ScanStepArgs sca{d_cgs.p, gcol_feat.p, cat_feats.p, ncat, d_plans.p + parity};
-                k_step_scan<<<k2_blocks(), 1024, 0, stream>>>(g, sca);
+                k_step_scan<<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 launch_check("k_step_scan");
                 if (ncat) {
                     k_step_cat<<<std::min<uint32_t>(cus * 2, div_up(static_cast<uint64_t>(JMAX) * 2 * ncat, 4)), 256, 0, stream>>>(g, sca);

@@ -347,23 +347,38 @@ struct ReduceArgs {
     uint32_t width;     // W
 };
 
-__global__ void k_hist_reduce(ReduceArgs a) {
+// A block takes 32 slots (bin * W + column) and splits the workgroups' partials of each into 8 stripes that meet in
+// LDS. grid: ceil(256 * W / 32) blocks of 256 threads.
+__global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
+    __shared__ int64_t red[2][8][32];
     uint32_t lb, n;
     leaf_rows(a.dev_left, a.begin, a.count, a.side, lb, n);
     uint32_t groups, per;
     hist_split(n, a.max_groups, a.min_rows_per_group, groups, per);
-    uint32_t slots = 256u * a.width;
-    for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < slots; s += gridDim.x * blockDim.x) {
-        uint32_t col = s % a.width, bin = s / a.width;
-        if (bin >= a.col_bins[col]) continue;
-        int64_t g = 0, h = 0;
+    const uint32_t slots = 256u * a.width;
+    const uint32_t tid = threadIdx.x, lane = tid & 31u, stripe = tid >> 5;
+    const uint32_t s = blockIdx.x * 32u + lane, col = s % a.width, bin = s / a.width;
+    const bool on = s < slots && bin < a.col_bins[col];
+    int64_t g = 0, h = 0;
+    if (on) {
         const int2 *p = reinterpret_cast<const int2 *>(a.partial) + s;
-        for (uint32_t w = 0; w < groups; ++w) {
-            int2 v = p[(size_t)w * slots];
+#pragma unroll 8
+        for (uint32_t w = stripe; w < groups; w += 8u) {
+            const int2 v = p[static_cast<size_t>(w) * slots];
             g += v.x;
             h += v.y;
         }
-        size_t o = 2 * ((size_t)a.col_offset[col] + bin);
+    }
+    red[0][stripe][lane] = g;
+    red[1][stripe][lane] = h;
+    __syncthreads();
+    if (stripe == 0 && on) {
+#pragma unroll
+        for (int k = 1; k < 8; ++k) {
+            g += red[0][k][lane];
+            h += red[1][k][lane];
+        }
+        const size_t o = 2 * (static_cast<size_t>(a.col_offset[col]) + bin);
         a.out[o] = g;
         a.out[o + 1] = h;
         if (a.parent) {
@@ -1552,7 +1567,8 @@ __device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_
     return word;
 }
 
-constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: two per thread of a 1024-thread block
+constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: TILE_RPT per thread of a 1024-thread block
+constexpr int TILE_RPT = STEP_TILE / 1024;
 constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
 // A split step's partials: workgroup b of a slab owns step_partial_stride(W) {g, h} pairs from pair b * stride,
 // whether it writes 256 * W pairs or 256 * W packed words (a step can mix both). The stride is padded so that
@@ -1846,8 +1862,6 @@ struct AdvShared {
     uint16_t cx[GROW_MAX_LEAVES];         // commit c: the leaf id split
     int16_t cpn[GROW_MAX_LEAVES];         // commit c: the split leaf's node above
     uint8_t cleft[GROW_MAX_LEAVES];       // commit c: the split leaf was its node's left child
-    double idg[GROW_MAX_LEAVES];          // committed leaf -> its speculative leaf's gain, as the replay goes
-    uint32_t idm[GROW_MAX_LEAVES];        // committed leaf -> its speculative leaf's meta
     double cgain[TCAP_MAX];               // speculation candidates' gains
     uint16_t cand[TCAP_MAX];              // speculation candidates
     uint16_t job_t[JMAX];
@@ -1856,33 +1870,6 @@ struct AdvShared {
 
 __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
     return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
-}
-
-// This lane's part of best_leaf (learner.rs:418-429) over the committed leaves lane, lane + 64, ... below n: the
-// first leaf with a split as 2 * leaf + (its gain is NaN), and the first highest gain that is not NaN.
-__device__ __forceinline__ void lane_best(const AdvShared &s, uint32_t lane, uint32_t n, int &first, double &kg, int &ki) {
-    first = 1 << 30;
-    kg = 0.0;
-    ki = -1;
-    for (uint32_t id = lane; id < n; id += 64u) {
-        if (!(s.idm[id] & 1u)) continue;
-        const double gk = s.idg[id];
-        const bool nan = gk != gk;
-        const int code = 2 * static_cast<int>(id) + (nan ? 1 : 0);
-        if (code < first) first = code;
-        if (nan) continue;
-        if (cand_better(gk, static_cast<int>(id), kg, ki)) {
-            kg = gk;
-            ki = static_cast<int>(id);
-        }
-    }
-}
-
-// LDS writes of one lane made visible to the rest of its wave.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
@@ -1907,21 +1894,33 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     }
     if (tid == 0) s.ncand = 0;
     __syncthreads();
-    for (uint32_t id = tid; id < n0; id += nt) {
-        const uint32_t k = s.leaf_t[id];
-        s.idg[id] = s.gain[k];
-        s.idm[id] = s.meta[k];
-    }
-    __syncthreads();
 
-    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave: each lane keeps the best of
-    // its leaves and recomputes it when one of them changes
+    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave: lane l holds committed leaves
+    // l, l + 64, ... in registers (gain, meta, speculative leaf, node above, left flag), so a commit costs two wave
+    // reductions and the two new leaves' loads
     if (tid < 64) {
+        constexpr int NPL = GROW_MAX_LEAVES / 64;
+        double rg[NPL];
+        uint32_t rm[NPL], rt[NPL];
+        int32_t rp[NPL];
+        uint32_t rl = 0, rtouch = 0;  // bit j: leaf lane + 64 j is a left child / changed by this replay
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const uint32_t id = lane + 64u * j;
+            rg[j] = 0.0;
+            rm[j] = 0;
+            rt[j] = 0;
+            rp[j] = -1;
+            if (id < n0) {
+                rt[j] = s.leaf_t[id];
+                rg[j] = s.gain[rt[j]];
+                rm[j] = s.meta[rt[j]];
+                rp[j] = s.pnode[id];
+                rl |= s.is_left[id] ? 1u << j : 0u;
+            }
+        }
         uint32_t n = n0, nc = 0, blocker = 0;
         bool done = false;
-        int lf, li;
-        double lg;
-        lane_best(s, lane, n, lf, lg, li);
         for (;;) {
             if (n >= L) {
                 done = true;
@@ -1929,46 +1928,98 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             }
             // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
             // otherwise the first highest gain among the rest (a NaN later never wins)
-            const int first = wave_min_i32(lf);
-            double kg = lg;
-            int ki = li;
+            int lfirst = 1 << 30, ki = -1;
+            double kg = 0.0;
+            bool lnan = false;
+#pragma unroll
+            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
+                const uint32_t id = lane + 64u * j;
+                const bool has = id < n && (rm[j] & 1u);
+                const bool nan = rg[j] != rg[j];
+                if (has) lfirst = 2 * static_cast<int>(id) + (nan ? 1 : 0);
+                lnan = lnan || (has && nan);
+                if (has && !nan && (ki < 0 || rg[j] >= kg)) {
+                    kg = rg[j];
+                    ki = static_cast<int>(id);
+                }
+            }
+            bool nan_first = false;
+            if (__ballot(lnan)) {
+                const int first = wave_min_i32(lfirst);
+                nan_first = first < (1 << 30) && (first & 1);
+            }
             wave_argmax(kg, ki);
-            const bool nan_first = first < (1 << 30) && (first & 1);
             if (nan_first || ki < 0 || !(kg > 0.0)) {
                 done = true;
                 break;
             }
-            const uint32_t x = static_cast<uint32_t>(ki);
-            const uint32_t m = s.idm[x];
+            const uint32_t x = static_cast<uint32_t>(ki), jx = x >> 6, lx = x & 63u;
+            uint32_t vm = 0, vt = 0;
+            int32_t vp = 0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+                if (jx == static_cast<uint32_t>(j)) {
+                    vm = rm[j];
+                    vt = rt[j];
+                    vp = rp[j];
+                }
+            const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vm), lx));
+            const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vt), lx));
             if (((m >> 1) & 3u) != T_EXPANDED) {
-                blocker = s.leaf_t[x];
+                blocker = k;
                 break;
             }
-            const uint32_t k = s.leaf_t[x];
+            const int32_t pn = __builtin_amdgcn_readlane(vp, lx);
+            const uint32_t xl = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rl), lx)) >> jx) & 1u;
             const uint32_t kid = (m >> 3) - 1u;
+            const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
+            const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
             if (lane == 0) {
-                const int16_t node = static_cast<int16_t>(n - 1);
                 s.ck[nc] = static_cast<uint16_t>(k);
                 s.cx[nc] = static_cast<uint16_t>(x);
-                s.cpn[nc] = s.pnode[x];
-                s.cleft[nc] = s.is_left[x];
-                s.leaf_t[x] = static_cast<uint16_t>(kid);
-                s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
-                s.pnode[x] = node;
-                s.pnode[n] = node;
-                s.is_left[x] = 1;
-                s.is_left[n] = 0;
-                s.touched[x] = 1;
-                s.touched[n] = 1;
-                s.idg[x] = s.gain[kid];
-                s.idm[x] = s.meta[kid];
-                s.idg[n] = s.gain[kid + 1];
-                s.idm[n] = s.meta[kid + 1];
+                s.cpn[nc] = static_cast<int16_t>(pn);
+                s.cleft[nc] = static_cast<uint8_t>(xl);
             }
-            wave_lds_sync();
+            // leaf x becomes the left child, leaf n the right one, both under node n - 1
+            const int32_t node = static_cast<int32_t>(n) - 1;
+            const uint32_t jn = n >> 6, ln = n & 63u;
+            // (jx and jn are wave-uniform: one register slot is touched for each)
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+                if (jx == static_cast<uint32_t>(j) && lane == lx) {
+                    rt[j] = kid;
+                    rg[j] = g0;
+                    rm[j] = m0;
+                    rp[j] = node;
+                }
+                if (jn == static_cast<uint32_t>(j) && lane == ln) {
+                    rt[j] = kid + 1;
+                    rg[j] = g1;
+                    rm[j] = m1;
+                    rp[j] = node;
+                }
+            }
+            const uint32_t bx = 1u << jx, bn = 1u << jn;
+            if (lane == lx) {
+                rl |= bx;
+                rtouch |= bx;
+            }
+            if (lane == ln) {
+                rl &= ~bn;
+                rtouch |= bn;
+            }
             ++nc;
             ++n;
-            if (lane == (x & 63u) || lane == ((n - 1u) & 63u)) lane_best(s, lane, n, lf, lg, li);
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const uint32_t id = lane + 64u * j;
+            if (id < n) {
+                s.leaf_t[id] = static_cast<uint16_t>(rt[j]);
+                s.pnode[id] = static_cast<int16_t>(rp[j]);
+                s.is_left[id] = static_cast<uint8_t>((rl >> j) & 1u);
+                s.touched[id] = static_cast<uint8_t>((rtouch >> j) & 1u);
+            }
         }
         if (lane == 0) {
             s.ncommit = nc;
@@ -2286,7 +2337,7 @@ struct StepView {
 
 struct StepShared {
     uint32_t list[STEP_TILE];  // the tile's rows of the built child
-    uint32_t wl[2][16];        // left counts per (sub-tile, wave)
+    uint32_t wl[TILE_RPT][16];  // left counts per (sub-tile, wave)
     uint32_t left_bins[8];     // the split's bins that go left
     uint32_t tile, prefix;
 };
@@ -2299,47 +2350,52 @@ __device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs 
     const uint64_t below_mask = (1ull << lane) - 1ull;
     const uint32_t t0 = t * STEP_TILE;
     const uint32_t valid = v.count - t0 < STEP_TILE ? v.count - t0 : STEP_TILE;
-    uint32_t row[2];
-    bool ok[2], left[2];
+    uint32_t row[TILE_RPT];
+    bool ok[TILE_RPT], left[TILE_RPT];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TILE_RPT; ++j) {
         uint32_t i = t0 + j * 1024 + tid;
         ok[j] = i < v.count;
         uint32_t ic = ok[j] ? i : v.count - 1;
         row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TILE_RPT; ++j) {
         uint32_t b = v.col[row[j]];
         left[j] = ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
     }
-    uint32_t below[2];
+    uint32_t below[TILE_RPT];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TILE_RPT; ++j) {
         unsigned long long m = __ballot(left[j]);
         below[j] = static_cast<uint32_t>(__popcll(m & below_mask));
         if (lane == 0) sh.wl[j][wave] = static_cast<uint32_t>(__popcll(m));
     }
     __syncthreads();
     // lefts before each row of the tile (rows in order: sub-tile, wave, lane)
-    uint32_t sub0 = 0, sub1 = 0, before0 = 0, before1 = 0;
+    uint32_t sub[TILE_RPT], before[TILE_RPT];
+#pragma unroll
+    for (int j = 0; j < TILE_RPT; ++j) sub[j] = before[j] = 0;
     for (uint32_t w = 0; w < 16; ++w) {
-        uint32_t v0 = sh.wl[0][w], v1 = sh.wl[1][w];
-        sub0 += v0;
-        sub1 += v1;
-        if (w < wave) {
-            before0 += v0;
-            before1 += v1;
+#pragma unroll
+        for (int j = 0; j < TILE_RPT; ++j) {
+            const uint32_t c = sh.wl[j][w];
+            sub[j] += c;
+            before[j] += w < wave ? c : 0u;
         }
     }
-    const uint32_t tile_left = sub0 + sub1;
-    uint32_t lrank[2] = {before0 + below[0], sub0 + before1 + below[1]};
+    uint32_t tile_left = 0, lrank[TILE_RPT];
+#pragma unroll
+    for (int j = 0; j < TILE_RPT; ++j) {
+        lrank[j] = tile_left + before[j] + below[j];
+        tile_left += sub[j];
+    }
     if (v.partition && tid == 0)
         __hip_atomic_store(v.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     if (v.hist) {  // the tile's rows of the built child, in order
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TILE_RPT; ++j) {
             uint32_t pos = j * 1024 + tid;
             if (ok[j] && (left[j] ? 1u : 0u) == v.built_left) sh.list[v.built_left ? lrank[j] : pos - lrank[j]] = row[j];
         }
@@ -2358,7 +2414,7 @@ __device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs 
         __syncthreads();
         const uint32_t lp = sh.prefix, rp = t0 - lp;  // lefts and rights before the tile
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TILE_RPT; ++j) {
             if (!ok[j]) continue;
             if (left[j]) {
                 uint32_t k = lp + lrank[j];
@@ -2813,52 +2869,38 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
     }
 }
 
-// Scan items (job, column group) in a grid-stride loop: the group's numerical features for both children, both
-// directions (split.rs:584-620), a wave per (feature, child, direction). Categorical features are k_step_cat's.
-// grid: any, 1024 threads.
-__global__ __launch_bounds__(1024) void k_step_scan(GrowState g, ScanStepArgs a) {
-    __shared__ Grown s_grown[2][CG_COLS][2];  // [child][column][direction]
-    __shared__ uint32_t s_found[2][CG_COLS][2];
+// Scan items (job, column, child), a wave each in a grid-stride loop: the column's numerical feature scanned in
+// both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's.
+// grid: any, 256 threads.
+__global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) {
     if (g.ctl->done) return;
     const StepPlan &P = *a.plan;
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t item = blockIdx.x; item < P.total_scan; item += gridDim.x) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t total = P.total_scan * (2u * CG_COLS);  // scan items count column groups
+    for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
+        const uint32_t gi = item / (2u * CG_COLS), sub = item % (2u * CG_COLS);
         uint32_t j = 0;  // the item's job: the last whose first item is at or below it
         for (uint32_t k = 1; k < P.njobs; ++k)
-            if (item >= P.jobs[k].scan_base) j = k;
+            if (gi >= P.jobs[k].scan_base) j = k;
         const JobPlan &J = P.jobs[j];
-        const ColGroup &cg = a.cgs[item - J.scan_base];
-        // wave w scans column w % 4 for child (w / 4) % 2 in direction w / 8
-        const uint32_t wave = tid >> 6, scol = wave & 3u, child = (wave >> 2) & 1u, dir = wave >> 3;
+        const ColGroup &cg = a.cgs[gi - J.scan_base];
+        const uint32_t scol = sub % CG_COLS, child = sub / CG_COLS;
         const int32_t sf = a.col_feat[cg.gcol + scol];
-        FeatDev sm = {};
-        bool sev = false;
-        if (sf >= 0) {
-            sm = g.feats[sf];
-            sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
-        }
-        const bool numerical = sf >= 0 && sm.kind != 2;
+        if (sf < 0) continue;
+        const FeatDev sm = g.feats[sf];
+        if (sm.kind == 2) continue;
+        const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
         const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
         const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
         const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
-        const bool searched = numerical && scan_searched(c, sm, sev);
-        if (searched && (dir == 0 || scan_two_way(sm))) {
-            Grown r = {};
-            bool found = scan_direction(c, g.cfg, sm, hist, static_cast<int>(dir), r);
-            if ((tid & 63u) == 0) {
-                s_grown[child][scol][dir] = r;
-                s_found[child][scol][dir] = found ? 1u : 0u;
-            }
+        FeatCand r = {};
+        if (scan_searched(c, sm, sev)) {
+            Grown rg = {}, fg = {};
+            const bool rf = scan_direction(c, g.cfg, sm, hist, 0, rg);
+            const bool ff = scan_two_way(sm) && scan_direction(c, g.cfg, sm, hist, 1, fg);
+            r = feature_candidate(c, sm, rf, rg, ff, fg);
         }
-        __syncthreads();
-        if (numerical && dir == 0 && (tid & 63u) == 0) {
-            FeatCand r = {};
-            if (searched)
-                r = feature_candidate(c, sm, s_found[child][scol][0] != 0, s_grown[child][scol][0],
-                                      scan_two_way(sm) && s_found[child][scol][1] != 0, s_grown[child][scol][1]);
-            g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
-        }
-        __syncthreads();  // s_grown is free for the next item
+        if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
     }
 }
 
