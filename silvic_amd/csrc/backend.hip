@@ -307,6 +307,7 @@ struct Context {
     DevBuf<uint32_t> part, part2, block_left, scalars;
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
+    DevBuf<uint32_t> d_fmt;  // per slab and k_step_rows workgroup: the format of its partial (1 packed, 0 pairs)
     DevBuf<int32_t> gcol_feat;
     DevBuf<uint32_t> cat_feats;  // the categorical features of the slabs
     uint32_t ncat = 0;
@@ -479,11 +480,12 @@ struct Context {
             std::vector<ColGroup> cg;
             std::vector<int32_t> gfeat;
             uint64_t poff = 0;
-            for (auto &s : slabs) {
+            for (size_t si = 0; si < slabs.size(); ++si) {
+                Slab &s = slabs[si];
                 s.step_partial_off = poff;
                 uint32_t gbase = static_cast<uint32_t>(gfeat.size());
                 for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) {
-                    ColGroup x{poff, s.width, c0, gbase + c0, 0, {}, {}};
+                    ColGroup x{poff, s.width, c0, gbase + c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}};
                     for (uint32_t k = 0; k < CG_COLS; ++k) {
                         bool real = c0 + k < s.feats.size();
                         x.offset[k] = real ? feats[s.feats[c0 + k]].hist_offset : 0u;
@@ -492,8 +494,9 @@ struct Context {
                     cg.push_back(x);
                 }
                 for (uint32_t c = 0; c < s.width; ++c) gfeat.push_back(c < s.feats.size() ? static_cast<int32_t>(s.feats[c]) : -1);
-                poff += static_cast<uint64_t>(cus + JMAX) * step_partial_stride(s.width);
+                poff += static_cast<uint64_t>(k1_groups()) * step_partial_stride(s.width);
             }
+            d_fmt.alloc(std::max<size_t>(slabs.size(), 1) * k1_groups());
             ncg = static_cast<uint32_t>(cg.size());
             step_partial_pairs = std::max<uint64_t>(poff, 1);
             d_cgs.alloc(std::max<size_t>(cg.size(), 1));
@@ -1309,7 +1312,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 }
                 for (size_t si = 0; si < slabs.size(); ++si) {
                     const Slab &sl = slabs[si];
-                    StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off,
+                    StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
                                 sl.col_bins.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
                     switch (sl.width) {
                     case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
@@ -1323,7 +1326,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     prof.step_events.emplace_back(e0, e1);
                     prof.step_launches += static_cast<double>(slabs.size());
                 }
-                ReduceStepArgs ra{step_partial.p, d_cgs.p, d_plans.p + parity};
+                ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
                 ScanStepArgs sca{d_cgs.p, gcol_feat.p, cat_feats.p, ncat, d_plans.p + parity};

@@ -2178,7 +2178,7 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             J.group_base = groups_before;
             J.packed = (ntiles <= groups && g.flush_rows >= STEP_TILE) ? 1u : 0u;
             J.ways = reduce_ways(groups);
-            red = hist ? g.ncg * (J.packed ? J.ways : 4u * J.ways) : 0u;
+            red = hist ? g.ncg * J.ways : 0u;
             scan = hist ? g.ncg : 0u;
             J.red_items = red;
             J.scan_items = scan;
@@ -2257,6 +2257,7 @@ struct StepArgs {
     uint64_t rows;
     uint32_t *buf0, *buf1;       // the partition buffers
     int32_t *partial;            // this slab's partials, step_partial_stride(W) pairs apart, one per workgroup
+    uint32_t *fmt;               // per workgroup of this slab: its partial is packed (1) or {g, h} pairs (0)
     const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
     unsigned long long *status;  // per-tile status words
     StepPlan *plan;              // this step's plan
@@ -2306,18 +2307,26 @@ __device__ uint32_t lookback(const unsigned long long *status, uint32_t t, uint3
     return prefix;
 }
 
-// Adds the packed 16/16 LDS words of this thread's slots into its i32 sums (optionally zeroing them). Block-wide.
-template <int SLOTS>
-__device__ __forceinline__ void unpack_slots(int32_t *lds, uint32_t tid, int32_t (&accg)[SLOTS], int32_t (&acch)[SLOTS],
-                                             bool clear) {
+// Moves the packed 16/16 LDS words into a workgroup's {g, h} pair partial (stored, or added to what an earlier
+// flush stored) and zeroes them. Slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W; bins past the
+// column's feature are not stored. Block-wide.
+template <int W>
+__device__ __forceinline__ void flush_pairs(int32_t *lds, int2 *pairs, uint32_t col_bins, bool add) {
+    constexpr int SLOTS = 256 * W / 1024;
+    const uint32_t tid = threadIdx.x;
     __syncthreads();
-#pragma unroll
+#pragma unroll 8
     for (int j = 0; j < SLOTS; ++j) {
-        int32_t v = lds[tid + j * 1024];
-        if (clear) lds[tid + j * 1024] = 0;
-        int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
-        accg[j] += gq;
-        acch[j] += (v - gq) >> 16;
+        const uint32_t slot = tid + j * 1024;
+        const int32_t v = lds[slot];
+        lds[slot] = 0;
+        if (slot / W < col_bins) {
+            const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
+            int2 o = add ? pairs[slot] : make_int2(0, 0);
+            o.x += gq;
+            o.y += (v - gq) >> 16;
+            pairs[slot] = o;
+        }
     }
     __syncthreads();
 }
@@ -2466,12 +2475,52 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
     }
 }
 
+// A workgroup's packed LDS words (every row added, none flushed) stored as its partial: int4 q * W + c holds bin
+// 4q + c % 4 of columns (c & ~3) .. (c & ~3) + 3. Task k takes column c = k % W and bins 4q..4q+3 (q = k / W),
+// reads LDS across the wave without bank conflicts, and a butterfly transpose in each quad of lanes (the group's 4
+// columns) leaves lane c % 4 with bin 4q + c % 4 of all four columns: a wave stores 1 KiB contiguously. The LDS
+// words must be complete (after a barrier). Block-wide, 1024 threads.
+template <int W>
+__device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t *partial) {
+    constexpr int SLOTS = 256 * W / 1024;
+    int4 *out = reinterpret_cast<int4 *>(partial);
+    const uint32_t tid = threadIdx.x, c4 = tid & 3u;
+#pragma unroll
+    for (int it = 0; it < SLOTS / 4; ++it) {
+        const uint32_t k = tid + 1024u * it, c = k % W, q = k / W;
+        int32_t v0 = lds[(4 * q + 0) * W + c], v1 = lds[(4 * q + 1) * W + c];
+        int32_t v2 = lds[(4 * q + 2) * W + c], v3 = lds[(4 * q + 3) * W + c];
+        // at level b a lane keeps the elements whose index bit b matches its own and swaps the other two with
+        // lane c4 ^ b; every choice is one select on a lane bit
+        {
+            const bool hi = (c4 & 1u) != 0;
+            const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v1, 0xB1, 0xf, 0xf, false);
+            const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v2 : v3, 0xB1, 0xf, 0xf, false);
+            const int32_t n0 = hi ? t0 : v0, n1 = hi ? v1 : t0, n2 = hi ? t1 : v2, n3 = hi ? v3 : t1;
+            v0 = n0;
+            v1 = n1;
+            v2 = n2;
+            v3 = n3;
+        }
+        {
+            const bool hi = (c4 & 2u) != 0;
+            const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v2, 0x4E, 0xf, 0xf, false);
+            const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v1 : v3, 0x4E, 0xf, 0xf, false);
+            const int32_t n0 = hi ? t0 : v0, n1 = hi ? t1 : v1, n2 = hi ? v2 : t0, n3 = hi ? v3 : t1;
+            v0 = n0;
+            v1 = n1;
+            v2 = n2;
+            v3 = n3;
+        }
+        out[q * W + c] = make_int4(v0, v1, v2, v3);  // column (c & ~3) + j at bin 4q + c4
+    }
+}
+
 template <int W>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     constexpr int DW = W / 4;
     constexpr int RPW = WAVE / DW;
-    // multi-tile workgroups keep 2 * SLOTS accumulator registers: at W = 128 that leaves room for 8 rows per lane
-    constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
+    constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);  // rows per lane in multi-tile workgroups
     constexpr int SLOTS = 256 * W / 1024;
     __shared__ int32_t lds[256 * W];
     __shared__ StepShared sh;
@@ -2507,11 +2556,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (v.hist)
         for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
 
-    if (packed) {
-        // one tile; the partial is the LDS words themselves, written column-group major: task k takes column
-        // c = k % W and bins 4q..4q+3 (q = k / W), reads LDS across the wave, and a butterfly transpose in each
-        // quad of lanes (the group's 4 columns) leaves lane c % 4 with bin 4q + c % 4 of all four columns, so the
-        // quad stores 64 contiguous bytes
+    if (packed) {  // one tile; the partial is the LDS words themselves
         __syncthreads();
         if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
         __syncthreads();
@@ -2519,45 +2564,17 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         if (!v.hist) return;
         hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         __syncthreads();
-        int4 *out = reinterpret_cast<int4 *>(a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
-        const uint32_t c4 = tid & 3u;
-#pragma unroll
-        for (int it = 0; it < SLOTS / 4; ++it) {
-            const uint32_t k = tid + 1024u * it, c = k % W, q = k / W;
-            int32_t v0 = lds[(4 * q + 0) * W + c], v1 = lds[(4 * q + 1) * W + c];
-            int32_t v2 = lds[(4 * q + 2) * W + c], v3 = lds[(4 * q + 3) * W + c];
-            // at level b a lane keeps the elements whose index bit b matches its own and swaps the other two with
-            // lane c4 ^ b; every choice is one select on a lane bit
-            {
-                const bool hi = (c4 & 1u) != 0;
-                const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v1, 0xB1, 0xf, 0xf, false);
-                const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v2 : v3, 0xB1, 0xf, 0xf, false);
-                const int32_t n0 = hi ? t0 : v0, n1 = hi ? v1 : t0, n2 = hi ? t1 : v2, n3 = hi ? v3 : t1;
-                v0 = n0;
-                v1 = n1;
-                v2 = n2;
-                v3 = n3;
-            }
-            {
-                const bool hi = (c4 & 2u) != 0;
-                const int32_t t0 = __builtin_amdgcn_update_dpp(0, hi ? v0 : v2, 0x4E, 0xf, 0xf, false);
-                const int32_t t1 = __builtin_amdgcn_update_dpp(0, hi ? v1 : v3, 0x4E, 0xf, 0xf, false);
-                const int32_t n0 = hi ? t0 : v0, n1 = hi ? t1 : v1, n2 = hi ? v2 : t0, n3 = hi ? v3 : t1;
-                v0 = n0;
-                v1 = n1;
-                v2 = n2;
-                v3 = n3;
-            }
-            out[(c / CG_COLS) * 256 + 4 * q + c4] = make_int4(v0, v1, v2, v3);  // column (c & ~3) + j at bin 4q + c4
-        }
+        store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
+        if (tid == 0) a.fmt[blockIdx.x] = 1u;
         return;
     }
 
-    // several tiles per workgroup: the packed words are unpacked into i32 sums every flush_rows rows
-    int32_t accg[SLOTS], acch[SLOTS];
-#pragma unroll
-    for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
-    uint32_t pending = 0;  // rows added to the packed LDS words since they were last unpacked
+    // several tiles per workgroup: whenever flush_rows rows have gone into the packed words they are added into the
+    // partial as {g, h} pairs; a workgroup that never flushes stores its partial packed instead
+    int2 *pairs = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
+    const uint32_t col_bins = a.col_bins[tid % W];  // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W
+    uint32_t pending = 0;  // rows added to the packed LDS words since they were last flushed
+    bool flushed = false;
     uint32_t next = gi;  // histogram-only launches take tiles gi, gi + groups, ...
     for (;;) {
         __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
@@ -2571,8 +2588,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         uint32_t c0 = 0;
         while (c0 < nb) {
             if (pending >= a.flush_rows) {
-                unpack_slots<SLOTS>(lds, tid, accg, acch, true);
+                flush_pairs<W>(lds, pairs, col_bins, flushed);
                 pending = 0;
+                flushed = true;
             }
             uint32_t room = a.flush_rows - pending;
             uint32_t c1 = nb - c0 < room ? nb : c0 + room;
@@ -2582,12 +2600,14 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
     }
     if (!v.hist) return;
-    unpack_slots<SLOTS>(lds, tid, accg, acch, false);
-    const uint32_t col_bins = a.col_bins[tid % W];  // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W
-    int2 *out = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
-#pragma unroll
-    for (int j = 0; j < SLOTS; ++j)
-        if ((tid + j * 1024) / W < col_bins) out[tid + j * 1024] = make_int2(accg[j], acch[j]);
+    if (!flushed) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
+        __syncthreads();
+        store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
+        if (tid == 0) a.fmt[blockIdx.x] = 1u;
+        return;
+    }
+    flush_pairs<W>(lds, pairs, col_bins, true);
+    if (tid == 0) a.fmt[blockIdx.x] = 0u;
 }
 
 // Four columns of one slab, reduced and scanned together by k_step_finish.
@@ -2596,7 +2616,7 @@ struct ColGroup {
     uint32_t width;    // the slab's W
     uint32_t c0;       // first column of the group in the slab
     uint32_t gcol;     // first column of the group in the global column arrays
-    uint32_t pad_;
+    uint32_t fmt;      // the slab's first k_step_rows workgroup in the partial-format flags
     uint32_t offset[4];  // per column: its feature's first bin in the flat histogram
     uint32_t bins[4];    // per column: the feature's bins (0 for padding)
 };
@@ -2639,6 +2659,7 @@ struct SelectArgs {
 
 struct ReduceStepArgs {
     const int32_t *partial;     // the step partial buffer
+    const uint32_t *fmt;        // the partials' formats (per slab, per k_step_rows workgroup: 1 packed, 0 pairs)
     const ColGroup *cgs;        // [ncg]
     StepPlan *plan;
 };
@@ -2747,9 +2768,9 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
 }
 
 // The built child's histogram of each job from its workgroups' partials, and its sibling's by subtraction in place
-// of the parent's (learner.rs:356-371). Work items (job, column group, slot range) in a grid-stride loop: a
-// thread adds one stripe of the partials of its slot (a bin's four columns for packed partials, one {g, h} pair
-// otherwise) and the stripes meet in LDS. grid: any, 256 threads.
+// of the parent's (learner.rs:356-371). Work items (job, column group, bin range) in a grid-stride loop: a thread
+// adds one stripe of the workgroups' partials of one bin of the group's four columns, reading each partial in its
+// own format (packed: one 16-byte load; {g, h} pairs: two), and the stripes meet in LDS. grid: any, 256 threads.
 __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs a) {
     __shared__ int64_t red[8][256];  // the stripes' sums, [value][thread]: conflict-free
     if (g.ctl->done) return;
@@ -2761,108 +2782,86 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
             if (item >= P.jobs[k].red_base) j = k;
         const JobPlan &J = P.jobs[j];
         const uint32_t ways = J.ways, groups = J.groups;
-        const bool packed = J.packed != 0;
-        const uint32_t per_cg = packed ? ways : 4u * ways;
-        const uint32_t r = item - J.red_base, cgi = r / per_cg, sub = r - cgi * per_cg;
+        const uint32_t r = item - J.red_base, cgi = r / ways, sub = r - cgi * ways;
         const ColGroup &cg = a.cgs[cgi];  // read in place: a column is picked per thread
         int64_t *built = g.pool + static_cast<size_t>(J.built_slot) * g.slot_stride;
         int64_t *parent = g.pool + static_cast<size_t>(J.parent_slot) * g.slot_stride;
-        const size_t pstride = step_partial_stride(cg.width);  // pairs from one partial to the next
-        const uint32_t ns = 256u / ways;                        // the item's slots
-        const uint32_t q = tid / ns;                            // this thread's stripe
-        if (packed) {
-            const uint32_t bin = sub * ns + tid % ns;
-            const size_t stride4 = pstride / 2;  // a partial's pairs in int4 units
-            const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + (cg.c0 / CG_COLS) * 256 + bin +
-                              static_cast<size_t>(J.group_base) * stride4;
-            int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
-            for (uint32_t w = q; w < groups; w += 8u * ways) {
-                int4 v[8];
+        const size_t stride4 = step_partial_stride(cg.width) / 2;  // int4s from one partial to the next
+        const uint32_t ns = 256u / ways;                           // the item's bins
+        const uint32_t q = tid / ns;                               // this thread's stripe
+        const uint32_t bin = sub * ns + tid % ns;
+        // bin `bin` of the group's columns in a partial: packed, int4 (bin / 4) * W + c0 + bin % 4; pairs, the int4s
+        // at (bin * W + c0) / 2 and the next
+        const int4 *src = reinterpret_cast<const int4 *>(a.partial + 2 * cg.partial) + static_cast<size_t>(J.group_base) * stride4;
+        const size_t po = static_cast<size_t>(bin / 4u) * cg.width + cg.c0 + bin % 4u;
+        const size_t qo = (static_cast<size_t>(bin) * cg.width + cg.c0) / 2;
+        const uint32_t *fmt = a.fmt + cg.fmt + J.group_base;
+        int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
+        for (uint32_t w = q; w < groups; w += 8u * ways) {
+            bool pk[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const uint32_t wk = w + k * ways;
-                    v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * stride4];
-                    if (wk >= groups) v[k] = make_int4(0, 0, 0, 0);
-                }
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t wk = w + k * ways;
+                pk[k] = fmt[wk < groups ? wk : q] != 0u;
+            }
+            int4 x[8], y[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const int32_t x[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t wk = w + k * ways;
+                const int4 *p = src + static_cast<size_t>(wk < groups ? wk : q) * stride4;
+                x[k] = p[pk[k] ? po : qo];
+                y[k] = pk[k] ? make_int4(0, 0, 0, 0) : p[qo + 1];
+                if (wk >= groups) x[k] = y[k] = make_int4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (pk[k]) {
+                    const int32_t v4[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(x[c])));
+                        const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v4[c])));
                         sg[c] += gq;
-                        sh[c] += (x[c] - gq) >> 16;
+                        sh[c] += (v4[c] - gq) >> 16;
                     }
+                } else {
+                    sg[0] += x[k].x;
+                    sh[0] += x[k].y;
+                    sg[1] += x[k].z;
+                    sh[1] += x[k].w;
+                    sg[2] += y[k].x;
+                    sh[2] += y[k].y;
+                    sg[3] += y[k].z;
+                    sh[3] += y[k].w;
                 }
             }
-            if (ways > 1u) {
+        }
+        if (ways > 1u) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    red[2 * c][tid] = sg[c];
-                    red[2 * c + 1][tid] = sh[c];
-                }
-                __syncthreads();
-                if (q == 0)
-                    for (uint32_t k = 1; k < ways; ++k) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            sg[c] += red[2 * c][tid + k * ns];
-                            sh[c] += red[2 * c + 1][tid + k * ns];
-                        }
-                    }
+            for (int c = 0; c < 4; ++c) {
+                red[2 * c][tid] = sg[c];
+                red[2 * c + 1][tid] = sh[c];
             }
-            if (q == 0) {
+            __syncthreads();
+            if (q == 0)
+                for (uint32_t k = 1; k < ways; ++k) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    if (bin < cg.bins[c]) {
-                        const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                        const int64_t pg = parent[o], ph = parent[o + 1];
-                        built[o] = sg[c];
-                        built[o + 1] = sh[c];
-                        parent[o] = pg - sg[c];
-                        parent[o + 1] = ph - sh[c];
+                    for (int c = 0; c < 4; ++c) {
+                        sg[c] += red[2 * c][tid + k * ns];
+                        sh[c] += red[2 * c + 1][tid + k * ns];
                     }
                 }
-            }
-        } else {
-            const uint32_t slot = sub * ns + tid % ns, cc = slot % CG_COLS, bin = slot / CG_COLS;
-            const bool used = bin < cg.bins[cc];
-            int64_t sg = 0, sh = 0;
-            if (used) {
-                const int2 *src = reinterpret_cast<const int2 *>(a.partial) + cg.partial + static_cast<size_t>(bin) * cg.width + cg.c0 +
-                                  cc + static_cast<size_t>(J.group_base) * pstride;
-                for (uint32_t w = q; w < groups; w += 8u * ways) {
-                    int2 v[8];
+        }
+        if (q == 0) {
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const uint32_t wk = w + k * ways;
-                        v[k] = src[static_cast<size_t>(wk < groups ? wk : q) * pstride];
-                        if (wk >= groups) v[k] = make_int2(0, 0);
-                    }
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        sg += v[k].x;
-                        sh += v[k].y;
-                    }
+            for (int c = 0; c < 4; ++c) {
+                if (bin < cg.bins[c]) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                    const int64_t pg = parent[o], ph = parent[o + 1];
+                    built[o] = sg[c];
+                    built[o + 1] = sh[c];
+                    parent[o] = pg - sg[c];
+                    parent[o + 1] = ph - sh[c];
                 }
-            }
-            if (ways > 1u) {
-                red[0][tid] = sg;
-                red[1][tid] = sh;
-                __syncthreads();
-                if (q == 0)
-                    for (uint32_t k = 1; k < ways; ++k) {
-                        sg += red[0][tid + k * ns];
-                        sh += red[1][tid + k * ns];
-                    }
-            }
-            if (q == 0 && used) {
-                const size_t o = 2 * (static_cast<size_t>(cg.offset[cc]) + bin);
-                const int64_t pg = parent[o], ph = parent[o + 1];
-                built[o] = sg;
-                built[o + 1] = sh;
-                parent[o] = pg - sg;
-                parent[o + 1] = ph - sh;
             }
         }
         __syncthreads();  // the LDS is free for the next item
