@@ -2351,32 +2351,39 @@ struct StepShared {
     uint32_t tile, prefix;
 };
 
-// One partition tile: its rows read in the leaf's order, its left count published, its offset from the look-back,
-// its rows scattered (left first-first, right last-first), and its rows of the built child left in sh.list in
-// order. Returns that row count. Block-wide.
-__device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs &a, uint32_t t, StepShared &sh) {
+// One partition tile in three parts. tile_front reads its rows in the leaf's order (TILE_RPT per thread: positions
+// tid, 1024 + tid, ...) and their split-feature bins, ranks the lefts, publishes the tile's left count and lists
+// its rows of the built child in sh.list, in order; tile_lookback (wave 0) takes the tile's offset from the
+// look-back; tile_scatter writes its rows, left first-first and right last-first. Between the last two the other
+// waves histogram the listed rows.
+struct TileState {
+    uint32_t row[TILE_RPT], lrank[TILE_RPT];  // lrank: lefts before the row in the tile
+    bool ok[TILE_RPT], left[TILE_RPT];
+    uint32_t tile_left;
+};
+
+// Returns the rows listed. Block-wide; the list is complete on return.
+__device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, TileState &st, StepShared &sh) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint64_t below_mask = (1ull << lane) - 1ull;
     const uint32_t t0 = t * STEP_TILE;
     const uint32_t valid = v.count - t0 < STEP_TILE ? v.count - t0 : STEP_TILE;
-    uint32_t row[TILE_RPT];
-    bool ok[TILE_RPT], left[TILE_RPT];
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
         uint32_t i = t0 + j * 1024 + tid;
-        ok[j] = i < v.count;
-        uint32_t ic = ok[j] ? i : v.count - 1;
-        row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
+        st.ok[j] = i < v.count;
+        uint32_t ic = st.ok[j] ? i : v.count - 1;
+        st.row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
     }
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
-        uint32_t b = v.col[row[j]];
-        left[j] = ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
+        uint32_t b = v.col[st.row[j]];
+        st.left[j] = st.ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
     }
     uint32_t below[TILE_RPT];
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
-        unsigned long long m = __ballot(left[j]);
+        unsigned long long m = __ballot(st.left[j]);
         below[j] = static_cast<uint32_t>(__popcll(m & below_mask));
         if (lane == 0) sh.wl[j][wave] = static_cast<uint32_t>(__popcll(m));
     }
@@ -2393,61 +2400,67 @@ __device__ __forceinline__ uint32_t step_tile(const StepView &v, const StepArgs 
             before[j] += w < wave ? c : 0u;
         }
     }
-    uint32_t tile_left = 0, lrank[TILE_RPT];
+    st.tile_left = 0;
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
-        lrank[j] = tile_left + before[j] + below[j];
-        tile_left += sub[j];
+        st.lrank[j] = st.tile_left + before[j] + below[j];
+        st.tile_left += sub[j];
     }
     if (v.partition && tid == 0)
-        __hip_atomic_store(v.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, tile_left), __ATOMIC_RELAXED,
+        __hip_atomic_store(v.status + t, status_word(v.epoch, t == 0 ? ST_INCL : ST_AGG, st.tile_left), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     if (v.hist) {  // the tile's rows of the built child, in order
 #pragma unroll
         for (int j = 0; j < TILE_RPT; ++j) {
             uint32_t pos = j * 1024 + tid;
-            if (ok[j] && (left[j] ? 1u : 0u) == v.built_left) sh.list[v.built_left ? lrank[j] : pos - lrank[j]] = row[j];
+            if (st.ok[j] && (st.left[j] ? 1u : 0u) == v.built_left)
+                sh.list[v.built_left ? st.lrank[j] : pos - st.lrank[j]] = st.row[j];
         }
     }
-    if (v.partition) {
-        if (wave == 0) {
-            uint32_t prefix = t == 0 ? 0u : lookback(v.status, t, v.epoch, a.ctl);
-            if (lane == 0) {
-                if (t > 0)
-                    __hip_atomic_store(v.status + t, status_word(v.epoch, ST_INCL, prefix + tile_left), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                sh.prefix = prefix;
-                if (t == v.ntiles - 1) v.job->left = prefix + tile_left;
-            }
-        }
-        __syncthreads();
-        const uint32_t lp = sh.prefix, rp = t0 - lp;  // lefts and rights before the tile
-#pragma unroll
-        for (int j = 0; j < TILE_RPT; ++j) {
-            if (!ok[j]) continue;
-            if (left[j]) {
-                uint32_t k = lp + lrank[j];
-                if (k < v.count) v.dst[v.begin + k] = row[j];
-            } else {
-                uint32_t k = rp + (j * 1024 + tid - lrank[j]);
-                if (k < v.count) v.dst[v.begin + v.count - 1 - k] = row[j];
-            }
-        }
-    }
-    const uint32_t nb = v.built_left ? tile_left : valid - tile_left;
     __syncthreads();  // the list is complete
-    return nb;
+    return v.built_left ? st.tile_left : valid - st.tile_left;
+}
+
+// The tile's offset into sh.prefix, published as its inclusive count. Wave 0 of a partition launch.
+__device__ __forceinline__ void tile_lookback(const StepView &v, const StepArgs &a, uint32_t t, const TileState &st,
+                                              StepShared &sh) {
+    const uint32_t prefix = t == 0 ? 0u : lookback(v.status, t, v.epoch, a.ctl);
+    if ((threadIdx.x & 63u) == 0) {
+        if (t > 0)
+            __hip_atomic_store(v.status + t, status_word(v.epoch, ST_INCL, prefix + st.tile_left), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        sh.prefix = prefix;
+        if (t == v.ntiles - 1) v.job->left = prefix + st.tile_left;
+    }
+}
+
+// The tile's rows written from the offset in sh.prefix (after a barrier that follows tile_lookback).
+__device__ __forceinline__ void tile_scatter(const StepView &v, uint32_t t, const TileState &st, const StepShared &sh) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lp = sh.prefix, rp = t * STEP_TILE - lp;  // lefts and rights before the tile
+#pragma unroll
+    for (int j = 0; j < TILE_RPT; ++j) {
+        if (!st.ok[j]) continue;
+        if (st.left[j]) {
+            uint32_t k = lp + st.lrank[j];
+            if (k < v.count) v.dst[v.begin + k] = st.row[j];
+        } else {
+            uint32_t k = rp + (j * 1024 + tid - st.lrank[j]);
+            if (k < v.count) v.dst[v.begin + v.count - 1 - k] = st.row[j];
+        }
+    }
 }
 
 // The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
-// lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free.
-template <int W, int UNROLL>
+// lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free. NW
+// waves take part; `wave` is this one's index among them.
+template <int W, int UNROLL, int NW = 16>
 __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
-                                          const uint32_t *bins32) {
+                                          const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6) {
     constexpr int DW = W / 4;
     constexpr int RPW = WAVE / DW;
-    constexpr uint32_t STEP = 16u * RPW * UNROLL;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    constexpr uint32_t STEP = NW * RPW * UNROLL;
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
     const uint32_t last = c1 - 1;
@@ -2560,10 +2573,20 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         __syncthreads();
         if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
         __syncthreads();
-        const uint32_t nb = step_tile(v, a, sh.tile, sh);
+        const uint32_t t = sh.tile;
+        TileState st;
+        const uint32_t nb = tile_front(v, t, st, sh);
+        // wave 0 resolves the tile's offset while the other waves histogram it (wv: the wave, uniform)
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        if (v.partition) {
+            if (wv == 0) tile_lookback(v, a, t, st, sh);
+            else if (v.hist) hist_list<W, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+        } else if (v.hist) {
+            hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
+        }
+        __syncthreads();  // the offset and the histogram are complete
+        if (v.partition) tile_scatter(v, t, st, sh);
         if (!v.hist) return;
-        hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
-        __syncthreads();
         store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
         if (tid == 0) a.fmt[blockIdx.x] = 1u;
         return;
@@ -2575,29 +2598,53 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     const uint32_t col_bins = a.col_bins[tid % W];  // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W
     uint32_t pending = 0;  // rows added to the packed LDS words since they were last flushed
     bool flushed = false;
-    uint32_t next = gi;  // histogram-only launches take tiles gi, gi + groups, ...
-    for (;;) {
-        __syncthreads();  // the previous tile's list and counts are consumed (and the LDS histogram is zeroed)
-        if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : next;
-        __syncthreads();
-        const uint32_t t = sh.tile;
+    // partition launches take tiles in ticket order, the next ticket drawn while the current tile is worked on (a
+    // look-back only ever waits on lower tiles, so holding a later one cannot block it); histogram-only launches
+    // take tiles gi, gi + groups, ...
+    __syncthreads();  // the LDS histogram is zeroed
+    if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
+    __syncthreads();
+    uint32_t t = sh.tile;
+    uint32_t next = gi + v.groups;
+    while (t < v.ntiles) {
+        TileState st;
+        const uint32_t nb = tile_front(v, t, st, sh);
+        uint32_t ticket = next;
+        if (v.partition && tid == 0) ticket = atomicAdd(&J.ticket, 1u);
         next += v.groups;
-        if (t >= v.ntiles) break;
-        const uint32_t nb = step_tile(v, a, t, sh);
-        if (!v.hist) continue;
-        uint32_t c0 = 0;
-        while (c0 < nb) {
-            if (pending >= a.flush_rows) {
-                flush_pairs<W>(lds, pairs, col_bins, flushed);
-                pending = 0;
-                flushed = true;
+        // a tile that takes the packed words past flush_rows rows is histogrammed by all waves around the flushes
+        // (block-wide); otherwise wave 0 resolves the tile's offset while the other waves histogram it
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        bool hist_done = !v.hist;
+        if (v.hist && pending + nb > a.flush_rows) {
+            uint32_t c0 = 0;
+            while (c0 < nb) {
+                if (pending >= a.flush_rows) {
+                    flush_pairs<W>(lds, pairs, col_bins, flushed);
+                    pending = 0;
+                    flushed = true;
+                }
+                uint32_t room = a.flush_rows - pending;
+                uint32_t c1 = nb - c0 < room ? nb : c0 + room;
+                hist_list<W, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+                pending += c1 - c0;
+                c0 = c1;
             }
-            uint32_t room = a.flush_rows - pending;
-            uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-            hist_list<W, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
-            pending += c1 - c0;
-            c0 = c1;
+            hist_done = true;
         }
+        if (v.partition) {
+            if (wv == 0) tile_lookback(v, a, t, st, sh);
+            else if (!hist_done) hist_list<W, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            __syncthreads();  // the offset is in sh.prefix
+            tile_scatter(v, t, st, sh);
+        } else if (!hist_done) {
+            hist_list<W, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
+        }
+        if (!hist_done) pending += nb;
+        __syncthreads();  // the tile's list is consumed
+        if (tid == 0) sh.tile = ticket;
+        __syncthreads();
+        t = sh.tile;
     }
     if (!v.hist) return;
     if (!flushed) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
