@@ -2348,14 +2348,34 @@ struct StepShared {
     uint32_t list[STEP_TILE];  // the tile's rows of the built child
     uint32_t wl[TILE_RPT][16];  // left counts per (sub-tile, wave)
     uint32_t left_bins[8];     // the split's bins that go left
-    uint32_t tile, prefix;
+    uint32_t tile, tile2, prefix;
 };
 
-// One partition tile in three parts. tile_front reads its rows in the leaf's order (TILE_RPT per thread: positions
-// tid, 1024 + tid, ...) and their split-feature bins, ranks the lefts, publishes the tile's left count and lists
-// its rows of the built child in sh.list, in order; tile_lookback (wave 0) takes the tile's offset from the
-// look-back; tile_scatter writes its rows, left first-first and right last-first. Between the last two the other
-// waves histogram the listed rows.
+// One partition tile in parts. tile_rows and tile_bins read its rows in the leaf's order (TILE_RPT per thread:
+// positions tid, 1024 + tid, ...) and their split-feature bins, so that a workgroup can load its next tile while
+// it works on this one; tile_front ranks the lefts, publishes the tile's left count and lists its rows of the built
+// child in sh.list, in order; tile_lookback (wave 0) takes the tile's offset from the look-back; tile_scatter
+// writes its rows, left first-first and right last-first. Between the last two the other waves histogram the
+// listed rows.
+struct TileRows {
+    uint32_t row[TILE_RPT], bin[TILE_RPT];
+};
+
+__device__ __forceinline__ void tile_rows(const StepView &v, uint32_t t, TileRows &r) {
+    const uint32_t t0 = t * STEP_TILE;
+#pragma unroll
+    for (int j = 0; j < TILE_RPT; ++j) {
+        const uint32_t i = t0 + j * 1024 + threadIdx.x;
+        const uint32_t ic = i < v.count ? i : v.count - 1;
+        r.row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
+    }
+}
+
+__device__ __forceinline__ void tile_bins(const StepView &v, TileRows &r) {
+#pragma unroll
+    for (int j = 0; j < TILE_RPT; ++j) r.bin[j] = v.col[r.row[j]];
+}
+
 struct TileState {
     uint32_t row[TILE_RPT], lrank[TILE_RPT];  // lrank: lefts before the row in the tile
     bool ok[TILE_RPT], left[TILE_RPT];
@@ -2363,21 +2383,17 @@ struct TileState {
 };
 
 // Returns the rows listed. Block-wide; the list is complete on return.
-__device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, TileState &st, StepShared &sh) {
+__device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, const TileRows &r, TileState &st,
+                                               StepShared &sh) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint64_t below_mask = (1ull << lane) - 1ull;
     const uint32_t t0 = t * STEP_TILE;
     const uint32_t valid = v.count - t0 < STEP_TILE ? v.count - t0 : STEP_TILE;
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
-        uint32_t i = t0 + j * 1024 + tid;
-        st.ok[j] = i < v.count;
-        uint32_t ic = st.ok[j] ? i : v.count - 1;
-        st.row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
-    }
-#pragma unroll
-    for (int j = 0; j < TILE_RPT; ++j) {
-        uint32_t b = v.col[st.row[j]];
+        st.ok[j] = t0 + j * 1024 + tid < v.count;
+        st.row[j] = r.row[j];
+        const uint32_t b = r.bin[j];
         st.left[j] = st.ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
     }
     uint32_t below[TILE_RPT];
@@ -2574,8 +2590,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
         __syncthreads();
         const uint32_t t = sh.tile;
+        TileRows r;
+        tile_rows(v, t, r);
+        tile_bins(v, r);
         TileState st;
-        const uint32_t nb = tile_front(v, t, st, sh);
+        const uint32_t nb = tile_front(v, t, r, st, sh);
         // wave 0 resolves the tile's offset while the other waves histogram it (wv: the wave, uniform)
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
@@ -2601,17 +2620,28 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     // partition launches take tiles in ticket order, the next ticket drawn while the current tile is worked on (a
     // look-back only ever waits on lower tiles, so holding a later one cannot block it); histogram-only launches
     // take tiles gi, gi + groups, ...
+    // A workgroup holds the tickets of its current and next tiles, and loads the next tile's rows while it
+    // histograms the current one (their split bins after it).
     __syncthreads();  // the LDS histogram is zeroed
-    if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
+    if (tid == 0) {
+        sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
+        sh.tile2 = v.partition ? atomicAdd(&J.ticket, 1u) : gi + v.groups;
+    }
     __syncthreads();
-    uint32_t t = sh.tile;
-    uint32_t next = gi + v.groups;
+    uint32_t t = sh.tile, tn = sh.tile2;
+    uint32_t next = gi + 2 * v.groups;
+    TileRows r;
+    if (t < v.ntiles) {
+        tile_rows(v, t, r);
+        tile_bins(v, r);
+    }
     while (t < v.ntiles) {
         TileState st;
-        const uint32_t nb = tile_front(v, t, st, sh);
+        const uint32_t nb = tile_front(v, t, r, st, sh);
         uint32_t ticket = next;
         if (v.partition && tid == 0) ticket = atomicAdd(&J.ticket, 1u);
         next += v.groups;
+        if (tn < v.ntiles) tile_rows(v, tn, r);
         // a tile that takes the packed words past flush_rows rows is histogrammed by all waves around the flushes
         // (block-wide); otherwise wave 0 resolves the tile's offset while the other waves histogram it
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2641,10 +2671,12 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
             hist_list<W, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         if (!hist_done) pending += nb;
+        if (tn < v.ntiles) tile_bins(v, r);
         __syncthreads();  // the tile's list is consumed
         if (tid == 0) sh.tile = ticket;
         __syncthreads();
-        t = sh.tile;
+        t = tn;
+        tn = sh.tile;
     }
     if (!v.hist) return;
     if (!flushed) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
