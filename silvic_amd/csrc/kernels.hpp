@@ -1872,6 +1872,142 @@ __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
     return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
 }
 
+// The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave: lane l holds committed
+// leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves) in registers (gain, meta, speculative leaf, node
+// above, left flag), so a commit costs two wave reductions and the two new leaves' loads. Leaves the commits,
+// the committed-leaf arrays and the outcome in `s`.
+template <int NPL>
+__device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
+    const uint32_t lane = threadIdx.x & 63u;
+    double rg[NPL];
+    uint32_t rm[NPL], rt[NPL];
+    int32_t rp[NPL];
+    uint32_t rl = 0, rtouch = 0;  // bit j: leaf lane + 64 j is a left child / changed by this replay
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t id = lane + 64u * j;
+        rg[j] = 0.0;
+        rm[j] = 0;
+        rt[j] = 0;
+        rp[j] = -1;
+        if (id < n0) {
+            rt[j] = s.leaf_t[id];
+            rg[j] = s.gain[rt[j]];
+            rm[j] = s.meta[rt[j]];
+            rp[j] = s.pnode[id];
+            rl |= s.is_left[id] ? 1u << j : 0u;
+        }
+    }
+    uint32_t n = n0, nc = 0, blocker = 0;
+    bool done = false;
+    for (;;) {
+        if (n >= L) {
+            done = true;
+            break;
+        }
+        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
+        // otherwise the first highest gain among the rest (a NaN later never wins)
+        int lfirst = 1 << 30, ki = -1;
+        double kg = 0.0;
+        bool lnan = false;
+#pragma unroll
+        for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
+            const uint32_t id = lane + 64u * j;
+            const bool has = id < n && (rm[j] & 1u);
+            const bool nan = rg[j] != rg[j];
+            if (has) lfirst = 2 * static_cast<int>(id) + (nan ? 1 : 0);
+            lnan = lnan || (has && nan);
+            if (has && !nan && (ki < 0 || rg[j] >= kg)) {
+                kg = rg[j];
+                ki = static_cast<int>(id);
+            }
+        }
+        bool nan_first = false;
+        if (__ballot(lnan)) {
+            const int first = wave_min_i32(lfirst);
+            nan_first = first < (1 << 30) && (first & 1);
+        }
+        wave_argmax(kg, ki);
+        if (nan_first || ki < 0 || !(kg > 0.0)) {
+            done = true;
+            break;
+        }
+        const uint32_t x = static_cast<uint32_t>(ki), jx = x >> 6, lx = x & 63u;
+        uint32_t vm = 0, vt = 0;
+        int32_t vp = 0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            if (jx == static_cast<uint32_t>(j)) {
+                vm = rm[j];
+                vt = rt[j];
+                vp = rp[j];
+            }
+        const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vm), lx));
+        const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vt), lx));
+        if (((m >> 1) & 3u) != T_EXPANDED) {
+            blocker = k;
+            break;
+        }
+        const int32_t pn = __builtin_amdgcn_readlane(vp, lx);
+        const uint32_t xl = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rl), lx)) >> jx) & 1u;
+        const uint32_t kid = (m >> 3) - 1u;
+        const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
+        const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
+        if (lane == 0) {
+            s.ck[nc] = static_cast<uint16_t>(k);
+            s.cx[nc] = static_cast<uint16_t>(x);
+            s.cpn[nc] = static_cast<int16_t>(pn);
+            s.cleft[nc] = static_cast<uint8_t>(xl);
+        }
+        // leaf x becomes the left child, leaf n the right one, both under node n - 1
+        const int32_t node = static_cast<int32_t>(n) - 1;
+        const uint32_t jn = n >> 6, ln = n & 63u;
+        // (jx and jn are wave-uniform: one register slot is touched for each)
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            if (jx == static_cast<uint32_t>(j) && lane == lx) {
+                rt[j] = kid;
+                rg[j] = g0;
+                rm[j] = m0;
+                rp[j] = node;
+            }
+            if (jn == static_cast<uint32_t>(j) && lane == ln) {
+                rt[j] = kid + 1;
+                rg[j] = g1;
+                rm[j] = m1;
+                rp[j] = node;
+            }
+        }
+        const uint32_t bx = 1u << jx, bn = 1u << jn;
+        if (lane == lx) {
+            rl |= bx;
+            rtouch |= bx;
+        }
+        if (lane == ln) {
+            rl &= ~bn;
+            rtouch |= bn;
+        }
+        ++nc;
+        ++n;
+    }
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t id = lane + 64u * j;
+        if (id < n) {
+            s.leaf_t[id] = static_cast<uint16_t>(rt[j]);
+            s.pnode[id] = static_cast<int16_t>(rp[j]);
+            s.is_left[id] = static_cast<uint8_t>((rl >> j) & 1u);
+            s.touched[id] = static_cast<uint8_t>((rtouch >> j) & 1u);
+        }
+    }
+    if (lane == 0) {
+        s.ncommit = nc;
+        s.n = n;
+        s.done = done ? 1u : 0u;
+        s.blocker = blocker;
+    }
+}
+
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     AdvShared &s = *reinterpret_cast<AdvShared *>(scratch);
     GrowCtl *ctl = g.ctl;
@@ -1895,138 +2031,12 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     if (tid == 0) s.ncand = 0;
     __syncthreads();
 
-    // -- the replay (learner.rs:158-163 with best_leaf, learner.rs:418-429), one wave: lane l holds committed leaves
-    // l, l + 64, ... in registers (gain, meta, speculative leaf, node above, left flag), so a commit costs two wave
-    // reductions and the two new leaves' loads
+    // -- the replay, one wave, with as few leaves per lane as the tree needs
     if (tid < 64) {
-        constexpr int NPL = GROW_MAX_LEAVES / 64;
-        double rg[NPL];
-        uint32_t rm[NPL], rt[NPL];
-        int32_t rp[NPL];
-        uint32_t rl = 0, rtouch = 0;  // bit j: leaf lane + 64 j is a left child / changed by this replay
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            const uint32_t id = lane + 64u * j;
-            rg[j] = 0.0;
-            rm[j] = 0;
-            rt[j] = 0;
-            rp[j] = -1;
-            if (id < n0) {
-                rt[j] = s.leaf_t[id];
-                rg[j] = s.gain[rt[j]];
-                rm[j] = s.meta[rt[j]];
-                rp[j] = s.pnode[id];
-                rl |= s.is_left[id] ? 1u << j : 0u;
-            }
-        }
-        uint32_t n = n0, nc = 0, blocker = 0;
-        bool done = false;
-        for (;;) {
-            if (n >= L) {
-                done = true;
-                break;
-            }
-            // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
-            // otherwise the first highest gain among the rest (a NaN later never wins)
-            int lfirst = 1 << 30, ki = -1;
-            double kg = 0.0;
-            bool lnan = false;
-#pragma unroll
-            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
-                const uint32_t id = lane + 64u * j;
-                const bool has = id < n && (rm[j] & 1u);
-                const bool nan = rg[j] != rg[j];
-                if (has) lfirst = 2 * static_cast<int>(id) + (nan ? 1 : 0);
-                lnan = lnan || (has && nan);
-                if (has && !nan && (ki < 0 || rg[j] >= kg)) {
-                    kg = rg[j];
-                    ki = static_cast<int>(id);
-                }
-            }
-            bool nan_first = false;
-            if (__ballot(lnan)) {
-                const int first = wave_min_i32(lfirst);
-                nan_first = first < (1 << 30) && (first & 1);
-            }
-            wave_argmax(kg, ki);
-            if (nan_first || ki < 0 || !(kg > 0.0)) {
-                done = true;
-                break;
-            }
-            const uint32_t x = static_cast<uint32_t>(ki), jx = x >> 6, lx = x & 63u;
-            uint32_t vm = 0, vt = 0;
-            int32_t vp = 0;
-#pragma unroll
-            for (int j = 0; j < NPL; ++j)
-                if (jx == static_cast<uint32_t>(j)) {
-                    vm = rm[j];
-                    vt = rt[j];
-                    vp = rp[j];
-                }
-            const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vm), lx));
-            const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vt), lx));
-            if (((m >> 1) & 3u) != T_EXPANDED) {
-                blocker = k;
-                break;
-            }
-            const int32_t pn = __builtin_amdgcn_readlane(vp, lx);
-            const uint32_t xl = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rl), lx)) >> jx) & 1u;
-            const uint32_t kid = (m >> 3) - 1u;
-            const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
-            const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
-            if (lane == 0) {
-                s.ck[nc] = static_cast<uint16_t>(k);
-                s.cx[nc] = static_cast<uint16_t>(x);
-                s.cpn[nc] = static_cast<int16_t>(pn);
-                s.cleft[nc] = static_cast<uint8_t>(xl);
-            }
-            // leaf x becomes the left child, leaf n the right one, both under node n - 1
-            const int32_t node = static_cast<int32_t>(n) - 1;
-            const uint32_t jn = n >> 6, ln = n & 63u;
-            // (jx and jn are wave-uniform: one register slot is touched for each)
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                if (jx == static_cast<uint32_t>(j) && lane == lx) {
-                    rt[j] = kid;
-                    rg[j] = g0;
-                    rm[j] = m0;
-                    rp[j] = node;
-                }
-                if (jn == static_cast<uint32_t>(j) && lane == ln) {
-                    rt[j] = kid + 1;
-                    rg[j] = g1;
-                    rm[j] = m1;
-                    rp[j] = node;
-                }
-            }
-            const uint32_t bx = 1u << jx, bn = 1u << jn;
-            if (lane == lx) {
-                rl |= bx;
-                rtouch |= bx;
-            }
-            if (lane == ln) {
-                rl &= ~bn;
-                rtouch |= bn;
-            }
-            ++nc;
-            ++n;
-        }
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            const uint32_t id = lane + 64u * j;
-            if (id < n) {
-                s.leaf_t[id] = static_cast<uint16_t>(rt[j]);
-                s.pnode[id] = static_cast<int16_t>(rp[j]);
-                s.is_left[id] = static_cast<uint8_t>((rl >> j) & 1u);
-                s.touched[id] = static_cast<uint8_t>((rtouch >> j) & 1u);
-            }
-        }
-        if (lane == 0) {
-            s.ncommit = nc;
-            s.n = n;
-            s.done = done ? 1u : 0u;
-            s.blocker = blocker;
-        }
+        if (L <= 64) replay<1>(s, n0, L);
+        else if (L <= 128) replay<2>(s, n0, L);
+        else if (L <= 256) replay<4>(s, n0, L);
+        else replay<GROW_MAX_LEAVES / 64>(s, n0, L);
     }
     __syncthreads();
     const uint32_t nc = s.ncommit, n = s.n;
