@@ -1862,7 +1862,8 @@ struct AdvShared {
     uint16_t cx[GROW_MAX_LEAVES];         // commit c: the leaf id split
     int16_t cpn[GROW_MAX_LEAVES];         // commit c: the split leaf's node above
     uint8_t cleft[GROW_MAX_LEAVES];       // commit c: the split leaf was its node's left child
-    double cgain[TCAP_MAX];               // speculation candidates' gains
+    uint64_t ckey[TCAP_MAX];              // speculation candidates' keys: higher gain (as f32), then lower leaf
+    uint32_t crank[TCAP_MAX];             // and their ranks
     uint16_t cand[TCAP_MAX];              // speculation candidates
     uint16_t job_t[JMAX];
     uint32_t ncand, ncommit, n, blocker, done, njobs;
@@ -2097,7 +2098,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && gk > 0.0 && k != blocker) {
             const uint32_t at = atomicAdd(&s.ncand, 1u);
             s.cand[at] = static_cast<uint16_t>(k);
-            s.cgain[at] = gk;
+            // a positive f32's bits order as the value: the key orders by gain to f32 precision, then lower leaf
+            s.ckey[at] = (static_cast<uint64_t>(__float_as_uint(static_cast<float>(gk))) << 32) | (0xffffffffu - k);
+            s.crank[at] = 0;
         }
     }
     __syncthreads();
@@ -2112,19 +2115,21 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     if (spec > room_t) spec = room_t;
     if (spec > room_s) spec = room_s;
     if (spec > ncand) spec = ncand;
-    // the spec highest gains (ties to the lower leaf); the blocker is job 0
-    for (uint32_t i = tid; i < ncand; i += nt) {
-        const uint32_t ki = s.cand[i];
-        const double gi = s.cgain[i];
+    // the spec highest keys; the blocker is job 0. Which leaves are expanded early changes no result (every
+    // expansion is the one its leaf gets when the replay reaches it), only the work done ahead. A candidate's rank
+    // (keys above its own) is summed over `nsl` slices of the others, one thread each.
+    const uint32_t nsl = ncand && ncand < nt ? nt / ncand : 1u;
+    for (uint32_t w = tid; w < ncand * nsl; w += nt) {
+        const uint32_t i = w % ncand, sl = w / ncand;
+        const uint64_t ki = s.ckey[i];
         uint32_t rank = 0;
 #pragma unroll 8
-        for (uint32_t j = 0; j < ncand; ++j) {
-            const double gj = s.cgain[j];
-            const uint32_t kj = s.cand[j];
-            rank += (gj > gi || (gj == gi && kj < ki)) ? 1u : 0u;
-        }
-        if (rank < spec) s.job_t[1 + rank] = static_cast<uint16_t>(ki);
+        for (uint32_t j = sl; j < ncand; j += nsl) rank += s.ckey[j] > ki ? 1u : 0u;
+        atomicAdd(&s.crank[i], rank);
     }
+    __syncthreads();
+    for (uint32_t i = tid; i < ncand; i += nt)
+        if (s.crank[i] < spec) s.job_t[1 + s.crank[i]] = s.cand[i];
     if (tid == 0) {
         s.job_t[0] = static_cast<uint16_t>(blocker);
         s.njobs = 1 + spec;
