@@ -906,7 +906,7 @@ struct Context {
             a.row_offset = row_offset;
             a.fraction = bag.fraction;
         }
-        k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, 1024)), 256, 0, stream>>>(a);
+        k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS)), TL_THREADS, 0, stream>>>(a);
         launch_check("k_tree_leaves");
         if (!sums) return;
         Pinned<unsigned long long> &h = h_sums;
@@ -1295,7 +1295,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_check("k_root_prep");
         k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr);
         launch_check("k_split_scan");
-        k_root_select<<<1, 1024, 0, stream>>>(g);
+        k_root_select<<<1, 512, 0, stream>>>(g);
         launch_check("k_root_select");
         // split steps: each is a no-op once the tree is complete; each commits at least one split
         uint32_t s = 0, batch = std::max<uint32_t>(2, last_steps ? last_steps : 8);

@@ -592,9 +592,10 @@ __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint64_t rows, c
     }
 }
 
-// Each row's leaf from a walk down the tree (nodes in LDS; four rows per thread in flight), in row order, and the
-// leaves' exact fixed-point sums rint(v * scale) of the in-bag rows' gradients: the sums k_leaf_sums makes over the
-// final partition (integers, so the order does not matter; cpu.rs:886-908). grid: any, 256 threads.
+// Each row's leaf from a walk down the tree (nodes in LDS; TL_RPT rows per thread in flight: the walk is a chain
+// of dependent gathers), in row order, and the leaves' exact fixed-point sums rint(v * scale) of the in-bag rows'
+// gradients: the sums k_leaf_sums makes over the final partition (integers, so the order does not matter;
+// cpu.rs:886-908). grid: any, TL_THREADS threads.
 struct TreeLeavesArgs {
     const uint8_t *colbins;            // column-major bins [feature][rows]
     uint64_t rows;
@@ -609,30 +610,32 @@ struct TreeLeavesArgs {
     double fraction;
 };
 constexpr uint32_t LEAVES_MAX_LDS = 512;  // the trees k_tree_leaves takes (device growth grows up to this)
+constexpr int TL_RPT = 8;
+constexpr uint32_t TL_THREADS = 512;
 
-__global__ __launch_bounds__(256) void k_tree_leaves(TreeLeavesArgs a) {
+__global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
     __shared__ DevNode sn[LEAVES_MAX_LDS - 1];
     __shared__ unsigned long long ls[LEAVES_MAX_LDS][2];
     for (uint32_t k = threadIdx.x; k < a.nn; k += blockDim.x) sn[k] = a.nodes[k];
     if (a.grad)
         for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
     __syncthreads();
-    const uint64_t stride = 4ull * gridDim.x * blockDim.x;
+    const uint64_t stride = static_cast<uint64_t>(TL_RPT) * gridDim.x * blockDim.x;
     for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; base < a.rows; base += stride) {
-        uint64_t r[4];
-        int32_t nd[4];
+        uint64_t r[TL_RPT];
+        int32_t nd[TL_RPT];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < TL_RPT; ++k) {
             r[k] = base + static_cast<uint64_t>(k) * gridDim.x * blockDim.x;
             nd[k] = r[k] < a.rows ? 0 : -1;
         }
         for (;;) {
-            uint32_t b[4];
+            uint32_t b[TL_RPT];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) b[k] = nd[k] >= 0 ? a.colbins[static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]] : 0u;
+            for (int k = 0; k < TL_RPT; ++k) b[k] = nd[k] >= 0 ? a.colbins[static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]] : 0u;
             bool any = false;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < TL_RPT; ++k) {
                 if (nd[k] < 0) continue;
                 const DevNode &x = sn[nd[k]];
                 nd[k] = ((x.left_bins[b[k] >> 5] >> (b[k] & 31u)) & 1u) ? x.left : x.right;
@@ -641,7 +644,7 @@ __global__ __launch_bounds__(256) void k_tree_leaves(TreeLeavesArgs a) {
             if (!any) break;
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < TL_RPT; ++k) {
             if (r[k] >= a.rows) continue;
             const uint32_t leaf = static_cast<uint32_t>(~nd[k]);
             a.leaf_of[r[k]] = static_cast<uint16_t>(leaf);
@@ -2229,8 +2232,8 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     }
 }
 
-// The root's best split (learner.rs:157-163), then the first step's plan. One block of 1024 threads.
-__global__ __launch_bounds__(1024) void k_root_select(GrowState g) {
+// The root's best split (learner.rs:157-163), then the first step's plan. One block of 512 threads.
+__global__ __launch_bounds__(512) void k_root_select(GrowState g) {
     __shared__ SplitOut o;
     __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
     ScanJob job = g.jobs[0];
