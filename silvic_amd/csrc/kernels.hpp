@@ -2893,25 +2893,34 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         const size_t po = static_cast<size_t>(bin / 4u) * cg.width + cg.c0 + bin % 4u;
         const size_t qo = (static_cast<size_t>(bin) * cg.width + cg.c0) / 2;
         const uint32_t *fmt = a.fmt + cg.fmt + J.group_base;
+        // the parent's bins are loaded with the partials (the writes below need them); every partial is first read
+        // as packed, and a {g, h} pair partial (a workgroup that flushed) is read again in its own layout
+        int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
+        if (q == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (bin < cg.bins[c]) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                    pg[c] = parent[o];
+                    ph[c] = parent[o + 1];
+                }
+            }
+        }
         int64_t sg[4] = {0, 0, 0, 0}, sh[4] = {0, 0, 0, 0};
         for (uint32_t w = q; w < groups; w += 8u * ways) {
             bool pk[8];
+            int4 x[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const uint32_t wk = w + k * ways;
-                pk[k] = fmt[wk < groups ? wk : q] != 0u;
+                const uint32_t wc = wk < groups ? wk : q;
+                pk[k] = fmt[wc] != 0u;
+                x[k] = src[static_cast<size_t>(wc) * stride4 + po];
             }
-            int4 x[8], y[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const uint32_t wk = w + k * ways;
-                const int4 *p = src + static_cast<size_t>(wk < groups ? wk : q) * stride4;
-                x[k] = p[pk[k] ? po : qo];
-                y[k] = pk[k] ? make_int4(0, 0, 0, 0) : p[qo + 1];
-                if (wk >= groups) x[k] = y[k] = make_int4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
+                if (wk >= groups) continue;
                 if (pk[k]) {
                     const int32_t v4[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
@@ -2921,14 +2930,16 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
                         sh[c] += (v4[c] - gq) >> 16;
                     }
                 } else {
-                    sg[0] += x[k].x;
-                    sh[0] += x[k].y;
-                    sg[1] += x[k].z;
-                    sh[1] += x[k].w;
-                    sg[2] += y[k].x;
-                    sh[2] += y[k].y;
-                    sg[3] += y[k].z;
-                    sh[3] += y[k].w;
+                    const int4 *p = src + static_cast<size_t>(wk) * stride4;
+                    const int4 a0 = p[qo], a1 = p[qo + 1];
+                    sg[0] += a0.x;
+                    sh[0] += a0.y;
+                    sg[1] += a0.z;
+                    sh[1] += a0.w;
+                    sg[2] += a1.x;
+                    sh[2] += a1.y;
+                    sg[3] += a1.z;
+                    sh[3] += a1.w;
                 }
             }
         }
@@ -2953,11 +2964,10 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
             for (int c = 0; c < 4; ++c) {
                 if (bin < cg.bins[c]) {
                     const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
-                    const int64_t pg = parent[o], ph = parent[o + 1];
                     built[o] = sg[c];
                     built[o + 1] = sh[c];
-                    parent[o] = pg - sg[c];
-                    parent[o + 1] = ph - sh[c];
+                    parent[o] = pg[c] - sg[c];
+                    parent[o + 1] = ph[c] - sh[c];
                 }
             }
         }
