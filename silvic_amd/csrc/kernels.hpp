@@ -1682,8 +1682,20 @@ struct StepPlan {
     uint32_t total_scan;    // k_step_scan work items
     uint32_t epoch;         // tags the step's tile status words
     uint32_t pad_[3];
+    // the jobs' first workgroup, reduce item and scan item side by side (a job search reads one run of words)
+    uint32_t group_base[JMAX], red_base[JMAX], scan_base[JMAX];
     JobPlan jobs[JMAX];
 };
+
+// The job whose range of work holds x: the last whose first element (bases[k]) is at or below it. The bases are read
+// as one unrolled run, so the search is one round of loads.
+__device__ __forceinline__ uint32_t job_of(const uint32_t (&bases)[JMAX], uint32_t njobs, uint32_t x) {
+    uint32_t j = 0;
+#pragma unroll
+    for (uint32_t k = 1; k < JMAX; ++k)
+        if (k < njobs && x >= bases[k]) j = k;
+    return j;
+}
 
 struct GrowCtl {
     uint32_t num_leaves;   // committed leaves
@@ -2208,6 +2220,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if (on) {
             J.red_base = red_before;
             J.scan_base = scan_before;
+            next.group_base[lane] = J.group_base;
+            next.red_base[lane] = red_before;
+            next.scan_base[lane] = scan_before;
             J.ticket = 0;
             J.left = 0;
             next.jobs[lane] = J;
@@ -2575,9 +2590,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (a.ctl->done) return;
     StepPlan &P = *a.plan;
     if (blockIdx.x >= P.total_groups) return;
-    uint32_t j = 0;  // the workgroup's job: the last whose first workgroup is at or below it
-    for (uint32_t k = 1; k < P.njobs; ++k)
-        if (blockIdx.x >= P.jobs[k].group_base) j = k;
+    const uint32_t j = job_of(P.group_base, P.njobs, blockIdx.x);
     JobPlan &J = P.jobs[j];
     StepView v;
     v.job = &J;
@@ -2874,9 +2887,7 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
     const StepPlan &P = *a.plan;
     const uint32_t tid = threadIdx.x;
     for (uint32_t item = blockIdx.x; item < P.total_red; item += gridDim.x) {
-        uint32_t j = 0;  // the item's job: the last whose first item is at or below it
-        for (uint32_t k = 1; k < P.njobs; ++k)
-            if (item >= P.jobs[k].red_base) j = k;
+        const uint32_t j = job_of(P.red_base, P.njobs, item);
         const JobPlan &J = P.jobs[j];
         const uint32_t ways = J.ways, groups = J.groups;
         const uint32_t r = item - J.red_base, cgi = r / ways, sub = r - cgi * ways;
@@ -2985,9 +2996,7 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
     const uint32_t total = P.total_scan * (2u * CG_COLS);  // scan items count column groups
     for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
         const uint32_t gi = item / (2u * CG_COLS), sub = item % (2u * CG_COLS);
-        uint32_t j = 0;  // the item's job: the last whose first item is at or below it
-        for (uint32_t k = 1; k < P.njobs; ++k)
-            if (gi >= P.jobs[k].scan_base) j = k;
+        const uint32_t j = job_of(P.scan_base, P.njobs, gi);
         const JobPlan &J = P.jobs[j];
         const ColGroup &cg = a.cgs[gi - J.scan_base];
         const uint32_t scol = sub % CG_COLS, child = sub / CG_COLS;
