@@ -1570,7 +1570,7 @@ __device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_
     return word;
 }
 
-constexpr uint32_t STEP_TILE = 2048;          // rows per partition tile: TILE_RPT per thread of a 1024-thread block
+constexpr uint32_t STEP_TILE = 4096;          // rows per partition tile: TILE_RPT per thread of a 1024-thread block
 constexpr int TILE_RPT = STEP_TILE / 1024;
 constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
 // A split step's partials: workgroup b of a slab owns step_partial_stride(W) {g, h} pairs from pair b * stride,
