@@ -317,7 +317,7 @@ struct Context {
     std::vector<uint8_t> used;
     uint32_t objective = SROCM_OBJ_REGRESSION;
     double sigmoid = 1.0;
-    int64_t max_quant = 1;
+    int64_t max_gq = 1, max_hq = 1;  // the last quantization's largest |g| and h units
     bool quantized_once = false;
 
     Pinned<int64_t> h_hist;
@@ -516,7 +516,7 @@ struct Context {
         }
         used.assign(nf, 1);
         part_len = 0;
-        max_quant = 1;
+        max_gq = max_hq = 1;
         quantized_once = false;
         grow_capacity = 0;
         pool.release();
@@ -600,7 +600,8 @@ struct Context {
             k_quantize<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, q);
             launch_check("k_quantize");
         }
-        max_quant = std::max(s.grad_max_q, s.hess_max_q);
+        max_gq = s.grad_max_q;
+        max_hq = s.hess_max_q;
         quantized_once = true;
     }
 
@@ -635,7 +636,11 @@ struct Context {
     // histograms
     // ------------------------------------------------------------------------------------------------
 
-    uint32_t flush_rows() const { return static_cast<uint32_t>(32767 / std::max<int64_t>(max_quant, 1)); }
+    // rows a packed word takes before its sums could leave their halves: g (low 16 bits, signed) within +-32767,
+    // h (high 16 bits, never negative) at most 65535
+    uint32_t flush_rows() const {
+        return static_cast<uint32_t>(std::min(32767 / std::max<int64_t>(max_gq, 1), 65535 / std::max<int64_t>(max_hq, 1)));
+    }
 
     uint32_t hist_groups(uint64_t n) const {
         uint32_t want = div_up(std::max<uint64_t>(n, 1), HIST_MIN_ROWS);

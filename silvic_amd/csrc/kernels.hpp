@@ -205,8 +205,9 @@ __global__ void k_iota(uint32_t *__restrict__ out, uint64_t n) {
 // (quantize.rs:100-107). A wave covers 64 / (W/4) rows, each lane one dword (4 columns) of a row. At step k a
 // lane adds byte x = (k + (lane%32)/8) % 4 of its dword, so the 32 lanes of each half-wave hit the 32 LDS banks
 // (bank = column mod 32 = 4 * (lane%8) + x) exactly once: every ds_add_u32 is conflict-free whatever the bins.
-// Every `flush_rows` rows (<= 32767 / max_q, so no 16-bit half can overflow) the packed words are unpacked
-// into per-thread registers (i32 g and h sums) and zeroed. Each workgroup writes its sums as a partial
+// Every `flush_rows` rows (at most 32767 / max |g| and 65535 / max h: the low half holds g as a signed 16-bit
+// value, the high half h, which is never negative, as an unsigned one) the packed words are unpacked into per-thread
+// registers (i32 g and h sums) and zeroed. Each workgroup writes its sums as a partial
 // histogram `partial[wg][bin * W + column] = {g, h}`; k_hist_reduce adds the partials.
 // ---------------------------------------------------------------------------------------------------------
 
@@ -322,7 +323,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
             lds[tid + j * 1024] = 0;
             int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
             accg[j] += gq;
-            acch[j] += (v - gq) >> 16;
+            acch[j] += static_cast<int32_t>(static_cast<uint32_t>(v - gq) >> 16);
         }
         __syncthreads();
     }
@@ -2357,7 +2358,7 @@ __device__ __forceinline__ void flush_pairs(int32_t *lds, int2 *pairs, uint32_t 
             const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
             int2 o = add ? pairs[slot] : make_int2(0, 0);
             o.x += gq;
-            o.y += (v - gq) >> 16;
+            o.y += static_cast<int32_t>(static_cast<uint32_t>(v - gq) >> 16);
             pairs[slot] = o;
         }
     }
@@ -2938,7 +2939,7 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
                     for (int c = 0; c < 4; ++c) {
                         const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v4[c])));
                         sg[c] += gq;
-                        sh[c] += (v4[c] - gq) >> 16;
+                        sh[c] += static_cast<int32_t>(static_cast<uint32_t>(v4[c] - gq) >> 16);
                     }
                 } else {
                     const int4 *p = src + static_cast<size_t>(wk) * stride4;
