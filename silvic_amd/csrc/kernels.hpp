@@ -2775,18 +2775,18 @@ struct ReduceStepArgs {
     StepPlan *plan;
 };
 
-// The end of job j, by one wave (learner.rs:294-352): both children's best splits from their per-feature
-// candidates (split.rs:866-880), their leaves in the speculative tree, and the job's leaf marked expanded.
-// Values every lane computes alike are kept uniform; lane 0 writes the scalars.
+// The end of job j, by one block (learner.rs:294-352): both children's best splits from their per-feature
+// candidates (split.rs:866-880; waves 0 and 1, one child each, while wave 2 counts the job's evaluated features),
+// then their leaves in the speculative tree and the job's leaf marked expanded (thread 0).
 __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
-    const uint32_t lane = threadIdx.x & 63u;
+    __shared__ SplitOut s_out[2];
+    __shared__ uint32_t s_used;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     GrowCtl *ctl = g.ctl;
-    const TLeaf pl = g.tl[J.t];
-    const SplitOut &info = pl.best;
     const int64_t left = static_cast<int64_t>(J.left);
     const int64_t right = J.parent_count - left;
-    if (!(left > 0 && right > 0)) {
-        if (lane == 0) {
+    if (!(left > 0 && right > 0)) {  // uniform over the block
+        if (threadIdx.x == 0) {
             ctl->error = 1;
             ctl->done = 1;
             const uint32_t info[8] = {j, J.t, J.count, J.left, J.ntiles, J.groups, J.packed, 0u};
@@ -2795,18 +2795,21 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
         return;
     }
     const int32_t kid = J.kid;
-    const int32_t depth = pl.depth + 1;
+    const int32_t depth = g.tl[J.t].depth + 1;
     const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
     const bool searched = J.hist && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
-    // the job's evaluated features (learner.rs:262-265), for the byte count
-    const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
-    uint32_t used = 0;
-    for (uint32_t f = lane; f < g.nf; f += 64u)
-        used += static_cast<uint32_t>(__popcll(__ballot(g.mask[f] != 0 && prow[f] != 0)));
-    SplitOut out[2] = {};
-    if (searched) {
-#pragma unroll
-        for (uint32_t ch = 0; ch < 2; ++ch) {
+    // waves 0 and 1: the best split of the left and the right child; wave 2: the job's evaluated features
+    // (learner.rs:262-265), for the byte count
+    if (wave == 2) {
+        const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
+        uint32_t used = 0;
+        for (uint32_t f = lane; f < g.nf; f += 64u)
+            used += static_cast<uint32_t>(__popcll(__ballot(g.mask[f] != 0 && prow[f] != 0)));
+        if (lane == 0) s_used = used;
+    } else if (wave < 2) {
+        const uint32_t ch = wave;
+        SplitOut out = {};
+        if (searched) {
             const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
             uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
             double best = 0.0;
@@ -2826,11 +2829,15 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
             wave_best(wb, wf);
             if (wf >= 0) {  // the winner, read once more where the scans left it
                 const int64_t cnt = ch == 0 ? left : right;
-                out[ch] = split_out(cands[wf], wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                out = split_out(cands[wf], wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
             }
         }
+        if (lane == 0) s_out[ch] = out;
     }
-    if (lane == 0) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const TLeaf &pl = g.tl[J.t];
+        const SplitOut &info = pl.best;
         TLeaf l = {}, r = {};
         l.begin = J.begin;
         l.count = J.left;
@@ -2857,10 +2864,10 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
         if (searched) {
             l.slot = J.built_side == 0 ? J.built_slot : J.parent_slot;
             r.slot = J.built_side == 0 ? J.parent_slot : J.built_slot;
-            l.best = out[0];
-            r.best = out[1];
-            l.has_best = out[0].found ? 1u : 0u;
-            r.has_best = out[1].found ? 1u : 0u;
+            l.best = s_out[0];
+            r.best = s_out[1];
+            l.has_best = s_out[0].found ? 1u : 0u;
+            r.has_best = s_out[1].found ? 1u : 0u;
         }
         g.tl[kid] = l;
         g.tl[kid + 1] = r;
@@ -2871,7 +2878,7 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
         if (J.hist) {  // the built child's histogram was made, searched or not
             const double built_rows = J.built_side == 0 ? static_cast<double>(left) : static_cast<double>(right);
             atomicAdd(&ctl->hist_rows, built_rows);
-            atomicAdd(&ctl->hist_bins, built_rows * static_cast<double>(used));
+            atomicAdd(&ctl->hist_bins, built_rows * static_cast<double>(s_used));
             atomicAdd(&ctl->hist_builds, 1.0);
         }
         atomicAdd(&ctl->part_rows, static_cast<double>(J.count));
@@ -3051,7 +3058,7 @@ __global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) 
     StepPlan &P = *a.plan;
     const uint32_t j = blockIdx.x;
     if (j >= P.njobs) return;
-    if (threadIdx.x < 64) job_select(g, P.jobs[j], j);
+    job_select(g, P.jobs[j], j);
     if (!arrive_last(a.all_count, P.njobs)) return;
     advance(g, *a.next, scratch);
 }
