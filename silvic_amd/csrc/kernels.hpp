@@ -2195,9 +2195,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const uint32_t tiles_before = wave_excl_sum(ntiles);
         const uint32_t total_tiles = wave_total(ntiles);
         uint32_t groups = 0;
-        if (on) {
-            uint64_t want = total_tiles ? static_cast<uint64_t>(ntiles) * g.target_groups / total_tiles : 1u;
-            groups = static_cast<uint32_t>(want < 1 ? 1 : (want > ntiles ? ntiles : want));
+        if (on) {  // at most `per` tiles a workgroup in every job, so no job's workgroups run long
+            const uint32_t per = total_tiles > g.target_groups ? (total_tiles + g.target_groups - 1) / g.target_groups : 1u;
+            groups = (ntiles + per - 1) / per;
             if (groups == 0) groups = 1;
         }
         const uint32_t groups_before = wave_excl_sum(groups);
