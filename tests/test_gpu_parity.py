@@ -294,6 +294,48 @@ def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves, qbins):
     assert np.array_equal(rocm.partition_rows(n), o_part[:n])
 
 
+# Edge cases of device growth, each against the oracle with the final partition row for row: one split; the
+# largest tree the device grows (512 leaves); a depth limit (jobs whose children are not histogrammed); a
+# min_data_in_leaf that stops the tree early; a tiny dataset; zero gradients (no split at all).
+@pytest.mark.parametrize("rows,cols,kw", [
+    (50_000, 16, dict(num_leaves=2)),
+    (200_000, 32, dict(num_leaves=512)),
+    (200_000, 32, dict(num_leaves=255, max_depth=4)),
+    (100_000, 16, dict(num_leaves=255, min_data_in_leaf=5000)),
+    (300, 16, dict(num_leaves=31, min_data_in_leaf=5)),
+    (20_000, 16, dict(num_leaves=31, zero=True)),
+])
+def test_grown_tree_edge_cases(rocm, rows, cols, kw):
+    say("grow edge", rows, cols, kw)
+    kw = dict(kw)
+    zero = kw.pop("zero", False)
+    data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=5)
+    g, h = binary_gradients(data, 3)
+    if zero:
+        g = np.zeros_like(g)
+    p = oracle.default_params(**kw)
+    o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
+    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed)
+    n = rocm.reset_partition()
+    mask = oracle.feature_mask(data.features, 1.0, 2, 0)
+    d = rocm.grow(p.cfg, p.num_leaves, p.max_depth, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
+    compare_trees(d, dict(o_tree), f"edge {kw}")
+    assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+    assert np.array_equal(rocm.partition_rows(n), o_part[:n])
+
+
+def test_grow_rejects_more_leaves_than_the_device_grows(rocm):
+    say("grow 513 leaves")
+    data = silvic_amd.synthetic(2, rows=5_000, cols=8, seed=5)
+    g, h = binary_gradients(data, 3)
+    spec, _ = quantized_setup(rocm, data, g, h)
+    n = rocm.reset_partition()
+    p = oracle.default_params(num_leaves=513)
+    with pytest.raises(_abi.SilvicError) as e:
+        rocm.grow(p.cfg, 513, -1, spec.grad_scale, spec.hess_scale, np.ones(len(data.features), bool), (0, n), n)
+    assert e.value.kind == _abi.KIND_NAMES[_abi.ERR_UNSUPPORTED]
+
+
 # categorical columns: the default parameters search sorted categorical rules (21 bins > max_cat_to_onehot 4);
 # max_cat_to_onehot 32 searches one-hot rules; cat_smooth 0 with min_data_per_group 1 ranks raw ratios.
 @pytest.mark.parametrize("rows,cols,leaves,kw", [(200_000, 28, 63, {}), (300_000, 12, 255, dict(max_cat_to_onehot=32)),
