@@ -475,7 +475,7 @@ struct Context {
             hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
         }
-        // groups of CG_COLS slab columns for k_step_finish, and the feature of every slab column
+        // groups of CG_COLS slab columns for k_step_reduce and k_step_scan, and the feature of every slab column
         {
             std::vector<ColGroup> cg;
             std::vector<int32_t> gfeat;
@@ -595,6 +595,9 @@ struct Context {
 
     void quantize(const srocm_quant_spec &s) {
         require_loaded();
+        // a histogram word packs g as a signed 16-bit half and h as an unsigned one
+        if (s.grad_max_q < 1 || s.grad_max_q > 32767 || s.hess_max_q < 1 || s.hess_max_q > 65535)
+            fail(SROCM_ERR_UNSUPPORTED, "quantized units must lie in 1..=32767 for gradients and 1..=65535 for hessians");
         QuantDev q{s.inv_grad_scale, s.inv_hess_scale, s.grad_max_q, s.hess_max_q, s.constant_hessian, s.stochastic, s.seed, s.iteration};
         if (rows) {
             k_quantize<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, q);
@@ -1044,7 +1047,7 @@ struct Context {
     DevBuf<MergeJob> d_merges;        // end of a tree: leaves whose expansion was dropped
     DevBuf<uint32_t> d_starts;
     Pinned<uint8_t> h_fix;            // staging of the runs and merges (rewritten only after a sync)
-    // split steps (k_step_rows, k_step_finish)
+    // split steps (k_step_rows, k_step_reduce, k_step_scan, k_step_cat, k_step_select)
     DevBuf<int32_t> step_partial;            // per slab: [cus + JMAX][256 * W] {g, h}
     DevBuf<unsigned long long> tile_status;  // per partition tile
     DevBuf<uint32_t> fin_counts;             // the jobs-selected counter of k_step_select

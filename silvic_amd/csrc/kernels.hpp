@@ -1573,7 +1573,7 @@ __device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_
 
 constexpr uint32_t STEP_TILE = 4096;          // rows per partition tile: TILE_RPT per thread of a 1024-thread block
 constexpr int TILE_RPT = STEP_TILE / 1024;
-constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_finish)
+constexpr uint32_t CG_COLS = 4;               // slab columns per column group (k_step_reduce, k_step_scan)
 // A split step's partials: workgroup b of a slab owns step_partial_stride(W) {g, h} pairs from pair b * stride,
 // whether it writes 256 * W pairs or 256 * W packed words (a step can mix both). The stride is padded so that
 // the same slot of consecutive partials does not fall at a power-of-two distance (which maps it to the same
@@ -1740,7 +1740,7 @@ struct GrowState {
     SplitCfgDev cfg;
     double sg, sh;
     uint32_t target_groups;   // k_step_rows workgroups a step is spread over
-    uint32_t ncg;             // column groups of k_step_finish
+    uint32_t ncg;             // column groups of k_step_reduce and k_step_scan
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
     uint32_t pad_;
 };
@@ -2277,11 +2277,11 @@ __global__ __launch_bounds__(512) void k_root_select(GrowState g) {
 // both children are stable; a leaf stored last-first is read back to front by the step that expands it and by
 // k_consolidate. Launches for a second or later slab only histogram.
 //
-// k_step_finish: work items (job, column group, bin chunk) handed out in order: each adds the job's partials of
-// its bins, writes the built child's histogram and forms the sibling by subtraction (learner.rs:356-371); the
-// last item of a column group scans its features for both children; the last group of a job selects both
-// children's splits (job_select); the last job runs advance. Hand-offs are counters that the last arriving
-// block resets; no block ever waits for another in k_step_finish.
+// Then, one launch each: k_step_reduce adds each job's partials (work items: job, column group, bin range), writes
+// the built child's histogram and forms the sibling by subtraction (learner.rs:356-371); k_step_scan and
+// k_step_cat scan every (job, feature, child); k_step_select selects both children's splits of each job
+// (job_select), and its last block to finish runs advance. That hand-off is a counter the last arriving block
+// resets; no block ever waits for another.
 // ---------------------------------------------------------------------------------------------------------
 
 struct StepArgs {
@@ -2721,7 +2721,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (tid == 0) a.fmt[blockIdx.x] = 0u;
 }
 
-// Four columns of one slab, reduced and scanned together by k_step_finish.
+// Four columns of one slab: a work unit of k_step_reduce and k_step_scan.
 struct ColGroup {
     uint64_t partial;  // the slab's partials, in {g, h} pairs from the start of the step partial buffer
     uint32_t width;    // the slab's W

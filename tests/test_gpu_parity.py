@@ -273,9 +273,11 @@ def compare_trees(d, o, name, exact_values=True):
 
 
 # (rows, features, leaves, gradient bins): the 700k-row root partitions in several tiles per workgroup; 300
-# features span three slabs; 32 gradient bins keep every workgroup's sums in {g, h} pairs.
+# features span three slabs; 32 gradient bins keep every workgroup's sums in {g, h} pairs; with 64 gradient bins
+# (1023 rows fill a packed word) the 1M-row steps flush their words several times within a workgroup.
 @pytest.mark.parametrize("rows,cols,leaves,qbins", [(20_000, 16, 31, 4), (400_000, 128, 255, 4), (700_000, 8, 63, 4),
-                                                    (60_000, 300, 63, 4), (150_000, 40, 63, 32)])
+                                                    (60_000, 300, 63, 4), (150_000, 40, 63, 32),
+                                                    (1_000_000, 8, 63, 64)])
 def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves, qbins):
     say("grow", rows, cols, leaves, qbins)
     data = silvic_amd.synthetic(2, rows=rows, cols=cols, seed=21)
