@@ -254,6 +254,29 @@ __device__ __forceinline__ void hist_split(uint32_t n, uint32_t max_groups, uint
     if (groups == 0) groups = 1;
 }
 
+// A lane's four adds per row dword, in the conflict-free order: at step k byte x = (k + rot) % 4, i.e. bits 8x..8x+7
+// (xs[k] = 8x), goes to column 4d + x (cols[k]).
+__device__ __forceinline__ void row_bin_lanes(uint32_t d, uint32_t rot, uint32_t (&xs)[4], uint32_t (&cols)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t x = (k + rot) & 3u;
+        xs[k] = 8u * x;
+        cols[k] = 4u * d + x;
+    }
+}
+
+// Adds gv to the LDS words (bin * W + column) of the four bins in a row dword: each bin is extracted in place (one
+// bit-field extract) and scaled into its word address with the column added (one shift-add).
+template <int W>
+__device__ __forceinline__ void add_row_bins(int32_t *lds, uint32_t dw, int32_t gv, const uint32_t (&xs)[4],
+                                             const uint32_t (&cols)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t b = __builtin_amdgcn_ubfe(dw, xs[k], 8u);
+        atomicAdd(&lds[b * W + cols[k]], gv);
+    }
+}
+
 // Loads are branch-free: row positions past the range are clamped to its last row and their gradients
 // zeroed, so the compiler issues every load of a step back to back instead of one masked load at a time. A
 // wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
@@ -283,6 +306,8 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
+    uint32_t xs[4], cols[4];
+    row_bin_lanes(d, rot, xs, cols);
     const uint32_t *rows = a.rows + lb;
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     uint32_t start = blockIdx.x * per;
@@ -306,15 +331,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
                 dw[u] = bins32[(size_t)r[u] * DW + d];
             }
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                int32_t gv = base + u * RPW + rsub < cend ? g[u] : 0;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    uint32_t x = (k + rot) & 3u;
-                    uint32_t b = (dw[u] >> (8u * x)) & 255u;
-                    atomicAdd(&lds[b * W + 4u * d + x], gv);
-                }
-            }
+            for (int u = 0; u < UNROLL; ++u) add_row_bins<W>(lds, dw[u], base + u * RPW + rsub < cend ? g[u] : 0, xs, cols);
         }
         __syncthreads();
 #pragma unroll
@@ -2513,6 +2530,8 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
+    uint32_t xs[4], cols[4];
+    row_bin_lanes(d, rot, xs, cols);
     const uint32_t last = c1 - 1;
     for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
         uint32_t r[UNROLL];
@@ -2526,15 +2545,7 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
             dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
         }
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                uint32_t x = (k + rot) & 3u;
-                uint32_t b = (dw[u] >> (8u * x)) & 255u;
-                atomicAdd(&lds[b * W + 4u * d + x], gv);
-            }
-        }
+        for (int u = 0; u < UNROLL; ++u) add_row_bins<W>(lds, dw[u], base + u * RPW + rsub < c1 ? gq[u] : 0, xs, cols);
     }
 }
 
