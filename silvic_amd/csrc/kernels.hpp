@@ -930,6 +930,21 @@ __device__ __forceinline__ void wave_argmax(double &g, int &i) {
     i = w == 0x7fffffff ? -1 : w;
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_max_u32_step(uint32_t v) {
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = dpp_max_u32_step<DPP_ROW_SHR1, 0xf>(v);
+    v = dpp_max_u32_step<DPP_ROW_SHR2, 0xf>(v);
+    v = dpp_max_u32_step<DPP_ROW_SHR4, 0xf>(v);
+    v = dpp_max_u32_step<DPP_ROW_SHR8, 0xf>(v);
+    v = dpp_max_u32_step<DPP_ROW_BCAST15, 0xa>(v);
+    v = dpp_max_u32_step<DPP_ROW_BCAST31, 0xc>(v);
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // A feature candidate as held by lane `owner`, broadcast to the wave.
 __device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
     FeatCand r;
@@ -1906,30 +1921,46 @@ __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
     return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
 }
 
+// A committed leaf's replay key: the top 23 bits of its positive gain (a positive double's bits order as its value),
+// then the lower leaf id (511 - id); 0 for a leaf without a split or a positive gain. One u32 max over the wave
+// finds the highest key; it is best_leaf's choice unless another leaf shares its gain prefix, which the replay
+// then settles on the exact gains.
+__device__ __forceinline__ uint32_t replay_key(double gain, uint32_t meta, uint32_t id) {
+    if (!(meta & 1u) || !(gain > 0.0)) return 0u;
+    uint32_t p = static_cast<uint32_t>(__builtin_bit_cast(uint64_t, gain) >> 40);
+    p = p ? p : 1u;
+    return (p << 9) | (GROW_MAX_LEAVES - 1u - id);
+}
+
 // The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave: lane l holds committed
-// leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves) in registers (gain, meta, speculative leaf, node
-// above, left flag), so a commit costs two wave reductions and the two new leaves' loads. Leaves the commits,
-// the committed-leaf arrays and the outcome in `s`.
+// leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves) in registers (replay key, meta, speculative leaf, node
+// above, left / has-split / NaN-gain flags). A commit is one u32 wave max of the keys (the reference's argmax only
+// matters while the best gain is positive: otherwise the tree stops), with an exact f64 argmax only when two
+// leaves share the winner's gain prefix; the rule that the first leaf with a split decides when its gain is NaN
+// takes a wave minimum, only while some leaf has a NaN gain. Leaves the commits, the committed-leaf arrays and the
+// outcome in `s`.
 template <int NPL>
 __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
     const uint32_t lane = threadIdx.x & 63u;
-    double rg[NPL];
-    uint32_t rm[NPL], rt[NPL];
+    uint32_t rk[NPL], rm[NPL], rt[NPL];
     int32_t rp[NPL];
-    uint32_t rl = 0, rtouch = 0;  // bit j: leaf lane + 64 j is a left child / changed by this replay
+    uint32_t rl = 0, rtouch = 0, rhas = 0, rnan = 0;  // bit j: leaf lane + 64 j is a left child / changed / ...
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const uint32_t id = lane + 64u * j;
-        rg[j] = 0.0;
+        rk[j] = 0;
         rm[j] = 0;
         rt[j] = 0;
         rp[j] = -1;
         if (id < n0) {
             rt[j] = s.leaf_t[id];
-            rg[j] = s.gain[rt[j]];
+            const double gj = s.gain[rt[j]];
             rm[j] = s.meta[rt[j]];
+            rk[j] = replay_key(gj, rm[j], id);
             rp[j] = s.pnode[id];
             rl |= s.is_left[id] ? 1u << j : 0u;
+            rhas |= (rm[j] & 1u) ? 1u << j : 0u;
+            rnan |= (rm[j] & 1u) && gj != gj ? 1u << j : 0u;
         }
     }
     uint32_t n = n0, nc = 0, blocker = 0;
@@ -1939,34 +1970,50 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
             done = true;
             break;
         }
-        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`),
-        // otherwise the first highest gain among the rest (a NaN later never wins)
-        int lfirst = 1 << 30, ki = -1;
-        double kg = 0.0;
-        bool lnan = false;
+        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
+        if (__ballot(rnan != 0u)) {
+            int lfirst = 1 << 30;
 #pragma unroll
-        for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
-            const uint32_t id = lane + 64u * j;
-            const bool has = id < n && (rm[j] & 1u);
-            const bool nan = rg[j] != rg[j];
-            if (has) lfirst = 2 * static_cast<int>(id) + (nan ? 1 : 0);
-            lnan = lnan || (has && nan);
-            if (has && !nan && (ki < 0 || rg[j] >= kg)) {
-                kg = rg[j];
-                ki = static_cast<int>(id);
+            for (int j = NPL - 1; j >= 0; --j)  // descending, so the lowest id is the one kept
+                if ((rhas >> j) & 1u) lfirst = 2 * static_cast<int>(lane + 64u * j) + static_cast<int>((rnan >> j) & 1u);
+            const int first = wave_min_i32(lfirst);
+            if (first < (1 << 30) && (first & 1)) {
+                done = true;
+                break;
             }
         }
-        bool nan_first = false;
-        if (__ballot(lnan)) {
-            const int first = wave_min_i32(lfirst);
-            nan_first = first < (1 << 30) && (first & 1);
-        }
-        wave_argmax(kg, ki);
-        if (nan_first || ki < 0 || !(kg > 0.0)) {
+        // otherwise the first highest gain among the rest (a NaN later never wins); none positive ends the tree
+        uint32_t lk = 0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) lk = rk[j] > lk ? rk[j] : lk;
+        const uint32_t best = wave_max_u32(lk);
+        if (best == 0u) {
             done = true;
             break;
         }
-        const uint32_t x = static_cast<uint32_t>(ki), jx = x >> 6, lx = x & 63u;
+        uint32_t x = GROW_MAX_LEAVES - 1u - (best & (GROW_MAX_LEAVES - 1u));
+        {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
+            const uint32_t bp = best >> 9;
+            uint32_t same = 0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) same += (rk[j] >> 9) == bp && rk[j] != best ? 1u : 0u;
+            if (__ballot(same != 0u)) {
+                double kg = 0.0;
+                int ki = -1;
+#pragma unroll
+                for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
+                    if ((rk[j] >> 9) != bp) continue;
+                    const double gj = s.gain[rt[j]];
+                    if (ki < 0 || gj >= kg) {
+                        kg = gj;
+                        ki = static_cast<int>(lane + 64u * j);
+                    }
+                }
+                wave_argmax(kg, ki);
+                x = static_cast<uint32_t>(ki);
+            }
+        }
+        const uint32_t jx = x >> 6, lx = x & 63u;
         uint32_t vm = 0, vt = 0;
         int32_t vp = 0;
 #pragma unroll
@@ -2001,13 +2048,13 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
         for (int j = 0; j < NPL; ++j) {
             if (jx == static_cast<uint32_t>(j) && lane == lx) {
                 rt[j] = kid;
-                rg[j] = g0;
+                rk[j] = replay_key(g0, m0, x);
                 rm[j] = m0;
                 rp[j] = node;
             }
             if (jn == static_cast<uint32_t>(j) && lane == ln) {
                 rt[j] = kid + 1;
-                rg[j] = g1;
+                rk[j] = replay_key(g1, m1, n);
                 rm[j] = m1;
                 rp[j] = node;
             }
@@ -2016,10 +2063,14 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
         if (lane == lx) {
             rl |= bx;
             rtouch |= bx;
+            rhas = (rhas & ~bx) | ((m0 & 1u) ? bx : 0u);
+            rnan = (rnan & ~bx) | ((m0 & 1u) && g0 != g0 ? bx : 0u);
         }
         if (lane == ln) {
             rl &= ~bn;
             rtouch |= bn;
+            rhas = (rhas & ~bn) | ((m1 & 1u) ? bn : 0u);
+            rnan = (rnan & ~bn) | ((m1 & 1u) && g1 != g1 ? bn : 0u);
         }
         ++nc;
         ++n;
@@ -2076,9 +2127,24 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     const uint32_t nc = s.ncommit, n = s.n;
     const bool done = s.done != 0;
 
-    // -- the commits applied to the tree (tree.rs:143-177): nodes, then the links into nodes split again
+    // -- the commits applied to the tree (tree.rs:143-177): nodes and the changed leaves, then the links into
+    // nodes split again
     const TreeDev &t = g.tree;
-    for (uint32_t c = tid; c < nc; c += nt) {
+    for (uint32_t id = tid; id < n; id += nt) {
+        if (!s.touched[id]) continue;
+        const uint32_t k = s.leaf_t[id];
+        const TLeaf &l = g.tl[k];
+        t.leaf_value[id] = l.value;
+        t.leaf_weight[id] = l.weight;
+        t.leaf_count[id] = l.cnt;
+        t.leaf_parent[id] = s.pnode[id];
+        t.leaf_depth[id] = l.depth;
+        t.leaf_range[2 * id] = l.begin;
+        t.leaf_range[2 * id + 1] = l.count;
+        g.leaf_t[id] = static_cast<int32_t>(k);
+        g.leaf_left[id] = s.is_left[id];
+    }
+    for (uint32_t c = nt - 1u - tid; c < nc; c += nt) {  // from the last thread down: beside the leaves' loads
         const TLeaf &p = g.tl[s.ck[c]];
         const SplitOut &info = p.best;
         const uint32_t node = n0 - 1 + c;
@@ -2101,20 +2167,6 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if (pn < 0) continue;
         if (s.cleft[c]) t.left_child[pn] = static_cast<int32_t>(n0 - 1 + c);
         else t.right_child[pn] = static_cast<int32_t>(n0 - 1 + c);
-    }
-    for (uint32_t id = tid; id < n; id += nt) {
-        if (!s.touched[id]) continue;
-        const uint32_t k = s.leaf_t[id];
-        const TLeaf &l = g.tl[k];
-        t.leaf_value[id] = l.value;
-        t.leaf_weight[id] = l.weight;
-        t.leaf_count[id] = l.cnt;
-        t.leaf_parent[id] = s.pnode[id];
-        t.leaf_depth[id] = l.depth;
-        t.leaf_range[2 * id] = l.begin;
-        t.leaf_range[2 * id + 1] = l.count;
-        g.leaf_t[id] = static_cast<int32_t>(k);
-        g.leaf_left[id] = s.is_left[id];
     }
     if (tid == 0) {
         ctl->num_leaves = n;
