@@ -326,6 +326,58 @@ def test_grown_tree_edge_cases(rocm, rows, cols, kw):
     assert np.array_equal(rocm.partition_rows(n), o_part[:n])
 
 
+def mirrored(half, feature):
+    """`half`, then `half` again with every other numerical feature's bin order reversed (missing values stay in the
+    NaN bin); `feature` is bin 0 in the first copy and bin 1 in the second."""
+    from silvic_amd.dataset import BinnedDataset, FeatureGroup
+    n = half.num_rows
+    groups = []
+    for gi, g in enumerate(half.groups):
+        d = np.concatenate([g.data, g.data]).reshape(2 * n, g.row_stride)
+        for j in g.features:
+            f = half.features[j]
+            if j == feature or f.num_bins == 0:
+                continue
+            assert f.kind == _abi.BINS_NUMERICAL
+            top = f.num_bins - 1 - int(bool(f.nan_bin))  # the last numerical bin
+            col = d[n:, f.column].astype(np.int64)
+            d[n:, f.column] = np.where(col <= top, top - col, col).astype(np.uint8)
+        if gi == half.features[feature].group:
+            c = half.features[feature].column
+            d[:n, c] = 0
+            d[n:, c] = 1
+        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
+    return BinnedDataset(2 * n, half.features, groups, half.total_bins, np.concatenate([half.label, half.label]))
+
+
+# Exact ties between leaves: two mirrored halves (negated gradients in exact quantized units, each numerical bin
+# order reversed) split apart at the root; every split of one half then has a twin of exactly equal gain in the
+# other (the same sums with the sides swapped), so best_leaf (learner.rs:418-429) breaks ties by the lower leaf id.
+def test_grown_tree_breaks_exact_gain_ties_by_leaf_id(rocm):
+    say("grow mirrored halves")
+    half = silvic_amd.synthetic(2, rows=30_000, cols=16, seed=11)
+    f0 = next(j for j, f in enumerate(half.features) if f.num_bins >= 3)
+    data = mirrored(half, f0)
+    rng = np.random.default_rng(4)
+    ga = rng.choice(np.array([-1.0, -0.5, 0.5, 1.0], np.float32), size=half.num_rows, p=[0.2, 0.2, 0.3, 0.3])
+    g = np.concatenate([ga, -ga]).astype(np.float32)
+    h = np.ones(data.num_rows, np.float32)
+    p = oracle.default_params(num_leaves=63, stochastic_rounding=0)
+    o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
+    gains = o_tree["split_gain"]
+    assert o_tree["split_feature"][0] == f0 and len(set(gains[1:].tolist())) <= (len(gains) - 1) // 2 + 1
+    rocm.load(data)
+    rocm.set_gradients(g, h)
+    spec = oracle.quant_spec(1.0, 1.0, None, 4, False, p.data_random_seed, 0)
+    rocm.quantize(spec)
+    n = rocm.reset_partition()
+    mask = oracle.feature_mask(data.features, 1.0, 2, 0)
+    d = rocm.grow(p.cfg, p.num_leaves, p.max_depth, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
+    compare_trees(d, dict(o_tree), "mirrored")
+    assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+    assert np.array_equal(rocm.partition_rows(n), o_part[:n])
+
+
 def test_grow_rejects_more_leaves_than_the_device_grows(rocm):
     say("grow 513 leaves")
     data = silvic_amd.synthetic(2, rows=5_000, cols=8, seed=5)
