@@ -328,6 +328,8 @@ struct Context {
     DevBuf<DevNode> d_nodes;
     Pinned<DevNode> h_nodes;
     Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
+    DevBuf<double> d_leaf_vw;           // a boosted tree's renewed leaf values, then weights (k_leaf_values)
+    Pinned<double> h_leaf_vw;           // and on their way to the host
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
@@ -891,7 +893,9 @@ struct Context {
 
     // The uploaded tree's leaf of every training row (leaf_of) and, when `sums` is set, the leaves' fixed-point
     // gradient sums over the in-bag rows, as leaf_sums over the grown tree's leaves gives them.
-    void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums) {
+    // With `device_sums` the sums stay in d_leaf_out for k_leaf_values (nothing waits on them).
+    void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums,
+                     bool device_sums = false) {
         leaf_of.alloc(rows);
         TreeLeavesArgs a{};
         a.colbins = train.col.p;
@@ -900,7 +904,7 @@ struct Context {
         a.nn = nn;
         a.nl = nl;
         a.leaf_of = leaf_of.p;
-        if (sums) {
+        if (sums || device_sums) {
             d_leaf_out.alloc(2 * nl);
             hip_check(hipMemsetAsync(d_leaf_out.p, 0, 2 * nl * 8, stream), "zero sums");
             a.grad = grad.p;
@@ -1567,8 +1571,27 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     std::vector<srocm_bin_split> splits;
     std::vector<GrowLeaf> leaves;
     std::vector<uint8_t> mask;
+    // A renewed tree's leaf values are made on the device and come back with the next wait on the stream (the
+    // next iteration's gradient maxima, or the end): its copy into `trees` waits for them.
+    struct Pending {
+        bool on = false;
+        HostTree tree;
+        std::vector<GrowLeaf> leaves;
+        uint32_t index = 0;
+    } pend;
+    auto finalize = [&]() {
+        if (!pend.on) return;
+        const uint32_t nl = pend.tree.num_leaves;
+        for (uint32_t l = 0; l < nl; ++l) {
+            pend.tree.leaf_value[l] = h_leaf_vw.p[l];
+            pend.tree.leaf_weight[l] = h_leaf_vw.p[nl + l];
+        }
+        if (trees) copy_tree(pend.tree, pend.leaves, &trees[pend.index]);
+        pend.on = false;
+    };
     for (uint32_t it = first; it < first + count; ++it) {
         auto [mg, mh] = compute_gradients();
+        finalize();
         srocm_quant_spec spec = make_quant_spec(mg, mh, constant_hessian, 1.0, p.num_grad_quant_bins, p.stochastic_rounding != 0,
                                                 p.data_random_seed, it);
         quantize(spec);
@@ -1611,22 +1634,38 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         const uint32_t nn = static_cast<uint32_t>(nodes.size()), nl = tree.num_leaves;
         upload_nodes(nodes.data(), nn, nl);
         static_assert(GROW_MAX_LEAVES <= LEAVES_MAX_LDS, "k_tree_leaves takes every device-grown tree");
-        if (p.quant_train_renew_leaf) {  // learner.rs:376-404: the rows' leaves from one walk give the sums and the scores
-            float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
-            std::vector<int64_t> sums(2 * static_cast<size_t>(nl));
-            tree_leaves(nn, nl, bag, gsc, hsc, sums.data());
-            for (size_t l = 0; l < leaves.size(); ++l) {
-                double sum_grad = static_cast<double>(sums[2 * l]) / static_cast<double>(gsc);
-                double sum_hess = static_cast<double>(sums[2 * l + 1]) / static_cast<double>(hsc);
-                tree.leaf_value[l] = round_to_zero(leaf_output_h(sum_grad, sum_hess, p.cfg.lambda_l1, p.cfg.lambda_l2));
-                tree.leaf_weight[l] = sum_hess;
-            }
+        const bool bias = trees_added == 0 && init_score_value != 0.0;
+        if (p.quant_train_renew_leaf) {
+            // learner.rs:376-404: the rows' leaves from one walk give the sums and the scores; the leaf values,
+            // shrunk (and moved by the initial score), come from k_leaf_values and reach the host later
+            const float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
+            tree_leaves(nn, nl, bag, gsc, hsc, nullptr, true);
+            d_leaf_values.alloc(nl);
+            d_leaf_vw.alloc(2 * static_cast<size_t>(nl));
+            h_leaf_vw.alloc(2 * static_cast<size_t>(nl));
+            LeafValueArgs la{d_leaf_out.p, nl, bias ? 1u : 0u, gsc, hsc, p.cfg.lambda_l1, p.cfg.lambda_l2,
+                             p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + nl, d_leaf_values.p};
+            k_leaf_values<<<1, 512, 0, stream>>>(la);
+            launch_check("k_leaf_values");
+            apply_tree(train, nn, 0.0f, true);
+            for (auto &v : valid) apply_tree(v, nn, 0.0f, false);
+            hip_check(hipMemcpyAsync(h_leaf_vw.p, d_leaf_vw.p, 2 * static_cast<size_t>(nl) * sizeof(double),
+                                     hipMemcpyDeviceToHost, stream), "read leaf values");
+            tree.shrink(p.learning_rate);  // the internal values (the leaf values are replaced on arrival)
+            if (bias) tree.add_bias(init_score_value);
+            pend.on = true;
+            pend.tree = tree;
+            pend.leaves = leaves;
+            pend.index = done;
+            ++done;
+            ++trees_added;
+            continue;
         }
         // boosting.rs:313-324
         tree.shrink(p.learning_rate);
         std::vector<float> lv(tree.leaf_value.size());
         for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i]);
-        if (trees_added == 0 && init_score_value != 0.0) {
+        if (bias) {
             tree.add_bias(init_score_value);
             for (size_t i = 0; i < lv.size(); ++i) lv[i] = static_cast<float>(tree.leaf_value[i] - init_score_value);  // replay.rs:38-40
         }
@@ -1636,6 +1675,10 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         if (trees) copy_tree(tree, leaves, &trees[done]);
         ++done;
         ++trees_added;
+    }
+    if (pend.on) {
+        sync();
+        finalize();
     }
     return done;
 }

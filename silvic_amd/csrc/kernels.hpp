@@ -730,6 +730,39 @@ __device__ __forceinline__ double leaf_output(double g, double h, double l1, dou
     return -(sign * reg) / (h + l2);
 }
 
+// The renewed leaf values of a grown tree from its leaves' fixed-point sums (learner.rs:376-404), shrunk by the
+// learning rate (tree.rs:180-185) and, for the first tree, moved by the initial score (tree.rs:188-193, with the
+// f32 values added to the scores taken without it: replay.rs:38-40): the host's double operations, in its order.
+// One block; leaf l: value[l], weight[l] (double) and lv[l] (the f32 added to the scores).
+struct LeafValueArgs {
+    const unsigned long long *sums;  // [nl][2] i64 fixed-point {g, h}
+    uint32_t nl, add_bias;
+    float gs, hs;                    // the fixed-point scales
+    double l1, l2, rate, bias;
+    double *value, *weight;
+    float *lv;
+};
+
+__device__ __forceinline__ double round_to_zero_d(double v) { return fabs(v) > static_cast<double>(1e-35f) ? v : 0.0; }
+
+__global__ void k_leaf_values(LeafValueArgs a) {
+    for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) {
+        const double sg = static_cast<double>(static_cast<int64_t>(a.sums[2 * l])) / static_cast<double>(a.gs);
+        const double sh = static_cast<double>(static_cast<int64_t>(a.sums[2 * l + 1])) / static_cast<double>(a.hs);
+        double v = round_to_zero_d(leaf_output(sg, sh, a.l1, a.l2));
+        v = round_to_zero_d(v * a.rate);
+        float f = static_cast<float>(v);
+        if (a.add_bias) {
+            v = round_to_zero_d(v + a.bias);
+            f = static_cast<float>(v - a.bias);
+        }
+        a.value[l] = v;
+        a.weight[l] = sh;
+        a.lv[l] = f;
+    }
+}
+
+
 // split.rs:214-233 LeafCtx::new
 __device__ __forceinline__ Ctx make_ctx(const SplitCfgDev &cfg, double sg, double sh, double ug, double uh, int64_t count) {
     Ctx c;
