@@ -23,6 +23,7 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <functional>
 #include <vector>
 
 namespace {
@@ -328,7 +329,9 @@ struct Context {
     DevBuf<DevNode> d_nodes;
     Pinned<DevNode> h_nodes;
     Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
-    DevBuf<double> d_leaf_vw;           // a boosted tree's renewed leaf values, then weights (k_leaf_values)
+    DevBuf<double> d_leaf_vw;           // a boosted tree's renewed leaf values, then (from GROW_MAX_LEAVES) weights
+    DevBuf<uint32_t> d_gate;            // the boosted tree's leaves once it is complete with a split (k_tree_nodes)
+    hipEvent_t tree_event = nullptr;    // a grown tree's readback has landed
     Pinned<double> h_leaf_vw;           // and on their way to the host
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
@@ -339,6 +342,7 @@ struct Context {
     Profile prof;
 
     ~Context() {
+        if (tree_event) (void)hipEventDestroy(tree_event);
         for (auto &e : prof.hist_events) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
@@ -877,8 +881,8 @@ struct Context {
     void apply_tree(DevData &d, uint32_t nn, float v0, bool from_leaf_of) {
         if (d.rows == 0) return;
         if (nn == 0) k_add_const<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, v0);
-        else if (from_leaf_of) k_add_leaf_values<<<grid_rows(d.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, d.scores.p, d.rows);
-        else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p);
+        else if (from_leaf_of) k_add_leaf_values<<<grid_rows(d.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, d.scores.p, d.rows, nullptr);
+        else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p, nullptr);
         launch_check("k_add_tree");
     }
 
@@ -893,9 +897,7 @@ struct Context {
 
     // The uploaded tree's leaf of every training row (leaf_of) and, when `sums` is set, the leaves' fixed-point
     // gradient sums over the in-bag rows, as leaf_sums over the grown tree's leaves gives them.
-    // With `device_sums` the sums stay in d_leaf_out for k_leaf_values (nothing waits on them).
-    void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums,
-                     bool device_sums = false) {
+    void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums) {
         leaf_of.alloc(rows);
         TreeLeavesArgs a{};
         a.colbins = train.col.p;
@@ -904,7 +906,7 @@ struct Context {
         a.nn = nn;
         a.nl = nl;
         a.leaf_of = leaf_of.p;
-        if (sums || device_sums) {
+        if (sums) {
             d_leaf_out.alloc(2 * nl);
             hip_check(hipMemsetAsync(d_leaf_out.p, 0, 2 * nl * 8, stream), "zero sums");
             a.grad = grad.p;
@@ -1158,8 +1160,9 @@ struct Context {
 
     // `final_order`: leave every leaf's rows ascending in the partition (the reference's order); without it the rows
     // of each leaf are only grouped, which is all the boosting loop needs before the next tree resets them.
+    // `after_steps` (when set) is called after each batch of split steps is launched, before the host waits on it.
     void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves,
-              bool final_order = true);
+              bool final_order = true, const std::function<void(const GrowState &)> *after_steps = nullptr);
 
     void copy_tree(const HostTree &t, const std::vector<GrowLeaf> &leaves, srocm_grown_tree *out) const {
         if (out->capacity_leaves < t.num_leaves) fail(SROCM_ERR_DEVICE, "grown tree has more leaves than the output holds");
@@ -1258,7 +1261,8 @@ std::pair<double, double> Context::compute_gradients() {
 // subtracts, searches the children and writes the tree. The host checks for the end of the tree once per batch of
 // steps (sized by the last tree's step count), reads the finished tree, and enqueues the final row order.
 void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits,
-                   std::vector<GrowLeaf> &leaves, bool final_order) {
+                   std::vector<GrowLeaf> &leaves, bool final_order,
+                   const std::function<void(const GrowState &)> *after_steps) {
     require_loaded();
     if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
     check_range(spec.root);
@@ -1352,7 +1356,16 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 k_step_select<<<JMAX, 512, 0, stream>>>(g, sa2);
                 launch_check("k_step_select");
             }
-            hc = read_ctl();
+            if (after_steps) {  // queued behind the readback, so the host takes the tree while they run
+                if (!tree_event) hip_check(hipEventCreateWithFlags(&tree_event, hipEventDisableTiming), "hipEventCreate");
+                hip_check(hipMemcpyAsync(hb, dtree.p, lay.bytes, hipMemcpyDeviceToHost, stream), "read tree");
+                hip_check(hipEventRecord(tree_event, stream), "event");
+                (*after_steps)(g);
+                hip_check(hipEventSynchronize(tree_event), "event synchronize");
+                hc = *reinterpret_cast<const GrowCtl *>(hb + lay.ctl);
+            } else {
+                hc = read_ctl();
+            }
             if (hc.done) break;
             if (s >= max_steps) fail(SROCM_ERR_INTERNAL, "the device learner did not finish the tree");
             batch = 2;
@@ -1369,6 +1382,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                                      (e[6] ? " workgroups, packed)" : " workgroups)"));
     }
     if (hc.error == 3) fail(SROCM_ERR_INTERNAL, "a partition tile waited too long for an earlier tile's count");
+    if (hc.error == 6) fail(SROCM_ERR_INTERNAL, "malformed device tree");
     if (hc.error) fail(SROCM_ERR_INTERNAL, "device learner error " + std::to_string(hc.error));
     const uint32_t n = hc.num_leaves, ni = n - 1, ntent = hc.ntent;
     auto *iv = reinterpret_cast<const double *>(hb + lay.iv);
@@ -1582,9 +1596,11 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     auto finalize = [&]() {
         if (!pend.on) return;
         const uint32_t nl = pend.tree.num_leaves;
+        // the leaves k_tree_nodes let through (after the tree's readback, so checked here)
+        if (h_leaf_vw.p[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
         for (uint32_t l = 0; l < nl; ++l) {
             pend.tree.leaf_value[l] = h_leaf_vw.p[l];
-            pend.tree.leaf_weight[l] = h_leaf_vw.p[nl + l];
+            pend.tree.leaf_weight[l] = h_leaf_vw.p[GROW_MAX_LEAVES + l];
         }
         if (trees) copy_tree(pend.tree, pend.leaves, &trees[pend.index]);
         pend.on = false;
@@ -1592,6 +1608,9 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     for (uint32_t it = first; it < first + count; ++it) {
         auto [mg, mh] = compute_gradients();
         finalize();
+        const bool bias = trees_added == 0 && init_score_value != 0.0;
+        const bool renew = p.quant_train_renew_leaf != 0;
+        const float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
         srocm_quant_spec spec = make_quant_spec(mg, mh, constant_hessian, 1.0, p.num_grad_quant_bins, p.stochastic_rounding != 0,
                                                 p.data_random_seed, it);
         quantize(spec);
@@ -1614,7 +1633,51 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         gs.root = srocm_leaf_range{0, local_rows};
         gs.root_count = local_rows;
         const bool last = it + 1 == first + count;
-        grow(gs, tree, splits, leaves, last);
+        // learner.rs:376-404 on the device, queued behind each batch of the tree's steps and gated there by the tree
+        // being complete with a split: the rows' leaves from one walk give the sums; k_leaf_values makes the shrunk
+        // (and, for the first tree, biased) leaf values; the scores take them; the values go to the host
+        const std::function<void(const GrowState &)> renew_on_device = [&](const GrowState &gst) {
+            const size_t L = GROW_MAX_LEAVES;
+            d_nodes.alloc(L);
+            d_leaf_out.alloc(2 * L);
+            d_leaf_values.alloc(L);
+            d_leaf_vw.alloc(2 * L + 1);
+            h_leaf_vw.alloc(2 * L + 1);
+            d_gate.alloc(1);
+            leaf_of.alloc(rows);
+            k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, d_leaf_vw.p + 2 * L);
+            launch_check("k_tree_nodes");
+            TreeLeavesArgs a{};
+            a.colbins = train.col.p;
+            a.rows = rows;
+            a.nodes = d_nodes.p;
+            a.leaf_of = leaf_of.p;
+            a.grad = grad.p;
+            a.hess = hess.p;
+            a.gs = gsc;
+            a.hs = hsc;
+            a.sums = d_leaf_out.p;
+            a.bag = bag.kind == SROCM_BAG_BERNOULLI ? 1u : 0u;
+            a.bag_seed = bag.seed;
+            a.bag_round = bag.round;
+            a.row_offset = row_offset;
+            a.fraction = bag.fraction;
+            a.gate = d_gate.p;
+            k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS)), TL_THREADS, 0, stream>>>(a);
+            launch_check("k_tree_leaves");
+            LeafValueArgs la{d_leaf_out.p, d_gate.p, 0u, bias ? 1u : 0u, gsc, hsc, p.cfg.lambda_l1, p.cfg.lambda_l2,
+                             p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + L, d_leaf_values.p};
+            k_leaf_values<<<1, 512, 0, stream>>>(la);
+            launch_check("k_leaf_values");
+            if (train.rows)
+                k_add_leaf_values<<<grid_rows(train.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, train.scores.p, train.rows, d_gate.p);
+            for (auto &v : valid)
+                if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
+            launch_check("k_add_tree");
+            hip_check(hipMemcpyAsync(h_leaf_vw.p, d_leaf_vw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost, stream),
+                      "read leaf values");
+        };
+        grow(gs, tree, splits, leaves, last, renew ? &renew_on_device : nullptr);
         if (tree.num_leaves == 1) {  // boosting.rs:301-310
             if (trees_added == 0) {
                 HostTree c;
@@ -1625,32 +1688,10 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             }
             break;
         }
-        std::vector<srocm_device_node> nodes(splits.size());
-        for (size_t k = 0; k < nodes.size(); ++k) {
-            nodes[k].split = splits[k];
-            nodes[k].left = tree.left_child[k];
-            nodes[k].right = tree.right_child[k];
-        }
-        const uint32_t nn = static_cast<uint32_t>(nodes.size()), nl = tree.num_leaves;
-        upload_nodes(nodes.data(), nn, nl);
         static_assert(GROW_MAX_LEAVES <= LEAVES_MAX_LDS, "k_tree_leaves takes every device-grown tree");
-        const bool bias = trees_added == 0 && init_score_value != 0.0;
-        if (p.quant_train_renew_leaf) {
-            // learner.rs:376-404: the rows' leaves from one walk give the sums and the scores; the leaf values,
-            // shrunk (and moved by the initial score), come from k_leaf_values and reach the host later
-            const float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
-            tree_leaves(nn, nl, bag, gsc, hsc, nullptr, true);
-            d_leaf_values.alloc(nl);
-            d_leaf_vw.alloc(2 * static_cast<size_t>(nl));
-            h_leaf_vw.alloc(2 * static_cast<size_t>(nl));
-            LeafValueArgs la{d_leaf_out.p, nl, bias ? 1u : 0u, gsc, hsc, p.cfg.lambda_l1, p.cfg.lambda_l2,
-                             p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + nl, d_leaf_values.p};
-            k_leaf_values<<<1, 512, 0, stream>>>(la);
-            launch_check("k_leaf_values");
-            apply_tree(train, nn, 0.0f, true);
-            for (auto &v : valid) apply_tree(v, nn, 0.0f, false);
-            hip_check(hipMemcpyAsync(h_leaf_vw.p, d_leaf_vw.p, 2 * static_cast<size_t>(nl) * sizeof(double),
-                                     hipMemcpyDeviceToHost, stream), "read leaf values");
+        if (renew) {
+            // the scores and leaf values were queued behind the tree's steps (renew_on_device); the values reach
+            // the host with the next wait
             tree.shrink(p.learning_rate);  // the internal values (the leaf values are replaced on arrival)
             if (bias) tree.add_bias(init_score_value);
             pend.on = true;
@@ -1661,6 +1702,14 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             ++trees_added;
             continue;
         }
+        std::vector<srocm_device_node> nodes(splits.size());
+        for (size_t k = 0; k < nodes.size(); ++k) {
+            nodes[k].split = splits[k];
+            nodes[k].left = tree.left_child[k];
+            nodes[k].right = tree.right_child[k];
+        }
+        const uint32_t nn = static_cast<uint32_t>(nodes.size()), nl = tree.num_leaves;
+        upload_nodes(nodes.data(), nn, nl);
         // boosting.rs:313-324
         tree.shrink(p.learning_rate);
         std::vector<float> lv(tree.leaf_value.size());

@@ -597,8 +597,10 @@ struct DevNode {
     uint32_t pad;
 };
 
+// `gate` (when set): the leaves of the tree to add, 0 for none (k_tree_nodes).
 __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint64_t rows, const DevNode *__restrict__ nodes,
-                           const float *__restrict__ leaf_values, float *__restrict__ scores) {
+                           const float *__restrict__ leaf_values, float *__restrict__ scores, const uint32_t *gate) {
+    if (gate && *gate == 0u) return;
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
         int32_t node = 0;
         while (node >= 0) {
@@ -626,6 +628,7 @@ struct TreeLeavesArgs {
     uint32_t bag, bag_seed, bag_round; // bag != 0: only rows in the bag (quantize.rs:147-149) are summed
     uint64_t row_offset;
     double fraction;
+    const uint32_t *gate;              // when set: the leaves (nn, nl from it), 0 for no tree (k_tree_nodes)
 };
 constexpr uint32_t LEAVES_MAX_LDS = 512;  // the trees k_tree_leaves takes (device growth grows up to this)
 constexpr int TL_RPT = 8;
@@ -634,9 +637,15 @@ constexpr uint32_t TL_THREADS = 512;
 __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
     __shared__ DevNode sn[LEAVES_MAX_LDS - 1];
     __shared__ unsigned long long ls[LEAVES_MAX_LDS][2];
-    for (uint32_t k = threadIdx.x; k < a.nn; k += blockDim.x) sn[k] = a.nodes[k];
+    uint32_t nn = a.nn, nl = a.nl;
+    if (a.gate) {
+        nl = *a.gate;
+        if (nl == 0u || nl > LEAVES_MAX_LDS) return;
+        nn = nl - 1u;
+    }
+    for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) sn[k] = a.nodes[k];
     if (a.grad)
-        for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
+        for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
     __syncthreads();
     const uint64_t stride = static_cast<uint64_t>(TL_RPT) * gridDim.x * blockDim.x;
     for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; base < a.rows; base += stride) {
@@ -674,7 +683,7 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
     }
     if (!a.grad) return;
     __syncthreads();
-    for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) {
+    for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) {
         if (ls[l][0]) atomicAdd(&a.sums[2 * l], ls[l][0]);
         if (ls[l][1]) atomicAdd(&a.sums[2 * l + 1], ls[l][1]);
     }
@@ -682,7 +691,8 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
 
 // scores[r] += the value of row r's leaf: the f32 add of k_add_tree, in row order.
 __global__ void k_add_leaf_values(const uint16_t *__restrict__ leaf_of, const float *__restrict__ leaf_values,
-                                  float *__restrict__ scores, uint64_t rows) {
+                                  float *__restrict__ scores, uint64_t rows, const uint32_t *gate) {
+    if (gate && *gate == 0u) return;
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
         scores[r] += leaf_values[leaf_of[r]];
 }
@@ -736,6 +746,7 @@ __device__ __forceinline__ double leaf_output(double g, double h, double l1, dou
 // One block; leaf l: value[l], weight[l] (double) and lv[l] (the f32 added to the scores).
 struct LeafValueArgs {
     const unsigned long long *sums;  // [nl][2] i64 fixed-point {g, h}
+    const uint32_t *gate;            // when set: nl from it, 0 for no tree (k_tree_nodes)
     uint32_t nl, add_bias;
     float gs, hs;                    // the fixed-point scales
     double l1, l2, rate, bias;
@@ -746,7 +757,8 @@ struct LeafValueArgs {
 __device__ __forceinline__ double round_to_zero_d(double v) { return fabs(v) > static_cast<double>(1e-35f) ? v : 0.0; }
 
 __global__ void k_leaf_values(LeafValueArgs a) {
-    for (uint32_t l = threadIdx.x; l < a.nl; l += blockDim.x) {
+    const uint32_t nl = a.gate ? *a.gate : a.nl;
+    for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) {
         const double sg = static_cast<double>(static_cast<int64_t>(a.sums[2 * l])) / static_cast<double>(a.gs);
         const double sh = static_cast<double>(static_cast<int64_t>(a.sums[2 * l + 1])) / static_cast<double>(a.hs);
         double v = round_to_zero_d(leaf_output(sg, sh, a.l1, a.l2));
@@ -2347,6 +2359,43 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             ctl->expansions = expansions0 + njobs;
             ctl->steps = steps0 + 1;
         }
+    }
+}
+
+// After a grown tree's steps: when the tree is complete with at least one split, its nodes for k_tree_leaves and
+// k_add_tree (as the host builds them from the tree it reads back: the split's bins, the column of its feature,
+// the children), its leaf sums zeroed, and *gate = its leaves; *gate = 0 otherwise (an unfinished tree or one
+// that never split: the gated kernels after it do nothing). Every node is checked as the host checks an uploaded
+// tree (a known feature; an internal child after its parent, a leaf child among the leaves), so the walks over it
+// end; a malformed tree flags ctl->error = 6 and closes the gate. *gate_out: the gate, for the host. One block.
+__global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *sums, uint32_t *gate, double *gate_out) {
+    __shared__ uint32_t bad;
+    GrowCtl *ctl = g.ctl;
+    const uint32_t n = ctl->done && !ctl->error ? ctl->num_leaves : 0u;
+    const uint32_t nl = n > 1u && n <= LEAVES_MAX_LDS ? n : 0u, nn = nl ? nl - 1u : 0u;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) {
+        DevNode d;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) d.left_bins[w] = g.tree.left_bins[static_cast<size_t>(k) * 8 + w];
+        const int32_t f = g.tree.split_feature[k];
+        d.feature = f >= 0 && static_cast<uint32_t>(f) < g.nf ? g.feats[f].col : 0u;
+        d.left = g.tree.left_child[k];
+        d.right = g.tree.right_child[k];
+        d.pad = 0;
+        nodes[k] = d;
+        bool ok = f >= 0 && static_cast<uint32_t>(f) < g.nf;
+        for (const int32_t c : {d.left, d.right})
+            ok = ok && (c >= 0 ? static_cast<uint32_t>(c) > k && static_cast<uint32_t>(c) < nn : static_cast<uint32_t>(~c) < nl);
+        if (!ok) atomicOr(&bad, 1u);
+    }
+    for (uint32_t i = threadIdx.x; i < 2u * nl; i += blockDim.x) sums[i] = 0ull;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (bad) ctl->error = 6;
+        *gate = bad ? 0u : nl;
+        *gate_out = static_cast<double>(bad ? 0u : nl);
     }
 }
 
