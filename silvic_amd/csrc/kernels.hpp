@@ -1918,6 +1918,13 @@ __global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_coun
         g.tree.leaf_depth[0] = 0;
         g.tree.leaf_range[0] = root_begin;
         g.tree.leaf_range[1] = root_count;
+        // both step plans empty until advance writes one: a step launched on an empty plan does nothing
+        for (int k = 0; k < 2; ++k) {
+            g.plans[k].njobs = 0;
+            g.plans[k].total_groups = 0;
+            g.plans[k].total_red = 0;
+            g.plans[k].total_scan = 0;
+        }
     }
 }
 
@@ -2733,8 +2740,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     __shared__ int32_t lds[256 * W];
     __shared__ StepShared sh;
 
-    if (a.ctl->done) return;
-    StepPlan &P = *a.plan;
+    StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     if (blockIdx.x >= P.total_groups) return;
     const uint32_t j = job_of(P.group_base, P.njobs, blockIdx.x);
     JobPlan &J = P.jobs[j];
@@ -3036,8 +3042,7 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
 // own format (packed: one 16-byte load; {g, h} pairs: two), and the stripes meet in LDS. grid: any, 256 threads.
 __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs a) {
     __shared__ int64_t red[8][256];  // the stripes' sums, [value][thread]: conflict-free
-    if (g.ctl->done) return;
-    const StepPlan &P = *a.plan;
+    const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     const uint32_t tid = threadIdx.x;
     for (uint32_t item = blockIdx.x; item < P.total_red; item += gridDim.x) {
         const uint32_t j = job_of(P.red_base, P.njobs, item);
@@ -3143,8 +3148,7 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
 // both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's.
 // grid: any, 256 threads.
 __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) {
-    if (g.ctl->done) return;
-    const StepPlan &P = *a.plan;
+    const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t total = P.total_scan * (2u * CG_COLS);  // scan items count column groups
     for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
@@ -3176,8 +3180,7 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
 // grid-stride loop. grid: any, 256 threads.
 __global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
     __shared__ CatScratch cats[4];
-    if (g.ctl->done) return;
-    const StepPlan &P = *a.plan;
+    const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t per_job = 2 * a.ncat, total = P.njobs * per_job;
     for (uint32_t item = blockIdx.x * 4 + wave; item < total; item += gridDim.x * 4) {
@@ -3199,6 +3202,14 @@ __global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
 // Block j selects both children of job j (job_select); the last block to finish runs advance. grid: JMAX blocks.
 __global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) {
     __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
+    // the next plan stays empty unless advance writes it (it runs after every block has arrived, so after this):
+    // the steps after a finished tree do nothing without reading the control block
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.next->njobs = 0;
+        a.next->total_groups = 0;
+        a.next->total_red = 0;
+        a.next->total_scan = 0;
+    }
     if (g.ctl->done) return;
     StepPlan &P = *a.plan;
     const uint32_t j = blockIdx.x;
