@@ -2316,8 +2316,11 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const uint32_t tiles_before = wave_excl_sum(ntiles);
         const uint32_t total_tiles = wave_total(ntiles);
         uint32_t groups = 0;
-        if (on) {  // at most `per` tiles a workgroup in every job, so no job's workgroups run long
-            const uint32_t per = total_tiles > g.target_groups ? (total_tiles + g.target_groups - 1) / g.target_groups : 1u;
+        if (on) {  // at most `per` tiles a workgroup in every job, so no job's workgroups run long; the rounding up in
+            // each job costs at most one workgroup a job, so with target - njobs per share the step fits in one
+            // round of workgroups (one per compute unit)
+            const uint32_t share = g.target_groups > njobs ? g.target_groups - njobs : 1u;
+            const uint32_t per = total_tiles > g.target_groups ? (total_tiles + share - 1) / share : 1u;
             groups = (ntiles + per - 1) / per;
             if (groups == 0) groups = 1;
         }
