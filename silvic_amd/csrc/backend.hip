@@ -331,8 +331,11 @@ struct Context {
     Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
     DevBuf<double> d_leaf_vw;           // a boosted tree's renewed leaf values, then (from GROW_MAX_LEAVES) weights
     DevBuf<uint32_t> d_gate;            // the boosted tree's leaves once it is complete with a split (k_tree_nodes)
+    DevBuf<DevScales> d_scales;         // the boosting loop's quantization, made on the device (k_quant_spec)
+    const DevScales *grow_dsc = nullptr;  // set while the boosting loop grows: the scales of GrowState
     hipEvent_t tree_event = nullptr;    // a grown tree's readback has landed
-    Pinned<double> h_leaf_vw;           // and on their way to the host
+    Pinned<double> h_leaf_vw[2];        // and on their way to the host (alternate trees, so one lands while the
+                                        // host still reads the other)
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
@@ -587,6 +590,7 @@ struct Context {
     uint32_t grid_rows(uint64_t n) const { return static_cast<uint32_t>(std::min<uint64_t>(std::max<uint64_t>(div_up(n, 256), 1), cus * 8ull)); }
 
     std::pair<double, double> compute_gradients();
+    void launch_gradients();  // the gradients and their maxima, without waiting for them
 
     std::pair<double, double> set_gradients(const float *g, const float *h, uint64_t n) {
         require_loaded();
@@ -999,7 +1003,7 @@ struct Context {
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             dim3 grid(div_up(num_features, 4), 1);
-            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p);
+            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
             launch_check("k_split_scan");
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
@@ -1152,6 +1156,7 @@ struct Context {
         g.cfg = cfg_dev(spec.cfg);
         g.sg = spec.grad_scale;
         g.sh = spec.hess_scale;
+        g.dsc = grow_dsc;
         g.target_groups = cus;
         g.ncg = ncg;
         g.flush_rows = flush_rows();
@@ -1241,6 +1246,11 @@ void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint6
 
 // objective/regression.rs:70-93 and objective/binary.rs:27-50 on the device; maxima as cpu.rs:774-778.
 std::pair<double, double> Context::compute_gradients() {
+    launch_gradients();
+    return read_maxima();
+}
+
+void Context::launch_gradients() {
     require_loaded();
     if (objective != SROCM_OBJ_REGRESSION && objective != SROCM_OBJ_BINARY)
         fail(SROCM_ERR_UNSUPPORTED, "this objective's gradients come through srocm_set_gradients");
@@ -1253,7 +1263,6 @@ std::pair<double, double> Context::compute_gradients() {
             k_grad_binary<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, sigmoid, scalars.p + 1);
         launch_check("k_grad");
     }
-    return read_maxima();
 }
 
 // learner.rs:121-352 on the device: split steps are enqueued without waiting; the device replays the reference's
@@ -1309,7 +1318,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
         k_root_prep<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_prep");
-        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr);
+        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, g.dsc);
         launch_check("k_split_scan");
         k_root_select<<<1, 512, 0, stream>>>(g);
         launch_check("k_root_select");
@@ -1592,28 +1601,38 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         HostTree tree;
         std::vector<GrowLeaf> leaves;
         uint32_t index = 0;
+        uint32_t buf = 0;  // h_leaf_vw[buf]
     } pend;
+    uint32_t vw_buf = 0;  // the h_leaf_vw the next renewed tree lands in
     auto finalize = [&]() {
         if (!pend.on) return;
         const uint32_t nl = pend.tree.num_leaves;
+        const double *vw = h_leaf_vw[pend.buf].p;
         // the leaves k_tree_nodes let through (after the tree's readback, so checked here)
-        if (h_leaf_vw.p[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
+        if (vw[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
         for (uint32_t l = 0; l < nl; ++l) {
-            pend.tree.leaf_value[l] = h_leaf_vw.p[l];
-            pend.tree.leaf_weight[l] = h_leaf_vw.p[GROW_MAX_LEAVES + l];
+            pend.tree.leaf_value[l] = vw[l];
+            pend.tree.leaf_weight[l] = vw[GROW_MAX_LEAVES + l];
         }
         if (trees) copy_tree(pend.tree, pend.leaves, &trees[pend.index]);
         pend.on = false;
     };
     for (uint32_t it = first; it < first + count; ++it) {
-        auto [mg, mh] = compute_gradients();
-        finalize();
+        // quantize.rs:56-84 on the device: nothing waits for the gradient maxima
+        launch_gradients();
+        d_scales.alloc(1);
+        k_quant_spec<<<1, 64, 0, stream>>>(scalars.p + 1, d_scales.p, p.num_grad_quant_bins, constant_hessian ? 1u : 0u, 1.0,
+                                           p.stochastic_rounding != 0 ? 1u : 0u, p.data_random_seed, it);
+        launch_check("k_quant_spec");
+        if (rows) {
+            k_quantize_dev<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, d_scales.p);
+            launch_check("k_quantize");
+        }
+        max_gq = static_cast<int64_t>(p.num_grad_quant_bins / 2);
+        max_hq = static_cast<int64_t>(p.num_grad_quant_bins);
+        quantized_once = true;
         const bool bias = trees_added == 0 && init_score_value != 0.0;
         const bool renew = p.quant_train_renew_leaf != 0;
-        const float gsc = fixed_point_scale(mg), hsc = fixed_point_scale(mh);
-        srocm_quant_spec spec = make_quant_spec(mg, mh, constant_hessian, 1.0, p.num_grad_quant_bins, p.stochastic_rounding != 0,
-                                                p.data_random_seed, it);
-        quantize(spec);
         srocm_bag bag{};
         if (p.bagging_fraction < 1.0 && p.bagging_freq > 0) {
             bag.kind = SROCM_BAG_BERNOULLI;
@@ -1627,8 +1646,8 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         gs.cfg = p.cfg;
         gs.num_leaves = p.num_leaves;
         gs.max_depth = p.max_depth;
-        gs.grad_scale = spec.grad_scale;
-        gs.hess_scale = spec.hess_scale;
+        gs.grad_scale = 1.0;  // unused: GrowState takes d_scales
+        gs.hess_scale = 1.0;
         gs.feature_mask = mask.data();
         gs.root = srocm_leaf_range{0, local_rows};
         gs.root_count = local_rows;
@@ -1642,7 +1661,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             d_leaf_out.alloc(2 * L);
             d_leaf_values.alloc(L);
             d_leaf_vw.alloc(2 * L + 1);
-            h_leaf_vw.alloc(2 * L + 1);
+            h_leaf_vw[vw_buf].alloc(2 * L + 1);
             d_gate.alloc(1);
             leaf_of.alloc(rows);
             k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, d_leaf_vw.p + 2 * L);
@@ -1654,8 +1673,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             a.leaf_of = leaf_of.p;
             a.grad = grad.p;
             a.hess = hess.p;
-            a.gs = gsc;
-            a.hs = hsc;
+            a.dsc = d_scales.p;
             a.sums = d_leaf_out.p;
             a.bag = bag.kind == SROCM_BAG_BERNOULLI ? 1u : 0u;
             a.bag_seed = bag.seed;
@@ -1665,7 +1683,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             a.gate = d_gate.p;
             k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS)), TL_THREADS, 0, stream>>>(a);
             launch_check("k_tree_leaves");
-            LeafValueArgs la{d_leaf_out.p, d_gate.p, 0u, bias ? 1u : 0u, gsc, hsc, p.cfg.lambda_l1, p.cfg.lambda_l2,
+            LeafValueArgs la{d_leaf_out.p, d_gate.p, d_scales.p, 0u, bias ? 1u : 0u, 1.0f, 1.0f, p.cfg.lambda_l1, p.cfg.lambda_l2,
                              p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + L, d_leaf_values.p};
             k_leaf_values<<<1, 512, 0, stream>>>(la);
             launch_check("k_leaf_values");
@@ -1674,10 +1692,16 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             for (auto &v : valid)
                 if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
             launch_check("k_add_tree");
-            hip_check(hipMemcpyAsync(h_leaf_vw.p, d_leaf_vw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost, stream),
-                      "read leaf values");
+            hip_check(hipMemcpyAsync(h_leaf_vw[vw_buf].p, d_leaf_vw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost,
+                                     stream), "read leaf values");
         };
+        struct ScalesFromDevice {  // GrowState takes the device's scales while this tree grows
+            const DevScales *&slot;
+            ScalesFromDevice(const DevScales *&s, const DevScales *v) : slot(s) { slot = v; }
+            ~ScalesFromDevice() { slot = nullptr; }
+        } from_device(grow_dsc, d_scales.p);
         grow(gs, tree, splits, leaves, last, renew ? &renew_on_device : nullptr);
+        finalize();  // the grown tree's readback came after the last tree's leaf values
         if (tree.num_leaves == 1) {  // boosting.rs:301-310
             if (trees_added == 0) {
                 HostTree c;
@@ -1698,6 +1722,8 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             pend.tree = tree;
             pend.leaves = leaves;
             pend.index = done;
+            pend.buf = vw_buf;
+            vw_buf ^= 1u;
             ++done;
             ++trees_added;
             continue;

@@ -101,6 +101,53 @@ __global__ void k_quantize(const float *__restrict__ grad, const float *__restri
         packed[r] = quantize_row(spec, grad[r], hess[r], row_offset + r);
 }
 
+// An iteration's quantization made on the device from the gradient maxima, so the boosting loop never waits for
+// them: the scales of quantize.rs:56-84 and the fixed-point scales of quantize.rs:153-159, in the host's double
+// operations (ceil(log2 x) from the exponent: exact for the float maxima these are).
+struct DevScales {
+    double sg, sh;    // grad_scale, hess_scale
+    float gsc, hsc;   // the leaf sums' fixed-point scales
+    QuantDev q;
+};
+
+__device__ __forceinline__ double positive_or_one_d(double v) { return v > 0.0 && __builtin_isfinite(v) ? v : 1.0; }
+
+__device__ __forceinline__ float fixed_point_scale_d(double max_abs) {
+    if (!__builtin_isfinite(max_abs) || max_abs <= 0.0) return 1.0f;
+    int ex = 0;
+    const double m = __builtin_frexp(max_abs, &ex);  // max_abs = m * 2^ex, m in [0.5, 1)
+    int e = 30 - (m == 0.5 ? ex - 1 : ex);
+    e = e < -126 ? -126 : (e > 127 ? 127 : e);
+    return __builtin_ldexpf(1.0f, e);
+}
+
+__global__ void k_quant_spec(const uint32_t *maxima, DevScales *out, uint32_t num_bins, uint32_t constant_hessian,
+                             double constant, uint32_t stochastic, uint32_t seed, uint32_t iteration) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const double mg = static_cast<double>(__uint_as_float(maxima[0])), mh = static_cast<double>(__uint_as_float(maxima[1]));
+    DevScales d;
+    d.q.grad_max_q = static_cast<int32_t>(num_bins / 2);
+    d.q.hess_max_q = static_cast<int32_t>(num_bins);
+    d.sg = positive_or_one_d(mg / static_cast<double>(d.q.grad_max_q));
+    d.sh = constant_hessian ? positive_or_one_d(constant) : positive_or_one_d(mh / static_cast<double>(d.q.hess_max_q));
+    d.q.inv_grad_scale = static_cast<float>(1.0 / d.sg);
+    d.q.inv_hess_scale = static_cast<float>(1.0 / d.sh);
+    d.q.constant_hessian = constant_hessian;
+    d.q.stochastic = stochastic;
+    d.q.seed = seed;
+    d.q.iteration = iteration;
+    d.gsc = fixed_point_scale_d(mg);
+    d.hsc = fixed_point_scale_d(mh);
+    *out = d;
+}
+
+__global__ void k_quantize_dev(const float *__restrict__ grad, const float *__restrict__ hess, int32_t *__restrict__ packed,
+                               uint64_t n, uint64_t row_offset, const DevScales *sc) {
+    const QuantDev spec = sc->q;
+    for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x)
+        packed[r] = quantize_row(spec, grad[r], hess[r], row_offset + r);
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // gradients (objective/regression.rs:70-93: f32 arithmetic) and their maxima (cpu.rs:774)
 // ---------------------------------------------------------------------------------------------------------
@@ -629,6 +676,7 @@ struct TreeLeavesArgs {
     uint64_t row_offset;
     double fraction;
     const uint32_t *gate;              // when set: the leaves (nn, nl from it), 0 for no tree (k_tree_nodes)
+    const DevScales *dsc;              // when set: gs and hs are its fixed-point scales
 };
 constexpr uint32_t LEAVES_MAX_LDS = 512;  // the trees k_tree_leaves takes (device growth grows up to this)
 constexpr int TL_RPT = 8;
@@ -638,6 +686,7 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
     __shared__ DevNode sn[LEAVES_MAX_LDS - 1];
     __shared__ unsigned long long ls[LEAVES_MAX_LDS][2];
     uint32_t nn = a.nn, nl = a.nl;
+    const float gs = a.dsc ? a.dsc->gsc : a.gs, hs = a.dsc ? a.dsc->hsc : a.hs;
     if (a.gate) {
         nl = *a.gate;
         if (nl == 0u || nl > LEAVES_MAX_LDS) return;
@@ -677,8 +726,8 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
             a.leaf_of[r[k]] = static_cast<uint16_t>(leaf);
             if (!a.grad) continue;
             if (a.bag && !(static_cast<double>(uniform(a.bag_seed, 2u, a.bag_round, a.row_offset + r[k])) < a.fraction)) continue;
-            atomicAdd(&ls[leaf][0], static_cast<unsigned long long>(to_fixed(a.grad[r[k]], a.gs)));
-            atomicAdd(&ls[leaf][1], static_cast<unsigned long long>(to_fixed(a.hess[r[k]], a.hs)));
+            atomicAdd(&ls[leaf][0], static_cast<unsigned long long>(to_fixed(a.grad[r[k]], gs)));
+            atomicAdd(&ls[leaf][1], static_cast<unsigned long long>(to_fixed(a.hess[r[k]], hs)));
         }
     }
     if (!a.grad) return;
@@ -747,6 +796,7 @@ __device__ __forceinline__ double leaf_output(double g, double h, double l1, dou
 struct LeafValueArgs {
     const unsigned long long *sums;  // [nl][2] i64 fixed-point {g, h}
     const uint32_t *gate;            // when set: nl from it, 0 for no tree (k_tree_nodes)
+    const DevScales *dsc;            // when set: gs and hs are its fixed-point scales
     uint32_t nl, add_bias;
     float gs, hs;                    // the fixed-point scales
     double l1, l2, rate, bias;
@@ -758,9 +808,10 @@ __device__ __forceinline__ double round_to_zero_d(double v) { return fabs(v) > s
 
 __global__ void k_leaf_values(LeafValueArgs a) {
     const uint32_t nl = a.gate ? *a.gate : a.nl;
+    const float gs = a.dsc ? a.dsc->gsc : a.gs, hs = a.dsc ? a.dsc->hsc : a.hs;
     for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) {
-        const double sg = static_cast<double>(static_cast<int64_t>(a.sums[2 * l])) / static_cast<double>(a.gs);
-        const double sh = static_cast<double>(static_cast<int64_t>(a.sums[2 * l + 1])) / static_cast<double>(a.hs);
+        const double sg = static_cast<double>(static_cast<int64_t>(a.sums[2 * l])) / static_cast<double>(gs);
+        const double sh = static_cast<double>(static_cast<int64_t>(a.sums[2 * l + 1])) / static_cast<double>(hs);
         double v = round_to_zero_d(leaf_output(sg, sh, a.l1, a.l2));
         v = round_to_zero_d(v * a.rate);
         float f = static_cast<float>(v);
@@ -1513,7 +1564,12 @@ __device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const Fea
 __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
                                                     SplitCfgDev cfg, double sg, double sh,
-                                                    uint8_t *cat_order /* [feature][256] or null */) {
+                                                    uint8_t *cat_order /* [feature][256] or null */,
+                                                    const DevScales *dsc /* when set: the scales */) {
+    if (dsc) {
+        sg = dsc->sg;
+        sh = dsc->sh;
+    }
     __shared__ CatScratch cats[4];
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1816,11 +1872,15 @@ struct GrowState {
     int32_t max_depth;
     SplitCfgDev cfg;
     double sg, sh;
+    const struct DevScales *dsc;  // when set, the scales are these (made on the device), not sg and sh
     uint32_t target_groups;   // k_step_rows workgroups a step is spread over
     uint32_t ncg;             // column groups of k_step_reduce and k_step_scan
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
     uint32_t pad_;
 };
+
+__device__ __forceinline__ double grow_sg(const GrowState &g) { return g.dsc ? g.dsc->sg : g.sg; }
+__device__ __forceinline__ double grow_sh(const GrowState &g) { return g.dsc ? g.dsc->sh : g.sh; }
 
 __device__ __forceinline__ bool depth_allows(const GrowState &g, int32_t d) { return g.max_depth <= 0 || d < g.max_depth; }
 
@@ -2414,7 +2474,7 @@ __global__ __launch_bounds__(512) void k_root_select(GrowState g) {
     __shared__ SplitOut o;
     __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
     ScanJob job = g.jobs[0];
-    select_split(job, job.count, g.nf, g.cfg, g.sg, g.sh, &o, g.splittable);
+    select_split(job, job.count, g.nf, g.cfg, grow_sg(g), grow_sh(g), &o, g.splittable);
     if (threadIdx.x == 0) {
         g.tl[0].best = o;
         g.tl[0].has_best = o.found ? 1u : 0u;
@@ -2983,7 +3043,7 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
             wave_best(wb, wf);
             if (wf >= 0) {  // the winner, read once more where the scans left it
                 const int64_t cnt = ch == 0 ? left : right;
-                out = split_out(cands[wf], wf, make_ctx(g.cfg, g.sg, g.sh, J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                out = split_out(cands[wf], wf, make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
             }
         }
         if (lane == 0) s_out[ch] = out;
@@ -3012,8 +3072,8 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
         const double lv = info.left_output, rv = info.right_output;
         l.value = lv != lv ? 0.0 : lv;
         r.value = rv != rv ? 0.0 : rv;
-        l.weight = info.left_hess * g.sh;
-        r.weight = info.right_hess * g.sh;
+        l.weight = info.left_hess * grow_sh(g);
+        r.weight = info.right_hess * grow_sh(g);
         l.slot = r.slot = -1;
         if (searched) {
             l.slot = J.built_side == 0 ? J.built_slot : J.parent_slot;
@@ -3167,7 +3227,7 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
         const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
         const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
         const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
-        const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
+        const Ctx c = make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[child], J.child_uh[child], cnt);
         FeatCand r = {};
         if (scan_searched(c, sm, sev)) {
             Grown rg = {}, fg = {};
@@ -3195,7 +3255,7 @@ __global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
         const bool sev = g.mask[f] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + f] != 0;
         const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
         const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
-        const Ctx c = make_ctx(g.cfg, g.sg, g.sh, J.child_ug[child], J.child_uh[child], cnt);
+        const Ctx c = make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[child], J.child_uh[child], cnt);
         FeatCand out = {};
         if (scan_searched(c, sm, sev)) out = categorical_candidate(c, g.cfg, sm, hist, cats[wave], nullptr);
         if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + f] = out;
