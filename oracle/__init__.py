@@ -50,6 +50,7 @@ def lib():
         P = C.POINTER
         sig = {
             "oracle_mix32": (C.c_uint32, [C.c_uint32]),
+            "oracle_mix32_n": (None, [P(C.c_uint32), C.c_uint64, P(C.c_uint32)]),
             "oracle_uniform": (C.c_float, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64]),
             "oracle_quant_spec": (None, [C.c_double, C.c_double, C.c_int, C.c_double, C.c_uint32, C.c_int,
                                          C.c_uint32, C.c_uint32, P(_abi.QuantSpec)]),
@@ -92,6 +93,7 @@ def lib():
             "oracle_model_times": (None, [C.c_void_p, P(C.c_double)]),
             "oracle_model_hist_bins": (C.c_double, [C.c_void_p]),
             "oracle_model_tree_left_bins": (None, [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32)]),
+            "oracle_model_tree_gains": (None, [C.c_void_p, C.c_uint32, P(C.c_double), P(C.c_double)]),
             "oracle_grow_tree": (C.c_void_p, [P(_abi.Dataset), P(C.c_float), P(C.c_float), P(Params), C.c_int]),
             "oracle_model_leaf_ranges": (None, [C.c_void_p, P(_abi.LeafRange)]),
             "oracle_model_partition": (None, [C.c_void_p, P(C.c_uint32)]),
@@ -118,6 +120,14 @@ def threads():
 
 def uniform(seed, stream, iteration, row):
     return lib().oracle_uniform(seed, stream, iteration, row)
+
+
+def mix32(x):
+    """mix32 of every element of a uint32 array."""
+    x = np.ascontiguousarray(x, dtype=np.uint32)
+    out = np.empty_like(x)
+    lib().oracle_mix32_n(ptr(x, C.c_uint32), x.size, ptr(out, C.c_uint32))
+    return out
 
 
 def quant_spec(max_abs_grad, max_hess, constant_hessian=None, num_bins=4, stochastic=True, seed=1, iteration=0):
@@ -271,6 +281,8 @@ class Model:
             lb = np.zeros(8 * max(ni, 1), np.uint32)
             L.oracle_model_tree_left_bins(handle, t, ptr(lb, C.c_uint32))
             a["left_bins"] = lb[: 8 * ni].reshape(-1, 8)
+            a["commit_gain"], a["open_gain"] = np.zeros(ni, np.float64), np.zeros(nl, np.float64)
+            L.oracle_model_tree_gains(handle, t, ptr(a["commit_gain"], C.c_double), ptr(a["open_gain"], C.c_double))
             self.trees.append(a)
         self.scores = np.zeros(num_rows, np.float32)
         L.oracle_model_scores(handle, ptr(self.scores, C.c_float), num_rows)

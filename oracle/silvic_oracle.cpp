@@ -1109,6 +1109,9 @@ struct Tree {
     std::vector<int64_t> internal_count;
     double shrinkage = 1.0;
     std::vector<int32_t> leaf_parent{-1}, leaf_depth{0};
+    // Test diagnostics, not part of silvic's tree: the f64 gain best_leaf compared when each node was committed,
+    // and each leaf's pending best gain when growth stopped (-inf without a candidate split).
+    std::vector<double> commit_gain, open_gain;
 
     struct Children {
         double left_value, right_value;
@@ -1379,7 +1382,10 @@ struct Learner {
             if (!best) break;
             split_leaf(backend, g, leaves, *best, mask, gs, hs);
         }
-        for (auto &l : leaves) g.leaves.push_back(l.range);
+        for (auto &l : leaves) {
+            g.leaves.push_back(l.range);
+            g.tree.open_gain.push_back(l.best ? l.best->gain : -std::numeric_limits<double>::infinity());
+        }
         return g;
     }
 
@@ -1422,6 +1428,7 @@ struct Learner {
         c.left_weight = info.left.hess * hs;
         c.right_weight = info.right.hess * hs;
         c.gain = static_cast<float>(info.gain + p->cfg.min_gain_to_split);
+        g.tree.commit_gain.push_back(info.gain);
         // learner.rs:459-485 apply_split: decision_type from MissingType and default_left (tree.rs:108-122)
         int8_t decision_type;
         if (info.categorical) decision_type = static_cast<int8_t>(1 | (2 << 2));
@@ -1597,6 +1604,9 @@ void copy_out(const std::vector<T> &v, T *out) {
 extern "C" {
 
 uint32_t oracle_mix32(uint32_t x) { return mix32(x); }
+void oracle_mix32_n(const uint32_t *x, uint64_t n, uint32_t *out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = mix32(x[i]);
+}
 float oracle_uniform(uint32_t seed, uint32_t stream, uint32_t iteration, uint64_t row) {
     return uniform(seed, stream, iteration, row);
 }
@@ -1785,6 +1795,12 @@ void oracle_model_partition(const void *model, uint32_t *out) {
 }
 
 double oracle_model_hist_bins(const void *model) { return static_cast<const Model *>(model)->hist_bins; }
+
+void oracle_model_tree_gains(const void *model, uint32_t tree, double *commit_gain, double *open_gain) {
+    const Tree &t = static_cast<const Model *>(model)->trees[tree];
+    copy_out(t.commit_gain, commit_gain);
+    copy_out(t.open_gain, open_gain);
+}
 
 void oracle_model_tree_left_bins(const void *model, uint32_t tree, uint32_t *out) {
     const Model *m = static_cast<const Model *>(model);

@@ -33,6 +33,8 @@ extern "C" {
 
 /* quantize.rs:14-31 */
 uint32_t oracle_mix32(uint32_t x);
+/* mix32 over an array (test helper). */
+void oracle_mix32_n(const uint32_t *x, uint64_t n, uint32_t *out);
 float oracle_uniform(uint32_t seed, uint32_t stream, uint32_t iteration, uint64_t row);
 /* quantize.rs:56-84; has_constant selects Some(constant_hessian) */
 void oracle_quant_spec(double max_abs_grad, double max_hess, int has_constant, double constant_hessian,
@@ -151,6 +153,10 @@ void oracle_model_leaf_ranges(const void *model, srocm_leaf_range *out);
 void oracle_model_partition(const void *model, uint32_t *out);
 /* Sum over histogram builds of rows x used feature columns (the "bins" work unit). */
 double oracle_model_hist_bins(const void *model);
+/* Test diagnostics of tree `tree`: per internal node the f64 gain best_leaf compared when it was committed
+ * (num_leaves-1 entries), per leaf its pending best gain when growth stopped (num_leaves entries; -inf without a
+ * candidate). Either pointer may be NULL. */
+void oracle_model_tree_gains(const void *model, uint32_t tree, double *commit_gain, double *open_gain);
 /* per internal node of tree `tree`, 8 words: the bins that go left (the BinSplit the learner handed the backend) */
 void oracle_model_tree_left_bins(const void *model, uint32_t tree, uint32_t *out);
 

@@ -99,3 +99,26 @@ def learner_gradients(first, last, bins, zeros=False):
         g = np.where(z, 0, g).astype(np.float32)
         hh = np.where(z, 0, hh).astype(np.float32)
     return g, hh
+
+
+def mirrored(half, feature):
+    """`half`, then `half` again with every other numerical feature's bin order reversed (missing values stay in the
+    NaN bin); `feature` is bin 0 in the first copy and bin 1 in the second."""
+    n = half.num_rows
+    groups = []
+    for gi, g in enumerate(half.groups):
+        d = np.concatenate([g.data, g.data]).reshape(2 * n, g.row_stride)
+        for j in g.features:
+            f = half.features[j]
+            if j == feature or f.num_bins == 0:
+                continue
+            assert f.kind == _abi.BINS_NUMERICAL
+            top = f.num_bins - 1 - int(bool(f.nan_bin))  # the last numerical bin
+            col = d[n:, f.column].astype(np.int64)
+            d[n:, f.column] = np.where(col <= top, top - col, col).astype(np.uint8)
+        if gi == half.features[feature].group:
+            c = half.features[feature].column
+            d[:n, c] = 0
+            d[n:, c] = 1
+        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
+    return BinnedDataset(2 * n, half.features, groups, half.total_bins, np.concatenate([half.label, half.label]))

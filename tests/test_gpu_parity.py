@@ -11,7 +11,7 @@ import pytest
 import oracle
 import silvic_amd
 from silvic_amd import _abi, bin_split, device_node
-from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients
+from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients, mirrored
 from tests.split_cases import categorical_cases, config, numerical_cases, quantized_cases, sums
 
 pytestmark = pytest.mark.gpu
@@ -324,30 +324,6 @@ def test_grown_tree_edge_cases(rocm, rows, cols, kw):
     compare_trees(d, dict(o_tree), f"edge {kw}")
     assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
     assert np.array_equal(rocm.partition_rows(n), o_part[:n])
-
-
-def mirrored(half, feature):
-    """`half`, then `half` again with every other numerical feature's bin order reversed (missing values stay in the
-    NaN bin); `feature` is bin 0 in the first copy and bin 1 in the second."""
-    from silvic_amd.dataset import BinnedDataset, FeatureGroup
-    n = half.num_rows
-    groups = []
-    for gi, g in enumerate(half.groups):
-        d = np.concatenate([g.data, g.data]).reshape(2 * n, g.row_stride)
-        for j in g.features:
-            f = half.features[j]
-            if j == feature or f.num_bins == 0:
-                continue
-            assert f.kind == _abi.BINS_NUMERICAL
-            top = f.num_bins - 1 - int(bool(f.nan_bin))  # the last numerical bin
-            col = d[n:, f.column].astype(np.int64)
-            d[n:, f.column] = np.where(col <= top, top - col, col).astype(np.uint8)
-        if gi == half.features[feature].group:
-            c = half.features[feature].column
-            d[:n, c] = 0
-            d[n:, c] = 1
-        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
-    return BinnedDataset(2 * n, half.features, groups, half.total_bins, np.concatenate([half.label, half.label]))
 
 
 # Exact ties between leaves: two mirrored halves (negated gradients in exact quantized units, each numerical bin

@@ -142,3 +142,74 @@ def test_every_objective_learns():
     p0 = y.mean()
     loss0 = -(p0 * np.log(p0) + (1 - p0) * np.log(1 - p0))
     assert loss < loss0
+
+
+def _commit_order_violations(tree, num_leaves_cap):
+    """best_leaf (learner.rs:418-429) commits the open leaf with the largest gain, the lowest leaf id among equal
+    gains, while that gain is positive. Checked from the finished tree alone: node t split leaf `leaf[t]` (the
+    leftmost leaf under t, since a split leaf keeps its id on the left); the leaf split at node j > t was open at t
+    when j's parent node came before t; a leaf never split was open after its parent node."""
+    n = tree["num_leaves"]
+    left, right = tree["left_child"], tree["right_child"]
+    gain, open_gain = tree["commit_gain"], tree["open_gain"]
+    parent = np.full(n - 1, -1)
+    leaf_parent = np.full(n, -1)
+    for p in range(n - 1):
+        for c in (left[p], right[p]):
+            if c >= 0:
+                parent[c] = p
+            else:
+                leaf_parent[~c] = p
+    leaf = np.empty(n - 1, np.int64)
+    for t in range(n - 1):
+        c = t
+        while c >= 0:
+            c = left[c]
+        leaf[t] = ~c
+    bad = []
+    for t in range(n - 1):
+        if not gain[t] > 0:
+            bad.append(("non-positive commit", t))
+        for j in range(t + 1, n - 1):
+            if parent[j] < t and not (gain[j] < gain[t] or (gain[j] == gain[t] and leaf[j] > leaf[t])):
+                bad.append(("later commit beats", t, j))
+        for l in range(n):
+            if leaf_parent[l] < t and not (open_gain[l] < gain[t] or (open_gain[l] == gain[t] and l > leaf[t])):
+                bad.append(("open leaf beats", t, l))
+    if n < num_leaves_cap and (open_gain > 0).any():
+        bad.append(("stopped with a positive gain",))
+    return bad
+
+
+def test_grown_trees_commit_leaves_in_best_first_order():
+    # learner.rs:167-169, 418-429: every tree of a boosted model and a single large tree
+    data = silvic_amd.synthetic(2, rows=40_000, cols=24, seed=9)
+    m = oracle.train(data, oracle.default_params(objective=_abi.OBJ_BINARY, num_iterations=4, num_leaves=63))
+    for tree in m.trees:
+        assert tree["num_leaves"] > 8
+        assert _commit_order_violations(tree, 63) == []
+    data1 = small_config1(30_000)
+    rng = np.random.default_rng(2)
+    g = (data1.label - rng.standard_normal(data1.num_rows)).astype(np.float32)
+    tree, _, _ = oracle.grow_tree(data1, g, np.ones_like(g), oracle.default_params(num_leaves=255,
+                                                                                   min_data_in_leaf=40))
+    assert tree["num_leaves"] > 100
+    assert _commit_order_violations(tree, 255) == []
+
+
+def test_exact_gain_ties_commit_the_lower_leaf_first():
+    # two mirrored halves: every split of one half has a twin of exactly equal f64 gain in the other
+    from tests.helpers import mirrored
+
+    half = silvic_amd.synthetic(2, rows=30_000, cols=16, seed=11)
+    f0 = next(j for j, f in enumerate(half.features) if f.num_bins >= 3)
+    data = mirrored(half, f0)
+    rng = np.random.default_rng(4)
+    ga = rng.choice(np.array([-1.0, -0.5, 0.5, 1.0], np.float32), size=half.num_rows, p=[0.2, 0.2, 0.3, 0.3])
+    g = np.concatenate([ga, -ga]).astype(np.float32)
+    tree, _, _ = oracle.grow_tree(data, g, np.ones_like(g), oracle.default_params(num_leaves=63,
+                                                                                   stochastic_rounding=0),
+                                  renew=False)
+    gains = tree["commit_gain"][1:]
+    assert len(np.unique(gains)) < len(gains), "the halves produce exactly tied gains"
+    assert _commit_order_violations(tree, 63) == []

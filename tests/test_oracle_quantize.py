@@ -107,3 +107,74 @@ def test_scales_follow_the_maxima():
 def test_in_bag_fraction():
     got = np.mean([oracle.lib().oracle_in_bag(4, 1, r, 0.7) for r in range(20_000)])
     assert abs(got - 0.7) < 0.02
+
+
+def _lightgbm_fixture():
+    import json
+    import pathlib
+
+    return json.loads((pathlib.Path(__file__).parent / "golden" / "lightgbm_bins_all_rows.json").read_text())
+
+
+def _fixture_columns(mix, rows):
+    """The numerical columns of gen_lightgbm_bins.py:64-86 built with the mixer `mix`."""
+    r = np.arange(rows, dtype=np.uint32)
+    mr = mix(r)
+
+    def unit(stream):
+        h = mix(mr ^ mix(np.array([stream], np.uint32))[0])
+        return (h >> np.uint32(8)).astype(np.float64) / 16777216.0
+
+    a20, a40, a60 = unit(20), unit(40), unit(60)
+    u50 = unit(50)
+    return {
+        "normal": (((unit(10) + unit(11)) + unit(12)) + unit(13) - 2.0) * 1.5,
+        "zeros_nan": np.where(a20 < 0.3, 0.0, np.where(a20 < 0.4, np.nan, ((unit(21) + unit(22)) - 1.0) * 3.0)),
+        "integers": np.floor(unit(30) * 20.0) - 5.0,
+        "mass_points": np.where(a40 < 0.5, 1.0, ((unit(41) * unit(42)) * unit(43)) * 1000.0),
+        "negative": -(u50 * u50 * 10.0) - 0.5,
+        "tiny": np.where(a60 < 0.2, 1e-36, np.where(a60 < 0.3, -1e-36, unit(61) - 0.5)),
+    }
+
+
+def _lightgbm_range(col):
+    """LightGBM 3.3.5 BinMapper's [min:max]: NaN dropped, |v| <= 1e-35 counted as zero, zero inside the range when
+    any row is zero."""
+    v = col[~np.isnan(col)]
+    zero = np.abs(v) <= 1e-35
+    nz = v[~zero]
+    lo, hi = nz.min(), nz.max()
+    if zero.any():
+        lo, hi = min(lo, 0.0), max(hi, 0.0)
+    return lo, hi
+
+
+def test_mix32_rebuilds_the_lightgbm_fixture_ranges():
+    # gen_lightgbm_bins.py:54-89 builds every feature from mix32; with 150,000 rows LightGBM's bin sample is all of
+    # them, so the recorded feature_infos are the exact extremes of the mix32-built columns, to the last bit
+    fx = _lightgbm_fixture()
+    cols = _fixture_columns(oracle.mix32, fx["rows"])
+    for name, col in cols.items():
+        lo, hi = fx["feature_infos"][name].strip("[]").split(":")
+        assert _lightgbm_range(col) == (float(lo), float(hi)), name
+
+
+def test_the_lightgbm_ranges_reject_a_wrong_mixer():
+    # the same check fails for a mixer one constant or one shift away from lowbias32
+    fx = _lightgbm_fixture()
+
+    def near_miss(mul2, shift2):
+        def mix(x):
+            x = x.astype(np.uint32)
+            x ^= x >> np.uint32(16)
+            x *= np.uint32(0x7FEB352D)
+            x ^= x >> np.uint32(shift2)
+            x *= np.uint32(mul2)
+            x ^= x >> np.uint32(16)
+            return x
+        return mix
+
+    for mix in (near_miss(0x846CA68D, 15), near_miss(0x846CA68B, 16)):
+        cols = _fixture_columns(mix, fx["rows"])
+        lo, hi = fx["feature_infos"]["normal"].strip("[]").split(":")
+        assert _lightgbm_range(cols["normal"]) != (float(lo), float(hi))
