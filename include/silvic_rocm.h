@@ -298,8 +298,9 @@ int srocm_scores(void *ctx, uint32_t dataset, float *out, size_t len);
 
 /* split::find_best_split (crates/silvic-core/src/split.rs:919-961) on a host histogram of `len` doubles
  * holding integer units, over `features` (their hist_offset/num_bins index `hist`), run on the device.
- * `evaluate` and `splittable` have one byte per feature. Needs no loaded dataset. Numerical features only; a
- * categorical feature among the evaluated ones returns SROCM_ERR_UNSUPPORTED. */
+ * `evaluate` and `splittable` have one byte per feature. Needs no loaded dataset. Numerical, one-hot and sorted
+ * categorical features (split.rs:582-844); a categorical rule's bins come back in `out->cat_bins` in the rule's
+ * order. */
 int srocm_find_best_split(void *ctx, const double *hist, size_t len, const srocm_feature *features,
                           uint32_t num_features, const uint8_t *evaluate, const srocm_sums *sums, double grad_scale,
                           double hess_scale, const srocm_split_config *cfg, srocm_split_info *out,

@@ -603,11 +603,32 @@ struct Context {
         return read_maxima();
     }
 
+    // The most rows one histogram workgroup adds up: k_hist spreads a leaf over at most one workgroup per compute
+    // unit in multiples of 64 rows (at least HIST_MIN_ROWS each); a split step gives a workgroup at most
+    // ceil(tiles / (cus - JMAX)) tiles of a job, the step's tiles being at most rows / STEP_TILE + JMAX.
+    uint64_t max_workgroup_rows() const {
+        const uint64_t n = std::max<uint64_t>(rows, 1);
+        const uint64_t hist = div_up(std::max<uint64_t>(div_up(n, cus), HIST_MIN_ROWS), 64) * 64 + 64;
+        const uint64_t share = cus > JMAX ? cus - JMAX : 1;
+        const uint64_t step = div_up(div_up(n, STEP_TILE) + JMAX, share) * STEP_TILE;
+        return std::max(hist, step);
+    }
+
+    // Quantized units a histogram can take: a packed word holds g as a signed 16-bit half and h as an unsigned one,
+    // and a workgroup's sums of either are i32 (the reference's CPU sums are i64, cpu.rs:517-525), so
+    // max_q * max_workgroup_rows() must stay below 2^31.
+    void check_quant_units(int64_t grad_max_q, int64_t hess_max_q) const {
+        if (grad_max_q < 1 || grad_max_q > 32767 || hess_max_q < 1 || hess_max_q > 65535)
+            fail(SROCM_ERR_UNSUPPORTED, "quantized units must lie in 1..=32767 for gradients and 1..=65535 for hessians");
+        const uint64_t wg = max_workgroup_rows();
+        if (static_cast<uint64_t>(std::max(grad_max_q, hess_max_q)) * wg > 2147483647ull)
+            fail(SROCM_ERR_UNSUPPORTED, "quantized units up to " + std::to_string(std::max(grad_max_q, hess_max_q)) + " over " +
+                                            std::to_string(wg) + " rows per histogram workgroup could overflow its 32-bit sums");
+    }
+
     void quantize(const srocm_quant_spec &s) {
         require_loaded();
-        // a histogram word packs g as a signed 16-bit half and h as an unsigned one
-        if (s.grad_max_q < 1 || s.grad_max_q > 32767 || s.hess_max_q < 1 || s.hess_max_q > 65535)
-            fail(SROCM_ERR_UNSUPPORTED, "quantized units must lie in 1..=32767 for gradients and 1..=65535 for hessians");
+        check_quant_units(s.grad_max_q, s.hess_max_q);
         QuantDev q{s.inv_grad_scale, s.inv_hess_scale, s.grad_max_q, s.hess_max_q, s.constant_hessian, s.stochastic, s.seed, s.iteration};
         if (rows) {
             k_quantize<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, q);
@@ -664,11 +685,13 @@ struct Context {
     // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
     void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
                      int64_t *parent, uint64_t bins_used) {
-        uint32_t grid = hist_groups(count);
+        int32_t *partials = partial.p;
+        const uint32_t grid = hist_groups(count);
+        const bool profiled = prof.on;
         for (auto &s : slabs) {
-            HistArgs a{s.bins.p, part.p, packed.p, partial.p, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
+            HistArgs a{s.bins.p, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
             hipEvent_t e0 = nullptr, e1 = nullptr;
-            if (prof.on) {
+            if (profiled) {
                 e0 = event();
                 e1 = event();
                 hip_check(hipEventRecord(e0, stream), "event");
@@ -679,16 +702,16 @@ struct Context {
             default: k_hist<128><<<grid, 1024, 0, stream>>>(a); break;
             }
             launch_check("k_hist");
-            if (prof.on) {
+            if (profiled) {
                 hip_check(hipEventRecord(e1, stream), "event");
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partial.p, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
+            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
             k_hist_reduce<<<div_up(256ull * s.width, 32), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
-        if (prof.on) {
+        if (profiled) {
             prof.builds += 1;
             if (!dev_left) {  // rows known on the host: rows x (used columns + 4 B gradients + 4 B row id) + the output
                 prof.rows += count;
@@ -1589,6 +1612,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     require_loaded();
     if (objective == SROCM_OBJ_LAMBDARANK) fail(SROCM_ERR_UNSUPPORTED, "lambdarank gradients stay on the host; drive the backend ops");
     bool constant_hessian = objective == SROCM_OBJ_REGRESSION && !has_weight;  // objective/mod.rs:84-89
+    check_quant_units(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
     uint32_t done = 0;
     HostTree tree;
     std::vector<srocm_bin_split> splits;
@@ -1706,7 +1730,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             if (trees_added == 0) {
                 HostTree c;
                 c.leaf_value[0] = init_score_value;
-                copy_tree(c, {}, &trees[done]);
+                if (trees) copy_tree(c, {}, &trees[done]);
                 ++done;
                 ++trees_added;
             }
@@ -1815,7 +1839,7 @@ int srocm_create(int ordinal, void **out) {
         auto c = std::make_unique<Context>();
         c->device = dev;
         c->cus = static_cast<uint32_t>(prop.multiProcessorCount);
-        c->device_name = prop.name;
+        c->device_name = prop.name[0] ? prop.name : prop.gcnArchName;  // the name can be empty; the architecture is not
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "create stream");
         c->h_u32.alloc(64);
         *out = c.release();

@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "exp_f64.hpp"
+#include "packed_word.hpp"
 
 namespace srocm {
 
@@ -385,9 +386,9 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
         for (int j = 0; j < SLOTS; ++j) {
             int32_t v = lds[tid + j * 1024];
             lds[tid + j * 1024] = 0;
-            int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
+            const int32_t gq = packed_g(v);
             accg[j] += gq;
-            acch[j] += static_cast<int32_t>(static_cast<uint32_t>(v - gq) >> 16);
+            acch[j] += packed_h(v, gq);
         }
         __syncthreads();
     }
@@ -2576,10 +2577,10 @@ __device__ __forceinline__ void flush_pairs(int32_t *lds, int2 *pairs, uint32_t 
         const int32_t v = lds[slot];
         lds[slot] = 0;
         if (slot / W < col_bins) {
-            const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v)));
+            const int32_t gq = packed_g(v);
             int2 o = add ? pairs[slot] : make_int2(0, 0);
             o.x += gq;
-            o.y += static_cast<int32_t>(static_cast<uint32_t>(v - gq) >> 16);
+            o.y += packed_h(v, gq);
             pairs[slot] = o;
         }
     }
@@ -3157,9 +3158,9 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
                     const int32_t v4[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const int32_t gq = static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(v4[c])));
+                        const int32_t gq = packed_g(v4[c]);
                         sg[c] += gq;
-                        sh[c] += static_cast<int32_t>(static_cast<uint32_t>(v4[c] - gq) >> 16);
+                        sh[c] += packed_h(v4[c], gq);
                     }
                 } else {
                     const int4 *p = src + static_cast<size_t>(wk) * stride4;

@@ -430,11 +430,25 @@ def params_to_lightgbm(params):
     (2, 120_000, 28, dict(objective=_abi.OBJ_BINARY, num_leaves=63, categorical=True), 6),
     # the wide sparse shape: 2000 features of at most 63 bins (mostly a handful) in 16 slabs
     (4, 30_000, 2000, dict(objective=_abi.OBJ_BINARY, num_leaves=63), 4),
+    # leaves not renewed: the tree's own outputs from the device scales (GrowState's scales, no host copy)
+    (2, 150_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=127, quant_train_renew_leaf=0), 6),
+    # the smallest and the largest quantization the reference accepts (config.rs:416-421)
+    (2, 150_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, num_grad_quant_bins=2), 6),
+    (2, 150_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, num_grad_quant_bins=64), 6),
+    (2, 150_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, num_grad_quant_bins=64,
+                          quant_train_renew_leaf=0), 4),
+    # weighted regression: non-constant hessians (objective/mod.rs:84-89), weighted sums in the leaf renewal
+    (1, 100_000, 28, dict(num_leaves=31, weighted=True), 8),
+    (1, 100_000, 28, dict(num_leaves=31, weighted=True, num_grad_quant_bins=16, quant_train_renew_leaf=0), 5),
 ])
 def test_boosting_matches_the_oracle(config, rows, cols, params, rounds):
     say("boost", config, rows, cols, params, rounds)
+    params = dict(params)
     categorical = bool(params.pop("categorical", False))
+    weighted = bool(params.pop("weighted", False))
     data = silvic_amd.synthetic(config, rows=rows, cols=cols, seed=13, categorical=categorical)
+    if weighted:
+        data.weight = np.random.default_rng(5).uniform(0.2, 3.0, rows).astype(np.float32)
     o, t = boost_both(data, params, rounds)
     assert len(t.trees) == len(o.trees) == rounds
     assert t.init_score == o.init_score
@@ -444,3 +458,24 @@ def test_boosting_matches_the_oracle(config, rows, cols, params, rounds):
     np.testing.assert_allclose(s, o.scores, rtol=1e-6, atol=1e-6)
     assert np.array_equal(s, o.scores), "scores are the same f32 adds"
     t.backend.close()
+
+
+def test_quantized_units_beyond_the_workgroup_sums_are_rejected(rocm):
+    # a workgroup's histogram sums are i32: units whose largest value times the rows one workgroup adds could pass
+    # 2^31 are refused before any kernel runs (the reference's CPU sums are i64 and take them)
+    # at 400k rows a workgroup adds at most 4096 rows, so even the widest units fit; at 8M rows it adds over 32768
+    wide = oracle.quant_spec(1.0, 1.0, None, 4, True, 1, 0)
+    wide.grad_max_q, wide.hess_max_q = 32767, 65535
+    for rows, fits in ((400_000, True), (8_000_000, False)):
+        say("quantize bound", rows)
+        data = silvic_amd.synthetic(2, rows=rows, cols=4, seed=3)
+        g, h = binary_gradients(data)
+        rocm.load(data)
+        rocm.set_gradients(g, h)
+        if fits:
+            rocm.quantize(wide)
+            continue
+        with pytest.raises(_abi.SilvicError) as e:
+            rocm.quantize(wide)
+        assert e.value.kind == "unsupported" and "32-bit sums" in str(e.value)
+        rocm.quantize(oracle.quant_spec(1.0, 1.0, None, 64, True, 1, 0))  # the reference's largest setting passes
