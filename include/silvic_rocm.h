@@ -351,6 +351,16 @@ int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iter
  * the trait: for callers that check or reuse the row order on the host. `len` is at most the training rows. */
 int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
 
+/* Backend::histogram (mod.rs:146-149, quantized mode) into a caller-owned DEVICE buffer `out` of `len` = 2 *
+ * total_bins int64 values ({g, h} units per bin), allocating nothing: no hipMalloc, no hipFree, no allocating
+ * library call. It has no counterpart in the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). The per-workgroup partials go to a
+ * 16 MiB scratch array that each GPU holds until the process ends and that every call on that GPU shares, so
+ * calls that overlap on one GPU race. At most 16 MiB / (256 * slab width * 8 B) workgroups run (64 for 128-wide
+ * slabs); a leaf whose rows per workgroup times the largest quantized unit could pass 2^31 is refused with
+ * SROCM_ERR_UNSUPPORTED. Runs on the context's stream; waits for the result when `wait` is nonzero. */
+int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size_t len, int wait);
+
 /* Per-kernel timing with HIP events on the backend's stream, and algorithmic byte counts; no counterpart in the
  * reference (a measurement hook). srocm_profile: enable (1) or disable (0); either resets the counters.
  * srocm_profile_read writes min(len, SROCM_PROFILE_VALUES) values:

@@ -152,6 +152,7 @@ _SIGNATURES = {
     "srocm_reset_partition": (C.c_int, [_P, C.POINTER(Bag), C.POINTER(C.c_uint32)]),
     "srocm_set_histogram_features": (C.c_int, [_P, C.POINTER(C.c_uint8), C.c_uint32]),
     "srocm_histogram": (C.c_int, [_P, LeafRange, C.c_int, C.POINTER(C.c_double), C.c_size_t]),
+    "srocm_histogram_noalloc": (C.c_int, [_P, LeafRange, C.c_void_p, C.c_size_t, C.c_int]),
     "srocm_partition": (C.c_int, [_P, LeafRange, C.POINTER(BinSplit), C.POINTER(C.c_uint32)]),
     "srocm_partition_and_histogram": (C.c_int, [_P, LeafRange, C.POINTER(BinSplit), C.c_uint32, C.c_int,
                                                 C.POINTER(C.c_double), C.c_size_t, C.POINTER(C.c_uint32)]),

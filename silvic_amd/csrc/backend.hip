@@ -19,12 +19,20 @@
 #include <cstring>
 #include <limits>
 #include <memory>
+#include <mutex>
 #include <optional>
 #include <stdexcept>
 #include <string>
 #include <thread>
 #include <functional>
 #include <vector>
+
+// The scratch of srocm_histogram_noalloc, the entry point that allocates nothing: the per-workgroup partial
+// histograms its k_hist launches write in full and its k_hist_reduce reads. Every GPU the library runs on holds its
+// own copy until the process ends. Host code never passes this name to a kernel or a copy: it uses the address
+// hipGetSymbolAddress returned for the device (scratch_address), resolved once per device at srocm_create.
+constexpr size_t NOALLOC_SCRATCH_PAIRS = size_t(2) << 20;  // {g, h} i32 pairs: 16 MiB
+static __device__ __align__(256) int2 scratch[NOALLOC_SCRATCH_PAIRS];
 
 namespace {
 
@@ -42,6 +50,22 @@ void hip_check(hipError_t e, const char *what) {
 }
 
 void launch_check(const char *what) { hip_check(hipGetLastError(), what); }
+
+// scratch's address on each device, resolved with that device current (each GPU holds its own copy of the array)
+std::mutex g_scratch_mu;
+std::vector<int2 *> g_scratch_at;
+
+int2 *scratch_address(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_at.size() <= static_cast<size_t>(dev)) g_scratch_at.resize(static_cast<size_t>(dev) + 1, nullptr);
+    if (!g_scratch_at[dev]) {
+        void *p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch address");
+        if (!p) fail(SROCM_ERR_DEVICE, "hip scratch address: null");
+        g_scratch_at[dev] = static_cast<int2 *>(p);
+    }
+    return g_scratch_at[dev];
+}
 
 template <typename T>
 struct DevBuf {
@@ -343,6 +367,7 @@ struct Context {
     DevBuf<unsigned long long> d_leaf_out;
 
     Profile prof;
+    int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
 
     ~Context() {
         if (tree_event) (void)hipEventDestroy(tree_event);
@@ -685,9 +710,12 @@ struct Context {
     // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
     void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
                      int64_t *parent, uint64_t bins_used) {
-        int32_t *partials = partial.p;
-        const uint32_t grid = hist_groups(count);
-        const bool profiled = prof.on;
+        launch_hist_into(begin, count, dev_left, side, out, parent, bins_used, partial.p, hist_groups(count), prof.on);
+    }
+
+    // launch_hist with the partials in `partials` (grid * 256 * max_width {g, h} pairs) over `grid` workgroups
+    void launch_hist_into(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
+                          int64_t *parent, uint64_t bins_used, int32_t *partials, uint32_t grid, bool profiled) {
         for (auto &s : slabs) {
             HistArgs a{s.bins.p, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
             hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -758,6 +786,34 @@ struct Context {
         sync();
         for (size_t i = 0; i < len; ++i) out[i] = static_cast<double>(h_hist.p[i]);
     }
+
+    // histogram() into a caller-owned device buffer (i64 {g, h} per bin), with the partials in the scratch array:
+    // allocates nothing. The workgroups are capped so their partials fit the scratch, which leaves more rows per
+    // workgroup; their i32 sums must still hold max_q * rows (the sizes beyond that are refused).
+    void histogram_noalloc(srocm_leaf_range leaf, int64_t *d_out, size_t len, int wait) {
+        require_loaded();
+        check_range(leaf);
+        if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
+        if (!d_out) fail(SROCM_ERR_DEVICE, "null histogram buffer");
+        if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
+        if (!scratch_at) fail(SROCM_ERR_DEVICE, "no scratch address for this device");
+        const uint32_t cap = static_cast<uint32_t>(NOALLOC_SCRATCH_PAIRS / (256ull * max_width));
+        const uint32_t grid = std::max<uint32_t>(1, std::min(hist_groups(leaf.count), cap));
+        const uint64_t per = div_up(std::max<uint64_t>(div_up(std::max<uint64_t>(leaf.count, 1), grid), HIST_MIN_ROWS), 64) * 64;
+        if (static_cast<uint64_t>(std::max(max_gq, max_hq)) * per > 2147483647ull)
+            fail(SROCM_ERR_UNSUPPORTED, "a leaf of " + std::to_string(leaf.count) + " rows over at most " + std::to_string(cap) +
+                                            " workgroups (the scratch's limit) could overflow their 32-bit sums at " +
+                                            std::to_string(std::max(max_gq, max_hq)) + " quantized units");
+        if (leaf.count == 0) {
+            k_zero_i64<<<grid_rows(len), 256, 0, stream>>>(d_out, len);
+            launch_check("k_zero_i64");
+        } else {
+            launch_hist_into(leaf.begin, leaf.count, nullptr, 0, d_out, nullptr, used_columns(),
+                             reinterpret_cast<int32_t *>(scratch_at), grid, false);
+        }
+        if (wait) sync();
+    }
+
 
     // ------------------------------------------------------------------------------------------------
     // partition
@@ -1840,6 +1896,7 @@ int srocm_create(int ordinal, void **out) {
         c->device = dev;
         c->cus = static_cast<uint32_t>(prop.multiProcessorCount);
         c->device_name = prop.name[0] ? prop.name : prop.gcnArchName;  // the name can be empty; the architecture is not
+        c->scratch_at = scratch_address(dev);
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "create stream");
         c->h_u32.alloc(64);
         *out = c.release();
@@ -2030,6 +2087,13 @@ int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iter
             fail(SROCM_ERR_CONFIG, "num_grad_quant_bins must be even and in 2..=64");
         uint32_t n = c.boost(*params, first_iteration, count, trees);
         if (trained) *trained = n;
+    });
+}
+
+int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size_t len, int wait) {
+    return guard(ctx, [&](Context &c) {
+        hip_check(hipSetDevice(c.device), "set device");
+        c.histogram_noalloc(leaf, out, len, wait);
     });
 }
 

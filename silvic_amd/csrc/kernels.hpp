@@ -241,6 +241,11 @@ __global__ void k_fill_f32(float *__restrict__ out, uint64_t n, float v) {
         out[r] = v;
 }
 
+__global__ void k_zero_i64(int64_t *__restrict__ out, uint64_t n) {
+    for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x)
+        out[r] = 0;
+}
+
 __global__ void k_iota(uint32_t *__restrict__ out, uint64_t n) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x)
         out[r] = static_cast<uint32_t>(r);

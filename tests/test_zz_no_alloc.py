@@ -1,0 +1,60 @@
+"""srocm_histogram_noalloc (the entry point that allocates nothing) against srocm_histogram, through the C ABI: two
+calls in a row, the second on a smaller leaf, each bit for bit equal to the allocating entry point's histogram.
+The device output buffer comes from the HIP runtime the library itself links (ctypes), not from torch."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+import silvic_amd
+from silvic_amd import _abi, bin_split
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipFree.argtypes = [C.c_void_p]
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    return hip
+
+
+def _noalloc(rocm, hip, dbuf, leaf, n):
+    rc = rocm._lib.srocm_histogram_noalloc(rocm._h, _abi.LeafRange(*leaf), dbuf, n, 1)
+    rocm._check(rc)
+    out = np.empty(n, np.int64)
+    assert hip.hipMemcpy(out.ctypes.data, dbuf, n * 8, 2) == 0  # hipMemcpyDeviceToHost
+    return out
+
+
+def test_noalloc_histogram_matches_the_allocating_one():
+    print("[case] noalloc histogram 400000 x 128", flush=True)
+    data = silvic_amd.synthetic(2, rows=400_000, cols=128, seed=21)
+    rng = np.random.default_rng(0)
+    scores = (rng.standard_normal(data.num_rows) * 0.5).astype(np.float32)
+    g, h, _, _ = oracle.gradients(_abi.OBJ_BINARY, scores, data.label)
+    rocm = silvic_amd.RocmBackend(0)
+    hip = _hip()
+    dbuf = C.c_void_p()
+    n = 2 * data.total_bins
+    assert hip.hipMalloc(C.byref(dbuf), n * 8) == 0
+    try:
+        rocm.load(data)
+        mg, mh = rocm.set_gradients(g, h)
+        rocm.quantize(oracle.quant_spec(mg, mh, None, 4, True, 1, 0))
+        rows = rocm.reset_partition()
+        meta = data.features[3]
+        left = rocm.partition((0, rows), bin_split(meta.group, meta.column, list(range(meta.num_bins // 3))))
+        for leaf in ((0, rows), (left, rows - left), (17, min(5000, left - 17))):
+            print("[case] leaf", leaf, flush=True)
+            want = rocm.histogram(leaf)
+            got = _noalloc(rocm, hip, dbuf, leaf, n)
+            assert np.array_equal(got.astype(np.float64), want), leaf
+        # an empty leaf is zeros, as the allocating entry point's
+        assert not _noalloc(rocm, hip, dbuf, (5, 0), n).any()
+    finally:
+        rocm.close()
+        hip.hipFree(dbuf)
