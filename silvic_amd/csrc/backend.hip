@@ -978,6 +978,16 @@ struct Context {
         sync();  // the staging is rewritten by the next call
     }
 
+    // k_tree_leaves for trees of up to max_leaves leaves (the gate, when set, holds the actual count)
+    void launch_tree_leaves(const TreeLeavesArgs &a, uint32_t max_leaves) {
+        const uint32_t grid = std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS));
+        if (max_leaves <= LEAVES_SMALL) k_tree_leaves<LEAVES_SMALL><<<grid, TL_THREADS, 0, stream>>>(a);
+        else if (max_leaves <= GROW_MAX_LEAVES) k_tree_leaves<GROW_MAX_LEAVES><<<grid, TL_THREADS, 0, stream>>>(a);
+        else fail(SROCM_ERR_UNSUPPORTED, "a tree of " + std::to_string(max_leaves) + " leaves; the row walk takes up to " +
+                                              std::to_string(GROW_MAX_LEAVES));
+        launch_check("k_tree_leaves");
+    }
+
     // The uploaded tree's leaf of every training row (leaf_of) and, when `sums` is set, the leaves' fixed-point
     // gradient sums over the in-bag rows, as leaf_sums over the grown tree's leaves gives them.
     void tree_leaves(uint32_t nn, uint32_t nl, const srocm_bag &bag, float gs, float hs, int64_t *sums) {
@@ -1003,8 +1013,7 @@ struct Context {
             a.row_offset = row_offset;
             a.fraction = bag.fraction;
         }
-        k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS)), TL_THREADS, 0, stream>>>(a);
-        launch_check("k_tree_leaves");
+        launch_tree_leaves(a, nl);
         if (!sums) return;
         Pinned<unsigned long long> &h = h_sums;
         h.alloc(2 * nl);
@@ -1399,7 +1408,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_check("k_root_prep");
         k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, g.dsc);
         launch_check("k_split_scan");
-        k_root_select<<<1, 512, 0, stream>>>(g);
+        if (L <= LEAVES_SMALL) k_root_select<LEAVES_SMALL><<<1, 512, 0, stream>>>(g);
+        else k_root_select<GROW_MAX_LEAVES><<<1, 512, 0, stream>>>(g);
         launch_check("k_root_select");
         // split steps: each is a no-op once the tree is complete; each commits at least one split
         uint32_t s = 0, batch = std::max<uint32_t>(2, last_steps ? last_steps : 8);
@@ -1441,7 +1451,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     launch_check("k_step_cat");
                 }
                 SelectArgs sa2{fin_counts.p, d_plans.p + parity, d_plans.p + (parity ^ 1u)};
-                k_step_select<<<JMAX, 512, 0, stream>>>(g, sa2);
+                if (L <= LEAVES_SMALL) k_step_select<LEAVES_SMALL><<<JMAX, 512, 0, stream>>>(g, sa2);
+                else k_step_select<GROW_MAX_LEAVES><<<JMAX, 512, 0, stream>>>(g, sa2);
                 launch_check("k_step_select");
             }
             if (after_steps) {  // queued behind the readback, so the host takes the tree while they run
@@ -1761,8 +1772,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             a.row_offset = row_offset;
             a.fraction = bag.fraction;
             a.gate = d_gate.p;
-            k_tree_leaves<<<std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS)), TL_THREADS, 0, stream>>>(a);
-            launch_check("k_tree_leaves");
+            launch_tree_leaves(a, p.num_leaves);
             LeafValueArgs la{d_leaf_out.p, d_gate.p, d_scales.p, 0u, bias ? 1u : 0u, 1.0f, 1.0f, p.cfg.lambda_l1, p.cfg.lambda_l2,
                              p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + L, d_leaf_values.p};
             k_leaf_values<<<1, 512, 0, stream>>>(la);
@@ -1792,7 +1802,6 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             }
             break;
         }
-        static_assert(GROW_MAX_LEAVES <= LEAVES_MAX_LDS, "k_tree_leaves takes every device-grown tree");
         if (renew) {
             // the scores and leaf values were queued behind the tree's steps (renew_on_device); the values reach
             // the host with the next wait

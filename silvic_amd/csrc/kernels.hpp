@@ -673,7 +673,7 @@ struct TreeLeavesArgs {
     const uint8_t *colbins;            // column-major bins [feature][rows]
     uint64_t rows;
     const DevNode *nodes;
-    uint32_t nn, nl;                   // internal nodes, leaves (nn >= 1, nl <= LEAVES_MAX_LDS)
+    uint32_t nn, nl;                   // internal nodes, leaves (nn >= 1, nl <= the kernel's MAXL)
     uint16_t *leaf_of;                 // [rows]
     const float *grad, *hess;          // null: no sums
     float gs, hs;
@@ -684,18 +684,21 @@ struct TreeLeavesArgs {
     const uint32_t *gate;              // when set: the leaves (nn, nl from it), 0 for no tree (k_tree_nodes)
     const DevScales *dsc;              // when set: gs and hs are its fixed-point scales
 };
-constexpr uint32_t LEAVES_MAX_LDS = 512;  // the trees k_tree_leaves takes (device growth grows up to this)
+// Instantiated for trees of up to 512 leaves (33 KiB of LDS: several blocks per compute unit) and up to 2048 (131 KiB:
+// one block).
+constexpr uint32_t LEAVES_SMALL = 512;
 constexpr int TL_RPT = 8;
 constexpr uint32_t TL_THREADS = 512;
 
+template <uint32_t MAXL>
 __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
-    __shared__ DevNode sn[LEAVES_MAX_LDS - 1];
-    __shared__ unsigned long long ls[LEAVES_MAX_LDS][2];
+    __shared__ DevNode sn[MAXL - 1];
+    __shared__ unsigned long long ls[MAXL][2];
     uint32_t nn = a.nn, nl = a.nl;
     const float gs = a.dsc ? a.dsc->gsc : a.gs, hs = a.dsc ? a.dsc->hsc : a.hs;
     if (a.gate) {
         nl = *a.gate;
-        if (nl == 0u || nl > LEAVES_MAX_LDS) return;
+        if (nl == 0u || nl > MAXL) return;
         nn = nl - 1u;
     }
     for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) sn[k] = a.nodes[k];
@@ -1745,9 +1748,13 @@ __device__ __forceinline__ uint32_t wave_total(uint32_t v) { return __shfl(wave_
 
 constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
 constexpr uint32_t SPEC_FLOOR = 4;         // speculative expansions a step may add whatever the budget
-constexpr uint32_t GROW_MAX_LEAVES = 512;  // num_leaves of a device-grown tree at most
-__host__ __device__ constexpr uint32_t grow_tcap(uint32_t num_leaves) { return 4 * num_leaves + 64; }
-constexpr uint32_t TCAP_MAX = 4 * GROW_MAX_LEAVES + 64;
+constexpr uint32_t GROW_MAX_LEAVES = 2048;  // num_leaves of a device-grown tree at most
+// Speculative leaves of a tree of num_leaves: 4 per leaf up to 512 leaves, then 2 per further leaf (the expansions
+// a tree keeps need 2 per leaf; the rest is the room for speculating ahead, which advance keeps within it).
+__host__ __device__ constexpr uint32_t grow_tcap(uint32_t num_leaves) {
+    return num_leaves <= 512 ? 4 * num_leaves + 64 : 2 * num_leaves + 1088;
+}
+
 constexpr uint32_t T_LEAF = 0, T_PLANNED = 1, T_EXPANDED = 2;  // a speculative leaf's state
 
 // A leaf of the speculative tree: the committed leaves and the children of every expansion.
@@ -2017,20 +2024,24 @@ __global__ void k_root_prep(GrowState g) {
 // `scratch` is LDS of at least sizeof(AdvShared) bytes.
 // ---------------------------------------------------------------------------------------------------------
 
+template <uint32_t MAXL>
 struct AdvShared {
-    double gain[TCAP_MAX];                // speculative leaves' best gains
-    uint32_t meta[TCAP_MAX];              // bit 0: has a best split; bits 1-2: state; bits 3..: kid + 1
-    uint16_t leaf_t[GROW_MAX_LEAVES];     // committed leaf -> speculative leaf, as the replay goes
-    int16_t pnode[GROW_MAX_LEAVES];       // committed leaf -> the internal node above it (-1: the root)
-    uint8_t is_left[GROW_MAX_LEAVES];     // committed leaf is its node's left child
-    uint8_t touched[GROW_MAX_LEAVES];     // committed leaf changed by this replay
-    uint16_t ck[GROW_MAX_LEAVES];         // commit c: the speculative leaf split (node n0 - 1 + c)
-    uint16_t cx[GROW_MAX_LEAVES];         // commit c: the leaf id split
-    int16_t cpn[GROW_MAX_LEAVES];         // commit c: the split leaf's node above
-    uint8_t cleft[GROW_MAX_LEAVES];       // commit c: the split leaf was its node's left child
-    uint64_t ckey[TCAP_MAX];              // speculation candidates' keys: higher gain (as f32), then lower leaf
-    uint32_t crank[TCAP_MAX];             // and their ranks
-    uint16_t cand[TCAP_MAX];              // speculation candidates
+    static constexpr uint32_t TCAP = grow_tcap(MAXL);
+    static constexpr uint32_t CAND = (TCAP + 1) / 2 + 1;  // unexpanded leaves: E + 1 of the 2E + 1 of E expansions
+    double gain[TCAP];                    // speculative leaves' best gains
+    uint32_t meta[TCAP];                  // bit 0: has a best split; bits 1-2: state; bits 3..: kid + 1
+    uint16_t leaf_t[MAXL];                // committed leaf -> speculative leaf, as the replay goes
+    int16_t pnode[MAXL];                  // committed leaf -> the internal node above it (-1: the root)
+    uint8_t is_left[MAXL];                // committed leaf is its node's left child
+    uint8_t touched[MAXL];                // committed leaf changed by this replay
+    uint16_t ck[MAXL];                    // commit c: the speculative leaf split (node n0 - 1 + c)
+    uint16_t cx[MAXL];                    // commit c: the leaf id split
+    int16_t cpn[MAXL];                    // commit c: the split leaf's node above
+    uint8_t cleft[MAXL];                  // commit c: the split leaf was its node's left child
+    uint64_t ckey[CAND];                  // speculation candidates' keys: higher gain (as f32), then lower leaf
+    uint32_t crank[CAND];                 // and their ranks
+    uint16_t cand[CAND];                  // speculation candidates
+    uint32_t rkey[MAXL > LEAVES_SMALL ? MAXL : 1];  // committed leaf's replay key (replay_lds)
     uint16_t job_t[JMAX];
     uint32_t ncand, ncommit, n, blocker, done, njobs;
 };
@@ -2039,15 +2050,16 @@ __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
     return (k.has ? 1u : 0u) | (k.state << 1) | (static_cast<uint32_t>(k.kid + 1) << 3);
 }
 
-// A committed leaf's replay key: the top 23 bits of its positive gain (a positive double's bits order as its value),
-// then the lower leaf id (511 - id); 0 for a leaf without a split or a positive gain. One u32 max over the wave
-// finds the highest key; it is best_leaf's choice unless another leaf shares its gain prefix, which the replay
-// then settles on the exact gains.
+// A committed leaf's replay key: the top 32 - IDB bits of its positive gain (a positive double's bits order as its
+// value), then the lower leaf id (2^IDB - 1 - id); 0 for a leaf without a split or a positive gain. One u32 max over
+// the wave finds the highest key; it is best_leaf's choice unless another leaf shares its gain prefix, which the
+// replay then settles on the exact gains. IDB = 9 takes trees of up to 512 leaves, 11 up to 2048.
+template <int IDB>
 __device__ __forceinline__ uint32_t replay_key(double gain, uint32_t meta, uint32_t id) {
     if (!(meta & 1u) || !(gain > 0.0)) return 0u;
-    uint32_t p = static_cast<uint32_t>(__builtin_bit_cast(uint64_t, gain) >> 40);
+    uint32_t p = static_cast<uint32_t>(__builtin_bit_cast(uint64_t, gain) >> (31 + IDB));
     p = p ? p : 1u;
-    return (p << 9) | (GROW_MAX_LEAVES - 1u - id);
+    return (p << IDB) | ((1u << IDB) - 1u - id);
 }
 
 // The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave: lane l holds committed
@@ -2057,8 +2069,11 @@ __device__ __forceinline__ uint32_t replay_key(double gain, uint32_t meta, uint3
 // leaves share the winner's gain prefix; the rule that the first leaf with a split decides when its gain is NaN
 // takes a wave minimum, only while some leaf has a NaN gain. Leaves the commits, the committed-leaf arrays and the
 // outcome in `s`.
-template <int NPL>
-__device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
+template <int NPL, typename S>
+__device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
+    constexpr int IDB = 9;
+    static_assert(NPL * 64 <= (1 << IDB), "leaf ids fit the key");
+    constexpr uint32_t IDM = (1u << IDB) - 1u;
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t rk[NPL], rm[NPL], rt[NPL];
     int32_t rp[NPL];
@@ -2074,7 +2089,7 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
             rt[j] = s.leaf_t[id];
             const double gj = s.gain[rt[j]];
             rm[j] = s.meta[rt[j]];
-            rk[j] = replay_key(gj, rm[j], id);
+            rk[j] = replay_key<IDB>(gj, rm[j], id);
             rp[j] = s.pnode[id];
             rl |= s.is_left[id] ? 1u << j : 0u;
             rhas |= (rm[j] & 1u) ? 1u << j : 0u;
@@ -2109,18 +2124,18 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
             done = true;
             break;
         }
-        uint32_t x = GROW_MAX_LEAVES - 1u - (best & (GROW_MAX_LEAVES - 1u));
+        uint32_t x = IDM - (best & IDM);
         {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
-            const uint32_t bp = best >> 9;
+            const uint32_t bp = best >> IDB;
             uint32_t same = 0;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) same += (rk[j] >> 9) == bp && rk[j] != best ? 1u : 0u;
+            for (int j = 0; j < NPL; ++j) same += (rk[j] >> IDB) == bp && rk[j] != best ? 1u : 0u;
             if (__ballot(same != 0u)) {
                 double kg = 0.0;
                 int ki = -1;
 #pragma unroll
                 for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
-                    if ((rk[j] >> 9) != bp) continue;
+                    if ((rk[j] >> IDB) != bp) continue;
                     const double gj = s.gain[rt[j]];
                     if (ki < 0 || gj >= kg) {
                         kg = gj;
@@ -2166,13 +2181,13 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
         for (int j = 0; j < NPL; ++j) {
             if (jx == static_cast<uint32_t>(j) && lane == lx) {
                 rt[j] = kid;
-                rk[j] = replay_key(g0, m0, x);
+                rk[j] = replay_key<IDB>(g0, m0, x);
                 rm[j] = m0;
                 rp[j] = node;
             }
             if (jn == static_cast<uint32_t>(j) && lane == ln) {
                 rt[j] = kid + 1;
-                rk[j] = replay_key(g1, m1, n);
+                rk[j] = replay_key<IDB>(g1, m1, n);
                 rm[j] = m1;
                 rp[j] = node;
             }
@@ -2211,8 +2226,151 @@ __device__ __forceinline__ void replay(AdvShared &s, uint32_t n0, uint32_t L) {
     }
 }
 
+// The replay for trees of more than 512 leaves: as replay, with each committed leaf's key, speculative leaf and node
+// above in LDS (s.rkey, s.leaf_t, s.pnode) rather than in registers, and each lane's largest key cached in a
+// register, which only the lanes owning the two leaves a commit changes recompute. The left / changed / has-split /
+// NaN-gain flags stay in registers, one bit per leaf of the lane. A lane other than the winner's holds a key with the
+// winner's gain prefix exactly when its largest key has that prefix, so the exact f64 argmax runs only when one does.
+template <int NPL, typename S>
+__device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
+    constexpr int IDB = 11;
+    static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 32, "leaf ids fit");
+    constexpr uint32_t IDM = (1u << IDB) - 1u;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t rl = 0, rtouch = 0, rhas = 0, rnan = 0, lk = 0;
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t id = lane + 64u * j;
+        uint32_t key = 0;
+        if (id < n0) {
+            const uint32_t t = s.leaf_t[id];
+            const double gj = s.gain[t];
+            const uint32_t m = s.meta[t];
+            key = replay_key<IDB>(gj, m, id);
+            rl |= s.is_left[id] ? 1u << j : 0u;
+            rhas |= (m & 1u) ? 1u << j : 0u;
+            rnan |= (m & 1u) && gj != gj ? 1u << j : 0u;
+        }
+        s.rkey[id] = key;
+        lk = key > lk ? key : lk;
+    }
+    uint32_t n = n0, nc = 0, blocker = 0;
+    bool done = false;
+    for (;;) {
+        if (n >= L) {
+            done = true;
+            break;
+        }
+        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
+        if (__ballot(rnan != 0u)) {
+            int lfirst = 1 << 30;
+            for (int j = NPL - 1; j >= 0; --j)  // descending, so the lowest id is the one kept
+                if ((rhas >> j) & 1u) lfirst = 2 * static_cast<int>(lane + 64u * j) + static_cast<int>((rnan >> j) & 1u);
+            const int first = wave_min_i32(lfirst);
+            if (first < (1 << 30) && (first & 1)) {
+                done = true;
+                break;
+            }
+        }
+        const uint32_t best = wave_max_u32(lk);
+        if (best == 0u) {
+            done = true;
+            break;
+        }
+        uint32_t x = IDM - (best & IDM);
+        {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
+            const uint32_t bp = best >> IDB;
+            bool other = lane != (x & 63u) && (lk >> IDB) == bp;
+            if (lane == (x & 63u)) {
+                for (int j = 0; j < NPL; ++j) {
+                    const uint32_t kj = s.rkey[lane + 64u * j];
+                    other = other || ((kj >> IDB) == bp && kj != best);
+                }
+            }
+            if (__ballot(other)) {
+                double kg = 0.0;
+                int ki = -1;
+                for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
+                    const uint32_t id = lane + 64u * j;
+                    if ((s.rkey[id] >> IDB) != bp) continue;
+                    const double gj = s.gain[s.leaf_t[id]];
+                    if (ki < 0 || gj >= kg) {
+                        kg = gj;
+                        ki = static_cast<int>(id);
+                    }
+                }
+                wave_argmax(kg, ki);
+                x = static_cast<uint32_t>(ki);
+            }
+        }
+        const uint32_t lx = x & 63u, jx = x >> 6;
+        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: one broadcast read
+        const uint32_t m = s.meta[k];
+        if (((m >> 1) & 3u) != T_EXPANDED) {
+            blocker = k;
+            break;
+        }
+        const int32_t pn = s.pnode[x];
+        const uint32_t xl = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rl), lx)) >> jx) & 1u;
+        const uint32_t kid = (m >> 3) - 1u;
+        const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
+        const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
+        if (lane == 0) {
+            s.ck[nc] = static_cast<uint16_t>(k);
+            s.cx[nc] = static_cast<uint16_t>(x);
+            s.cpn[nc] = static_cast<int16_t>(pn);
+            s.cleft[nc] = static_cast<uint8_t>(xl);
+        }
+        // leaf x becomes the left child, leaf n the right one, both under node n - 1; the owning lanes write them
+        const int32_t node = static_cast<int32_t>(n) - 1;
+        const uint32_t ln = n & 63u, jn = n >> 6;
+        const uint32_t bx = 1u << jx, bn = 1u << jn;
+        if (lane == lx) {
+            s.leaf_t[x] = static_cast<uint16_t>(kid);
+            s.pnode[x] = static_cast<int16_t>(node);
+            s.rkey[x] = replay_key<IDB>(g0, m0, x);
+            rl |= bx;
+            rtouch |= bx;
+            rhas = (rhas & ~bx) | ((m0 & 1u) ? bx : 0u);
+            rnan = (rnan & ~bx) | ((m0 & 1u) && g0 != g0 ? bx : 0u);
+        }
+        if (lane == ln) {
+            s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
+            s.pnode[n] = static_cast<int16_t>(node);
+            s.rkey[n] = replay_key<IDB>(g1, m1, n);
+            rl &= ~bn;
+            rtouch |= bn;
+            rhas = (rhas & ~bn) | ((m1 & 1u) ? bn : 0u);
+            rnan = (rnan & ~bn) | ((m1 & 1u) && g1 != g1 ? bn : 0u);
+        }
+        if (lane == lx || lane == ln) {
+            uint32_t mx = 0;
+            for (int j = 0; j < NPL; ++j) {
+                const uint32_t kj = s.rkey[lane + 64u * j];
+                mx = kj > mx ? kj : mx;
+            }
+            lk = mx;
+        }
+        ++nc;
+        ++n;
+    }
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t id = lane + 64u * j;
+        if (id < n) {
+            s.is_left[id] = static_cast<uint8_t>((rl >> j) & 1u);
+            s.touched[id] = static_cast<uint8_t>((rtouch >> j) & 1u);
+        }
+    }
+    if (lane == 0) {
+        s.ncommit = nc;
+        s.n = n;
+        s.done = done ? 1u : 0u;
+        s.blocker = blocker;
+    }
+}
+
+template <uint32_t MAXL>
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
-    AdvShared &s = *reinterpret_cast<AdvShared *>(scratch);
+    AdvShared<MAXL> &s = *reinterpret_cast<AdvShared<MAXL> *>(scratch);
     GrowCtl *ctl = g.ctl;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, nt = blockDim.x;
     if (ctl->done) return;
@@ -2236,10 +2394,15 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
 
     // -- the replay, one wave, with as few leaves per lane as the tree needs
     if (tid < 64) {
-        if (L <= 64) replay<1>(s, n0, L);
-        else if (L <= 128) replay<2>(s, n0, L);
-        else if (L <= 256) replay<4>(s, n0, L);
-        else replay<GROW_MAX_LEAVES / 64>(s, n0, L);
+        if constexpr (MAXL <= LEAVES_SMALL) {
+            if (L <= 64) replay<1>(s, n0, L);
+            else if (L <= 128) replay<2>(s, n0, L);
+            else if (L <= 256) replay<4>(s, n0, L);
+            else replay<LEAVES_SMALL / 64>(s, n0, L);
+        } else {
+            if (L <= 1024) replay_lds<16>(s, n0, L);
+            else replay_lds<MAXL / 64>(s, n0, L);
+        }
     }
     __syncthreads();
     const uint32_t nc = s.ncommit, n = s.n;
@@ -2448,7 +2611,7 @@ __global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *su
     __shared__ uint32_t bad;
     GrowCtl *ctl = g.ctl;
     const uint32_t n = ctl->done && !ctl->error ? ctl->num_leaves : 0u;
-    const uint32_t nl = n > 1u && n <= LEAVES_MAX_LDS ? n : 0u, nn = nl ? nl - 1u : 0u;
+    const uint32_t nl = n > 1u && n <= GROW_MAX_LEAVES ? n : 0u, nn = nl ? nl - 1u : 0u;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
     for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) {
@@ -2475,10 +2638,12 @@ __global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *su
     }
 }
 
-// The root's best split (learner.rs:157-163), then the first step's plan. One block of 512 threads.
+// The root's best split (learner.rs:157-163), then the first step's plan. One block of 512 threads; MAXL: the
+// largest tree it takes (LEAVES_SMALL or GROW_MAX_LEAVES).
+template <uint32_t MAXL>
 __global__ __launch_bounds__(512) void k_root_select(GrowState g) {
     __shared__ SplitOut o;
-    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
+    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared<MAXL>)];
     ScanJob job = g.jobs[0];
     select_split(job, job.count, g.nf, g.cfg, grow_sg(g), grow_sh(g), &o, g.splittable);
     if (threadIdx.x == 0) {
@@ -2490,7 +2655,7 @@ __global__ __launch_bounds__(512) void k_root_select(GrowState g) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __threadfence();
-    advance(g, g.plans[0], scratch);
+    advance<MAXL>(g, g.plans[0], scratch);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -3269,8 +3434,9 @@ __global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
 }
 
 // Block j selects both children of job j (job_select); the last block to finish runs advance. grid: JMAX blocks.
+template <uint32_t MAXL>
 __global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) {
-    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared)];
+    __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared<MAXL>)];
     // the next plan stays empty unless advance writes it (it runs after every block has arrived, so after this):
     // the steps after a finished tree do nothing without reading the control block
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -3285,7 +3451,7 @@ __global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) 
     if (j >= P.njobs) return;
     job_select(g, P.jobs[j], j);
     if (!arrive_last(a.all_count, P.njobs)) return;
-    advance(g, *a.next, scratch);
+    advance<MAXL>(g, *a.next, scratch);
 }
 
 }  // namespace srocm

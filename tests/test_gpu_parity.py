@@ -297,7 +297,7 @@ def test_grown_tree_matches_the_oracle(rocm, rows, cols, leaves, qbins):
 
 
 # Edge cases of device growth, each against the oracle with the final partition row for row: one split; the
-# largest tree the device grows (512 leaves); a depth limit (jobs whose children are not histogrammed); a
+# largest tree of the register replay (512 leaves); a depth limit (jobs whose children are not histogrammed); a
 # min_data_in_leaf that stops the tree early; a tiny dataset; zero gradients (no split at all).
 @pytest.mark.parametrize("rows,cols,kw", [
     (50_000, 16, dict(num_leaves=2)),
@@ -355,15 +355,49 @@ def test_grown_tree_breaks_exact_gain_ties_by_leaf_id(rocm):
 
 
 def test_grow_rejects_more_leaves_than_the_device_grows(rocm):
-    say("grow 513 leaves")
+    say("grow 2049 leaves")
     data = silvic_amd.synthetic(2, rows=5_000, cols=8, seed=5)
     g, h = binary_gradients(data, 3)
     spec, _ = quantized_setup(rocm, data, g, h)
     n = rocm.reset_partition()
-    p = oracle.default_params(num_leaves=513)
+    p = oracle.default_params(num_leaves=2049)
     with pytest.raises(_abi.SilvicError) as e:
-        rocm.grow(p.cfg, 513, -1, spec.grad_scale, spec.hess_scale, np.ones(len(data.features), bool), (0, n), n)
+        rocm.grow(p.cfg, 2049, -1, spec.grad_scale, spec.hess_scale, np.ones(len(data.features), bool), (0, n), n)
     assert e.value.kind == _abi.KIND_NAMES[_abi.ERR_UNSUPPORTED]
+
+
+# Trees beyond 512 leaves (the replay keeps its leaves in LDS): config 5's shape (U[0,1) features, a
+# piecewise-constant regression target) at 2M rows, max_bin 255, grown to 1000 and 2047 leaves with the final
+# partition row for row, and boosted to 2047 leaves per tree.
+@pytest.mark.parametrize("leaves", [1000, 2047])
+def test_large_trees_match_the_oracle(rocm, leaves):
+    say("grow large", leaves)
+    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=3)
+    rng = np.random.default_rng(8)
+    g = (data.label - rng.standard_normal(data.num_rows).astype(np.float32) * 0.1).astype(np.float32)
+    h = np.ones_like(g)
+    p = oracle.default_params(num_leaves=leaves, min_data_in_leaf=20)
+    o_tree, o_ranges, o_part = oracle.grow_tree(data, g, h, p, renew=False)
+    assert o_tree["num_leaves"] == leaves
+    spec, _ = quantized_setup(rocm, data, g, h, seed=p.data_random_seed)
+    n = rocm.reset_partition()
+    mask = oracle.feature_mask(data.features, 1.0, 2, 0)
+    d = rocm.grow(p.cfg, p.num_leaves, p.max_depth, spec.grad_scale, spec.hess_scale, mask, (0, n), n)
+    compare_trees(d, dict(o_tree), f"grow {leaves}")
+    assert np.array_equal(d["leaf_range"].astype(np.int64), o_ranges)
+    assert np.array_equal(rocm.partition_rows(n), o_part[:n])
+
+
+def test_boosting_large_trees_matches_the_oracle():
+    say("boost 2047 leaves")
+    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=4)
+    o, t = boost_both(data, dict(num_leaves=2047), 3)
+    assert len(t.trees) == len(o.trees) == 3
+    for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+        assert ot["num_leaves"] == 2047
+        compare_trees(d, ot, f"tree {i}", exact_values=False)
+    assert np.array_equal(t.backend.scores(0), o.scores)
+    t.backend.close()
 
 
 # categorical columns: the default parameters search sorted categorical rules (21 bins > max_cat_to_onehot 4);
