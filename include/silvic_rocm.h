@@ -83,12 +83,19 @@ typedef struct srocm_dataset {
     uint32_t num_queries;
 } srocm_dataset;
 
-/* ObjectiveSetup (crates/silvic-core/src/backend/mod.rs:56-71). Lambdarank gradients are computed by the
- * caller and handed over with srocm_set_gradients. */
+/* ObjectiveSetup (crates/silvic-core/src/backend/mod.rs:56-71), the fields of its LambdaRank variant included.
+ * Lambdarank gradients are computed on the host in f64 (objective/lambdarank.rs:190-420) by
+ * srocm_compute_gradients and by the boosting loop; they need the training set's query_boundaries. */
 enum { SROCM_OBJ_REGRESSION = 0, SROCM_OBJ_BINARY = 1, SROCM_OBJ_LAMBDARANK = 2 };
 typedef struct srocm_objective {
-    uint32_t kind;  /* SROCM_OBJ_* */
-    double sigmoid; /* binary */
+    uint32_t kind;                  /* SROCM_OBJ_* */
+    double sigmoid;                 /* binary and lambdarank */
+    uint32_t norm;                  /* lambdarank: lambdarank_norm */
+    uint32_t truncation_level;      /* lambdarank: lambdarank_truncation_level */
+    const double *label_gain;       /* lambdarank: gain of each label value */
+    uint32_t num_label_gain;
+    const double *inverse_max_dcg;  /* lambdarank: per training query (the training set's num_queries), or NULL
+                                     * for the backend to derive them from the labels as objective/mod.rs:39-55 */
 } srocm_objective;
 
 /* QuantSpec (crates/silvic-core/src/quantize.rs:33-51). */

@@ -35,7 +35,9 @@ class Params(C.Structure):
                 ("feature_fraction_seed", C.c_uint32), ("data_random_seed", C.c_uint32),
                 ("num_grad_quant_bins", C.c_uint32), ("use_quantized_grad", C.c_uint8),
                 ("quant_train_renew_leaf", C.c_uint8), ("stochastic_rounding", C.c_uint8),
-                ("boost_from_average", C.c_uint8)]
+                ("boost_from_average", C.c_uint8), ("lambdarank_norm", C.c_uint32),
+                ("lambdarank_truncation_level", C.c_uint32), ("label_gain", C.POINTER(C.c_double)),
+                ("num_label_gain", C.c_uint32)]
 
 
 _lib = None
@@ -80,6 +82,13 @@ def lib():
             "oracle_feature_mask": (None, [P(_abi.Feature), C.c_uint32, C.c_double, C.c_uint32, C.c_uint32,
                                            P(C.c_uint8)]),
             "oracle_default_params": (None, [P(Params)]),
+            "oracle_lambdarank_query": (None, [P(C.c_float), P(C.c_float), P(C.c_float), C.c_uint32, P(C.c_double),
+                                               C.c_uint32, C.c_double, C.c_double, C.c_int, C.c_uint32,
+                                               P(C.c_float), P(C.c_float)]),
+            "oracle_max_dcg_at_k": (C.c_double, [C.c_uint32, P(C.c_float), C.c_uint32, P(C.c_double), C.c_uint32]),
+            "oracle_sigmoid_table_get": (C.c_double, [C.c_double, C.c_double]),
+            "oracle_lambdarank_gradients": (None, [P(_abi.Dataset), P(Params), P(C.c_float), P(C.c_float),
+                                                   P(C.c_float)]),
             "oracle_train": (C.c_void_p, [P(_abi.Dataset), P(Params)]),
             "oracle_model_free": (None, [C.c_void_p]),
             "oracle_model_num_trees": (C.c_uint32, [C.c_void_p]),
@@ -167,6 +176,40 @@ def gradients(objective, scores, label, sigmoid=1.0, weight=None):
                            None if w is None else ptr(w, C.c_float), n, ptr(g, C.c_float), ptr(h, C.c_float),
                            C.byref(mg), C.byref(mh))
     return g, h, mg.value, mh.value
+
+
+def lambdarank_query(scores, label, label_gain, inverse_max_dcg, sigmoid=1.0, norm=True, truncation_level=30,
+                     weight=None):
+    """One query's lambdarank gradients (objective/lambdarank.rs:254-301)."""
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    label = np.ascontiguousarray(label, dtype=np.float32)
+    gain = np.ascontiguousarray(label_gain, dtype=np.float64)
+    n = len(scores)
+    g = np.full(n, np.nan, np.float32)
+    h = np.full(n, np.nan, np.float32)
+    w = None if weight is None else np.ascontiguousarray(weight, dtype=np.float32)
+    lib().oracle_lambdarank_query(ptr(scores, C.c_float), ptr(label, C.c_float),
+                                  None if w is None else ptr(w, C.c_float), n, ptr(gain, C.c_double), len(gain),
+                                  inverse_max_dcg, sigmoid, int(norm), truncation_level, ptr(g, C.c_float),
+                                  ptr(h, C.c_float))
+    return g, h
+
+
+def max_dcg_at_k(k, labels, label_gain):
+    labels = np.ascontiguousarray(labels, dtype=np.float32)
+    gain = np.ascontiguousarray(label_gain, dtype=np.float64)
+    return lib().oracle_max_dcg_at_k(k, ptr(labels, C.c_float), len(labels), ptr(gain, C.c_double), len(gain))
+
+
+def lambdarank_gradients(data, params, scores):
+    """Every query's gradients of a dataset with query boundaries, under ``params``' lambdarank settings."""
+    ds = data.as_c()
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    g = np.empty(data.num_rows, np.float32)
+    h = np.empty(data.num_rows, np.float32)
+    lib().oracle_lambdarank_gradients(C.byref(ds), C.byref(params), ptr(scores, C.c_float), ptr(g, C.c_float),
+                                      ptr(h, C.c_float))
+    return g, h
 
 
 def histogram(data, packed, max_quant, rows, used=None):

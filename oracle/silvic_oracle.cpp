@@ -304,6 +304,194 @@ double max_abs(const float *v, uint64_t n) {
     return m;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// objective/lambdarank.rs: LambdarankNDCG with f64 accumulation, and objective/mod.rs:34-62 lambdarank_setup
+// ---------------------------------------------------------------------------------------------------------
+
+constexpr size_t RANK_MAX_POSITION = 10000;        // lambdarank.rs:22
+constexpr double RANK_MIN_SIGMOID_INPUT = -50.0;   // lambdarank.rs:25
+constexpr size_t RANK_SIGMOID_BINS = 1024 * 1024;  // lambdarank.rs:28
+constexpr double RANK_SCORE_DISTANCE_EPSILON = static_cast<double>(0.01f);  // lambdarank.rs:31
+constexpr size_t RANK_QUERIES_PER_TASK = 16;       // lambdarank.rs:249
+
+// lambdarank.rs:34-43
+const std::vector<double> &rank_discounts() {
+    static const std::vector<double> d = [] {
+        std::vector<double> v(RANK_MAX_POSITION);
+        for (size_t i = 0; i < RANK_MAX_POSITION; ++i) v[i] = 1.0 / std::log2(2.0 + static_cast<double>(i));
+        return v;
+    }();
+    return d;
+}
+double rank_discount(size_t rank) {
+    const auto &d = rank_discounts();
+    return rank < d.size() ? d[rank] : 1.0 / std::log2(2.0 + static_cast<double>(rank));
+}
+
+// lambdarank.rs:46-116 SigmoidTable
+struct SigmoidTable {
+    double sigmoid, min_input, max_input, idx_factor;
+    std::vector<double> values;
+    explicit SigmoidTable(double s) : sigmoid(s) {
+        min_input = RANK_MIN_SIGMOID_INPUT / s / 2.0;
+        max_input = -min_input;
+        idx_factor = static_cast<double>(RANK_SIGMOID_BINS) / (max_input - min_input);
+        values.resize(RANK_SIGMOID_BINS);
+        for (size_t i = 0; i < RANK_SIGMOID_BINS; ++i) {
+            double score = static_cast<double>(i) / idx_factor + min_input;
+            values[i] = 1.0 / (1.0 + std::exp(score * s));
+        }
+    }
+    double get(double delta) const {
+        if (delta <= min_input) return values[0];
+        if (delta >= max_input) return values[RANK_SIGMOID_BINS - 1];
+        return values[std::min(static_cast<size_t>((delta - min_input) * idx_factor), RANK_SIGMOID_BINS - 1)];
+    }
+};
+
+const SigmoidTable &sigmoid_table(double s) {
+    static std::mutex mu;
+    static std::unique_ptr<SigmoidTable> last;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!last || last->sigmoid != s) last = std::make_unique<SigmoidTable>(s);
+    return *last;
+}
+
+// lambdarank.rs:119-139 max_dcg_at_k
+double max_dcg_at_k(size_t k, const float *labels, size_t n, const std::vector<double> &label_gain) {
+    std::vector<size_t> label_count(label_gain.size(), 0);
+    for (size_t i = 0; i < n; ++i) label_count[static_cast<size_t>(labels[i])] += 1;
+    size_t top_label = label_gain.size() - 1;
+    double dcg = 0.0;
+    for (size_t j = 0; j < std::min(k, n); ++j) {
+        while (top_label > 0 && label_count[top_label] == 0) --top_label;
+        dcg += rank_discount(j) * label_gain[top_label];
+        label_count[top_label] -= 1;  // wrapping_sub: label 0 may go "below zero" unchecked
+    }
+    return dcg;
+}
+
+// lambdarank.rs:165-170 descending_key
+uint32_t descending_key(float score) {
+    float z = score + 0.0f;
+    uint32_t bits;
+    std::memcpy(&bits, &z, 4);
+    uint32_t ascending = (bits >> 31) == 1 ? ~bits : (bits | (1u << 31));
+    return ~ascending;
+}
+
+struct RankSetup {
+    double sigmoid = 1.0;
+    bool norm = true;
+    uint32_t truncation_level = 30;
+    std::vector<double> label_gain, inverse_max_dcg;
+};
+
+// lambdarank.rs:254-301 query_gradients with load_ranked (:304-322), worst_score (:325-332), accumulate_pairs
+// (:336-378)
+void rank_query(const RankSetup &st, size_t query, const float *scores, const float *label, const float *weight,
+                size_t n, float *grad, float *hess) {
+    if (n == 0) return;
+    const SigmoidTable &table = sigmoid_table(st.sigmoid);
+    std::vector<uint64_t> keys(n);
+    for (size_t row = 0; row < n; ++row) keys[row] = (static_cast<uint64_t>(descending_key(scores[row])) << 32) | row;
+    std::sort(keys.begin(), keys.end());
+    std::vector<size_t> order(n);
+    for (size_t k = 0; k < n; ++k) order[k] = static_cast<size_t>(keys[k] & 0xffffffffull);
+    std::vector<double> score(n), gain(n), discount(n), lambda(n, 0.0), hessian(n, 0.0);
+    std::vector<float> lab(n);
+    for (size_t k = 0; k < n; ++k) {
+        score[k] = static_cast<double>(scores[order[k]]);
+        lab[k] = label[order[k]];
+        gain[k] = st.label_gain[static_cast<size_t>(lab[k])];
+        discount[k] = rank_discount(k);
+    }
+    size_t worst = n - 1;
+    if (worst > 0 && score[worst] == -std::numeric_limits<double>::infinity()) worst -= 1;
+    const bool norm_by_distance = st.norm && score[0] != score[worst];
+    const double inverse_max_dcg = st.inverse_max_dcg[query];
+    size_t valid = n;
+    for (size_t k = 0; k < n; ++k)
+        if (score[k] == -std::numeric_limits<double>::infinity()) {
+            valid = k;
+            break;
+        }
+    const double sigmoid_squared = st.sigmoid * st.sigmoid;
+    double sum_lambdas = 0.0;
+    const size_t last_i = std::min<size_t>(st.truncation_level, valid == 0 ? 0 : valid - 1);
+    for (size_t i = 0; i < last_i; ++i) {
+        double score_i = score[i], gain_i = gain[i], discount_i = discount[i];
+        float label_i = lab[i];
+        double lambda_i = lambda[i], hessian_i = hessian[i];
+        for (size_t j = i + 1; j < valid; ++j) {
+            if (lab[j] == label_i) continue;
+            double sign = label_i > lab[j] ? 1.0 : -1.0;
+            double delta_score = sign * (score_i - score[j]);
+            double dcg_gap = sign * (gain_i - gain[j]);
+            double paired_discount = std::fabs(discount_i - discount[j]);
+            double delta_pair_ndcg = dcg_gap * paired_discount * inverse_max_dcg;
+            if (norm_by_distance) delta_pair_ndcg /= RANK_SCORE_DISTANCE_EPSILON + std::fabs(delta_score);
+            double p = table.get(delta_score);
+            double p_lambda = p * (-st.sigmoid * delta_pair_ndcg);
+            double p_hessian = p * (1.0 - p) * (sigmoid_squared * delta_pair_ndcg);
+            lambda_i += sign * p_lambda;
+            lambda[j] -= sign * p_lambda;
+            hessian_i += p_hessian;
+            hessian[j] += p_hessian;
+            sum_lambdas -= 2.0 * p_lambda;
+        }
+        lambda[i] = lambda_i;
+        hessian[i] = hessian_i;
+    }
+    double norm_factor = st.norm && sum_lambdas > 0.0 ? std::log2(1.0 + sum_lambdas) / sum_lambdas : 1.0;
+    for (size_t k = 0; k < n; ++k) {
+        size_t row = order[k];
+        float g = static_cast<float>(lambda[k] * norm_factor);
+        float h = static_cast<float>(hessian[k] * norm_factor);
+        if (weight) {
+            g *= weight[row];
+            h *= weight[row];
+        }
+        grad[row] = g;
+        hess[row] = h;
+    }
+}
+
+// objective/mod.rs:34-62 lambdarank_setup, with lambdarank.rs:172-188 check_labels
+RankSetup lambdarank_setup(const srocm_dataset *d, double sigmoid, bool norm, uint32_t truncation,
+                           const double *label_gain, uint32_t num_label_gain) {
+    if (!d->query_boundaries || d->num_queries == 0) throw std::runtime_error("ranking tasks require query information");
+    RankSetup st;
+    st.sigmoid = sigmoid;
+    st.norm = norm;
+    st.truncation_level = truncation;
+    if (label_gain && num_label_gain) st.label_gain.assign(label_gain, label_gain + num_label_gain);
+    else
+        for (uint32_t i = 0; i < 31; ++i) st.label_gain.push_back(static_cast<double>((1u << i) - 1));  // config.rs:118-121
+    for (uint64_t r = 0; r < d->num_rows; ++r) {
+        float l = d->label[r];
+        if (std::fabs(static_cast<double>(l) - static_cast<double>(static_cast<int32_t>(l))) > K_EPSILON ||
+            l < 0.0f || static_cast<size_t>(l) >= st.label_gain.size())
+            throw std::runtime_error("bad ranking label");
+    }
+    for (uint32_t q = 0; q < d->num_queries; ++q) {
+        uint32_t b = d->query_boundaries[q], e = d->query_boundaries[q + 1];
+        double max_dcg = max_dcg_at_k(truncation, d->label + b, e - b, st.label_gain);
+        st.inverse_max_dcg.push_back(max_dcg > 0.0 ? 1.0 / max_dcg : 0.0);
+    }
+    return st;
+}
+
+// lambdarank.rs:190-246 gradients: every query, parallel over queries
+void rank_gradients(const RankSetup &st, const srocm_dataset *d, const float *scores, float *grad, float *hess) {
+    par_chunks(d->num_queries, RANK_QUERIES_PER_TASK, [&](uint64_t, uint64_t qb, uint64_t qe) {
+        for (uint64_t q = qb; q < qe; ++q) {
+            uint32_t b = d->query_boundaries[q], e = d->query_boundaries[q + 1];
+            rank_query(st, q, scores + b, d->label + b, d->weight ? d->weight + b : nullptr, e - b, grad + b, hess + b);
+        }
+    });
+}
+
 // objective/mod.rs:92-109, binary.rs:11-25, regression.rs:60-67
 double init_score(uint32_t objective, double sigmoid, const float *label, const float *weight, uint64_t n) {
     double sum_label = 0.0, sum_weight = 0.0;
@@ -1196,6 +1384,8 @@ struct CpuBackend {
     double times[T_COUNT] = {0};
     double hist_bins = 0.0;
 
+    RankSetup rank;  // lambdarank
+
     void load(const srocm_dataset *d, uint32_t obj, double sig) {
         data = d;
         layout = group_layout(d);
@@ -1210,7 +1400,8 @@ struct CpuBackend {
     void init_scores(double v) { std::fill(scores.begin(), scores.end(), static_cast<float>(v)); }
     std::pair<double, double> compute_gradients() {
         Timer t(&times[T_GRAD]);
-        gradients(objective, sigmoid, scores.data(), data->label, data->weight, data->num_rows, grad.data(), hess.data());
+        if (objective == SROCM_OBJ_LAMBDARANK) rank_gradients(rank, data, scores.data(), grad.data(), hess.data());
+        else gradients(objective, sigmoid, scores.data(), data->label, data->weight, data->num_rows, grad.data(), hess.data());
         return {max_abs(grad.data(), grad.size()), max_abs(hess.data(), hess.size())};
     }
     void quantize(const srocm_quant_spec &s) {
@@ -1493,7 +1684,13 @@ Model *train(const srocm_dataset *d, const oracle_params *p) {
     Clock::time_point start = Clock::now();
     CpuBackend backend;
     backend.load(d, p->objective, p->sigmoid);
-    double init = p->boost_from_average ? init_score(p->objective, p->sigmoid, d->label, d->weight, d->num_rows) : 0.0;
+    if (p->objective == SROCM_OBJ_LAMBDARANK)
+        backend.rank = lambdarank_setup(d, p->sigmoid, p->lambdarank_norm != 0, p->lambdarank_truncation_level,
+                                        p->label_gain, p->num_label_gain);
+    // objective/mod.rs:92-97: no initial score for lambdarank
+    double init = p->boost_from_average && p->objective != SROCM_OBJ_LAMBDARANK
+                      ? init_score(p->objective, p->sigmoid, d->label, d->weight, d->num_rows)
+                      : 0.0;
     init = std::fabs(init) > K_EPSILON ? init : 0.0;
     backend.init_scores(init);
     model->init_score = init;
@@ -1698,8 +1895,36 @@ void oracle_feature_mask(const srocm_feature *features, uint32_t num_features, d
     feature_mask(features, num_features, fraction, seed, iteration, mask);
 }
 
+void oracle_lambdarank_query(const float *scores, const float *label, const float *weight, uint32_t n,
+                             const double *label_gain, uint32_t num_label_gain, double inverse_max_dcg,
+                             double sigmoid, int norm, uint32_t truncation_level, float *grad, float *hess) {
+    RankSetup st;
+    st.sigmoid = sigmoid;
+    st.norm = norm != 0;
+    st.truncation_level = truncation_level;
+    st.label_gain.assign(label_gain, label_gain + num_label_gain);
+    st.inverse_max_dcg = {inverse_max_dcg};
+    rank_query(st, 0, scores, label, weight, n, grad, hess);
+}
+
+double oracle_max_dcg_at_k(uint32_t k, const float *labels, uint32_t n, const double *label_gain,
+                           uint32_t num_label_gain) {
+    return max_dcg_at_k(k, labels, n, std::vector<double>(label_gain, label_gain + num_label_gain));
+}
+
+double oracle_sigmoid_table_get(double sigmoid, double delta) { return sigmoid_table(sigmoid).get(delta); }
+
+void oracle_lambdarank_gradients(const srocm_dataset *data, const oracle_params *p, const float *scores, float *grad,
+                                 float *hess) {
+    RankSetup st = lambdarank_setup(data, p->sigmoid, p->lambdarank_norm != 0, p->lambdarank_truncation_level,
+                                    p->label_gain, p->num_label_gain);
+    rank_gradients(st, data, scores, grad, hess);
+}
+
 void oracle_default_params(oracle_params *p) {
     std::memset(p, 0, sizeof(*p));
+    p->lambdarank_norm = 1;
+    p->lambdarank_truncation_level = 30;
     p->objective = SROCM_OBJ_REGRESSION;
     p->sigmoid = 1.0;
     p->num_iterations = 100;

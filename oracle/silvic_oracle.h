@@ -105,7 +105,7 @@ void oracle_feature_mask(const srocm_feature *features, uint32_t num_features, d
 
 /* Training parameters the path reads (config.rs:123-167 defaults). */
 typedef struct oracle_params {
-    uint32_t objective;            /* SROCM_OBJ_REGRESSION / SROCM_OBJ_BINARY */
+    uint32_t objective;            /* SROCM_OBJ_REGRESSION / SROCM_OBJ_BINARY / SROCM_OBJ_LAMBDARANK */
     double sigmoid;
     uint32_t num_iterations;
     double learning_rate;
@@ -123,9 +123,27 @@ typedef struct oracle_params {
     uint8_t quant_train_renew_leaf;
     uint8_t stochastic_rounding;
     uint8_t boost_from_average;
+    /* lambdarank (config.rs:101-103, 152-154); label_gain NULL: LightGBM's default 2^i - 1, i < 31 */
+    uint32_t lambdarank_norm;
+    uint32_t lambdarank_truncation_level;
+    const double *label_gain;
+    uint32_t num_label_gain;
 } oracle_params;
 
 void oracle_default_params(oracle_params *p);
+
+/* LambdarankNDCG for one query (objective/lambdarank.rs:254-301) with a given inverse max DCG; grad/hess hold n. */
+void oracle_lambdarank_query(const float *scores, const float *label, const float *weight, uint32_t n,
+                             const double *label_gain, uint32_t num_label_gain, double inverse_max_dcg,
+                             double sigmoid, int norm, uint32_t truncation_level, float *grad, float *hess);
+/* lambdarank.rs:119-139 */
+double oracle_max_dcg_at_k(uint32_t k, const float *labels, uint32_t n, const double *label_gain,
+                           uint32_t num_label_gain);
+/* lambdarank.rs:104-116 SigmoidTable::get */
+double oracle_sigmoid_table_get(double sigmoid, double delta);
+/* Every query's gradients of a dataset with query boundaries (lambdarank.rs:190-246, setup objective/mod.rs:34-62). */
+void oracle_lambdarank_gradients(const srocm_dataset *data, const oracle_params *params, const float *scores,
+                                 float *grad, float *hess);
 
 /* boosting.rs:83-149 train_from (no init model, no validation sets). Returns a model handle. */
 void *oracle_train(const srocm_dataset *data, const oracle_params *params);

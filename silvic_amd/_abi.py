@@ -59,7 +59,9 @@ class Dataset(C.Structure):
 
 
 class Objective(C.Structure):
-    _fields_ = [("kind", C.c_uint32), ("sigmoid", C.c_double)]
+    _fields_ = [("kind", C.c_uint32), ("sigmoid", C.c_double), ("norm", C.c_uint32), ("truncation_level", C.c_uint32),
+                ("label_gain", C.POINTER(C.c_double)), ("num_label_gain", C.c_uint32),
+                ("inverse_max_dcg", C.POINTER(C.c_double))]
 
 
 class QuantSpec(C.Structure):
@@ -217,6 +219,10 @@ def load_synth():
         lib.synth_label.argtypes = [C.c_void_p]
         lib.synth_bounds.restype = C.POINTER(C.c_double)
         lib.synth_bounds.argtypes = [C.c_void_p, C.c_uint32]
+        lib.synth_num_queries.restype = C.c_uint32
+        lib.synth_num_queries.argtypes = [C.c_void_p]
+        lib.synth_query_boundaries.restype = C.POINTER(C.c_uint32)
+        lib.synth_query_boundaries.argtypes = [C.c_void_p]
         _synth = lib
     return _synth
 

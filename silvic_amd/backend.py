@@ -14,6 +14,9 @@ from . import _abi
 from ._abi import BinSplit, DeviceNode, LeafRange
 
 
+# LightGBM's default label_gain: 2^i - 1 for i < 31 (config.rs:118-121)
+DEFAULT_LABEL_GAIN = [float((1 << i) - 1) for i in range(31)]
+
 def _p(a, t):
     return a.ctypes.data_as(C.POINTER(t))
 
@@ -69,12 +72,18 @@ class RocmBackend:
         self._check(self._lib.srocm_name(self._h, buf, 256))
         return buf.value.decode()
 
-    def load(self, train, valid=(), objective=_abi.OBJ_REGRESSION, sigmoid=1.0):
-        """``Backend::load`` (mod.rs:125-126)."""
+    def load(self, train, valid=(), objective=_abi.OBJ_REGRESSION, sigmoid=1.0, norm=True, truncation_level=30,
+             label_gain=None, inverse_max_dcg=None):
+        """``Backend::load`` (mod.rs:125-126). Lambdarank takes ``ObjectiveSetup::LambdaRank``'s fields
+        (mod.rs:62-71): ``label_gain`` defaults to LightGBM's 2^i - 1 (i < 31), and ``inverse_max_dcg`` (one per
+        training query) is derived from the labels by the backend when not given."""
         t = train.as_c()
         vs = [v.as_c() for v in valid]
         arr = (C.POINTER(_abi.Dataset) * max(1, len(vs)))(*[C.pointer(v) for v in vs])
-        obj = _abi.Objective(objective, sigmoid)
+        gain = np.ascontiguousarray(DEFAULT_LABEL_GAIN if label_gain is None else label_gain, dtype=np.float64)
+        inv = None if inverse_max_dcg is None else np.ascontiguousarray(inverse_max_dcg, dtype=np.float64)
+        obj = _abi.Objective(objective, sigmoid, int(bool(norm)), int(truncation_level), _p(gain, C.c_double),
+                             len(gain), None if inv is None else _p(inv, C.c_double))
         self._check(self._lib.srocm_load(self._h, C.byref(t), arr, len(vs), C.byref(obj)))
         self._datasets = [train, *valid]
         self.total_bins = train.total_bins

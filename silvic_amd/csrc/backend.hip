@@ -10,6 +10,7 @@
 
 #include "../../include/silvic_rocm.h"
 #include "kernels.hpp"
+#include "lambdarank.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -366,6 +367,9 @@ struct Context {
     DevBuf<LeafJob> d_leaf_jobs;
     DevBuf<unsigned long long> d_leaf_out;
 
+    srocm_rank::Ranker ranker;  // lambdarank: the setup, the sigmoid and discount tables
+    Pinned<float> h_rank_scores, h_rank_grad, h_rank_hess;
+
     Profile prof;
     int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
 
@@ -408,11 +412,58 @@ struct Context {
     // load (cpu.rs:707-746 checks; device layout)
     // ------------------------------------------------------------------------------------------------
 
+    // ObjectiveSetup::LambdaRank (backend/mod.rs:62-71) and the training set's query boundaries, checked as silvic's
+    // setup checks them (objective/mod.rs:34-62; lambdarank.rs:172-188 for the labels)
+    void load_ranking(const srocm_dataset *t, const srocm_objective *obj) {
+        const uint64_t nq = t->num_queries;
+        if (!t->query_boundaries || nq == 0) fail(SROCM_ERR_DATA, "ranking tasks require query information");
+        if (t->query_boundaries[0] != 0 || t->query_boundaries[nq] != t->num_rows)
+            fail(SROCM_ERR_DATA, "query boundaries must run from 0 to the number of rows");
+        for (uint64_t q = 0; q < nq; ++q)
+            if (t->query_boundaries[q + 1] < t->query_boundaries[q]) fail(SROCM_ERR_DATA, "query boundaries must not decrease");
+        if (!obj->label_gain || obj->num_label_gain == 0) fail(SROCM_ERR_CONFIG, "lambdarank needs label gains");
+        for (uint64_t r = 0; r < t->num_rows; ++r) {
+            const float l = t->label[r];
+            if (std::fabs(static_cast<double>(l) - static_cast<double>(static_cast<int32_t>(l))) > K_EPS_H)
+                fail(SROCM_ERR_DATA, "label should be int type (met " + std::to_string(l) + ") for ranking task");
+            if (l < 0.0f) fail(SROCM_ERR_DATA, "label should be non-negative (met " + std::to_string(l) + ") for ranking task");
+            if (static_cast<uint64_t>(l) >= obj->num_label_gain)
+                fail(SROCM_ERR_DATA, "label " + std::to_string(static_cast<uint64_t>(l)) +
+                                         " is not less than the number of label mappings (" + std::to_string(obj->num_label_gain) + ")");
+        }
+        srocm_rank::Setup st;
+        st.sigmoid = obj->sigmoid;
+        st.norm = obj->norm != 0;
+        st.truncation_level = obj->truncation_level;
+        st.label_gain.assign(obj->label_gain, obj->label_gain + obj->num_label_gain);
+        if (obj->inverse_max_dcg) st.inverse_max_dcg.assign(obj->inverse_max_dcg, obj->inverse_max_dcg + nq);
+        st.boundaries.assign(t->query_boundaries, t->query_boundaries + nq + 1);
+        ranker.configure(std::move(st));
+        if (!obj->inverse_max_dcg) ranker.derive_inverse_max_dcg(t->label);
+    }
+
+    // lambdarank gradients: the scores come to the host, the gradients are computed there (f64, every host thread)
+    // and go back; their maxima are taken on the device. Waits for the stream.
+    void ranking_gradients() {
+        h_rank_scores.alloc(rows);
+        h_rank_grad.alloc(rows);
+        h_rank_hess.alloc(rows);
+        hip_check(hipMemcpyAsync(h_rank_scores.p, train.scores.p, rows * 4, hipMemcpyDeviceToHost, stream), "read scores");
+        sync();
+        const unsigned threads = std::max(1u, std::min(64u, std::thread::hardware_concurrency()));
+        ranker.gradients(h_rank_scores.p, h_label_v.data(), has_weight ? h_weight_v.data() : nullptr, h_rank_grad.p,
+                         h_rank_hess.p, threads);
+        hip_check(hipMemcpyAsync(grad.p, h_rank_grad.p, rows * 4, hipMemcpyHostToDevice, stream), "upload grad");
+        hip_check(hipMemcpyAsync(hess.p, h_rank_hess.p, rows * 4, hipMemcpyHostToDevice, stream), "upload hess");
+        k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, scalars.p + 1);
+        launch_check("k_max_abs");
+    }
+
     void load(const srocm_dataset *t, const srocm_dataset *const *v, uint32_t nv, const srocm_objective *obj) {
         if (!t || !obj) fail(SROCM_ERR_DATA, "load needs a training set and an objective");
         if (t->num_rows > 0xFFFFFFFFull) fail(SROCM_ERR_UNSUPPORTED, std::to_string(t->num_rows) + " rows on one rank; the limit is 2^32 - 1");
         if (obj->kind == SROCM_OBJ_LAMBDARANK) {
-            // gradients arrive through srocm_set_gradients
+            load_ranking(t, obj);
         } else if (obj->kind != SROCM_OBJ_REGRESSION && obj->kind != SROCM_OBJ_BINARY) {
             fail(SROCM_ERR_CONFIG, "unknown objective");
         }
@@ -1340,10 +1391,10 @@ std::pair<double, double> Context::compute_gradients() {
 
 void Context::launch_gradients() {
     require_loaded();
-    if (objective != SROCM_OBJ_REGRESSION && objective != SROCM_OBJ_BINARY)
-        fail(SROCM_ERR_UNSUPPORTED, "this objective's gradients come through srocm_set_gradients");
     hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
-    if (rows) {
+    if (rows && objective == SROCM_OBJ_LAMBDARANK) {
+        ranking_gradients();
+    } else if (rows) {
         const float *w = has_weight ? weight.p : nullptr;
         if (objective == SROCM_OBJ_REGRESSION)
             k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, scalars.p + 1);
@@ -1677,7 +1728,6 @@ static void feature_mask(const std::vector<srocm_feature> &feats, double fractio
 // boosting.rs:227-324 train_one_iter / add, `count` times
 uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t count, srocm_grown_tree *trees) {
     require_loaded();
-    if (objective == SROCM_OBJ_LAMBDARANK) fail(SROCM_ERR_UNSUPPORTED, "lambdarank gradients stay on the host; drive the backend ops");
     bool constant_hessian = objective == SROCM_OBJ_REGRESSION && !has_weight;  // objective/mod.rs:84-89
     check_quant_units(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
     uint32_t done = 0;

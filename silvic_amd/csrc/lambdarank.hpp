@@ -1,0 +1,222 @@
+// lambdarank.hpp - LambdaRank-NDCG gradients on the host, in f64, as silvic's CPU backend computes them
+// (crates/silvic-core/src/objective/lambdarank.rs:190-420: LightGBM 3.3.5 `GetGradientsForOneQuery` with f64
+// accumulation, then the f32 store and the row weight).
+//
+// Per query: the rows are ranked by score, descending, ties by row (lambdarank.rs:142-170); every pair of ranks
+// (i, j) with i below the truncation level, j > i and different labels adds its lambda and hessian to both items,
+// i's row of pairs in j order after what the earlier rows added to i (lambdarank.rs:355-400); the sums are scaled by
+// log2(1 + s) / s of the query's lambda sum s when normalizing (lambdarank.rs:287-300). The pair probability comes
+// from LightGBM's 2^20-entry sigmoid table (lambdarank.rs:44-116) and the discounts 1 / log2(2 + rank) from its
+// 10,000-entry table (lambdarank.rs:30-43); both are built here with the C library's exp and log2, as the reference
+// builds them with Rust's f64::exp / f64::log2 on the same host. Queries run in parallel on host threads; a
+// query's result depends only on its own rows, so the thread count changes nothing.
+#pragma once
+
+#include <stdint.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <vector>
+
+namespace srocm_rank {
+
+constexpr size_t SIGMOID_BINS = size_t(1) << 20;    // lambdarank.rs:28
+constexpr double MIN_SIGMOID_INPUT = -50.0;          // lambdarank.rs:25
+constexpr size_t DISCOUNT_TABLE = 10000;             // lambdarank.rs:22 (kMaxPosition)
+constexpr double DISTANCE_EPSILON = static_cast<double>(0.01f);  // lambdarank.rs:31
+constexpr size_t QUERIES_PER_CLAIM = 16;             // queries a thread takes at a time
+
+struct Setup {
+    double sigmoid = 1.0;
+    bool norm = true;
+    uint32_t truncation_level = 30;
+    std::vector<double> label_gain;
+    std::vector<double> inverse_max_dcg;  // per query
+    std::vector<uint32_t> boundaries;     // num_queries + 1
+};
+
+// A key whose ascending order is the score's descending order; +0.0f folds -0 into 0 (equal under `>`).
+inline uint32_t rank_key(float score) {
+    float s = score + 0.0f;
+    uint32_t bits;
+    std::memcpy(&bits, &s, 4);
+    const uint32_t ascending = (bits >> 31) ? ~bits : (bits | 0x80000000u);
+    return ~ascending;
+}
+
+class Ranker {
+public:
+    void configure(Setup s) {
+        setup_ = std::move(s);
+        if (table_.empty() || table_sigmoid_ != setup_.sigmoid) build_table(setup_.sigmoid);
+        if (discount_.empty()) {
+            discount_.resize(DISCOUNT_TABLE);
+            for (size_t i = 0; i < DISCOUNT_TABLE; ++i) discount_[i] = 1.0 / std::log2(2.0 + static_cast<double>(i));
+        }
+    }
+
+    const Setup &setup() const { return setup_; }
+
+    // DCG of the best ordering of a query's labels, truncated at k (lambdarank.rs:119-139): the labels in
+    // descending order, each weighted by its rank's discount, summed in rank order.
+    double max_dcg_at_k(size_t k, const float *labels, size_t n) const {
+        std::vector<size_t> count(setup_.label_gain.size(), 0);
+        for (size_t i = 0; i < n; ++i) count[static_cast<size_t>(labels[i])] += 1;
+        size_t top = count.size() - 1;
+        double dcg = 0.0;
+        for (size_t j = 0; j < std::min(k, n); ++j) {
+            while (top > 0 && count[top] == 0) --top;
+            dcg += discount(j) * setup_.label_gain[top];
+            count[top] -= 1;
+        }
+        return dcg;
+    }
+
+    // objective/mod.rs:39-55: 1 / max DCG of each query at the truncation level, 0 for a query without gain
+    void derive_inverse_max_dcg(const float *label) {
+        const size_t nq = setup_.boundaries.size() - 1;
+        setup_.inverse_max_dcg.resize(nq);
+        for (size_t q = 0; q < nq; ++q) {
+            const size_t b = setup_.boundaries[q], e = setup_.boundaries[q + 1];
+            const double m = max_dcg_at_k(setup_.truncation_level, label + b, e - b);
+            setup_.inverse_max_dcg[q] = m > 0.0 ? 1.0 / m : 0.0;
+        }
+    }
+
+    // grad/hess of every row from scores, labels and optional weights.
+    void gradients(const float *scores, const float *label, const float *weight, float *grad, float *hess,
+                   unsigned threads) const {
+        const size_t nq = setup_.boundaries.empty() ? 0 : setup_.boundaries.size() - 1;
+        std::atomic<size_t> next{0};
+        auto work = [&]() {
+            Scratch sc;
+            for (;;) {
+                const size_t q0 = next.fetch_add(QUERIES_PER_CLAIM);
+                if (q0 >= nq) break;
+                const size_t q1 = std::min(nq, q0 + QUERIES_PER_CLAIM);
+                for (size_t q = q0; q < q1; ++q) one_query(q, scores, label, weight, grad, hess, sc);
+            }
+        };
+        threads = std::max(1u, threads);
+        std::vector<std::thread> pool;
+        for (unsigned t = 1; t < threads; ++t) pool.emplace_back(work);
+        work();
+        for (auto &t : pool) t.join();
+    }
+
+private:
+    struct Scratch {
+        std::vector<uint64_t> keys;
+        std::vector<uint32_t> row;      // local row of each rank
+        std::vector<double> score, gain, disc, lambda, hessian;
+        std::vector<float> lab;
+    };
+
+    Setup setup_;
+    std::vector<double> table_, discount_;
+    double table_sigmoid_ = 0.0, min_input_ = 0.0, max_input_ = 0.0, idx_factor_ = 0.0;
+
+    // LightGBM's sigmoid table: 1 / (1 + exp(sigmoid * x)) at the lower edge of each bin over [-50, 50] / sigmoid / 2
+    void build_table(double sigmoid) {
+        min_input_ = MIN_SIGMOID_INPUT / sigmoid / 2.0;
+        max_input_ = -min_input_;
+        idx_factor_ = static_cast<double>(SIGMOID_BINS) / (max_input_ - min_input_);
+        table_.resize(SIGMOID_BINS);
+        for (size_t i = 0; i < SIGMOID_BINS; ++i) {
+            const double x = static_cast<double>(i) / idx_factor_ + min_input_;
+            table_[i] = 1.0 / (1.0 + std::exp(x * sigmoid));
+        }
+        table_sigmoid_ = sigmoid;
+    }
+
+    double pair_probability(double delta) const {
+        if (delta <= min_input_) return table_[0];
+        if (delta >= max_input_) return table_[SIGMOID_BINS - 1];
+        const size_t at = static_cast<size_t>((delta - min_input_) * idx_factor_);
+        return table_[std::min(at, SIGMOID_BINS - 1)];
+    }
+
+    double discount(size_t rank) const {
+        return rank < DISCOUNT_TABLE ? discount_[rank] : 1.0 / std::log2(2.0 + static_cast<double>(rank));
+    }
+
+    void one_query(size_t q, const float *scores, const float *label, const float *weight, float *grad, float *hess,
+                   Scratch &sc) const {
+        const size_t b = setup_.boundaries[q], n = setup_.boundaries[q + 1] - b;
+        if (n == 0) return;
+        sc.keys.resize(n);
+        for (size_t r = 0; r < n; ++r) sc.keys[r] = (static_cast<uint64_t>(rank_key(scores[b + r])) << 32) | r;
+        std::sort(sc.keys.begin(), sc.keys.end());
+        sc.row.resize(n);
+        sc.score.resize(n);
+        sc.lab.resize(n);
+        sc.gain.resize(n);
+        sc.disc.resize(n);
+        sc.lambda.assign(n, 0.0);
+        sc.hessian.assign(n, 0.0);
+        for (size_t k = 0; k < n; ++k) {
+            const uint32_t r = static_cast<uint32_t>(sc.keys[k] & 0xffffffffu);
+            sc.row[k] = r;
+            sc.score[k] = static_cast<double>(scores[b + r]);
+            sc.lab[k] = label[b + r];
+            sc.gain[k] = setup_.label_gain[static_cast<size_t>(sc.lab[k])];
+            sc.disc[k] = discount(k);
+        }
+        // -inf scores rank last; the lowest score skips one trailing -inf (lambdarank.rs:333-340)
+        size_t valid = n;
+        for (size_t k = 0; k < n; ++k)
+            if (sc.score[k] == -std::numeric_limits<double>::infinity()) {
+                valid = k;
+                break;
+            }
+        size_t worst = n - 1;
+        if (worst > 0 && sc.score[worst] == -std::numeric_limits<double>::infinity()) --worst;
+        const double sigmoid = setup_.sigmoid, sigmoid2 = sigmoid * sigmoid;
+        const double inv_max_dcg = setup_.inverse_max_dcg[q];
+        const bool by_distance = setup_.norm && sc.score[0] != sc.score[worst];
+        const size_t rows_i = std::min<size_t>(setup_.truncation_level, valid > 0 ? valid - 1 : 0);
+        double sum_lambdas = 0.0;
+        for (size_t i = 0; i < rows_i; ++i) {
+            const double si = sc.score[i], gi = sc.gain[i], di = sc.disc[i];
+            const float li = sc.lab[i];
+            double lam_i = sc.lambda[i], hes_i = sc.hessian[i];
+            for (size_t j = i + 1; j < valid; ++j) {
+                if (sc.lab[j] == li) continue;
+                const double sign = li > sc.lab[j] ? 1.0 : -1.0;
+                const double delta_score = sign * (si - sc.score[j]);
+                const double dcg_gap = sign * (gi - sc.gain[j]);
+                const double paired_discount = std::fabs(di - sc.disc[j]);
+                double delta_ndcg = dcg_gap * paired_discount * inv_max_dcg;
+                if (by_distance) delta_ndcg /= DISTANCE_EPSILON + std::fabs(delta_score);
+                const double p = pair_probability(delta_score);
+                const double p_lambda = p * (-sigmoid * delta_ndcg);
+                const double p_hessian = p * (1.0 - p) * (sigmoid2 * delta_ndcg);
+                lam_i += sign * p_lambda;
+                sc.lambda[j] -= sign * p_lambda;
+                hes_i += p_hessian;
+                sc.hessian[j] += p_hessian;
+                sum_lambdas -= 2.0 * p_lambda;
+            }
+            sc.lambda[i] = lam_i;
+            sc.hessian[i] = hes_i;
+        }
+        const double factor = setup_.norm && sum_lambdas > 0.0 ? std::log2(1.0 + sum_lambdas) / sum_lambdas : 1.0;
+        for (size_t k = 0; k < n; ++k) {
+            const size_t row = b + sc.row[k];
+            float g = static_cast<float>(sc.lambda[k] * factor);
+            float h = static_cast<float>(sc.hessian[k] * factor);
+            if (weight) {
+                g *= weight[row];
+                h *= weight[row];
+            }
+            grad[row] = g;
+            hess[row] = h;
+        }
+    }
+};
+
+}  // namespace srocm_rank

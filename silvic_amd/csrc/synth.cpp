@@ -44,6 +44,7 @@ inline double normal(uint32_t seed, uint32_t stream, uint64_t row) {
 constexpr uint32_t NAN_STREAM = 1u << 20;
 constexpr uint32_t AUX_STREAM = 1u << 21;
 constexpr uint32_t LABEL_STREAM = 1u << 22;
+constexpr uint32_t QUERY_STREAM = 1u << 23;
 
 struct Workload {
     uint32_t config = 0;
@@ -60,7 +61,22 @@ struct Workload {
     std::vector<std::vector<uint8_t>> g_data;
     uint64_t total_bins = 0;
     std::vector<float> label;
+    std::vector<uint32_t> query_boundaries;  // config 3: num_queries + 1
 };
+
+// Config 3's queries: Zipf-like sizes, floor(10 * u^(-1 / 0.35)) clipped to [10, 200] (a mean of about 100 rows),
+// until the rows run out (the last query takes what is left).
+std::vector<uint32_t> query_boundaries(uint32_t seed, uint64_t rows) {
+    std::vector<uint32_t> b{0};
+    uint64_t at = 0;
+    for (uint64_t q = 0; at < rows; ++q) {
+        const double size = std::floor(10.0 * std::pow(unit(seed, QUERY_STREAM, q), -1.0 / 0.35));
+        const uint64_t n = std::min<uint64_t>(static_cast<uint64_t>(std::clamp(size, 10.0, 200.0)), rows - at);
+        at += n;
+        b.push_back(static_cast<uint32_t>(at));
+    }
+    return b;
+}
 
 // Raw value of feature j at row r (NaN for missing), per configuration.
 double value(const Workload &w, uint32_t j, uint64_t r) {
@@ -115,8 +131,8 @@ float label_of(const Workload &w, uint64_t r, const std::vector<double> &x) {
         double p = 1.0 / (1.0 + std::exp(-z));
         return unit(s, LABEL_STREAM, r) < p ? 1.0f : 0.0f;
     }
-    case 3: {  // relevance 0..4 from a noisy monotone function of 8 features
-        double z = 0.0;
+    case 3: {  // relevance 0..4 from a noisy monotone function of 8 features (4 normal, 4 exponential: mean 4)
+        double z = -4.0;
         for (uint32_t i = 0; i < 8; ++i) z += v(i * 3);
         z += normal(s, LABEL_STREAM, r);
         return static_cast<float>(std::clamp(std::floor(z * 0.6 + 2.0), 0.0, 4.0));
@@ -242,6 +258,7 @@ void *synth_create(uint32_t config, uint64_t rows, uint32_t cols, uint32_t seed,
     w->g_data.resize(w->g_features.size());
     for (size_t g = 0; g < w->g_data.size(); ++g) w->g_data[g].assign(rows * w->g_stride[g], 0);
     w->label.resize(rows);
+    if (config == 3) w->query_boundaries = query_boundaries(seed, rows);
     parallel(rows, [&](uint64_t b, uint64_t e) {
         std::vector<double> x(cols);
         for (uint64_t r = b; r < e; ++r) {
@@ -287,6 +304,12 @@ void synth_group(const void *h, uint32_t g, uint32_t *out4) {
 const uint32_t *synth_group_features(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_features[g].data(); }
 const uint8_t *synth_group_data(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_data[g].data(); }
 const float *synth_label(const void *h) { return static_cast<const Workload *>(h)->label.data(); }
+// Query boundaries (num_queries + 1 of them) for the ranking configuration; 0 queries otherwise.
+uint32_t synth_num_queries(const void *h) {
+    const Workload *w = static_cast<const Workload *>(h);
+    return w->query_boundaries.empty() ? 0u : static_cast<uint32_t>(w->query_boundaries.size() - 1);
+}
+const uint32_t *synth_query_boundaries(const void *h) { return static_cast<const Workload *>(h)->query_boundaries.data(); }
 // The upper bounds of feature j (count = num_bins - nan_bin).
 const double *synth_bounds(const void *h, uint32_t j) { return static_cast<const Workload *>(h)->bounds[j].data(); }
 

@@ -54,6 +54,7 @@ class BinnedDataset:
     label: np.ndarray
     weight: np.ndarray = None
     row_offset: int = 0
+    query_boundaries: np.ndarray = None  # ranking: num_queries + 1 row offsets
     _keep: list = field(default_factory=list, repr=False)
 
     def bin(self, feature, rows=None):
@@ -83,10 +84,15 @@ class BinnedDataset:
         if self.weight is not None:
             weight = np.ascontiguousarray(self.weight, dtype=np.float32)
             keep.append(weight)
+        qb, nq = None, 0
+        if self.query_boundaries is not None:
+            qarr = np.ascontiguousarray(self.query_boundaries, dtype=np.uint32)
+            keep.append(qarr)
+            qb, nq = qarr.ctypes.data_as(C.POINTER(C.c_uint32)), len(qarr) - 1
         ds = _abi.Dataset(
             self.num_rows, self.row_offset, len(self.features), len(self.groups), feats, groups, self.total_bins,
             label.ctypes.data_as(C.POINTER(C.c_float)),
-            weight.ctypes.data_as(C.POINTER(C.c_float)) if weight is not None else None, None, 0)
+            weight.ctypes.data_as(C.POINTER(C.c_float)) if weight is not None else None, qb, nq)
         self._keep = keep
         return ds
 
@@ -164,6 +170,7 @@ def as_categorical(data, features):
 
 def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=False):
     """Configuration ``config`` (1-5) as a binned dataset, generated natively; ``rows``/``cols`` shrink it.
+    Configuration 3 carries query boundaries (Zipf-like sizes in 10..200).
     ``categorical``: config 2's integer features (the last quarter) as categorical features (see as_categorical)."""
     lib = _abi.load_synth()
     drows, dcols, dbin, _ = CONFIGS[config]
@@ -195,9 +202,11 @@ def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=Fa
             groups.append(FeatureGroup([int(f) for f in fidx], stride, off, total, data))
         label = np.ctypeslib.as_array(lib.synth_label(h), shape=(rows,)).copy()
         total = int(lib.synth_total_bins(h))
+        nq = int(lib.synth_num_queries(h))
+        queries = np.ctypeslib.as_array(lib.synth_query_boundaries(h), shape=(nq + 1,)).copy() if nq else None
     finally:
         lib.synth_free(h)
-    data = BinnedDataset(rows, features, groups, total, label)
+    data = BinnedDataset(rows, features, groups, total, label, query_boundaries=queries)
     if categorical:
         if config != 2:
             raise ValueError("categorical features are defined for configuration 2")

@@ -35,6 +35,9 @@ DEFAULTS = {
     "min_data_per_group": 100,
     "boost_from_average": True,
     "sigmoid": 1.0,
+    "label_gain": None,
+    "lambdarank_truncation_level": 30,
+    "lambdarank_norm": True,
     "use_quantized_grad": True,
     "num_grad_quant_bins": 4,
     "quant_train_renew_leaf": True,
@@ -55,7 +58,7 @@ ALIASES = {
 }
 
 OBJECTIVES = {"regression": _abi.OBJ_REGRESSION, "l2": _abi.OBJ_REGRESSION, "regression_l2": _abi.OBJ_REGRESSION,
-              "mse": _abi.OBJ_REGRESSION, "binary": _abi.OBJ_BINARY}
+              "mse": _abi.OBJ_REGRESSION, "binary": _abi.OBJ_BINARY, "lambdarank": _abi.OBJ_LAMBDARANK}
 
 
 def resolve_params(params):
@@ -113,8 +116,10 @@ class Trainer:
         self.params = resolve_params(params)
         choose_device(self.params) if backend is None else None
         self.backend = backend or RocmBackend(int(self.params["gpu_device_id"]))
-        self.backend.load(train_set, objective=OBJECTIVES[self.params["objective"]],
-                          sigmoid=float(self.params["sigmoid"]))
+        p = self.params
+        self.backend.load(train_set, objective=OBJECTIVES[p["objective"]], sigmoid=float(p["sigmoid"]),
+                          norm=bool(p["lambdarank_norm"]), truncation_level=int(p["lambdarank_truncation_level"]),
+                          label_gain=p["label_gain"])
         self.tp = train_params(self.params)
         init = C.c_double()
         self.backend._check(self.backend._lib.srocm_boost_init(self.backend._h, C.byref(self.tp), C.byref(init)))

@@ -452,7 +452,8 @@ def boost_both(data, params, rounds):
 def params_to_lightgbm(params):
     out = dict(params)
     if "objective" in out:
-        out["objective"] = {_abi.OBJ_REGRESSION: "regression", _abi.OBJ_BINARY: "binary"}[out["objective"]]
+        out["objective"] = {_abi.OBJ_REGRESSION: "regression", _abi.OBJ_BINARY: "binary",
+                            _abi.OBJ_LAMBDARANK: "lambdarank"}[out["objective"]]
     return out
 
 
@@ -491,6 +492,64 @@ def test_boosting_matches_the_oracle(config, rows, cols, params, rounds):
     s = t.backend.scores(0)
     np.testing.assert_allclose(s, o.scores, rtol=1e-6, atol=1e-6)
     assert np.array_equal(s, o.scores), "scores are the same f32 adds"
+    t.backend.close()
+
+
+def test_headline_workload_at_full_size(rocm):
+    # config 2 as the bench runs it: 10M rows x 128 features, binary, 255 leaves, num_grad_quant_bins 4. The root
+    # histogram bit for bit, then three boosted trees and the scores identical to the oracle's
+    say("full size 10M x 128")
+    data = silvic_amd.synthetic(2)
+    assert (data.num_rows, len(data.features)) == (10_000_000, 128)
+    g, h = binary_gradients(data)
+    spec, packed = quantized_setup(rocm, data, g, h)
+    n = rocm.reset_partition()
+    root = rocm.histogram((0, n))
+    assert np.array_equal(root, oracle.histogram(data, packed, 4, np.arange(n, dtype=np.uint32)))
+    say("full size boost 3")
+    o, t = boost_both(data, dict(objective=_abi.OBJ_BINARY, num_leaves=255), 3)
+    assert len(t.trees) == len(o.trees) == 3
+    for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+        assert ot["num_leaves"] == 255
+        compare_trees(d, ot, f"tree {i}", exact_values=False)
+    assert np.array_equal(t.backend.scores(0), o.scores)
+    t.backend.close()
+
+
+# Config 3 (lambdarank, ndcg): queries of 10..200 documents, 136 features, labels 0..4. The gradients are computed
+# on the host in f64 (objective/lambdarank.rs), the trees on the device.
+def test_lambdarank_gradients_match_the_oracle():
+    say("lambdarank gradients 200k")
+    data = silvic_amd.synthetic(3, rows=200_000, seed=5)
+    p = oracle.default_params(objective=_abi.OBJ_LAMBDARANK)
+    t = silvic_amd.Trainer(dict(objective="lambdarank", num_leaves=31, device_type="rocm"), data)
+    try:
+        for step in range(3):  # tied scores (all 0: rank order by row), then the scores of 1 and 2 trees
+            scores = t.backend.scores(0)
+            mg, mh = t.backend.compute_gradients()
+            g, h = t.backend.gradients()
+            og, oh = oracle.lambdarank_gradients(data, p, scores)
+            assert np.array_equal(g, og) and np.array_equal(h, oh), step
+            assert mg == float(np.abs(og).max()) and mh == float(oh.max())
+            t.step(1)
+    finally:
+        t.backend.close()
+
+
+@pytest.mark.parametrize("rows,params,rounds", [
+    (200_000, dict(num_leaves=127), 6),
+    (120_000, dict(num_leaves=63, bagging_fraction=0.7, bagging_freq=1, lambdarank_truncation_level=10), 5),
+])
+def test_lambdarank_boosting_matches_the_oracle(rows, params, rounds):
+    say("boost lambdarank", rows, params, rounds)
+    data = silvic_amd.synthetic(3, rows=rows, seed=7)
+    params = dict(params, objective=_abi.OBJ_LAMBDARANK)
+    o, t = boost_both(data, params, rounds)
+    assert len(t.trees) == len(o.trees) == rounds
+    assert t.init_score == o.init_score == 0.0
+    for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+        compare_trees(d, ot, f"tree {i}", exact_values=False)
+    assert np.array_equal(t.backend.scores(0), o.scores)
     t.backend.close()
 
 
