@@ -112,12 +112,13 @@ class Booster:
 class Trainer:
     """A loaded device with the boosting state, so iterations can be run in steps (``step``)."""
 
-    def __init__(self, params, train_set, backend=None):
+    def __init__(self, params, train_set, backend=None, valid_sets=()):
         self.params = resolve_params(params)
         choose_device(self.params) if backend is None else None
         self.backend = backend or RocmBackend(int(self.params["gpu_device_id"]))
         p = self.params
-        self.backend.load(train_set, objective=OBJECTIVES[p["objective"]], sigmoid=float(p["sigmoid"]),
+        self.backend.load(train_set, valid=tuple(valid_sets), objective=OBJECTIVES[p["objective"]],
+                          sigmoid=float(p["sigmoid"]),
                           norm=bool(p["lambdarank_norm"]), truncation_level=int(p["lambdarank_truncation_level"]),
                           label_gain=p["label_gain"])
         self.tp = train_params(self.params)
@@ -147,10 +148,11 @@ class Trainer:
         return added
 
 
-def train(params, train_set, num_boost_round=100):
-    """Trains ``num_boost_round`` trees (``num_iterations`` in ``params`` wins, as LightGBM's alias rules)."""
+def train(params, train_set, num_boost_round=100, valid_sets=()):
+    """Trains ``num_boost_round`` trees (``num_iterations`` in ``params`` wins, as LightGBM's alias rules);
+    ``valid_sets`` (binned with the training set's layout) have their scores updated with every tree."""
     p = resolve_params(params)
     rounds = int(p.get("num_iterations", num_boost_round)) if "num_iterations" in (params or {}) else num_boost_round
-    t = Trainer(params, train_set)
+    t = Trainer(params, train_set, valid_sets=valid_sets)
     t.step(rounds)
     return Booster(t.trees, t.init_score, p)

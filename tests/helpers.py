@@ -122,3 +122,14 @@ def mirrored(half, feature):
             d[n:, c] = 1
         groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
     return BinnedDataset(2 * n, half.features, groups, half.total_bins, np.concatenate([half.label, half.label]))
+
+
+def row_slice(data, start, stop):
+    """Rows [start, stop) of ``data`` as a dataset with the same features, groups and bins (a validation set binned
+    with the training set's mappers, as silvic requires, cpu.rs:707-728)."""
+    groups = []
+    for g in data.groups:
+        d = g.data.reshape(data.num_rows, g.row_stride)[start:stop]
+        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
+    weight = None if data.weight is None else data.weight[start:stop].copy()
+    return BinnedDataset(stop - start, data.features, groups, data.total_bins, data.label[start:stop].copy(), weight)

@@ -5,13 +5,15 @@ arrays and leaf values must be identical; scores must agree within 1e-6 relative
 they match exactly in practice). Every test prints the case it runs before touching the GPU.
 """
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
 import oracle
 import silvic_amd
 from silvic_amd import _abi, bin_split, device_node
-from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients, mirrored
+from tests.helpers import cpu_dataset, cpu_gradients, learner_dataset, learner_gradients, mirrored, row_slice
 from tests.split_cases import categorical_cases, config, numerical_cases, quantized_cases, sums
 
 pytestmark = pytest.mark.gpu
@@ -551,6 +553,40 @@ def test_lambdarank_boosting_matches_the_oracle(rows, params, rounds):
         compare_trees(d, ot, f"tree {i}", exact_values=False)
     assert np.array_equal(t.backend.scores(0), o.scores)
     t.backend.close()
+
+
+# Validation sets (Backend::load's `valid`, cpu.rs:707-728; scores(1), cpu.rs:929): two sets binned with the
+# training set's layout; after boosting, their scores equal the oracle's trees replayed onto their rows with its
+# add_tree (cpu.rs:605-695), the initial score first and the first tree's values without it (replay.rs:38-40).
+@pytest.mark.parametrize("objective,renew", [(_abi.OBJ_BINARY, 1), (_abi.OBJ_REGRESSION, 0)])
+def test_validation_scores_match_the_oracle(objective, renew):
+    say("validation sets", objective, renew)
+    full = silvic_amd.synthetic(2 if objective == _abi.OBJ_BINARY else 1, rows=160_000, cols=40, seed=17)
+    train, valid1, valid2 = row_slice(full, 0, 100_000), row_slice(full, 100_000, 140_000), row_slice(full, 140_000, 160_000)
+    params = dict(objective=objective, num_leaves=63, quant_train_renew_leaf=renew)
+    rounds = 6
+    o = oracle.train(train, oracle.default_params(num_iterations=rounds, **params))
+    t = silvic_amd.Trainer(dict(params_to_lightgbm(params), num_iterations=rounds, device_type="rocm"), train,
+                           valid_sets=[valid1, valid2])
+    try:
+        t.step(rounds)
+        assert len(t.trees) == len(o.trees) == rounds
+        for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+            compare_trees(d, ot, f"tree {i}", exact_values=False)
+        assert np.array_equal(t.backend.scores(0), o.scores)
+        for k, valid in ((1, valid1), (2, valid2)):
+            vs = np.full(valid.num_rows, np.float32(o.init_score), np.float32)
+            for i, tr in enumerate(o.trees):
+                assert tr["num_leaves"] > 1
+                nodes = [device_node(_abi.BinSplit(full.features[f].group, full.features[f].column,
+                                                   (C.c_uint32 * 8)(*[int(w) for w in tr["left_bins"][n]])),
+                                     int(tr["left_child"][n]), int(tr["right_child"][n]))
+                         for n, f in enumerate(tr["split_feature"])]
+                lv = tr["leaf_value"] - (o.init_score if i == 0 else 0.0)
+                vs = oracle.add_tree(valid, nodes, lv.astype(np.float32), vs)
+            assert np.array_equal(t.backend.scores(k), vs), k
+    finally:
+        t.backend.close()
 
 
 def test_quantized_units_beyond_the_workgroup_sums_are_rejected(rocm):
