@@ -916,31 +916,6 @@ __device__ __forceinline__ void scan_add_step(double &g, double &h, int64_t &c) 
     c += static_cast<int64_t>(dpp_u64<CTRL, ROW_MASK>(static_cast<uint64_t>(c)));
 }
 
-// A run of candidates in scan order: whether it holds the stopping candidate, and its best candidate before
-// the stop (highest gain, the first on ties; -1 when none). A run combines with the run after it: that run
-// counts only when no stop came before it.
-struct ScanRun {
-    uint32_t stopped;
-    double gain;
-    int32_t k;
-};
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void scan_run_step(ScanRun &r, uint32_t lane) {
-    ScanRun a;
-    a.stopped = dpp_u32<CTRL, ROW_MASK>(r.stopped);
-    a.gain = double_of(dpp_u64<CTRL, ROW_MASK>(bits_of(r.gain)));
-    a.k = static_cast<int32_t>(dpp_u32<CTRL, ROW_MASK>(static_cast<uint32_t>(r.k)));
-    if (!dpp_has_source<CTRL, ROW_MASK>(lane)) return;
-    // a precedes r
-    if (a.stopped) {
-        r = a;
-    } else if (!(r.k >= 0 && (a.k < 0 || r.gain > a.gain))) {
-        r.gain = a.gain;
-        r.k = a.k;
-    }
-}
-
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t lane) {
     uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), lane));
     uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), lane));
@@ -1076,122 +1051,6 @@ __device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t ow
 }
 
 
-// One scan direction over `n` bins of a feature's histogram slice `h` (i64 {g,h} pairs): element k is bin
-// t0 + step * k. Lane l holds elements 4l..4l+3. Returns whether a candidate beat min_gain_shift.
-// split.rs:420-462: candidates run until the first one where the other side is too small while the growing side
-// is not (excluded); each has the gain of its two sides, -inf when the growing side is too small; the best is
-// the first maximum (split.rs:508-531); all of it as one ordered wave scan.
-__device__ bool wave_scan(const Ctx &c, const SplitCfgDev &cfg, const int64_t *h, int t0, int step, int n, Grown &out) {
-    const uint32_t lane = threadIdx.x & 63u;
-    double pg[4], ph[4];
-    int64_t pc[4];
-    double lg = 0.0, lh = 0.0;
-    int64_t lc = 0;
-    double gu[4], hu[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int k = 4 * static_cast<int>(lane) + j;
-        int t = t0 + step * (k < n ? k : 0);
-        gu[j] = k < n ? static_cast<double>(h[2 * t]) : 0.0;
-        hu[j] = k < n ? static_cast<double>(h[2 * t + 1]) : 0.0;
-    }
-    // per-bin counts (split.rs:196-198, 236-238): `(x + 0.5) as i64`; one conversion when the wave's are all in u32
-    double xc[4];
-    bool small = true;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int k = 4 * static_cast<int>(lane) + j;
-        xc[j] = k < n ? hu[j] * c.scale_hess * c.cnt_factor + 0.5 : 0.0;
-        small = small && xc[j] >= 0.0 && xc[j] < 4294967296.0;
-    }
-    int64_t cis[4];
-    if (__all(small)) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) cis[j] = static_cast<int64_t>(static_cast<uint32_t>(xc[j]));
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) cis[j] = sat_i64(xc[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int64_t ci = cis[j];
-        lg += gu[j];
-        lh += hu[j];
-        lc += ci;
-        pg[j] = lg;
-        ph[j] = lh;
-        pc[j] = lc;
-    }
-    // exclusive prefix of the lane totals over the wave (exact: integer-valued)
-    double eg = lg, eh = lh;
-    int64_t ec = lc;
-    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
-    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
-    eg -= lg;
-    eh -= lh;
-    ec -= lc;
-    const int64_t min_count = cfg.min_data_in_leaf > 1 ? cfg.min_data_in_leaf : 1;
-    const double min_hess = cfg.min_sum_hessian_in_leaf;
-    ScanRun run = {0u, -__builtin_inf(), -1};
-    double gains[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int k = 4 * static_cast<int>(lane) + j;
-        pg[j] += eg;
-        ph[j] += eh;
-        pc[j] += ec;
-        gains[j] = -__builtin_inf();
-        if (k < n && !run.stopped) {
-            double hh = K_EPSILON + ph[j] * c.scale_hess;
-            bool skip = pc[j] < min_count || hh < min_hess || ph[j] <= 0.0;
-            bool other_small = c.num_data - pc[j] < min_count || c.sum_hess - hh < min_hess || c.units_hess - ph[j] <= 0.0;
-            if (other_small && !skip) {
-                run.stopped = 1u;
-            } else {
-                double gg = pg[j] * c.scale_grad;
-                double gain = leaf_gain(c.sum_grad - gg, c.sum_hess - hh, cfg.lambda_l1, cfg.lambda_l2) +
-                              leaf_gain(gg, hh, cfg.lambda_l1, cfg.lambda_l2);
-                gains[j] = (skip || gain != gain) ? -__builtin_inf() : gain;  // NaN never wins (split.rs:508-531)
-                if (run.k < 0 || gains[j] > run.gain) {
-                    run.gain = gains[j];
-                    run.k = k;
-                }
-            }
-        }
-    }
-    scan_run_step<DPP_ROW_SHR1, 0xf>(run, lane);
-    scan_run_step<DPP_ROW_SHR2, 0xf>(run, lane);
-    scan_run_step<DPP_ROW_SHR4, 0xf>(run, lane);
-    scan_run_step<DPP_ROW_SHR8, 0xf>(run, lane);
-    scan_run_step<DPP_ROW_BCAST15, 0xa>(run, lane);
-    scan_run_step<DPP_ROW_BCAST31, 0xc>(run, lane);
-    const int32_t first = __builtin_amdgcn_readlane(run.k, 63);
-    const double best = double_of(readlane_u64(bits_of(run.gain), 63));
-    // NaN gains never become the best; an all -inf run fails here as in the reference's comparison
-    if (first < 0 || !(best > c.min_gain_shift)) return false;
-    const uint32_t owner = static_cast<uint32_t>(first) >> 2;
-    const int jj = first & 3;
-    double og = 0.0, oh = 0.0;
-    int64_t oc = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (j == jj) {
-            og = pg[j];
-            oh = ph[j];
-            oc = pc[j];
-        }
-    out.ug = double_of(readlane_u64(bits_of(og), owner));
-    out.uh = double_of(readlane_u64(bits_of(oh), owner));
-    out.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
-    out.gain = best;
-    out.bin = static_cast<uint32_t>(t0 + step * first);
-    return true;
-}
-
 struct FeatDev {
     uint32_t num_bins, hist_offset, kind, nan_bin;
     uint32_t col;  // column-major index among the non-trivial features
@@ -1204,24 +1063,210 @@ struct ScanJob {
     FeatCand *out;        // [num_features]
 };
 
-// split.rs:584-620 find_numerical, in two parts so that a feature's two scan directions can run on two waves.
-// Direction 0 is the reverse scan (split.rs:557-567: missing values go left); direction 1, only for a feature with
-// a NaN bin and more than two bins, the forward scan over the bins before the NaN bin (split.rs:571-580).
+// split.rs:584-620 find_numerical: the reverse scan (split.rs:557-567: missing values go left) always; the forward
+// scan over the bins before the NaN bin (split.rs:571-580) only for a feature with a NaN bin and more than two bins.
 __device__ __forceinline__ bool scan_searched(const Ctx &c, const FeatDev &m, bool evaluate) {
     return c.valid && evaluate && m.num_bins >= 2 && (m.kind == 1 || m.kind == 2);
 }
 __device__ __forceinline__ bool scan_two_way(const FeatDev &m) { return m.nan_bin && m.num_bins > 2; }
 
-// One direction's scan of a searched feature (wave-wide). Returns whether it found a candidate.
-__device__ __forceinline__ bool scan_direction(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist,
-                                               int dir, Grown &out) {
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_max_i32_step(int v) {
+    const int o = __builtin_amdgcn_update_dpp(static_cast<int>(0x80000000u), v, CTRL, ROW_MASK, 0xf, false);
+    return o > v ? o : v;
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = dpp_max_i32_step<DPP_ROW_SHR1, 0xf>(v);
+    v = dpp_max_i32_step<DPP_ROW_SHR2, 0xf>(v);
+    v = dpp_max_i32_step<DPP_ROW_SHR4, 0xf>(v);
+    v = dpp_max_i32_step<DPP_ROW_SHR8, 0xf>(v);
+    v = dpp_max_i32_step<DPP_ROW_BCAST15, 0xa>(v);
+    v = dpp_max_i32_step<DPP_ROW_BCAST31, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// One candidate of a scan (split.rs:420-462): the accumulated side's exact units and rows; returns its gain, -inf
+// when the candidate is skipped (that side too small) or NaN (split.rs:508-531), and sets `stop` when the other side
+// is too small while this one is not (the reference's `break`).
+__device__ __forceinline__ double candidate_gain(const Ctx &c, const SplitCfgDev &cfg, double ug, double uh, int64_t cnt,
+                                                int64_t min_count, bool &stop) {
+    const double hh = K_EPSILON + uh * c.scale_hess;
+    const bool skip = cnt < min_count || hh < cfg.min_sum_hessian_in_leaf || uh <= 0.0;
+    const bool other_small = c.num_data - cnt < min_count || c.sum_hess - hh < cfg.min_sum_hessian_in_leaf ||
+                             c.units_hess - uh <= 0.0;
+    stop = other_small && !skip;
+    const double gg = ug * c.scale_grad;
+    const double gain = leaf_gain(c.sum_grad - gg, c.sum_hess - hh, cfg.lambda_l1, cfg.lambda_l2) +
+                        leaf_gain(gg, hh, cfg.lambda_l1, cfg.lambda_l2);
+    return (skip || gain != gain) ? -__builtin_inf() : gain;
+}
+
+// Both scan directions of a numerical feature (split.rs:555-620) from one pass over its bins, wave-wide. Lane l
+// holds bins 4l .. 4l + 3 in natural order; the scanned bins are 0 .. top, top being the last bin before the NaN bin
+// when the feature scans both ways and the last bin otherwise. Every accumulated side is a sum of exact integers
+// (histogram units, per-bin counts rounded as split.rs:196-198), so the reverse scan's right side from bin b up is
+// the total minus the prefix below b, the same values the reference's running sums reach.
+// - Reverse (missing values go left): visits b = top .. 1; stops at the first b, in that order the highest, where
+//   the other side is too small while the accumulated one is not; keeps the first maximum in its order, so the
+//   highest b on equal gains. Threshold b - 1.
+// - Forward (missing values go right; two-way features only): visits b = 0 .. top; stops at the lowest such b;
+//   keeps the lowest b on equal gains. Threshold b.
+__device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool &rf,
+                               Grown &rg, bool &ff, Grown &fg) {
+    const int lane = static_cast<int>(threadIdx.x & 63u);
     const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
     const int nb = static_cast<int>(m.num_bins);
-    if (scan_two_way(m)) {
-        const int last = nb - 2;
-        return dir == 0 ? wave_scan(c, cfg, h, last, -1, last, out) : wave_scan(c, cfg, h, 0, 1, last + 1, out);
+    const bool two = scan_two_way(m);
+    const int top = two ? nb - 2 : nb - 1;
+    double gu[4], hu[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int b = 4 * lane + j;
+        const int t = b <= top ? b : 0;
+        gu[j] = b <= top ? static_cast<double>(h[2 * t]) : 0.0;
+        hu[j] = b <= top ? static_cast<double>(h[2 * t + 1]) : 0.0;
     }
-    return dir == 0 ? wave_scan(c, cfg, h, nb - 1, -1, nb - 1, out) : false;
+    // per-bin counts: `(x + 0.5) as i64`, one conversion when the wave's are all in u32
+    double xc[4];
+    bool small = true;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        xc[j] = 4 * lane + j <= top ? hu[j] * c.scale_hess * c.cnt_factor + 0.5 : 0.0;
+        small = small && xc[j] >= 0.0 && xc[j] < 4294967296.0;
+    }
+    int64_t ci[4];
+    if (__all(small)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ci[j] = static_cast<int64_t>(static_cast<uint32_t>(xc[j]));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ci[j] = sat_i64(xc[j]);
+    }
+    // inclusive prefix P(b) over bins 0 .. top
+    double pg[4], ph[4];
+    int64_t pc[4];
+    double lg = 0.0, lh = 0.0;
+    int64_t lc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lg += gu[j];
+        lh += hu[j];
+        lc += ci[j];
+        pg[j] = lg;
+        ph[j] = lh;
+        pc[j] = lc;
+    }
+    double eg = lg, eh = lh;
+    int64_t ec = lc;
+    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
+    const double tg = readlane_f64(eg, 63), th = readlane_f64(eh, 63);
+    const int64_t tc = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(ec), 63));
+    eg -= lg;
+    eh -= lh;
+    ec -= lc;
+    const int64_t min_count = cfg.min_data_in_leaf > 1 ? cfg.min_data_in_leaf : 1;
+    double rgu[4], rhu[4], grv[4], gfv[4];
+    int64_t rcu[4];
+    int stop_r = -1, stop_f = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int b = 4 * lane + j;
+        pg[j] += eg;
+        ph[j] += eh;
+        pc[j] += ec;
+        // reverse: the right side from bin b up
+        rgu[j] = tg - (pg[j] - gu[j]);
+        rhu[j] = th - (ph[j] - hu[j]);
+        rcu[j] = tc - (pc[j] - ci[j]);
+        grv[j] = -__builtin_inf();
+        gfv[j] = -__builtin_inf();
+        if (b <= top) {
+            bool stop = false;
+            if (b >= 1) {
+                grv[j] = candidate_gain(c, cfg, rgu[j], rhu[j], rcu[j], min_count, stop);
+                if (stop) stop_r = b;  // b grows with j: the lane's highest
+            }
+            if (two) {
+                gfv[j] = candidate_gain(c, cfg, pg[j], ph[j], pc[j], min_count, stop);
+                if (stop && stop_f == 0x7fffffff) stop_f = b;  // the lane's lowest
+            }
+        }
+    }
+    rf = false;
+    ff = false;
+    {  // reverse: candidates above the highest stop, the highest b among equal gains
+        const int lo = wave_max_i32(stop_r) + 1;  // >= 0
+        double bg = -__builtin_inf();
+        int bb = -1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * lane + j;
+            if (b >= 1 && b >= lo && b <= top && (bb < 0 || grv[j] >= bg)) {
+                bg = grv[j];
+                bb = b;
+            }
+        }
+        const double best = wave_max_f64(bb >= 0 ? bg : -__builtin_inf());
+        const int first = wave_max_i32(bb >= 0 && bg == best ? bb : -1);
+        if (first >= 0 && best > c.min_gain_shift) {
+            const uint32_t owner = static_cast<uint32_t>(first) >> 2;
+            const int jj = first & 3;
+            double og = 0.0, oh = 0.0;
+            int64_t oc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j == jj) {
+                    og = rgu[j];
+                    oh = rhu[j];
+                    oc = rcu[j];
+                }
+            rg.ug = readlane_f64(og, owner);
+            rg.uh = readlane_f64(oh, owner);
+            rg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
+            rg.gain = best;
+            rg.bin = static_cast<uint32_t>(first);
+            rf = true;
+        }
+    }
+    if (two) {  // forward: candidates below the lowest stop, the lowest b among equal gains
+        const int hi = wave_min_i32(stop_f);
+        double bg = -__builtin_inf();
+        int bb = -1;
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+            const int b = 4 * lane + j;
+            if (b < hi && b <= top && (bb < 0 || gfv[j] >= bg)) {
+                bg = gfv[j];
+                bb = b;
+            }
+        }
+        const double best = wave_max_f64(bb >= 0 ? bg : -__builtin_inf());
+        const int first = wave_min_i32(bb >= 0 && bg == best ? bb : 0x7fffffff);
+        if (first != 0x7fffffff && best > c.min_gain_shift) {
+            const uint32_t owner = static_cast<uint32_t>(first) >> 2;
+            const int jj = first & 3;
+            double og = 0.0, oh = 0.0;
+            int64_t oc = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j == jj) {
+                    og = pg[j];
+                    oh = ph[j];
+                    oc = pc[j];
+                }
+            fg.ug = readlane_f64(og, owner);
+            fg.uh = readlane_f64(oh, owner);
+            fg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
+            fg.gain = best;
+            fg.bin = static_cast<uint32_t>(first);
+            ff = true;
+        }
+    }
 }
 
 // The feature's candidate from its scans' results (rf/rg reverse, ff/fg forward).
@@ -1564,8 +1609,8 @@ __device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const Fea
     if (!scan_searched(c, m, evaluate)) return FeatCand{};
     if (m.kind == 2) return categorical_candidate(c, cfg, m, hist, sc, order_out);
     Grown rg = {}, fg = {};
-    bool rf = scan_direction(c, cfg, m, hist, 0, rg);
-    bool ff = scan_two_way(m) ? scan_direction(c, cfg, m, hist, 1, fg) : false;
+    bool rf, ff;
+    scan_numerical(c, cfg, m, hist, rf, rg, ff, fg);
     return feature_candidate(c, m, rf, rg, ff, fg);
 }
 
@@ -3402,8 +3447,8 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
         FeatCand r = {};
         if (scan_searched(c, sm, sev)) {
             Grown rg = {}, fg = {};
-            const bool rf = scan_direction(c, g.cfg, sm, hist, 0, rg);
-            const bool ff = scan_two_way(sm) && scan_direction(c, g.cfg, sm, hist, 1, fg);
+            bool rf, ff;
+            scan_numerical(c, g.cfg, sm, hist, rf, rg, ff, fg);
             r = feature_candidate(c, sm, rf, rg, ff, fg);
         }
         if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
