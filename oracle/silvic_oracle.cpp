@@ -537,6 +537,7 @@ constexpr uint64_t ROW_CHUNK = 8192;         // cpu.rs:42
 // cpu.rs:46-99 GroupLayout
 struct GroupLayout {
     size_t group = 0, stride = 0, hist_offset = 0, bins = 0;
+    size_t bin_bytes = 1;  // 2: u16 bins (the extension for more than 256 bins; no counterpart in cpu.rs)
     std::vector<int64_t> column_features;  // -1: no feature
     std::vector<size_t> offsets;
     std::vector<std::pair<uint32_t, uint32_t>> runs;
@@ -585,6 +586,7 @@ std::vector<GroupLayout> group_layout(const srocm_dataset *d) {
         L.bins = g.total_bins;
         L.stride = g.row_stride;
         L.hist_offset = g.hist_offset;
+        L.bin_bytes = g.bin_bytes == 2 ? 2 : 1;
         size_t width = 0;
         for (uint32_t k = 0; k < g.num_features; ++k)
             width = std::max<size_t>(width, d->features[g.features[k]].column + 1);
@@ -594,8 +596,11 @@ std::vector<GroupLayout> group_layout(const srocm_dataset *d) {
             uint32_t f = g.features[k];
             const srocm_feature &m = d->features[f];
             if (m.hist_offset < g.hist_offset || m.hist_offset - g.hist_offset + m.num_bins > L.bins ||
-                m.column >= L.stride)
+                m.column + L.bin_bytes > L.stride)
                 throw std::runtime_error("feature lies outside its group's bins or row");
+            if (L.bin_bytes == 2 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
+                throw std::runtime_error("a 2-byte group holds numerical features of at most 1024 bins");
+            if (L.bin_bytes == 1 && m.num_bins > 256) throw std::runtime_error("a feature of more than 256 byte bins");
             L.column_features[m.column] = f;
             L.offsets[m.column] = m.hist_offset - g.hist_offset;
         }
@@ -612,9 +617,31 @@ size_t block_rows(size_t rows, const GroupLayout &g) {
     return std::max<size_t>(std::max(min_rows, (rows + MAX_BLOCKS_PER_GROUP - 1) / MAX_BLOCKS_PER_GROUP), 1);
 }
 
-// cpu.rs:307-314 add_run, cpu.rs:277-304 accumulate_rows (prefetching left to the hardware)
+// The u16 bin at byte offset `column` of a row (2-byte groups).
+inline uint32_t bin16(const uint8_t *row, size_t column) {
+    return static_cast<uint32_t>(row[column]) | (static_cast<uint32_t>(row[column + 1]) << 8);
+}
+
+// The bin of a row's feature at byte offset `column` of a group with `bin_bytes`.
+inline uint32_t bin_at(const srocm_group &g, size_t row, size_t column) {
+    const uint8_t *r = g.data + row * g.row_stride;
+    return g.bin_bytes == 2 ? bin16(r, column) : r[column];
+}
+
+// cpu.rs:307-314 add_run, cpu.rs:277-304 accumulate_rows (prefetching left to the hardware). A 2-byte group adds
+// its features' u16 bins; every add is an exact integer one, so the order of the adds changes nothing.
 inline void accumulate(const GroupLayout &g, const uint8_t *data, const uint32_t *rows, const int64_t *values,
                        size_t n, int64_t *acc) {
+    if (g.bin_bytes == 2) {
+        for (size_t i = 0; i < n; ++i) {
+            const uint8_t *row = data + static_cast<size_t>(rows[i]) * g.stride;
+            int64_t v = values[i];
+            for (const auto &run : g.runs)
+                for (uint32_t c = run.first; c < run.second; ++c)
+                    if (g.column_features[c] >= 0) acc[g.offsets[c] + bin16(row, c)] += v;
+        }
+        return;
+    }
     size_t width = g.runs.empty() ? 0 : g.runs.back().second;
     for (size_t i = 0; i < n; ++i) {
         const uint8_t *bins = data + static_cast<size_t>(rows[i]) * g.stride;
@@ -729,7 +756,12 @@ uint32_t stable_partition(uint32_t *rows, size_t n, const std::function<bool(uin
     return static_cast<uint32_t>(total_left);
 }
 
-inline bool goes_left(const srocm_bin_split &s, uint8_t bin) { return (s.left_bins[bin / 32] >> (bin % 32)) & 1u; }
+// BinSplit::goes_left (backend/mod.rs:34-37); a split on a 2-byte group's feature carries a numerical rule in its
+// words (threshold, NaN bin + 1 when missing values go left), since a mask of up to 1024 bins does not fit.
+inline bool goes_left(const srocm_bin_split &s, uint32_t bin, bool wide) {
+    if (wide) return bin <= s.left_bins[0] || (s.left_bins[1] != 0 && bin == s.left_bins[1] - 1);
+    return (s.left_bins[bin / 32] >> (bin % 32)) & 1u;
+}
 
 // cpu.rs:666-695 add_tree_to (a plain walk: the reference's branch-free walk visits the same nodes)
 void add_tree_to(const srocm_dataset *d, const srocm_device_node *nodes, uint32_t num_nodes,
@@ -757,8 +789,7 @@ void add_tree_to(const srocm_dataset *d, const srocm_device_node *nodes, uint32_
             while (node >= 0) {
                 const srocm_device_node &nd = nodes[node];
                 const srocm_group &g = d->groups[nd.split.group];
-                uint8_t bin = g.data[row * g.row_stride + nd.split.column];
-                node = goes_left(nd.split, bin) ? nd.left : nd.right;
+                node = goes_left(nd.split, bin_at(g, row, nd.split.column), g.bin_bytes == 2) ? nd.left : nd.right;
             }
             scores[row] += leaf_values[~node];
         }
@@ -770,7 +801,7 @@ void add_tree_to(const srocm_dataset *d, const srocm_device_node *nodes, uint32_
 // ---------------------------------------------------------------------------------------------------------
 
 constexpr double MIN_SCORE = -std::numeric_limits<double>::infinity();  // split.rs:39
-constexpr size_t MAX_BINS = 256;                                         // split.rs:43
+constexpr size_t MAX_BINS = 1024;  // split.rs:43 has 256, silvic's largest feature; 2-byte features take 1024
 
 // split.rs:145-154
 inline double sign_of(double x) { return static_cast<double>(static_cast<int>(x > 0.0) - static_cast<int>(x < 0.0)); }
@@ -1443,7 +1474,7 @@ struct CpuBackend {
         if (static_cast<uint64_t>(leaf.begin) + leaf.count > partition.size()) throw std::runtime_error("leaf outside the partition");
         const srocm_group &g = data->groups[s.group];
         return stable_partition(partition.data() + leaf.begin, leaf.count,
-                                [&](uint32_t row) { return goes_left(s, g.data[static_cast<size_t>(row) * g.row_stride + s.column]); });
+                                [&](uint32_t row) { return goes_left(s, bin_at(g, row, s.column), g.bin_bytes == 2); });
     }
     void leaf_sums(const std::vector<srocm_leaf_range> &leaves, float gs, float hs, std::vector<int64_t> &out) {
         Timer t(&times[T_SUMS]);
@@ -1521,7 +1552,10 @@ struct Learner {
     srocm_bin_split bin_split(const srocm_feature &m, const oracle_split_info &info) const {
         srocm_bin_split s{};
         auto set = [&](uint32_t bin) { s.left_bins[bin / 32] |= 1u << (bin % 32); };
-        if (!info.categorical) {
+        if (data->groups[m.group].bin_bytes == 2) {  // the numerical rule of a 2-byte feature, as goes_left reads it
+            s.left_bins[0] = info.threshold;
+            s.left_bins[1] = info.default_left && m.nan_bin ? m.num_bins : 0u;
+        } else if (!info.categorical) {
             for (uint32_t b = 0; b <= info.threshold; ++b) set(b);
             if (info.default_left && m.kind == SROCM_BINS_NUMERICAL && m.nan_bin) set(m.num_bins - 1);
         } else {
@@ -1850,7 +1884,7 @@ void oracle_histogram(const srocm_dataset *data, const int32_t *packed, int64_t 
 uint32_t oracle_partition(const srocm_dataset *data, uint32_t *rows, uint64_t count, const srocm_bin_split *split) {
     const srocm_group &g = data->groups[split->group];
     return stable_partition(rows, count, [&](uint32_t row) {
-        return goes_left(*split, g.data[static_cast<size_t>(row) * g.row_stride + split->column]);
+        return goes_left(*split, bin_at(g, row, split->column), g.bin_bytes == 2);
     });
 }
 

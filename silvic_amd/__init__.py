@@ -9,9 +9,9 @@ command (``python -m silvic_amd.build``); nothing falls back to a CPU path.
 """
 
 from ._abi import DeviceError, SilvicError
-from .backend import RocmBackend, bin_split, device_node
+from .backend import RocmBackend, bin_split, device_node, wide_bin_split
 from .dataset import BinnedDataset, FeatureGroup, FeatureMeta, from_bins, synthetic
 from .engine import Booster, Trainer, train
 
 __all__ = ["BinnedDataset", "Booster", "DeviceError", "FeatureGroup", "FeatureMeta", "RocmBackend", "SilvicError",
-           "Trainer", "bin_split", "device_node", "from_bins", "synthetic", "train"]
+           "Trainer", "bin_split", "device_node", "from_bins", "synthetic", "train", "wide_bin_split"]

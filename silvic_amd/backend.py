@@ -241,5 +241,12 @@ def bin_split(group, column, left_bins):
     return BinSplit(group, column, (C.c_uint32 * 8)(*words))
 
 
+def wide_bin_split(group, column, threshold, nan_bin=None):
+    """A ``BinSplit`` on a feature of two-byte bins: bins up to ``threshold`` go left, and the NaN bin ``nan_bin``
+    too when given (words 0 and 1 hold the rule; a bit set cannot hold 1024 bins)."""
+    words = [threshold, 0 if nan_bin is None else nan_bin + 1] + [0] * 6
+    return BinSplit(group, column, (C.c_uint32 * 8)(*words))
+
+
 def device_node(split, left, right):
     return DeviceNode(split, left, right)

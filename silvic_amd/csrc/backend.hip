@@ -265,16 +265,29 @@ constexpr uint32_t HIST_MIN_ROWS = 2048;   // rows per histogram workgroup befor
 constexpr uint64_t ROW_BLOCK = 256;
 
 struct Slab {
-    uint32_t width = 0;
-    std::vector<uint32_t> feats;  // feature ids
-    DevBuf<uint8_t> bins;         // [rows][width]
-    DevBuf<uint32_t> col_offset, col_bins;
+    uint32_t width = 0;            // W: LDS and partial columns
+    bool wide = false;             // two-byte bins: W / 4 features, each 4 virtual columns (k_hist<W, true>)
+    std::vector<uint32_t> feats;   // feature ids
+    DevBuf<uint8_t> bins;          // [rows][row_bytes()]
+    DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per virtual column
+    uint32_t row_bytes() const { return wide ? width / 2 : width; }
+    uint32_t capacity() const { return wide ? width / 4 : width; }
     uint64_t step_partial_off = 0;  // the slab's partials in the step partial buffer, in {g, h} pairs
+};
+
+// Where k_repack writes one feature's bins.
+struct RepackTo {
+    uint8_t *col;        // its column-major bins
+    uint32_t col16;      // two bytes per bin there
+    uint8_t *slab;       // its slab's rows (nullptr: none)
+    uint32_t row_bytes;  // bytes per slab row
+    uint32_t slab_wide;  // two bytes per bin in the slab row
+    uint32_t slab_col;   // its feature index in the slab
 };
 
 struct DevData {
     uint64_t rows = 0;
-    DevBuf<uint8_t> col;  // [nt feature][rows]
+    DevBuf<uint8_t> col;  // [nt feature][rows], one byte per bin, or two (Context::col16)
     DevBuf<float> scores;
 };
 
@@ -323,6 +336,10 @@ struct Context {
     std::vector<Slab> slabs;
     uint64_t rows = 0, row_offset = 0;
     uint32_t max_width = 32;
+    uint32_t col16 = 0;                     // some group has two-byte bins: column-major bins are u16
+    bool has_narrow = true, has_wide = false;  // features of one-byte / two-byte bins (a scan kernel each)
+    std::vector<uint32_t> group_bin_bytes;  // per group: 1 or 2
+    std::vector<uint32_t> nt_slab, nt_slab_col;  // per non-trivial feature: its slab and column there
 
     DevData train;
     std::vector<DevData> valid;
@@ -486,16 +503,27 @@ struct Context {
         feat_nt.assign(nf, -1);
         nt_feat.clear();
         group_col_nt.assign(t->num_groups, {});
-        for (uint32_t g = 0; g < t->num_groups; ++g) group_col_nt[g].assign(t->groups[g].row_stride, -1);
+        group_bin_bytes.assign(t->num_groups, 1);
+        col16 = 0;
+        for (uint32_t g = 0; g < t->num_groups; ++g) {
+            group_col_nt[g].assign(t->groups[g].row_stride, -1);
+            const uint32_t bb = t->groups[g].bin_bytes;
+            if (bb > 2) fail(SROCM_ERR_DATA, "group " + std::to_string(g) + " has " + std::to_string(bb) + "-byte bins");
+            group_bin_bytes[g] = bb == 2 ? 2u : 1u;
+            if (bb == 2) col16 = 1;
+        }
         uint64_t bins_seen = 0;
         for (uint32_t f = 0; f < nf; ++f) {
             const srocm_feature &m = feats[f];
             if (m.num_bins == 0) continue;
-            if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
             if (m.kind != SROCM_BINS_NUMERICAL && m.kind != SROCM_BINS_CATEGORICAL) fail(SROCM_ERR_DATA, "bad feature kind");
             if (m.group >= t->num_groups) fail(SROCM_ERR_DATA, "feature in a missing group");
             const srocm_group &g = t->groups[m.group];
-            if (m.column >= g.row_stride || m.hist_offset < g.hist_offset ||
+            const uint32_t bb = group_bin_bytes[m.group];
+            if (bb == 1 && m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature of one-byte bins has more than 256 bins");
+            if (bb == 2 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
+                fail(SROCM_ERR_UNSUPPORTED, "two-byte bins hold numerical features of at most 1024 bins");
+            if (m.column + bb > g.row_stride || m.hist_offset < g.hist_offset ||
                 m.hist_offset - g.hist_offset + m.num_bins > g.total_bins || m.hist_offset + m.num_bins > total_bins)
                 fail(SROCM_ERR_DATA, "feature " + std::to_string(f) + " lies outside its group's bins or row");
             feat_nt[f] = static_cast<int32_t>(nt_feat.size());
@@ -504,17 +532,31 @@ struct Context {
             bins_seen += m.num_bins;
         }
         (void)bins_seen;
-        // slabs: consecutive non-trivial features, up to 128 per slab
+        // slabs: consecutive non-trivial features of one bin width, up to 128 byte features or 32 two-byte
+        // features per slab
         slabs.clear();
         max_width = 32;
-        for (size_t i = 0; i < nt_feat.size(); i += MAX_SLAB_FEATURES) {
-            Slab s;
-            size_t end = std::min(nt_feat.size(), i + MAX_SLAB_FEATURES);
-            s.feats.assign(nt_feat.begin() + static_cast<long>(i), nt_feat.begin() + static_cast<long>(end));
-            uint32_t n = static_cast<uint32_t>(s.feats.size());
-            s.width = n <= 32 ? 32 : (n <= 64 ? 64 : 128);
-            max_width = std::max(max_width, s.width);
-            slabs.push_back(std::move(s));
+        nt_slab.assign(nt_feat.size(), 0);
+        nt_slab_col.assign(nt_feat.size(), 0);
+        for (int wide = 0; wide < 2; ++wide) {
+            std::vector<uint32_t> members;
+            for (size_t i = 0; i < nt_feat.size(); ++i)
+                if ((group_bin_bytes[feats[nt_feat[i]].group] == 2) == (wide != 0)) members.push_back(static_cast<uint32_t>(i));
+            const size_t per = wide ? MAX_SLAB_FEATURES / 4 : MAX_SLAB_FEATURES;
+            for (size_t i = 0; i < members.size(); i += per) {
+                Slab s;
+                s.wide = wide != 0;
+                const size_t end = std::min(members.size(), i + per);
+                for (size_t k = i; k < end; ++k) {
+                    nt_slab[members[k]] = static_cast<uint32_t>(slabs.size());
+                    nt_slab_col[members[k]] = static_cast<uint32_t>(k - i);
+                    s.feats.push_back(nt_feat[members[k]]);
+                }
+                const uint32_t n = static_cast<uint32_t>(s.feats.size()) * (s.wide ? 4u : 1u);  // virtual columns
+                s.width = n <= 32 ? 32 : (n <= 64 ? 64 : 128);
+                max_width = std::max(max_width, s.width);
+                slabs.push_back(std::move(s));
+            }
         }
         // device buffers
         train = DevData{};
@@ -544,19 +586,38 @@ struct Context {
         scalars.alloc(16);
         partial.alloc(static_cast<size_t>(cus) * 256 * max_width * 2);
         std::vector<FeatDev> fd(nf);
-        for (uint32_t f = 0; f < nf; ++f)
+        has_narrow = has_wide = false;
+        for (uint32_t f = 0; f < nf; ++f) {
             fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin,
-                            feat_nt[f] < 0 ? 0u : static_cast<uint32_t>(feat_nt[f])};
+                            feat_nt[f] < 0 ? 0u : static_cast<uint32_t>(feat_nt[f]),
+                            feats[f].num_bins && group_bin_bytes[feats[f].group] == 2 ? 1u : 0u};
+            // each feature's candidate (an empty one for a trivial feature) is written by the scan of its kind
+            (fd[f].wide ? has_wide : has_narrow) = true;
+        }
         dfeats.alloc(nf);
         hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
         for (auto &s : slabs) {
-            std::vector<uint32_t> off(s.width, 0), nb(s.width, 0);
+            // virtual column v: a byte feature's column; in a wide slab, bins congruent to v / (W/4) mod 4 of
+            // feature v % (W/4)
+            std::vector<uint32_t> off(s.width, 0), nb(s.width, 0), st(s.width, 1);
             for (size_t c = 0; c < s.feats.size(); ++c) {
-                off[c] = feats[s.feats[c]].hist_offset;
-                nb[c] = feats[s.feats[c]].num_bins;
+                const srocm_feature &m = feats[s.feats[c]];
+                if (!s.wide) {
+                    off[c] = m.hist_offset;
+                    nb[c] = m.num_bins;
+                    continue;
+                }
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const size_t v = q * (s.width / 4) + c;
+                    off[v] = m.hist_offset + q;
+                    nb[v] = m.num_bins > q ? (m.num_bins - q + 3) / 4 : 0u;
+                    st[v] = 4;
+                }
             }
             s.col_offset.alloc(s.width);
             s.col_bins.alloc(s.width);
+            s.col_stride.alloc(s.width);
+            hip_check(hipMemcpy(s.col_stride.p, st.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
         }
@@ -569,16 +630,23 @@ struct Context {
                 Slab &s = slabs[si];
                 s.step_partial_off = poff;
                 uint32_t gbase = static_cast<uint32_t>(gfeat.size());
+                // a wide slab's virtual column v holds bins q, q + 4, ... (q = v / (W/4)) of feature v % (W/4); the
+                // scan visits each feature once, at its q = 0 column
+                const uint32_t cap = s.capacity();
                 for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) {
-                    ColGroup x{poff, s.width, c0, gbase + c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}};
+                    ColGroup x{poff, s.width, c0, gbase + c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}, {}};
                     for (uint32_t k = 0; k < CG_COLS; ++k) {
-                        bool real = c0 + k < s.feats.size();
-                        x.offset[k] = real ? feats[s.feats[c0 + k]].hist_offset : 0u;
-                        x.bins[k] = real ? feats[s.feats[c0 + k]].num_bins : 0u;
+                        const uint32_t v = c0 + k, c = v % cap, q = v / cap;
+                        const bool real = c < s.feats.size() && (s.wide || q == 0);
+                        const srocm_feature &m = feats[real ? s.feats[c] : 0];
+                        x.offset[k] = real ? m.hist_offset + q : 0u;
+                        x.bins[k] = real && m.num_bins > q ? (m.num_bins - q + (s.wide ? 3 : 0)) / (s.wide ? 4 : 1) : 0u;
+                        x.stride[k] = s.wide ? 4u : 1u;
                     }
                     cg.push_back(x);
                 }
-                for (uint32_t c = 0; c < s.width; ++c) gfeat.push_back(c < s.feats.size() ? static_cast<int32_t>(s.feats[c]) : -1);
+                for (uint32_t c = 0; c < s.width; ++c)
+                    gfeat.push_back(c < s.feats.size() && c < cap ? static_cast<int32_t>(s.feats[c]) : -1);
                 poff += static_cast<uint64_t>(k1_groups()) * step_partial_stride(s.width);
             }
             d_fmt.alloc(std::max<size_t>(slabs.size(), 1) * k1_groups());
@@ -613,13 +681,14 @@ struct Context {
     void upload_bins(const srocm_dataset *d, DevData &out, bool with_slabs) {
         out.rows = d->num_rows;
         uint64_t n = d->num_rows;
-        out.col.alloc(std::max<uint64_t>(1, nt_feat.size() * n));
+        const uint64_t cb = col16 ? 2 : 1;
+        out.col.alloc(std::max<uint64_t>(1, nt_feat.size() * n * cb));
         out.scores.alloc(std::max<uint64_t>(n, 1));
         hip_check(hipMemsetAsync(out.scores.p, 0, std::max<uint64_t>(n, 1) * sizeof(float), stream), "zero scores");
         if (with_slabs)
             for (auto &s : slabs) {
-                s.bins.alloc(std::max<uint64_t>(1, n * s.width));
-                hip_check(hipMemsetAsync(s.bins.p, 0, std::max<uint64_t>(1, n * s.width), stream), "zero slab");
+                s.bins.alloc(std::max<uint64_t>(1, n * s.row_bytes()));
+                hip_check(hipMemsetAsync(s.bins.p, 0, std::max<uint64_t>(1, n * s.row_bytes()), stream), "zero slab");
             }
         if (n == 0) return;
         DevBuf<uint8_t> staging;
@@ -631,24 +700,21 @@ struct Context {
             for (uint32_t c = 0; c < grp.row_stride; ++c) {
                 int32_t nt = group_col_nt[g][c];
                 if (nt < 0) continue;
-                uint32_t f = nt_feat[nt];
-                uint8_t *slab_bins = nullptr;
-                uint32_t width = 0, slab_col = 0;
+                RepackTo to{out.col.p + static_cast<size_t>(nt) * n * cb, col16, nullptr, 0, 0, 0};
                 if (with_slabs) {
-                    uint32_t s = static_cast<uint32_t>(nt) / MAX_SLAB_FEATURES;
-                    slab_bins = slabs[s].bins.p;
-                    width = slabs[s].width;
-                    slab_col = static_cast<uint32_t>(nt) % MAX_SLAB_FEATURES;
+                    const Slab &sl = slabs[nt_slab[nt]];
+                    to.slab = sl.bins.p;
+                    to.row_bytes = sl.row_bytes();
+                    to.slab_wide = sl.wide ? 1u : 0u;
+                    to.slab_col = nt_slab_col[nt];
                 }
-                (void)f;
-                repack(staging.p, grp.row_stride, c, n, out.col.p + static_cast<size_t>(nt) * n, slab_bins, width, slab_col);
+                repack(staging.p, grp.row_stride, c, group_bin_bytes[g], n, to);
             }
             sync();  // staging is reused
         }
     }
 
-    void repack(const uint8_t *src, uint32_t stride, uint32_t column, uint64_t n, uint8_t *col, uint8_t *slab,
-                uint32_t width, uint32_t slab_col);
+    void repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bin_bytes, uint64_t n, const RepackTo &to);
 
     // ------------------------------------------------------------------------------------------------
     // gradients, quantization, partition reset
@@ -775,10 +841,13 @@ struct Context {
                 e1 = event();
                 hip_check(hipEventRecord(e0, stream), "event");
             }
-            switch (s.width) {
+            switch (s.width + (s.wide ? 1u : 0u)) {
             case 32: k_hist<32><<<grid, 1024, 0, stream>>>(a); break;
             case 64: k_hist<64><<<grid, 1024, 0, stream>>>(a); break;
-            default: k_hist<128><<<grid, 1024, 0, stream>>>(a); break;
+            case 128: k_hist<128><<<grid, 1024, 0, stream>>>(a); break;
+            case 33: k_hist<32, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 65: k_hist<64, true><<<grid, 1024, 0, stream>>>(a); break;
+            default: k_hist<128, true><<<grid, 1024, 0, stream>>>(a); break;
             }
             launch_check("k_hist");
             if (profiled) {
@@ -786,16 +855,18 @@ struct Context {
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
+            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, s.col_stride.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
             k_hist_reduce<<<div_up(256ull * s.width, 32), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
         if (profiled) {
             prof.builds += 1;
-            if (!dev_left) {  // rows known on the host: rows x (used columns + 4 B gradients + 4 B row id) + the output
+            if (!dev_left) {  // rows known on the host: rows x (used bins + 4 B gradients + 4 B row id) + the output
+                // (with any two-byte group, every bin counts two bytes)
                 prof.rows += count;
                 prof.bins += static_cast<double>(count) * static_cast<double>(bins_used);
-                prof.hist_bytes += static_cast<double>(count) * (static_cast<double>(bins_used) + 8.0) + 16.0 * static_cast<double>(total_bins);
+                prof.hist_bytes += static_cast<double>(count) * (static_cast<double>(bins_used) * (col16 ? 2.0 : 1.0) + 8.0) +
+                                   16.0 * static_cast<double>(total_bins);
             }
         }
     }
@@ -917,7 +988,9 @@ struct Context {
             return;
         }
         PartArgs a = part_args(leaf.begin, leaf.count);
-        a.col = train.col.p + static_cast<size_t>(nt) * rows;
+        a.col = train.col.p + static_cast<size_t>(nt) * rows * (col16 ? 2 : 1);
+        a.col16 = col16;
+        a.wide = group_bin_bytes[split.group] == 2 ? 1u : 0u;
         std::memcpy(a.left_bins, split.left_bins, sizeof(a.left_bins));
         run_partition(a, leaf.count);
     }
@@ -997,7 +1070,7 @@ struct Context {
             dn[k].feature = static_cast<uint32_t>(group_col_nt[n.split.group][n.split.column]);
             dn[k].left = n.left;
             dn[k].right = n.right;
-            dn[k].pad = 0;
+            dn[k].wide = group_bin_bytes[n.split.group] == 2 ? 1u : 0u;
         }
         d_nodes.alloc(std::max<uint32_t>(nn, 1));
         if (nn) hip_check(hipMemcpyAsync(d_nodes.p, dn, nn * sizeof(DevNode), hipMemcpyHostToDevice, stream), "upload tree");
@@ -1016,7 +1089,7 @@ struct Context {
         if (d.rows == 0) return;
         if (nn == 0) k_add_const<<<grid_rows(d.rows), 256, 0, stream>>>(d.scores.p, d.rows, v0);
         else if (from_leaf_of) k_add_leaf_values<<<grid_rows(d.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, d.scores.p, d.rows, nullptr);
-        else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p, nullptr);
+        else k_add_tree<<<grid_rows(d.rows), 256, 0, stream>>>(d.col.p, col16, d.rows, d_nodes.p, d_leaf_values.p, d.scores.p, nullptr);
         launch_check("k_add_tree");
     }
 
@@ -1045,6 +1118,7 @@ struct Context {
         leaf_of.alloc(rows);
         TreeLeavesArgs a{};
         a.colbins = train.col.p;
+        a.col16 = col16;
         a.rows = rows;
         a.nodes = d_nodes.p;
         a.nn = nn;
@@ -1112,10 +1186,11 @@ struct Context {
         std::vector<FeatDev> fd(num_features);
         for (uint32_t f = 0; f < num_features; ++f) {
             const srocm_feature &m = features[f];
-            if (m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature has more than 256 bins (bins are bytes)");
+            if (m.num_bins > 1024 || (m.num_bins > 256 && m.kind != SROCM_BINS_NUMERICAL))
+                fail(SROCM_ERR_UNSUPPORTED, "a feature of more than 1024 bins, or a categorical one of more than 256");
             if (m.num_bins && static_cast<uint64_t>(m.hist_offset) + m.num_bins > len / 2)
                 fail(SROCM_ERR_DEVICE, "feature " + std::to_string(f) + " lies outside the histogram");
-            fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin, 0u};
+            fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin, 0u, m.num_bins > 256 ? 1u : 0u};
         }
         std::vector<int64_t> units(len);
         for (size_t i = 0; i < len; ++i) units[i] = static_cast<int64_t>(hist[i]);
@@ -1142,7 +1217,10 @@ struct Context {
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             dim3 grid(div_up(num_features, 4), 1);
-            k_split_scan<<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
+            bool narrow = false, wide = false;
+            for (const FeatDev &x : fd) (x.wide ? wide : narrow) = true;
+            if (narrow) k_split_scan<false><<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
+            if (wide) k_split_scan<true><<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
             launch_check("k_split_scan");
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
@@ -1368,18 +1446,25 @@ struct Context {
     }
 };
 
-__global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint32_t column, uint64_t n,
-                         uint8_t *__restrict__ col, uint8_t *__restrict__ slab, uint32_t width, uint32_t slab_col) {
+// One feature's bins from its group's rows (one byte, or two little-endian) into its column-major bins and its
+// slab column.
+__global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint32_t column, uint32_t bin_bytes,
+                         uint64_t n, RepackTo to) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x) {
-        uint8_t b = src[r * stride + column];
-        col[r] = b;
-        if (slab) slab[r * width + slab_col] = b;
+        const uint8_t *p = src + r * stride + column;
+        const uint32_t b = bin_bytes == 2 ? static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) : p[0];
+        if (to.col16) reinterpret_cast<uint16_t *>(to.col)[r] = static_cast<uint16_t>(b);
+        else to.col[r] = static_cast<uint8_t>(b);
+        if (!to.slab) continue;
+        uint8_t *row = to.slab + r * to.row_bytes;
+        if (to.slab_wide) reinterpret_cast<uint16_t *>(row)[to.slab_col] = static_cast<uint16_t>(b);
+        else row[to.slab_col] = static_cast<uint8_t>(b);
     }
 }
 
-void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint64_t n, uint8_t *col, uint8_t *slab,
-                     uint32_t width, uint32_t slab_col) {
-    k_repack<<<grid_rows(n), 256, 0, stream>>>(src, stride, column, n, col, slab, width, slab_col);
+void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bin_bytes, uint64_t n,
+                     const RepackTo &to) {
+    k_repack<<<grid_rows(n), 256, 0, stream>>>(src, stride, column, bin_bytes, n, to);
     launch_check("k_repack");
 }
 
@@ -1457,7 +1542,10 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         launch_hist(spec.root.begin, spec.root.count, nullptr, 0, pool.p, nullptr, used_root);
         k_root_prep<<<1, 256, 0, stream>>>(g);
         launch_check("k_root_prep");
-        k_split_scan<<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, g.dsc);
+        if (has_narrow)
+            k_split_scan<false><<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, g.dsc);
+        if (has_wide)
+            k_split_scan<true><<<dim3(div_up(nf, 4), 1), 256, 0, stream>>>(d_jobs.p, dfeats.p, d_eval.p, nf, g.cfg, g.sg, g.sh, nullptr, g.dsc);
         launch_check("k_split_scan");
         if (L <= LEAVES_SMALL) k_root_select<LEAVES_SMALL><<<1, 512, 0, stream>>>(g);
         else k_root_select<GROW_MAX_LEAVES><<<1, 512, 0, stream>>>(g);
@@ -1477,12 +1565,15 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 }
                 for (size_t si = 0; si < slabs.size(); ++si) {
                     const Slab &sl = slabs[si];
-                    StepArgs sa{sl.bins.p, packed.p, train.col.p, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
+                    StepArgs sa{sl.bins.p, packed.p, train.col.p, col16, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
                                 sl.col_bins.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
-                    switch (sl.width) {
+                    switch (sl.width + (sl.wide ? 1u : 0u)) {
                     case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 64: k_step_rows<64><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    default: k_step_rows<128><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 128: k_step_rows<128><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 33: k_step_rows<32, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 65: k_step_rows<64, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    default: k_step_rows<128, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     }
                     launch_check("k_step_rows");
                 }
@@ -1495,7 +1586,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
                 ScanStepArgs sca{d_cgs.p, gcol_feat.p, cat_feats.p, ncat, d_plans.p + parity};
-                k_step_scan<<<scan_blocks(), 256, 0, stream>>>(g, sca);
+                if (has_narrow) k_step_scan<false><<<scan_blocks(), 256, 0, stream>>>(g, sca);
+                if (has_wide) k_step_scan<true><<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 launch_check("k_step_scan");
                 if (ncat) {
                     k_step_cat<<<std::min<uint32_t>(cus * 2, div_up(static_cast<uint64_t>(JMAX) * 2 * ncat, 4)), 256, 0, stream>>>(g, sca);
@@ -1652,9 +1744,9 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         prof.rows += hc.hist_rows;
         prof.bins += hc.hist_bins;
         prof.part_rows += hc.part_rows;
-        // partition: 4 B row id read, 1 B split bin, 4 B row id write per parent row; histogram: the built
-        // child's used columns and 4 B packed gradients per row
-        prof.step_bytes += 9.0 * hc.part_rows + hc.hist_bins + 4.0 * hc.hist_rows;
+        // partition: 4 B row id read, the split's bin (1 B, 2 B with two-byte groups), 4 B row id write per parent
+        // row; histogram: the built child's used bins and 4 B packed gradients per row
+        prof.step_bytes += (col16 ? 10.0 : 9.0) * hc.part_rows + hc.hist_bins * (col16 ? 2.0 : 1.0) + 4.0 * hc.hist_rows;
         prof.expansions += hc.expansions;
         prof.splits += static_cast<double>(ni);
         prof.steps += hc.steps;
@@ -1809,6 +1901,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             launch_check("k_tree_nodes");
             TreeLeavesArgs a{};
             a.colbins = train.col.p;
+            a.col16 = col16;
             a.rows = rows;
             a.nodes = d_nodes.p;
             a.leaf_of = leaf_of.p;
@@ -1830,7 +1923,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             if (train.rows)
                 k_add_leaf_values<<<grid_rows(train.rows), 256, 0, stream>>>(leaf_of.p, d_leaf_values.p, train.scores.p, train.rows, d_gate.p);
             for (auto &v : valid)
-                if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
+                if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, col16, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
             launch_check("k_add_tree");
             hip_check(hipMemcpyAsync(h_leaf_vw[vw_buf].p, d_leaf_vw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost,
                                      stream), "read leaf values");

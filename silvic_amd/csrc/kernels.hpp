@@ -246,6 +246,20 @@ __global__ void k_zero_i64(int64_t *__restrict__ out, uint64_t n) {
         out[r] = 0;
 }
 
+// Column-major bins, one byte per bin, or two (little-endian u16) when the dataset has features of more than 256
+// bins (`col16`).
+__device__ __forceinline__ uint32_t col_bin(const uint8_t *col, uint32_t col16, size_t i) {
+    return col16 ? static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(col)[i]) : static_cast<uint32_t>(col[i]);
+}
+
+// Whether a split sends `bin` left: a byte feature's split is its 256-bit mask (BinSplit::goes_left,
+// backend/mod.rs:34-37); a feature of more than 256 bins (`wide`) carries its numerical rule in the words instead:
+// lb[0] the threshold, lb[1] the NaN bin + 1 when missing values go left (0 otherwise).
+__device__ __forceinline__ bool rule_left(const uint32_t *lb, uint32_t wide, uint32_t bin) {
+    if (wide) return bin <= lb[0] || (lb[1] != 0u && bin == lb[1] - 1u);
+    return ((lb[bin >> 5] >> (bin & 31u)) & 1u) != 0u;
+}
+
 __global__ void k_iota(uint32_t *__restrict__ out, uint64_t n) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x)
         out[r] = static_cast<uint32_t>(r);
@@ -330,13 +344,25 @@ __device__ __forceinline__ void add_row_bins(int32_t *lds, uint32_t dw, int32_t 
     }
 }
 
+// A wide slab (two-byte bins of up to 1024, W / 4 features) keeps the byte slab's LDS and partial shape: bin b of
+// its column c is word (b >> 2) * W + (b & 3) * (W / 4) + c, i.e. a wide column is four virtual byte columns (bins
+// congruent to 0, 1, 2, 3 mod 4). A lane's dword holds the bins of columns 2d and 2d + 1.
+template <int W>
+__device__ __forceinline__ void add_row_bins_wide(int32_t *lds, uint32_t dw, int32_t gv, uint32_t d) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t b = min((dw >> (16 * k)) & 0xffffu, 1023u);  // clamped: invalid bins stay inside the LDS
+        atomicAdd(&lds[(b >> 2) * W + (b & 3u) * (W / 4) + 2u * d + k], gv);
+    }
+}
+
 // Loads are branch-free: row positions past the range are clamped to its last row and their gradients
 // zeroed, so the compiler issues every load of a step back to back instead of one masked load at a time. A
 // wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
-// step, and hands them out with a shuffle.
-template <int W>
+// step, and hands them out with a shuffle. WIDE: the slab's rows are W / 4 two-byte bins.
+template <int W, bool WIDE = false>
 __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
-    constexpr int DW = W / 4;                 // dwords per row
+    constexpr int DW = WIDE ? W / 8 : W / 4;  // dwords per row
     constexpr int RPW = WAVE / DW;            // rows per wave step
     // row ids of one step fit one wave-wide load; at W = 128 the 64 accumulator registers leave room for 8
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
@@ -384,7 +410,11 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
                 dw[u] = bins32[(size_t)r[u] * DW + d];
             }
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) add_row_bins<W>(lds, dw[u], base + u * RPW + rsub < cend ? g[u] : 0, xs, cols);
+            for (int u = 0; u < UNROLL; ++u) {
+                const int32_t gv = base + u * RPW + rsub < cend ? g[u] : 0;
+                if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
+                else add_row_bins<W>(lds, dw[u], gv, xs, cols);
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -410,6 +440,7 @@ struct ReduceArgs {
     const int32_t *partial;
     const uint32_t *col_offset;
     const uint32_t *col_bins;
+    const uint32_t *col_stride;  // flat-histogram bins between a column's consecutive bins: 1, or 4 (wide slab)
     int64_t *out;       // built child's histogram
     int64_t *parent;    // parent's histogram, overwritten with the sibling's (or null)
     const uint32_t *dev_left;
@@ -449,7 +480,7 @@ __global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
             g += red[0][k][lane];
             h += red[1][k][lane];
         }
-        const size_t o = 2 * (static_cast<size_t>(a.col_offset[col]) + bin);
+        const size_t o = 2 * (static_cast<size_t>(a.col_offset[col]) + static_cast<size_t>(bin) * a.col_stride[col]);
         a.out[o] = g;
         a.out[o + 1] = h;
         if (a.parent) {
@@ -471,6 +502,7 @@ struct PartArgs {
     const uint32_t *src;   // rows
     uint32_t *dst;
     const uint8_t *col;    // column-major bins of the split feature (null: bagging predicate)
+    uint32_t col16, wide;  // u16 column-major bins; the split is a wide feature's numerical rule
     uint32_t *block_left;  // [grid]
     uint32_t *dev_left;    // total left count (written by block 0 of pass 2)
     uint32_t begin, count;
@@ -489,10 +521,7 @@ __device__ __forceinline__ uint32_t part_per_block(uint32_t count, uint32_t bloc
 }
 
 __device__ __forceinline__ bool part_left(const PartArgs &a, uint32_t row) {
-    if (a.col) {
-        uint32_t bin = a.col[row];
-        return (a.left_bins[bin >> 5] >> (bin & 31u)) & 1u;
-    }
+    if (a.col) return rule_left(a.left_bins, a.wide, col_bin(a.col, a.col16, row));
     return static_cast<double>(uniform(a.bag_seed, 2u, a.bag_round, a.row_offset + row)) < a.fraction;
 }
 
@@ -647,19 +676,20 @@ struct DevNode {
     uint32_t left_bins[8];
     uint32_t feature;  // index of the feature's column-major bins
     int32_t left, right;
-    uint32_t pad;
+    uint32_t wide;     // left_bins hold a numerical rule (rule_left)
 };
 
 // `gate` (when set): the leaves of the tree to add, 0 for none (k_tree_nodes).
-__global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint64_t rows, const DevNode *__restrict__ nodes,
-                           const float *__restrict__ leaf_values, float *__restrict__ scores, const uint32_t *gate) {
+__global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint32_t col16, uint64_t rows,
+                           const DevNode *__restrict__ nodes, const float *__restrict__ leaf_values,
+                           float *__restrict__ scores, const uint32_t *gate) {
     if (gate && *gate == 0u) return;
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x) {
         int32_t node = 0;
         while (node >= 0) {
             const DevNode &nd = nodes[node];
-            uint32_t bin = colbins[(size_t)nd.feature * rows + r];
-            node = ((nd.left_bins[bin >> 5] >> (bin & 31u)) & 1u) ? nd.left : nd.right;
+            const uint32_t bin = col_bin(colbins, col16, (size_t)nd.feature * rows + r);
+            node = rule_left(nd.left_bins, nd.wide, bin) ? nd.left : nd.right;
         }
         scores[r] += leaf_values[~node];
     }
@@ -671,6 +701,7 @@ __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint64_t rows, c
 // cpu.rs:886-908). grid: any, TL_THREADS threads.
 struct TreeLeavesArgs {
     const uint8_t *colbins;            // column-major bins [feature][rows]
+    uint32_t col16;                    // two bytes per bin
     uint64_t rows;
     const DevNode *nodes;
     uint32_t nn, nl;                   // internal nodes, leaves (nn >= 1, nl <= the kernel's MAXL)
@@ -717,13 +748,14 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
         for (;;) {
             uint32_t b[TL_RPT];
 #pragma unroll
-            for (int k = 0; k < TL_RPT; ++k) b[k] = nd[k] >= 0 ? a.colbins[static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]] : 0u;
+            for (int k = 0; k < TL_RPT; ++k)
+                b[k] = nd[k] >= 0 ? col_bin(a.colbins, a.col16, static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]) : 0u;
             bool any = false;
 #pragma unroll
             for (int k = 0; k < TL_RPT; ++k) {
                 if (nd[k] < 0) continue;
                 const DevNode &x = sn[nd[k]];
-                nd[k] = ((x.left_bins[b[k] >> 5] >> (b[k] & 31u)) & 1u) ? x.left : x.right;
+                nd[k] = rule_left(x.left_bins, x.wide, b[k]) ? x.left : x.right;
                 any = any || nd[k] >= 0;
             }
             if (!any) break;
@@ -1053,7 +1085,8 @@ __device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t ow
 
 struct FeatDev {
     uint32_t num_bins, hist_offset, kind, nan_bin;
-    uint32_t col;  // column-major index among the non-trivial features
+    uint32_t col;   // column-major index among the non-trivial features
+    uint32_t wide;  // two-byte bins (up to 1024, numerical): splits carry a numerical rule (rule_left)
 };
 
 struct ScanJob {
@@ -1099,6 +1132,153 @@ __device__ __forceinline__ double candidate_gain(const Ctx &c, const SplitCfgDev
     const double gain = leaf_gain(c.sum_grad - gg, c.sum_hess - hh, cfg.lambda_l1, cfg.lambda_l2) +
                         leaf_gain(gg, hh, cfg.lambda_l1, cfg.lambda_l2);
     return (skip || gain != gain) ? -__builtin_inf() : gain;
+}
+
+// A candidate's stop test alone (candidate_gain's `stop`, without the gain).
+__device__ __forceinline__ bool candidate_stop(const Ctx &c, const SplitCfgDev &cfg, double uh, int64_t cnt,
+                                               int64_t min_count) {
+    const double hh = K_EPSILON + uh * c.scale_hess;
+    const bool skip = cnt < min_count || hh < cfg.min_sum_hessian_in_leaf || uh <= 0.0;
+    const bool other_small = c.num_data - cnt < min_count || c.sum_hess - hh < cfg.min_sum_hessian_in_leaf ||
+                             c.units_hess - uh <= 0.0;
+    return other_small && !skip;
+}
+
+// scan_numerical for a feature of up to 1024 bins (two-byte bins, an extension): lane l holds bins
+// 16l .. 16l + 15. The same candidates, stops and ties as scan_numerical, in two passes over the lane's bins so that
+// only the units stay in registers: the first finds both directions' stops, the second evaluates the candidates in
+// range, re-forming the exact prefix sums as it goes.
+__device__ void scan_numerical_wide(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist,
+                                    bool &rf, Grown &rg, bool &ff, Grown &fg) {
+    constexpr int NPB = 16;
+    const int lane = static_cast<int>(threadIdx.x & 63u);
+    const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
+    const int nb = static_cast<int>(m.num_bins);
+    const bool two = scan_two_way(m);
+    const int top = two ? nb - 2 : nb - 1;
+    double gu[NPB], hu[NPB];
+#pragma unroll
+    for (int j = 0; j < NPB; ++j) {
+        const int b = NPB * lane + j;
+        const int t = b <= top ? b : 0;
+        gu[j] = b <= top ? static_cast<double>(h[2 * t]) : 0.0;
+        hu[j] = b <= top ? static_cast<double>(h[2 * t + 1]) : 0.0;
+    }
+    // per-bin counts (split.rs:196-198): `(x + 0.5) as i64`
+    auto count_of = [&](int j) {
+        return NPB * lane + j <= top ? sat_i64(hu[j] * c.scale_hess * c.cnt_factor + 0.5) : int64_t{0};
+    };
+    double lg = 0.0, lh = 0.0;
+    int64_t lc = 0;
+#pragma unroll
+    for (int j = 0; j < NPB; ++j) {
+        lg += gu[j];
+        lh += hu[j];
+        lc += count_of(j);
+    }
+    double eg = lg, eh = lh;
+    int64_t ec = lc;
+    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
+    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
+    const double tg = readlane_f64(eg, 63), th = readlane_f64(eh, 63);
+    const int64_t tc = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(ec), 63));
+    eg -= lg;
+    eh -= lh;
+    ec -= lc;
+    const int64_t min_count = cfg.min_data_in_leaf > 1 ? cfg.min_data_in_leaf : 1;
+    // pass 1: the stops (reverse: the highest stopping bin; forward: the lowest)
+    int stop_r = -1, stop_f = 0x7fffffff;
+    {
+        double pg = eg, ph = eh;
+        int64_t pc = ec;
+        for (int j = 0; j < NPB; ++j) {
+            const int b = NPB * lane + j;
+            const int64_t cj = count_of(j);
+            const double bg = pg, bh = ph;  // the prefix below b
+            const int64_t bc = pc;
+            pg += gu[j];
+            ph += hu[j];
+            pc += cj;
+            if (b > top) continue;
+            if (b >= 1 && candidate_stop(c, cfg, th - bh, tc - bc, min_count)) stop_r = b;
+            if (two && stop_f == 0x7fffffff && candidate_stop(c, cfg, ph, pc, min_count)) stop_f = b;
+            (void)bg;
+        }
+    }
+    const int lo = wave_max_i32(stop_r) + 1;
+    const int hi = two ? wave_min_i32(stop_f) : 0;
+    // pass 2: the candidates in range; each lane keeps its best of each direction with its accumulated side
+    double brg = -__builtin_inf(), bfg = -__builtin_inf();
+    int brb = -1, bfb = -1;
+    double rug = 0.0, ruh = 0.0, fug = 0.0, fuh = 0.0;
+    int64_t ruc = 0, fuc = 0;
+    {
+        double pg = eg, ph = eh;
+        int64_t pc = ec;
+        for (int j = 0; j < NPB; ++j) {
+            const int b = NPB * lane + j;
+            const int64_t cj = count_of(j);
+            const double ag = tg - pg, ah = th - ph;  // the right side from b up
+            const int64_t ac = tc - pc;
+            pg += gu[j];
+            ph += hu[j];
+            pc += cj;
+            if (b > top) continue;
+            bool stop;
+            if (b >= 1 && b >= lo) {
+                const double gv = candidate_gain(c, cfg, ag, ah, ac, min_count, stop);
+                if (brb < 0 || gv >= brg) {  // visited downward: the highest b on equal gains
+                    brg = gv;
+                    brb = b;
+                    rug = ag;
+                    ruh = ah;
+                    ruc = ac;
+                }
+            }
+            if (two && b < hi) {
+                const double gv = candidate_gain(c, cfg, pg, ph, pc, min_count, stop);
+                if (bfb < 0 || gv > bfg) {  // visited upward: the lowest b on equal gains
+                    bfg = gv;
+                    bfb = b;
+                    fug = pg;
+                    fuh = ph;
+                    fuc = pc;
+                }
+            }
+        }
+    }
+    rf = false;
+    ff = false;
+    {
+        const double best = wave_max_f64(brb >= 0 ? brg : -__builtin_inf());
+        const int first = wave_max_i32(brb >= 0 && brg == best ? brb : -1);
+        if (first >= 0 && best > c.min_gain_shift) {
+            const uint32_t owner = static_cast<uint32_t>(first) / NPB;
+            rg.ug = readlane_f64(rug, owner);
+            rg.uh = readlane_f64(ruh, owner);
+            rg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(ruc), owner));
+            rg.gain = best;
+            rg.bin = static_cast<uint32_t>(first);
+            rf = true;
+        }
+    }
+    if (two) {
+        const double best = wave_max_f64(bfb >= 0 ? bfg : -__builtin_inf());
+        const int first = wave_min_i32(bfb >= 0 && bfg == best ? bfb : 0x7fffffff);
+        if (first != 0x7fffffff && best > c.min_gain_shift) {
+            const uint32_t owner = static_cast<uint32_t>(first) / NPB;
+            fg.ug = readlane_f64(fug, owner);
+            fg.uh = readlane_f64(fuh, owner);
+            fg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(fuc), owner));
+            fg.gain = best;
+            fg.bin = static_cast<uint32_t>(first);
+            ff = true;
+        }
+    }
 }
 
 // Both scan directions of a numerical feature (split.rs:555-620) from one pass over its bins, wave-wide. Lane l
@@ -1603,18 +1783,26 @@ __device__ __forceinline__ FeatCand categorical_candidate(const Ctx &c, const Sp
     return sorted_scan(c, cfg, m, hist, sc, order_out);
 }
 
-// split.rs:584-620 find_numerical (or a categorical search) for one feature of one leaf, by one wave.
+// split.rs:584-620 find_numerical (or a categorical search) for one feature of one leaf, by one wave. WIDE: the
+// feature has two-byte bins (numerical, up to 1024); the kernels that scan them are instantiated apart, so the
+// wide scan's registers do not lower the occupancy of the byte-bin scan.
+template <bool WIDE>
 __device__ FeatCand scan_feature(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool evaluate,
                                  CatScratch &sc, uint8_t *order_out) {
     if (!scan_searched(c, m, evaluate)) return FeatCand{};
-    if (m.kind == 2) return categorical_candidate(c, cfg, m, hist, sc, order_out);
     Grown rg = {}, fg = {};
     bool rf, ff;
-    scan_numerical(c, cfg, m, hist, rf, rg, ff, fg);
+    if constexpr (WIDE) {
+        scan_numerical_wide(c, cfg, m, hist, rf, rg, ff, fg);
+    } else {
+        if (m.kind == 2) return categorical_candidate(c, cfg, m, hist, sc, order_out);
+        scan_numerical(c, cfg, m, hist, rf, rg, ff, fg);
+    }
     return feature_candidate(c, m, rf, rg, ff, fg);
 }
 
 // grid: (ceil(num_features / 4), num_jobs); 4 waves per block, a wave per feature.
+template <bool WIDE>
 __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
                                                     SplitCfgDev cfg, double sg, double sh,
@@ -1627,9 +1815,9 @@ __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ 
     __shared__ CatScratch cats[4];
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (f >= num_features) return;
+    if (f >= num_features || (feats[f].wide != 0) != WIDE) return;  // the other instantiation's feature
     Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job.count);
-    FeatCand r = scan_feature(c, cfg, feats[f], job.hist, evaluate[f] != 0, cats[threadIdx.x >> 6],
+    FeatCand r = scan_feature<WIDE>(c, cfg, feats[f], job.hist, evaluate[f] != 0, cats[threadIdx.x >> 6],
                               cat_order ? cat_order + static_cast<size_t>(f) * 256 : nullptr);
     if ((threadIdx.x & 63) == 0) job.out[f] = r;
 }
@@ -1748,8 +1936,13 @@ __global__ __launch_bounds__(256) void k_split_select(const ScanJob *__restrict_
 // ---------------------------------------------------------------------------------------------------------
 
 // learner.rs:432-452 bin_split: word w of the bins that go left; numerical: bins 0..=threshold and the NaN bin when
-// missing values go left; categorical: the rule's bins.
-__device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_t w) {
+// missing values go left; categorical: the rule's bins. A wide feature's split carries its rule instead (threshold,
+// NaN bin + 1 when missing values go left; rule_left).
+__device__ __forceinline__ uint32_t left_bins_word(const SplitOut &info, uint32_t w, uint32_t wide) {
+    if (wide) {
+        if (w == 0) return info.threshold;
+        return w == 1 && info.default_left && info.nan_idx != NO_BIN ? info.nan_idx + 1u : 0u;
+    }
     if (info.rule != RULE_NUMERICAL) return info.cat_mask[w];
     const uint32_t upto = info.threshold + 1;
     const uint32_t lo = 32 * w;
@@ -1849,6 +2042,7 @@ struct JobPlan {
     uint32_t begin, count;        // its rows in the partition
     uint32_t col;                 // column-major index of the split feature
     uint32_t left_bins[8];
+    uint32_t wide;                // left_bins hold a wide feature's numerical rule (rule_left)
     uint32_t built_side;          // 0: the left child is histogrammed, 1: the right (learner.rs:271-275)
     uint32_t hist;                // the built child is histogrammed (learner.rs:266-268)
     int32_t parent_slot, built_slot;
@@ -2475,8 +2669,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const SplitOut &info = p.best;
         const uint32_t node = n0 - 1 + c;
         t.split_feature[node] = info.feature;
+        const uint32_t wide = g.feats[info.feature].wide;
 #pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = left_bins_word(info, w);
+        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = left_bins_word(info, w, wide);
         t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
         t.threshold_bin[node] = info.threshold;
         t.default_left[node] = static_cast<uint8_t>(info.default_left);
@@ -2568,8 +2763,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             J.begin = l.begin;
             J.count = l.count;
             J.col = info.col;
+            J.wide = g.feats[info.feature].wide;
 #pragma unroll
-            for (uint32_t w = 0; w < 8; ++w) J.left_bins[w] = left_bins_word(info, w);
+            for (uint32_t w = 0; w < 8; ++w) J.left_bins[w] = left_bins_word(info, w, J.wide);
             J.built_side = info.left_count <= info.right_count ? 0u : 1u;
             hist = (l.slot >= 0 && depth_allows(g, l.depth + 1)) ? 1u : 0u;
             J.hist = hist;
@@ -2667,7 +2863,7 @@ __global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *su
         d.feature = f >= 0 && static_cast<uint32_t>(f) < g.nf ? g.feats[f].col : 0u;
         d.left = g.tree.left_child[k];
         d.right = g.tree.right_child[k];
-        d.pad = 0;
+        d.wide = f >= 0 && static_cast<uint32_t>(f) < g.nf ? g.feats[f].wide : 0u;
         nodes[k] = d;
         bool ok = f >= 0 && static_cast<uint32_t>(f) < g.nf;
         for (const int32_t c : {d.left, d.right})
@@ -2725,6 +2921,7 @@ struct StepArgs {
     const uint8_t *bins;         // slab rows: row r at bins + r * W
     const int32_t *gh;           // packed quantized gradients per row
     const uint8_t *colbase;      // column-major bins [feature][rows]
+    uint32_t col16;              // two bytes per column-major bin
     uint64_t rows;
     uint32_t *buf0, *buf1;       // the partition buffers
     int32_t *partial;            // this slab's partials, step_partial_stride(W) pairs apart, one per workgroup
@@ -2811,6 +3008,8 @@ struct StepView {
     uint32_t *dst;
     bool rev, hist, partition;
     const uint8_t *col;
+    uint32_t col16;       // column-major bins are two bytes
+    uint32_t wide;        // the split is a wide feature's numerical rule
     uint32_t built_left;  // 1: the left child is histogrammed
     uint32_t epoch;
 };
@@ -2844,7 +3043,7 @@ __device__ __forceinline__ void tile_rows(const StepView &v, uint32_t t, TileRow
 
 __device__ __forceinline__ void tile_bins(const StepView &v, TileRows &r) {
 #pragma unroll
-    for (int j = 0; j < TILE_RPT; ++j) r.bin[j] = v.col[r.row[j]];
+    for (int j = 0; j < TILE_RPT; ++j) r.bin[j] = col_bin(v.col, v.col16, r.row[j]);
 }
 
 struct TileState {
@@ -2864,8 +3063,7 @@ __device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, co
     for (int j = 0; j < TILE_RPT; ++j) {
         st.ok[j] = t0 + j * 1024 + tid < v.count;
         st.row[j] = r.row[j];
-        const uint32_t b = r.bin[j];
-        st.left[j] = st.ok[j] && ((sh.left_bins[b >> 5] >> (b & 31u)) & 1u);
+        st.left[j] = st.ok[j] && rule_left(sh.left_bins, v.wide, r.bin[j]);
     }
     uint32_t below[TILE_RPT];
 #pragma unroll
@@ -2941,10 +3139,10 @@ __device__ __forceinline__ void tile_scatter(const StepView &v, uint32_t t, cons
 // The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
 // lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free. NW
 // waves take part; `wave` is this one's index among them.
-template <int W, int UNROLL, int NW = 16>
+template <int W, bool WIDE, int UNROLL, int NW = 16>
 __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
                                           const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6) {
-    constexpr int DW = W / 4;
+    constexpr int DW = WIDE ? W / 8 : W / 4;
     constexpr int RPW = WAVE / DW;
     constexpr uint32_t STEP = NW * RPW * UNROLL;
     const uint32_t lane = threadIdx.x & 63u;
@@ -2965,7 +3163,11 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
             dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
         }
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) add_row_bins<W>(lds, dw[u], base + u * RPW + rsub < c1 ? gq[u] : 0, xs, cols);
+        for (int u = 0; u < UNROLL; ++u) {
+            const int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
+            if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
+            else add_row_bins<W>(lds, dw[u], gv, xs, cols);
+        }
     }
 }
 
@@ -3010,9 +3212,9 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
     }
 }
 
-template <int W>
+template <int W, bool WIDE = false>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
-    constexpr int DW = W / 4;
+    constexpr int DW = WIDE ? W / 8 : W / 4;
     constexpr int RPW = WAVE / DW;
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);  // rows per lane in multi-tile workgroups
     constexpr int SLOTS = 256 * W / 1024;
@@ -3038,7 +3240,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     v.src = J.src_buf ? a.buf1 : a.buf0;
     v.dst = J.src_buf ? a.buf0 : a.buf1;
     v.rev = J.src_rev != 0;
-    v.col = a.colbase + static_cast<size_t>(J.col) * a.rows;
+    v.col16 = a.col16;
+    v.wide = J.wide;
+    v.col = a.colbase + static_cast<size_t>(J.col) * a.rows * (a.col16 ? 2u : 1u);
     v.built_left = J.built_side == 0 ? 1u : 0u;
     v.epoch = P.epoch;
     const uint32_t tid = threadIdx.x;
@@ -3061,9 +3265,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (v.hist) hist_list<W, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (v.hist) hist_list<W, WIDE, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
         } else if (v.hist) {
-            hist_list<W, 16>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         __syncthreads();  // the offset and the histogram are complete
         if (v.partition) tile_scatter(v, t, st, sh);
@@ -3118,7 +3322,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 }
                 uint32_t room = a.flush_rows - pending;
                 uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                hist_list<W, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+                hist_list<W, WIDE, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
                 pending += c1 - c0;
                 c0 = c1;
             }
@@ -3126,11 +3330,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (!hist_done) hist_list<W, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (!hist_done) hist_list<W, WIDE, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
             __syncthreads();  // the offset is in sh.prefix
             tile_scatter(v, t, st, sh);
         } else if (!hist_done) {
-            hist_list<W, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         if (!hist_done) pending += nb;
         if (tn < v.ntiles) tile_bins(v, r);
@@ -3160,6 +3364,7 @@ struct ColGroup {
     uint32_t fmt;      // the slab's first k_step_rows workgroup in the partial-format flags
     uint32_t offset[4];  // per column: its feature's first bin in the flat histogram
     uint32_t bins[4];    // per column: the feature's bins (0 for padding)
+    uint32_t stride[4];  // per column: flat-histogram bins between its consecutive bins (4 in a wide slab)
 };
 
 // Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
@@ -3348,7 +3553,7 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 if (bin < cg.bins[c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + static_cast<size_t>(bin) * cg.stride[c]);
                     pg[c] = parent[o];
                     ph[c] = parent[o + 1];
                 }
@@ -3411,7 +3616,7 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 if (bin < cg.bins[c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + bin);
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + static_cast<size_t>(bin) * cg.stride[c]);
                     built[o] = sg[c];
                     built[o + 1] = sh[c];
                     parent[o] = pg[c] - sg[c];
@@ -3424,8 +3629,9 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
 }
 
 // Scan items (job, column, child), a wave each in a grid-stride loop: the column's numerical feature scanned in
-// both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's.
-// grid: any, 256 threads.
+// both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's; features
+// of two-byte bins are k_step_scan<true>'s, the others k_step_scan<false>'s. grid: any, 256 threads.
+template <bool WIDE>
 __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) {
     const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     const uint32_t lane = threadIdx.x & 63u;
@@ -3439,7 +3645,7 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
         const int32_t sf = a.col_feat[cg.gcol + scol];
         if (sf < 0) continue;
         const FeatDev sm = g.feats[sf];
-        if (sm.kind == 2) continue;
+        if (sm.kind == 2 || (sm.wide != 0) != WIDE) continue;
         const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
         const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
         const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
@@ -3448,7 +3654,8 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
         if (scan_searched(c, sm, sev)) {
             Grown rg = {}, fg = {};
             bool rf, ff;
-            scan_numerical(c, g.cfg, sm, hist, rf, rg, ff, fg);
+            if constexpr (WIDE) scan_numerical_wide(c, g.cfg, sm, hist, rf, rg, ff, fg);
+            else scan_numerical(c, g.cfg, sm, hist, rf, rg, ff, fg);
             r = feature_candidate(c, sm, rf, rg, ff, fg);
         }
         if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;

@@ -52,6 +52,7 @@ struct Workload {
     uint32_t cols = 0;
     uint32_t seed = 0;
     uint32_t max_bin = 255;
+    uint32_t bin_bytes = 1;  // 2 when max_bin > 256
     // per input feature
     std::vector<uint32_t> num_bins, group, column, hist_offset, kind, nan_bin;
     std::vector<std::vector<double>> bounds;
@@ -192,12 +193,12 @@ void find_bins(std::vector<double> sample, uint32_t max_bin, std::vector<double>
     bounds.push_back(std::numeric_limits<double>::infinity());
 }
 
-inline uint8_t bin_of(const std::vector<double> &bounds, bool nan_bin, double v) {
+inline uint32_t bin_of(const std::vector<double> &bounds, bool nan_bin, double v) {
     if (std::isnan(v)) {
-        if (nan_bin) return static_cast<uint8_t>(bounds.size());
+        if (nan_bin) return static_cast<uint32_t>(bounds.size());
         v = 0.0;
     }
-    return static_cast<uint8_t>(std::lower_bound(bounds.begin(), bounds.end(), v) - bounds.begin());
+    return static_cast<uint32_t>(std::lower_bound(bounds.begin(), bounds.end(), v) - bounds.begin());
 }
 
 }  // namespace
@@ -205,15 +206,17 @@ inline uint8_t bin_of(const std::vector<double> &bounds, bool nan_bin, double v)
 extern "C" {
 
 // Builds configuration `config` (1..5) with `rows` rows and `cols` features, binned with at most `max_bin`
-// bins per feature (2..256). Returns NULL for an unknown configuration or bad sizes.
+// bins per feature (2..1024; above 256 the bins are stored as little-endian u16, two bytes per feature, the
+// extension for max_bin > 255). Returns NULL for an unknown configuration or bad sizes.
 void *synth_create(uint32_t config, uint64_t rows, uint32_t cols, uint32_t seed, uint32_t max_bin) {
-    if (config < 1 || config > 5 || rows == 0 || cols == 0 || max_bin < 2 || max_bin > 256) return nullptr;
+    if (config < 1 || config > 5 || rows == 0 || cols == 0 || max_bin < 2 || max_bin > 1024) return nullptr;
     auto w = std::make_unique<Workload>();
     w->config = config;
     w->rows = rows;
     w->cols = cols;
     w->seed = seed;
     w->max_bin = max_bin;
+    w->bin_bytes = max_bin > 256 ? 2u : 1u;
     // bin mappers from a sample of up to 200k rows (bin_construct_sample_cnt, config.rs:143)
     uint64_t sample_rows = std::min<uint64_t>(rows, 200000);
     uint64_t step = rows / sample_rows;
@@ -248,13 +251,13 @@ void *synth_create(uint32_t config, uint64_t rows, uint32_t cols, uint32_t seed,
             w->g_total_bins.push_back(0);
         }
         w->group.push_back(static_cast<uint32_t>(w->g_features.size() - 1));
-        w->column.push_back(static_cast<uint32_t>(w->g_features.back().size()));
+        w->column.push_back(static_cast<uint32_t>(w->g_features.back().size()) * w->bin_bytes);
         w->g_features.back().push_back(j);
         w->g_total_bins.back() += nb;
         offset += nb;
     }
     w->total_bins = offset;
-    for (auto &f : w->g_features) w->g_stride.push_back(static_cast<uint32_t>((f.size() + 3) / 4 * 4));
+    for (auto &f : w->g_features) w->g_stride.push_back(static_cast<uint32_t>((f.size() * w->bin_bytes + 3) / 4 * 4));
     w->g_data.resize(w->g_features.size());
     for (size_t g = 0; g < w->g_data.size(); ++g) w->g_data[g].assign(rows * w->g_stride[g], 0);
     w->label.resize(rows);
@@ -266,7 +269,10 @@ void *synth_create(uint32_t config, uint64_t rows, uint32_t cols, uint32_t seed,
                 x[j] = value(*w, j, r);
                 if (w->num_bins[j] == 0) continue;
                 uint32_t g = w->group[j];
-                w->g_data[g][r * w->g_stride[g] + w->column[j]] = bin_of(w->bounds[j], w->nan_bin[j] != 0, x[j]);
+                const uint32_t b = bin_of(w->bounds[j], w->nan_bin[j] != 0, x[j]);
+                uint8_t *at = &w->g_data[g][r * w->g_stride[g] + w->column[j]];
+                at[0] = static_cast<uint8_t>(b);
+                if (w->bin_bytes == 2) at[1] = static_cast<uint8_t>(b >> 8);
             }
             w->label[r] = label_of(*w, r, x);
         }
@@ -293,13 +299,14 @@ void synth_features(const void *h, uint32_t *out) {
 uint32_t synth_num_groups(const void *h) { return static_cast<uint32_t>(static_cast<const Workload *>(h)->g_features.size()); }
 uint64_t synth_total_bins(const void *h) { return static_cast<const Workload *>(h)->total_bins; }
 
-// Group `g`: row stride, hist offset, total bins, feature count.
-void synth_group(const void *h, uint32_t g, uint32_t *out4) {
+// Group `g`: row stride, hist offset, total bins, feature count, bytes per bin.
+void synth_group(const void *h, uint32_t g, uint32_t *out5) {
     const Workload *w = static_cast<const Workload *>(h);
-    out4[0] = w->g_stride[g];
-    out4[1] = w->g_hist_offset[g];
-    out4[2] = w->g_total_bins[g];
-    out4[3] = static_cast<uint32_t>(w->g_features[g].size());
+    out5[0] = w->g_stride[g];
+    out5[1] = w->g_hist_offset[g];
+    out5[2] = w->g_total_bins[g];
+    out5[3] = static_cast<uint32_t>(w->g_features[g].size());
+    out5[4] = w->bin_bytes;
 }
 const uint32_t *synth_group_features(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_features[g].data(); }
 const uint8_t *synth_group_data(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_data[g].data(); }

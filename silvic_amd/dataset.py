@@ -34,13 +34,15 @@ class FeatureMeta:
 
 @dataclass
 class FeatureGroup:
-    """FeatureGroup (data/mod.rs:48-59): ``data[row * row_stride + column]``."""
+    """FeatureGroup (data/mod.rs:48-59): ``data[row * row_stride + column]``. ``bin_bytes`` 2 (an extension for
+    max_bin > 255) stores each bin as a little-endian u16 at byte offset ``column``."""
 
     features: list
     row_stride: int
     hist_offset: int
     total_bins: int
     data: np.ndarray
+    bin_bytes: int = 1
 
 
 @dataclass
@@ -61,7 +63,11 @@ class BinnedDataset:
         """Bins of ``feature`` at ``rows`` (all rows by default), as ``BinnedDataset::bin`` (data/mod.rs:81-87)."""
         meta = self.features[feature]
         g = self.groups[meta.group]
-        col = g.data.reshape(self.num_rows, g.row_stride)[:, meta.column]
+        m = g.data.reshape(self.num_rows, g.row_stride)
+        if g.bin_bytes == 2:
+            col = m[:, meta.column].astype(np.uint16) | (m[:, meta.column + 1].astype(np.uint16) << 8)
+        else:
+            col = m[:, meta.column]
         return col if rows is None else col[rows]
 
     def as_c(self):
@@ -77,7 +83,7 @@ class BinnedDataset:
             keep += [fidx, data]
             groups[i] = _abi.Group(g.row_stride, g.hist_offset, g.total_bins, len(g.features),
                                    fidx.ctypes.data_as(C.POINTER(C.c_uint32)),
-                                   data.ctypes.data_as(C.POINTER(C.c_uint8)))
+                                   data.ctypes.data_as(C.POINTER(C.c_uint8)), g.bin_bytes)
         label = np.ascontiguousarray(self.label, dtype=np.float32)
         keep.append(label)
         weight = None
@@ -144,7 +150,7 @@ CONFIGS = {
     2: (10_000_000, 128, 255, _abi.OBJ_BINARY),
     3: (2_000_000, 136, 255, _abi.OBJ_LAMBDARANK),
     4: (1_000_000, 2000, 63, _abi.OBJ_BINARY),
-    5: (50_000_000, 32, 255, _abi.OBJ_REGRESSION),
+    5: (50_000_000, 32, 1023, _abi.OBJ_REGRESSION),
 }
 
 
@@ -193,13 +199,13 @@ def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=Fa
                 bounds = np.ctypeslib.as_array(lib.synth_bounds(h, j), shape=(nbounds,)).copy()
             features.append(FeatureMeta(nb, g, c, off, kind, bool(nan), bounds))
         groups = []
-        info = (C.c_uint32 * 4)()
+        info = (C.c_uint32 * 5)()
         for g in range(lib.synth_num_groups(h)):
             lib.synth_group(h, g, info)
-            stride, off, total, nf = (int(v) for v in info)
+            stride, off, total, nf, bb = (int(v) for v in info)
             fidx = np.ctypeslib.as_array(lib.synth_group_features(h, g), shape=(nf,)).copy()
             data = np.ctypeslib.as_array(lib.synth_group_data(h, g), shape=(rows * stride,)).copy()
-            groups.append(FeatureGroup([int(f) for f in fidx], stride, off, total, data))
+            groups.append(FeatureGroup([int(f) for f in fidx], stride, off, total, data, bb))
         label = np.ctypeslib.as_array(lib.synth_label(h), shape=(rows,)).copy()
         total = int(lib.synth_total_bins(h))
         nq = int(lib.synth_num_queries(h))

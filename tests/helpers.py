@@ -130,6 +130,24 @@ def row_slice(data, start, stop):
     groups = []
     for g in data.groups:
         d = g.data.reshape(data.num_rows, g.row_stride)[start:stop]
-        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy()))
+        groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy(),
+                                   g.bin_bytes))
     weight = None if data.weight is None else data.weight[start:stop].copy()
     return BinnedDataset(stop - start, data.features, groups, data.total_bins, data.label[start:stop].copy(), weight)
+
+
+def joined(a, b):
+    """The features of ``a`` and then ``b`` (same rows) as one dataset, ``b``'s groups and bins after ``a``'s, with
+    ``a``'s labels: a dataset of both one-byte and two-byte groups."""
+    assert a.num_rows == b.num_rows
+    ng = len(a.groups)
+    feats = list(a.features)
+    for f in b.features:
+        feats.append(FeatureMeta(f.num_bins, f.group + ng, f.column, f.hist_offset + a.total_bins, f.kind, f.nan_bin,
+                                 f.bounds))
+    groups = list(a.groups)
+    nf = len(a.features)
+    for g in b.groups:
+        groups.append(FeatureGroup([j + nf for j in g.features], g.row_stride, g.hist_offset + a.total_bins,
+                                   g.total_bins, g.data, g.bin_bytes))
+    return BinnedDataset(a.num_rows, feats, groups, a.total_bins + b.total_bins, a.label, a.weight)

@@ -154,3 +154,44 @@ def categorical_cases():
         cfg = config(min_data_in_leaf=0, min_sum_hessian_in_leaf=0.0, min_data_per_group=0, cat_smooth=0.0)
         out.append((f"zero hessian {nb}", h, h[1::2].astype(np.int64), categorical(nb), cfg))
     return out
+
+
+def wide_numerical_cases(count=40):
+    """Numerical features of 257..1024 bins (2-byte bins, an extension the reference does not have), generated as
+    the cases above: (name, hist, rows, meta, cfg)."""
+    rng = Lcg(19)
+    out = []
+    for case in range(count):
+        nan_bin = case % 2 == 1
+        num_bins = 257 + rng.below(768)
+        hist, rows = random_hist(rng, num_bins, 0.25)
+        cfg = config(lambda_l1=0.5 if case % 3 == 0 else 0.0, lambda_l2=2.0 if case % 5 == 0 else 0.0)
+        out.append((f"wide case {case} bins {num_bins} nan {nan_bin}", hist, rows, numerical(num_bins, nan_bin), cfg))
+    return out
+
+
+def brute_force_numerical(hist, rows, cfg, nan_bin):
+    """brute_force over numerical_candidates with the sides' sums from cumulative sums (the candidates of a
+    1000-bin feature are too many for the direct loop)."""
+    num_bins = len(rows)
+    numeric = num_bins - int(nan_bin)
+    g, h, n = hist[0::2], hist[1::2], rows.astype(np.int64)
+    tg, th, tn = float(g.sum()), float(h.sum()), int(n.sum())
+    shift = leaf_gain(tg, th, cfg.lambda_l1, cfg.lambda_l2) + cfg.min_gain_to_split
+    end = numeric if nan_bin else numeric - 1
+    cg, ch, cn = np.cumsum(g[:numeric]), np.cumsum(h[:numeric]), np.cumsum(n[:numeric])
+    best = MIN_SCORE
+    for t in range(end):
+        for nan_left in (False, True):
+            lg, lh, ln = float(cg[t]), float(ch[t]), int(cn[t])
+            if nan_left and nan_bin:
+                lg, lh, ln = lg + g[numeric], lh + h[numeric], ln + int(n[numeric])
+            rg, rh, rn = tg - lg, th - lh, tn - ln
+            if not (ln >= cfg.min_data_in_leaf and ln > 0 and lh >= cfg.min_sum_hessian_in_leaf and lh > 0.0):
+                continue
+            if not (rn >= cfg.min_data_in_leaf and rn > 0 and rh >= cfg.min_sum_hessian_in_leaf and rh > 0.0):
+                continue
+            gain = leaf_gain(lg, lh, cfg.lambda_l1, cfg.lambda_l2) + leaf_gain(rg, rh, cfg.lambda_l1, cfg.lambda_l2)
+            if gain > shift:
+                best = max(best, gain - shift)
+    return best

@@ -374,7 +374,7 @@ def test_grow_rejects_more_leaves_than_the_device_grows(rocm):
 @pytest.mark.parametrize("leaves", [1000, 2047])
 def test_large_trees_match_the_oracle(rocm, leaves):
     say("grow large", leaves)
-    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=3)
+    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=3, max_bin=255)
     rng = np.random.default_rng(8)
     g = (data.label - rng.standard_normal(data.num_rows).astype(np.float32) * 0.1).astype(np.float32)
     h = np.ones_like(g)
@@ -392,7 +392,7 @@ def test_large_trees_match_the_oracle(rocm, leaves):
 
 def test_boosting_large_trees_matches_the_oracle():
     say("boost 2047 leaves")
-    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=4)
+    data = silvic_amd.synthetic(5, rows=2_000_000, cols=32, seed=4, max_bin=255)
     o, t = boost_both(data, dict(num_leaves=2047), 3)
     assert len(t.trees) == len(o.trees) == 3
     for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
