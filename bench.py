@@ -21,21 +21,181 @@ HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "split_step_traffic_10Mx128.md")
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a
-    copy kernel of known size), for the default workload; None when the summary is absent."""
+def measured_traffic(kernel, per):
+    """HBM bytes per `per` ("launch" or "tree") of the kernel whose name starts with `kernel`, from the committed
+    summary of rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this script's timed iterations (scaled by a copy of
+    known size), for the default workload; None when the summary is absent."""
     import re
 
     try:
         text = open(TRAFFIC_FILE).read()
     except OSError:
         return None
-    m = re.search(r"^traffic_bytes_per_launch " + re.escape(kernel) + r": (\d+)$", text, re.M)
+    m = re.search(r"^traffic_bytes_per_" + per + " " + re.escape(kernel) + r"[^:]*: (\d+)$", text, re.M)
     return float(m.group(1)) if m else None
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def kernel_key(name):
+    """A short, stable name for a dispatch's kernel: the template instance of the step and histogram kernels, the
+    plain name otherwise."""
+    n = name.replace("void ", "").replace("srocm::", "").replace("(anonymous namespace)::", "")
+    return n.split("(")[0].strip()
+
+
+def timed_window(rows, warmup, steps):
+    """The dispatch records of the timed iterations (after `warmup` iterations, `steps` of them) of a run of this
+    script. An iteration starts after the previous tree's score update (k_add_leaf_values) that precedes its tree's
+    k_grow_init, so a window begins with an iteration's gradients. `rows` are rocprofv3 CSV records in dispatch
+    order."""
+    starts = [i for i, r in enumerate(rows) if kernel_key(r["Kernel_Name"]).startswith("k_grow_init")]
+    if warmup < 1 or len(starts) < warmup + steps:
+        raise SystemExit(f"the profile holds {len(starts)} trees; a window of {steps} after {warmup} warm-up "
+                         "iterations (at least one) needs more")
+
+    def begin(t):
+        if t >= len(starts):
+            return len(rows)
+        ends = [i for i in range(starts[t]) if kernel_key(rows[i]["Kernel_Name"]).startswith("k_add_leaf_values")]
+        return ends[-1] + 1 if ends else starts[t]
+
+    return rows[begin(warmup):begin(warmup + steps)]
+
+
+def read_counters(folder):
+    """rocprofv3 --pmc CSV of `folder` as (dispatch records in order, {dispatch: {counter: value}})."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(folder, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {folder}")
+    recs, vals = {}, {}
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            d = int(r["Dispatch_Id"])
+            recs[d] = r
+            vals.setdefault(d, {})
+            vals[d][r["Counter_Name"]] = vals[d].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    order = [recs[d] for d in sorted(recs)]
+    return order, vals
+
+
+def pmc_summary(args):
+    """Per-tree and per-launch counters of the timed window (--steps iterations after --warmup) from rocprofv3 runs
+    of this script; prints a markdown summary. FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what each reads
+    for the runtime's copy kernel moving a known size (--calibrate-copy): the copies are the
+    `__amd_rocclr_copyBuffer` dispatches before the dataset upload (`k_repack`)."""
+    fetch_dir, write_dir = args.pmc_summary[:2]
+    lds_dir = args.pmc_summary[2] if len(args.pmc_summary) > 2 else None
+    out = []
+    per_tree = {}
+    launches = {}
+    scale = {}
+    for counter, folder in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        order, vals = read_counters(folder)
+        first_load = next((i for i, r in enumerate(order) if "k_repack" in r["Kernel_Name"]), len(order))
+        copies = [vals[int(r["Dispatch_Id"])].get(counter, 0.0) for r in order[:first_load]
+                  if "copyBuffer" in r["Kernel_Name"]][:4]
+        known_kib = args.calibrate_copy * 1024.0
+        if not copies or not known_kib:
+            raise SystemExit(f"{counter}: no calibration copies (run the profile with --calibrate-copy MB and pass "
+                             "the same --calibrate-copy here)")
+        measured = sum(copies) / len(copies)
+        scale[counter] = known_kib / measured
+        win = timed_window(order, args.warmup, args.steps)
+        for r in win:
+            k = kernel_key(r["Kernel_Name"])
+            v = vals[int(r["Dispatch_Id"])].get(counter, 0.0) * 1024.0 * scale[counter]
+            per_tree.setdefault(k, {}).setdefault(counter, 0.0)
+            per_tree[k][counter] += v / args.steps
+            if counter == "FETCH_SIZE":
+                launches[k] = launches.get(k, 0) + 1
+        out.append(f"- {counter}: the {len(copies)} calibration copies of {args.calibrate_copy} MiB read "
+                   f"{measured:.0f} KiB each; scale {scale[counter]:.3f}")
+    out.append("")
+    out.append("| kernel | launches per tree | FETCH MB per tree | WRITE MB per tree | HBM MB per tree | "
+               "HBM MB per launch |")
+    out.append("|---|---:|---:|---:|---:|---:|")
+    rank = sorted(per_tree, key=lambda k: -(per_tree[k].get("FETCH_SIZE", 0) + per_tree[k].get("WRITE_SIZE", 0)))
+    for k in rank[:12]:
+        f, w = per_tree[k].get("FETCH_SIZE", 0.0), per_tree[k].get("WRITE_SIZE", 0.0)
+        lpt = launches.get(k, 0) / args.steps
+        out.append(f"| `{k}` | {lpt:.2f} | {f / 1e6:.1f} | {w / 1e6:.1f} | {(f + w) / 1e6:.1f} | "
+                   f"{(f + w) / lpt / 1e6 if lpt else 0:.1f} |")
+    out.append("")
+    for k in rank:
+        if k.startswith("k_step_rows") or k.startswith("k_hist<"):
+            t = per_tree[k].get("FETCH_SIZE", 0.0) + per_tree[k].get("WRITE_SIZE", 0.0)
+            lpt = launches.get(k, 0) / args.steps
+            out.append(f"traffic_bytes_per_tree {k}: {t:.0f}")
+            out.append(f"traffic_bytes_per_launch {k}: {t / lpt if lpt else 0:.0f}")
+    if lds_dir:
+        order, vals = read_counters(lds_dir)
+        win = timed_window(order, args.warmup, args.steps)
+        agg = {}
+        for r in win:
+            k = kernel_key(r["Kernel_Name"])
+            a = agg.setdefault(k, {"n": 0, "ns": 0.0})
+            a["n"] += 1
+            a["ns"] += float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+            for c, v in vals[int(r["Dispatch_Id"])].items():
+                a[c] = a.get(c, 0.0) + v
+        out.append("")
+        out.append("| kernel | launches per tree | LDS atomic lane-ops per launch | LDS atomics/s | LDS instructions per "
+                   "launch | bank-conflict share of LDS cycles |")
+        out.append("|---|---:|---:|---:|---:|---:|")
+        for k in sorted(agg, key=lambda k: -agg[k].get("SQ_INSTS_LDS_ATOMIC", 0.0)):
+            a = agg[k]
+            atom = a.get("SQ_INSTS_LDS_ATOMIC", 0.0) * 64  # wave instructions x 64 lanes
+            if not a.get("SQ_INSTS_LDS", 0.0):
+                continue
+            rate = atom / (a["ns"] * 1e-9) if a["ns"] else 0.0
+            act = a.get("SQ_LDS_IDX_ACTIVE", 0.0)
+            share = a.get("SQ_LDS_BANK_CONFLICT", 0.0) / act if act else 0.0
+            out.append(f"| `{k}` | {a['n'] / args.steps:.2f} | {atom / a['n']:.3g} | {rate:.3g} | "
+                       f"{a.get('SQ_INSTS_LDS', 0.0) / a['n']:.3g} | {share:.1%} |")
+    print("\n".join(out))
+
+
+def trace_summary(args):
+    """Per-iteration kernel time of the timed window (--steps iterations after --warmup) from a rocprofv3
+    --kernel-trace run of this script, with the idle time between consecutive dispatches; prints a markdown table."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(args.trace_summary, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {args.trace_summary}")
+    rows = []
+    for f in files:
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    win = timed_window(rows, args.warmup, args.steps)
+    agg, gaps = {}, 0.0
+    prev = None
+    for r in win:
+        s, e = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        k = kernel_key(r["Kernel_Name"])
+        a = agg.setdefault(k, [0, 0.0])
+        a[0] += 1
+        a[1] += (e - s) / 1e3
+        if prev is not None and s > prev:
+            gaps += (s - prev) / 1e3
+        prev = max(prev or 0, e)
+    span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e3
+    print(f"{args.steps} iterations, {span / args.steps:.1f} us per iteration from the first dispatch of the window "
+          f"to the last; busy {sum(v[1] for v in agg.values()) / args.steps:.1f} us, idle between dispatches "
+          f"{gaps / args.steps:.1f} us per iteration")
+    print()
+    print("| kernel | launches per iteration | us per iteration | avg us per launch | share of busy time |")
+    print("|---|---:|---:|---:|---:|")
+    busy = sum(v[1] for v in agg.values())
+    for k, (n, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"| `{k}` | {n / args.steps:.2f} | {us / args.steps:.1f} | {us / n:.1f} | {us / busy:.1%} |")
 
 
 def copy_calibration(nbytes):
@@ -62,8 +222,8 @@ def copy_calibration(nbytes):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--rows", type=int, default=10_000_000)
     ap.add_argument("--cols", type=int, default=128)
     ap.add_argument("--leaves", type=int, default=255)
@@ -72,7 +232,19 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="first run 4 device-to-device copies of MB MiB (the runtime's copy kernel): known bytes for "
                          "scaling hardware memory counters")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="no GPU: summarize rocprofv3 --pmc runs of this script (FETCH_SIZE dir, WRITE_SIZE dir, and "
+                         "optionally an LDS-counter dir) over its timed iterations (--warmup, --steps as in the run)")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="no GPU: per-iteration kernel times of a rocprofv3 --kernel-trace run of this script over "
+                         "its timed iterations (--warmup, --steps as in the run)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args)
+        return
+    if args.trace_summary:
+        trace_summary(args)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported (the path is single-GPU; "
               "multi-GPU sharding is a design note, not a measured configuration)", file=sys.stderr)
@@ -101,26 +273,44 @@ def main():
 
     warm = trainer.step(args.warmup)
     log(f"warmup {len(warm)} iterations done")
-    trainer.backend._check(lib.srocm_profile(h, 1))
+    # The timed iterations run without the per-kernel events (each event is a marker in the stream that idles the
+    # GPU for a few microseconds). Training is deterministic, so a second trainer repeats the same warm-up and the
+    # same iterations with the events on: the kernel times and work counts are those of the timed trees.
     t0 = time.perf_counter()
     timed = trainer.step(args.steps)
     elapsed = time.perf_counter() - t0
+    if len(timed) != args.steps:
+        log(f"training ended after {len(timed)} of {args.steps} timed iterations")
+    gpu_trees = trainer.trees
+    trainer.backend.close()
+    trainer = silvic_amd.Trainer(params, data)
+    lib, h = trainer.backend._lib, trainer.backend._h
+    trainer.step(args.warmup)
+    trainer.backend._check(lib.srocm_profile(h, 1))
+    t1 = time.perf_counter()
+    profiled = trainer.step(args.steps)
+    elapsed_profiled = time.perf_counter() - t1
     prof = (C.c_double * 15)()
     trainer.backend._check(lib.srocm_profile_read(h, prof, 15))
     trainer.backend._check(lib.srocm_profile(h, 0))
-    if len(timed) != args.steps:
-        log(f"training ended after {len(timed)} of {args.steps} timed iterations")
+    same_trees = all(np.array_equal(a["split_feature"], b["split_feature"]) and
+                     np.array_equal(a["threshold_bin"], b["threshold_bin"]) for a, b in zip(gpu_trees, trainer.trees))
+    if not same_trees:
+        log("the repeated iterations grew different trees")
     (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
      part_rows, _, _, grow_steps, expansions, kept) = list(prof)
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
+    psteps = max(len(profiled), 1)
     # every histogram is built by k_hist (roots) or k_step_rows (split steps, which also partition)
     bins_per_s = hist_bins / ((hist_ms + step_ms) / 1e3) if hist_ms + step_ms else 0.0
     step_gbps = step_bytes / (step_ms / 1e3) / 1e9 if step_ms else 0.0
     default_workload = (args.rows, args.cols, args.leaves) == (10_000_000, 128, 255)
-    traffic = measured_traffic("k_step_rows<128>") if default_workload else None
+    traffic = measured_traffic("k_step_rows<128", "launch") if default_workload else None
+    traffic_tree = measured_traffic("k_step_rows<128", "tree") if default_workload else None
     root_gbps = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms else 0.0
-    log(f"{steps} iterations in {elapsed:.3f}s; k_step_rows: {step_launches:.0f} launches, {step_ms:.1f} ms, "
+    log(f"{steps} iterations in {elapsed:.3f}s; the same {psteps} again with kernel events in {elapsed_profiled:.3f}s: "
+        f"k_step_rows: {step_launches:.0f} launches, {step_ms:.1f} ms, "
         f"{step_gbps:.0f} GB/s algorithmic; k_hist (roots): {hist_launches:.0f} launches, {hist_ms:.1f} ms, "
         f"{root_gbps:.0f} GB/s; {builds:.0f} histograms, {part_rows:.3g} rows partitioned; {grow_steps:.0f} split "
         f"steps expanded {expansions:.0f} leaves for {kept:.0f} kept splits")
@@ -145,7 +335,6 @@ def main():
             m, cpu_elapsed = m1, one
         cpu_iters = len(m.trees) / cpu_elapsed
         # the trees the oracle grew must be the device's (split features, threshold bins, counts; values 1e-6)
-        gpu_trees = trainer.trees
         same = 0
         for d, o in zip(gpu_trees, m.trees):
             ok = (d["num_leaves"] == o["num_leaves"] and np.array_equal(d["split_feature"], o["split_feature"])
@@ -181,14 +370,21 @@ def main():
                                "num_grad_quant_bins=4", "rows": args.rows, "features": args.cols,
                    "num_leaves": args.leaves, "total_bins": data.total_bins, "parallelism": "single GPU"},
         "hist_bins_per_s": bins_per_s,
-        "step_kernel_ms_per_iter": step_ms / steps,
-        "root_hist_ms_per_iter": hist_ms / steps,
+        "step_kernel_ms_per_iter": step_ms / psteps,
+        "root_hist_ms_per_iter": hist_ms / psteps,
         "roofline": {"bound": "hbm", "achieved": step_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": step_gbps / HBM_PEAK_GBPS, "traffic": traffic,
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,
                      "kernel": "k_step_rows<128> (split step: stable partition + built-child histogram)",
                      "launches": step_launches, "avg_launch_us": step_ms / step_launches * 1e3 if step_launches else None,
                      "bytes_per_launch": step_bytes / step_launches if step_launches else None,
+                     "per_tree": {"launches": step_launches / psteps, "kernel_ms": step_ms / psteps,
+                                  "algorithmic_bytes": step_bytes / psteps, "traffic_bytes": traffic_tree,
+                                  "traffic_over_algorithmic": traffic_tree / (step_bytes / psteps)
+                                  if traffic_tree and step_bytes else None},
+                     "timing": f"HIP events around every k_step_rows / k_hist launch on the backend's stream, over "
+                               f"a repeat of the {psteps} timed iterations (same trees: "
+                               f"{'yes' if same_trees else 'NO'})",
                      "root_k_hist": {"launches": hist_launches, "achieved": root_gbps,
                                      "avg_launch_us": hist_ms / hist_launches * 1e3 if hist_launches else None}},
         "cpu_baseline": cpu,

@@ -321,6 +321,7 @@ struct GrowLeaf {
 struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipStream_t copy_stream = nullptr;  // a grown tree's readback, beside the kernels queued after the tree's steps
     std::string error;
     std::string device_name;
     uint32_t cus = 256;
@@ -376,6 +377,7 @@ struct Context {
     DevBuf<DevScales> d_scales;         // the boosting loop's quantization, made on the device (k_quant_spec)
     const DevScales *grow_dsc = nullptr;  // set while the boosting loop grows: the scales of GrowState
     hipEvent_t tree_event = nullptr;    // a grown tree's readback has landed
+    hipEvent_t steps_event = nullptr;   // a batch of split steps has ended (the readback waits for it)
     Pinned<double> h_leaf_vw[2];        // and on their way to the host (alternate trees, so one lands while the
                                         // host still reads the other)
     Pinned<float> h_lv;
@@ -405,6 +407,8 @@ struct Context {
             (void)hipEventDestroy(e.second);
         }
         for (auto e : prof.pool) (void)hipEventDestroy(e);
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
+        if (steps_event) (void)hipEventDestroy(steps_event);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -1598,10 +1602,16 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 else k_step_select<GROW_MAX_LEAVES><<<JMAX, 512, 0, stream>>>(g, sa2);
                 launch_check("k_step_select");
             }
-            if (after_steps) {  // queued behind the readback, so the host takes the tree while they run
+            if (after_steps) {
+                // the readback goes on its own stream once the steps end, so the kernels queued after the steps do
+                // not wait for the copy and the host takes the tree while they run (none of them writes the tree
+                // block, except k_tree_nodes' error flag for a malformed tree, which the host learns of anyway)
                 if (!tree_event) hip_check(hipEventCreateWithFlags(&tree_event, hipEventDisableTiming), "hipEventCreate");
-                hip_check(hipMemcpyAsync(hb, dtree.p, lay.bytes, hipMemcpyDeviceToHost, stream), "read tree");
-                hip_check(hipEventRecord(tree_event, stream), "event");
+                if (!steps_event) hip_check(hipEventCreateWithFlags(&steps_event, hipEventDisableTiming), "hipEventCreate");
+                hip_check(hipEventRecord(steps_event, stream), "event");
+                hip_check(hipStreamWaitEvent(copy_stream, steps_event, 0), "stream wait");
+                hip_check(hipMemcpyAsync(hb, dtree.p, lay.bytes, hipMemcpyDeviceToHost, copy_stream), "read tree");
+                hip_check(hipEventRecord(tree_event, copy_stream), "event");
                 (*after_steps)(g);
                 hip_check(hipEventSynchronize(tree_event), "event synchronize");
                 hc = *reinterpret_cast<const GrowCtl *>(hb + lay.ctl);
@@ -2050,6 +2060,7 @@ int srocm_create(int ordinal, void **out) {
         c->device_name = prop.name[0] ? prop.name : prop.gcnArchName;  // the name can be empty; the architecture is not
         c->scratch_at = scratch_address(dev);
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "create stream");
+        hip_check(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking), "create stream");
         c->h_u32.alloc(64);
         *out = c.release();
         g_create_error.clear();
