@@ -11,6 +11,7 @@
 #include "../../include/silvic_rocm.h"
 #include "kernels.hpp"
 #include "lambdarank.hpp"
+#include "rank_kernels.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -261,6 +262,7 @@ struct HostTree {
 // ---------------------------------------------------------------------------------------------------------
 
 constexpr uint32_t MAX_SLAB_FEATURES = 128;
+constexpr uint32_t RANK_DEVICE_MAX = 512;  // rows of the largest query k_rank_pairs takes
 constexpr uint32_t HIST_MIN_ROWS = 2048;   // rows per histogram workgroup before another one is used
 constexpr uint64_t ROW_BLOCK = 256;
 
@@ -388,6 +390,12 @@ struct Context {
 
     srocm_rank::Ranker ranker;  // lambdarank: the setup, the sigmoid and discount tables
     Pinned<float> h_rank_scores, h_rank_grad, h_rank_hess;
+    // lambdarank on the device (k_rank_pairs): the power of two its queries fit, 0 when a query has more rows than
+    // RANK_DEVICE_MAX (then the host computes every query); the setup, the tables and the per-row / per-query sums
+    uint32_t rank_nmax = 0;
+    DevBuf<uint32_t> d_rank_bounds;
+    DevBuf<double> d_rank_imd, d_rank_gain, d_rank_table, d_rank_disc, d_rank_lam, d_rank_hes, d_rank_qsum, d_rank_factor;
+    Pinned<double> h_rank_qsum, h_rank_factor;
 
     Profile prof;
     int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
@@ -463,9 +471,73 @@ struct Context {
         if (!obj->inverse_max_dcg) ranker.derive_inverse_max_dcg(t->label);
     }
 
-    // lambdarank gradients: the scores come to the host, the gradients are computed there (f64, every host thread)
-    // and go back; their maxima are taken on the device. Waits for the stream.
+    // The device's copy of the lambdarank setup, when every query fits k_rank_pairs (at most RANK_DEVICE_MAX rows).
+    void upload_ranking() {
+        const srocm_rank::Setup &st = ranker.setup();
+        const uint64_t nq = st.boundaries.size() - 1;
+        uint32_t biggest = 0;
+        for (uint64_t q = 0; q < nq; ++q) biggest = std::max(biggest, st.boundaries[q + 1] - st.boundaries[q]);
+        rank_nmax = 0;
+        if (biggest > RANK_DEVICE_MAX) return;
+        rank_nmax = 64;
+        while (rank_nmax < biggest) rank_nmax <<= 1;
+        d_rank_bounds.alloc(nq + 1);
+        d_rank_imd.alloc(nq);
+        d_rank_gain.alloc(st.label_gain.size());
+        d_rank_table.alloc(srocm_rank::SIGMOID_BINS);
+        d_rank_disc.alloc(srocm_rank::DISCOUNT_TABLE);
+        d_rank_lam.alloc(std::max<uint64_t>(rows, 1));
+        d_rank_hes.alloc(std::max<uint64_t>(rows, 1));
+        d_rank_qsum.alloc(nq);
+        d_rank_factor.alloc(nq);
+        h_rank_qsum.alloc(nq);
+        h_rank_factor.alloc(nq);
+        hip_check(hipMemcpy(d_rank_bounds.p, st.boundaries.data(), (nq + 1) * 4, hipMemcpyHostToDevice), "upload queries");
+        hip_check(hipMemcpy(d_rank_imd.p, st.inverse_max_dcg.data(), nq * 8, hipMemcpyHostToDevice), "upload max dcg");
+        hip_check(hipMemcpy(d_rank_gain.p, st.label_gain.data(), st.label_gain.size() * 8, hipMemcpyHostToDevice), "upload gains");
+        hip_check(hipMemcpy(d_rank_table.p, ranker.sigmoid_table().data(), srocm_rank::SIGMOID_BINS * 8, hipMemcpyHostToDevice),
+                  "upload sigmoid table");
+        hip_check(hipMemcpy(d_rank_disc.p, ranker.discounts().data(), srocm_rank::DISCOUNT_TABLE * 8, hipMemcpyHostToDevice),
+                  "upload discounts");
+    }
+
+    // lambdarank gradients (lambdarank.rs:190-420). On the device when the queries fit k_rank_pairs: the pair sums,
+    // then the per-query normalization factors log2(1 + s) / s on the host (one log2 a query; the sums come back and
+    // the factors go out, so this waits for the stream), then k_rank_scale. Otherwise the scores come to the host and
+    // the gradients are computed there (f64, every host thread) and go back. The maxima are taken on the device.
     void ranking_gradients() {
+        if (rank_nmax) {
+            const srocm_rank::Setup &st = ranker.setup();
+            const uint32_t nq = static_cast<uint32_t>(st.boundaries.size() - 1);
+            RankArgs ra{train.scores.p, label.p, d_rank_bounds.p, d_rank_imd.p, d_rank_gain.p, d_rank_table.p,
+                        d_rank_disc.p, st.sigmoid, st.sigmoid * st.sigmoid, ranker.min_input(), ranker.max_input(),
+                        ranker.idx_factor(), st.norm ? 1u : 0u, st.truncation_level, d_rank_lam.p, d_rank_hes.p,
+                        d_rank_qsum.p};
+            switch (rank_nmax) {
+            case 64: k_rank_pairs<64><<<nq, 64, 0, stream>>>(ra); break;
+            case 128: k_rank_pairs<128><<<nq, 64, 0, stream>>>(ra); break;
+            case 256: k_rank_pairs<256><<<nq, 64, 0, stream>>>(ra); break;
+            default: k_rank_pairs<512><<<nq, 64, 0, stream>>>(ra); break;
+            }
+            launch_check("k_rank_pairs");
+            const double *factor = nullptr;
+            if (st.norm) {
+                hip_check(hipMemcpyAsync(h_rank_qsum.p, d_rank_qsum.p, nq * 8, hipMemcpyDeviceToHost, stream), "read sums");
+                sync();
+                for (uint32_t q = 0; q < nq; ++q) {  // lambdarank.rs:287-300, as srocm_rank::Ranker takes it
+                    const double sl = h_rank_qsum.p[q];
+                    h_rank_factor.p[q] = sl > 0.0 ? std::log2(1.0 + sl) / sl : 1.0;
+                }
+                hip_check(hipMemcpyAsync(d_rank_factor.p, h_rank_factor.p, nq * 8, hipMemcpyHostToDevice, stream), "upload factors");
+                factor = d_rank_factor.p;
+            }
+            k_rank_scale<<<nq, 64, 0, stream>>>(d_rank_bounds.p, d_rank_lam.p, d_rank_hes.p, factor,
+                                                has_weight ? weight.p : nullptr, grad.p, hess.p);
+            launch_check("k_rank_scale");
+            k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, scalars.p + 1);
+            launch_check("k_max_abs");
+            return;
+        }
         h_rank_scores.alloc(rows);
         h_rank_grad.alloc(rows);
         h_rank_hess.alloc(rows);
@@ -581,6 +653,7 @@ struct Context {
             h_weight_v.assign(t->weight, t->weight + rows);
             hip_check(hipMemcpy(weight.p, t->weight, rows * sizeof(float), hipMemcpyHostToDevice), "upload weight");
         }
+        if (obj->kind == SROCM_OBJ_LAMBDARANK) upload_ranking();
         grad.alloc(rows);
         hess.alloc(rows);
         packed.alloc(rows);

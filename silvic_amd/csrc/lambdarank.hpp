@@ -22,6 +22,12 @@
 #include <thread>
 #include <vector>
 
+#ifdef __HIPCC__
+#define SRANK_HD __host__ __device__
+#else
+#define SRANK_HD
+#endif
+
 namespace srocm_rank {
 
 constexpr size_t SIGMOID_BINS = size_t(1) << 20;    // lambdarank.rs:28
@@ -40,12 +46,43 @@ struct Setup {
 };
 
 // A key whose ascending order is the score's descending order; +0.0f folds -0 into 0 (equal under `>`).
-inline uint32_t rank_key(float score) {
+SRANK_HD inline uint32_t rank_key(float score) {
     float s = score + 0.0f;
     uint32_t bits;
-    std::memcpy(&bits, &s, 4);
+    __builtin_memcpy(&bits, &s, 4);
     const uint32_t ascending = (bits >> 31) ? ~bits : (bits | 0x80000000u);
     return ~ascending;
+}
+
+// The pair probability from LightGBM's sigmoid table (lambdarank.rs:96-116): the clamped ends, else the bin of
+// (delta - min_input) * idx_factor. Shared by the host and the device, so both take the same f64 operations.
+SRANK_HD inline double table_probability(const double *table, double min_input, double max_input, double idx_factor,
+                                         double delta) {
+    if (delta <= min_input) return table[0];
+    if (delta >= max_input) return table[SIGMOID_BINS - 1];
+    const uint64_t at = static_cast<uint64_t>((delta - min_input) * idx_factor);
+    return table[at < SIGMOID_BINS - 1 ? at : SIGMOID_BINS - 1];
+}
+
+// One pair (i above j in the ranking, different labels) as lambdarank.rs:355-400 adds it: the sign, the lambda term
+// p_lambda and the hessian term. Shared by the host and the device.
+struct PairTerm {
+    double sign, p_lambda, p_hessian;
+};
+SRANK_HD inline PairTerm pair_term(double si, float li, double gi, double di, double sj, float lj, double gj, double dj,
+                                   double inv_max_dcg, bool by_distance, double sigmoid, double sigmoid2,
+                                   const double *table, double min_input, double max_input, double idx_factor) {
+    PairTerm t;
+    t.sign = li > lj ? 1.0 : -1.0;
+    const double delta_score = t.sign * (si - sj);
+    const double dcg_gap = t.sign * (gi - gj);
+    const double paired_discount = fabs(di - dj);
+    double delta_ndcg = dcg_gap * paired_discount * inv_max_dcg;
+    if (by_distance) delta_ndcg /= DISTANCE_EPSILON + fabs(delta_score);
+    const double p = table_probability(table, min_input, max_input, idx_factor, delta_score);
+    t.p_lambda = p * (-sigmoid * delta_ndcg);
+    t.p_hessian = p * (1.0 - p) * (sigmoid2 * delta_ndcg);
+    return t;
 }
 
 class Ranker {
@@ -60,6 +97,11 @@ public:
     }
 
     const Setup &setup() const { return setup_; }
+    const std::vector<double> &sigmoid_table() const { return table_; }
+    const std::vector<double> &discounts() const { return discount_; }
+    double min_input() const { return min_input_; }
+    double max_input() const { return max_input_; }
+    double idx_factor() const { return idx_factor_; }
 
     // DCG of the best ordering of a query's labels, truncated at k (lambdarank.rs:119-139): the labels in
     // descending order, each weighted by its rank's discount, summed in rank order.
@@ -133,13 +175,6 @@ private:
         table_sigmoid_ = sigmoid;
     }
 
-    double pair_probability(double delta) const {
-        if (delta <= min_input_) return table_[0];
-        if (delta >= max_input_) return table_[SIGMOID_BINS - 1];
-        const size_t at = static_cast<size_t>((delta - min_input_) * idx_factor_);
-        return table_[std::min(at, SIGMOID_BINS - 1)];
-    }
-
     double discount(size_t rank) const {
         return rank < DISCOUNT_TABLE ? discount_[rank] : 1.0 / std::log2(2.0 + static_cast<double>(rank));
     }
@@ -186,20 +221,14 @@ private:
             double lam_i = sc.lambda[i], hes_i = sc.hessian[i];
             for (size_t j = i + 1; j < valid; ++j) {
                 if (sc.lab[j] == li) continue;
-                const double sign = li > sc.lab[j] ? 1.0 : -1.0;
-                const double delta_score = sign * (si - sc.score[j]);
-                const double dcg_gap = sign * (gi - sc.gain[j]);
-                const double paired_discount = std::fabs(di - sc.disc[j]);
-                double delta_ndcg = dcg_gap * paired_discount * inv_max_dcg;
-                if (by_distance) delta_ndcg /= DISTANCE_EPSILON + std::fabs(delta_score);
-                const double p = pair_probability(delta_score);
-                const double p_lambda = p * (-sigmoid * delta_ndcg);
-                const double p_hessian = p * (1.0 - p) * (sigmoid2 * delta_ndcg);
-                lam_i += sign * p_lambda;
-                sc.lambda[j] -= sign * p_lambda;
-                hes_i += p_hessian;
-                sc.hessian[j] += p_hessian;
-                sum_lambdas -= 2.0 * p_lambda;
+                const PairTerm t = pair_term(si, li, gi, di, sc.score[j], sc.lab[j], sc.gain[j], sc.disc[j], inv_max_dcg,
+                                             by_distance, sigmoid, sigmoid2, table_.data(), min_input_, max_input_,
+                                             idx_factor_);
+                lam_i += t.sign * t.p_lambda;
+                sc.lambda[j] -= t.sign * t.p_lambda;
+                hes_i += t.p_hessian;
+                sc.hessian[j] += t.p_hessian;
+                sum_lambdas -= 2.0 * t.p_lambda;
             }
             sc.lambda[i] = lam_i;
             sc.hessian[i] = hes_i;

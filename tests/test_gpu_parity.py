@@ -538,6 +538,40 @@ def test_lambdarank_gradients_match_the_oracle():
         t.backend.close()
 
 
+# The device path (k_rank_pairs: every query of at most 512 rows) under other settings: no normalization, a short
+# truncation, row weights, sigmoid 2; and the host path (a query of more than 512 rows sends every query to the
+# host), both against the oracle bit for bit.
+@pytest.mark.parametrize("case", ["no norm, truncation 5", "weights, sigmoid 2", "one query of 700 rows"])
+def test_lambdarank_gradient_paths_match_the_oracle(case):
+    say("lambdarank gradients", case)
+    data = silvic_amd.synthetic(3, rows=60_000, seed=9)
+    kw = {}
+    if case.startswith("no norm"):
+        kw = dict(lambdarank_norm=False, lambdarank_truncation_level=5)
+    elif case.startswith("weights"):
+        data.weight = np.random.default_rng(3).uniform(0.5, 2.0, data.num_rows).astype(np.float32)
+        kw = dict(sigmoid=2.0)
+    else:
+        qb = data.query_boundaries
+        k = int(np.searchsorted(qb, 700))
+        data.query_boundaries = np.concatenate([[0], qb[k:]]).astype(qb.dtype)  # rows 0..qb[k] become one query
+        assert np.diff(data.query_boundaries).max() > 512
+    p = oracle.default_params(objective=_abi.OBJ_LAMBDARANK, **kw)
+    t = silvic_amd.Trainer(dict(objective="lambdarank", num_leaves=31, device_type="rocm", **kw), data)
+    try:
+        for step in range(3):
+            scores = t.backend.scores(0)
+            mg, mh = t.backend.compute_gradients()
+            g, h = t.backend.gradients()
+            og, oh = oracle.lambdarank_gradients(data, p, scores)
+            assert np.array_equal(g.view(np.uint32), og.view(np.uint32)), step
+            assert np.array_equal(h.view(np.uint32), oh.view(np.uint32)), step
+            assert mg == float(np.abs(og).max()) and mh == float(np.abs(oh).max())
+            t.step(1)
+    finally:
+        t.backend.close()
+
+
 @pytest.mark.parametrize("rows,params,rounds", [
     (200_000, dict(num_leaves=127), 6),
     (120_000, dict(num_leaves=63, bagging_fraction=0.7, bagging_freq=1, lambdarank_truncation_level=10), 5),
