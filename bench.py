@@ -17,6 +17,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "histogram bins/s + boosting iters/s at 10M×128 int8-quantized; % HBM peak"
+# The workloads: the headline (binary, the default) and two more shapes of the same path, each with its synthetic
+# configuration, objective, leaves and bins. Only the headline carries the metric above; the others name theirs.
+WORKLOADS = {
+    "binary": dict(config=2, rows=10_000_000, cols=128, leaves=255, max_bin=255, objective="binary",
+                   describe="binary, {rows} rows x {cols} f32 features binned to <=255 bins (half N(0,1), quarter "
+                            "lognormal, quarter integers, 10% NaN), {leaves} leaves, num_grad_quant_bins=4"),
+    "lambdarank": dict(config=3, rows=2_000_000, cols=136, leaves=127, max_bin=255, objective="lambdarank",
+                       describe="lambdarank NDCG, {rows} documents in queries of 10-200 (Zipf-like), {cols} f32 "
+                                "features, labels 0-4, <=255 bins, {leaves} leaves, truncation 30, "
+                                "num_grad_quant_bins=4"),
+    "wide": dict(config=5, rows=50_000_000, cols=32, leaves=2047, max_bin=1023, objective="regression",
+                 describe="L2 regression, {rows} rows x {cols} U[0,1) f32 features binned to <=1023 bins (two-byte "
+                          "bins), piecewise-constant target, {leaves} leaves, num_grad_quant_bins=4"),
+}
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "split_step_traffic_10Mx128.md")
 
@@ -224,9 +238,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--cols", type=int, default=128)
-    ap.add_argument("--leaves", type=int, default=255)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="binary",
+                    help="binary: the headline 10M x 128 workload; lambdarank: 2M documents x 136; wide: 50M x 32 at "
+                         "1023 bins and 2047 leaves")
+    ap.add_argument("--rows", type=int, default=None)
+    ap.add_argument("--cols", type=int, default=None)
+    ap.add_argument("--leaves", type=int, default=None)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of oracle work for the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -239,6 +256,10 @@ def main():
                     help="no GPU: per-iteration kernel times of a rocprofv3 --kernel-trace run of this script over "
                          "its timed iterations (--warmup, --steps as in the run)")
     args = ap.parse_args()
+    wl = WORKLOADS[args.workload]
+    args.rows = wl["rows"] if args.rows is None else args.rows
+    args.cols = wl["cols"] if args.cols is None else args.cols
+    args.leaves = wl["leaves"] if args.leaves is None else args.leaves
     if args.pmc_summary:
         pmc_summary(args)
         return
@@ -261,11 +282,10 @@ def main():
         copy_calibration(args.calibrate_copy << 20)
 
     t0 = time.perf_counter()
-    data = silvic_amd.synthetic(2, rows=args.rows, cols=args.cols, seed=7)
-    log(f"generated {args.rows} x {args.cols} in {time.perf_counter() - t0:.1f}s; total_bins {data.total_bins}")
-    params = {"objective": "binary", "num_leaves": args.leaves, "max_bin": 255, "num_grad_quant_bins": 4,
-              "device_type": "rocm"}
-    params.pop("max_bin")
+    data = silvic_amd.synthetic(wl["config"], rows=args.rows, cols=args.cols, seed=7, max_bin=wl["max_bin"])
+    log(f"generated {args.workload}: {args.rows} x {args.cols} in {time.perf_counter() - t0:.1f}s; total_bins "
+        f"{data.total_bins}")
+    params = {"objective": wl["objective"], "num_leaves": args.leaves, "num_grad_quant_bins": 4, "device_type": "rocm"}
     t0 = time.perf_counter()
     trainer = silvic_amd.Trainer(params, data)
     log(f"loaded on {trainer.backend.name()} in {time.perf_counter() - t0:.1f}s")
@@ -305,7 +325,7 @@ def main():
     # every histogram is built by k_hist (roots) or k_step_rows (split steps, which also partition)
     bins_per_s = hist_bins / ((hist_ms + step_ms) / 1e3) if hist_ms + step_ms else 0.0
     step_gbps = step_bytes / (step_ms / 1e3) / 1e9 if step_ms else 0.0
-    default_workload = (args.rows, args.cols, args.leaves) == (10_000_000, 128, 255)
+    default_workload = args.workload == "binary" and (args.rows, args.cols, args.leaves) == (10_000_000, 128, 255)
     traffic = measured_traffic("k_step_rows<128", "launch") if default_workload else None
     traffic_tree = measured_traffic("k_step_rows<128", "tree") if default_workload else None
     root_gbps = hist_bytes / (hist_ms / 1e3) / 1e9 if hist_ms else 0.0
@@ -321,13 +341,15 @@ def main():
 
         oracle.set_threads(0)
         threads = oracle.threads()
-        p = oracle.default_params(objective=_abi.OBJ_BINARY, num_leaves=args.leaves, num_iterations=1)
+        objective = {"binary": _abi.OBJ_BINARY, "lambdarank": _abi.OBJ_LAMBDARANK,
+                     "regression": _abi.OBJ_REGRESSION}[wl["objective"]]
+        p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=1)
         t0 = time.perf_counter()
         m1 = oracle.train(data, p)
         one = time.perf_counter() - t0
         n_cpu = max(1, min(args.warmup + steps, int(args.cpu_budget / max(one, 1e-3))))
         if n_cpu > 1:
-            p = oracle.default_params(objective=_abi.OBJ_BINARY, num_leaves=args.leaves, num_iterations=n_cpu)
+            p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=n_cpu)
             t0 = time.perf_counter()
             m = oracle.train(data, p)
             cpu_elapsed = time.perf_counter() - t0
@@ -346,14 +368,16 @@ def main():
         log(f"oracle: {len(m.trees)} iterations in {cpu_elapsed:.1f}s on {threads} threads; "
             f"trees identical to the device's: {same}/{compared}")
         cpu = {"value": cpu_iters, "unit": "iters/s", "cores": threads, "kind": "port",
-               "sample": f"{len(m.trees)} boosting iterations of the same {args.rows}x{args.cols} binary workload "
+               "sample": f"{len(m.trees)} boosting iterations of the same {args.rows}x{args.cols} {args.workload} workload "
                          f"({args.leaves} leaves), oracle (C++ restatement of silvic's CPU trainer) on {threads} "
                          f"threads",
                "hist_bins_per_s": m.hist_bins / m.times["histogram"] if m.times["histogram"] else None,
                "trees_identical": f"{same}/{compared}", "seconds": cpu_elapsed}
 
+    describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves)
+    slab = "k_step_rows<128, true>" if wl["max_bin"] > 255 else "k_step_rows<128>"
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == "binary" else f"boosting iters/s, {args.workload} workload; % HBM peak",
         "value": iters_per_s,
         "unit": "iters/s",
         "n_gpus": 1,
@@ -365,9 +389,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8-quantized gradients (integer histograms), f64 split search",
         "data": "synthetic",
-        "config": {"workload": f"binary, {args.rows} rows x {args.cols} f32 features binned to <=255 bins "
-                               f"(half N(0,1), quarter lognormal, quarter integers, 10% NaN), {args.leaves} leaves, "
-                               "num_grad_quant_bins=4", "rows": args.rows, "features": args.cols,
+        "config": {"workload": describe, "rows": args.rows, "features": args.cols,
                    "num_leaves": args.leaves, "total_bins": data.total_bins, "parallelism": "single GPU"},
         "hist_bins_per_s": bins_per_s,
         "step_kernel_ms_per_iter": step_ms / psteps,
@@ -375,7 +397,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": step_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": step_gbps / HBM_PEAK_GBPS, "traffic": traffic,
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic else None,
-                     "kernel": "k_step_rows<128> (split step: stable partition + built-child histogram)",
+                     "kernel": f"{slab} (split step: stable partition + built-child histogram)",
                      "launches": step_launches, "avg_launch_us": step_ms / step_launches * 1e3 if step_launches else None,
                      "bytes_per_launch": step_bytes / step_launches if step_launches else None,
                      "per_tree": {"launches": step_launches / psteps, "kernel_ms": step_ms / psteps,
