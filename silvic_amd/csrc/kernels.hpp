@@ -2282,7 +2282,9 @@ struct AdvShared {
     uint16_t cand[CAND];                  // speculation candidates
     uint32_t rkey[MAXL > LEAVES_SMALL ? MAXL : 1];  // committed leaf's replay key (replay_lds)
     uint16_t job_t[JMAX];
-    uint32_t ncand, ncommit, n, blocker, done, njobs;
+    uint64_t skey[JMAX];                  // select_top: the selected candidates' keys
+    uint16_t scand[JMAX];                 // and leaves
+    uint32_t ncand, ncommit, n, blocker, done, njobs, band, above, nsel;
 };
 
 __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
@@ -2520,7 +2522,8 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             const uint32_t bp = best >> IDB;
             bool other = lane != (x & 63u) && (lk >> IDB) == bp;
             if (lane == (x & 63u)) {
-                for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {  // unrolled: the LDS reads issue together
                     const uint32_t kj = s.rkey[lane + 64u * j];
                     other = other || ((kj >> IDB) == bp && kj != best);
                 }
@@ -2583,6 +2586,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         }
         if (lane == lx || lane == ln) {
             uint32_t mx = 0;
+#pragma unroll
             for (int j = 0; j < NPL; ++j) {
                 const uint32_t kj = s.rkey[lane + 64u * j];
                 mx = kj > mx ? kj : mx;
@@ -2604,6 +2608,78 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         s.n = n;
         s.done = done ? 1u : 0u;
         s.blocker = blocker;
+    }
+}
+
+// The `spec` highest of the `ncand` candidate keys s.ckey (distinct 64-bit keys) into s.job_t[1 .. spec], in key
+// order, by a radix selection over the keys' 64 bits, 8 at a time from the top: a 256-bucket count of the
+// candidates that still match the prefix found so far, the bucket where the count from the top reaches what is
+// left to take, and the candidates above it taken. Every key is distinct, so after at most 8 rounds the prefix
+// is a whole key. Block-wide; s.crank holds the counts.
+template <uint32_t MAXL>
+__device__ void select_top(AdvShared<MAXL> &s, uint32_t ncand, uint32_t spec) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, nt = blockDim.x;
+    uint32_t *count = s.crank;  // 256 buckets
+    uint64_t prefix = 0, mask = 0;  // the bits fixed so far
+    uint32_t taken = 0;             // candidates above the prefix, all taken
+    if (tid == 0) s.nsel = 0;
+    for (int shift = 56; shift >= 0 && taken < spec; shift -= 8) {
+        for (uint32_t i = tid; i < 256u; i += nt) count[i] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < ncand; i += nt) {
+            const uint64_t k = s.ckey[i];
+            if ((k & mask) == prefix) atomicAdd(&count[static_cast<uint32_t>(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {  // lane l: buckets 255 - 4 l down to 252 - 4 l
+            uint32_t c = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) c += count[255u - 4u * lane - static_cast<uint32_t>(q)];
+            const uint32_t incl = wave_incl_sum(c), before = incl - c;
+            const unsigned long long hit = __ballot(taken + incl >= spec);
+            if (lane == static_cast<uint32_t>(__builtin_ctzll(hit))) {  // the total reaches it: some lane hits
+                uint32_t above = before, b = 255u - 4u * lane;
+                for (int q = 0; q < 4; ++q, --b) {
+                    if (taken + above + count[b] >= spec) break;
+                    above += count[b];
+                }
+                s.band = b;
+                s.above = above;
+            }
+        }
+        __syncthreads();
+        const uint32_t b = s.band, above = s.above, cb = count[b];  // read before the counts are cleared again
+        // every matching candidate above bucket b is in
+        for (uint32_t i = tid; i < ncand; i += nt) {
+            const uint64_t k = s.ckey[i];
+            if ((k & mask) == prefix && (static_cast<uint32_t>(k >> shift) & 255u) > b) {
+                const uint32_t at = atomicAdd(&s.nsel, 1u);
+                s.skey[at] = k;
+                s.scand[at] = s.cand[i];
+            }
+        }
+        taken += above;
+        prefix |= static_cast<uint64_t>(b) << shift;
+        mask |= uint64_t(255) << shift;
+        __syncthreads();
+        if (taken + cb == spec) {  // uniform: bucket b completes the selection (always so once the key is whole)
+            for (uint32_t i = tid; i < ncand; i += nt) {
+                const uint64_t k = s.ckey[i];
+                if ((k & mask) == prefix) {
+                    const uint32_t at = atomicAdd(&s.nsel, 1u);
+                    s.skey[at] = k;
+                    s.scand[at] = s.cand[i];
+                }
+            }
+            taken = spec;
+            __syncthreads();
+        }
+    }
+    if (tid < spec) {  // the selected ones in key order
+        const uint64_t ki = s.skey[tid];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < spec; ++j) rank += s.skey[j] > ki ? 1u : 0u;
+        s.job_t[1 + rank] = s.scand[tid];
     }
 }
 
@@ -2721,21 +2797,26 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     if (spec > room_t) spec = room_t;
     if (spec > room_s) spec = room_s;
     if (spec > ncand) spec = ncand;
-    // the spec highest keys; the blocker is job 0. Which leaves are expanded early changes no result (every
-    // expansion is the one its leaf gets when the replay reaches it), only the work done ahead. A candidate's rank
-    // (keys above its own) is summed over `nsl` slices of the others, one thread each.
-    const uint32_t nsl = ncand && ncand < nt ? nt / ncand : 1u;
-    for (uint32_t w = tid; w < ncand * nsl; w += nt) {
-        const uint32_t i = w % ncand, sl = w / ncand;
-        const uint64_t ki = s.ckey[i];
-        uint32_t rank = 0;
+    // The spec highest keys; the blocker is job 0. Which leaves are expanded early changes no result (every
+    // expansion is the one its leaf gets when the replay reaches it), only the work done ahead. Up to 512 candidates,
+    // each one's rank (keys above its own) is summed over `nsl` slices of the others, one thread each; beyond that
+    // (trees of thousands of leaves), a radix selection finds the spec-th key in linear passes.
+    if (ncand <= 512u) {
+        const uint32_t nsl = ncand && ncand < nt ? nt / ncand : 1u;
+        for (uint32_t w = tid; w < ncand * nsl; w += nt) {
+            const uint32_t i = w % ncand, sl = w / ncand;
+            const uint64_t ki = s.ckey[i];
+            uint32_t rank = 0;
 #pragma unroll 8
-        for (uint32_t j = sl; j < ncand; j += nsl) rank += s.ckey[j] > ki ? 1u : 0u;
-        atomicAdd(&s.crank[i], rank);
+            for (uint32_t j = sl; j < ncand; j += nsl) rank += s.ckey[j] > ki ? 1u : 0u;
+            atomicAdd(&s.crank[i], rank);
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < ncand; i += nt)
+            if (s.crank[i] < spec) s.job_t[1 + s.crank[i]] = s.cand[i];
+    } else {
+        select_top<MAXL>(s, ncand, spec);
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < ncand; i += nt)
-        if (s.crank[i] < spec) s.job_t[1 + s.crank[i]] = s.cand[i];
     if (tid == 0) {
         s.job_t[0] = static_cast<uint16_t>(blocker);
         s.njobs = 1 + spec;
@@ -3470,44 +3551,42 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
         if (lane == 0) s_out[ch] = out;
     }
     __syncthreads();
+    // the children's best splits, copied a dword a thread (no child-sized copy through one thread's stack)
+    static_assert(sizeof(SplitOut) % 4 == 0 && sizeof(SplitOut) / 4 <= 64, "a split copies in one wave");
+    if (threadIdx.x < 128) {
+        const uint32_t ch = threadIdx.x >> 6, d = threadIdx.x & 63u;
+        if (d < sizeof(SplitOut) / 4)
+            reinterpret_cast<uint32_t *>(&g.tl[kid + static_cast<int32_t>(ch)].best)[d] =
+                reinterpret_cast<const uint32_t *>(&s_out[ch])[d];
+    }
     if (threadIdx.x == 0) {
-        const TLeaf &pl = g.tl[J.t];
-        const SplitOut &info = pl.best;
-        TLeaf l = {}, r = {};
-        l.begin = J.begin;
-        l.count = J.left;
-        r.begin = J.begin + J.left;
-        r.count = J.count - J.left;
-        l.ug = info.left_grad;
-        l.uh = info.left_hess;
-        r.ug = info.right_grad;
-        r.uh = info.right_hess;
-        l.cnt = left;
-        r.cnt = right;
-        l.buf = r.buf = 1u - J.src_buf;
-        l.rev = 0;  // the split step writes the left child first-first and the right child last-first
-        r.rev = 1;
-        l.depth = r.depth = depth;
-        l.state = r.state = T_LEAF;
-        l.kid = r.kid = -1;
+        const SplitOut &info = g.tl[J.t].best;
+        const uint32_t has[2] = {s_out[0].found ? 1u : 0u, s_out[1].found ? 1u : 0u};
+        const double gain[2] = {s_out[0].gain, s_out[1].gain};
         const double lv = info.left_output, rv = info.right_output;
-        l.value = lv != lv ? 0.0 : lv;
-        r.value = rv != rv ? 0.0 : rv;
-        l.weight = info.left_hess * grow_sh(g);
-        r.weight = info.right_hess * grow_sh(g);
-        l.slot = r.slot = -1;
-        if (searched) {
-            l.slot = J.built_side == 0 ? J.built_slot : J.parent_slot;
-            r.slot = J.built_side == 0 ? J.parent_slot : J.built_slot;
-            l.best = s_out[0];
-            r.best = s_out[1];
-            l.has_best = s_out[0].found ? 1u : 0u;
-            r.has_best = s_out[1].found ? 1u : 0u;
+        const double lh = info.left_hess, rh = info.right_hess;
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ++ch) {
+            TLeaf &c = g.tl[kid + static_cast<int32_t>(ch)];
+            c.begin = ch == 0 ? J.begin : J.begin + J.left;
+            c.count = ch == 0 ? J.left : J.count - J.left;
+            c.ug = ch == 0 ? info.left_grad : info.right_grad;
+            c.uh = ch == 0 ? lh : rh;
+            c.cnt = ch == 0 ? left : right;
+            // the built child's histogram goes to the job's new slot, the other child keeps its parent's
+            c.slot = searched ? ((J.built_side == ch) ? J.built_slot : J.parent_slot) : -1;
+            c.has_best = searched ? has[ch] : 0u;
+            c.buf = 1u - J.src_buf;
+            c.rev = ch;  // the split step writes the left child first-first and the right child last-first
+            c.depth = depth;
+            c.state = T_LEAF;
+            c.kid = -1;
+            c.pad_ = 0;
+            const double v = ch == 0 ? lv : rv;
+            c.value = v != v ? 0.0 : v;
+            c.weight = (ch == 0 ? lh : rh) * grow_sh(g);
+            g.tk[kid + static_cast<int32_t>(ch)] = TKey{gain[ch], searched ? has[ch] : 0u, T_LEAF, -1, 0u};
         }
-        g.tl[kid] = l;
-        g.tl[kid + 1] = r;
-        g.tk[kid] = TKey{l.best.gain, l.has_best, T_LEAF, -1, 0u};
-        g.tk[kid + 1] = TKey{r.best.gain, r.has_best, T_LEAF, -1, 0u};
         g.tl[J.t].state = T_EXPANDED;
         g.tk[J.t].state = T_EXPANDED;
         if (J.hist) {  // the built child's histogram was made, searched or not
