@@ -2280,7 +2280,6 @@ struct AdvShared {
     uint64_t ckey[CAND];                  // speculation candidates' keys: higher gain (as f32), then lower leaf
     uint32_t crank[CAND];                 // and their ranks
     uint16_t cand[CAND];                  // speculation candidates
-    uint32_t rkey[MAXL > LEAVES_SMALL ? MAXL : 1];  // committed leaf's replay key (replay_lds)
     uint16_t job_t[JMAX];
     uint64_t skey[JMAX];                  // select_top: the selected candidates' keys
     uint16_t scand[JMAX];                 // and leaves
@@ -2467,10 +2466,10 @@ __device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
     }
 }
 
-// The replay for trees of more than 512 leaves: as replay, with each committed leaf's key, speculative leaf and node
-// above in LDS (s.rkey, s.leaf_t, s.pnode) rather than in registers, and each lane's largest key cached in a
-// register, which only the lanes owning the two leaves a commit changes recompute. The left / changed / has-split /
-// NaN-gain flags stay in registers, one bit per leaf of the lane. A lane other than the winner's holds a key with the
+// The replay for trees of more than 512 leaves: as replay, with each committed leaf's speculative leaf and node
+// above in LDS (s.leaf_t, s.pnode) rather than in registers; the keys stay in registers (NPL a lane), with each
+// lane's largest key cached, which only the lanes owning the two leaves a commit changes recompute. The left /
+// changed / has-split / NaN-gain flags are per-lane bitmasks. A lane other than the winner's holds a key with the
 // winner's gain prefix exactly when its largest key has that prefix, so the exact f64 argmax runs only when one does.
 template <int NPL, typename S>
 __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
@@ -2479,6 +2478,8 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     constexpr uint32_t IDM = (1u << IDB) - 1u;
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t rl = 0, rtouch = 0, rhas = 0, rnan = 0, lk = 0;
+    uint32_t rk[NPL];  // the lane's leaves' replay keys
+#pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const uint32_t id = lane + 64u * j;
         uint32_t key = 0;
@@ -2491,7 +2492,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             rhas |= (m & 1u) ? 1u << j : 0u;
             rnan |= (m & 1u) && gj != gj ? 1u << j : 0u;
         }
-        s.rkey[id] = key;
+        rk[j] = key;
         lk = key > lk ? key : lk;
     }
     uint32_t n = n0, nc = 0, blocker = 0;
@@ -2522,18 +2523,18 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             const uint32_t bp = best >> IDB;
             bool other = lane != (x & 63u) && (lk >> IDB) == bp;
             if (lane == (x & 63u)) {
+                uint32_t hit = 0;
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) {  // unrolled: the LDS reads issue together
-                    const uint32_t kj = s.rkey[lane + 64u * j];
-                    other = other || ((kj >> IDB) == bp && kj != best);
-                }
+                for (int j = 0; j < NPL; ++j) hit |= ((rk[j] >> IDB) == bp && rk[j] != best) ? 1u : 0u;
+                other = other || hit != 0u;
             }
             if (__ballot(other)) {
                 double kg = 0.0;
                 int ki = -1;
+#pragma unroll
                 for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
                     const uint32_t id = lane + 64u * j;
-                    if ((s.rkey[id] >> IDB) != bp) continue;
+                    if ((rk[j] >> IDB) != bp) continue;
                     const double gj = s.gain[s.leaf_t[id]];
                     if (ki < 0 || gj >= kg) {
                         kg = gj;
@@ -2569,7 +2570,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         if (lane == lx) {
             s.leaf_t[x] = static_cast<uint16_t>(kid);
             s.pnode[x] = static_cast<int16_t>(node);
-            s.rkey[x] = replay_key<IDB>(g0, m0, x);
+            rk[jx] = replay_key<IDB>(g0, m0, x);  // jx is wave-uniform: an indexed register move
             rl |= bx;
             rtouch |= bx;
             rhas = (rhas & ~bx) | ((m0 & 1u) ? bx : 0u);
@@ -2578,7 +2579,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         if (lane == ln) {
             s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
             s.pnode[n] = static_cast<int16_t>(node);
-            s.rkey[n] = replay_key<IDB>(g1, m1, n);
+            rk[jn] = replay_key<IDB>(g1, m1, n);
             rl &= ~bn;
             rtouch |= bn;
             rhas = (rhas & ~bn) | ((m1 & 1u) ? bn : 0u);
@@ -2587,10 +2588,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         if (lane == lx || lane == ln) {
             uint32_t mx = 0;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-                const uint32_t kj = s.rkey[lane + 64u * j];
-                mx = kj > mx ? kj : mx;
-            }
+            for (int j = 0; j < NPL; ++j) mx = rk[j] > mx ? rk[j] : mx;
             lk = mx;
         }
         ++nc;
