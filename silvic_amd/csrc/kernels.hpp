@@ -2387,15 +2387,9 @@ __device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
             }
         }
         const uint32_t jx = x >> 6, lx = x & 63u;
-        uint32_t vm = 0, vt = 0;
-        int32_t vp = 0;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j)
-            if (jx == static_cast<uint32_t>(j)) {
-                vm = rm[j];
-                vt = rt[j];
-                vp = rp[j];
-            }
+        // jx is wave-uniform: indexed register reads
+        const uint32_t vm = rm[jx], vt = rt[jx];
+        const int32_t vp = rp[jx];
         const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vm), lx));
         const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(vt), lx));
         if (((m >> 1) & 3u) != T_EXPANDED) {
@@ -2416,21 +2410,18 @@ __device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
         // leaf x becomes the left child, leaf n the right one, both under node n - 1
         const int32_t node = static_cast<int32_t>(n) - 1;
         const uint32_t jn = n >> 6, ln = n & 63u;
-        // (jx and jn are wave-uniform: one register slot is touched for each)
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-            if (jx == static_cast<uint32_t>(j) && lane == lx) {
-                rt[j] = kid;
-                rk[j] = replay_key<IDB>(g0, m0, x);
-                rm[j] = m0;
-                rp[j] = node;
-            }
-            if (jn == static_cast<uint32_t>(j) && lane == ln) {
-                rt[j] = kid + 1;
-                rk[j] = replay_key<IDB>(g1, m1, n);
-                rm[j] = m1;
-                rp[j] = node;
-            }
+        // (jx and jn are wave-uniform: indexed register moves, one slot each)
+        if (lane == lx) {
+            rt[jx] = kid;
+            rk[jx] = replay_key<IDB>(g0, m0, x);
+            rm[jx] = m0;
+            rp[jx] = node;
+        }
+        if (lane == ln) {
+            rt[jn] = kid + 1;
+            rk[jn] = replay_key<IDB>(g1, m1, n);
+            rm[jn] = m1;
+            rp[jn] = node;
         }
         const uint32_t bx = 1u << jx, bn = 1u << jn;
         if (lane == lx) {
