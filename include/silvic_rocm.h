@@ -219,8 +219,9 @@ typedef struct srocm_grown_tree {
     int32_t *leaf_parent;
     int32_t *leaf_depth;
     srocm_leaf_range *leaf_range;
-    /* per internal node, 8 words: the bins that go left (BinSplit::left_bins); a categorical node has
-     * threshold_bin 0 and default_left 0. May be null. */
+    /* per internal node, 8 words: the bins that go left (BinSplit::left_bins; for a feature of a 2-byte group, the
+     * numerical rule of srocm_group.bin_bytes); a categorical node has threshold_bin 0 and default_left 0. May be
+     * null. */
     uint32_t *left_bins;
 } srocm_grown_tree;
 
