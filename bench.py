@@ -27,6 +27,9 @@ WORKLOADS = {
                        describe="lambdarank NDCG, {rows} documents in queries of 10-200 (Zipf-like), {cols} f32 "
                                 "features, labels 0-4, <=255 bins, {leaves} leaves, truncation 30, "
                                 "num_grad_quant_bins=4"),
+    "sparse": dict(config=4, rows=1_000_000, cols=2000, leaves=63, max_bin=63, objective="binary",
+                   describe="binary, {rows} rows x {cols} f32 features, 98% exact zeros (nonzeros exp(1) or integers "
+                            "of cardinality 2-16), binned to <=63 bins, {leaves} leaves, num_grad_quant_bins=4"),
     "wide": dict(config=5, rows=50_000_000, cols=32, leaves=2047, max_bin=1023, objective="regression",
                  describe="L2 regression, {rows} rows x {cols} U[0,1) f32 features binned to <=1023 bins (two-byte "
                           "bins), piecewise-constant target, {leaves} leaves, num_grad_quant_bins=4"),
@@ -239,8 +242,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="binary",
-                    help="binary: the headline 10M x 128 workload; lambdarank: 2M documents x 136; wide: 50M x 32 at "
-                         "1023 bins and 2047 leaves")
+                    help="binary: the headline 10M x 128 workload; lambdarank: 2M documents x 136; sparse: 1M x 2000 "
+                         "mostly-zero features of <=63 bins; wide: 50M x 32 at 1023 bins and 2047 leaves")
     ap.add_argument("--rows", type=int, default=None)
     ap.add_argument("--cols", type=int, default=None)
     ap.add_argument("--leaves", type=int, default=None)

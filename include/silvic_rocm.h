@@ -58,12 +58,15 @@ typedef struct srocm_feature {
     uint32_t nan_bin;     /* numerical: 1 when bin num_bins-1 holds NaN (MissingType::NaN) */
 } srocm_feature;
 
-/* FeatureGroup (crates/silvic-core/src/data/mod.rs:48-59), plus `bin_bytes`, an extension the reference does not
- * have (it rejects max_bin > 255, config.rs:407-412): 0 or 1 for silvic's byte bins; 2 for a group of numerical
- * features with up to 1024 bins each, stored as little-endian u16 at byte offset `column` of the row. A split on a
- * feature of a 2-byte group (srocm_bin_split, srocm_device_node, srocm_grown_tree.left_bins) encodes its numerical
- * rule in place of the 256-bit mask: left_bins[0] is the threshold (bins 0..=threshold go left), left_bins[1] is
- * the NaN bin + 1 when missing values go left (0 otherwise), the other words are 0. */
+/* FeatureGroup (crates/silvic-core/src/data/mod.rs:48-59), plus `bin_bits`, an extension the reference does not
+ * have (its bins are always bytes, and it rejects max_bin > 255, config.rs:407-412):
+ *   0 or 8: silvic's byte bins, data[row * row_stride + column];
+ *   16: numerical features of up to 1024 bins, each bin a little-endian u16 at byte offset `column` of the row;
+ *   4:  features of up to 16 bins, two to a byte: `column` counts 4-bit slots, slot c is the low half of byte c / 2
+ *       when c is even, the high half when it is odd.
+ * A split on a feature of a 16-bit group (srocm_bin_split, srocm_device_node, srocm_grown_tree.left_bins) encodes its
+ * numerical rule in place of the 256-bit mask: left_bins[0] is the threshold (bins 0..=threshold go left),
+ * left_bins[1] is the NaN bin + 1 when missing values go left (0 otherwise), the other words are 0. */
 typedef struct srocm_group {
     uint32_t row_stride;      /* bytes per row, the feature bytes rounded up to 4 */
     uint32_t hist_offset;     /* index of the group's first bin in the flat histogram */
@@ -71,7 +74,7 @@ typedef struct srocm_group {
     uint32_t num_features;
     const uint32_t *features; /* indices into the dataset's features, in column order */
     const uint8_t *data;      /* row-major bins: data[row * row_stride + column] */
-    uint32_t bin_bytes;       /* 0 or 1: u8 bins; 2: u16 bins (extension) */
+    uint32_t bin_bits;        /* 0 or 8: u8 bins; 16: u16 bins; 4: two bins a byte (extensions) */
 } srocm_group;
 
 /* BinnedDataset (crates/silvic-core/src/data/mod.rs:61-74). */
@@ -220,7 +223,7 @@ typedef struct srocm_grown_tree {
     int32_t *leaf_depth;
     srocm_leaf_range *leaf_range;
     /* per internal node, 8 words: the bins that go left (BinSplit::left_bins; for a feature of a 2-byte group, the
-     * numerical rule of srocm_group.bin_bytes); a categorical node has threshold_bin 0 and default_left 0. May be
+     * numerical rule of srocm_group.bin_bits); a categorical node has threshold_bin 0 and default_left 0. May be
      * null. */
     uint32_t *left_bins;
 } srocm_grown_tree;

@@ -534,10 +534,13 @@ constexpr size_t DENSE_RUN_NUM = 3;          // cpu.rs:39
 constexpr size_t DENSE_RUN_DEN = 4;          // cpu.rs:40
 constexpr uint64_t ROW_CHUNK = 8192;         // cpu.rs:42
 
+// A group's bits per bin: 8 (0 means 8, silvic's bytes), or the extensions 16 and 4.
+inline uint32_t group_bits(const srocm_group &g) { return g.bin_bits == 0 ? 8u : g.bin_bits; }
+
 // cpu.rs:46-99 GroupLayout
 struct GroupLayout {
     size_t group = 0, stride = 0, hist_offset = 0, bins = 0;
-    size_t bin_bytes = 1;  // 2: u16 bins (the extension for more than 256 bins; no counterpart in cpu.rs)
+    size_t bits = 8;  // 16: u16 bins, 4: two bins a byte (extensions; no counterpart in cpu.rs)
     std::vector<int64_t> column_features;  // -1: no feature
     std::vector<size_t> offsets;
     std::vector<std::pair<uint32_t, uint32_t>> runs;
@@ -586,7 +589,8 @@ std::vector<GroupLayout> group_layout(const srocm_dataset *d) {
         L.bins = g.total_bins;
         L.stride = g.row_stride;
         L.hist_offset = g.hist_offset;
-        L.bin_bytes = g.bin_bytes == 2 ? 2 : 1;
+        L.bits = group_bits(g);
+        if (L.bits != 4 && L.bits != 8 && L.bits != 16) throw std::runtime_error("a group's bins are 4, 8 or 16 bits");
         size_t width = 0;
         for (uint32_t k = 0; k < g.num_features; ++k)
             width = std::max<size_t>(width, d->features[g.features[k]].column + 1);
@@ -595,12 +599,13 @@ std::vector<GroupLayout> group_layout(const srocm_dataset *d) {
         for (uint32_t k = 0; k < g.num_features; ++k) {
             uint32_t f = g.features[k];
             const srocm_feature &m = d->features[f];
-            if (m.hist_offset < g.hist_offset || m.hist_offset - g.hist_offset + m.num_bins > L.bins ||
-                m.column + L.bin_bytes > L.stride)
+            const size_t end_byte = L.bits == 4 ? m.column / 2 + 1 : m.column + L.bits / 8;
+            if (m.hist_offset < g.hist_offset || m.hist_offset - g.hist_offset + m.num_bins > L.bins || end_byte > L.stride)
                 throw std::runtime_error("feature lies outside its group's bins or row");
-            if (L.bin_bytes == 2 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
+            if (L.bits == 16 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
                 throw std::runtime_error("a 2-byte group holds numerical features of at most 1024 bins");
-            if (L.bin_bytes == 1 && m.num_bins > 256) throw std::runtime_error("a feature of more than 256 byte bins");
+            if (L.bits == 8 && m.num_bins > 256) throw std::runtime_error("a feature of more than 256 byte bins");
+            if (L.bits == 4 && m.num_bins > 16) throw std::runtime_error("a feature of more than 16 4-bit bins");
             L.column_features[m.column] = f;
             L.offsets[m.column] = m.hist_offset - g.hist_offset;
         }
@@ -622,23 +627,28 @@ inline uint32_t bin16(const uint8_t *row, size_t column) {
     return static_cast<uint32_t>(row[column]) | (static_cast<uint32_t>(row[column + 1]) << 8);
 }
 
-// The bin of a row's feature at byte offset `column` of a group with `bin_bytes`.
+// The 4-bit bin in slot `column` of a row (two to a byte, the low half first).
+inline uint32_t bin4(const uint8_t *row, size_t column) { return (row[column / 2] >> (4 * (column % 2))) & 15u; }
+
+// The bin of a row's feature in column `column` of a group (a byte offset, or a 4-bit slot).
 inline uint32_t bin_at(const srocm_group &g, size_t row, size_t column) {
     const uint8_t *r = g.data + row * g.row_stride;
-    return g.bin_bytes == 2 ? bin16(r, column) : r[column];
+    const uint32_t bits = group_bits(g);
+    return bits == 16 ? bin16(r, column) : (bits == 4 ? bin4(r, column) : r[column]);
 }
 
-// cpu.rs:307-314 add_run, cpu.rs:277-304 accumulate_rows (prefetching left to the hardware). A 2-byte group adds
-// its features' u16 bins; every add is an exact integer one, so the order of the adds changes nothing.
+// cpu.rs:307-314 add_run, cpu.rs:277-304 accumulate_rows (prefetching left to the hardware). A 16-bit group adds
+// its features' u16 bins, a 4-bit group its features' half-byte bins; every add is an exact integer one, so the
+// order of the adds changes nothing.
 inline void accumulate(const GroupLayout &g, const uint8_t *data, const uint32_t *rows, const int64_t *values,
                        size_t n, int64_t *acc) {
-    if (g.bin_bytes == 2) {
+    if (g.bits != 8) {
         for (size_t i = 0; i < n; ++i) {
             const uint8_t *row = data + static_cast<size_t>(rows[i]) * g.stride;
             int64_t v = values[i];
             for (const auto &run : g.runs)
                 for (uint32_t c = run.first; c < run.second; ++c)
-                    if (g.column_features[c] >= 0) acc[g.offsets[c] + bin16(row, c)] += v;
+                    if (g.column_features[c] >= 0) acc[g.offsets[c] + (g.bits == 16 ? bin16(row, c) : bin4(row, c))] += v;
         }
         return;
     }
@@ -789,7 +799,7 @@ void add_tree_to(const srocm_dataset *d, const srocm_device_node *nodes, uint32_
             while (node >= 0) {
                 const srocm_device_node &nd = nodes[node];
                 const srocm_group &g = d->groups[nd.split.group];
-                node = goes_left(nd.split, bin_at(g, row, nd.split.column), g.bin_bytes == 2) ? nd.left : nd.right;
+                node = goes_left(nd.split, bin_at(g, row, nd.split.column), group_bits(g) == 16) ? nd.left : nd.right;
             }
             scores[row] += leaf_values[~node];
         }
@@ -1474,7 +1484,7 @@ struct CpuBackend {
         if (static_cast<uint64_t>(leaf.begin) + leaf.count > partition.size()) throw std::runtime_error("leaf outside the partition");
         const srocm_group &g = data->groups[s.group];
         return stable_partition(partition.data() + leaf.begin, leaf.count,
-                                [&](uint32_t row) { return goes_left(s, bin_at(g, row, s.column), g.bin_bytes == 2); });
+                                [&](uint32_t row) { return goes_left(s, bin_at(g, row, s.column), group_bits(g) == 16); });
     }
     void leaf_sums(const std::vector<srocm_leaf_range> &leaves, float gs, float hs, std::vector<int64_t> &out) {
         Timer t(&times[T_SUMS]);
@@ -1552,7 +1562,7 @@ struct Learner {
     srocm_bin_split bin_split(const srocm_feature &m, const oracle_split_info &info) const {
         srocm_bin_split s{};
         auto set = [&](uint32_t bin) { s.left_bins[bin / 32] |= 1u << (bin % 32); };
-        if (data->groups[m.group].bin_bytes == 2) {  // the numerical rule of a 2-byte feature, as goes_left reads it
+        if (group_bits(data->groups[m.group]) == 16) {  // the numerical rule of a 2-byte feature, as goes_left reads it
             s.left_bins[0] = info.threshold;
             s.left_bins[1] = info.default_left && m.nan_bin ? m.num_bins : 0u;
         } else if (!info.categorical) {
@@ -1884,7 +1894,7 @@ void oracle_histogram(const srocm_dataset *data, const int32_t *packed, int64_t 
 uint32_t oracle_partition(const srocm_dataset *data, uint32_t *rows, uint64_t count, const srocm_bin_split *split) {
     const srocm_group &g = data->groups[split->group];
     return stable_partition(rows, count, [&](uint32_t row) {
-        return goes_left(*split, bin_at(g, row, split->column), g.bin_bytes == 2);
+        return goes_left(*split, bin_at(g, row, split->column), group_bits(g) == 16);
     });
 }
 

@@ -48,7 +48,7 @@ class Feature(C.Structure):
 class Group(C.Structure):
     _fields_ = [("row_stride", C.c_uint32), ("hist_offset", C.c_uint32), ("total_bins", C.c_uint32),
                 ("num_features", C.c_uint32), ("features", C.POINTER(C.c_uint32)),
-                ("data", C.POINTER(C.c_uint8)), ("bin_bytes", C.c_uint32)]
+                ("data", C.POINTER(C.c_uint8)), ("bin_bits", C.c_uint32)]
 
 
 class Dataset(C.Structure):

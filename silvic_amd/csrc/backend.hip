@@ -341,7 +341,7 @@ struct Context {
     uint32_t max_width = 32;
     uint32_t col16 = 0;                     // some group has two-byte bins: column-major bins are u16
     bool has_narrow = true, has_wide = false;  // features of one-byte / two-byte bins (a scan kernel each)
-    std::vector<uint32_t> group_bin_bytes;  // per group: 1 or 2
+    std::vector<uint32_t> group_bits;  // per group: bits per bin, 8, 16 (wide slabs) or 4 (two to a byte)
     std::vector<uint32_t> nt_slab, nt_slab_col;  // per non-trivial feature: its slab and column there
 
     DevData train;
@@ -563,8 +563,13 @@ struct Context {
         auto check_layout = [&](const srocm_dataset *d) {
             if (d->num_groups != t->num_groups || d->num_features != t->num_features)
                 fail(SROCM_ERR_DATA, "validation set binned with a different layout than the training set");
-            for (uint32_t g = 0; g < d->num_groups; ++g)
+            for (uint32_t g = 0; g < d->num_groups; ++g) {
                 if (!d->groups[g].data && d->num_rows) fail(SROCM_ERR_DATA, "group without data");
+                const uint32_t a = d->groups[g].bin_bits ? d->groups[g].bin_bits : 8u;
+                const uint32_t b = t->groups[g].bin_bits ? t->groups[g].bin_bits : 8u;
+                if (a != b || d->groups[g].row_stride != t->groups[g].row_stride)
+                    fail(SROCM_ERR_DATA, "validation set binned with a different layout than the training set");
+            }
         };
         for (uint32_t i = 0; i < nv; ++i) check_layout(v[i]);
         loaded = false;
@@ -579,14 +584,15 @@ struct Context {
         feat_nt.assign(nf, -1);
         nt_feat.clear();
         group_col_nt.assign(t->num_groups, {});
-        group_bin_bytes.assign(t->num_groups, 1);
+        group_bits.assign(t->num_groups, 8);
         col16 = 0;
         for (uint32_t g = 0; g < t->num_groups; ++g) {
-            group_col_nt[g].assign(t->groups[g].row_stride, -1);
-            const uint32_t bb = t->groups[g].bin_bytes;
-            if (bb > 2) fail(SROCM_ERR_DATA, "group " + std::to_string(g) + " has " + std::to_string(bb) + "-byte bins");
-            group_bin_bytes[g] = bb == 2 ? 2u : 1u;
-            if (bb == 2) col16 = 1;
+            const uint32_t bits = t->groups[g].bin_bits == 0 ? 8u : t->groups[g].bin_bits;
+            if (bits != 4 && bits != 8 && bits != 16)
+                fail(SROCM_ERR_DATA, "group " + std::to_string(g) + " has " + std::to_string(bits) + "-bit bins");
+            group_bits[g] = bits;
+            group_col_nt[g].assign(static_cast<size_t>(t->groups[g].row_stride) * (bits == 4 ? 2 : 1), -1);
+            if (bits == 16) col16 = 1;
         }
         uint64_t bins_seen = 0;
         for (uint32_t f = 0; f < nf; ++f) {
@@ -595,11 +601,13 @@ struct Context {
             if (m.kind != SROCM_BINS_NUMERICAL && m.kind != SROCM_BINS_CATEGORICAL) fail(SROCM_ERR_DATA, "bad feature kind");
             if (m.group >= t->num_groups) fail(SROCM_ERR_DATA, "feature in a missing group");
             const srocm_group &g = t->groups[m.group];
-            const uint32_t bb = group_bin_bytes[m.group];
-            if (bb == 1 && m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature of one-byte bins has more than 256 bins");
-            if (bb == 2 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
+            const uint32_t bits = group_bits[m.group];
+            if (bits == 8 && m.num_bins > 256) fail(SROCM_ERR_UNSUPPORTED, "a feature of one-byte bins has more than 256 bins");
+            if (bits == 16 && (m.kind != SROCM_BINS_NUMERICAL || m.num_bins > 1024))
                 fail(SROCM_ERR_UNSUPPORTED, "two-byte bins hold numerical features of at most 1024 bins");
-            if (m.column + bb > g.row_stride || m.hist_offset < g.hist_offset ||
+            if (bits == 4 && m.num_bins > 16) fail(SROCM_ERR_UNSUPPORTED, "a feature of 4-bit bins has more than 16 bins");
+            const uint64_t end_byte = bits == 4 ? m.column / 2 + 1 : m.column + bits / 8;  // past the feature's bytes
+            if (end_byte > g.row_stride || m.hist_offset < g.hist_offset ||
                 m.hist_offset - g.hist_offset + m.num_bins > g.total_bins || m.hist_offset + m.num_bins > total_bins)
                 fail(SROCM_ERR_DATA, "feature " + std::to_string(f) + " lies outside its group's bins or row");
             feat_nt[f] = static_cast<int32_t>(nt_feat.size());
@@ -617,7 +625,7 @@ struct Context {
         for (int wide = 0; wide < 2; ++wide) {
             std::vector<uint32_t> members;
             for (size_t i = 0; i < nt_feat.size(); ++i)
-                if ((group_bin_bytes[feats[nt_feat[i]].group] == 2) == (wide != 0)) members.push_back(static_cast<uint32_t>(i));
+                if ((group_bits[feats[nt_feat[i]].group] == 16) == (wide != 0)) members.push_back(static_cast<uint32_t>(i));
             const size_t per = wide ? MAX_SLAB_FEATURES / 4 : MAX_SLAB_FEATURES;
             for (size_t i = 0; i < members.size(); i += per) {
                 Slab s;
@@ -667,7 +675,7 @@ struct Context {
         for (uint32_t f = 0; f < nf; ++f) {
             fd[f] = FeatDev{feats[f].num_bins, feats[f].hist_offset, feats[f].kind, feats[f].nan_bin,
                             feat_nt[f] < 0 ? 0u : static_cast<uint32_t>(feat_nt[f]),
-                            feats[f].num_bins && group_bin_bytes[feats[f].group] == 2 ? 1u : 0u};
+                            feats[f].num_bins && group_bits[feats[f].group] == 16 ? 1u : 0u};
             // each feature's candidate (an empty one for a trivial feature) is written by the scan of its kind
             (fd[f].wide ? has_wide : has_narrow) = true;
         }
@@ -774,7 +782,7 @@ struct Context {
             uint64_t bytes = n * grp.row_stride;
             staging.alloc(bytes);
             hip_check(hipMemcpyAsync(staging.p, grp.data, bytes, hipMemcpyHostToDevice, stream), "upload group");
-            for (uint32_t c = 0; c < grp.row_stride; ++c) {
+            for (uint32_t c = 0; c < group_col_nt[g].size(); ++c) {
                 int32_t nt = group_col_nt[g][c];
                 if (nt < 0) continue;
                 RepackTo to{out.col.p + static_cast<size_t>(nt) * n * cb, col16, nullptr, 0, 0, 0};
@@ -785,13 +793,13 @@ struct Context {
                     to.slab_wide = sl.wide ? 1u : 0u;
                     to.slab_col = nt_slab_col[nt];
                 }
-                repack(staging.p, grp.row_stride, c, group_bin_bytes[g], n, to);
+                repack(staging.p, grp.row_stride, c, group_bits[g], n, to);
             }
             sync();  // staging is reused
         }
     }
 
-    void repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bin_bytes, uint64_t n, const RepackTo &to);
+    void repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bits, uint64_t n, const RepackTo &to);
 
     // ------------------------------------------------------------------------------------------------
     // gradients, quantization, partition reset
@@ -1067,7 +1075,7 @@ struct Context {
         PartArgs a = part_args(leaf.begin, leaf.count);
         a.col = train.col.p + static_cast<size_t>(nt) * rows * (col16 ? 2 : 1);
         a.col16 = col16;
-        a.wide = group_bin_bytes[split.group] == 2 ? 1u : 0u;
+        a.wide = group_bits[split.group] == 16 ? 1u : 0u;
         std::memcpy(a.left_bins, split.left_bins, sizeof(a.left_bins));
         run_partition(a, leaf.count);
     }
@@ -1147,7 +1155,7 @@ struct Context {
             dn[k].feature = static_cast<uint32_t>(group_col_nt[n.split.group][n.split.column]);
             dn[k].left = n.left;
             dn[k].right = n.right;
-            dn[k].wide = group_bin_bytes[n.split.group] == 2 ? 1u : 0u;
+            dn[k].wide = group_bits[n.split.group] == 16 ? 1u : 0u;
         }
         d_nodes.alloc(std::max<uint32_t>(nn, 1));
         if (nn) hip_check(hipMemcpyAsync(d_nodes.p, dn, nn * sizeof(DevNode), hipMemcpyHostToDevice, stream), "upload tree");
@@ -1523,25 +1531,28 @@ struct Context {
     }
 };
 
-// One feature's bins from its group's rows (one byte, or two little-endian) into its column-major bins and its
-// slab column.
-__global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint32_t column, uint32_t bin_bytes,
+// One feature's bins from its group's rows (a byte, two little-endian bytes, or half a byte: `column` counts 4-bit
+// slots, low half first) into its column-major bins and its slab column.
+__global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint32_t column, uint32_t bits,
                          uint64_t n, RepackTo to) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < n; r += (uint64_t)gridDim.x * blockDim.x) {
-        const uint8_t *p = src + r * stride + column;
-        const uint32_t b = bin_bytes == 2 ? static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) : p[0];
+        const uint8_t *row = src + r * stride;
+        uint32_t b;
+        if (bits == 16) b = static_cast<uint32_t>(row[column]) | (static_cast<uint32_t>(row[column + 1]) << 8);
+        else if (bits == 4) b = (static_cast<uint32_t>(row[column >> 1]) >> (4 * (column & 1u))) & 15u;
+        else b = row[column];
         if (to.col16) reinterpret_cast<uint16_t *>(to.col)[r] = static_cast<uint16_t>(b);
         else to.col[r] = static_cast<uint8_t>(b);
         if (!to.slab) continue;
-        uint8_t *row = to.slab + r * to.row_bytes;
-        if (to.slab_wide) reinterpret_cast<uint16_t *>(row)[to.slab_col] = static_cast<uint16_t>(b);
-        else row[to.slab_col] = static_cast<uint8_t>(b);
+        uint8_t *dst = to.slab + r * to.row_bytes;
+        if (to.slab_wide) reinterpret_cast<uint16_t *>(dst)[to.slab_col] = static_cast<uint16_t>(b);
+        else dst[to.slab_col] = static_cast<uint8_t>(b);
     }
 }
 
-void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bin_bytes, uint64_t n,
+void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint32_t bits, uint64_t n,
                      const RepackTo &to) {
-    k_repack<<<grid_rows(n), 256, 0, stream>>>(src, stride, column, bin_bytes, n, to);
+    k_repack<<<grid_rows(n), 256, 0, stream>>>(src, stride, column, bits, n, to);
     launch_check("k_repack");
 }
 

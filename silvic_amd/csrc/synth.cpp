@@ -299,14 +299,14 @@ void synth_features(const void *h, uint32_t *out) {
 uint32_t synth_num_groups(const void *h) { return static_cast<uint32_t>(static_cast<const Workload *>(h)->g_features.size()); }
 uint64_t synth_total_bins(const void *h) { return static_cast<const Workload *>(h)->total_bins; }
 
-// Group `g`: row stride, hist offset, total bins, feature count, bytes per bin.
+// Group `g`: row stride, hist offset, total bins, feature count, bits per bin (8, or 16 above 256 bins).
 void synth_group(const void *h, uint32_t g, uint32_t *out5) {
     const Workload *w = static_cast<const Workload *>(h);
     out5[0] = w->g_stride[g];
     out5[1] = w->g_hist_offset[g];
     out5[2] = w->g_total_bins[g];
     out5[3] = static_cast<uint32_t>(w->g_features[g].size());
-    out5[4] = w->bin_bytes;
+    out5[4] = 8 * w->bin_bytes;
 }
 const uint32_t *synth_group_features(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_features[g].data(); }
 const uint8_t *synth_group_data(const void *h, uint32_t g) { return static_cast<const Workload *>(h)->g_data[g].data(); }

@@ -34,15 +34,16 @@ class FeatureMeta:
 
 @dataclass
 class FeatureGroup:
-    """FeatureGroup (data/mod.rs:48-59): ``data[row * row_stride + column]``. ``bin_bytes`` 2 (an extension for
-    max_bin > 255) stores each bin as a little-endian u16 at byte offset ``column``."""
+    """FeatureGroup (data/mod.rs:48-59): ``data[row * row_stride + column]``. ``bin_bits`` (extensions silvic does
+    not have): 8, silvic's byte bins; 16, each bin a little-endian u16 at byte offset ``column`` (max_bin > 255);
+    4, two bins a byte, ``column`` counting 4-bit slots (the low half of byte column // 2 first)."""
 
     features: list
     row_stride: int
     hist_offset: int
     total_bins: int
     data: np.ndarray
-    bin_bytes: int = 1
+    bin_bits: int = 8
 
 
 @dataclass
@@ -64,8 +65,10 @@ class BinnedDataset:
         meta = self.features[feature]
         g = self.groups[meta.group]
         m = g.data.reshape(self.num_rows, g.row_stride)
-        if g.bin_bytes == 2:
+        if g.bin_bits == 16:
             col = m[:, meta.column].astype(np.uint16) | (m[:, meta.column + 1].astype(np.uint16) << 8)
+        elif g.bin_bits == 4:
+            col = (m[:, meta.column // 2] >> (4 * (meta.column % 2))) & 15
         else:
             col = m[:, meta.column]
         return col if rows is None else col[rows]
@@ -83,7 +86,7 @@ class BinnedDataset:
             keep += [fidx, data]
             groups[i] = _abi.Group(g.row_stride, g.hist_offset, g.total_bins, len(g.features),
                                    fidx.ctypes.data_as(C.POINTER(C.c_uint32)),
-                                   data.ctypes.data_as(C.POINTER(C.c_uint8)), g.bin_bytes)
+                                   data.ctypes.data_as(C.POINTER(C.c_uint8)), g.bin_bits)
         label = np.ascontiguousarray(self.label, dtype=np.float32)
         keep.append(label)
         weight = None
@@ -174,6 +177,46 @@ def as_categorical(data, features):
     return data
 
 
+def pack_nibbles(data, min_run=2):
+    """``data`` with its features of at most 16 bins stored two to a byte (``bin_bits`` 4), the others as they were:
+    each run of at least ``min_run`` consecutive such features of one byte group becomes a group of its own. Bins,
+    histogram offsets, feature order and every bin value are unchanged, so a learner sees the same dataset."""
+    new_groups, metas = [], [FeatureMeta(**vars(f)) for f in data.features]
+    for g in data.groups:
+        if g.bin_bits not in (0, 8):
+            new_groups.append(g)
+            continue
+        rows = g.data.reshape(data.num_rows, g.row_stride)
+        runs, cur = [], []  # consecutive features, split where a feature has more than 16 bins
+        for f in g.features:
+            small = 0 < data.features[f].num_bins <= 16
+            if cur and small != cur[0][1]:
+                runs.append(cur)
+                cur = []
+            cur.append((f, small))
+        if cur:
+            runs.append(cur)
+        for run in runs:
+            fs = [f for f, _ in run]
+            nib = run[0][1] and len(fs) >= min_run
+            slots = len(fs)
+            stride = ((slots + 1) // 2 + 3) // 4 * 4 if nib else (slots + 3) // 4 * 4
+            packed = np.zeros((data.num_rows, stride), np.uint8)
+            for k, f in enumerate(fs):
+                b = rows[:, data.features[f].column]
+                if nib:
+                    packed[:, k // 2] |= (b & 15) << (4 * (k % 2))
+                else:
+                    packed[:, k] = b
+                metas[f].group = len(new_groups)
+                metas[f].column = k
+            lo = min(data.features[f].hist_offset for f in fs)
+            hi = max(data.features[f].hist_offset + data.features[f].num_bins for f in fs)
+            new_groups.append(FeatureGroup(fs, stride, lo, hi - lo, packed.reshape(-1), 4 if nib else 8))
+    return BinnedDataset(data.num_rows, metas, new_groups, data.total_bins, data.label, data.weight,
+                         data.row_offset, data.query_boundaries)
+
+
 def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=False):
     """Configuration ``config`` (1-5) as a binned dataset, generated natively; ``rows``/``cols`` shrink it.
     Configuration 3 carries query boundaries (Zipf-like sizes in 10..200).
@@ -202,10 +245,10 @@ def synthetic(config, rows=None, cols=None, seed=7, max_bin=None, categorical=Fa
         info = (C.c_uint32 * 5)()
         for g in range(lib.synth_num_groups(h)):
             lib.synth_group(h, g, info)
-            stride, off, total, nf, bb = (int(v) for v in info)
+            stride, off, total, nf, bits = (int(v) for v in info)
             fidx = np.ctypeslib.as_array(lib.synth_group_features(h, g), shape=(nf,)).copy()
             data = np.ctypeslib.as_array(lib.synth_group_data(h, g), shape=(rows * stride,)).copy()
-            groups.append(FeatureGroup([int(f) for f in fidx], stride, off, total, data, bb))
+            groups.append(FeatureGroup([int(f) for f in fidx], stride, off, total, data, bits))
         label = np.ctypeslib.as_array(lib.synth_label(h), shape=(rows,)).copy()
         total = int(lib.synth_total_bins(h))
         nq = int(lib.synth_num_queries(h))

@@ -131,7 +131,7 @@ def row_slice(data, start, stop):
     for g in data.groups:
         d = g.data.reshape(data.num_rows, g.row_stride)[start:stop]
         groups.append(FeatureGroup(g.features, g.row_stride, g.hist_offset, g.total_bins, d.reshape(-1).copy(),
-                                   g.bin_bytes))
+                                   g.bin_bits))
     weight = None if data.weight is None else data.weight[start:stop].copy()
     return BinnedDataset(stop - start, data.features, groups, data.total_bins, data.label[start:stop].copy(), weight)
 
@@ -149,5 +149,5 @@ def joined(a, b):
     nf = len(a.features)
     for g in b.groups:
         groups.append(FeatureGroup([j + nf for j in g.features], g.row_stride, g.hist_offset + a.total_bins,
-                                   g.total_bins, g.data, g.bin_bytes))
+                                   g.total_bins, g.data, g.bin_bits))
     return BinnedDataset(a.num_rows, feats, groups, a.total_bins + b.total_bins, a.label, a.weight)

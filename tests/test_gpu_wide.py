@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 def wide_data(rows, cols, seed):
     data = silvic_amd.synthetic(5, rows=rows, cols=cols, seed=seed, max_bin=1023)
-    assert all(g.bin_bytes == 2 for g in data.groups)
+    assert all(g.bin_bits == 16 for g in data.groups)
     assert max(f.num_bins for f in data.features) > 256
     return data
 

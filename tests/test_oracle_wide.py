@@ -16,7 +16,7 @@ from tests.split_cases import (MIN_SCORE, brute_force_numerical, close, sums, wi
 
 def wide_data(rows=30_000, cols=12, seed=5):
     data = silvic_amd.synthetic(5, rows=rows, cols=cols, seed=seed, max_bin=1023)
-    assert all(g.bin_bytes == 2 for g in data.groups)
+    assert all(g.bin_bits == 16 for g in data.groups)
     assert max(f.num_bins for f in data.features) > 256
     return data
 
