@@ -82,6 +82,38 @@ def timed_window(rows, warmup, steps):
     return rows[begin(warmup):begin(warmup + steps)]
 
 
+def step_kernels(data):
+    """The k_step_rows instances the backend launches for `data`, with their slab counts. Byte features in the order
+    of their bin classes (more than 128 bins, more than 64, the rest), 128 to a slab while it holds one of more than
+    128 bins, else 256; a slab's rows the fewest bytes (32..256) that hold its features, and as many features to an
+    LDS column as that row length and its largest bin count allow (four of at most 64 bins, two of at most 128).
+    Two-byte features 32 to a slab."""
+    bits = [g.bin_bits or 8 for g in data.groups]
+
+    def cls(b):
+        return 4 if b <= 64 else (2 if b <= 128 else 1)
+
+    nb = sorted((cls(f.num_bins) for f in data.features if f.num_bins > 0 and bits[f.group] != 16))
+    wide = sum(1 for f in data.features if f.num_bins > 0 and bits[f.group] == 16)
+    out = {}
+    b = 0
+    while b < len(nb):
+        e = min(len(nb), b + (128 if nb[b] == 1 else 256))
+        n, max_pack = e - b, min(nb[b:e])
+        row = 32
+        while row < n:
+            row *= 2
+        pack = next((p for p in (4, 2) if p <= max_pack and 32 * p <= row and row // p <= 128), 1)
+        k = f"k_step_rows<{row // pack}>" if pack == 1 else f"k_step_rows<{row // pack}, false, {pack}>"
+        out[k] = out.get(k, 0) + 1
+        b = e
+    for i in range(0, wide, 32):
+        cols = 4 * min(32, wide - i)
+        k = f"k_step_rows<{32 if cols <= 32 else (64 if cols <= 64 else 128)}, true>"
+        out[k] = out.get(k, 0) + 1
+    return ", ".join(f"{k} x{n}" for k, n in out.items())
+
+
 def read_counters(folder):
     """rocprofv3 --pmc CSV of `folder` as (dispatch records in order, {dispatch: {counter: value}})."""
     import csv
@@ -378,7 +410,7 @@ def main():
                "trees_identical": f"{same}/{compared}", "seconds": cpu_elapsed}
 
     describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves)
-    slab = "k_step_rows<128, true>" if wl["max_bin"] > 255 else "k_step_rows<128>"
+    slab = step_kernels(data)
     out = {
         "metric": METRIC if args.workload == "binary" else f"boosting iters/s, {args.workload} workload; % HBM peak",
         "value": iters_per_s,

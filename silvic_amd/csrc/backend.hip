@@ -269,11 +269,15 @@ constexpr uint64_t ROW_BLOCK = 256;
 struct Slab {
     uint32_t width = 0;            // W: LDS and partial columns
     bool wide = false;             // two-byte bins: W / 4 features, each 4 virtual columns (k_hist<W, true>)
+    uint32_t pack = 1;             // byte bins, `pack` features of at most 256 / pack bins a column (k_hist<W, false, pack>)
     std::vector<uint32_t> feats;   // feature ids
     DevBuf<uint8_t> bins;          // [rows][row_bytes()]
-    DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per virtual column
-    uint32_t row_bytes() const { return wide ? width / 2 : width; }
-    uint32_t capacity() const { return wide ? width / 4 : width; }
+    DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per feature slot: segment * W + column (virtual column)
+    uint32_t row_bytes() const { return wide ? width / 2 : width * pack; }
+    uint32_t capacity() const { return wide ? width / 4 : width * pack; }
+    uint32_t seg_shift() const { return pack == 4 ? 6u : (pack == 2 ? 7u : 8u); }
+    uint32_t slots() const { return width * pack; }  // entries of the per-slot arrays
+    uint32_t kernel() const { return width + (wide ? 1u : 0u) + (pack > 1 ? pack : 0u); }  // launch switch key
     uint64_t step_partial_off = 0;  // the slab's partials in the step partial buffer, in {g, h} pairs
 };
 
@@ -354,10 +358,11 @@ struct Context {
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
     DevBuf<uint32_t> d_fmt;  // per slab and k_step_rows workgroup: the format of its partial (1 packed, 0 pairs)
-    DevBuf<int32_t> gcol_feat;
+    DevBuf<int32_t> scan_feat;  // numerical slab features, CG_COLS a scan group, -1 padding
     DevBuf<uint32_t> cat_feats;  // the categorical features of the slabs
     uint32_t ncat = 0;
-    uint32_t ncg = 0;
+    uint32_t ncg = 0;  // column groups of k_step_reduce
+    uint32_t nsg = 0;  // scan groups of k_step_scan
     uint64_t step_partial_pairs = 0;
     uint32_t part_len = 0;
     std::vector<uint8_t> used;
@@ -616,31 +621,61 @@ struct Context {
             bins_seen += m.num_bins;
         }
         (void)bins_seen;
-        // slabs: consecutive non-trivial features of one bin width, up to 128 byte features or 32 two-byte
-        // features per slab
+        // slabs. Two-byte features: up to 32 a slab, in feature order. Byte features: in the order of their bin
+        // classes (more than 128 bins, more than 64, the rest; feature order within a class), up to 128 a slab
+        // while the slab holds a feature of more than 128 bins, else up to 256. A slab's rows are the fewest bytes
+        // (32, 64, 128 or 256) that hold its features, and its LDS columns hold as many features each (`pack`) as
+        // that row length and its largest bin count allow: four of at most 64 bins, two of at most 128.
         slabs.clear();
         max_width = 32;
         nt_slab.assign(nt_feat.size(), 0);
         nt_slab_col.assign(nt_feat.size(), 0);
-        for (int wide = 0; wide < 2; ++wide) {
-            std::vector<uint32_t> members;
-            for (size_t i = 0; i < nt_feat.size(); ++i)
-                if ((group_bits[feats[nt_feat[i]].group] == 16) == (wide != 0)) members.push_back(static_cast<uint32_t>(i));
-            const size_t per = wide ? MAX_SLAB_FEATURES / 4 : MAX_SLAB_FEATURES;
-            for (size_t i = 0; i < members.size(); i += per) {
+        {
+            auto bin_class = [&](uint32_t i) {  // 4: at most 64 bins, 2: at most 128, 1: more
+                const uint32_t nb = feats[nt_feat[i]].num_bins;
+                return nb <= 64 ? 4u : (nb <= 128 ? 2u : 1u);
+            };
+            std::vector<uint32_t> narrow, wide;
+            for (uint32_t c : {1u, 2u, 4u})
+                for (uint32_t i = 0; i < nt_feat.size(); ++i)
+                    if (group_bits[feats[nt_feat[i]].group] != 16 && bin_class(i) == c) narrow.push_back(i);
+            for (uint32_t i = 0; i < nt_feat.size(); ++i)
+                if (group_bits[feats[nt_feat[i]].group] == 16) wide.push_back(i);
+            auto add_slab = [&](const std::vector<uint32_t> &members, size_t b, size_t e, bool is_wide) {
                 Slab s;
-                s.wide = wide != 0;
-                const size_t end = std::min(members.size(), i + per);
-                for (size_t k = i; k < end; ++k) {
+                s.wide = is_wide;
+                uint32_t max_pack = 4;
+                for (size_t k = b; k < e; ++k) {
                     nt_slab[members[k]] = static_cast<uint32_t>(slabs.size());
-                    nt_slab_col[members[k]] = static_cast<uint32_t>(k - i);
+                    nt_slab_col[members[k]] = static_cast<uint32_t>(k - b);
                     s.feats.push_back(nt_feat[members[k]]);
+                    max_pack = std::min(max_pack, bin_class(members[k]));
                 }
-                const uint32_t n = static_cast<uint32_t>(s.feats.size()) * (s.wide ? 4u : 1u);  // virtual columns
-                s.width = n <= 32 ? 32 : (n <= 64 ? 64 : 128);
+                const uint32_t n = static_cast<uint32_t>(e - b);
+                if (is_wide) {  // four virtual columns a feature
+                    s.width = 4 * n <= 32 ? 32 : (4 * n <= 64 ? 64 : 128);
+                } else {
+                    uint32_t row = 32;
+                    while (row < n) row *= 2;
+                    s.pack = 1;
+                    for (uint32_t p : {4u, 2u})
+                        if (p <= max_pack && 32 * p <= row && row / p <= 128) {
+                            s.pack = p;
+                            break;
+                        }
+                    s.width = row / s.pack;
+                }
                 max_width = std::max(max_width, s.width);
                 slabs.push_back(std::move(s));
+            };
+            for (size_t b = 0; b < narrow.size();) {
+                const size_t per = bin_class(narrow[b]) == 1 ? MAX_SLAB_FEATURES : 2 * MAX_SLAB_FEATURES;
+                const size_t e = std::min(narrow.size(), b + per);
+                add_slab(narrow, b, e, false);
+                b = e;
             }
+            for (size_t b = 0; b < wide.size(); b += MAX_SLAB_FEATURES / 4)
+                add_slab(wide, b, std::min(wide.size(), b + MAX_SLAB_FEATURES / 4), true);
         }
         // device buffers
         train = DevData{};
@@ -682,9 +717,10 @@ struct Context {
         dfeats.alloc(nf);
         hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
         for (auto &s : slabs) {
-            // virtual column v: a byte feature's column; in a wide slab, bins congruent to v / (W/4) mod 4 of
-            // feature v % (W/4)
-            std::vector<uint32_t> off(s.width, 0), nb(s.width, 0), st(s.width, 1);
+            // slot i: a byte feature's (column i % W, segment i / W); in a wide slab, virtual column i, bins
+            // congruent to i / (W/4) mod 4 of feature i % (W/4)
+            const uint32_t ns = s.slots();
+            std::vector<uint32_t> off(ns, 0), nb(ns, 0), st(ns, 1);
             for (size_t c = 0; c < s.feats.size(); ++c) {
                 const srocm_feature &m = feats[s.feats[c]];
                 if (!s.wide) {
@@ -699,54 +735,58 @@ struct Context {
                     st[v] = 4;
                 }
             }
-            s.col_offset.alloc(s.width);
-            s.col_bins.alloc(s.width);
-            s.col_stride.alloc(s.width);
-            hip_check(hipMemcpy(s.col_stride.p, st.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
-            hip_check(hipMemcpy(s.col_offset.p, off.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
-            hip_check(hipMemcpy(s.col_bins.p, nb.data(), s.width * 4, hipMemcpyHostToDevice), "upload slab");
+            s.col_offset.alloc(ns);
+            s.col_bins.alloc(ns);
+            s.col_stride.alloc(ns);
+            hip_check(hipMemcpy(s.col_stride.p, st.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
+            hip_check(hipMemcpy(s.col_offset.p, off.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
+            hip_check(hipMemcpy(s.col_bins.p, nb.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
         }
-        // groups of CG_COLS slab columns for k_step_reduce and k_step_scan, and the feature of every slab column
+        // groups of CG_COLS slab columns for k_step_reduce, the numerical features in groups of CG_COLS for
+        // k_step_scan, and the categorical ones for k_step_cat
         {
             std::vector<ColGroup> cg;
-            std::vector<int32_t> gfeat;
+            std::vector<int32_t> sfeat;
+            std::vector<uint32_t> cats;
             uint64_t poff = 0;
             for (size_t si = 0; si < slabs.size(); ++si) {
                 Slab &s = slabs[si];
                 s.step_partial_off = poff;
-                uint32_t gbase = static_cast<uint32_t>(gfeat.size());
-                // a wide slab's virtual column v holds bins q, q + 4, ... (q = v / (W/4)) of feature v % (W/4); the
-                // scan visits each feature once, at its q = 0 column
+                // a wide slab's virtual column v holds bins q, q + 4, ... (q = v / (W/4)) of feature v % (W/4); a
+                // packed slab's column c holds feature seg * W + c in bins [seg, seg + 1) * 2^seg_shift
                 const uint32_t cap = s.capacity();
                 for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) {
-                    ColGroup x{poff, s.width, c0, gbase + c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}, {}};
+                    ColGroup x{poff, s.width, c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}, {}, s.seg_shift()};
                     for (uint32_t k = 0; k < CG_COLS; ++k) {
-                        const uint32_t v = c0 + k, c = v % cap, q = v / cap;
-                        const bool real = c < s.feats.size() && (s.wide || q == 0);
-                        const srocm_feature &m = feats[real ? s.feats[c] : 0];
-                        x.offset[k] = real ? m.hist_offset + q : 0u;
-                        x.bins[k] = real && m.num_bins > q ? (m.num_bins - q + (s.wide ? 3 : 0)) / (s.wide ? 4 : 1) : 0u;
+                        const uint32_t v = c0 + k;
                         x.stride[k] = s.wide ? 4u : 1u;
+                        for (uint32_t seg = 0; seg < s.pack; ++seg) {
+                            const uint32_t c = s.wide ? v % cap : seg * s.width + v, q = s.wide ? v / cap : 0u;
+                            const bool real = c < s.feats.size();
+                            const srocm_feature &m = feats[real ? s.feats[c] : 0];
+                            x.offset[seg][k] = real ? m.hist_offset + q : 0u;
+                            x.bins[seg][k] = real && m.num_bins > q ? (m.num_bins - q + (s.wide ? 3 : 0)) / (s.wide ? 4 : 1) : 0u;
+                        }
                     }
                     cg.push_back(x);
                 }
-                for (uint32_t c = 0; c < s.width; ++c)
-                    gfeat.push_back(c < s.feats.size() && c < cap ? static_cast<int32_t>(s.feats[c]) : -1);
+                for (uint32_t f : s.feats) {
+                    if (feats[f].kind == SROCM_BINS_CATEGORICAL) cats.push_back(f);
+                    else sfeat.push_back(static_cast<int32_t>(f));
+                }
                 poff += static_cast<uint64_t>(k1_groups()) * step_partial_stride(s.width);
             }
+            while (sfeat.size() % CG_COLS) sfeat.push_back(-1);
             d_fmt.alloc(std::max<size_t>(slabs.size(), 1) * k1_groups());
             ncg = static_cast<uint32_t>(cg.size());
+            nsg = static_cast<uint32_t>(sfeat.size() / CG_COLS);
             step_partial_pairs = std::max<uint64_t>(poff, 1);
             d_cgs.alloc(std::max<size_t>(cg.size(), 1));
-            gcol_feat.alloc(std::max<size_t>(gfeat.size(), 1));
-            if (!cg.empty()) {
+            scan_feat.alloc(std::max<size_t>(sfeat.size(), 1));
+            if (!cg.empty())
                 hip_check(hipMemcpy(d_cgs.p, cg.data(), cg.size() * sizeof(ColGroup), hipMemcpyHostToDevice), "upload column groups");
-                hip_check(hipMemcpy(gcol_feat.p, gfeat.data(), gfeat.size() * 4, hipMemcpyHostToDevice), "upload columns");
-            }
-            // the categorical features in the slabs, scanned by k_step_cat
-            std::vector<uint32_t> cats;
-            for (int32_t f : gfeat)
-                if (f >= 0 && feats[f].kind == SROCM_BINS_CATEGORICAL) cats.push_back(static_cast<uint32_t>(f));
+            if (!sfeat.empty())
+                hip_check(hipMemcpy(scan_feat.p, sfeat.data(), sfeat.size() * 4, hipMemcpyHostToDevice), "upload scanned features");
             ncat = static_cast<uint32_t>(cats.size());
             cat_feats.alloc(std::max<size_t>(cats.size(), 1));
             if (!cats.empty())
@@ -926,13 +966,19 @@ struct Context {
                 e1 = event();
                 hip_check(hipEventRecord(e0, stream), "event");
             }
-            switch (s.width + (s.wide ? 1u : 0u)) {
+            switch (s.kernel()) {
             case 32: k_hist<32><<<grid, 1024, 0, stream>>>(a); break;
             case 64: k_hist<64><<<grid, 1024, 0, stream>>>(a); break;
             case 128: k_hist<128><<<grid, 1024, 0, stream>>>(a); break;
             case 33: k_hist<32, true><<<grid, 1024, 0, stream>>>(a); break;
             case 65: k_hist<64, true><<<grid, 1024, 0, stream>>>(a); break;
-            default: k_hist<128, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 129: k_hist<128, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 36: k_hist<32, false, 4><<<grid, 1024, 0, stream>>>(a); break;
+            case 68: k_hist<64, false, 4><<<grid, 1024, 0, stream>>>(a); break;
+            case 34: k_hist<32, false, 2><<<grid, 1024, 0, stream>>>(a); break;
+            case 66: k_hist<64, false, 2><<<grid, 1024, 0, stream>>>(a); break;
+            case 130: k_hist<128, false, 2><<<grid, 1024, 0, stream>>>(a); break;
+            default: throw std::logic_error("no histogram kernel for the slab");
             }
             launch_check("k_hist");
             if (profiled) {
@@ -940,7 +986,7 @@ struct Context {
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, s.col_stride.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width};
+            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, s.col_stride.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width, s.seg_shift()};
             k_hist_reduce<<<div_up(256ull * s.width, 32), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
@@ -1461,6 +1507,7 @@ struct Context {
         g.dsc = grow_dsc;
         g.target_groups = cus;
         g.ncg = ncg;
+        g.nsg = nsg;
         g.flush_rows = flush_rows();
         return g;
     }
@@ -1655,13 +1702,19 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     const Slab &sl = slabs[si];
                     StepArgs sa{sl.bins.p, packed.p, train.col.p, col16, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
                                 sl.col_bins.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
-                    switch (sl.width + (sl.wide ? 1u : 0u)) {
+                    switch (sl.kernel()) {
                     case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 64: k_step_rows<64><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 128: k_step_rows<128><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 33: k_step_rows<32, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 65: k_step_rows<64, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    default: k_step_rows<128, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 129: k_step_rows<128, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 36: k_step_rows<32, false, 4><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 68: k_step_rows<64, false, 4><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 34: k_step_rows<32, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 66: k_step_rows<64, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 130: k_step_rows<128, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    default: throw std::logic_error("no split-step kernel for the slab");
                     }
                     launch_check("k_step_rows");
                 }
@@ -1673,7 +1726,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
-                ScanStepArgs sca{d_cgs.p, gcol_feat.p, cat_feats.p, ncat, d_plans.p + parity};
+                ScanStepArgs sca{scan_feat.p, cat_feats.p, ncat, d_plans.p + parity};
                 if (has_narrow) k_step_scan<false><<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 if (has_wide) k_step_scan<true><<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 launch_check("k_step_scan");

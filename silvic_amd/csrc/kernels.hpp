@@ -322,24 +322,30 @@ __device__ __forceinline__ void hist_split(uint32_t n, uint32_t max_groups, uint
 }
 
 // A lane's four adds per row dword, in the conflict-free order: at step k byte x = (k + rot) % 4, i.e. bits 8x..8x+7
-// (xs[k] = 8x), goes to column 4d + x (cols[k]).
+// (xs[k] = 8x), is the row's byte i = 4d + x and goes to column i (cols[k]). In a packed slab (PACK features of at
+// most 256 / PACK bins a column) byte i goes to column i % W, in the rows of its segment i / W: cols[k] is then
+// the word offset of that segment's column, and a bin b adds to word b * W + cols[k] as in a byte slab (the bank
+// is still the column's).
+template <int W, int PACK>
 __device__ __forceinline__ void row_bin_lanes(uint32_t d, uint32_t rot, uint32_t (&xs)[4], uint32_t (&cols)[4]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const uint32_t x = (k + rot) & 3u;
+        const uint32_t i = 4u * d + x;
         xs[k] = 8u * x;
-        cols[k] = 4u * d + x;
+        cols[k] = PACK == 1 ? i : (i / W) * (256u / PACK) * W + i % W;
     }
 }
 
 // Adds gv to the LDS words (bin * W + column) of the four bins in a row dword: each bin is extracted in place (one
 // bit-field extract) and scaled into its word address with the column added (one shift-add).
-template <int W>
+template <int W, int PACK = 1>
 __device__ __forceinline__ void add_row_bins(int32_t *lds, uint32_t dw, int32_t gv, const uint32_t (&xs)[4],
                                              const uint32_t (&cols)[4]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t b = __builtin_amdgcn_ubfe(dw, xs[k], 8u);
+        uint32_t b = __builtin_amdgcn_ubfe(dw, xs[k], 8u);
+        if constexpr (PACK > 1) b &= 256u / PACK - 1u;  // a packed column's segment: invalid bins stay in it
         atomicAdd(&lds[b * W + cols[k]], gv);
     }
 }
@@ -359,10 +365,12 @@ __device__ __forceinline__ void add_row_bins_wide(int32_t *lds, uint32_t dw, int
 // Loads are branch-free: row positions past the range are clamped to its last row and their gradients
 // zeroed, so the compiler issues every load of a step back to back instead of one masked load at a time. A
 // wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
-// step, and hands them out with a shuffle. WIDE: the slab's rows are W / 4 two-byte bins.
-template <int W, bool WIDE = false>
+// step, and hands them out with a shuffle. WIDE: the slab's rows are W / 4 two-byte bins. PACK: the slab's rows
+// are W * PACK bytes, PACK features of at most 256 / PACK bins to an LDS column.
+template <int W, bool WIDE = false, int PACK = 1>
 __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
-    constexpr int DW = WIDE ? W / 8 : W / 4;  // dwords per row
+    static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
+    constexpr int DW = WIDE ? W / 8 : W * PACK / 4;  // dwords per row
     constexpr int RPW = WAVE / DW;            // rows per wave step
     // row ids of one step fit one wave-wide load; at W = 128 the 64 accumulator registers leave room for 8
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
@@ -386,7 +394,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
     uint32_t xs[4], cols[4];
-    row_bin_lanes(d, rot, xs, cols);
+    row_bin_lanes<W, PACK>(d, rot, xs, cols);
     const uint32_t *rows = a.rows + lb;
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     uint32_t start = blockIdx.x * per;
@@ -413,7 +421,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
             for (int u = 0; u < UNROLL; ++u) {
                 const int32_t gv = base + u * RPW + rsub < cend ? g[u] : 0;
                 if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
-                else add_row_bins<W>(lds, dw[u], gv, xs, cols);
+                else add_row_bins<W, PACK>(lds, dw[u], gv, xs, cols);
             }
         }
         __syncthreads();
@@ -447,6 +455,7 @@ struct ReduceArgs {
     uint32_t begin, count, side;
     uint32_t max_groups, min_rows_per_group;
     uint32_t width;     // W
+    uint32_t seg_shift; // a packed slab's column holds a feature each 2^seg_shift bins: 8 (one feature), 7 or 6
 };
 
 // A block takes 32 slots (bin * W + column) and splits the workgroups' partials of each into 8 stripes that meet in
@@ -460,7 +469,9 @@ __global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
     const uint32_t slots = 256u * a.width;
     const uint32_t tid = threadIdx.x, lane = tid & 31u, stripe = tid >> 5;
     const uint32_t s = blockIdx.x * 32u + lane, col = s % a.width, bin = s / a.width;
-    const bool on = s < slots && bin < a.col_bins[col];
+    // the slot's feature: segment bin >> seg_shift of the column (its index in the per-feature arrays), its bin
+    const uint32_t vb = bin & ((1u << a.seg_shift) - 1u), fs = (bin >> a.seg_shift) * a.width + col;
+    const bool on = s < slots && vb < a.col_bins[fs];
     int64_t g = 0, h = 0;
     if (on) {
         const int2 *p = reinterpret_cast<const int2 *>(a.partial) + s;
@@ -480,7 +491,7 @@ __global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
             g += red[0][k][lane];
             h += red[1][k][lane];
         }
-        const size_t o = 2 * (static_cast<size_t>(a.col_offset[col]) + static_cast<size_t>(bin) * a.col_stride[col]);
+        const size_t o = 2 * (static_cast<size_t>(a.col_offset[fs]) + static_cast<size_t>(vb) * a.col_stride[fs]);
         a.out[o] = g;
         a.out[o + 1] = h;
         if (a.parent) {
@@ -2126,7 +2137,8 @@ struct GrowState {
     double sg, sh;
     const struct DevScales *dsc;  // when set, the scales are these (made on the device), not sg and sh
     uint32_t target_groups;   // k_step_rows workgroups a step is spread over
-    uint32_t ncg;             // column groups of k_step_reduce and k_step_scan
+    uint32_t ncg;             // column groups of k_step_reduce
+    uint32_t nsg;             // scan groups of k_step_scan (four numerical features each)
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
     uint32_t pad_;
 };
@@ -2874,7 +2886,7 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             J.packed = (ntiles <= groups && g.flush_rows >= STEP_TILE) ? 1u : 0u;
             J.ways = reduce_ways(groups);
             red = hist ? g.ncg * J.ways : 0u;
-            scan = hist ? g.ncg : 0u;
+            scan = hist ? g.nsg : 0u;
             J.red_items = red;
             J.scan_items = scan;
             J.built_slot = hist ? static_cast<int32_t>(slot0 + hist_before) : -1;
@@ -3209,17 +3221,17 @@ __device__ __forceinline__ void tile_scatter(const StepView &v, uint32_t t, cons
 // The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
 // lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free. NW
 // waves take part; `wave` is this one's index among them.
-template <int W, bool WIDE, int UNROLL, int NW = 16>
+template <int W, bool WIDE, int PACK, int UNROLL, int NW = 16>
 __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
                                           const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6) {
-    constexpr int DW = WIDE ? W / 8 : W / 4;
+    constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
     constexpr uint32_t STEP = NW * RPW * UNROLL;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t d = lane % DW, rsub = lane / DW;
     const uint32_t rot = (lane & 31u) >> 3;
     uint32_t xs[4], cols[4];
-    row_bin_lanes(d, rot, xs, cols);
+    row_bin_lanes<W, PACK>(d, rot, xs, cols);
     const uint32_t last = c1 - 1;
     for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
         uint32_t r[UNROLL];
@@ -3236,7 +3248,7 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
         for (int u = 0; u < UNROLL; ++u) {
             const int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
             if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
-            else add_row_bins<W>(lds, dw[u], gv, xs, cols);
+            else add_row_bins<W, PACK>(lds, dw[u], gv, xs, cols);
         }
     }
 }
@@ -3282,11 +3294,13 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
     }
 }
 
-template <int W, bool WIDE = false>
+template <int W, bool WIDE = false, int PACK = 1>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
-    constexpr int DW = WIDE ? W / 8 : W / 4;
+    static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
+    constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
-    constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);  // rows per lane in multi-tile workgroups
+    // rows per lane in multi-tile workgroups (16 at W = 32 with packed columns spills)
+    constexpr int UNROLL = (W == 128 || (W == 32 && PACK > 1)) ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr int SLOTS = 256 * W / 1024;
     __shared__ int32_t lds[256 * W];
     __shared__ StepShared sh;
@@ -3335,9 +3349,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (v.hist) hist_list<W, WIDE, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (v.hist) hist_list<W, WIDE, PACK, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
         } else if (v.hist) {
-            hist_list<W, WIDE, 16>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, PACK, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         __syncthreads();  // the offset and the histogram are complete
         if (v.partition) tile_scatter(v, t, st, sh);
@@ -3350,7 +3364,8 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     // several tiles per workgroup: whenever flush_rows rows have gone into the packed words they are added into the
     // partial as {g, h} pairs; a workgroup that never flushes stores its partial packed instead
     int2 *pairs = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
-    const uint32_t col_bins = a.col_bins[tid % W];  // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W
+    // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W; a packed column's features are all stored
+    const uint32_t col_bins = PACK > 1 ? 256u : a.col_bins[tid % W];
     uint32_t pending = 0;  // rows added to the packed LDS words since they were last flushed
     bool flushed = false;
     // partition launches take tiles in ticket order, the next ticket drawn while the current tile is worked on (a
@@ -3392,7 +3407,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 }
                 uint32_t room = a.flush_rows - pending;
                 uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                hist_list<W, WIDE, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+                hist_list<W, WIDE, PACK, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
                 pending += c1 - c0;
                 c0 = c1;
             }
@@ -3400,11 +3415,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (!hist_done) hist_list<W, WIDE, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (!hist_done) hist_list<W, WIDE, PACK, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
             __syncthreads();  // the offset is in sh.prefix
             tile_scatter(v, t, st, sh);
         } else if (!hist_done) {
-            hist_list<W, WIDE, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, PACK, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         if (!hist_done) pending += nb;
         if (tn < v.ntiles) tile_bins(v, r);
@@ -3430,11 +3445,11 @@ struct ColGroup {
     uint64_t partial;  // the slab's partials, in {g, h} pairs from the start of the step partial buffer
     uint32_t width;    // the slab's W
     uint32_t c0;       // first column of the group in the slab
-    uint32_t gcol;     // first column of the group in the global column arrays
     uint32_t fmt;      // the slab's first k_step_rows workgroup in the partial-format flags
-    uint32_t offset[4];  // per column: its feature's first bin in the flat histogram
-    uint32_t bins[4];    // per column: the feature's bins (0 for padding)
-    uint32_t stride[4];  // per column: flat-histogram bins between its consecutive bins (4 in a wide slab)
+    uint32_t offset[4][4];  // per segment and column: its feature's first bin in the flat histogram
+    uint32_t bins[4][4];    // per segment and column: the feature's bins (0 for padding)
+    uint32_t stride[4];     // per column: flat-histogram bins between its consecutive bins (4 in a wide slab)
+    uint32_t seg_shift;     // a column holds a feature each 2^seg_shift bins (8: one; 7 or 6 in a packed slab)
 };
 
 // Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
@@ -3460,8 +3475,7 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
 }
 
 struct ScanStepArgs {
-    const ColGroup *cgs;        // [ncg]
-    const int32_t *col_feat;    // per global column: the feature, -1 for padding
+    const int32_t *scan_feat;   // the numerical features to scan, four a scan group, -1 for padding
     const uint32_t *cat_feats;  // the categorical features (k_step_cat)
     uint32_t ncat;
     StepPlan *plan;
@@ -3616,12 +3630,13 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         const uint32_t *fmt = a.fmt + cg.fmt + J.group_base;
         // the parent's bins are loaded with the partials (the writes below need them); every partial is first read
         // as packed, and a {g, h} pair partial (a workgroup that flushed) is read again in its own layout
+        const uint32_t seg = bin >> cg.seg_shift, vb = bin & ((1u << cg.seg_shift) - 1u);
         int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (bin < cg.bins[c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + static_cast<size_t>(bin) * cg.stride[c]);
+                if (vb < cg.bins[seg][c]) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[seg][c]) + static_cast<size_t>(vb) * cg.stride[c]);
                     pg[c] = parent[o];
                     ph[c] = parent[o + 1];
                 }
@@ -3683,8 +3698,8 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (bin < cg.bins[c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[c]) + static_cast<size_t>(bin) * cg.stride[c]);
+                if (vb < cg.bins[seg][c]) {
+                    const size_t o = 2 * (static_cast<size_t>(cg.offset[seg][c]) + static_cast<size_t>(vb) * cg.stride[c]);
                     built[o] = sg[c];
                     built[o + 1] = sh[c];
                     parent[o] = pg[c] - sg[c];
@@ -3708,9 +3723,8 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
         const uint32_t gi = item / (2u * CG_COLS), sub = item % (2u * CG_COLS);
         const uint32_t j = job_of(P.scan_base, P.njobs, gi);
         const JobPlan &J = P.jobs[j];
-        const ColGroup &cg = a.cgs[gi - J.scan_base];
         const uint32_t scol = sub % CG_COLS, child = sub / CG_COLS;
-        const int32_t sf = a.col_feat[cg.gcol + scol];
+        const int32_t sf = a.scan_feat[(gi - J.scan_base) * CG_COLS + scol];
         if (sf < 0) continue;
         const FeatDev sm = g.feats[sf];
         if (sm.kind == 2 || (sm.wide != 0) != WIDE) continue;

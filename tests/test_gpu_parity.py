@@ -465,7 +465,7 @@ def params_to_lightgbm(params):
     (2, 100_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=63, bagging_fraction=0.8, bagging_freq=2,
                           feature_fraction=0.7, lambda_l2=1.0), 8),
     (2, 120_000, 28, dict(objective=_abi.OBJ_BINARY, num_leaves=63, categorical=True), 6),
-    # the wide sparse shape: 2000 features of at most 63 bins (mostly a handful) in 16 slabs
+    # the wide sparse shape: 2000 features of at most 63 bins (mostly a handful) in 8 packed slabs
     (4, 30_000, 2000, dict(objective=_abi.OBJ_BINARY, num_leaves=63), 4),
     # leaves not renewed: the tree's own outputs from the device scales (GrowState's scales, no host copy)
     (2, 150_000, 64, dict(objective=_abi.OBJ_BINARY, num_leaves=127, quant_train_renew_leaf=0), 6),
