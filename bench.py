@@ -22,17 +22,17 @@ METRIC = "histogram bins/s + boosting iters/s at 10M×128 int8-quantized; % HBM 
 WORKLOADS = {
     "binary": dict(config=2, rows=10_000_000, cols=128, leaves=255, max_bin=255, objective="binary",
                    describe="binary, {rows} rows x {cols} f32 features binned to <=255 bins (half N(0,1), quarter "
-                            "lognormal, quarter integers, 10% NaN), {leaves} leaves, num_grad_quant_bins=4"),
+                            "lognormal, quarter integers, 10% NaN), {leaves} leaves, num_grad_quant_bins={bins}"),
     "lambdarank": dict(config=3, rows=2_000_000, cols=136, leaves=127, max_bin=255, objective="lambdarank",
                        describe="lambdarank NDCG, {rows} documents in queries of 10-200 (Zipf-like), {cols} f32 "
                                 "features, labels 0-4, <=255 bins, {leaves} leaves, truncation 30, "
-                                "num_grad_quant_bins=4"),
+                                "num_grad_quant_bins={bins}"),
     "sparse": dict(config=4, rows=1_000_000, cols=2000, leaves=63, max_bin=63, objective="binary",
                    describe="binary, {rows} rows x {cols} f32 features, 98% exact zeros (nonzeros exp(1) or integers "
-                            "of cardinality 2-16), binned to <=63 bins, {leaves} leaves, num_grad_quant_bins=4"),
+                            "of cardinality 2-16), binned to <=63 bins, {leaves} leaves, num_grad_quant_bins={bins}"),
     "wide": dict(config=5, rows=50_000_000, cols=32, leaves=2047, max_bin=1023, objective="regression",
                  describe="L2 regression, {rows} rows x {cols} U[0,1) f32 features binned to <=1023 bins (two-byte "
-                          "bins), piecewise-constant target, {leaves} leaves, num_grad_quant_bins=4"),
+                          "bins), piecewise-constant target, {leaves} leaves, num_grad_quant_bins={bins}"),
 }
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "split_step_traffic_10Mx128.md")
@@ -82,13 +82,15 @@ def timed_window(rows, warmup, steps):
     return rows[begin(warmup):begin(warmup + steps)]
 
 
-def step_kernels(data):
+def step_kernels(data, quant_bins=4):
     """The k_step_rows instances the backend launches for `data`, with their slab counts. Byte features in the order
     of their bin classes (more than 128 bins, more than 64, the rest), 128 to a slab while it holds one of more than
     128 bins, else 256; a slab's rows the fewest bytes (32..256) that hold its features, and as many features to an
     LDS column as that row length and its largest bin count allow (four of at most 64 bins, two of at most 128).
-    Two-byte features 32 to a slab."""
+    Two-byte features 32 to a slab. With units the packed 16/16 LDS words would flush every fewer than 256 rows,
+    separate 32-bit g and h counters: 64 byte or 16 two-byte features a slab, one a column."""
     bits = [g.bin_bits or 8 for g in data.groups]
+    q32 = min(32767 // max(quant_bins // 2, 1), 65535 // max(quant_bins, 1)) < 256
 
     def cls(b):
         return 4 if b <= 64 else (2 if b <= 128 else 1)
@@ -98,18 +100,20 @@ def step_kernels(data):
     out = {}
     b = 0
     while b < len(nb):
-        e = min(len(nb), b + (128 if nb[b] == 1 else 256))
-        n, max_pack = e - b, min(nb[b:e])
+        e = min(len(nb), b + (64 if q32 else (128 if nb[b] == 1 else 256)))
+        n, max_pack = e - b, 1 if q32 else min(nb[b:e])
         row = 32
         while row < n:
             row *= 2
         pack = next((p for p in (4, 2) if p <= max_pack and 32 * p <= row and row // p <= 128), 1)
         k = f"k_step_rows<{row // pack}>" if pack == 1 else f"k_step_rows<{row // pack}, false, {pack}>"
+        if q32:
+            k = f"k_step_rows<{row}, false, 1, true>"
         out[k] = out.get(k, 0) + 1
         b = e
-    for i in range(0, wide, 32):
-        cols = 4 * min(32, wide - i)
-        k = f"k_step_rows<{32 if cols <= 32 else (64 if cols <= 64 else 128)}, true>"
+    for i in range(0, wide, 16 if q32 else 32):
+        cols = 4 * min(16 if q32 else 32, wide - i)
+        k = f"k_step_rows<{32 if cols <= 32 else (64 if cols <= 64 else 128)}, true{', 1, true' if q32 else ''}>"
         out[k] = out.get(k, 0) + 1
     return ", ".join(f"{k} x{n}" for k, n in out.items())
 
@@ -279,6 +283,8 @@ def main():
     ap.add_argument("--rows", type=int, default=None)
     ap.add_argument("--cols", type=int, default=None)
     ap.add_argument("--leaves", type=int, default=None)
+    ap.add_argument("--quant-bins", type=int, default=4, metavar="B",
+                    help="num_grad_quant_bins (the reference takes 2..64; up to 32766, 16-bit units, is an extension)")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of oracle work for the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -320,7 +326,8 @@ def main():
     data = silvic_amd.synthetic(wl["config"], rows=args.rows, cols=args.cols, seed=7, max_bin=wl["max_bin"])
     log(f"generated {args.workload}: {args.rows} x {args.cols} in {time.perf_counter() - t0:.1f}s; total_bins "
         f"{data.total_bins}")
-    params = {"objective": wl["objective"], "num_leaves": args.leaves, "num_grad_quant_bins": 4, "device_type": "rocm"}
+    params = {"objective": wl["objective"], "num_leaves": args.leaves, "num_grad_quant_bins": args.quant_bins,
+              "device_type": "rocm"}
     t0 = time.perf_counter()
     trainer = silvic_amd.Trainer(params, data)
     log(f"loaded on {trainer.backend.name()} in {time.perf_counter() - t0:.1f}s")
@@ -378,13 +385,15 @@ def main():
         threads = oracle.threads()
         objective = {"binary": _abi.OBJ_BINARY, "lambdarank": _abi.OBJ_LAMBDARANK,
                      "regression": _abi.OBJ_REGRESSION}[wl["objective"]]
-        p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=1)
+        p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=1,
+                                  num_grad_quant_bins=args.quant_bins)
         t0 = time.perf_counter()
         m1 = oracle.train(data, p)
         one = time.perf_counter() - t0
         n_cpu = max(1, min(args.warmup + steps, int(args.cpu_budget / max(one, 1e-3))))
         if n_cpu > 1:
-            p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=n_cpu)
+            p = oracle.default_params(objective=objective, num_leaves=args.leaves, num_iterations=n_cpu,
+                                      num_grad_quant_bins=args.quant_bins)
             t0 = time.perf_counter()
             m = oracle.train(data, p)
             cpu_elapsed = time.perf_counter() - t0
@@ -409,10 +418,11 @@ def main():
                "hist_bins_per_s": m.hist_bins / m.times["histogram"] if m.times["histogram"] else None,
                "trees_identical": f"{same}/{compared}", "seconds": cpu_elapsed}
 
-    describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves)
-    slab = step_kernels(data)
+    describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves, bins=args.quant_bins)
+    slab = step_kernels(data, args.quant_bins)
     out = {
-        "metric": METRIC if args.workload == "binary" else f"boosting iters/s, {args.workload} workload; % HBM peak",
+        "metric": METRIC if args.workload == "binary" and args.quant_bins == 4 else
+                  f"boosting iters/s, {args.workload} workload at num_grad_quant_bins={args.quant_bins}; % HBM peak",
         "value": iters_per_s,
         "unit": "iters/s",
         "n_gpus": 1,

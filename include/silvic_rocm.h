@@ -280,7 +280,10 @@ int srocm_set_gradients(void *ctx, const float *grad, const float *hess, uint64_
  * on the device (no counterpart in the trait: for callers that check or reuse them on the host). */
 int srocm_gradients(void *ctx, float *grad, float *hess, size_t len);
 
-/* Backend::quantize (mod.rs:134-135). */
+/* Backend::quantize (mod.rs:134-135). Units up to grad_max_q 32767 and hess_max_q 65535 (the halves of the packed
+ * word), whose largest times the rows one histogram workgroup takes stays below 2^31 (SROCM_ERR_UNSUPPORTED
+ * otherwise: a workgroup's sums are 32-bit). Units of more than 127 (g) or 255 (h) are an extension, accumulated in
+ * separate 32-bit LDS counters rather than packed words; the slabs are laid out again when the mode changes. */
 int srocm_quantize(void *ctx, const srocm_quant_spec *spec);
 
 /* Backend::reset_partition (mod.rs:137-138). */
@@ -336,7 +339,8 @@ typedef struct srocm_train_params {
     double sigmoid;
     double learning_rate;
     int32_t max_depth;
-    uint32_t num_grad_quant_bins;
+    uint32_t num_grad_quant_bins;  /* even, 2..=64 as the reference (config.rs:416-421); up to 32766 as an
+                                    * extension (g_q within +-16383, h_q at most 32766: 16-bit units) */
     srocm_split_config cfg;
     double bagging_fraction;
     uint32_t bagging_freq;

@@ -261,7 +261,6 @@ struct HostTree {
 // The context
 // ---------------------------------------------------------------------------------------------------------
 
-constexpr uint32_t MAX_SLAB_FEATURES = 128;
 constexpr uint32_t RANK_DEVICE_MAX = 512;  // rows of the largest query k_rank_pairs takes
 constexpr uint32_t HIST_MIN_ROWS = 2048;   // rows per histogram workgroup before another one is used
 constexpr uint64_t ROW_BLOCK = 256;
@@ -270,6 +269,7 @@ struct Slab {
     uint32_t width = 0;            // W: LDS and partial columns
     bool wide = false;             // two-byte bins: W / 4 features, each 4 virtual columns (k_hist<W, true>)
     uint32_t pack = 1;             // byte bins, `pack` features of at most 256 / pack bins a column (k_hist<W, false, pack>)
+    bool q32 = false;              // separate 32-bit g and h LDS counters (k_hist<W, wide, 1, true>)
     std::vector<uint32_t> feats;   // feature ids
     DevBuf<uint8_t> bins;          // [rows][row_bytes()]
     DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per feature slot: segment * W + column (virtual column)
@@ -277,7 +277,7 @@ struct Slab {
     uint32_t capacity() const { return wide ? width / 4 : width * pack; }
     uint32_t seg_shift() const { return pack == 4 ? 6u : (pack == 2 ? 7u : 8u); }
     uint32_t slots() const { return width * pack; }  // entries of the per-slot arrays
-    uint32_t kernel() const { return width + (wide ? 1u : 0u) + (pack > 1 ? pack : 0u); }  // launch switch key
+    uint32_t kernel() const { return width + (wide ? 1u : 0u) + (pack > 1 ? pack : 0u) + (q32 ? 1000u : 0u); }  // launch key
     uint64_t step_partial_off = 0;  // the slab's partials in the step partial buffer, in {g, h} pairs
 };
 
@@ -343,6 +343,9 @@ struct Context {
     std::vector<Slab> slabs;
     uint64_t rows = 0, row_offset = 0;
     uint32_t max_width = 32;
+    bool q32 = false;  // slabs laid out for separate 32-bit g and h LDS counters (set_mode)
+    uint32_t hist_cap = 0;     // k_hist workgroups a leaf is spread over at most
+    uint32_t step_target = 0;  // k_step_rows workgroups a step is spread over (its grid: step_target + JMAX)
     uint32_t col16 = 0;                     // some group has two-byte bins: column-major bins are u16
     bool has_narrow = true, has_wide = false;  // features of one-byte / two-byte bins (a scan kernel each)
     std::vector<uint32_t> group_bits;  // per group: bits per bin, 8, 16 (wide slabs) or 4 (two to a byte)
@@ -621,62 +624,9 @@ struct Context {
             bins_seen += m.num_bins;
         }
         (void)bins_seen;
-        // slabs. Two-byte features: up to 32 a slab, in feature order. Byte features: in the order of their bin
-        // classes (more than 128 bins, more than 64, the rest; feature order within a class), up to 128 a slab
-        // while the slab holds a feature of more than 128 bins, else up to 256. A slab's rows are the fewest bytes
-        // (32, 64, 128 or 256) that hold its features, and its LDS columns hold as many features each (`pack`) as
-        // that row length and its largest bin count allow: four of at most 64 bins, two of at most 128.
-        slabs.clear();
-        max_width = 32;
-        nt_slab.assign(nt_feat.size(), 0);
-        nt_slab_col.assign(nt_feat.size(), 0);
-        {
-            auto bin_class = [&](uint32_t i) {  // 4: at most 64 bins, 2: at most 128, 1: more
-                const uint32_t nb = feats[nt_feat[i]].num_bins;
-                return nb <= 64 ? 4u : (nb <= 128 ? 2u : 1u);
-            };
-            std::vector<uint32_t> narrow, wide;
-            for (uint32_t c : {1u, 2u, 4u})
-                for (uint32_t i = 0; i < nt_feat.size(); ++i)
-                    if (group_bits[feats[nt_feat[i]].group] != 16 && bin_class(i) == c) narrow.push_back(i);
-            for (uint32_t i = 0; i < nt_feat.size(); ++i)
-                if (group_bits[feats[nt_feat[i]].group] == 16) wide.push_back(i);
-            auto add_slab = [&](const std::vector<uint32_t> &members, size_t b, size_t e, bool is_wide) {
-                Slab s;
-                s.wide = is_wide;
-                uint32_t max_pack = 4;
-                for (size_t k = b; k < e; ++k) {
-                    nt_slab[members[k]] = static_cast<uint32_t>(slabs.size());
-                    nt_slab_col[members[k]] = static_cast<uint32_t>(k - b);
-                    s.feats.push_back(nt_feat[members[k]]);
-                    max_pack = std::min(max_pack, bin_class(members[k]));
-                }
-                const uint32_t n = static_cast<uint32_t>(e - b);
-                if (is_wide) {  // four virtual columns a feature
-                    s.width = 4 * n <= 32 ? 32 : (4 * n <= 64 ? 64 : 128);
-                } else {
-                    uint32_t row = 32;
-                    while (row < n) row *= 2;
-                    s.pack = 1;
-                    for (uint32_t p : {4u, 2u})
-                        if (p <= max_pack && 32 * p <= row && row / p <= 128) {
-                            s.pack = p;
-                            break;
-                        }
-                    s.width = row / s.pack;
-                }
-                max_width = std::max(max_width, s.width);
-                slabs.push_back(std::move(s));
-            };
-            for (size_t b = 0; b < narrow.size();) {
-                const size_t per = bin_class(narrow[b]) == 1 ? MAX_SLAB_FEATURES : 2 * MAX_SLAB_FEATURES;
-                const size_t e = std::min(narrow.size(), b + per);
-                add_slab(narrow, b, e, false);
-                b = e;
-            }
-            for (size_t b = 0; b < wide.size(); b += MAX_SLAB_FEATURES / 4)
-                add_slab(wide, b, std::min(wide.size(), b + MAX_SLAB_FEATURES / 4), true);
-        }
+        q32 = false;
+        hist_cap = step_target = cus;
+        build_slabs();
         // device buffers
         train = DevData{};
         upload_bins(t, train, true);
@@ -704,7 +654,6 @@ struct Context {
         part2.alloc(rows);
         block_left.alloc(cus * 4 + 16);
         scalars.alloc(16);
-        partial.alloc(static_cast<size_t>(cus) * 256 * max_width * 2);
         std::vector<FeatDev> fd(nf);
         has_narrow = has_wide = false;
         for (uint32_t f = 0; f < nf; ++f) {
@@ -716,6 +665,83 @@ struct Context {
         }
         dfeats.alloc(nf);
         hip_check(hipMemcpy(dfeats.p, fd.data(), nf * sizeof(FeatDev), hipMemcpyHostToDevice), "upload features");
+        build_slab_tables();
+        used.assign(nf, 1);
+        part_len = 0;
+        max_gq = max_hq = 1;
+        quantized_once = false;
+        grow_capacity = 0;
+        pool.release();
+        sync();
+        loaded = true;
+    }
+
+    // Slabs. Two-byte features: up to 32 a slab, in feature order. Byte features: in the order of their bin classes
+    // (more than 128 bins, more than 64, the rest; feature order within a class), up to 128 a slab while the slab
+    // holds a feature of more than 128 bins, else up to 256. A slab's rows are the fewest bytes (32, 64, 128 or
+    // 256) that hold its features, and its LDS columns hold as many features each (`pack`) as that row length and
+    // its largest bin count allow: four of at most 64 bins, two of at most 128. With separate 32-bit g and h LDS
+    // counters (q32) a slab has at most 64 columns and one feature a column: 64 byte or 16 two-byte features.
+    void build_slabs() {
+        slabs.clear();
+        max_width = 32;
+        nt_slab.assign(nt_feat.size(), 0);
+        nt_slab_col.assign(nt_feat.size(), 0);
+        {
+            const uint32_t max_cols = q32 ? 64u : 128u;  // LDS columns a slab can take
+            auto bin_class = [&](uint32_t i) {  // 4: at most 64 bins, 2: at most 128, 1: more
+                const uint32_t nb = feats[nt_feat[i]].num_bins;
+                return nb <= 64 ? 4u : (nb <= 128 ? 2u : 1u);
+            };
+            std::vector<uint32_t> narrow, wide;
+            for (uint32_t c : {1u, 2u, 4u})
+                for (uint32_t i = 0; i < nt_feat.size(); ++i)
+                    if (group_bits[feats[nt_feat[i]].group] != 16 && bin_class(i) == c) narrow.push_back(i);
+            for (uint32_t i = 0; i < nt_feat.size(); ++i)
+                if (group_bits[feats[nt_feat[i]].group] == 16) wide.push_back(i);
+            auto add_slab = [&](const std::vector<uint32_t> &members, size_t b, size_t e, bool is_wide) {
+                Slab s;
+                s.wide = is_wide;
+                s.q32 = q32;
+                uint32_t max_pack = q32 ? 1u : 4u;
+                for (size_t k = b; k < e; ++k) {
+                    nt_slab[members[k]] = static_cast<uint32_t>(slabs.size());
+                    nt_slab_col[members[k]] = static_cast<uint32_t>(k - b);
+                    s.feats.push_back(nt_feat[members[k]]);
+                    max_pack = std::min(max_pack, bin_class(members[k]));
+                }
+                const uint32_t n = static_cast<uint32_t>(e - b);
+                if (is_wide) {  // four virtual columns a feature
+                    s.width = 4 * n <= 32 ? 32 : (4 * n <= 64 ? 64 : 128);
+                } else {
+                    uint32_t row = 32;
+                    while (row < n) row *= 2;
+                    s.pack = 1;
+                    for (uint32_t p : {4u, 2u})
+                        if (p <= max_pack && 32 * p <= row && row / p <= max_cols) {
+                            s.pack = p;
+                            break;
+                        }
+                    s.width = row / s.pack;
+                }
+                max_width = std::max(max_width, s.width);
+                slabs.push_back(std::move(s));
+            };
+            for (size_t b = 0; b < narrow.size();) {
+                const size_t per = std::min<size_t>(256, static_cast<size_t>(max_cols) * (q32 ? 1u : bin_class(narrow[b])));
+                const size_t e = std::min(narrow.size(), b + per);
+                add_slab(narrow, b, e, false);
+                b = e;
+            }
+            for (size_t b = 0; b < wide.size(); b += max_cols / 4)
+                add_slab(wide, b, std::min(wide.size(), b + max_cols / 4), true);
+        }
+    }
+
+    // The slab tables: per slab slot its feature's flat bins, the column groups of k_step_reduce, the numerical
+    // features (in groups of CG_COLS) of k_step_scan, the categorical ones of k_step_cat, and the partial buffers.
+    void build_slab_tables() {
+        partial.alloc(static_cast<size_t>(hist_cap) * 256 * max_width * 2);
         for (auto &s : slabs) {
             // slot i: a byte feature's (column i % W, segment i / W); in a wide slab, virtual column i, bins
             // congruent to i / (W/4) mod 4 of feature i % (W/4)
@@ -792,14 +818,57 @@ struct Context {
             if (!cats.empty())
                 hip_check(hipMemcpy(cat_feats.p, cats.data(), cats.size() * 4, hipMemcpyHostToDevice), "upload categorical features");
         }
-        used.assign(nf, 1);
-        part_len = 0;
-        max_gq = max_hq = 1;
-        quantized_once = false;
-        grow_capacity = 0;
-        pool.release();
+    }
+
+    // Chooses between packed 16/16 LDS words and separate 32-bit g and h counters (`q32`, for quantized units the
+    // packed words would flush every few rows), and the workgroup counts: with units of up to `units`, no
+    // workgroup may add up more than (2^31 - 1) / units rows, since its sums are 32-bit. Packed words take at most
+    // 255 units, so one workgroup per compute unit always fits; separate counters take up to 65535, for which the
+    // histogram and split-step workgroups are multiplied as the rows need. When the mode changes the slabs are laid
+    // out again and refilled on the device from the column-major bins; when the counts change, the tables and
+    // partial buffers follow.
+    void set_mode(bool want, int64_t units) {
+        uint32_t hc = cus, st = cus;
+        if (want) {
+            const uint64_t cap = 2147483647ull / static_cast<uint64_t>(std::max<int64_t>(units, 1));  // rows a workgroup takes
+            const uint64_t n = std::max<uint64_t>(rows, 1);
+            // k_hist: div_up(n, groups) rows, rounded up to 64, at least HIST_MIN_ROWS (max_workgroup_rows)
+            hc = static_cast<uint32_t>(std::max<uint64_t>(cus, div_up(n, cap - 128)));
+            // k_step_rows: at most div_up(tiles + JMAX, target - JMAX) tiles of STEP_TILE rows
+            st = static_cast<uint32_t>(std::max<uint64_t>(cus, div_up(div_up(n, STEP_TILE) + JMAX, cap / STEP_TILE) + JMAX));
+        }
+        if (want == q32 && hc == hist_cap && st == step_target) return;
         sync();
-        loaded = true;
+        const bool relayout = want != q32;
+        q32 = want;
+        hist_cap = hc;
+        step_target = st;
+        if (!relayout) {
+            build_slab_tables();
+            if (grow_capacity) step_partial.alloc(2 * step_partial_pairs);
+            sync();
+            return;
+        }
+        build_slabs();
+        for (auto &sl : slabs) {
+            sl.bins.alloc(std::max<uint64_t>(1, rows * sl.row_bytes()));
+            hip_check(hipMemsetAsync(sl.bins.p, 0, std::max<uint64_t>(1, rows * sl.row_bytes()), stream), "zero slab");
+        }
+        const uint64_t cb = col16 ? 2 : 1;
+        for (uint32_t nt = 0; rows && nt < nt_feat.size(); ++nt) {
+            const Slab &sl = slabs[nt_slab[nt]];
+            RepackTo to{nullptr, col16, sl.bins.p, sl.row_bytes(), sl.wide ? 1u : 0u, nt_slab_col[nt]};
+            repack(train.col.p + static_cast<size_t>(nt) * rows * cb, static_cast<uint32_t>(cb), 0, col16 ? 16u : 8u, rows, to);
+        }
+        build_slab_tables();
+        if (grow_capacity) step_partial.alloc(2 * step_partial_pairs);
+        sync();
+    }
+
+    // packed 16/16 words flush every fewer rows than this: separate counters instead
+    static constexpr uint32_t Q32_BELOW_FLUSH = 256;
+    static uint32_t packed_flush_rows(int64_t gq, int64_t hq) {
+        return static_cast<uint32_t>(std::min(32767 / std::max<int64_t>(gq, 1), 65535 / std::max<int64_t>(hq, 1)));
     }
 
     // Repacks a dataset's groups into slab rows (training set) and column-major bins, on the device.
@@ -870,13 +939,13 @@ struct Context {
         return read_maxima();
     }
 
-    // The most rows one histogram workgroup adds up: k_hist spreads a leaf over at most one workgroup per compute
-    // unit in multiples of 64 rows (at least HIST_MIN_ROWS each); a split step gives a workgroup at most
-    // ceil(tiles / (cus - JMAX)) tiles of a job, the step's tiles being at most rows / STEP_TILE + JMAX.
+    // The most rows one histogram workgroup adds up: k_hist spreads a leaf over at most hist_cap workgroups in
+    // multiples of 64 rows (at least HIST_MIN_ROWS each); a split step gives a workgroup at most
+    // ceil(tiles / (step_target - JMAX)) tiles of a job, the step's tiles being at most rows / STEP_TILE + JMAX.
     uint64_t max_workgroup_rows() const {
         const uint64_t n = std::max<uint64_t>(rows, 1);
-        const uint64_t hist = div_up(std::max<uint64_t>(div_up(n, cus), HIST_MIN_ROWS), 64) * 64 + 64;
-        const uint64_t share = cus > JMAX ? cus - JMAX : 1;
+        const uint64_t hist = div_up(std::max<uint64_t>(div_up(n, hist_cap), HIST_MIN_ROWS), 64) * 64 + 64;
+        const uint64_t share = step_target > JMAX ? step_target - JMAX : 1;
         const uint64_t step = div_up(div_up(n, STEP_TILE) + JMAX, share) * STEP_TILE;
         return std::max(hist, step);
     }
@@ -884,9 +953,12 @@ struct Context {
     // Quantized units a histogram can take: a packed word holds g as a signed 16-bit half and h as an unsigned one,
     // and a workgroup's sums of either are i32 (the reference's CPU sums are i64, cpu.rs:517-525), so
     // max_q * max_workgroup_rows() must stay below 2^31.
-    void check_quant_units(int64_t grad_max_q, int64_t hess_max_q) const {
+    static void check_unit_range(int64_t grad_max_q, int64_t hess_max_q) {
         if (grad_max_q < 1 || grad_max_q > 32767 || hess_max_q < 1 || hess_max_q > 65535)
             fail(SROCM_ERR_UNSUPPORTED, "quantized units must lie in 1..=32767 for gradients and 1..=65535 for hessians");
+    }
+    void check_quant_units(int64_t grad_max_q, int64_t hess_max_q) const {
+        check_unit_range(grad_max_q, hess_max_q);
         const uint64_t wg = max_workgroup_rows();
         if (static_cast<uint64_t>(std::max(grad_max_q, hess_max_q)) * wg > 2147483647ull)
             fail(SROCM_ERR_UNSUPPORTED, "quantized units up to " + std::to_string(std::max(grad_max_q, hess_max_q)) + " over " +
@@ -895,6 +967,8 @@ struct Context {
 
     void quantize(const srocm_quant_spec &s) {
         require_loaded();
+        check_unit_range(s.grad_max_q, s.hess_max_q);
+        set_mode(packed_flush_rows(s.grad_max_q, s.hess_max_q) < Q32_BELOW_FLUSH, std::max(s.grad_max_q, s.hess_max_q));
         check_quant_units(s.grad_max_q, s.hess_max_q);
         QuantDev q{s.inv_grad_scale, s.inv_hess_scale, s.grad_max_q, s.hess_max_q, s.constant_hessian, s.stochastic, s.seed, s.iteration};
         if (rows) {
@@ -938,14 +1012,16 @@ struct Context {
     // ------------------------------------------------------------------------------------------------
 
     // rows a packed word takes before its sums could leave their halves: g (low 16 bits, signed) within +-32767,
-    // h (high 16 bits, never negative) at most 65535
+    // h (high 16 bits, never negative) at most 65535; with separate counters, rows before an i32 counter could
+    // overflow (check_quant_units keeps a workgroup's rows below that)
     uint32_t flush_rows() const {
-        return static_cast<uint32_t>(std::min(32767 / std::max<int64_t>(max_gq, 1), 65535 / std::max<int64_t>(max_hq, 1)));
+        if (q32) return static_cast<uint32_t>(2147483647 / std::max<int64_t>(std::max(max_gq, max_hq), 1));
+        return packed_flush_rows(max_gq, max_hq);
     }
 
     uint32_t hist_groups(uint64_t n) const {
         uint32_t want = div_up(std::max<uint64_t>(n, 1), HIST_MIN_ROWS);
-        return std::max<uint32_t>(1, std::min<uint32_t>(want, cus));
+        return std::max<uint32_t>(1, std::min<uint32_t>(want, hist_cap));
     }
 
     // The histogram of rows part[begin..+count] (or the `side` child of that range split at *dev_left) into
@@ -978,6 +1054,10 @@ struct Context {
             case 34: k_hist<32, false, 2><<<grid, 1024, 0, stream>>>(a); break;
             case 66: k_hist<64, false, 2><<<grid, 1024, 0, stream>>>(a); break;
             case 130: k_hist<128, false, 2><<<grid, 1024, 0, stream>>>(a); break;
+            case 1032: k_hist<32, false, 1, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 1064: k_hist<64, false, 1, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 1033: k_hist<32, true, 1, true><<<grid, 1024, 0, stream>>>(a); break;
+            case 1065: k_hist<64, true, 1, true><<<grid, 1024, 0, stream>>>(a); break;
             default: throw std::logic_error("no histogram kernel for the slab");
             }
             launch_check("k_hist");
@@ -1430,7 +1510,7 @@ struct Context {
     TreeLayout tree_layout;
     uint32_t grow_capacity = 0;
 
-    uint32_t k1_groups() const { return cus + JMAX; }  // k_step_rows' grid
+    uint32_t k1_groups() const { return step_target + JMAX; }  // k_step_rows' grid
     uint32_t scan_blocks() const { return 8 * cus; }   // k_step_scan's grid: four waves a block, a wave per item
     uint32_t reduce_blocks() const { return 8 * cus; } // k_step_reduce's grid
 
@@ -1505,7 +1585,7 @@ struct Context {
         g.sg = spec.grad_scale;
         g.sh = spec.hess_scale;
         g.dsc = grow_dsc;
-        g.target_groups = cus;
+        g.target_groups = step_target;
         g.ncg = ncg;
         g.nsg = nsg;
         g.flush_rows = flush_rows();
@@ -1588,8 +1668,12 @@ __global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint3
         if (bits == 16) b = static_cast<uint32_t>(row[column]) | (static_cast<uint32_t>(row[column + 1]) << 8);
         else if (bits == 4) b = (static_cast<uint32_t>(row[column >> 1]) >> (4 * (column & 1u))) & 15u;
         else b = row[column];
-        if (to.col16) reinterpret_cast<uint16_t *>(to.col)[r] = static_cast<uint16_t>(b);
-        else to.col[r] = static_cast<uint8_t>(b);
+        if (!to.col) {
+        } else if (to.col16) {
+            reinterpret_cast<uint16_t *>(to.col)[r] = static_cast<uint16_t>(b);
+        } else {
+            to.col[r] = static_cast<uint8_t>(b);
+        }
         if (!to.slab) continue;
         uint8_t *dst = to.slab + r * to.row_bytes;
         if (to.slab_wide) reinterpret_cast<uint16_t *>(dst)[to.slab_col] = static_cast<uint16_t>(b);
@@ -1714,6 +1798,10 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     case 34: k_step_rows<32, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 66: k_step_rows<64, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     case 130: k_step_rows<128, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 1032: k_step_rows<32, false, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 1064: k_step_rows<64, false, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 1033: k_step_rows<32, true, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    case 1065: k_step_rows<64, true, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
                     default: throw std::logic_error("no split-step kernel for the slab");
                     }
                     launch_check("k_step_rows");
@@ -1968,6 +2056,8 @@ static void feature_mask(const std::vector<srocm_feature> &feats, double fractio
 uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t count, srocm_grown_tree *trees) {
     require_loaded();
     bool constant_hessian = objective == SROCM_OBJ_REGRESSION && !has_weight;  // objective/mod.rs:84-89
+    check_unit_range(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
+    set_mode(packed_flush_rows(p.num_grad_quant_bins / 2, p.num_grad_quant_bins) < Q32_BELOW_FLUSH, p.num_grad_quant_bins);
     check_quant_units(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
     uint32_t done = 0;
     HostTree tree;
@@ -2383,8 +2473,10 @@ int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iter
     return guard(ctx, [&](Context &c) {
         if (!params) fail(SROCM_ERR_CONFIG, "null parameters");
         if (params->num_leaves < 2) fail(SROCM_ERR_CONFIG, "num_leaves must be at least 2");
-        if (params->num_grad_quant_bins < 2 || params->num_grad_quant_bins > 64 || params->num_grad_quant_bins % 2)
-            fail(SROCM_ERR_CONFIG, "num_grad_quant_bins must be even and in 2..=64");
+        // the reference takes 2..=64 (config.rs:416-421); up to 32766 is an extension (a packed row word holds h_q
+        // below 32768)
+        if (params->num_grad_quant_bins < 2 || params->num_grad_quant_bins > 32766 || params->num_grad_quant_bins % 2)
+            fail(SROCM_ERR_CONFIG, "num_grad_quant_bins must be even and in 2..=32766");
         uint32_t n = c.boost(*params, first_iteration, count, trees);
         if (trained) *trained = n;
     });

@@ -338,27 +338,44 @@ __device__ __forceinline__ void row_bin_lanes(uint32_t d, uint32_t rot, uint32_t
 }
 
 // Adds gv to the LDS words (bin * W + column) of the four bins in a row dword: each bin is extracted in place (one
-// bit-field extract) and scaled into its word address with the column added (one shift-add).
-template <int W, int PACK = 1>
-__device__ __forceinline__ void add_row_bins(int32_t *lds, uint32_t dw, int32_t gv, const uint32_t (&xs)[4],
+// bit-field extract) and scaled into its word address with the column added (one shift-add). Q32: the LDS holds
+// separate 32-bit g and h counters (g words first, then 256 * W h words), and gv, hv are the row's g and h.
+template <int W, int PACK = 1, bool Q32 = false>
+__device__ __forceinline__ void add_row_bins(int32_t *lds, uint32_t dw, int32_t gv, int32_t hv, const uint32_t (&xs)[4],
                                              const uint32_t (&cols)[4]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         uint32_t b = __builtin_amdgcn_ubfe(dw, xs[k], 8u);
         if constexpr (PACK > 1) b &= 256u / PACK - 1u;  // a packed column's segment: invalid bins stay in it
         atomicAdd(&lds[b * W + cols[k]], gv);
+        if constexpr (Q32) atomicAdd(&lds[256 * W + b * W + cols[k]], hv);
     }
 }
 
 // A wide slab (two-byte bins of up to 1024, W / 4 features) keeps the byte slab's LDS and partial shape: bin b of
 // its column c is word (b >> 2) * W + (b & 3) * (W / 4) + c, i.e. a wide column is four virtual byte columns (bins
 // congruent to 0, 1, 2, 3 mod 4). A lane's dword holds the bins of columns 2d and 2d + 1.
-template <int W>
-__device__ __forceinline__ void add_row_bins_wide(int32_t *lds, uint32_t dw, int32_t gv, uint32_t d) {
+template <int W, bool Q32 = false>
+__device__ __forceinline__ void add_row_bins_wide(int32_t *lds, uint32_t dw, int32_t gv, int32_t hv, uint32_t d) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const uint32_t b = min((dw >> (16 * k)) & 0xffffu, 1023u);  // clamped: invalid bins stay inside the LDS
-        atomicAdd(&lds[(b >> 2) * W + (b & 3u) * (W / 4) + 2u * d + k], gv);
+        const uint32_t w = (b >> 2) * W + (b & 3u) * (W / 4) + 2u * d + k;
+        atomicAdd(&lds[w], gv);
+        if constexpr (Q32) atomicAdd(&lds[256 * W + w], hv);
+    }
+}
+
+// A row's quantized pair as the LDS adds take it: the packed word itself, or (Q32) its g and h apart.
+template <bool Q32>
+__device__ __forceinline__ void row_units(int32_t word, bool on, int32_t &gv, int32_t &hv) {
+    if constexpr (Q32) {
+        const int32_t g = packed_g(word);
+        gv = on ? g : 0;
+        hv = on ? packed_h(word, g) : 0;
+    } else {
+        gv = on ? word : 0;
+        hv = 0;
     }
 }
 
@@ -367,16 +384,17 @@ __device__ __forceinline__ void add_row_bins_wide(int32_t *lds, uint32_t dw, int
 // wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
 // step, and hands them out with a shuffle. WIDE: the slab's rows are W / 4 two-byte bins. PACK: the slab's rows
 // are W * PACK bytes, PACK features of at most 256 / PACK bins to an LDS column.
-template <int W, bool WIDE = false, int PACK = 1>
+template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false>
 __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
+    static_assert(!Q32 || W <= 64, "separate g and h counters take twice the LDS");
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;  // dwords per row
     constexpr int RPW = WAVE / DW;            // rows per wave step
     // row ids of one step fit one wave-wide load; at W = 128 the 64 accumulator registers leave room for 8
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr uint32_t STEP = 16u * RPW * UNROLL;          // rows per block step (16 waves)
     constexpr int SLOTS = 256 * W / 1024;
-    __shared__ int32_t lds[256 * W];
+    __shared__ int32_t lds[(Q32 ? 2 : 1) * 256 * W];
 
     uint32_t lb, n;
     leaf_rows(a.dev_left, a.begin, a.count, a.side, lb, n);
@@ -384,7 +402,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     hist_split(n, a.max_groups, a.min_rows_per_group, groups, per);
     if (blockIdx.x >= groups) return;
     const uint32_t tid = threadIdx.x;
-    for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
+    for (int j = 0; j < (Q32 ? 2 : 1) * SLOTS; ++j) lds[tid + j * 1024] = 0;
     int32_t accg[SLOTS], acch[SLOTS];
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
@@ -401,7 +419,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     uint32_t end = start + per < n ? start + per : n;
 
     for (uint32_t chunk = start; chunk < end; chunk += a.flush_rows) {
-        uint32_t cend = chunk + a.flush_rows < end ? chunk + a.flush_rows : end;
+        uint32_t cend = end - chunk > a.flush_rows ? chunk + a.flush_rows : end;
         uint32_t last = cend - 1;
         uint32_t base = chunk + wave * RPW * UNROLL;
         uint32_t cidx = rows[min(base + lane, last)];
@@ -419,9 +437,10 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
             }
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
-                const int32_t gv = base + u * RPW + rsub < cend ? g[u] : 0;
-                if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
-                else add_row_bins<W, PACK>(lds, dw[u], gv, xs, cols);
+                int32_t gv, hv;
+                row_units<Q32>(g[u], base + u * RPW + rsub < cend, gv, hv);
+                if constexpr (WIDE) add_row_bins_wide<W, Q32>(lds, dw[u], gv, hv, d);
+                else add_row_bins<W, PACK, Q32>(lds, dw[u], gv, hv, xs, cols);
             }
         }
         __syncthreads();
@@ -429,9 +448,15 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
         for (int j = 0; j < SLOTS; ++j) {
             int32_t v = lds[tid + j * 1024];
             lds[tid + j * 1024] = 0;
-            const int32_t gq = packed_g(v);
-            accg[j] += gq;
-            acch[j] += packed_h(v, gq);
+            if constexpr (Q32) {
+                accg[j] += v;
+                acch[j] += lds[256 * W + tid + j * 1024];
+                lds[256 * W + tid + j * 1024] = 0;
+            } else {
+                const int32_t gq = packed_g(v);
+                accg[j] += gq;
+                acch[j] += packed_h(v, gq);
+            }
         }
         __syncthreads();
     }
@@ -3057,10 +3082,10 @@ __device__ uint32_t lookback(const unsigned long long *status, uint32_t t, uint3
     return prefix;
 }
 
-// Moves the packed 16/16 LDS words into a workgroup's {g, h} pair partial (stored, or added to what an earlier
-// flush stored) and zeroes them. Slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W; bins past the
-// column's feature are not stored. Block-wide.
-template <int W>
+// Moves the packed 16/16 LDS words (Q32: the separate g and h counters) into a workgroup's {g, h} pair partial
+// (stored, or added to what an earlier flush stored) and zeroes them. Slot tid + 1024 j is bin (tid + 1024 j) / W
+// of column tid % W; bins past the column's feature are not stored. Block-wide.
+template <int W, bool Q32 = false>
 __device__ __forceinline__ void flush_pairs(int32_t *lds, int2 *pairs, uint32_t col_bins, bool add) {
     constexpr int SLOTS = 256 * W / 1024;
     const uint32_t tid = threadIdx.x;
@@ -3070,11 +3095,19 @@ __device__ __forceinline__ void flush_pairs(int32_t *lds, int2 *pairs, uint32_t 
         const uint32_t slot = tid + j * 1024;
         const int32_t v = lds[slot];
         lds[slot] = 0;
+        int32_t gq, hq;
+        if constexpr (Q32) {
+            gq = v;
+            hq = lds[256 * W + slot];
+            lds[256 * W + slot] = 0;
+        } else {
+            gq = packed_g(v);
+            hq = packed_h(v, gq);
+        }
         if (slot / W < col_bins) {
-            const int32_t gq = packed_g(v);
             int2 o = add ? pairs[slot] : make_int2(0, 0);
             o.x += gq;
-            o.y += packed_h(v, gq);
+            o.y += hq;
             pairs[slot] = o;
         }
     }
@@ -3221,7 +3254,7 @@ __device__ __forceinline__ void tile_scatter(const StepView &v, uint32_t t, cons
 // The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
 // lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free. NW
 // waves take part; `wave` is this one's index among them.
-template <int W, bool WIDE, int PACK, int UNROLL, int NW = 16>
+template <int W, bool WIDE, int PACK, bool Q32, int UNROLL, int NW = 16>
 __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
                                           const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6) {
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
@@ -3246,9 +3279,10 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            const int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
-            if constexpr (WIDE) add_row_bins_wide<W>(lds, dw[u], gv, d);
-            else add_row_bins<W, PACK>(lds, dw[u], gv, xs, cols);
+            int32_t gv, hv;
+            row_units<Q32>(gq[u], base + u * RPW + rsub < c1, gv, hv);
+            if constexpr (WIDE) add_row_bins_wide<W, Q32>(lds, dw[u], gv, hv, d);
+            else add_row_bins<W, PACK, Q32>(lds, dw[u], gv, hv, xs, cols);
         }
     }
 }
@@ -3294,15 +3328,16 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
     }
 }
 
-template <int W, bool WIDE = false, int PACK = 1>
+template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
+    static_assert(!Q32 || W <= 64, "separate g and h counters take twice the LDS");
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
     // rows per lane in multi-tile workgroups (16 at W = 32 with packed columns spills)
     constexpr int UNROLL = (W == 128 || (W == 32 && PACK > 1)) ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr int SLOTS = 256 * W / 1024;
-    __shared__ int32_t lds[256 * W];
+    __shared__ int32_t lds[(Q32 ? 2 : 1) * 256 * W];
     __shared__ StepShared sh;
 
     StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
@@ -3333,7 +3368,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (tid < 8) sh.left_bins[tid] = J.left_bins[tid];  // visible after the first barrier below
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     if (v.hist)
-        for (int j = 0; j < SLOTS; ++j) lds[tid + j * 1024] = 0;
+        for (int j = 0; j < (Q32 ? 2 : 1) * SLOTS; ++j) lds[tid + j * 1024] = 0;
 
     if (packed) {  // one tile; the partial is the LDS words themselves
         __syncthreads();
@@ -3349,13 +3384,19 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (v.hist) hist_list<W, WIDE, PACK, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (v.hist) hist_list<W, WIDE, PACK, Q32, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
         } else if (v.hist) {
-            hist_list<W, WIDE, PACK, 16>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, PACK, Q32, 16>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         __syncthreads();  // the offset and the histogram are complete
         if (v.partition) tile_scatter(v, t, st, sh);
         if (!v.hist) return;
+        if constexpr (Q32) {  // the counters as a {g, h} pair partial
+            int2 *pairs = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
+            flush_pairs<W, true>(lds, pairs, 256u, false);
+            if (tid == 0) a.fmt[blockIdx.x] = 0u;
+            return;
+        }
         store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
         if (tid == 0) a.fmt[blockIdx.x] = 1u;
         return;
@@ -3401,13 +3442,13 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
             uint32_t c0 = 0;
             while (c0 < nb) {
                 if (pending >= a.flush_rows) {
-                    flush_pairs<W>(lds, pairs, col_bins, flushed);
+                    flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
                     pending = 0;
                     flushed = true;
                 }
                 uint32_t room = a.flush_rows - pending;
                 uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                hist_list<W, WIDE, PACK, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+                hist_list<W, WIDE, PACK, Q32, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
                 pending += c1 - c0;
                 c0 = c1;
             }
@@ -3415,11 +3456,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (!hist_done) hist_list<W, WIDE, PACK, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (!hist_done) hist_list<W, WIDE, PACK, Q32, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
             __syncthreads();  // the offset is in sh.prefix
             tile_scatter(v, t, st, sh);
         } else if (!hist_done) {
-            hist_list<W, WIDE, PACK, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
+            hist_list<W, WIDE, PACK, Q32, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
         }
         if (!hist_done) pending += nb;
         if (tn < v.ntiles) tile_bins(v, r);
@@ -3430,13 +3471,13 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         tn = sh.tile;
     }
     if (!v.hist) return;
-    if (!flushed) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
+    if (!flushed && !Q32) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
         __syncthreads();
         store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
         if (tid == 0) a.fmt[blockIdx.x] = 1u;
         return;
     }
-    flush_pairs<W>(lds, pairs, col_bins, true);
+    flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
     if (tid == 0) a.fmt[blockIdx.x] = 0u;
 }
 

@@ -623,22 +623,26 @@ def test_validation_scores_match_the_oracle(objective, renew):
         t.backend.close()
 
 
-def test_quantized_units_beyond_the_workgroup_sums_are_rejected(rocm):
-    # a workgroup's histogram sums are i32: units whose largest value times the rows one workgroup adds could pass
-    # 2^31 are refused before any kernel runs (the reference's CPU sums are i64 and take them)
-    # at 400k rows a workgroup adds at most 4096 rows, so even the widest units fit; at 8M rows it adds over 32768
+def test_the_widest_units_spread_the_workgroups_and_wider_ones_are_rejected(rocm):
+    # a workgroup's histogram sums are i32, so for units of up to 65535 the histogram and split-step workgroups are
+    # spread until none adds up more than (2^31 - 1) / 65535 rows (at 8M rows, one a compute unit would add 31k);
+    # units past the packed word's halves are refused before any kernel runs
     wide = oracle.quant_spec(1.0, 1.0, None, 4, True, 1, 0)
     wide.grad_max_q, wide.hess_max_q = 32767, 65535
-    for rows, fits in ((400_000, True), (8_000_000, False)):
-        say("quantize bound", rows)
+    for rows in (400_000, 8_000_000):
+        say("widest units", rows)
         data = silvic_amd.synthetic(2, rows=rows, cols=4, seed=3)
         g, h = binary_gradients(data)
         rocm.load(data)
         rocm.set_gradients(g, h)
-        if fits:
-            rocm.quantize(wide)
-            continue
+        rocm.quantize(wide)
+        packed = oracle.quantize(wide, g, h)
+        assert rocm.reset_partition() == rows
+        assert np.array_equal(rocm.histogram((0, rows)), oracle.histogram(data, packed, 65535, np.arange(rows, dtype=np.uint32)))
+    for gq, hq in ((32768, 4), (2, 65536), (0, 4)):
+        bad = oracle.quant_spec(1.0, 1.0, None, 4, True, 1, 0)
+        bad.grad_max_q, bad.hess_max_q = gq, hq
         with pytest.raises(_abi.SilvicError) as e:
-            rocm.quantize(wide)
-        assert e.value.kind == "unsupported" and "32-bit sums" in str(e.value)
-        rocm.quantize(oracle.quant_spec(1.0, 1.0, None, 64, True, 1, 0))  # the reference's largest setting passes
+            rocm.quantize(bad)
+        assert e.value.kind == "unsupported" and "must lie in" in str(e.value)
+    rocm.quantize(oracle.quant_spec(1.0, 1.0, None, 64, True, 1, 0))  # the reference's largest setting passes

@@ -178,3 +178,44 @@ def test_the_lightgbm_ranges_reject_a_wrong_mixer():
         cols = _fixture_columns(mix, fx["rows"])
         lo, hi = fx["feature_infos"]["normal"].strip("[]").split(":")
         assert _lightgbm_range(cols["normal"]) != (float(lo), float(hi))
+
+
+# 16-bit units (num_grad_quant_bins up to 32766) are an extension of the reference, which takes 2..=64
+# (config.rs:416-421): pinned by closed forms only. The units stay within their bounds, the packed word round trips
+# them, and the oracle's histogram (64-bit packed blocks of INT32_MAX / max_q rows, cpu.rs:479-525) equals direct
+# sums of the unpacked units.
+def test_sixteen_bit_units_round_trip_and_sum_exactly():
+    import silvic_amd
+    from tests.helpers import naive_histogram
+
+    data = silvic_amd.synthetic(2, rows=20_000, cols=24, seed=9)
+    rng = np.random.default_rng(4)
+    g = rng.standard_normal(data.num_rows).astype(np.float32)
+    h = rng.uniform(0.05, 1.0, data.num_rows).astype(np.float32)
+    for bins in (256, 4096, 32766):
+        spec = oracle.quant_spec(float(np.abs(g).max()), float(h.max()), None, bins, True, 3, 1)
+        assert spec.grad_max_q == bins // 2 and spec.hess_max_q == bins
+        packed = oracle.quantize(spec, g, h)
+        gq, hq = oracle.unpack(packed)
+        assert gq.min() >= -bins // 2 and gq.max() <= bins // 2 and hq.min() >= 0 and hq.max() <= bins
+        assert np.array_equal(packed, (hq.astype(np.int64) * 65536 + gq).astype(np.int32))
+        assert np.abs(gq).max() > bins // 4  # the range is used
+        # stochastic rounding brackets the scaled value
+        sg = g.astype(np.float64) / spec.grad_scale
+        assert (np.abs(gq - sg) < 1.0 + 1e-3).all()
+        rows = np.sort(rng.choice(data.num_rows, 7_000, replace=False)).astype(np.uint32)
+        got = oracle.histogram(data, packed, max(bins // 2, bins), rows)
+        assert np.array_equal(got, naive_histogram(data, rows, gq[rows], hq[rows])), bins
+
+
+def test_the_rocm_trainer_takes_sixteen_bit_units():
+    from silvic_amd import _abi, engine
+
+    for bins in (2, 64, 256, 32766):
+        assert engine.resolve_params({"num_grad_quant_bins": bins})["num_grad_quant_bins"] == bins
+    for bins in (0, 7, 32768):
+        try:
+            engine.resolve_params({"num_grad_quant_bins": bins})
+        except _abi.SilvicError:
+            continue
+        raise AssertionError(bins)

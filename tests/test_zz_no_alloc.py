@@ -58,3 +58,38 @@ def test_noalloc_histogram_matches_the_allocating_one():
     finally:
         rocm.close()
         hip.hipFree(dbuf)
+
+
+def test_noalloc_refuses_units_its_scratch_cannot_spread():
+    # with the widest units a workgroup may add at most (2^31 - 1) / 65535 rows; the allocating entry point spreads a
+    # 10M-row leaf over enough workgroups, the scratch holds too few of them, so the no-allocation one refuses it
+    print("[case] noalloc widest units 10000000 x 4", flush=True)
+    data = silvic_amd.synthetic(2, rows=10_000_000, cols=4, seed=5)
+    rng = np.random.default_rng(1)
+    scores = (rng.standard_normal(data.num_rows) * 0.5).astype(np.float32)
+    g, h, _, _ = oracle.gradients(_abi.OBJ_BINARY, scores, data.label)
+    rocm = silvic_amd.RocmBackend(0)
+    hip = _hip()
+    dbuf = C.c_void_p()
+    n = 2 * data.total_bins
+    assert hip.hipMalloc(C.byref(dbuf), n * 8) == 0
+    try:
+        rocm.load(data)
+        rocm.set_gradients(g, h)
+        wide = oracle.quant_spec(1.0, 1.0, None, 4, True, 1, 0)
+        wide.grad_max_q, wide.hess_max_q = 32767, 65535
+        rocm.quantize(wide)
+        rows = rocm.reset_partition()
+        want = rocm.histogram((0, rows))
+        assert np.array_equal(want, oracle.histogram(data, oracle.quantize(wide, g, h), 65535,
+                                                     np.arange(rows, dtype=np.uint32)))
+        with pytest.raises(_abi.SilvicError) as e:
+            _noalloc(rocm, hip, dbuf, (0, rows), n)
+        assert e.value.kind == "unsupported" and "scratch's limit" in str(e.value)
+        # a leaf the scratch's workgroups can take still matches
+        print("[case] noalloc widest units, 2M-row leaf", flush=True)
+        assert np.array_equal(_noalloc(rocm, hip, dbuf, (0, 2_000_000), n).astype(np.float64),
+                              rocm.histogram((0, 2_000_000)))
+    finally:
+        rocm.close()
+        hip.hipFree(dbuf)
