@@ -2278,20 +2278,40 @@ __global__ void k_grow_init(GrowState g, uint32_t root_begin, uint32_t root_coun
 }
 
 // learner.rs:143-156: the root's sums from the sums feature's bins (split.rs:101-108), and its search job.
-__global__ void k_root_prep(GrowState g) {
+// The root's sums are those of one feature's bins taken in bin order as f64. Every bin and every partial sum is an
+// integer of magnitude below 2^53 (rows times units stays below 2^48), so each of those additions is exact and the
+// result is the exact integer sum, which the block adds in i64 and converts once. grid: 1, 256 threads.
+__global__ __launch_bounds__(256) void k_root_prep(GrowState g) {
+    __shared__ int64_t part[2][4];
     const TLeaf &l = g.tl[0];
     const int64_t *h = g.pool + (size_t)l.slot * g.slot_stride;
     for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) g.evaluate[f] = g.mask[f];
+    const FeatDev m = g.feats[g.sums_feature];
+    int64_t sg = 0, sh = 0;
+    for (uint32_t b = threadIdx.x; b < m.num_bins; b += blockDim.x) {
+        sg += h[2 * ((size_t)m.hist_offset + b)];
+        sh += h[2 * ((size_t)m.hist_offset + b) + 1];
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        sg += static_cast<int64_t>(__shfl_xor(static_cast<long long>(sg), o));
+        sh += static_cast<int64_t>(__shfl_xor(static_cast<long long>(sh), o));
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0) {
+        part[0][wave] = sg;
+        part[1][wave] = sh;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        FeatDev m = g.feats[g.sums_feature];
-        double sg = 0.0, sh = 0.0;
-        for (uint32_t b = 0; b < m.num_bins; ++b) {
-            sg = sg + static_cast<double>(h[2 * ((size_t)m.hist_offset + b)]);
-            sh = sh + static_cast<double>(h[2 * ((size_t)m.hist_offset + b) + 1]);
+        int64_t tg = 0, th = 0;
+        for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
+            tg += part[0][w];
+            th += part[1][w];
         }
-        g.tl[0].ug = sg;
-        g.tl[0].uh = sh;
-        g.jobs[0] = ScanJob{h, sg, sh, l.cnt, g.cands};
+        const double dg = static_cast<double>(tg), dh = static_cast<double>(th);
+        g.tl[0].ug = dg;
+        g.tl[0].uh = dh;
+        g.jobs[0] = ScanJob{h, dg, dh, l.cnt, g.cands};
     }
 }
 
