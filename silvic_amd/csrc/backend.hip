@@ -271,7 +271,8 @@ struct Slab {
     uint32_t pack = 1;             // byte bins, `pack` features of at most 256 / pack bins a column (k_hist<W, false, pack>)
     bool q32 = false;              // separate 32-bit g and h LDS counters (k_hist<W, wide, 1, true>)
     std::vector<uint32_t> feats;   // feature ids
-    DevBuf<uint8_t> bins;          // [rows][row_bytes()]
+    uint64_t bins_off = 0;         // its rows in Context::slab_bins: [rows][row_bytes()]
+    uint64_t col_bins_off = 0;     // its col_bins in Context::slab_col_bins (slots() entries)
     DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per feature slot: segment * W + column (virtual column)
     uint32_t row_bytes() const { return wide ? width / 2 : width * pack; }
     uint32_t capacity() const { return wide ? width / 4 : width * pack; }
@@ -344,6 +345,10 @@ struct Context {
     uint64_t rows = 0, row_offset = 0;
     uint32_t max_width = 32;
     bool q32 = false;  // slabs laid out for separate 32-bit g and h LDS counters (set_mode)
+    // every slab's rows in one buffer, each slab's at a multiple of 256 bytes, slabs of one row length
+    // slab_stride() apart, so that a k_step_rows launch finds its later slabs by arithmetic
+    DevBuf<uint8_t> slab_bins;
+    DevBuf<uint32_t> slab_col_bins;  // every slab's col_bins, consecutive
     uint32_t hist_cap = 0;     // k_hist workgroups a leaf is spread over at most
     uint32_t step_target = 0;  // k_step_rows workgroups a step is spread over (its grid: step_target + JMAX)
     uint32_t col16 = 0;                     // some group has two-byte bins: column-major bins are u16
@@ -742,6 +747,7 @@ struct Context {
     // features (in groups of CG_COLS) of k_step_scan, the categorical ones of k_step_cat, and the partial buffers.
     void build_slab_tables() {
         partial.alloc(static_cast<size_t>(hist_cap) * 256 * max_width * 2);
+        std::vector<uint32_t> all_bins;  // slab_col_bins
         for (auto &s : slabs) {
             // slot i: a byte feature's (column i % W, segment i / W); in a wide slab, virtual column i, bins
             // congruent to i / (W/4) mod 4 of feature i % (W/4)
@@ -767,7 +773,12 @@ struct Context {
             hip_check(hipMemcpy(s.col_stride.p, st.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_offset.p, off.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
             hip_check(hipMemcpy(s.col_bins.p, nb.data(), ns * 4, hipMemcpyHostToDevice), "upload slab");
+            s.col_bins_off = all_bins.size();
+            all_bins.insert(all_bins.end(), nb.begin(), nb.end());
         }
+        slab_col_bins.alloc(std::max<size_t>(all_bins.size(), 1));
+        if (!all_bins.empty())
+            hip_check(hipMemcpy(slab_col_bins.p, all_bins.data(), all_bins.size() * 4, hipMemcpyHostToDevice), "upload slab");
         // groups of CG_COLS slab columns for k_step_reduce, the numerical features in groups of CG_COLS for
         // k_step_scan, and the categorical ones for k_step_cat
         {
@@ -850,14 +861,11 @@ struct Context {
             return;
         }
         build_slabs();
-        for (auto &sl : slabs) {
-            sl.bins.alloc(std::max<uint64_t>(1, rows * sl.row_bytes()));
-            hip_check(hipMemsetAsync(sl.bins.p, 0, std::max<uint64_t>(1, rows * sl.row_bytes()), stream), "zero slab");
-        }
+        alloc_slab_bins(rows);
         const uint64_t cb = col16 ? 2 : 1;
         for (uint32_t nt = 0; rows && nt < nt_feat.size(); ++nt) {
             const Slab &sl = slabs[nt_slab[nt]];
-            RepackTo to{nullptr, col16, sl.bins.p, sl.row_bytes(), sl.wide ? 1u : 0u, nt_slab_col[nt]};
+            RepackTo to{nullptr, col16, slab_bins.p + sl.bins_off, sl.row_bytes(), sl.wide ? 1u : 0u, nt_slab_col[nt]};
             repack(train.col.p + static_cast<size_t>(nt) * rows * cb, static_cast<uint32_t>(cb), 0, col16 ? 16u : 8u, rows, to);
         }
         build_slab_tables();
@@ -871,6 +879,20 @@ struct Context {
         return static_cast<uint32_t>(std::min(32767 / std::max<int64_t>(gq, 1), 65535 / std::max<int64_t>(hq, 1)));
     }
 
+    // bytes from one slab's rows to the next slab's of the same row length
+    uint64_t slab_stride(const Slab &sl) const { return (std::max<uint64_t>(rows, 1) * sl.row_bytes() + 255) & ~uint64_t(255); }
+
+    // slab_bins for `n` rows (zeroed: padding bytes are bin 0), each slab at its offset
+    void alloc_slab_bins(uint64_t n) {
+        uint64_t total = 0;
+        for (auto &sl : slabs) {
+            sl.bins_off = total;
+            total += (std::max<uint64_t>(n, 1) * sl.row_bytes() + 255) & ~uint64_t(255);
+        }
+        slab_bins.alloc(std::max<uint64_t>(total, 1));
+        hip_check(hipMemsetAsync(slab_bins.p, 0, std::max<uint64_t>(total, 1), stream), "zero slabs");
+    }
+
     // Repacks a dataset's groups into slab rows (training set) and column-major bins, on the device.
     void upload_bins(const srocm_dataset *d, DevData &out, bool with_slabs) {
         out.rows = d->num_rows;
@@ -879,11 +901,7 @@ struct Context {
         out.col.alloc(std::max<uint64_t>(1, nt_feat.size() * n * cb));
         out.scores.alloc(std::max<uint64_t>(n, 1));
         hip_check(hipMemsetAsync(out.scores.p, 0, std::max<uint64_t>(n, 1) * sizeof(float), stream), "zero scores");
-        if (with_slabs)
-            for (auto &s : slabs) {
-                s.bins.alloc(std::max<uint64_t>(1, n * s.row_bytes()));
-                hip_check(hipMemsetAsync(s.bins.p, 0, std::max<uint64_t>(1, n * s.row_bytes()), stream), "zero slab");
-            }
+        if (with_slabs) alloc_slab_bins(n);
         if (n == 0) return;
         DevBuf<uint8_t> staging;
         for (uint32_t g = 0; g < d->num_groups; ++g) {
@@ -897,7 +915,7 @@ struct Context {
                 RepackTo to{out.col.p + static_cast<size_t>(nt) * n * cb, col16, nullptr, 0, 0, 0};
                 if (with_slabs) {
                     const Slab &sl = slabs[nt_slab[nt]];
-                    to.slab = sl.bins.p;
+                    to.slab = slab_bins.p + sl.bins_off;
                     to.row_bytes = sl.row_bytes();
                     to.slab_wide = sl.wide ? 1u : 0u;
                     to.slab_col = nt_slab_col[nt];
@@ -1035,7 +1053,7 @@ struct Context {
     void launch_hist_into(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
                           int64_t *parent, uint64_t bins_used, int32_t *partials, uint32_t grid, bool profiled) {
         for (auto &s : slabs) {
-            HistArgs a{s.bins.p, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
+            HistArgs a{slab_bins.p + s.bins_off, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (profiled) {
                 e0 = event();
@@ -1782,34 +1800,44 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     e1 = event();
                     hip_check(hipEventRecord(e0, stream), "event");
                 }
-                for (size_t si = 0; si < slabs.size(); ++si) {
+                // the first slab's launch partitions; the others histogram the built children, consecutive slabs
+                // of one kernel in one launch (k1 workgroups a slab)
+                uint32_t launches = 0;
+                for (size_t si = 0; si < slabs.size();) {
+                    size_t sj = si + 1;
+                    if (si > 0)
+                        while (sj < slabs.size() && slabs[sj].kernel() == slabs[si].kernel()) ++sj;
                     const Slab &sl = slabs[si];
-                    StepArgs sa{sl.bins.p, packed.p, train.col.p, col16, rows, part.p, part2.p, step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
-                                sl.col_bins.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
-                    switch (sl.kernel()) {
-                    case 32: k_step_rows<32><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 64: k_step_rows<64><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 128: k_step_rows<128><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 33: k_step_rows<32, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 65: k_step_rows<64, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 129: k_step_rows<128, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 36: k_step_rows<32, false, 4><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 68: k_step_rows<64, false, 4><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 34: k_step_rows<32, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 66: k_step_rows<64, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 130: k_step_rows<128, false, 2><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 1032: k_step_rows<32, false, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 1064: k_step_rows<64, false, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 1033: k_step_rows<32, true, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
-                    case 1065: k_step_rows<64, true, 1, true><<<k1_groups(), 1024, 0, stream>>>(sa); break;
+                    StepArgs sa{slab_bins.p + sl.bins_off, slab_stride(sl), step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
+                                slab_col_bins.p + sl.col_bins_off, k1_groups(), packed.p, train.col.p, col16, rows, part.p, part2.p,
+                                tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
+                    const uint32_t grid = k1_groups() * static_cast<uint32_t>(sj - si);
+                    switch (slabs[si].kernel()) {
+                    case 32: k_step_rows<32><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 64: k_step_rows<64><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 128: k_step_rows<128><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 33: k_step_rows<32, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 65: k_step_rows<64, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 129: k_step_rows<128, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 36: k_step_rows<32, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 68: k_step_rows<64, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 34: k_step_rows<32, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 66: k_step_rows<64, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 130: k_step_rows<128, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 1032: k_step_rows<32, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 1064: k_step_rows<64, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 1033: k_step_rows<32, true, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 1065: k_step_rows<64, true, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
                     default: throw std::logic_error("no split-step kernel for the slab");
                     }
                     launch_check("k_step_rows");
+                    ++launches;
+                    si = sj;
                 }
                 if (prof.on) {
                     hip_check(hipEventRecord(e1, stream), "event");
                     prof.step_events.emplace_back(e0, e1);
-                    prof.step_launches += static_cast<double>(slabs.size());
+                    prof.step_launches += static_cast<double>(launches);
                 }
                 ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);

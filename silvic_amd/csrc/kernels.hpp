@@ -3044,21 +3044,26 @@ __global__ __launch_bounds__(512) void k_root_select(GrowState g) {
 // resets; no block ever waits for another.
 // ---------------------------------------------------------------------------------------------------------
 
+// A launch takes one slab, or (histogram only) several slabs of one kernel, k1 workgroups each: slab s of the
+// launch is the first one's buffers moved by s strides (its rows by bins_stride bytes, its partials by k1
+// partials, its formats by k1 entries, its column bins by W * PACK entries).
 struct StepArgs {
-    const uint8_t *bins;         // slab rows: row r at bins + r * W
+    const uint8_t *bins;         // the first slab's rows: row r at bins + r * row bytes
+    uint64_t bins_stride;
+    int32_t *partial;            // its partials, step_partial_stride(W) pairs apart, one per workgroup
+    uint32_t *fmt;               // per workgroup: its partial is packed (1) or {g, h} pairs (0)
+    const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
+    uint32_t k1;                 // workgroups a slab
     const int32_t *gh;           // packed quantized gradients per row
     const uint8_t *colbase;      // column-major bins [feature][rows]
     uint32_t col16;              // two bytes per column-major bin
     uint64_t rows;
     uint32_t *buf0, *buf1;       // the partition buffers
-    int32_t *partial;            // this slab's partials, step_partial_stride(W) pairs apart, one per workgroup
-    uint32_t *fmt;               // per workgroup of this slab: its partial is packed (1) or {g, h} pairs (0)
-    const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
     unsigned long long *status;  // per-tile status words
     StepPlan *plan;              // this step's plan
     GrowCtl *ctl;
     uint32_t flush_rows;
-    uint32_t partition;          // 1: this launch partitions (the first slab's); 0: histogram only
+    uint32_t partition;          // 1: this launch partitions (the first slab's alone); 0: histogram only
 };
 
 __device__ __forceinline__ unsigned long long status_word(uint32_t epoch, uint32_t flag, uint32_t value) {
@@ -3360,9 +3365,18 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     __shared__ int32_t lds[(Q32 ? 2 : 1) * 256 * W];
     __shared__ StepShared sh;
 
+    // a launch of histogram-only slabs takes k1 workgroups a slab: wg is the workgroup within its slab
+    const uint32_t sl = blockIdx.x / a.k1, wg = blockIdx.x - sl * a.k1;
+    struct {
+        const uint8_t *bins;
+        int32_t *partial;
+        uint32_t *fmt;
+        const uint32_t *col_bins;
+    } R = {a.bins + sl * a.bins_stride, a.partial + static_cast<size_t>(sl) * a.k1 * 2 * step_partial_stride(W),
+           a.fmt + sl * a.k1, a.col_bins + sl * (W * PACK)};
     StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
-    if (blockIdx.x >= P.total_groups) return;
-    const uint32_t j = job_of(P.group_base, P.njobs, blockIdx.x);
+    if (wg >= P.total_groups) return;
+    const uint32_t j = job_of(P.group_base, P.njobs, wg);
     JobPlan &J = P.jobs[j];
     StepView v;
     v.job = &J;
@@ -3374,7 +3388,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     v.count = J.count;
     v.ntiles = J.ntiles;
     v.groups = J.groups;
-    const uint32_t gi = blockIdx.x - J.group_base;  // the workgroup within its job
+    const uint32_t gi = wg - J.group_base;  // the workgroup within its job
     const bool packed = J.packed != 0;  // then one tile per workgroup
     v.src = J.src_buf ? a.buf1 : a.buf0;
     v.dst = J.src_buf ? a.buf0 : a.buf1;
@@ -3386,7 +3400,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     v.epoch = P.epoch;
     const uint32_t tid = threadIdx.x;
     if (tid < 8) sh.left_bins[tid] = J.left_bins[tid];  // visible after the first barrier below
-    const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
+    const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(R.bins);
     if (v.hist)
         for (int j = 0; j < (Q32 ? 2 : 1) * SLOTS; ++j) lds[tid + j * 1024] = 0;
 
@@ -3412,21 +3426,21 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         if (v.partition) tile_scatter(v, t, st, sh);
         if (!v.hist) return;
         if constexpr (Q32) {  // the counters as a {g, h} pair partial
-            int2 *pairs = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
+            int2 *pairs = reinterpret_cast<int2 *>(R.partial) + static_cast<size_t>(wg) * step_partial_stride(W);
             flush_pairs<W, true>(lds, pairs, 256u, false);
-            if (tid == 0) a.fmt[blockIdx.x] = 0u;
+            if (tid == 0) R.fmt[wg] = 0u;
             return;
         }
-        store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
-        if (tid == 0) a.fmt[blockIdx.x] = 1u;
+        store_packed_partial<W>(lds, R.partial + 2 * static_cast<size_t>(wg) * step_partial_stride(W));
+        if (tid == 0) R.fmt[wg] = 1u;
         return;
     }
 
     // several tiles per workgroup: whenever flush_rows rows have gone into the packed words they are added into the
     // partial as {g, h} pairs; a workgroup that never flushes stores its partial packed instead
-    int2 *pairs = reinterpret_cast<int2 *>(a.partial) + static_cast<size_t>(blockIdx.x) * step_partial_stride(W);
+    int2 *pairs = reinterpret_cast<int2 *>(R.partial) + static_cast<size_t>(wg) * step_partial_stride(W);
     // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W; a packed column's features are all stored
-    const uint32_t col_bins = PACK > 1 ? 256u : a.col_bins[tid % W];
+    const uint32_t col_bins = PACK > 1 ? 256u : R.col_bins[tid % W];
     uint32_t pending = 0;  // rows added to the packed LDS words since they were last flushed
     bool flushed = false;
     // partition launches take tiles in ticket order, the next ticket drawn while the current tile is worked on (a
@@ -3493,12 +3507,12 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (!v.hist) return;
     if (!flushed && !Q32) {  // every row still in the packed words: the partial is packed, as a one-tile workgroup's
         __syncthreads();
-        store_packed_partial<W>(lds, a.partial + 2 * static_cast<size_t>(blockIdx.x) * step_partial_stride(W));
-        if (tid == 0) a.fmt[blockIdx.x] = 1u;
+        store_packed_partial<W>(lds, R.partial + 2 * static_cast<size_t>(wg) * step_partial_stride(W));
+        if (tid == 0) R.fmt[wg] = 1u;
         return;
     }
     flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
-    if (tid == 0) a.fmt[blockIdx.x] = 0u;
+    if (tid == 0) R.fmt[wg] = 0u;
 }
 
 // Four columns of one slab: a work unit of k_step_reduce and k_step_scan.
