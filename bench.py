@@ -82,38 +82,14 @@ def timed_window(rows, warmup, steps):
     return rows[begin(warmup):begin(warmup + steps)]
 
 
-def step_kernels(data, quant_bins=4):
-    """The k_step_rows instances the backend launches for `data`, with their slab counts. Byte features in the order
-    of their bin classes (more than 128 bins, more than 64, the rest), 128 to a slab while it holds one of more than
-    128 bins, else 256; a slab's rows the fewest bytes (32..256) that hold its features, and as many features to an
-    LDS column as that row length and its largest bin count allow (four of at most 64 bins, two of at most 128).
-    Two-byte features 32 to a slab. With units the packed 16/16 LDS words would flush every fewer than 256 rows,
-    separate 32-bit g and h counters: 64 byte or 16 two-byte features a slab, one a column."""
-    bits = [g.bin_bits or 8 for g in data.groups]
-    q32 = min(32767 // max(quant_bins // 2, 1), 65535 // max(quant_bins, 1)) < 256
-
-    def cls(b):
-        return 4 if b <= 64 else (2 if b <= 128 else 1)
-
-    nb = sorted((cls(f.num_bins) for f in data.features if f.num_bins > 0 and bits[f.group] != 16))
-    wide = sum(1 for f in data.features if f.num_bins > 0 and bits[f.group] == 16)
+def step_kernels(layout):
+    """The k_step_rows instances the backend launches for a slab layout (RocmBackend.slab_layout()), with their
+    slab counts."""
     out = {}
-    b = 0
-    while b < len(nb):
-        e = min(len(nb), b + (64 if q32 else (128 if nb[b] == 1 else 256)))
-        n, max_pack = e - b, 1 if q32 else min(nb[b:e])
-        row = 32
-        while row < n:
-            row *= 2
-        pack = next((p for p in (4, 2) if p <= max_pack and 32 * p <= row and row // p <= 128), 1)
-        k = f"k_step_rows<{row // pack}>" if pack == 1 else f"k_step_rows<{row // pack}, false, {pack}>"
-        if q32:
-            k = f"k_step_rows<{row}, false, 1, true>"
-        out[k] = out.get(k, 0) + 1
-        b = e
-    for i in range(0, wide, 16 if q32 else 32):
-        cols = 4 * min(16 if q32 else 32, wide - i)
-        k = f"k_step_rows<{32 if cols <= 32 else (64 if cols <= 64 else 128)}, true{', 1, true' if q32 else ''}>"
+    for sl in layout:
+        dp = (4 if sl["row_bytes"] <= 1024 else 8) if sl["dense"] else 0
+        k = (f"k_step_rows<{sl['width']}, {'true' if sl['wide'] else 'false'}, {max(sl['pack'], 1)}, "
+             f"{'true' if sl['q32'] else 'false'}, {dp}>")
         out[k] = out.get(k, 0) + 1
     return ", ".join(f"{k} x{n}" for k, n in out.items())
 
@@ -331,10 +307,13 @@ def main():
     t0 = time.perf_counter()
     trainer = silvic_amd.Trainer(params, data)
     log(f"loaded on {trainer.backend.name()} in {time.perf_counter() - t0:.1f}s")
+
     lib, h = trainer.backend._lib, trainer.backend._h
 
     warm = trainer.step(args.warmup)
     log(f"warmup {len(warm)} iterations done")
+    layout = trainer.backend.slab_layout()  # as the boosting loop left it (the quantization picks the counters)
+    log(f"slabs: {step_kernels(layout)}")
     # The timed iterations run without the per-kernel events (each event is a marker in the stream that idles the
     # GPU for a few microseconds). Training is deterministic, so a second trainer repeats the same warm-up and the
     # same iterations with the events on: the kernel times and work counts are those of the timed trees.
@@ -420,7 +399,7 @@ def main():
                "trees_identical": f"{same}/{compared}", "seconds": cpu_elapsed}
 
     describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves, bins=args.quant_bins)
-    slab = step_kernels(data, args.quant_bins)
+    slab = step_kernels(layout)
     out = {
         "metric": METRIC if args.workload == "binary" and args.quant_bins == 4 else
                   f"boosting iters/s, {args.workload} workload at num_grad_quant_bins={args.quant_bins}; % HBM peak",

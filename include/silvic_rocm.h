@@ -397,6 +397,12 @@ int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size
 int srocm_profile(void *ctx, int enable);
 int srocm_profile_read(void *ctx, double *out, uint32_t len);
 
+/* The loaded training set's slab layout (no counterpart in the reference: the layout is this backend's), for
+ * measurement and inspection. Writes 4 values per slab, for up to `cap` slabs: LDS columns, row bytes, features a
+ * column (0: stacked by bin count), flags (1: two-byte bins, 2: separate 32-bit g and h counters, 4: stacked), and
+ * the slab count into *count. */
+int srocm_slab_layout(void *ctx, uint32_t *out, uint32_t cap, uint32_t *count);
+
 #ifdef __cplusplus
 }
 #endif

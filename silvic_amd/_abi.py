@@ -172,6 +172,7 @@ _SIGNATURES = {
                               C.POINTER(C.c_uint32)]),
     "srocm_profile": (C.c_int, [_P, C.c_int]),
     "srocm_profile_read": (C.c_int, [_P, C.POINTER(C.c_double), C.c_uint32]),
+    "srocm_slab_layout": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_uint32, C.POINTER(C.c_uint32)]),
 }
 
 EXPORTS = tuple(_SIGNATURES)

@@ -72,6 +72,17 @@ class RocmBackend:
         self._check(self._lib.srocm_name(self._h, buf, 256))
         return buf.value.decode()
 
+    def slab_layout(self):
+        """The loaded training set's slabs (``srocm_slab_layout``): per slab its LDS columns, row bytes, features a
+        column (0: stacked by bin count) and whether it holds two-byte bins, separate 32-bit g/h counters or stacked
+        features."""
+        n = C.c_uint32()
+        self._check(self._lib.srocm_slab_layout(self._h, None, 0, C.byref(n)))
+        out = (C.c_uint32 * (4 * max(n.value, 1)))()
+        self._check(self._lib.srocm_slab_layout(self._h, out, n.value, C.byref(n)))
+        return [dict(width=out[4 * i], row_bytes=out[4 * i + 1], pack=out[4 * i + 2], wide=bool(out[4 * i + 3] & 1),
+                     q32=bool(out[4 * i + 3] & 2), dense=bool(out[4 * i + 3] & 4)) for i in range(n.value)]
+
     def load(self, train, valid=(), objective=_abi.OBJ_REGRESSION, sigmoid=1.0, norm=True, truncation_level=30,
              label_gain=None, inverse_max_dcg=None):
         """``Backend::load`` (mod.rs:125-126). Lambdarank takes ``ObjectiveSetup::LambdaRank``'s fields

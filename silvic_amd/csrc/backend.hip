@@ -270,15 +270,22 @@ struct Slab {
     bool wide = false;             // two-byte bins: W / 4 features, each 4 virtual columns (k_hist<W, true>)
     uint32_t pack = 1;             // byte bins, `pack` features of at most 256 / pack bins a column (k_hist<W, false, pack>)
     bool q32 = false;              // separate 32-bit g and h LDS counters (k_hist<W, wide, 1, true>)
+    uint32_t dense_passes = 0;     // a dense slab (k_hist<128, false, 1, false, DP>): features stacked by bin count
+    uint32_t dense_row = 0;        // its row bytes (128 per feature a column)
+    std::vector<uint32_t> pos_word, slot_flat;  // its tables (host): per row byte its LDS word, per slot its flat bin + 1
+    uint64_t pos_off = 0, slot_off = 0;         // and their places in Context::slab_pos_word / slab_slot_flat
     std::vector<uint32_t> feats;   // feature ids
     uint64_t bins_off = 0;         // its rows in Context::slab_bins: [rows][row_bytes()]
     uint64_t col_bins_off = 0;     // its col_bins in Context::slab_col_bins (slots() entries)
     DevBuf<uint32_t> col_offset, col_bins, col_stride;  // per feature slot: segment * W + column (virtual column)
-    uint32_t row_bytes() const { return wide ? width / 2 : width * pack; }
-    uint32_t capacity() const { return wide ? width / 4 : width * pack; }
+    uint32_t row_bytes() const { return dense_passes ? dense_row : (wide ? width / 2 : width * pack); }
+    uint32_t capacity() const { return dense_passes ? dense_row : (wide ? width / 4 : width * pack); }
     uint32_t seg_shift() const { return pack == 4 ? 6u : (pack == 2 ? 7u : 8u); }
     uint32_t slots() const { return width * pack; }  // entries of the per-slot arrays
-    uint32_t kernel() const { return width + (wide ? 1u : 0u) + (pack > 1 ? pack : 0u) + (q32 ? 1000u : 0u); }  // launch key
+    uint32_t kernel() const {  // launch key
+        return dense_passes ? 3000u + dense_passes : width + (wide ? 1u : 0u) + (pack > 1 ? pack : 0u) + (q32 ? 1000u : 0u);
+    }
+    bool same_launch(const Slab &o) const { return kernel() == o.kernel() && row_bytes() == o.row_bytes(); }
     uint64_t step_partial_off = 0;  // the slab's partials in the step partial buffer, in {g, h} pairs
 };
 
@@ -289,7 +296,9 @@ struct RepackTo {
     uint8_t *slab;       // its slab's rows (nullptr: none)
     uint32_t row_bytes;  // bytes per slab row
     uint32_t slab_wide;  // two bytes per bin in the slab row
-    uint32_t slab_col;   // its feature index in the slab
+    uint32_t slab_col;   // its byte (or two-byte) position in the slab row
+    uint32_t num_bins;   // the feature's bins: a larger bin sets *bad
+    uint32_t *bad;       // (nullptr: no check)
 };
 
 struct DevData {
@@ -349,6 +358,7 @@ struct Context {
     // slab_stride() apart, so that a k_step_rows launch finds its later slabs by arithmetic
     DevBuf<uint8_t> slab_bins;
     DevBuf<uint32_t> slab_col_bins;  // every slab's col_bins, consecutive
+    DevBuf<uint32_t> slab_pos_word, slab_slot_flat;  // the dense slabs' tables, consecutive
     uint32_t hist_cap = 0;     // k_hist workgroups a leaf is spread over at most
     uint32_t step_target = 0;  // k_step_rows workgroups a step is spread over (its grid: step_target + JMAX)
     uint32_t col16 = 0;                     // some group has two-byte bins: column-major bins are u16
@@ -633,6 +643,8 @@ struct Context {
         hist_cap = step_target = cus;
         build_slabs();
         // device buffers
+        scalars.alloc(16);
+        hip_check(hipMemsetAsync(scalars.p + 15, 0, 4, stream), "zero bin check");
         train = DevData{};
         upload_bins(t, train, true);
         valid.clear();
@@ -641,6 +653,9 @@ struct Context {
             upload_bins(v[i], d, false);
             valid.push_back(std::move(d));
         }
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p + 15, 4, hipMemcpyDeviceToHost, stream), "read bin check");
+        sync();
+        if (h_u32.p[0]) fail(SROCM_ERR_DATA, "a bin at or above its feature's num_bins");
         label.alloc(rows);
         h_label_v.assign(t->label, t->label + rows);
         hip_check(hipMemcpy(label.p, t->label, rows * sizeof(float), hipMemcpyHostToDevice), "upload label");
@@ -658,7 +673,6 @@ struct Context {
         part.alloc(rows);
         part2.alloc(rows);
         block_left.alloc(cus * 4 + 16);
-        scalars.alloc(16);
         std::vector<FeatDev> fd(nf);
         has_narrow = has_wide = false;
         for (uint32_t f = 0; f < nf; ++f) {
@@ -740,7 +754,96 @@ struct Context {
             }
             for (size_t b = 0; b < wide.size(); b += max_cols / 4)
                 add_slab(wide, b, std::min(wide.size(), b + max_cols / 4), true);
+            // more than one slab of byte features: dense slabs instead, when they take fewer LDS columns
+            size_t packed = 0;
+            while (packed < slabs.size() && !slabs[packed].wide) ++packed;
+            if (!q32 && packed > 1) build_dense(narrow, packed);
         }
+    }
+
+    // Dense slabs for the byte features `narrow` (non-trivial feature indices), in place of their `packed` slabs at
+    // the start of `slabs`, when they take fewer LDS columns (so fewer partial words a workgroup) than those. The
+    // features, largest bin count first, are dealt over k slabs in turn (k from the features' count and bins up,
+    // until each slab fits); in a slab, each of the 128 LDS columns holds up to `per` features (per = ceil(its
+    // features / 128)), stacked by bin count, a feature going to the column of fewest bins so far, whose bins must fit
+    // its 256 rows. Feature j of column c is the row's byte c + 128 j. False (nothing changed) when they do not fit
+    // or take no fewer columns.
+    static constexpr uint32_t DENSE_FEATURES = 2048;  // a slab's features at most (rows of 2048 bytes, 8 passes)
+    bool build_dense(const std::vector<uint32_t> &narrow, size_t packed) {
+        uint32_t packed_cols = 0;
+        for (size_t si = 0; si < packed; ++si) packed_cols += slabs[si].width;
+        std::vector<uint32_t> order(narrow);
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+            return feats[nt_feat[x]].num_bins > feats[nt_feat[y]].num_bins;
+        });
+        uint64_t total_bins = 0;
+        for (uint32_t i : order) total_bins += feats[nt_feat[i]].num_bins;
+        const size_t k0 = std::max<size_t>((order.size() + DENSE_FEATURES - 1) / DENSE_FEATURES, (total_bins + 32767) / 32768);
+        for (size_t k = k0; k * 128 < packed_cols; ++k) {
+            std::vector<Slab> out(k);
+            std::vector<std::pair<uint32_t, uint32_t>> place(nt_feat.size());  // nt -> (slab, byte)
+            bool ok = true;
+            for (size_t si = 0; si < k && ok; ++si) {
+                std::vector<uint32_t> part;
+                for (size_t j = si; j < order.size(); j += k) part.push_back(order[j]);
+                const uint32_t per = static_cast<uint32_t>((part.size() + 127) / 128);
+                if (per * 128 > DENSE_FEATURES) {
+                    ok = false;
+                    break;
+                }
+                std::vector<uint32_t> sum(128, 0);
+                std::vector<std::vector<uint32_t>> col(128);
+                for (uint32_t i : part) {
+                    const uint32_t nb = feats[nt_feat[i]].num_bins;
+                    int best = -1;
+                    for (int c = 0; c < 128; ++c)
+                        if (col[c].size() < per && (best < 0 || sum[c] < sum[best])) best = c;
+                    if (best < 0 || sum[best] + nb > 256) {
+                        ok = false;
+                        break;
+                    }
+                    col[best].push_back(i);
+                    sum[best] += nb;
+                }
+                if (!ok) break;
+                Slab &s = out[si];
+                s.width = 128;
+                s.dense_row = 128 * per;
+                s.dense_passes = per <= 8 ? 4 : 8;  // 32 * per dwords a row, 64 a pass
+                s.pos_word.resize(256ull * s.dense_passes);
+                for (uint32_t p = 0; p < s.pos_word.size(); ++p) s.pos_word[p] = 256u * 128u + p % 128;  // the spare row
+                s.slot_flat.assign(256ull * 128, 0u);
+                for (uint32_t c = 0; c < 128; ++c) {
+                    uint32_t base = 0;
+                    for (uint32_t j = 0; j < col[c].size(); ++j) {
+                        const uint32_t i = col[c][j], pos = c + 128 * j;
+                        const srocm_feature &m = feats[nt_feat[i]];
+                        s.pos_word[pos] = base * 128 + c;
+                        for (uint32_t b = 0; b < m.num_bins; ++b) s.slot_flat[(base + b) * 128 + c] = m.hist_offset + b + 1;
+                        place[i] = {static_cast<uint32_t>(si), pos};
+                        base += m.num_bins;
+                    }
+                }
+                for (uint32_t i : part) s.feats.push_back(nt_feat[i]);
+                std::sort(s.feats.begin(), s.feats.end());
+            }
+            if (!ok) continue;
+            // the dense slabs replace the packed ones at the start of `slabs`
+            slabs.erase(slabs.begin(), slabs.begin() + static_cast<std::ptrdiff_t>(packed));
+            const uint32_t shift = static_cast<uint32_t>(k) - static_cast<uint32_t>(packed);  // later slabs move by this
+            for (uint32_t i = 0; i < nt_feat.size(); ++i)
+                if (group_bits[feats[nt_feat[i]].group] != 16) {
+                    nt_slab[i] = place[i].first;
+                    nt_slab_col[i] = place[i].second;
+                } else {
+                    nt_slab[i] += shift;
+                }
+            slabs.insert(slabs.begin(), std::make_move_iterator(out.begin()), std::make_move_iterator(out.end()));
+            max_width = 32;
+            for (auto &sl : slabs) max_width = std::max(max_width, sl.width);
+            return true;
+        }
+        return false;
     }
 
     // The slab tables: per slab slot its feature's flat bins, the column groups of k_step_reduce, the numerical
@@ -748,12 +851,19 @@ struct Context {
     void build_slab_tables() {
         partial.alloc(static_cast<size_t>(hist_cap) * 256 * max_width * 2);
         std::vector<uint32_t> all_bins;  // slab_col_bins
+        std::vector<uint32_t> all_pos, all_slot;  // slab_pos_word, slab_slot_flat
         for (auto &s : slabs) {
             // slot i: a byte feature's (column i % W, segment i / W); in a wide slab, virtual column i, bins
-            // congruent to i / (W/4) mod 4 of feature i % (W/4)
+            // congruent to i / (W/4) mod 4 of feature i % (W/4); a dense slab's slots are in its own tables
             const uint32_t ns = s.slots();
             std::vector<uint32_t> off(ns, 0), nb(ns, 0), st(ns, 1);
-            for (size_t c = 0; c < s.feats.size(); ++c) {
+            if (s.dense_passes) {
+                s.pos_off = all_pos.size();
+                all_pos.insert(all_pos.end(), s.pos_word.begin(), s.pos_word.end());
+                s.slot_off = all_slot.size();
+                all_slot.insert(all_slot.end(), s.slot_flat.begin(), s.slot_flat.end());
+            }
+            for (size_t c = 0; c < s.feats.size() && !s.dense_passes; ++c) {
                 const srocm_feature &m = feats[s.feats[c]];
                 if (!s.wide) {
                     off[c] = m.hist_offset;
@@ -779,6 +889,12 @@ struct Context {
         slab_col_bins.alloc(std::max<size_t>(all_bins.size(), 1));
         if (!all_bins.empty())
             hip_check(hipMemcpy(slab_col_bins.p, all_bins.data(), all_bins.size() * 4, hipMemcpyHostToDevice), "upload slab");
+        slab_pos_word.alloc(std::max<size_t>(all_pos.size(), 1));
+        slab_slot_flat.alloc(std::max<size_t>(all_slot.size(), 4));
+        if (!all_pos.empty()) {
+            hip_check(hipMemcpy(slab_pos_word.p, all_pos.data(), all_pos.size() * 4, hipMemcpyHostToDevice), "upload dense slab");
+            hip_check(hipMemcpy(slab_slot_flat.p, all_slot.data(), all_slot.size() * 4, hipMemcpyHostToDevice), "upload dense slab");
+        }
         // groups of CG_COLS slab columns for k_step_reduce, the numerical features in groups of CG_COLS for
         // k_step_scan, and the categorical ones for k_step_cat
         {
@@ -793,8 +909,9 @@ struct Context {
                 // packed slab's column c holds feature seg * W + c in bins [seg, seg + 1) * 2^seg_shift
                 const uint32_t cap = s.capacity();
                 for (uint32_t c0 = 0; c0 < s.width; c0 += CG_COLS) {
-                    ColGroup x{poff, s.width, c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}, {}, s.seg_shift()};
-                    for (uint32_t k = 0; k < CG_COLS; ++k) {
+                    ColGroup x{poff, s.width, c0, static_cast<uint32_t>(si) * k1_groups(), {}, {}, {}, s.seg_shift(),
+                               s.dense_passes ? 1u : 0u, static_cast<uint32_t>(s.slot_off)};
+                    for (uint32_t k = 0; k < CG_COLS && !s.dense_passes; ++k) {
                         const uint32_t v = c0 + k;
                         x.stride[k] = s.wide ? 4u : 1u;
                         for (uint32_t seg = 0; seg < s.pack; ++seg) {
@@ -865,7 +982,7 @@ struct Context {
         const uint64_t cb = col16 ? 2 : 1;
         for (uint32_t nt = 0; rows && nt < nt_feat.size(); ++nt) {
             const Slab &sl = slabs[nt_slab[nt]];
-            RepackTo to{nullptr, col16, slab_bins.p + sl.bins_off, sl.row_bytes(), sl.wide ? 1u : 0u, nt_slab_col[nt]};
+            RepackTo to{nullptr, col16, slab_bins.p + sl.bins_off, sl.row_bytes(), sl.wide ? 1u : 0u, nt_slab_col[nt], 0u, nullptr};
             repack(train.col.p + static_cast<size_t>(nt) * rows * cb, static_cast<uint32_t>(cb), 0, col16 ? 16u : 8u, rows, to);
         }
         build_slab_tables();
@@ -912,7 +1029,9 @@ struct Context {
             for (uint32_t c = 0; c < group_col_nt[g].size(); ++c) {
                 int32_t nt = group_col_nt[g][c];
                 if (nt < 0) continue;
-                RepackTo to{out.col.p + static_cast<size_t>(nt) * n * cb, col16, nullptr, 0, 0, 0};
+                // every bin must be below its feature's count: the slabs' LDS addresses rely on it (checked after)
+                RepackTo to{out.col.p + static_cast<size_t>(nt) * n * cb, col16, nullptr, 0, 0, 0,
+                            feats[nt_feat[nt]].num_bins, scalars.p + 15};
                 if (with_slabs) {
                     const Slab &sl = slabs[nt_slab[nt]];
                     to.slab = slab_bins.p + sl.bins_off;
@@ -1053,7 +1172,8 @@ struct Context {
     void launch_hist_into(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
                           int64_t *parent, uint64_t bins_used, int32_t *partials, uint32_t grid, bool profiled) {
         for (auto &s : slabs) {
-            HistArgs a{slab_bins.p + s.bins_off, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS};
+            HistArgs a{slab_bins.p + s.bins_off, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS,
+                       slab_pos_word.p + s.pos_off, s.row_bytes() / 4};
             hipEvent_t e0 = nullptr, e1 = nullptr;
             if (profiled) {
                 e0 = event();
@@ -1072,6 +1192,8 @@ struct Context {
             case 34: k_hist<32, false, 2><<<grid, 1024, 0, stream>>>(a); break;
             case 66: k_hist<64, false, 2><<<grid, 1024, 0, stream>>>(a); break;
             case 130: k_hist<128, false, 2><<<grid, 1024, 0, stream>>>(a); break;
+            case 3004: k_hist<128, false, 1, false, 4><<<grid, 1024, 0, stream>>>(a); break;
+            case 3008: k_hist<128, false, 1, false, 8><<<grid, 1024, 0, stream>>>(a); break;
             case 1032: k_hist<32, false, 1, true><<<grid, 1024, 0, stream>>>(a); break;
             case 1064: k_hist<64, false, 1, true><<<grid, 1024, 0, stream>>>(a); break;
             case 1033: k_hist<32, true, 1, true><<<grid, 1024, 0, stream>>>(a); break;
@@ -1084,7 +1206,8 @@ struct Context {
                 prof.hist_events.emplace_back(e0, e1);
                 prof.hist_launches += 1;
             }
-            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, s.col_stride.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width, s.seg_shift()};
+            ReduceArgs r{partials, s.col_offset.p, s.col_bins.p, s.col_stride.p, out, parent, dev_left, begin, count, side, grid, HIST_MIN_ROWS, s.width, s.seg_shift(),
+                         s.dense_passes ? slab_slot_flat.p + s.slot_off : nullptr};
             k_hist_reduce<<<div_up(256ull * s.width, 32), 256, 0, stream>>>(r);
             launch_check("k_hist_reduce");
         }
@@ -1686,6 +1809,7 @@ __global__ void k_repack(const uint8_t *__restrict__ src, uint32_t stride, uint3
         if (bits == 16) b = static_cast<uint32_t>(row[column]) | (static_cast<uint32_t>(row[column + 1]) << 8);
         else if (bits == 4) b = (static_cast<uint32_t>(row[column >> 1]) >> (4 * (column & 1u))) & 15u;
         else b = row[column];
+        if (to.bad && b >= to.num_bins) *to.bad = 1u;  // every writer stores the same value
         if (!to.col) {
         } else if (to.col16) {
             reinterpret_cast<uint16_t *>(to.col)[r] = static_cast<uint16_t>(b);
@@ -1806,11 +1930,12 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 for (size_t si = 0; si < slabs.size();) {
                     size_t sj = si + 1;
                     if (si > 0)
-                        while (sj < slabs.size() && slabs[sj].kernel() == slabs[si].kernel()) ++sj;
+                        while (sj < slabs.size() && slabs[sj].same_launch(slabs[si])) ++sj;
                     const Slab &sl = slabs[si];
                     StepArgs sa{slab_bins.p + sl.bins_off, slab_stride(sl), step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
-                                slab_col_bins.p + sl.col_bins_off, k1_groups(), packed.p, train.col.p, col16, rows, part.p, part2.p,
-                                tile_status.p, d_plans.p + parity, g.ctl, flush_rows(), si == 0 ? 1u : 0u};
+                                slab_col_bins.p + sl.col_bins_off, slab_pos_word.p + sl.pos_off, sl.row_bytes() / 4, k1_groups(), packed.p,
+                                train.col.p, col16, rows, part.p, part2.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(),
+                                si == 0 ? 1u : 0u};
                     const uint32_t grid = k1_groups() * static_cast<uint32_t>(sj - si);
                     switch (slabs[si].kernel()) {
                     case 32: k_step_rows<32><<<grid, 1024, 0, stream>>>(sa); break;
@@ -1824,6 +1949,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     case 34: k_step_rows<32, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
                     case 66: k_step_rows<64, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
                     case 130: k_step_rows<128, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 3004: k_step_rows<128, false, 1, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
+                    case 3008: k_step_rows<128, false, 1, false, 8><<<grid, 1024, 0, stream>>>(sa); break;
                     case 1032: k_step_rows<32, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
                     case 1064: k_step_rows<64, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
                     case 1033: k_step_rows<32, true, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
@@ -1839,7 +1966,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     prof.step_events.emplace_back(e0, e1);
                     prof.step_launches += static_cast<double>(launches);
                 }
-                ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity};
+                ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity, slab_slot_flat.p};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
                 ScanStepArgs sca{scan_feat.p, cat_feats.p, ncat, d_plans.p + parity};
@@ -2349,6 +2476,20 @@ int srocm_name(void *ctx, char *buf, size_t len) {
             std::strncpy(buf, n.c_str(), len - 1);
             buf[len - 1] = 0;
         }
+    });
+}
+
+int srocm_slab_layout(void *ctx, uint32_t *out, uint32_t cap, uint32_t *count) {
+    return guard(ctx, [&](Context &c) {
+        c.require_loaded();
+        for (size_t i = 0; i < c.slabs.size() && i < cap && out; ++i) {
+            const Slab &s = c.slabs[i];
+            out[4 * i] = s.width;
+            out[4 * i + 1] = s.row_bytes();
+            out[4 * i + 2] = s.dense_passes ? 0u : (s.wide ? 1u : s.pack);
+            out[4 * i + 3] = (s.wide ? 1u : 0u) | (s.q32 ? 2u : 0u) | (s.dense_passes ? 4u : 0u);
+        }
+        if (count) *count = static_cast<uint32_t>(c.slabs.size());
     });
 }
 

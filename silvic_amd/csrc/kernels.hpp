@@ -288,6 +288,8 @@ struct HistArgs {
     uint32_t flush_rows;
     uint32_t max_groups;      // == gridDim.x
     uint32_t min_rows_per_group;
+    const uint32_t *pos_word; // dense slab: per row byte, its LDS word at bin 0 (segment base * W + column)
+    uint32_t dw_row;          // dense slab: dwords per row
 };
 
 // The rows of the leaf after resolving a device-side left count; identical in every kernel that calls it.
@@ -379,22 +381,75 @@ __device__ __forceinline__ void row_units(int32_t word, bool on, int32_t &gv, in
     }
 }
 
+// A dense slab (DP passes): features stacked in the LDS columns by their bin counts, W = 128 columns of 256 bin rows
+// and a spare row 256. The feature at row byte i is in column i % 128 at rows [base, base + bins) of it; pos_word[i]
+// = base * W + i % 128, and positions past the slab's features point at the spare row (their bytes are 0). A row of
+// up to 64 * DP dwords is read by the whole wave, lane l taking dwords l, l + 64, ... (pass p): byte x of dword
+// 64p + l is position 256p + 4l + x, so the 32 lanes of a half-wave add to 32 distinct columns, as in a byte slab.
+template <int DP>
+__device__ __forceinline__ void dense_lanes(const uint32_t *pos_word, uint32_t lane, uint32_t (&xs)[4],
+                                            uint32_t (&cols)[DP][4]) {
+    const uint32_t rot = (lane & 31u) >> 3;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t x = (k + rot) & 3u;
+        xs[k] = 8u * x;
+#pragma unroll
+        for (int p = 0; p < DP; ++p) cols[p][k] = pos_word[256u * p + 4u * lane + x];
+    }
+}
+
+// The rows list[c0 .. c1) of a dense slab into the LDS, UNROLL rows a wave at a time over NW waves (`wave` among
+// them); dwords past the row (dw_row) read as 0, i.e. bin 0 of spare positions.
+template <int W, int DP, int UNROLL, int NW = 16>
+__device__ __forceinline__ void hist_list_dense(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1,
+                                                const int32_t *gh, const uint32_t *bins32, uint32_t dw_row,
+                                                const uint32_t (&xs)[4], const uint32_t (&cols)[DP][4],
+                                                uint32_t wave = threadIdx.x >> 6) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t last = c1 - 1;
+    for (uint32_t base = c0 + wave * UNROLL; base < c1; base += NW * UNROLL) {
+        uint32_t r[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) r[u] = list[min(base + u, last)];
+        int32_t gq[UNROLL];
+        uint32_t dw[UNROLL][DP];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            gq[u] = gh[r[u]];
+#pragma unroll
+            for (int p = 0; p < DP; ++p) {
+                const uint32_t d = 64u * p + lane;
+                dw[u][p] = d < dw_row ? bins32[static_cast<size_t>(r[u]) * dw_row + d] : 0u;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int32_t gv = base + u < c1 ? gq[u] : 0;
+#pragma unroll
+            for (int p = 0; p < DP; ++p) add_row_bins<W>(lds, dw[u][p], gv, 0, xs, cols[p]);
+        }
+    }
+}
+
 // Loads are branch-free: row positions past the range are clamped to its last row and their gradients
 // zeroed, so the compiler issues every load of a step back to back instead of one masked load at a time. A
 // wave fetches the row ids of its next step in one coalesced load (lane l: id l) while it works on the current
 // step, and hands them out with a shuffle. WIDE: the slab's rows are W / 4 two-byte bins. PACK: the slab's rows
 // are W * PACK bytes, PACK features of at most 256 / PACK bins to an LDS column.
-template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false>
+template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false, int DP = 0>
 __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
     static_assert(!Q32 || W <= 64, "separate g and h counters take twice the LDS");
+    static_assert(DP == 0 || (W == 128 && !WIDE && PACK == 1 && !Q32), "a dense slab has 128 byte columns");
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;  // dwords per row
     constexpr int RPW = WAVE / DW;            // rows per wave step
     // row ids of one step fit one wave-wide load; at W = 128 the 64 accumulator registers leave room for 8
     constexpr int UNROLL = W == 128 ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr uint32_t STEP = 16u * RPW * UNROLL;          // rows per block step (16 waves)
     constexpr int SLOTS = 256 * W / 1024;
-    __shared__ int32_t lds[(Q32 ? 2 : 1) * 256 * W];
+    constexpr int LDS_WORDS = (Q32 ? 2 : 1) * 256 * W + (DP ? W : 0);  // a dense slab's spare row
+    __shared__ int32_t lds[LDS_WORDS];
 
     uint32_t lb, n;
     leaf_rows(a.dev_left, a.begin, a.count, a.side, lb, n);
@@ -402,7 +457,7 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     hist_split(n, a.max_groups, a.min_rows_per_group, groups, per);
     if (blockIdx.x >= groups) return;
     const uint32_t tid = threadIdx.x;
-    for (int j = 0; j < (Q32 ? 2 : 1) * SLOTS; ++j) lds[tid + j * 1024] = 0;
+    for (uint32_t k = tid; k < static_cast<uint32_t>(LDS_WORDS); k += 1024) lds[k] = 0;
     int32_t accg[SLOTS], acch[SLOTS];
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) accg[j] = acch[j] = 0;
@@ -417,30 +472,36 @@ __global__ __launch_bounds__(1024) void k_hist(HistArgs a) {
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(a.bins);
     uint32_t start = blockIdx.x * per;
     uint32_t end = start + per < n ? start + per : n;
+    uint32_t dcols[DP ? DP : 1][4];
+    if constexpr (DP > 0) dense_lanes<DP>(a.pos_word, lane, xs, dcols);
 
     for (uint32_t chunk = start; chunk < end; chunk += a.flush_rows) {
         uint32_t cend = end - chunk > a.flush_rows ? chunk + a.flush_rows : end;
-        uint32_t last = cend - 1;
-        uint32_t base = chunk + wave * RPW * UNROLL;
-        uint32_t cidx = rows[min(base + lane, last)];
-        for (; base < cend; base += STEP) {
-            uint32_t r[UNROLL];
+        if constexpr (DP > 0) {
+            hist_list_dense<W, DP, DP <= 4 ? 4 : 2>(lds, rows, chunk, cend, a.gh, bins32, a.dw_row, xs, dcols);
+        } else {
+            uint32_t last = cend - 1;
+            uint32_t base = chunk + wave * RPW * UNROLL;
+            uint32_t cidx = rows[min(base + lane, last)];
+            for (; base < cend; base += STEP) {
+                uint32_t r[UNROLL];
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) r[u] = __shfl(cidx, u * RPW + rsub);
-            cidx = rows[min(base + STEP + lane, last)];
-            uint32_t dw[UNROLL];
-            int32_t g[UNROLL];
+                for (int u = 0; u < UNROLL; ++u) r[u] = __shfl(cidx, u * RPW + rsub);
+                cidx = rows[min(base + STEP + lane, last)];
+                uint32_t dw[UNROLL];
+                int32_t g[UNROLL];
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                g[u] = a.gh[r[u]];
-                dw[u] = bins32[(size_t)r[u] * DW + d];
-            }
+                for (int u = 0; u < UNROLL; ++u) {
+                    g[u] = a.gh[r[u]];
+                    dw[u] = bins32[(size_t)r[u] * DW + d];
+                }
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) {
-                int32_t gv, hv;
-                row_units<Q32>(g[u], base + u * RPW + rsub < cend, gv, hv);
-                if constexpr (WIDE) add_row_bins_wide<W, Q32>(lds, dw[u], gv, hv, d);
-                else add_row_bins<W, PACK, Q32>(lds, dw[u], gv, hv, xs, cols);
+                for (int u = 0; u < UNROLL; ++u) {
+                    int32_t gv, hv;
+                    row_units<Q32>(g[u], base + u * RPW + rsub < cend, gv, hv);
+                    if constexpr (WIDE) add_row_bins_wide<W, Q32>(lds, dw[u], gv, hv, d);
+                    else add_row_bins<W, PACK, Q32>(lds, dw[u], gv, hv, xs, cols);
+                }
             }
         }
         __syncthreads();
@@ -481,6 +542,7 @@ struct ReduceArgs {
     uint32_t max_groups, min_rows_per_group;
     uint32_t width;     // W
     uint32_t seg_shift; // a packed slab's column holds a feature each 2^seg_shift bins: 8 (one feature), 7 or 6
+    const uint32_t *slot_flat;  // a dense slab: per slot (bin * W + column) its flat-histogram bin + 1, 0 for none
 };
 
 // A block takes 32 slots (bin * W + column) and splits the workgroups' partials of each into 8 stripes that meet in
@@ -494,9 +556,11 @@ __global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
     const uint32_t slots = 256u * a.width;
     const uint32_t tid = threadIdx.x, lane = tid & 31u, stripe = tid >> 5;
     const uint32_t s = blockIdx.x * 32u + lane, col = s % a.width, bin = s / a.width;
-    // the slot's feature: segment bin >> seg_shift of the column (its index in the per-feature arrays), its bin
+    // the slot's feature: segment bin >> seg_shift of the column (its index in the per-feature arrays), its bin;
+    // in a dense slab the slot's flat bin from the table
     const uint32_t vb = bin & ((1u << a.seg_shift) - 1u), fs = (bin >> a.seg_shift) * a.width + col;
-    const bool on = s < slots && vb < a.col_bins[fs];
+    const uint32_t flat1 = a.slot_flat && s < slots ? a.slot_flat[s] : 0u;
+    const bool on = s < slots && (a.slot_flat ? flat1 != 0u : vb < a.col_bins[fs]);
     int64_t g = 0, h = 0;
     if (on) {
         const int2 *p = reinterpret_cast<const int2 *>(a.partial) + s;
@@ -516,7 +580,8 @@ __global__ __launch_bounds__(256) void k_hist_reduce(ReduceArgs a) {
             g += red[0][k][lane];
             h += red[1][k][lane];
         }
-        const size_t o = 2 * (static_cast<size_t>(a.col_offset[fs]) + static_cast<size_t>(vb) * a.col_stride[fs]);
+        const size_t o = a.slot_flat ? 2 * static_cast<size_t>(flat1 - 1u)
+                                     : 2 * (static_cast<size_t>(a.col_offset[fs]) + static_cast<size_t>(vb) * a.col_stride[fs]);
         a.out[o] = g;
         a.out[o + 1] = h;
         if (a.parent) {
@@ -3053,6 +3118,8 @@ struct StepArgs {
     int32_t *partial;            // its partials, step_partial_stride(W) pairs apart, one per workgroup
     uint32_t *fmt;               // per workgroup: its partial is packed (1) or {g, h} pairs (0)
     const uint32_t *col_bins;    // per slab column: its feature's bins (0 for padding)
+    const uint32_t *pos_word;    // a dense slab: per row byte, its LDS word at bin 0 (256 * DP entries a slab)
+    uint32_t dw_row;             // a dense slab: dwords per row
     uint32_t k1;                 // workgroups a slab
     const int32_t *gh;           // packed quantized gradients per row
     const uint8_t *colbase;      // column-major bins [feature][rows]
@@ -3353,16 +3420,27 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
     }
 }
 
-template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false>
+// A split step's histogram of list[c0 .. c1): hist_list, or hist_list_dense for a dense slab (DP passes).
+template <int W, bool WIDE, int PACK, bool Q32, int DP, int UNROLL, int NW = 16>
+__device__ __forceinline__ void step_hist(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
+                                          const uint32_t *bins32, uint32_t dw_row, const uint32_t (&xs)[4],
+                                          const uint32_t (&dcols)[DP ? DP : 1][4], uint32_t wave = threadIdx.x >> 6) {
+    if constexpr (DP > 0) hist_list_dense<W, DP, DP <= 4 ? 2 : 1, NW>(lds, list, c0, c1, gh, bins32, dw_row, xs, dcols, wave);
+    else hist_list<W, WIDE, PACK, Q32, UNROLL, NW>(lds, list, c0, c1, gh, bins32, wave);
+}
+
+template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false, int DP = 0>
 __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
     static_assert(!Q32 || W <= 64, "separate g and h counters take twice the LDS");
+    static_assert(DP == 0 || (W == 128 && !WIDE && PACK == 1 && !Q32), "a dense slab has 128 byte columns");
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
     // rows per lane in multi-tile workgroups (16 at W = 32 with packed columns spills)
     constexpr int UNROLL = (W == 128 || (W == 32 && PACK > 1)) ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr int SLOTS = 256 * W / 1024;
-    __shared__ int32_t lds[(Q32 ? 2 : 1) * 256 * W];
+    constexpr int LDS_WORDS = (Q32 ? 2 : 1) * 256 * W + (DP ? W : 0);  // a dense slab's spare row
+    __shared__ int32_t lds[LDS_WORDS];
     __shared__ StepShared sh;
 
     // a launch of histogram-only slabs takes k1 workgroups a slab: wg is the workgroup within its slab
@@ -3372,8 +3450,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         int32_t *partial;
         uint32_t *fmt;
         const uint32_t *col_bins;
+        const uint32_t *pos_word;
     } R = {a.bins + sl * a.bins_stride, a.partial + static_cast<size_t>(sl) * a.k1 * 2 * step_partial_stride(W),
-           a.fmt + sl * a.k1, a.col_bins + sl * (W * PACK)};
+           a.fmt + sl * a.k1, a.col_bins + sl * (W * PACK), a.pos_word + sl * 256u * (DP ? DP : 1)};
     StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     if (wg >= P.total_groups) return;
     const uint32_t j = job_of(P.group_base, P.njobs, wg);
@@ -3402,7 +3481,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (tid < 8) sh.left_bins[tid] = J.left_bins[tid];  // visible after the first barrier below
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(R.bins);
     if (v.hist)
-        for (int j = 0; j < (Q32 ? 2 : 1) * SLOTS; ++j) lds[tid + j * 1024] = 0;
+        for (uint32_t k = tid; k < static_cast<uint32_t>(LDS_WORDS); k += 1024) lds[k] = 0;
+    uint32_t dxs[4], dcols[DP ? DP : 1][4];
+    if constexpr (DP > 0) dense_lanes<DP>(R.pos_word, tid & 63u, dxs, dcols);
 
     if (packed) {  // one tile; the partial is the LDS words themselves
         __syncthreads();
@@ -3418,9 +3499,9 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (v.hist) hist_list<W, WIDE, PACK, Q32, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (v.hist) step_hist<W, WIDE, PACK, Q32, DP, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1);
         } else if (v.hist) {
-            hist_list<W, WIDE, PACK, Q32, 16>(lds, sh.list, 0, nb, a.gh, bins32);
+            step_hist<W, WIDE, PACK, Q32, DP, 16>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols);
         }
         __syncthreads();  // the offset and the histogram are complete
         if (v.partition) tile_scatter(v, t, st, sh);
@@ -3440,7 +3521,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     // partial as {g, h} pairs; a workgroup that never flushes stores its partial packed instead
     int2 *pairs = reinterpret_cast<int2 *>(R.partial) + static_cast<size_t>(wg) * step_partial_stride(W);
     // slot tid + 1024 j is bin (tid + 1024 j) / W of column tid % W; a packed column's features are all stored
-    const uint32_t col_bins = PACK > 1 ? 256u : R.col_bins[tid % W];
+    const uint32_t col_bins = (PACK > 1 || DP > 0) ? 256u : R.col_bins[tid % W];
     uint32_t pending = 0;  // rows added to the packed LDS words since they were last flushed
     bool flushed = false;
     // partition launches take tiles in ticket order, the next ticket drawn while the current tile is worked on (a
@@ -3482,7 +3563,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 }
                 uint32_t room = a.flush_rows - pending;
                 uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                hist_list<W, WIDE, PACK, Q32, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32);
+                step_hist<W, WIDE, PACK, Q32, DP, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32, a.dw_row, dxs, dcols);
                 pending += c1 - c0;
                 c0 = c1;
             }
@@ -3490,11 +3571,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (!hist_done) hist_list<W, WIDE, PACK, Q32, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, wv - 1);
+            else if (!hist_done) step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1);
             __syncthreads();  // the offset is in sh.prefix
             tile_scatter(v, t, st, sh);
         } else if (!hist_done) {
-            hist_list<W, WIDE, PACK, Q32, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32);
+            step_hist<W, WIDE, PACK, Q32, DP, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols);
         }
         if (!hist_done) pending += nb;
         if (tn < v.ntiles) tile_bins(v, r);
@@ -3525,6 +3606,8 @@ struct ColGroup {
     uint32_t bins[4][4];    // per segment and column: the feature's bins (0 for padding)
     uint32_t stride[4];     // per column: flat-histogram bins between its consecutive bins (4 in a wide slab)
     uint32_t seg_shift;     // a column holds a feature each 2^seg_shift bins (8: one; 7 or 6 in a packed slab)
+    uint32_t dense;         // a dense slab: the slots' flat bins come from the slot table at slot_base
+    uint32_t slot_base;
 };
 
 // Block-wide hand-off through `counter`: true in every thread of the block that arrives last of `target` blocks,
@@ -3567,6 +3650,7 @@ struct ReduceStepArgs {
     const uint32_t *fmt;        // the partials' formats (per slab, per k_step_rows workgroup: 1 packed, 0 pairs)
     const ColGroup *cgs;        // [ncg]
     StepPlan *plan;
+    const uint32_t *slot_flat;  // dense slabs: per slot, its flat-histogram bin + 1 (0: none)
 };
 
 // The end of job j, by one block (learner.rs:294-352): both children's best splits from their per-feature
@@ -3706,14 +3790,27 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         // the parent's bins are loaded with the partials (the writes below need them); every partial is first read
         // as packed, and a {g, h} pair partial (a workgroup that flushed) is read again in its own layout
         const uint32_t seg = bin >> cg.seg_shift, vb = bin & ((1u << cg.seg_shift) - 1u);
+        // the flat bin (x2) of each of the four columns' slot, or -1
+        int64_t fo[4];
+        if (cg.dense) {
+            const uint4 t = *reinterpret_cast<const uint4 *>(a.slot_flat + cg.slot_base + static_cast<size_t>(bin) * cg.width + cg.c0);
+            const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) fo[c] = tv[c] ? 2 * (static_cast<int64_t>(tv[c]) - 1) : -1;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                fo[c] = vb < cg.bins[seg][c]
+                            ? 2 * (static_cast<int64_t>(cg.offset[seg][c]) + static_cast<int64_t>(vb) * cg.stride[c])
+                            : -1;
+        }
         int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (vb < cg.bins[seg][c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[seg][c]) + static_cast<size_t>(vb) * cg.stride[c]);
-                    pg[c] = parent[o];
-                    ph[c] = parent[o + 1];
+                if (fo[c] >= 0) {
+                    pg[c] = parent[fo[c]];
+                    ph[c] = parent[fo[c] + 1];
                 }
             }
         }
@@ -3773,12 +3870,11 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (vb < cg.bins[seg][c]) {
-                    const size_t o = 2 * (static_cast<size_t>(cg.offset[seg][c]) + static_cast<size_t>(vb) * cg.stride[c]);
-                    built[o] = sg[c];
-                    built[o + 1] = sh[c];
-                    parent[o] = pg[c] - sg[c];
-                    parent[o + 1] = ph[c] - sh[c];
+                if (fo[c] >= 0) {
+                    built[fo[c]] = sg[c];
+                    built[fo[c] + 1] = sh[c];
+                    parent[fo[c]] = pg[c] - sg[c];
+                    parent[fo[c] + 1] = ph[c] - sh[c];
                 }
             }
         }
