@@ -376,11 +376,14 @@ struct Context {
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
     DevBuf<uint32_t> d_fmt;  // per slab and k_step_rows workgroup: the format of its partial (1 packed, 0 pairs)
-    DevBuf<int32_t> scan_feat;  // numerical slab features, CG_COLS a scan group, -1 padding
+    DevBuf<int32_t> unit_feat;   // k_step_scan's units: UNIT_FEATS numerical features each, -1 padding
+    DevBuf<uint32_t> unit_segl;  // and their lanes a feature (64, 16, 4)
     DevBuf<uint32_t> cat_feats;  // the categorical features of the slabs
     uint32_t ncat = 0;
     uint32_t ncg = 0;  // column groups of k_step_reduce
-    uint32_t nsg = 0;  // scan groups of k_step_scan
+    uint32_t nsg = 0;  // scan units of k_step_scan
+    bool has_seg_units = false;  // some units scan several features (k_step_scan_seg)
+    bool has_narrow64 = false;   // some units scan one byte feature (k_step_scan<false>)
     uint64_t step_partial_pairs = 0;
     uint32_t part_len = 0;
     std::vector<uint8_t> used;
@@ -930,17 +933,50 @@ struct Context {
                 }
                 poff += static_cast<uint64_t>(k1_groups()) * step_partial_stride(s.width);
             }
-            while (sfeat.size() % CG_COLS) sfeat.push_back(-1);
+            // scan units: byte features of at most 16 bins 16 a wave, of at most 64 bins 4 a wave, the others (and
+            // two-byte features) one a wave; when that saves under a quarter of the waves, every feature one a wave
+            // (the units of several features take a kernel of their own)
+            auto unit_lanes = [&](int32_t f) {
+                const uint32_t nb = feats[f].num_bins;
+                return group_bits[feats[f].group] == 16 || nb > 64 ? 64u : (nb > 16 ? 16u : 4u);
+            };
+            size_t seg_units = 0;
+            for (uint32_t segl : {4u, 16u, 64u}) {
+                size_t n = 0;
+                for (int32_t f : sfeat) n += unit_lanes(f) == segl;
+                seg_units += (n + 64 / segl - 1) / (64 / segl);
+            }
+            const bool segmented = seg_units * 4 <= sfeat.size() * 3;
+            std::vector<int32_t> ufeat;
+            std::vector<uint32_t> usegl;
+            for (uint32_t segl : {4u, 16u, 64u}) {
+                std::vector<int32_t> members;
+                for (int32_t f : sfeat)
+                    if ((segmented ? unit_lanes(f) : 64u) == segl) members.push_back(f);
+                const size_t per = 64 / segl;
+                for (size_t b = 0; b < members.size(); b += per) {
+                    for (size_t k = 0; k < UNIT_FEATS; ++k)
+                        ufeat.push_back(k < per && b + k < members.size() ? members[b + k] : -1);
+                    usegl.push_back(segl);
+                }
+            }
             d_fmt.alloc(std::max<size_t>(slabs.size(), 1) * k1_groups());
             ncg = static_cast<uint32_t>(cg.size());
-            nsg = static_cast<uint32_t>(sfeat.size() / CG_COLS);
+            nsg = static_cast<uint32_t>(usegl.size());
+            has_seg_units = segmented;
+            has_narrow64 = false;
+            for (size_t u = 0; u < usegl.size(); ++u)
+                if (usegl[u] == 64 && group_bits[feats[ufeat[u * UNIT_FEATS]].group] != 16) has_narrow64 = true;
             step_partial_pairs = std::max<uint64_t>(poff, 1);
             d_cgs.alloc(std::max<size_t>(cg.size(), 1));
-            scan_feat.alloc(std::max<size_t>(sfeat.size(), 1));
+            unit_feat.alloc(std::max<size_t>(ufeat.size(), 1));
+            unit_segl.alloc(std::max<size_t>(usegl.size(), 1));
             if (!cg.empty())
                 hip_check(hipMemcpy(d_cgs.p, cg.data(), cg.size() * sizeof(ColGroup), hipMemcpyHostToDevice), "upload column groups");
-            if (!sfeat.empty())
-                hip_check(hipMemcpy(scan_feat.p, sfeat.data(), sfeat.size() * 4, hipMemcpyHostToDevice), "upload scanned features");
+            if (!ufeat.empty()) {
+                hip_check(hipMemcpy(unit_feat.p, ufeat.data(), ufeat.size() * 4, hipMemcpyHostToDevice), "upload scan units");
+                hip_check(hipMemcpy(unit_segl.p, usegl.data(), usegl.size() * 4, hipMemcpyHostToDevice), "upload scan units");
+            }
             ncat = static_cast<uint32_t>(cats.size());
             cat_feats.alloc(std::max<size_t>(cats.size(), 1));
             if (!cats.empty())
@@ -1568,12 +1604,47 @@ struct Context {
         ScanJob job{dh.p, sums.grad, sums.hess, sums.count, dc.p};
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
+            // numerical byte features of 2..64 bins go in scan units of several (k_split_scan_seg), as in a tree
+            std::vector<uint8_t> seg(num_features, 0);
+            std::vector<int32_t> ufeat;
+            std::vector<uint32_t> usegl;
+            for (uint32_t segl : {4u, 16u}) {
+                std::vector<int32_t> members;
+                for (uint32_t f = 0; f < num_features; ++f) {
+                    const FeatDev &x = fd[f];
+                    if (x.kind == SROCM_BINS_NUMERICAL && !x.wide && x.num_bins >= 2 && x.num_bins <= 64 &&
+                        (x.num_bins > 16 ? 16u : 4u) == segl) {
+                        members.push_back(static_cast<int32_t>(f));
+                        seg[f] = 1;
+                    }
+                }
+                const size_t per = 64 / segl;
+                for (size_t b = 0; b < members.size(); b += per) {
+                    for (size_t k = 0; k < UNIT_FEATS; ++k) ufeat.push_back(k < per && b + k < members.size() ? members[b + k] : -1);
+                    usegl.push_back(segl);
+                }
+            }
+            DevBuf<uint8_t> dseg;
+            DevBuf<int32_t> dufeat;
+            DevBuf<uint32_t> dusegl;
+            dseg.alloc(num_features);
+            hip_check(hipMemcpyAsync(dseg.p, seg.data(), num_features, hipMemcpyHostToDevice, stream), "upload scan units");
             dim3 grid(div_up(num_features, 4), 1);
             bool narrow = false, wide = false;
             for (const FeatDev &x : fd) (x.wide ? wide : narrow) = true;
-            if (narrow) k_split_scan<false><<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
+            if (narrow) k_split_scan<false><<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr, dseg.p);
             if (wide) k_split_scan<true><<<grid, 256, 0, stream>>>(dj.p, dfd.p, dev.p, num_features, cfg_dev(cfg), sg, sh, dorder.p, nullptr);
             launch_check("k_split_scan");
+            if (!usegl.empty()) {
+                dufeat.alloc(ufeat.size());
+                dusegl.alloc(usegl.size());
+                hip_check(hipMemcpyAsync(dufeat.p, ufeat.data(), ufeat.size() * 4, hipMemcpyHostToDevice, stream), "upload scan units");
+                hip_check(hipMemcpyAsync(dusegl.p, usegl.data(), usegl.size() * 4, hipMemcpyHostToDevice, stream), "upload scan units");
+                k_split_scan_seg<<<dim3(div_up(usegl.size(), 4), 1), 256, 0, stream>>>(dj.p, dfd.p, dev.p, dufeat.p, dusegl.p,
+                                                                                      static_cast<uint32_t>(usegl.size()), cfg_dev(cfg), sg, sh);
+                launch_check("k_split_scan_seg");
+            }
+            sync();  // the unit buffers are locals
         }
         k_split_select<<<1, 256, 0, stream>>>(dj.p, num_features, cfg_dev(cfg), sg, sh, dso.p, dsp.p);
         launch_check("k_split_select");
@@ -1969,8 +2040,9 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity, slab_slot_flat.p};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
-                ScanStepArgs sca{scan_feat.p, cat_feats.p, ncat, d_plans.p + parity};
-                if (has_narrow) k_step_scan<false><<<scan_blocks(), 256, 0, stream>>>(g, sca);
+                ScanStepArgs sca{unit_feat.p, unit_segl.p, cat_feats.p, ncat, d_plans.p + parity};
+                if (has_narrow64) k_step_scan<false><<<scan_blocks(), 256, 0, stream>>>(g, sca);
+                if (has_seg_units) k_step_scan_seg<<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 if (has_wide) k_step_scan<true><<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 launch_check("k_step_scan");
                 if (ncat) {

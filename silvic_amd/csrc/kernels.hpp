@@ -1245,6 +1245,89 @@ __device__ __forceinline__ bool candidate_stop(const Ctx &c, const SplitCfgDev &
     return other_small && !skip;
 }
 
+constexpr uint32_t UNIT_FEATS = 16;  // features a scan unit holds at most (segments of 4 lanes)
+
+// A scan's lanes: the wave (SEGL = 64), or segments of SEGL = 16 or 4 lanes, each scanning its own feature of at most
+// 4 * SEGL bins (t = lane % SEGL holds bins 4t .. 4t + 3). The wave-wide operations below, taken over a segment:
+// inclusive sums (DPP row shifts stay inside a row of 16 lanes; a 4-lane segment masks the lanes below the shift),
+// the segment's last value, maxima and minima, and a lane's value read by its segment.
+template <int SEGL>
+__device__ __forceinline__ void seg_scan_add(double &g, double &h, int64_t &c) {
+    if constexpr (SEGL == 64) {
+        scan_add_step<DPP_ROW_SHR1, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR2, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR4, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR8, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_BCAST15, 0xa>(g, h, c);
+        scan_add_step<DPP_ROW_BCAST31, 0xc>(g, h, c);
+    } else if constexpr (SEGL == 16) {
+        scan_add_step<DPP_ROW_SHR1, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR2, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR4, 0xf>(g, h, c);
+        scan_add_step<DPP_ROW_SHR8, 0xf>(g, h, c);
+    } else {
+        static_assert(SEGL == 4, "segments of 64, 16 or 4 lanes");
+        const uint32_t t = threadIdx.x & 3u;
+        const double g1 = double_of(dpp_u64<DPP_ROW_SHR1, 0xf>(bits_of(g))), h1 = double_of(dpp_u64<DPP_ROW_SHR1, 0xf>(bits_of(h)));
+        const int64_t c1 = static_cast<int64_t>(dpp_u64<DPP_ROW_SHR1, 0xf>(static_cast<uint64_t>(c)));
+        if (t >= 1) {
+            g += g1;
+            h += h1;
+            c += c1;
+        }
+        const double g2 = double_of(dpp_u64<DPP_ROW_SHR2, 0xf>(bits_of(g))), h2 = double_of(dpp_u64<DPP_ROW_SHR2, 0xf>(bits_of(h)));
+        const int64_t c2 = static_cast<int64_t>(dpp_u64<DPP_ROW_SHR2, 0xf>(static_cast<uint64_t>(c)));
+        if (t >= 2) {
+            g += g2;
+            h += h2;
+            c += c2;
+        }
+    }
+}
+template <int SEGL>
+__device__ __forceinline__ double seg_read_f64(double v, uint32_t t) {
+    if constexpr (SEGL == 64) return readlane_f64(v, t);
+    else return __shfl(v, static_cast<int>(t), SEGL);
+}
+template <int SEGL>
+__device__ __forceinline__ int64_t seg_read_i64(int64_t v, uint32_t t) {
+    if constexpr (SEGL == 64) return static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(v), t));
+    else return static_cast<int64_t>(__shfl(static_cast<long long>(v), static_cast<int>(t), SEGL));
+}
+template <int SEGL>
+__device__ __forceinline__ int seg_max_i32(int v) {
+    if constexpr (SEGL == 64) {
+        return wave_max_i32(v);
+    } else {
+#pragma unroll
+        for (int o = SEGL / 2; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, SEGL));
+        return v;
+    }
+}
+template <int SEGL>
+__device__ __forceinline__ int seg_min_i32(int v) {
+    if constexpr (SEGL == 64) {
+        return wave_min_i32(v);
+    } else {
+#pragma unroll
+        for (int o = SEGL / 2; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, SEGL));
+        return v;
+    }
+}
+template <int SEGL>
+__device__ __forceinline__ double seg_max_f64(double v) {  // v is never NaN
+    if constexpr (SEGL == 64) {
+        return wave_max_f64(v);
+    } else {
+#pragma unroll
+        for (int o = SEGL / 2; o > 0; o >>= 1) {
+            const double w = __shfl_xor(v, o, SEGL);
+            v = w > v ? w : v;
+        }
+        return v;
+    }
+}
+
 // scan_numerical for a feature of up to 1024 bins (two-byte bins, an extension): lane l holds bins
 // 16l .. 16l + 15. The same candidates, stops and ties as scan_numerical, in two passes over the lane's bins so that
 // only the units stay in registers: the first finds both directions' stops, the second evaluates the candidates in
@@ -1392,9 +1475,10 @@ __device__ void scan_numerical_wide(const Ctx &c, const SplitCfgDev &cfg, const 
 //   highest b on equal gains. Threshold b - 1.
 // - Forward (missing values go right; two-way features only): visits b = 0 .. top; stops at the lowest such b;
 //   keeps the lowest b on equal gains. Threshold b.
+template <int SEGL = 64>
 __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatDev &m, const int64_t *hist, bool &rf,
                                Grown &rg, bool &ff, Grown &fg) {
-    const int lane = static_cast<int>(threadIdx.x & 63u);
+    const int lane = static_cast<int>(threadIdx.x & static_cast<uint32_t>(SEGL - 1));  // the lane in its segment
     const int64_t *h = hist + 2 * static_cast<size_t>(m.hist_offset);
     const int nb = static_cast<int>(m.num_bins);
     const bool two = scan_two_way(m);
@@ -1439,14 +1523,9 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
     }
     double eg = lg, eh = lh;
     int64_t ec = lc;
-    scan_add_step<DPP_ROW_SHR1, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR2, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR4, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_SHR8, 0xf>(eg, eh, ec);
-    scan_add_step<DPP_ROW_BCAST15, 0xa>(eg, eh, ec);
-    scan_add_step<DPP_ROW_BCAST31, 0xc>(eg, eh, ec);
-    const double tg = readlane_f64(eg, 63), th = readlane_f64(eh, 63);
-    const int64_t tc = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(ec), 63));
+    seg_scan_add<SEGL>(eg, eh, ec);
+    const double tg = seg_read_f64<SEGL>(eg, SEGL - 1), th = seg_read_f64<SEGL>(eh, SEGL - 1);
+    const int64_t tc = seg_read_i64<SEGL>(ec, SEGL - 1);
     eg -= lg;
     eh -= lh;
     ec -= lc;
@@ -1481,7 +1560,7 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
     rf = false;
     ff = false;
     {  // reverse: candidates above the highest stop, the highest b among equal gains
-        const int lo = wave_max_i32(stop_r) + 1;  // >= 0
+        const int lo = seg_max_i32<SEGL>(stop_r) + 1;  // >= 0
         double bg = -__builtin_inf();
         int bb = -1;
 #pragma unroll
@@ -1492,8 +1571,8 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
                 bb = b;
             }
         }
-        const double best = wave_max_f64(bb >= 0 ? bg : -__builtin_inf());
-        const int first = wave_max_i32(bb >= 0 && bg == best ? bb : -1);
+        const double best = seg_max_f64<SEGL>(bb >= 0 ? bg : -__builtin_inf());
+        const int first = seg_max_i32<SEGL>(bb >= 0 && bg == best ? bb : -1);
         if (first >= 0 && best > c.min_gain_shift) {
             const uint32_t owner = static_cast<uint32_t>(first) >> 2;
             const int jj = first & 3;
@@ -1506,16 +1585,16 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
                     oh = rhu[j];
                     oc = rcu[j];
                 }
-            rg.ug = readlane_f64(og, owner);
-            rg.uh = readlane_f64(oh, owner);
-            rg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
+            rg.ug = seg_read_f64<SEGL>(og, owner);
+            rg.uh = seg_read_f64<SEGL>(oh, owner);
+            rg.count = seg_read_i64<SEGL>(oc, owner);
             rg.gain = best;
             rg.bin = static_cast<uint32_t>(first);
             rf = true;
         }
     }
     if (two) {  // forward: candidates below the lowest stop, the lowest b among equal gains
-        const int hi = wave_min_i32(stop_f);
+        const int hi = seg_min_i32<SEGL>(stop_f);
         double bg = -__builtin_inf();
         int bb = -1;
 #pragma unroll
@@ -1526,8 +1605,8 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
                 bb = b;
             }
         }
-        const double best = wave_max_f64(bb >= 0 ? bg : -__builtin_inf());
-        const int first = wave_min_i32(bb >= 0 && bg == best ? bb : 0x7fffffff);
+        const double best = seg_max_f64<SEGL>(bb >= 0 ? bg : -__builtin_inf());
+        const int first = seg_min_i32<SEGL>(bb >= 0 && bg == best ? bb : 0x7fffffff);
         if (first != 0x7fffffff && best > c.min_gain_shift) {
             const uint32_t owner = static_cast<uint32_t>(first) >> 2;
             const int jj = first & 3;
@@ -1540,9 +1619,9 @@ __device__ void scan_numerical(const Ctx &c, const SplitCfgDev &cfg, const FeatD
                     oh = ph[j];
                     oc = pc[j];
                 }
-            fg.ug = readlane_f64(og, owner);
-            fg.uh = readlane_f64(oh, owner);
-            fg.count = static_cast<int64_t>(readlane_u64(static_cast<uint64_t>(oc), owner));
+            fg.ug = seg_read_f64<SEGL>(og, owner);
+            fg.uh = seg_read_f64<SEGL>(oh, owner);
+            fg.count = seg_read_i64<SEGL>(oc, owner);
             fg.gain = best;
             fg.bin = static_cast<uint32_t>(first);
             ff = true;
@@ -1908,7 +1987,8 @@ __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ 
                                                     const uint8_t *__restrict__ evaluate, uint32_t num_features,
                                                     SplitCfgDev cfg, double sg, double sh,
                                                     uint8_t *cat_order /* [feature][256] or null */,
-                                                    const DevScales *dsc /* when set: the scales */) {
+                                                    const DevScales *dsc /* when set: the scales */,
+                                                    const uint8_t *skip = nullptr /* features k_split_scan_seg takes */) {
     if (dsc) {
         sg = dsc->sg;
         sh = dsc->sh;
@@ -1917,10 +1997,34 @@ __global__ __launch_bounds__(256) void k_split_scan(const ScanJob *__restrict__ 
     const ScanJob &job = jobs[blockIdx.y];
     uint32_t f = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (f >= num_features || (feats[f].wide != 0) != WIDE) return;  // the other instantiation's feature
+    if (skip && skip[f]) return;
     Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job.count);
     FeatCand r = scan_feature<WIDE>(c, cfg, feats[f], job.hist, evaluate[f] != 0, cats[threadIdx.x >> 6],
                               cat_order ? cat_order + static_cast<size_t>(f) * 256 : nullptr);
     if ((threadIdx.x & 63) == 0) job.out[f] = r;
+}
+
+// k_split_scan for scan units of several numerical byte features of at most 64 bins (16 or 4 lanes a feature, as
+// k_step_scan_seg): unit u holds unit_feat[u * UNIT_FEATS ...] (-1 padding), unit_segl[u] lanes each. A wave per
+// unit and job. grid: (ceil(units / 4), jobs), 256 threads.
+__global__ __launch_bounds__(256) void k_split_scan_seg(const ScanJob *__restrict__ jobs, const FeatDev *__restrict__ feats,
+                                                        const uint8_t *__restrict__ evaluate, const int32_t *unit_feat,
+                                                        const uint32_t *unit_segl, uint32_t units, SplitCfgDev cfg,
+                                                        double sg, double sh) {
+    const ScanJob &job = jobs[blockIdx.y];
+    const uint32_t u = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (u >= units) return;
+    const uint32_t segl = unit_segl[u];  // 16 or 4, wave-uniform
+    const int32_t f = unit_feat[u * UNIT_FEATS + lane / segl];
+    const FeatDev m = f >= 0 ? feats[f] : FeatDev{};
+    const Ctx c = make_ctx(cfg, sg, sh, job.units_grad, job.units_hess, job.count);
+    Grown rg = {}, fg = {};
+    bool rf = false, ff = false;
+    if (segl == 16u) scan_numerical<16>(c, cfg, m, job.hist, rf, rg, ff, fg);
+    else scan_numerical<4>(c, cfg, m, job.hist, rf, rg, ff, fg);
+    FeatCand r = {};
+    if (f >= 0 && scan_searched(c, m, evaluate[f] != 0)) r = feature_candidate(c, m, rf, rg, ff, fg);
+    if ((lane & (segl - 1u)) == 0 && f >= 0) job.out[f] = r;
 }
 
 // The leaf's SplitInfo (split.rs:631-651 finish) and splittable flags from the per-feature candidates: the
@@ -2228,7 +2332,7 @@ struct GrowState {
     const struct DevScales *dsc;  // when set, the scales are these (made on the device), not sg and sh
     uint32_t target_groups;   // k_step_rows workgroups a step is spread over
     uint32_t ncg;             // column groups of k_step_reduce
-    uint32_t nsg;             // scan groups of k_step_scan (four numerical features each)
+    uint32_t nsg;             // scan units of k_step_scan (a wave per unit and child)
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
     uint32_t pad_;
 };
@@ -3632,8 +3736,11 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
     return s_last != 0;
 }
 
+// A scan unit is one wave's scan of a child: one feature (SEGL 64), or 4 features of at most 64 bins (SEGL 16) or
+// 16 of at most 16 bins (SEGL 4), a segment of lanes each (UNIT_FEATS entries a unit).
 struct ScanStepArgs {
-    const int32_t *scan_feat;   // the numerical features to scan, four a scan group, -1 for padding
+    const int32_t *unit_feat;   // per scan unit, UNIT_FEATS numerical features (segment order), -1 for padding
+    const uint32_t *unit_segl;  // per scan unit, its lanes a feature: 64, 16 or 4
     const uint32_t *cat_feats;  // the categorical features (k_step_cat)
     uint32_t ncat;
     StepPlan *plan;
@@ -3886,19 +3993,20 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
 // both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's; features
 // of two-byte bins are k_step_scan<true>'s, the others k_step_scan<false>'s. grid: any, 256 threads.
 template <bool WIDE>
-__global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) {
+__global__ __launch_bounds__(256, WIDE ? 1 : 4) void k_step_scan(GrowState g, ScanStepArgs a) {
     const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t total = P.total_scan * (2u * CG_COLS);  // scan items count column groups
+    const uint32_t total = P.total_scan * 2u;  // scan items count units: a wave per unit and child
     for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
-        const uint32_t gi = item / (2u * CG_COLS), sub = item % (2u * CG_COLS);
+        const uint32_t gi = item >> 1, child = item & 1u;
         const uint32_t j = job_of(P.scan_base, P.njobs, gi);
         const JobPlan &J = P.jobs[j];
-        const uint32_t scol = sub % CG_COLS, child = sub / CG_COLS;
-        const int32_t sf = a.scan_feat[(gi - J.scan_base) * CG_COLS + scol];
+        const uint32_t u = gi - J.scan_base;
+        if (a.unit_segl[u] != 64u) continue;  // k_step_scan_seg's
+        const int32_t sf = a.unit_feat[u * UNIT_FEATS];
         if (sf < 0) continue;
         const FeatDev sm = g.feats[sf];
-        if (sm.kind == 2 || (sm.wide != 0) != WIDE) continue;
+        if (sm.kind == 2 || (sm.wide != 0) != WIDE) continue;  // the other instantiation's, or k_step_cat's
         const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
         const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
         const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
@@ -3912,6 +4020,37 @@ __global__ __launch_bounds__(256) void k_step_scan(GrowState g, ScanStepArgs a) 
             r = feature_candidate(c, sm, rf, rg, ff, fg);
         }
         if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
+    }
+}
+
+// The scan units of several byte features a wave (k_step_scan's items of 16 or 4 lanes a feature): every segment
+// scans (its shuffles take the whole wave), a padding or unsearched one keeping nothing. Its own kernel, so that the
+// wave-wide scan keeps its registers (and occupancy). grid: any, 256 threads.
+__global__ __launch_bounds__(256) void k_step_scan_seg(GrowState g, ScanStepArgs a) {
+    const StepPlan &P = *a.plan;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t total = P.total_scan * 2u;
+    for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
+        const uint32_t gi = item >> 1, child = item & 1u;
+        const uint32_t j = job_of(P.scan_base, P.njobs, gi);
+        const JobPlan &J = P.jobs[j];
+        const uint32_t u = gi - J.scan_base;
+        const uint32_t segl = a.unit_segl[u];  // wave-uniform
+        if (segl == 64u) continue;  // k_step_scan's
+        const uint32_t t = lane & (segl - 1u);
+        const int32_t sf = a.unit_feat[u * UNIT_FEATS + lane / segl];
+        const FeatDev sm = sf >= 0 ? g.feats[sf] : FeatDev{};
+        const bool sev = sf >= 0 && g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
+        const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
+        const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
+        const Ctx c = make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[child], J.child_uh[child], cnt);
+        Grown rg = {}, fg = {};
+        bool rf = false, ff = false;
+        if (segl == 16u) scan_numerical<16>(c, g.cfg, sm, hist, rf, rg, ff, fg);
+        else scan_numerical<4>(c, g.cfg, sm, hist, rf, rg, ff, fg);
+        FeatCand r = {};
+        if (sf >= 0 && scan_searched(c, sm, sev)) r = feature_candidate(c, sm, rf, rg, ff, fg);
+        if (t == 0 && sf >= 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
     }
 }
 
