@@ -383,6 +383,7 @@ struct Context {
     uint32_t ncg = 0;  // column groups of k_step_reduce
     uint32_t nsg = 0;  // scan units of k_step_scan
     bool has_seg_units = false;  // some units scan several features (k_step_scan_seg)
+    uint32_t nseg_units = 0;     // those units, first in the unit list
     bool has_narrow64 = false;   // some units scan one byte feature (k_step_scan<false>)
     uint64_t step_partial_pairs = 0;
     uint32_t part_len = 0;
@@ -964,6 +965,8 @@ struct Context {
             ncg = static_cast<uint32_t>(cg.size());
             nsg = static_cast<uint32_t>(usegl.size());
             has_seg_units = segmented;
+            nseg_units = 0;
+            while (nseg_units < usegl.size() && usegl[nseg_units] != 64) ++nseg_units;
             has_narrow64 = false;
             for (size_t u = 0; u < usegl.size(); ++u)
                 if (usegl[u] == 64 && group_bits[feats[ufeat[u * UNIT_FEATS]].group] != 16) has_narrow64 = true;
@@ -2040,7 +2043,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                 ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity, slab_slot_flat.p};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
                 launch_check("k_step_reduce");
-                ScanStepArgs sca{unit_feat.p, unit_segl.p, cat_feats.p, ncat, d_plans.p + parity};
+                ScanStepArgs sca{unit_feat.p, unit_segl.p, nseg_units, cat_feats.p, ncat, d_plans.p + parity};
                 if (has_narrow64) k_step_scan<false><<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 if (has_seg_units) k_step_scan_seg<<<scan_blocks(), 256, 0, stream>>>(g, sca);
                 if (has_wide) k_step_scan<true><<<scan_blocks(), 256, 0, stream>>>(g, sca);

@@ -3741,6 +3741,7 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t target) 
 struct ScanStepArgs {
     const int32_t *unit_feat;   // per scan unit, UNIT_FEATS numerical features (segment order), -1 for padding
     const uint32_t *unit_segl;  // per scan unit, its lanes a feature: 64, 16 or 4
+    uint32_t nseg;              // the units of several features come first
     const uint32_t *cat_feats;  // the categorical features (k_step_cat)
     uint32_t ncat;
     StepPlan *plan;
@@ -3897,27 +3898,26 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         // the parent's bins are loaded with the partials (the writes below need them); every partial is first read
         // as packed, and a {g, h} pair partial (a workgroup that flushed) is read again in its own layout
         const uint32_t seg = bin >> cg.seg_shift, vb = bin & ((1u << cg.seg_shift) - 1u);
-        // the flat bin (x2) of each of the four columns' slot, or -1
-        int64_t fo[4];
+        // the flat bin + 1 of each of the four columns' slot (0: none)
+        uint32_t fl[4];
         if (cg.dense) {
             const uint4 t = *reinterpret_cast<const uint4 *>(a.slot_flat + cg.slot_base + static_cast<size_t>(bin) * cg.width + cg.c0);
-            const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) fo[c] = tv[c] ? 2 * (static_cast<int64_t>(tv[c]) - 1) : -1;
+            fl[0] = t.x;
+            fl[1] = t.y;
+            fl[2] = t.z;
+            fl[3] = t.w;
         } else {
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                fo[c] = vb < cg.bins[seg][c]
-                            ? 2 * (static_cast<int64_t>(cg.offset[seg][c]) + static_cast<int64_t>(vb) * cg.stride[c])
-                            : -1;
+            for (int c = 0; c < 4; ++c) fl[c] = vb < cg.bins[seg][c] ? cg.offset[seg][c] + vb * cg.stride[c] + 1u : 0u;
         }
         int64_t pg[4] = {0, 0, 0, 0}, ph[4] = {0, 0, 0, 0};
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (fo[c] >= 0) {
-                    pg[c] = parent[fo[c]];
-                    ph[c] = parent[fo[c] + 1];
+                if (fl[c]) {
+                    const size_t o = 2 * static_cast<size_t>(fl[c] - 1u);
+                    pg[c] = parent[o];
+                    ph[c] = parent[o + 1];
                 }
             }
         }
@@ -3977,11 +3977,12 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         if (q == 0) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (fo[c] >= 0) {
-                    built[fo[c]] = sg[c];
-                    built[fo[c] + 1] = sh[c];
-                    parent[fo[c]] = pg[c] - sg[c];
-                    parent[fo[c] + 1] = ph[c] - sh[c];
+                if (fl[c]) {
+                    const size_t o = 2 * static_cast<size_t>(fl[c] - 1u);
+                    built[o] = sg[c];
+                    built[o + 1] = sh[c];
+                    parent[o] = pg[c] - sg[c];
+                    parent[o + 1] = ph[c] - sh[c];
                 }
             }
         }
@@ -4002,7 +4003,7 @@ __global__ __launch_bounds__(256, WIDE ? 1 : 4) void k_step_scan(GrowState g, Sc
         const uint32_t j = job_of(P.scan_base, P.njobs, gi);
         const JobPlan &J = P.jobs[j];
         const uint32_t u = gi - J.scan_base;
-        if (a.unit_segl[u] != 64u) continue;  // k_step_scan_seg's
+        if (u < a.nseg) continue;  // k_step_scan_seg's
         const int32_t sf = a.unit_feat[u * UNIT_FEATS];
         if (sf < 0) continue;
         const FeatDev sm = g.feats[sf];
@@ -4035,8 +4036,8 @@ __global__ __launch_bounds__(256) void k_step_scan_seg(GrowState g, ScanStepArgs
         const uint32_t j = job_of(P.scan_base, P.njobs, gi);
         const JobPlan &J = P.jobs[j];
         const uint32_t u = gi - J.scan_base;
-        const uint32_t segl = a.unit_segl[u];  // wave-uniform
-        if (segl == 64u) continue;  // k_step_scan's
+        if (u >= a.nseg) continue;  // k_step_scan's
+        const uint32_t segl = a.unit_segl[u];  // 16 or 4, wave-uniform
         const uint32_t t = lane & (segl - 1u);
         const int32_t sf = a.unit_feat[u * UNIT_FEATS + lane / segl];
         const FeatDev sm = sf >= 0 ? g.feats[sf] : FeatDev{};
