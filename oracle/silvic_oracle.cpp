@@ -345,7 +345,10 @@ struct SigmoidTable {
     double get(double delta) const {
         if (delta <= min_input) return values[0];
         if (delta >= max_input) return values[RANK_SIGMOID_BINS - 1];
-        return values[std::min(static_cast<size_t>((delta - min_input) * idx_factor), RANK_SIGMOID_BINS - 1)];
+        // Rust's `as usize` saturates: NaN and negatives give 0, anything at or past the last bin the last
+        const double x = (delta - min_input) * idx_factor;
+        const double last = static_cast<double>(RANK_SIGMOID_BINS - 1);
+        return values[x >= last ? RANK_SIGMOID_BINS - 1 : (x > 0.0 ? static_cast<size_t>(x) : 0)];
     }
 };
 

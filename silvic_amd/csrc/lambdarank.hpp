@@ -54,35 +54,55 @@ SRANK_HD inline uint32_t rank_key(float score) {
     return ~ascending;
 }
 
-// The pair probability from LightGBM's sigmoid table (lambdarank.rs:96-116): the clamped ends, else the bin of
-// (delta - min_input) * idx_factor. Shared by the host and the device, so both take the same f64 operations.
-SRANK_HD inline double table_probability(const double *table, double min_input, double max_input, double idx_factor,
-                                         double delta) {
-    if (delta <= min_input) return table[0];
-    if (delta >= max_input) return table[SIGMOID_BINS - 1];
-    const uint64_t at = static_cast<uint64_t>((delta - min_input) * idx_factor);
-    return table[at < SIGMOID_BINS - 1 ? at : SIGMOID_BINS - 1];
+// The bin of LightGBM's sigmoid table a score difference takes (lambdarank.rs:96-116): the clamped ends, else the bin
+// of (delta - min_input) * idx_factor truncated, at most the last. The reference's cast saturates: a product at or
+// above the last bin takes the last, a NaN or negative one bin 0; in between the truncation fits 32 bits. Shared by
+// the host and the device, so both take the same f64 operations.
+SRANK_HD inline uint32_t table_bin(double min_input, double max_input, double idx_factor, double delta) {
+    constexpr uint32_t last = static_cast<uint32_t>(SIGMOID_BINS - 1);
+    if (delta <= min_input) return 0;
+    if (delta >= max_input) return last;
+    const double x = (delta - min_input) * idx_factor;
+    return x >= static_cast<double>(last) ? last : (x > 0.0 ? static_cast<uint32_t>(x) : 0u);
 }
 
 // One pair (i above j in the ranking, different labels) as lambdarank.rs:355-400 adds it: the sign, the lambda term
-// p_lambda and the hessian term. Shared by the host and the device.
+// p_lambda and the hessian term. In two parts around the table read, so the device can have the reads of a row in
+// flight while it adds up the row before; the host takes both parts at once (pair_term). Shared by the host and the
+// device.
 struct PairTerm {
     double sign, p_lambda, p_hessian;
 };
+struct PairPrep {
+    double sign, delta_ndcg;
+    uint32_t bin;  // of the sigmoid table
+};
+SRANK_HD inline PairPrep pair_prep(double si, float li, double gi, double di, double sj, float lj, double gj, double dj,
+                                   double inv_max_dcg, bool by_distance, double min_input, double max_input,
+                                   double idx_factor) {
+    PairPrep q;
+    q.sign = li > lj ? 1.0 : -1.0;
+    const double delta_score = q.sign * (si - sj);
+    const double dcg_gap = q.sign * (gi - gj);
+    const double paired_discount = fabs(di - dj);
+    q.delta_ndcg = dcg_gap * paired_discount * inv_max_dcg;
+    if (by_distance) q.delta_ndcg /= DISTANCE_EPSILON + fabs(delta_score);
+    q.bin = table_bin(min_input, max_input, idx_factor, delta_score);
+    return q;
+}
+SRANK_HD inline PairTerm pair_finish(const PairPrep &q, double p, double sigmoid, double sigmoid2) {
+    PairTerm t;
+    t.sign = q.sign;
+    t.p_lambda = p * (-sigmoid * q.delta_ndcg);
+    t.p_hessian = p * (1.0 - p) * (sigmoid2 * q.delta_ndcg);
+    return t;
+}
 SRANK_HD inline PairTerm pair_term(double si, float li, double gi, double di, double sj, float lj, double gj, double dj,
                                    double inv_max_dcg, bool by_distance, double sigmoid, double sigmoid2,
                                    const double *table, double min_input, double max_input, double idx_factor) {
-    PairTerm t;
-    t.sign = li > lj ? 1.0 : -1.0;
-    const double delta_score = t.sign * (si - sj);
-    const double dcg_gap = t.sign * (gi - gj);
-    const double paired_discount = fabs(di - dj);
-    double delta_ndcg = dcg_gap * paired_discount * inv_max_dcg;
-    if (by_distance) delta_ndcg /= DISTANCE_EPSILON + fabs(delta_score);
-    const double p = table_probability(table, min_input, max_input, idx_factor, delta_score);
-    t.p_lambda = p * (-sigmoid * delta_ndcg);
-    t.p_hessian = p * (1.0 - p) * (sigmoid2 * delta_ndcg);
-    return t;
+    const PairPrep q = pair_prep(si, li, gi, di, sj, lj, gj, dj, inv_max_dcg, by_distance, min_input, max_input,
+                                 idx_factor);
+    return pair_finish(q, table[q.bin], sigmoid, sigmoid2);
 }
 
 class Ranker {

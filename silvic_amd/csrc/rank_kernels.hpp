@@ -2,13 +2,13 @@
 // which follows crates/silvic-core/src/objective/lambdarank.rs:190-420).
 //
 // One wave per query (k_rank_pairs): the query's rows are ranked by score (descending, ties by row) with a bitonic
-// sort in LDS, then every row i above the truncation level takes its pairs (i, j), j > i, in order. The lanes compute
-// the pair terms of row i for all j at once (the arithmetic is srocm_rank::pair_term, shared with the host), and lane
-// j adds its own term to row j's sums, so each row's "as j" sums are taken over i in increasing order, as the host
-// takes them. Row i's own sums and the query's lambda sum are running f64 sums in pair order; three lanes take them
-// (lambda, hessian, lambda sum), each adding the terms of row i in j order, so every sum has the host's operation
-// sequence. A pair the host skips (equal labels) contributes +0.0, which leaves a running sum unchanged: such a sum
-// starts at +0.0 and never becomes -0.0 (x + (-x) rounds to +0.0), so x + 0.0 == x bit for bit.
+// sort in LDS, then every row i above the truncation level takes its pairs (i, j), j > i, in order. A ballot over the
+// ranks j marks the pairs the host takes (below the first -inf score, a different label); the marked lanes compute
+// their pair terms (the arithmetic is srocm_rank's, shared with the host), and lane j adds its own term to rank j's
+// sums, so each rank's "as j" sums are taken over i in increasing order, as the host takes them. Row i's own sums and
+// the query's lambda sum are running f64 sums in pair order: the marked terms are listed in LDS in j order, and three
+// lanes (lambda, hessian, lambda sum) each add up their list, so every sum has the host's operation sequence. The
+// table reads of row i + 1 are issued before row i is added up, so their latency hides behind that serial sum.
 //
 // The unscaled sums go to per-row f64 buffers and the lambda sum to a per-query buffer. The normalization factor
 // log2(1 + s) / s takes the host's log2 (one call per query, on the host, between k_rank_pairs and k_rank_scale), so
@@ -34,27 +34,55 @@ struct RankArgs {
     double *qsum;                  // per query: the lambda sum
 };
 
-// A query of at most NMAX rows on one wave (64 threads). NMAX: a power of two, 64..512.
+// The value of a per-rank register array at rank k (lane k % 64, slot k / 64), on every lane; k is the same on all.
+// Every slot is read from the lane, then the slot chosen, so the array is never indexed by a variable (which would
+// put it in scratch memory).
+template <int M>
+__device__ __forceinline__ double rank_value(const double (&v)[M], uint32_t k) {
+    if (k < 64) return readlane_f64(v[0], k);  // the truncation level's rows, most often
+    double x = readlane_f64(v[0], k & 63u);
+#pragma unroll
+    for (int m = 1; m < M; ++m) {
+        const double y = readlane_f64(v[m], k & 63u);
+        x = static_cast<uint32_t>(m) == (k >> 6) ? y : x;
+    }
+    return x;
+}
+template <int M>
+__device__ __forceinline__ float rank_value(const float (&v)[M], uint32_t k) {
+    if (k < 64) return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0]), k));
+    float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0]), k & 63u));
+#pragma unroll
+    for (int m = 1; m < M; ++m) {
+        const float y = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[m]), k & 63u));
+        x = static_cast<uint32_t>(m) == (k >> 6) ? y : x;
+    }
+    return x;
+}
+
+// A query of at most NMAX rows on one wave (64 threads). NMAX: a power of two, 64..512. Lane l keeps ranks l + 64 m
+// in registers: the row, score, label, gain and discount, and the rank's lambda and hessian sums.
 template <int NMAX>
 __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
     constexpr int M = NMAX / 64;
-    __shared__ uint64_t keys[NMAX];
-    __shared__ double s_score[NMAX], s_gain[NMAX], s_disc[NMAX];
-    __shared__ float s_lab[NMAX];
-    __shared__ double terms[NMAX][3];  // row i's pair with rank j: lambda term, hessian term, -2 * p_lambda
+    constexpr uint32_t STRIDE = NMAX + 4;  // the three term lists 32 bytes apart in the banks
+    __shared__ __align__(16) double lds[3 * STRIDE];  // the sort's keys, then row i's terms in j order
+    uint64_t *keys = reinterpret_cast<uint64_t *>(lds);
     const uint32_t q = blockIdx.x, lane = threadIdx.x;
     const uint32_t b = a.bounds[q], n = a.bounds[q + 1] - b;
     if (n == 0) {
         if (lane == 0) a.qsum[q] = 0.0;
         return;
     }
-    // rank by score, descending, ties by row (lambdarank.rs:142-170): ascending (key, row)
-    for (uint32_t k = lane; k < NMAX; k += 64)
+    // rank by score, descending, ties by row (lambdarank.rs:142-170): ascending (key, row), over the power of two
+    // at or above n (at least 2), the keys past n sorting last
+    const uint32_t span = n <= 2 ? 2u : 1u << (32 - __builtin_clz(n - 1));
+    for (uint32_t k = lane; k < span; k += 64)
         keys[k] = k < n ? (static_cast<uint64_t>(srocm_rank::rank_key(a.scores[b + k])) << 32) | k : ~0ull;
     __syncthreads();
-    for (uint32_t size = 2; size <= NMAX; size <<= 1) {
+    for (uint32_t size = 2; size <= span; size <<= 1) {
         for (uint32_t half = size >> 1; half > 0; half >>= 1) {
-            for (uint32_t t = lane; t < NMAX; t += 64) {
+            for (uint32_t t = lane; t < span; t += 64) {
                 const uint32_t o = t ^ half;
                 if (o > t) {
                     const uint64_t x = keys[t], y = keys[o];
@@ -67,97 +95,131 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
             __syncthreads();
         }
     }
+    uint32_t row[M];
+    double sc[M], gn[M], dc[M];
+    float lb[M];
     uint32_t first_inf = n;  // the first rank with a -inf score: pairs stop there (lambdarank.rs:333-340)
-    for (uint32_t k = lane; k < n; k += 64) {
-        const uint32_t r = static_cast<uint32_t>(keys[k] & 0xffffffffu);
-        const double s = static_cast<double>(a.scores[b + r]);
-        const float l = a.label[b + r];
-        s_score[k] = s;
-        s_lab[k] = l;
-        s_gain[k] = a.label_gain[static_cast<uint32_t>(l)];
-        s_disc[k] = a.discount[k];
-        if (s == -__builtin_inf() && k < first_inf) first_inf = k;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const uint32_t k = lane + 64u * m;
+        row[m] = 0;
+        sc[m] = gn[m] = dc[m] = 0.0;
+        lb[m] = 0.0f;
+        if (k < n) {
+            const uint32_t r = static_cast<uint32_t>(keys[k] & 0xffffffffu);
+            row[m] = r;
+            sc[m] = static_cast<double>(a.scores[b + r]);
+            lb[m] = a.label[b + r];
+            gn[m] = a.label_gain[static_cast<uint32_t>(lb[m])];
+            dc[m] = a.discount[k];
+            if (sc[m] == -__builtin_inf() && k < first_inf) first_inf = k;
+        }
     }
     for (int o = 32; o > 0; o >>= 1) first_inf = min(first_inf, static_cast<uint32_t>(__shfl_xor(static_cast<int>(first_inf), o)));
-    __syncthreads();
+    __syncthreads();  // the keys are read: the LDS holds the terms from here on
     const uint32_t valid = first_inf;
     uint32_t worst = n - 1;
-    if (worst > 0 && s_score[worst] == -__builtin_inf()) --worst;
-    const bool by_distance = a.norm && s_score[0] != s_score[worst];
+    if (worst > 0 && rank_value(sc, worst) == -__builtin_inf()) --worst;
+    const bool by_distance = a.norm && rank_value(sc, 0) != rank_value(sc, worst);
     const uint32_t rows_i = min(a.truncation, valid > 0 ? valid - 1 : 0u);
     const double inv_max_dcg = a.inv_max_dcg[q];
-    double lam[M], hes[M];  // ranks lane + 64 m
+    double lam[M], hes[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) lam[m] = hes[m] = 0.0;
     double acc = 0.0;  // lane 2: the query's lambda sum
-    for (uint32_t i = 0; i < rows_i; ++i) {
-        const double si = s_score[i], gi = s_gain[i], di = s_disc[i];
-        const float li = s_lab[i];
+
+    // Row i's pairs the host takes (j > i, below the first -inf score, a different label): the ballot of each slot,
+    // and each taken lane's arithmetic up to the table read. Step i starts row i (its table reads stay in flight) and
+    // adds up row i - 1, whose terms step i - 1 listed.
+    uint64_t take[M];
+    double sign[M], ndcg[M], prob[M];
+    uint32_t count = 0;  // row i - 1's taken pairs
+    for (uint32_t i = 0; i <= rows_i; ++i) {
+        double own_lam = 0.0, own_hes = 0.0;
+        if (i > 0) {
+            // row i - 1's terms: lane j adds its own to rank j's sums and lists it at its place among the row's
+            // taken pairs
+            count = 0;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const uint32_t j = lane + 64u * m;
-            double tl = 0.0, th = 0.0, tp = 0.0;
-            if (j > i && j < valid && s_lab[j] != li) {
-                const srocm_rank::PairTerm t =
-                    srocm_rank::pair_term(si, li, gi, di, s_score[j], s_lab[j], s_gain[j], s_disc[j], inv_max_dcg,
-                                          by_distance, a.sigmoid, a.sigmoid2, a.table, a.min_input, a.max_input,
-                                          a.idx_factor);
-                tl = t.sign * t.p_lambda;
-                th = t.p_hessian;
-                tp = -(2.0 * t.p_lambda);
-                lam[m] -= tl;
-                hes[m] += th;
+            for (int m = 0; m < M; ++m) {
+                if ((take[m] >> lane) & 1ull) {
+                    srocm_rank::PairPrep pp;
+                    pp.sign = sign[m];
+                    pp.delta_ndcg = ndcg[m];
+                    const srocm_rank::PairTerm t = srocm_rank::pair_finish(pp, prob[m], a.sigmoid, a.sigmoid2);
+                    const double tl = t.sign * t.p_lambda, th = t.p_hessian;
+                    lam[m] -= tl;
+                    hes[m] += th;
+                    const uint32_t at = count + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(take[m] >> 32),
+                                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(take[m]), 0u));
+                    lds[at] = tl;
+                    lds[STRIDE + at] = th;
+                    lds[2 * STRIDE + at] = -(2.0 * t.p_lambda);
+                }
+                count += static_cast<uint32_t>(__builtin_popcountll(take[m]));
             }
-            if (j < NMAX) {
-                terms[j][0] = tl;
-                terms[j][1] = th;
-                terms[j][2] = tp;
+            __syncthreads();
+            own_lam = rank_value(lam, i - 1);
+            own_hes = rank_value(hes, i - 1);
+        }
+        if (i < rows_i) {
+            const double si = rank_value(sc, i), gi = rank_value(gn, i), di = rank_value(dc, i);
+            const float li = rank_value(lb, i);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint32_t j = lane + 64u * m;
+                take[m] = 64u * m < valid ? __ballot(j > i && j < valid && lb[m] != li) : 0ull;
+                if ((take[m] >> lane) & 1ull) {
+                    const srocm_rank::PairPrep pp = srocm_rank::pair_prep(si, li, gi, di, sc[m], lb[m], gn[m], dc[m],
+                                                                          inv_max_dcg, by_distance, a.min_input,
+                                                                          a.max_input, a.idx_factor);
+                    sign[m] = pp.sign;
+                    ndcg[m] = pp.delta_ndcg;
+                    prob[m] = a.table[pp.bin];
+                }
             }
         }
-        __syncthreads();
-        // row i's own sums (from its "as j" sums so far) and the query's lambda sum, in j order on lanes 0-2
-        const uint32_t owner = i & 63u, mi = i >> 6;
-        double li_lam = 0.0, li_hes = 0.0;
+        if (i > 0 && count > 0) {
+            // row i - 1's own sums (from its sums as a lower rank) and the query's lambda sum, the terms in j order,
+            // on lanes 0-2
+            double s = lane == 0 ? own_lam : (lane == 1 ? own_hes : acc);
+            if (lane < 3) {
+                const double *src = lds + lane * STRIDE;
+                uint32_t k = 0;
+                for (; k + 8 <= count; k += 8) {
+                    const double2 x0 = *reinterpret_cast<const double2 *>(src + k);
+                    const double2 x1 = *reinterpret_cast<const double2 *>(src + k + 2);
+                    const double2 x2 = *reinterpret_cast<const double2 *>(src + k + 4);
+                    const double2 x3 = *reinterpret_cast<const double2 *>(src + k + 6);
+                    s += x0.x;
+                    s += x0.y;
+                    s += x1.x;
+                    s += x1.y;
+                    s += x2.x;
+                    s += x2.y;
+                    s += x3.x;
+                    s += x3.y;
+                }
+                for (; k < count; ++k) s += src[k];
+                if (lane == 2) acc = s;
+            }
+            const double new_lam = readlane_f64(s, 0), new_hes = readlane_f64(s, 1);
+            const uint32_t r = i - 1;
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-            if (static_cast<uint32_t>(m) == mi) {
-                li_lam = lam[m];
-                li_hes = hes[m];
-            }
-        li_lam = __shfl(li_lam, static_cast<int>(owner));
-        li_hes = __shfl(li_hes, static_cast<int>(owner));
-        if (lane < 3) {
-            double s = lane == 0 ? li_lam : (lane == 1 ? li_hes : acc);
-            uint32_t j = i + 1;
-            for (; j + 4 <= valid; j += 4) {
-                const double t0 = terms[j][lane], t1 = terms[j + 1][lane], t2 = terms[j + 2][lane], t3 = terms[j + 3][lane];
-                s += t0;
-                s += t1;
-                s += t2;
-                s += t3;
-            }
-            for (; j < valid; ++j) s += terms[j][lane];
-            if (lane == 0) li_lam = s;
-            else if (lane == 1) li_hes = s;
-            else acc = s;
+            for (int m = 0; m < M; ++m)
+                if (static_cast<uint32_t>(m) == (r >> 6) && lane == (r & 63u)) {
+                    lam[m] = new_lam;
+                    hes[m] = new_hes;
+                }
         }
-        li_lam = __shfl(li_lam, 0);
-        li_hes = __shfl(li_hes, 1);
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-            if (static_cast<uint32_t>(m) == mi && lane == owner) {
-                lam[m] = li_lam;
-                hes[m] = li_hes;
-            }
-        __syncthreads();  // the terms are rewritten for the next row
+        if (i > 0) __syncthreads();  // the term lists are rewritten for the next row
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         const uint32_t k = lane + 64u * m;
         if (k < n) {
-            const uint32_t r = static_cast<uint32_t>(keys[k] & 0xffffffffu);
-            a.lam[b + r] = lam[m];
-            a.hes[b + r] = hes[m];
+            a.lam[b + row[m]] = lam[m];
+            a.hes[b + row[m]] = hes[m];
         }
     }
     if (lane == 2) a.qsum[q] = acc;

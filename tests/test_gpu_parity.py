@@ -539,19 +539,28 @@ def test_lambdarank_gradients_match_the_oracle():
 
 
 # The device path (k_rank_pairs: every query of at most 512 rows) under other settings: no normalization, a short
-# truncation, row weights, sigmoid 2; and the host path (a query of more than 512 rows sends every query to the
-# host), both against the oracle bit for bit.
-@pytest.mark.parametrize("case", ["no norm, truncation 5", "weights, sigmoid 2", "one query of 700 rows"])
+# truncation, row weights, sigmoid 2, labels drawn uniformly (most pairs taken, where the synthetic queries take
+# few), a query of 500 rows (the 512-row kernel); and the host path (a query of more than 512 rows sends every query
+# to the host), both against the oracle bit for bit.
+@pytest.mark.parametrize("case", ["no norm, truncation 5", "weights, sigmoid 2", "uniform labels",
+                                  "one query of 500 rows, uniform labels", "one query of 700 rows"])
 def test_lambdarank_gradient_paths_match_the_oracle(case):
     say("lambdarank gradients", case)
     data = silvic_amd.synthetic(3, rows=60_000, seed=9)
     kw = {}
+    if "uniform labels" in case:
+        data.label = np.random.default_rng(4).integers(0, 5, data.num_rows).astype(np.float32)
     if case.startswith("no norm"):
         kw = dict(lambdarank_norm=False, lambdarank_truncation_level=5)
     elif case.startswith("weights"):
         data.weight = np.random.default_rng(3).uniform(0.5, 2.0, data.num_rows).astype(np.float32)
         kw = dict(sigmoid=2.0)
-    else:
+    elif case.startswith("one query of 500"):
+        qb = data.query_boundaries
+        k = int(np.searchsorted(qb, 500))
+        data.query_boundaries = np.concatenate([[0, 500], qb[k + 1:]]).astype(qb.dtype)
+        assert 256 < np.diff(data.query_boundaries).max() <= 512
+    elif case.startswith("one query of 700"):
         qb = data.query_boundaries
         k = int(np.searchsorted(qb, 700))
         data.query_boundaries = np.concatenate([[0], qb[k:]]).astype(qb.dtype)  # rows 0..qb[k] become one query
