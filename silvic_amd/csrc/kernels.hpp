@@ -2191,6 +2191,7 @@ __device__ __forceinline__ uint32_t wave_total(uint32_t v) { return __shfl(wave_
 
 constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
 constexpr uint32_t SPEC_FLOOR = 4;         // speculative expansions a step may add whatever the budget
+constexpr uint32_t SPEC_FEW = 8;           // at most this many: picked by repeated wave maxima (top_few)
 constexpr uint32_t GROW_MAX_LEAVES = 2048;  // num_leaves of a device-grown tree at most
 // Speculative leaves of a tree of num_leaves: 4 per leaf up to 512 leaves, then 2 per further leaf (the expansions
 // a tree keeps need 2 per leaf; the rest is the room for speculating ahead, which advance keeps within it).
@@ -2831,6 +2832,40 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
 // candidates that still match the prefix found so far, the bucket where the count from the top reaches what is
 // left to take, and the candidates above it taken. Every key is distinct, so after at most 8 rounds the prefix
 // is a whole key. Block-wide; s.crank holds the counts.
+// The `spec` highest candidate keys for a few expansions (spec <= SPEC_FEW), on one wave: `spec` rounds of a wave
+// maximum over the keys not yet taken, each lane holding candidates lane, lane + 64, ... (at most 64 of them, a bit
+// each in `taken`). The keys are distinct (they end in the leaf), so round r finds the key ranked r: jobs 1 .. spec in
+// descending key order, as the ranking orders them.
+template <typename S>
+__device__ __forceinline__ void top_few(S &s, uint32_t ncand, uint32_t spec) {
+    static_assert(S::CAND <= 64u * 64u, "a lane's candidates fit the taken mask");
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t taken = 0;
+    for (uint32_t r = 0; r < spec; ++r) {
+        uint64_t best = 0;
+        uint32_t at = 0;
+        uint32_t q = 0;
+        for (uint32_t i = lane; i < ncand; i += 64u, ++q) {
+            const uint64_t k = s.ckey[i];
+            if (!((taken >> q) & 1ull) && k > best) {
+                best = k;
+                at = i;
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t ob = __shfl_xor(best, o);
+            const uint32_t oa = static_cast<uint32_t>(__shfl_xor(static_cast<int>(at), o));
+            if (ob > best) {
+                best = ob;
+                at = oa;
+            }
+        }
+        // every candidate key is nonzero (a positive gain's bits), so the winner is a real candidate
+        if ((at & 63u) == lane) taken |= 1ull << (at >> 6);
+        if (lane == 0) s.job_t[1 + r] = s.cand[at];
+    }
+}
+
 template <uint32_t MAXL>
 __device__ void select_top(AdvShared<MAXL> &s, uint32_t ncand, uint32_t spec) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, nt = blockDim.x;
@@ -3016,7 +3051,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     // expansion is the one its leaf gets when the replay reaches it), only the work done ahead. Up to 512 candidates,
     // each one's rank (keys above its own) is summed over `nsl` slices of the others, one thread each; beyond that
     // (trees of thousands of leaves), a radix selection finds the spec-th key in linear passes.
-    if (ncand <= 512u) {
+    if (spec <= SPEC_FEW) {
+        if (tid < 64) top_few(s, ncand, spec);
+    } else if (ncand <= 512u) {
         const uint32_t nsl = ncand && ncand < nt ? nt / ncand : 1u;
         for (uint32_t w = tid; w < ncand * nsl; w += nt) {
             const uint32_t i = w % ncand, sl = w / ncand;
@@ -3873,6 +3910,27 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
 // of the parent's (learner.rs:356-371). Work items (job, column group, bin range) in a grid-stride loop: a thread
 // adds one stripe of the workgroups' partials of one bin of the group's four columns, reading each partial in its
 // own format (packed: one 16-byte load; {g, h} pairs: two), and the stripes meet in LDS. grid: any, 256 threads.
+// One child's candidate of numerical feature sf in job j (split.rs:584-620), on one wave: the feature scanned in both
+// directions over the child's histogram (the built one, or the sibling the reduce formed in the parent's slot).
+template <bool WIDE>
+__device__ __forceinline__ void scan_child(const GrowState &g, const JobPlan &J, uint32_t j, int32_t sf, const FeatDev &sm,
+                                           uint32_t child) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
+    const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
+    const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
+    const Ctx c = make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[child], J.child_uh[child], cnt);
+    FeatCand r = {};
+    if (scan_searched(c, sm, sev)) {
+        Grown rg = {}, fg = {};
+        bool rf, ff;
+        if constexpr (WIDE) scan_numerical_wide(c, g.cfg, sm, hist, rf, rg, ff, fg);
+        else scan_numerical(c, g.cfg, sm, hist, rf, rg, ff, fg);
+        r = feature_candidate(c, sm, rf, rg, ff, fg);
+    }
+    if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
+}
+
 __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs a) {
     __shared__ int64_t red[8][256];  // the stripes' sums, [value][thread]: conflict-free
     const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
@@ -3990,13 +4048,12 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
     }
 }
 
-// Scan items (job, column, child), a wave each in a grid-stride loop: the column's numerical feature scanned in
-// both directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's; features
-// of two-byte bins are k_step_scan<true>'s, the others k_step_scan<false>'s. grid: any, 256 threads.
+// Scan items (job, unit, child), a wave each in a grid-stride loop: the unit's numerical feature scanned in both
+// directions (split.rs:584-620) and its candidate written. Categorical features are k_step_cat's; features of
+// two-byte bins are k_step_scan<true>'s, the others k_step_scan<false>'s. grid: any, 256 threads.
 template <bool WIDE>
 __global__ __launch_bounds__(256, WIDE ? 1 : 4) void k_step_scan(GrowState g, ScanStepArgs a) {
     const StepPlan &P = *a.plan;  // empty once the tree is done (k_step_select)
-    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t total = P.total_scan * 2u;  // scan items count units: a wave per unit and child
     for (uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); item < total; item += gridDim.x * 4u) {
         const uint32_t gi = item >> 1, child = item & 1u;
@@ -4008,19 +4065,7 @@ __global__ __launch_bounds__(256, WIDE ? 1 : 4) void k_step_scan(GrowState g, Sc
         if (sf < 0) continue;
         const FeatDev sm = g.feats[sf];
         if (sm.kind == 2 || (sm.wide != 0) != WIDE) continue;  // the other instantiation's, or k_step_cat's
-        const bool sev = g.mask[sf] != 0 && g.splittable[static_cast<size_t>(J.t) * g.nf + sf] != 0;
-        const int64_t *hist = g.pool + static_cast<size_t>(child == J.built_side ? J.built_slot : J.parent_slot) * g.slot_stride;
-        const int64_t cnt = child == 0 ? static_cast<int64_t>(J.left) : J.parent_count - static_cast<int64_t>(J.left);
-        const Ctx c = make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[child], J.child_uh[child], cnt);
-        FeatCand r = {};
-        if (scan_searched(c, sm, sev)) {
-            Grown rg = {}, fg = {};
-            bool rf, ff;
-            if constexpr (WIDE) scan_numerical_wide(c, g.cfg, sm, hist, rf, rg, ff, fg);
-            else scan_numerical(c, g.cfg, sm, hist, rf, rg, ff, fg);
-            r = feature_candidate(c, sm, rf, rg, ff, fg);
-        }
-        if (lane == 0) g.cands[(static_cast<size_t>(j) * 2 + child) * g.nf + sf] = r;
+        scan_child<WIDE>(g, J, j, sf, sm, child);
     }
 }
 
