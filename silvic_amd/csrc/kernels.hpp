@@ -796,7 +796,7 @@ __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint32_t col16, 
     }
 }
 
-// Each row's leaf from a walk down the tree (nodes in LDS; TL_RPT rows per thread in flight: the walk is a chain
+// Each row's leaf from a walk down the tree (nodes in LDS; several rows per thread in flight: the walk is a chain
 // of dependent gathers), in row order, and the leaves' exact fixed-point sums rint(v * scale) of the in-bag rows'
 // gradients: the sums k_leaf_sums makes over the final partition (integers, so the order does not matter;
 // cpu.rs:886-908). grid: any, TL_THREADS threads.
@@ -824,6 +824,9 @@ constexpr uint32_t TL_THREADS = 512;
 
 template <uint32_t MAXL>
 __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
+    // rows per thread in flight: a tree of more than 512 leaves takes one block per compute unit (its nodes fill the
+    // LDS) and is deeper, so each thread walks more rows at once
+    constexpr int RPT = MAXL > LEAVES_SMALL ? 4 * TL_RPT : TL_RPT;
     __shared__ DevNode sn[MAXL - 1];
     __shared__ unsigned long long ls[MAXL][2];
     uint32_t nn = a.nn, nl = a.nl;
@@ -837,23 +840,23 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
     if (a.grad)
         for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
     __syncthreads();
-    const uint64_t stride = static_cast<uint64_t>(TL_RPT) * gridDim.x * blockDim.x;
+    const uint64_t stride = static_cast<uint64_t>(RPT) * gridDim.x * blockDim.x;
     for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; base < a.rows; base += stride) {
-        uint64_t r[TL_RPT];
-        int32_t nd[TL_RPT];
+        uint64_t r[RPT];
+        int32_t nd[RPT];
 #pragma unroll
-        for (int k = 0; k < TL_RPT; ++k) {
+        for (int k = 0; k < RPT; ++k) {
             r[k] = base + static_cast<uint64_t>(k) * gridDim.x * blockDim.x;
             nd[k] = r[k] < a.rows ? 0 : -1;
         }
         for (;;) {
-            uint32_t b[TL_RPT];
+            uint32_t b[RPT];
 #pragma unroll
-            for (int k = 0; k < TL_RPT; ++k)
+            for (int k = 0; k < RPT; ++k)
                 b[k] = nd[k] >= 0 ? col_bin(a.colbins, a.col16, static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]) : 0u;
             bool any = false;
 #pragma unroll
-            for (int k = 0; k < TL_RPT; ++k) {
+            for (int k = 0; k < RPT; ++k) {
                 if (nd[k] < 0) continue;
                 const DevNode &x = sn[nd[k]];
                 nd[k] = rule_left(x.left_bins, x.wide, b[k]) ? x.left : x.right;
@@ -862,7 +865,7 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
             if (!any) break;
         }
 #pragma unroll
-        for (int k = 0; k < TL_RPT; ++k) {
+        for (int k = 0; k < RPT; ++k) {
             if (r[k] >= a.rows) continue;
             const uint32_t leaf = static_cast<uint32_t>(~nd[k]);
             a.leaf_of[r[k]] = static_cast<uint16_t>(leaf);
