@@ -2503,6 +2503,7 @@ struct AdvShared {
     int16_t pnode[MAXL];                  // committed leaf -> the internal node above it (-1: the root)
     uint8_t is_left[MAXL];                // committed leaf is its node's left child
     uint8_t touched[MAXL];                // committed leaf changed by this replay
+    uint32_t key[MAXL];                   // replay_lds: committed leaf's replay key (0: none)
     uint16_t ck[MAXL];                    // commit c: the speculative leaf split (node n0 - 1 + c)
     uint16_t cx[MAXL];                    // commit c: the leaf id split
     int16_t cpn[MAXL];                    // commit c: the split leaf's node above
@@ -2687,19 +2688,19 @@ __device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
     }
 }
 
-// The replay for trees of more than 512 leaves: as replay, with each committed leaf's speculative leaf and node
-// above in LDS (s.leaf_t, s.pnode) rather than in registers; the keys stay in registers (NPL a lane), with each
-// lane's largest key cached, which only the lanes owning the two leaves a commit changes recompute. The left /
-// changed / has-split / NaN-gain flags are per-lane bitmasks. A lane other than the winner's holds a key with the
-// winner's gain prefix exactly when its largest key has that prefix, so the exact f64 argmax runs only when one does.
+// The replay for trees of more than 512 leaves: as replay, with the committed leaves' state in LDS (speculative
+// leaf, node above, left and changed flags, and each leaf's replay key in s.key) and only each lane's largest key in
+// a register. A lane other than the winner's holds a key with the winner's gain prefix exactly when its largest key
+// has that prefix; the winner's own other keys, and its new largest key after the commit, are read from s.key by NPL
+// lanes at once. Leaves with a split and a NaN gain are counted, and the NaN rule looks at the leaves only while
+// there are some.
 template <int NPL, typename S>
 __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     constexpr int IDB = 11;
-    static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 32, "leaf ids fit");
+    static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 64, "leaf ids fit");
     constexpr uint32_t IDM = (1u << IDB) - 1u;
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t rl = 0, rtouch = 0, rhas = 0, rnan = 0, lk = 0;
-    uint32_t rk[NPL];  // the lane's leaves' replay keys
+    uint32_t lk = 0, nan_lane = 0;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const uint32_t id = lane + 64u * j;
@@ -2709,13 +2710,12 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             const double gj = s.gain[t];
             const uint32_t m = s.meta[t];
             key = replay_key<IDB>(gj, m, id);
-            rl |= s.is_left[id] ? 1u << j : 0u;
-            rhas |= (m & 1u) ? 1u << j : 0u;
-            rnan |= (m & 1u) && gj != gj ? 1u << j : 0u;
+            nan_lane += (m & 1u) && gj != gj ? 1u : 0u;
         }
-        rk[j] = key;
+        s.key[id] = key;
         lk = key > lk ? key : lk;
     }
+    uint32_t nan_leaves = wave_total(nan_lane);
     uint32_t n = n0, nc = 0, blocker = 0;
     bool done = false;
     for (;;) {
@@ -2724,10 +2724,15 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             break;
         }
         // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
-        if (__ballot(rnan != 0u)) {
+        if (nan_leaves) {
             int lfirst = 1 << 30;
-            for (int j = NPL - 1; j >= 0; --j)  // descending, so the lowest id is the one kept
-                if ((rhas >> j) & 1u) lfirst = 2 * static_cast<int>(lane + 64u * j) + static_cast<int>((rnan >> j) & 1u);
+            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
+                const uint32_t id = lane + 64u * j;
+                if (id >= n) continue;
+                const uint32_t t = s.leaf_t[id];
+                const double gj = s.gain[t];
+                if (s.meta[t] & 1u) lfirst = 2 * static_cast<int>(id) + (gj != gj ? 1 : 0);
+            }
             const int first = wave_min_i32(lfirst);
             if (first < (1 << 30) && (first & 1)) {
                 done = true;
@@ -2741,21 +2746,18 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         }
         uint32_t x = IDM - (best & IDM);
         {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
-            const uint32_t bp = best >> IDB;
-            bool other = lane != (x & 63u) && (lk >> IDB) == bp;
-            if (lane == (x & 63u)) {
-                uint32_t hit = 0;
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) hit |= ((rk[j] >> IDB) == bp && rk[j] != best) ? 1u : 0u;
-                other = other || hit != 0u;
+            const uint32_t bp = best >> IDB, lw = x & 63u;
+            bool other = lane != lw && (lk >> IDB) == bp;
+            if (lane < static_cast<uint32_t>(NPL)) {  // the winner's lane's keys (0 past the leaves)
+                const uint32_t kk = s.key[lw + 64u * lane];
+                other = other || ((kk >> IDB) == bp && kk != best);
             }
             if (__ballot(other)) {
                 double kg = 0.0;
                 int ki = -1;
-#pragma unroll
                 for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
                     const uint32_t id = lane + 64u * j;
-                    if ((rk[j] >> IDB) != bp) continue;
+                    if ((s.key[id] >> IDB) != bp) continue;
                     const double gj = s.gain[s.leaf_t[id]];
                     if (ki < 0 || gj >= kg) {
                         kg = gj;
@@ -2766,61 +2768,45 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
                 x = static_cast<uint32_t>(ki);
             }
         }
-        const uint32_t lx = x & 63u, jx = x >> 6;
-        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: one broadcast read
+        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: broadcast reads
         const uint32_t m = s.meta[k];
         if (((m >> 1) & 3u) != T_EXPANDED) {
             blocker = k;
             break;
         }
         const int32_t pn = s.pnode[x];
-        const uint32_t xl = (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rl), lx)) >> jx) & 1u;
+        const uint32_t xl = s.is_left[x];
         const uint32_t kid = (m >> 3) - 1u;
         const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
         const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
+        const uint32_t k0 = replay_key<IDB>(g0, m0, x), k1 = replay_key<IDB>(g1, m1, n);
+        // leaf x becomes the left child, leaf n the right one, both under node n - 1
+        const int32_t node = static_cast<int32_t>(n) - 1;
         if (lane == 0) {
             s.ck[nc] = static_cast<uint16_t>(k);
             s.cx[nc] = static_cast<uint16_t>(x);
             s.cpn[nc] = static_cast<int16_t>(pn);
             s.cleft[nc] = static_cast<uint8_t>(xl);
-        }
-        // leaf x becomes the left child, leaf n the right one, both under node n - 1; the owning lanes write them
-        const int32_t node = static_cast<int32_t>(n) - 1;
-        const uint32_t ln = n & 63u, jn = n >> 6;
-        const uint32_t bx = 1u << jx, bn = 1u << jn;
-        if (lane == lx) {
             s.leaf_t[x] = static_cast<uint16_t>(kid);
             s.pnode[x] = static_cast<int16_t>(node);
-            rk[jx] = replay_key<IDB>(g0, m0, x);  // jx is wave-uniform: an indexed register move
-            rl |= bx;
-            rtouch |= bx;
-            rhas = (rhas & ~bx) | ((m0 & 1u) ? bx : 0u);
-            rnan = (rnan & ~bx) | ((m0 & 1u) && g0 != g0 ? bx : 0u);
-        }
-        if (lane == ln) {
+            s.is_left[x] = 1;
+            s.touched[x] = 1;
+            s.key[x] = k0;
             s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
             s.pnode[n] = static_cast<int16_t>(node);
-            rk[jn] = replay_key<IDB>(g1, m1, n);
-            rl &= ~bn;
-            rtouch |= bn;
-            rhas = (rhas & ~bn) | ((m1 & 1u) ? bn : 0u);
-            rnan = (rnan & ~bn) | ((m1 & 1u) && g1 != g1 ? bn : 0u);
+            s.is_left[n] = 0;
+            s.touched[n] = 1;
+            s.key[n] = k1;
         }
-        if (lane == lx || lane == ln) {
-            uint32_t mx = 0;
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) mx = rk[j] > mx ? rk[j] : mx;
-            lk = mx;
-        }
+        nan_leaves += ((m0 & 1u) && g0 != g0 ? 1u : 0u) + ((m1 & 1u) && g1 != g1 ? 1u : 0u);
+        // the lanes' largest keys: x's lane (its largest was x's old key) from its keys, n's lane takes k1 as well
+        const uint32_t lx = x & 63u, ln = n & 63u;
+        const uint32_t kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : 0u;
+        const uint32_t mx = wave_max_u32(kk);
+        if (lane == lx) lk = mx;
+        else if (lane == ln) lk = k1 > lk ? k1 : lk;
         ++nc;
         ++n;
-    }
-    for (int j = 0; j < NPL; ++j) {
-        const uint32_t id = lane + 64u * j;
-        if (id < n) {
-            s.is_left[id] = static_cast<uint8_t>((rl >> j) & 1u);
-            s.touched[id] = static_cast<uint8_t>((rtouch >> j) & 1u);
-        }
     }
     if (lane == 0) {
         s.ncommit = nc;
