@@ -2503,7 +2503,7 @@ struct AdvShared {
     int16_t pnode[MAXL];                  // committed leaf -> the internal node above it (-1: the root)
     uint8_t is_left[MAXL];                // committed leaf is its node's left child
     uint8_t touched[MAXL];                // committed leaf changed by this replay
-    uint32_t key[MAXL];                   // replay_lds: committed leaf's replay key (0: none)
+    uint32_t key[MAXL];                   // committed leaf's replay key (0: none)
     uint16_t ck[MAXL];                    // commit c: the speculative leaf split (node n0 - 1 + c)
     uint16_t cx[MAXL];                    // commit c: the leaf id split
     int16_t cpn[MAXL];                    // commit c: the split leaf's node above
@@ -2533,7 +2533,138 @@ __device__ __forceinline__ uint32_t replay_key(double gain, uint32_t meta, uint3
     return (p << IDB) | ((1u << IDB) - 1u - id);
 }
 
-// The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave: lane l holds committed
+// The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave. Lane l owns committed
+// leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves); their state is in LDS (speculative leaf, node above,
+// left and changed flags, and the replay key in s.key) and only the lane's largest key is in a register. A commit is
+// one u32 wave max of those (the reference's argmax only matters while the best gain is positive: otherwise the tree
+// stops), with an exact f64 argmax only when two leaves share the winner's gain prefix: a lane other than the
+// winner's holds such a key exactly when its largest key has the prefix, and the winner's own other keys, like its
+// new largest key after the commit, are read from s.key by NPL lanes at once. The rule that the first leaf with a
+// split decides when its gain is NaN takes a wave minimum, only while some leaf has a NaN gain (they are counted).
+// Leaves the commits, the committed-leaf arrays and the outcome in `s`.
+template <int NPL, typename S>
+__device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
+    constexpr int IDB = 11;
+    static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 64, "leaf ids fit");
+    constexpr uint32_t IDM = (1u << IDB) - 1u;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t lk = 0, nan_lane = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const uint32_t id = lane + 64u * j;
+        uint32_t key = 0;
+        if (id < n0) {
+            const uint32_t t = s.leaf_t[id];
+            const double gj = s.gain[t];
+            const uint32_t m = s.meta[t];
+            key = replay_key<IDB>(gj, m, id);
+            nan_lane += (m & 1u) && gj != gj ? 1u : 0u;
+        }
+        s.key[id] = key;
+        lk = key > lk ? key : lk;
+    }
+    uint32_t nan_leaves = wave_total(nan_lane);
+    uint32_t n = n0, nc = 0, blocker = 0;
+    bool done = false;
+    for (;;) {
+        if (n >= L) {
+            done = true;
+            break;
+        }
+        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
+        if (nan_leaves) {
+            int lfirst = 1 << 30;
+            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
+                const uint32_t id = lane + 64u * j;
+                if (id >= n) continue;
+                const uint32_t t = s.leaf_t[id];
+                const double gj = s.gain[t];
+                if (s.meta[t] & 1u) lfirst = 2 * static_cast<int>(id) + (gj != gj ? 1 : 0);
+            }
+            const int first = wave_min_i32(lfirst);
+            if (first < (1 << 30) && (first & 1)) {
+                done = true;
+                break;
+            }
+        }
+        const uint32_t best = wave_max_u32(lk);
+        if (best == 0u) {
+            done = true;
+            break;
+        }
+        uint32_t x = IDM - (best & IDM);
+        {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
+            const uint32_t bp = best >> IDB, lw = x & 63u;
+            bool other = lane != lw && (lk >> IDB) == bp;
+            if (lane < static_cast<uint32_t>(NPL)) {  // the winner's lane's keys (0 past the leaves)
+                const uint32_t kk = s.key[lw + 64u * lane];
+                other = other || ((kk >> IDB) == bp && kk != best);
+            }
+            if (__ballot(other)) {
+                double kg = 0.0;
+                int ki = -1;
+                for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
+                    const uint32_t id = lane + 64u * j;
+                    if ((s.key[id] >> IDB) != bp) continue;
+                    const double gj = s.gain[s.leaf_t[id]];
+                    if (ki < 0 || gj >= kg) {
+                        kg = gj;
+                        ki = static_cast<int>(id);
+                    }
+                }
+                wave_argmax(kg, ki);
+                x = static_cast<uint32_t>(ki);
+            }
+        }
+        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: broadcast reads
+        const uint32_t m = s.meta[k];
+        if (((m >> 1) & 3u) != T_EXPANDED) {
+            blocker = k;
+            break;
+        }
+        const int32_t pn = s.pnode[x];
+        const uint32_t xl = s.is_left[x];
+        const uint32_t kid = (m >> 3) - 1u;
+        const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
+        const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
+        const uint32_t k0 = replay_key<IDB>(g0, m0, x), k1 = replay_key<IDB>(g1, m1, n);
+        // leaf x becomes the left child, leaf n the right one, both under node n - 1
+        const int32_t node = static_cast<int32_t>(n) - 1;
+        if (lane == 0) {
+            s.ck[nc] = static_cast<uint16_t>(k);
+            s.cx[nc] = static_cast<uint16_t>(x);
+            s.cpn[nc] = static_cast<int16_t>(pn);
+            s.cleft[nc] = static_cast<uint8_t>(xl);
+            s.leaf_t[x] = static_cast<uint16_t>(kid);
+            s.pnode[x] = static_cast<int16_t>(node);
+            s.is_left[x] = 1;
+            s.touched[x] = 1;
+            s.key[x] = k0;
+            s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
+            s.pnode[n] = static_cast<int16_t>(node);
+            s.is_left[n] = 0;
+            s.touched[n] = 1;
+            s.key[n] = k1;
+        }
+        nan_leaves += ((m0 & 1u) && g0 != g0 ? 1u : 0u) + ((m1 & 1u) && g1 != g1 ? 1u : 0u);
+        // the lanes' largest keys: x's lane (its largest was x's old key) from its keys, n's lane takes k1 as well
+        const uint32_t lx = x & 63u, ln = n & 63u;
+        const uint32_t kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : 0u;
+        const uint32_t mx = wave_max_u32(kk);
+        if (lane == lx) lk = mx;
+        else if (lane == ln) lk = k1 > lk ? k1 : lk;
+        ++nc;
+        ++n;
+    }
+    if (lane == 0) {
+        s.ncommit = nc;
+        s.n = n;
+        s.done = done ? 1u : 0u;
+        s.blocker = blocker;
+    }
+}
+
+// The replay of replay_lds for trees of up to 128 leaves (NPL 1 or 2), where registers beat LDS: lane l holds committed
 // leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves) in registers (replay key, meta, speculative leaf, node
 // above, left / has-split / NaN-gain flags). A commit is one u32 wave max of the keys (the reference's argmax only
 // matters while the best gain is positive: otherwise the tree stops), with an exact f64 argmax only when two
@@ -2688,134 +2819,6 @@ __device__ __forceinline__ void replay(S &s, uint32_t n0, uint32_t L) {
     }
 }
 
-// The replay for trees of more than 512 leaves: as replay, with the committed leaves' state in LDS (speculative
-// leaf, node above, left and changed flags, and each leaf's replay key in s.key) and only each lane's largest key in
-// a register. A lane other than the winner's holds a key with the winner's gain prefix exactly when its largest key
-// has that prefix; the winner's own other keys, and its new largest key after the commit, are read from s.key by NPL
-// lanes at once. Leaves with a split and a NaN gain are counted, and the NaN rule looks at the leaves only while
-// there are some.
-template <int NPL, typename S>
-__device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
-    constexpr int IDB = 11;
-    static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 64, "leaf ids fit");
-    constexpr uint32_t IDM = (1u << IDB) - 1u;
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t lk = 0, nan_lane = 0;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-        const uint32_t id = lane + 64u * j;
-        uint32_t key = 0;
-        if (id < n0) {
-            const uint32_t t = s.leaf_t[id];
-            const double gj = s.gain[t];
-            const uint32_t m = s.meta[t];
-            key = replay_key<IDB>(gj, m, id);
-            nan_lane += (m & 1u) && gj != gj ? 1u : 0u;
-        }
-        s.key[id] = key;
-        lk = key > lk ? key : lk;
-    }
-    uint32_t nan_leaves = wave_total(nan_lane);
-    uint32_t n = n0, nc = 0, blocker = 0;
-    bool done = false;
-    for (;;) {
-        if (n >= L) {
-            done = true;
-            break;
-        }
-        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
-        if (nan_leaves) {
-            int lfirst = 1 << 30;
-            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
-                const uint32_t id = lane + 64u * j;
-                if (id >= n) continue;
-                const uint32_t t = s.leaf_t[id];
-                const double gj = s.gain[t];
-                if (s.meta[t] & 1u) lfirst = 2 * static_cast<int>(id) + (gj != gj ? 1 : 0);
-            }
-            const int first = wave_min_i32(lfirst);
-            if (first < (1 << 30) && (first & 1)) {
-                done = true;
-                break;
-            }
-        }
-        const uint32_t best = wave_max_u32(lk);
-        if (best == 0u) {
-            done = true;
-            break;
-        }
-        uint32_t x = IDM - (best & IDM);
-        {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
-            const uint32_t bp = best >> IDB, lw = x & 63u;
-            bool other = lane != lw && (lk >> IDB) == bp;
-            if (lane < static_cast<uint32_t>(NPL)) {  // the winner's lane's keys (0 past the leaves)
-                const uint32_t kk = s.key[lw + 64u * lane];
-                other = other || ((kk >> IDB) == bp && kk != best);
-            }
-            if (__ballot(other)) {
-                double kg = 0.0;
-                int ki = -1;
-                for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
-                    const uint32_t id = lane + 64u * j;
-                    if ((s.key[id] >> IDB) != bp) continue;
-                    const double gj = s.gain[s.leaf_t[id]];
-                    if (ki < 0 || gj >= kg) {
-                        kg = gj;
-                        ki = static_cast<int>(id);
-                    }
-                }
-                wave_argmax(kg, ki);
-                x = static_cast<uint32_t>(ki);
-            }
-        }
-        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: broadcast reads
-        const uint32_t m = s.meta[k];
-        if (((m >> 1) & 3u) != T_EXPANDED) {
-            blocker = k;
-            break;
-        }
-        const int32_t pn = s.pnode[x];
-        const uint32_t xl = s.is_left[x];
-        const uint32_t kid = (m >> 3) - 1u;
-        const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
-        const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
-        const uint32_t k0 = replay_key<IDB>(g0, m0, x), k1 = replay_key<IDB>(g1, m1, n);
-        // leaf x becomes the left child, leaf n the right one, both under node n - 1
-        const int32_t node = static_cast<int32_t>(n) - 1;
-        if (lane == 0) {
-            s.ck[nc] = static_cast<uint16_t>(k);
-            s.cx[nc] = static_cast<uint16_t>(x);
-            s.cpn[nc] = static_cast<int16_t>(pn);
-            s.cleft[nc] = static_cast<uint8_t>(xl);
-            s.leaf_t[x] = static_cast<uint16_t>(kid);
-            s.pnode[x] = static_cast<int16_t>(node);
-            s.is_left[x] = 1;
-            s.touched[x] = 1;
-            s.key[x] = k0;
-            s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
-            s.pnode[n] = static_cast<int16_t>(node);
-            s.is_left[n] = 0;
-            s.touched[n] = 1;
-            s.key[n] = k1;
-        }
-        nan_leaves += ((m0 & 1u) && g0 != g0 ? 1u : 0u) + ((m1 & 1u) && g1 != g1 ? 1u : 0u);
-        // the lanes' largest keys: x's lane (its largest was x's old key) from its keys, n's lane takes k1 as well
-        const uint32_t lx = x & 63u, ln = n & 63u;
-        const uint32_t kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : 0u;
-        const uint32_t mx = wave_max_u32(kk);
-        if (lane == lx) lk = mx;
-        else if (lane == ln) lk = k1 > lk ? k1 : lk;
-        ++nc;
-        ++n;
-    }
-    if (lane == 0) {
-        s.ncommit = nc;
-        s.n = n;
-        s.done = done ? 1u : 0u;
-        s.blocker = blocker;
-    }
-}
-
 // The `spec` highest of the `ncand` candidate keys s.ckey (distinct 64-bit keys) into s.job_t[1 .. spec], in key
 // order, by a radix selection over the keys' 64 bits, 8 at a time from the top: a 256-bucket count of the
 // candidates that still match the prefix found so far, the bucket where the count from the top reaches what is
@@ -2951,8 +2954,8 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if constexpr (MAXL <= LEAVES_SMALL) {
             if (L <= 64) replay<1>(s, n0, L);
             else if (L <= 128) replay<2>(s, n0, L);
-            else if (L <= 256) replay<4>(s, n0, L);
-            else replay<LEAVES_SMALL / 64>(s, n0, L);
+            else if (L <= 256) replay_lds<4>(s, n0, L);
+            else replay_lds<LEAVES_SMALL / 64>(s, n0, L);
         } else {
             if (L <= 1024) replay_lds<16>(s, n0, L);
             else replay_lds<MAXL / 64>(s, n0, L);
