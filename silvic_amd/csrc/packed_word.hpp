@@ -9,20 +9,20 @@
 #include <stdint.h>
 
 #ifdef __HIPCC__
-#define SROCM_HD __host__ __device__ __forceinline__
+#define SROCM_PACKED_HD __host__ __device__ __forceinline__
 #else
-#define SROCM_HD inline
+#define SROCM_PACKED_HD inline
 #endif
 
 namespace srocm {
 
 // the signed low half
-SROCM_HD int32_t packed_g(int32_t word) {
+SROCM_PACKED_HD int32_t packed_g(int32_t word) {
     return static_cast<int16_t>(static_cast<uint16_t>(static_cast<uint32_t>(word)));
 }
 
 // the unsigned high half, given the low half g = packed_g(word)
-SROCM_HD int32_t packed_h(int32_t word, int32_t g) {
+SROCM_PACKED_HD int32_t packed_h(int32_t word, int32_t g) {
     return static_cast<int32_t>((static_cast<uint32_t>(word) - static_cast<uint32_t>(g)) >> 16);
 }
 
