@@ -3553,12 +3553,56 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
     }
 }
 
+// hist_list for a 128-column byte slab with 8 columns a lane: a wave covers 4 rows a step, lane l the dword pair
+// l % 16 of row l / 16, so a row is one 128-byte line read by 16 lanes and a wave has 4 * UNROLL rows in flight for
+// the registers that 2 * UNROLL rows take at a dword a lane. Each lane rotates its pair right by `rot` bytes once a
+// row, so that its k-th add takes byte (k + rot) % 8 (column 8d + (k + rot) % 8): with rot = d / 8 + 2 * (l / 16)
+// the 64 lanes of an add reach every bank of the row's 128 columns twice (32 banks) or once (64).
+template <int UNROLL, int NW = 16>
+__device__ __forceinline__ void hist_list_pairs(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1,
+                                                const int32_t *gh, const uint32_t *bins32, uint32_t wave) {
+    constexpr uint32_t W = 128, RPW = 4;
+    constexpr uint32_t STEP = NW * RPW * UNROLL;
+    const uint32_t lane = threadIdx.x & 63u, d = lane & 15u, rsub = lane >> 4;
+    const uint32_t rot = ((d >> 3) + 2u * rsub) & 7u;
+    const bool swap = rot >= 4u;
+    const uint32_t sh = 8u * (rot & 3u);
+    uint32_t cols[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cols[k] = 8u * d + ((static_cast<uint32_t>(k) + rot) & 7u);
+    const uint2 *rows2 = reinterpret_cast<const uint2 *>(bins32);
+    const uint32_t last = c1 - 1;
+    for (uint32_t base = c0 + wave * RPW * UNROLL; base < c1; base += STEP) {
+        uint32_t r[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) r[u] = list[min(base + u * RPW + rsub, last)];
+        uint2 v[UNROLL];
+        int32_t gq[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            gq[u] = gh[r[u]];
+            v[u] = rows2[static_cast<size_t>(r[u]) * (W / 8) + d];
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int32_t gv = base + u * RPW + rsub < c1 ? gq[u] : 0;
+            const uint32_t a = swap ? v[u].y : v[u].x, b = swap ? v[u].x : v[u].y;  // the pair rotated by 4 bytes
+            const uint32_t lo = __builtin_amdgcn_alignbit(b, a, sh), hi = __builtin_amdgcn_alignbit(a, b, sh);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) atomicAdd(&lds[__builtin_amdgcn_ubfe(lo, 8u * k, 8u) * W + cols[k]], gv);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) atomicAdd(&lds[__builtin_amdgcn_ubfe(hi, 8u * k, 8u) * W + cols[4 + k]], gv);
+        }
+    }
+}
+
 // A split step's histogram of list[c0 .. c1): hist_list, or hist_list_dense for a dense slab (DP passes).
 template <int W, bool WIDE, int PACK, bool Q32, int DP, int UNROLL, int NW = 16>
 __device__ __forceinline__ void step_hist(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
                                           const uint32_t *bins32, uint32_t dw_row, const uint32_t (&xs)[4],
                                           const uint32_t (&dcols)[DP ? DP : 1][4], uint32_t wave = threadIdx.x >> 6) {
     if constexpr (DP > 0) hist_list_dense<W, DP, DP <= 4 ? 2 : 1, NW>(lds, list, c0, c1, gh, bins32, dw_row, xs, dcols, wave);
+    else if constexpr (W == 128 && !WIDE && PACK == 1 && !Q32) hist_list_pairs<UNROLL * 3 / 4, NW>(lds, list, c0, c1, gh, bins32, wave);
     else hist_list<W, WIDE, PACK, Q32, UNROLL, NW>(lds, list, c0, c1, gh, bins32, wave);
 }
 
