@@ -3556,15 +3556,16 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
 // hist_list for a 128-column byte slab with 8 columns a lane: a wave covers 4 rows a step, lane l the dword pair
 // l % 16 of row l / 16, so a row is one 128-byte line read by 16 lanes and a wave has 4 * UNROLL rows in flight for
 // the registers that 2 * UNROLL rows take at a dword a lane. Each lane rotates its pair right by `rot` bytes once a
-// row, so that its k-th add takes byte (k + rot) % 8 (column 8d + (k + rot) % 8): with rot = d / 8 + 2 * (l / 16)
-// the 64 lanes of an add reach every bank of the row's 128 columns twice (32 banks) or once (64).
+// row, so that its k-th add takes byte (k + rot) % 8 (column 8d + (k + rot) % 8). The LDS serves an instruction a
+// half-wave (32 lanes, two rows) at a time; with rot = d / 4 + 4 * (row % 2) the 8 lanes of a half-wave whose
+// columns share a bank group (d % 4 alike) take 8 different bytes, so no two of its lanes meet in a bank.
 template <int UNROLL, int NW = 16>
 __device__ __forceinline__ void hist_list_pairs(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1,
                                                 const int32_t *gh, const uint32_t *bins32, uint32_t wave) {
     constexpr uint32_t W = 128, RPW = 4;
     constexpr uint32_t STEP = NW * RPW * UNROLL;
     const uint32_t lane = threadIdx.x & 63u, d = lane & 15u, rsub = lane >> 4;
-    const uint32_t rot = ((d >> 3) + 2u * rsub) & 7u;
+    const uint32_t rot = ((d >> 2) + 4u * (rsub & 1u)) & 7u;
     const bool swap = rot >= 4u;
     const uint32_t sh = 8u * (rot & 3u);
     uint32_t cols[8];
