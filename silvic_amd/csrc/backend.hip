@@ -429,6 +429,7 @@ struct Context {
 
     ~Context() {
         if (tree_event) (void)hipEventDestroy(tree_event);
+        if (steps_event) (void)hipEventDestroy(steps_event);
         for (auto &e : prof.hist_events) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
