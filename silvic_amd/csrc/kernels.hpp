@@ -2925,6 +2925,58 @@ __device__ void select_top(AdvShared<MAXL> &s, uint32_t ncand, uint32_t spec) {
     }
 }
 
+// The commits applied to the tree (tree.rs:143-177) by waves w0 .. w0 + nw - 1 of the block (nw >= 2): wave w0
+// writes the new nodes and then, once they have landed, the links into nodes split again (a later commit of the step
+// may split a leaf a node of the same step points to); the other waves write the changed leaves.
+template <uint32_t MAXL>
+__device__ void apply_commits(const GrowState &g, const AdvShared<MAXL> &s, uint32_t n0, uint32_t nc, uint32_t n,
+                              uint32_t w0, uint32_t nw) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const TreeDev &t = g.tree;
+    if (wave == w0) {
+        for (uint32_t c = lane; c < nc; c += 64u) {
+            const TLeaf &p = g.tl[s.ck[c]];
+            const SplitOut &info = p.best;
+            const uint32_t node = n0 - 1 + c;
+            t.split_feature[node] = info.feature;
+            const uint32_t wide = g.feats[info.feature].wide;
+#pragma unroll
+            for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = left_bins_word(info, w, wide);
+            t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
+            t.threshold_bin[node] = info.threshold;
+            t.default_left[node] = static_cast<uint8_t>(info.default_left);
+            t.left_child[node] = ~static_cast<int32_t>(s.cx[c]);
+            t.right_child[node] = ~static_cast<int32_t>(n0 + c);
+            t.internal_weight[node] = p.weight;
+            t.internal_value[node] = p.value;
+            t.internal_count[node] = p.cnt;
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the nodes' children have landed before the links overwrite some
+        for (uint32_t c = lane; c < nc; c += 64u) {
+            const int32_t pn = s.cpn[c];
+            if (pn < 0) continue;
+            if (s.cleft[c]) t.left_child[pn] = static_cast<int32_t>(n0 - 1 + c);
+            else t.right_child[pn] = static_cast<int32_t>(n0 - 1 + c);
+        }
+        return;
+    }
+    if (wave <= w0 || wave >= w0 + nw) return;
+    for (uint32_t id = (wave - w0 - 1) * 64u + lane; id < n; id += (nw - 1) * 64u) {
+        if (!s.touched[id]) continue;
+        const uint32_t k = s.leaf_t[id];
+        const TLeaf &l = g.tl[k];
+        t.leaf_value[id] = l.value;
+        t.leaf_weight[id] = l.weight;
+        t.leaf_count[id] = l.cnt;
+        t.leaf_parent[id] = s.pnode[id];
+        t.leaf_depth[id] = l.depth;
+        t.leaf_range[2 * id] = l.begin;
+        t.leaf_range[2 * id + 1] = l.count;
+        g.leaf_t[id] = static_cast<int32_t>(k);
+        g.leaf_left[id] = s.is_left[id];
+    }
+}
+
 template <uint32_t MAXL>
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     AdvShared<MAXL> &s = *reinterpret_cast<AdvShared<MAXL> *>(scratch);
@@ -2965,54 +3017,15 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     const uint32_t nc = s.ncommit, n = s.n;
     const bool done = s.done != 0;
 
-    // -- the commits applied to the tree (tree.rs:143-177): nodes and the changed leaves, then the links into
-    // nodes split again
-    const TreeDev &t = g.tree;
-    for (uint32_t id = tid; id < n; id += nt) {
-        if (!s.touched[id]) continue;
-        const uint32_t k = s.leaf_t[id];
-        const TLeaf &l = g.tl[k];
-        t.leaf_value[id] = l.value;
-        t.leaf_weight[id] = l.weight;
-        t.leaf_count[id] = l.cnt;
-        t.leaf_parent[id] = s.pnode[id];
-        t.leaf_depth[id] = l.depth;
-        t.leaf_range[2 * id] = l.begin;
-        t.leaf_range[2 * id + 1] = l.count;
-        g.leaf_t[id] = static_cast<int32_t>(k);
-        g.leaf_left[id] = s.is_left[id];
-    }
-    for (uint32_t c = nt - 1u - tid; c < nc; c += nt) {  // from the last thread down: beside the leaves' loads
-        const TLeaf &p = g.tl[s.ck[c]];
-        const SplitOut &info = p.best;
-        const uint32_t node = n0 - 1 + c;
-        t.split_feature[node] = info.feature;
-        const uint32_t wide = g.feats[info.feature].wide;
-#pragma unroll
-        for (uint32_t w = 0; w < 8; ++w) t.left_bins[static_cast<size_t>(node) * 8 + w] = left_bins_word(info, w, wide);
-        t.split_gain[node] = static_cast<float>(info.gain + g.cfg.min_gain_to_split);
-        t.threshold_bin[node] = info.threshold;
-        t.default_left[node] = static_cast<uint8_t>(info.default_left);
-        t.left_child[node] = ~static_cast<int32_t>(s.cx[c]);
-        t.right_child[node] = ~static_cast<int32_t>(n0 + c);
-        t.internal_weight[node] = p.weight;
-        t.internal_value[node] = p.value;
-        t.internal_count[node] = p.cnt;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (uint32_t c = tid; c < nc; c += nt) {
-        const int32_t pn = s.cpn[c];
-        if (pn < 0) continue;
-        if (s.cleft[c]) t.left_child[pn] = static_cast<int32_t>(n0 - 1 + c);
-        else t.right_child[pn] = static_cast<int32_t>(n0 - 1 + c);
-    }
     if (tid == 0) {
         ctl->num_leaves = n;
         ctl->pending = pending0 - nc;
         if (done) ctl->done = 1;
     }
-    if (done) return;
+    if (done) {
+        apply_commits(g, s, n0, nc, n, 0, nt >> 6);
+        return;
+    }
 
     // -- speculation candidates: unexpanded leaves with a positive gain, the blocker aside
     const uint32_t blocker = s.blocker;
@@ -3072,10 +3085,13 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             ctl->error = 4;
             ctl->done = 1;
         }
+        apply_commits(g, s, n0, nc, n, 0, nt >> 6);
         return;
     }
 
-    // -- the jobs (learner.rs:249-290), one lane each; then prefix sums over the jobs on the same wave
+    // -- the jobs (learner.rs:249-290), one lane each; then prefix sums over the jobs on the same wave. The other
+    // waves meanwhile apply the commits to the tree (nothing the plan reads).
+    if (tid >= 64) apply_commits(g, s, n0, nc, n, 1, (nt >> 6) - 1);
     if (tid < 64) {
         const bool on = lane < njobs;
         JobPlan J = {};
