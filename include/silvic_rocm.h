@@ -93,8 +93,10 @@ typedef struct srocm_dataset {
 } srocm_dataset;
 
 /* ObjectiveSetup (crates/silvic-core/src/backend/mod.rs:56-71), the fields of its LambdaRank variant included.
- * Lambdarank gradients are computed on the host in f64 (objective/lambdarank.rs:190-420) by
- * srocm_compute_gradients and by the boosting loop; they need the training set's query_boundaries. */
+ * Lambdarank gradients (objective/lambdarank.rs:190-420) are computed by srocm_compute_gradients and by the
+ * boosting loop, bit-identical to silvic's f64 CPU path either way: on the device (k_rank_pairs) for queries of at
+ * most 512 rows, on the library's host threads in f64 for longer ones. They need the training set's
+ * query_boundaries. */
 enum { SROCM_OBJ_REGRESSION = 0, SROCM_OBJ_BINARY = 1, SROCM_OBJ_LAMBDARANK = 2 };
 typedef struct srocm_objective {
     uint32_t kind;                  /* SROCM_OBJ_* */
@@ -372,10 +374,11 @@ int srocm_boost(void *ctx, const srocm_train_params *params, uint32_t first_iter
  * the trait: for callers that check or reuse the row order on the host. `len` is at most the training rows. */
 int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
 
-/* Backend::histogram (mod.rs:146-149, quantized mode) into a caller-owned DEVICE buffer `out` of `len` = 2 *
- * total_bins int64 values ({g, h} units per bin), allocating nothing: no hipMalloc, no hipFree, no allocating
- * library call. It has no counterpart in the reference; it is for callers that cannot allocate (code under HIP
- * graph capture, tight serving loops, harnesses that forbid allocation). The per-workgroup partials go to a
+/* The quantized histogram of a leaf's rows into a caller-owned DEVICE buffer `out` of `len` = 2 * total_bins
+ * int64 values (the {g, h} sums of quantized units per bin, in the flat histogram order srocm_histogram uses),
+ * allocating nothing: no hipMalloc, no hipFree, no allocating library call. It has no counterpart in the
+ * reference; it is for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation). The per-workgroup partials go to a
  * 16 MiB scratch array that each GPU holds until the process ends and that every call on that GPU shares, so
  * calls that overlap on one GPU race. At most 16 MiB / (256 * slab width * 8 B) workgroups run (64 for 128-wide
  * slabs); a leaf whose rows per workgroup times the largest quantized unit could pass 2^31 is refused with

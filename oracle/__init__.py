@@ -87,6 +87,7 @@ def lib():
                                                P(C.c_float), P(C.c_float)]),
             "oracle_max_dcg_at_k": (C.c_double, [C.c_uint32, P(C.c_float), C.c_uint32, P(C.c_double), C.c_uint32]),
             "oracle_sigmoid_table_get": (C.c_double, [C.c_double, C.c_double]),
+            "oracle_check_labels": (C.c_int, [P(C.c_float), C.c_uint64, C.c_uint32]),
             "oracle_lambdarank_gradients": (None, [P(_abi.Dataset), P(Params), P(C.c_float), P(C.c_float),
                                                    P(C.c_float)]),
             "oracle_train": (C.c_void_p, [P(_abi.Dataset), P(Params)]),
@@ -199,6 +200,12 @@ def max_dcg_at_k(k, labels, label_gain):
     labels = np.ascontiguousarray(labels, dtype=np.float32)
     gain = np.ascontiguousarray(label_gain, dtype=np.float64)
     return lib().oracle_max_dcg_at_k(k, ptr(labels, C.c_float), len(labels), ptr(gain, C.c_double), len(gain))
+
+
+def check_labels(label, num_gains):
+    """lambdarank.rs:172-188: 0 when every label passes, else 1 (not an integer), 2 (negative) or 3 (too large)."""
+    label = np.ascontiguousarray(label, dtype=np.float32)
+    return lib().oracle_check_labels(ptr(label, C.c_float), len(label), num_gains)
 
 
 def lambdarank_gradients(data, params, scores):
@@ -334,6 +341,10 @@ class Model:
         self.times = dict(zip(["gradients", "quantize", "reset_partition", "histogram", "partition",
                                "split_search", "leaf_sums", "add_tree", "total"], t.tolist()))
         self.hist_bins = L.oracle_model_hist_bins(handle)
+        # the last tree's partition (empty for a model that grew no tree)
+        self.partition = np.zeros(num_rows, np.uint32)
+        if self.trees:
+            L.oracle_model_partition(handle, ptr(self.partition, C.c_uint32))
 
 
 def train(data, params):

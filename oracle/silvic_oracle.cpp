@@ -360,10 +360,36 @@ const SigmoidTable &sigmoid_table(double s) {
     return *last;
 }
 
+// Rust's `as` casts of an f32 label (lambdarank.rs:172-188, :349): NaN gives 0, out-of-range values the nearest end
+// of the target type, the rest truncate toward zero
+int32_t as_i32(float l) {
+    if (std::isnan(l)) return 0;
+    if (l <= -2147483648.0f) return std::numeric_limits<int32_t>::min();
+    if (l >= 2147483648.0f) return std::numeric_limits<int32_t>::max();
+    return static_cast<int32_t>(l);
+}
+size_t as_usize(float l) {
+    if (std::isnan(l) || l <= 0.0f) return 0;
+    if (l >= 18446744073709551616.0f) return std::numeric_limits<size_t>::max();
+    return static_cast<size_t>(l);
+}
+
+// lambdarank.rs:172-188 check_labels: 0 when every label passes, else the first failing check (1: not an integer,
+// 2: negative, 3: not below the number of label gains)
+int check_labels(const float *label, uint64_t n, size_t num_gains) {
+    for (uint64_t r = 0; r < n; ++r) {
+        const float l = label[r];
+        if (std::fabs(static_cast<double>(l) - static_cast<double>(as_i32(l))) > K_EPSILON) return 1;
+        if (l < 0.0f) return 2;
+        if (as_usize(l) >= num_gains) return 3;
+    }
+    return 0;
+}
+
 // lambdarank.rs:119-139 max_dcg_at_k
 double max_dcg_at_k(size_t k, const float *labels, size_t n, const std::vector<double> &label_gain) {
     std::vector<size_t> label_count(label_gain.size(), 0);
-    for (size_t i = 0; i < n; ++i) label_count[static_cast<size_t>(labels[i])] += 1;
+    for (size_t i = 0; i < n; ++i) label_count[as_usize(labels[i])] += 1;
     size_t top_label = label_gain.size() - 1;
     double dcg = 0.0;
     for (size_t j = 0; j < std::min(k, n); ++j) {
@@ -406,7 +432,7 @@ void rank_query(const RankSetup &st, size_t query, const float *scores, const fl
     for (size_t k = 0; k < n; ++k) {
         score[k] = static_cast<double>(scores[order[k]]);
         lab[k] = label[order[k]];
-        gain[k] = st.label_gain[static_cast<size_t>(lab[k])];
+        gain[k] = st.label_gain[as_usize(lab[k])];
         discount[k] = rank_discount(k);
     }
     size_t worst = n - 1;
@@ -471,12 +497,7 @@ RankSetup lambdarank_setup(const srocm_dataset *d, double sigmoid, bool norm, ui
     if (label_gain && num_label_gain) st.label_gain.assign(label_gain, label_gain + num_label_gain);
     else
         for (uint32_t i = 0; i < 31; ++i) st.label_gain.push_back(static_cast<double>((1u << i) - 1));  // config.rs:118-121
-    for (uint64_t r = 0; r < d->num_rows; ++r) {
-        float l = d->label[r];
-        if (std::fabs(static_cast<double>(l) - static_cast<double>(static_cast<int32_t>(l))) > K_EPSILON ||
-            l < 0.0f || static_cast<size_t>(l) >= st.label_gain.size())
-            throw std::runtime_error("bad ranking label");
-    }
+    if (check_labels(d->label, d->num_rows, st.label_gain.size())) throw std::runtime_error("bad ranking label");
     for (uint32_t q = 0; q < d->num_queries; ++q) {
         uint32_t b = d->query_boundaries[q], e = d->query_boundaries[q + 1];
         double max_dcg = max_dcg_at_k(truncation, d->label + b, e - b, st.label_gain);
@@ -1794,6 +1815,7 @@ Model *train(const srocm_dataset *d, const oracle_params *p) {
         model->splits.push_back(grown.splits);
     }
     backend.times[T_TOTAL] = std::chrono::duration<double>(Clock::now() - start).count();
+    model->partition = backend.partition;  // the last tree's row order (learner.rs:121-352)
     std::copy(backend.times, backend.times + T_COUNT, model->times);
     model->hist_bins = backend.hist_bins;
     model->scores = std::move(backend.scores);
@@ -1960,6 +1982,8 @@ double oracle_max_dcg_at_k(uint32_t k, const float *labels, uint32_t n, const do
 }
 
 double oracle_sigmoid_table_get(double sigmoid, double delta) { return sigmoid_table(sigmoid).get(delta); }
+
+int oracle_check_labels(const float *label, uint64_t n, uint32_t num_gains) { return check_labels(label, n, num_gains); }
 
 void oracle_lambdarank_gradients(const srocm_dataset *data, const oracle_params *p, const float *scores, float *grad,
                                  float *hess) {

@@ -137,6 +137,8 @@ void oracle_lambdarank_query(const float *scores, const float *label, const floa
                              const double *label_gain, uint32_t num_label_gain, double inverse_max_dcg,
                              double sigmoid, int norm, uint32_t truncation_level, float *grad, float *hess);
 /* lambdarank.rs:119-139 */
+// lambdarank.rs:172-188 check_labels (Rust's saturating casts: a NaN label passes as label 0)
+int oracle_check_labels(const float *label, uint64_t n, uint32_t num_gains);
 double oracle_max_dcg_at_k(uint32_t k, const float *labels, uint32_t n, const double *label_gain,
                            uint32_t num_label_gain);
 /* lambdarank.rs:104-116 SigmoidTable::get */

@@ -480,12 +480,12 @@ struct Context {
             if (t->query_boundaries[q + 1] < t->query_boundaries[q]) fail(SROCM_ERR_DATA, "query boundaries must not decrease");
         if (!obj->label_gain || obj->num_label_gain == 0) fail(SROCM_ERR_CONFIG, "lambdarank needs label gains");
         for (uint64_t r = 0; r < t->num_rows; ++r) {
-            const float l = t->label[r];
-            if (std::fabs(static_cast<double>(l) - static_cast<double>(static_cast<int32_t>(l))) > K_EPS_H)
+            const float l = t->label[r];  // Rust's saturating casts: a NaN label passes every check as label 0
+            if (std::fabs(static_cast<double>(l) - static_cast<double>(srocm_rank::label_as_i32(l))) > K_EPS_H)
                 fail(SROCM_ERR_DATA, "label should be int type (met " + std::to_string(l) + ") for ranking task");
             if (l < 0.0f) fail(SROCM_ERR_DATA, "label should be non-negative (met " + std::to_string(l) + ") for ranking task");
-            if (static_cast<uint64_t>(l) >= obj->num_label_gain)
-                fail(SROCM_ERR_DATA, "label " + std::to_string(static_cast<uint64_t>(l)) +
+            if (srocm_rank::label_as_index(l) >= obj->num_label_gain)
+                fail(SROCM_ERR_DATA, "label " + std::to_string(srocm_rank::label_as_index(l)) +
                                          " is not less than the number of label mappings (" + std::to_string(obj->num_label_gain) + ")");
         }
         srocm_rank::Setup st;
@@ -995,7 +995,10 @@ struct Context {
     // histogram and split-step workgroups are multiplied as the rows need. When the mode changes the slabs are laid
     // out again and refilled on the device from the column-major bins; when the counts change, the tables and
     // partial buffers follow.
-    void set_mode(bool want, int64_t units) {
+    struct WorkgroupCounts {
+        uint32_t hist_cap, step_target;  // k_hist workgroups at most, k_step_rows workgroups a step is spread over
+    };
+    WorkgroupCounts mode_counts(bool want, int64_t units) const {
         uint32_t hc = cus, st = cus;
         if (want) {
             const uint64_t cap = 2147483647ull / static_cast<uint64_t>(std::max<int64_t>(units, 1));  // rows a workgroup takes
@@ -1005,6 +1008,11 @@ struct Context {
             // k_step_rows: at most div_up(tiles + JMAX, target - JMAX) tiles of STEP_TILE rows
             st = static_cast<uint32_t>(std::max<uint64_t>(cus, div_up(div_up(n, STEP_TILE) + JMAX, cap / STEP_TILE) + JMAX));
         }
+        return {hc, st};
+    }
+    void set_mode(bool want, int64_t units) {
+        const WorkgroupCounts wc = mode_counts(want, units);
+        const uint32_t hc = wc.hist_cap, st = wc.step_target;
         if (want == q32 && hc == hist_cap && st == step_target) return;
         sync();
         const bool relayout = want != q32;
@@ -1119,24 +1127,28 @@ struct Context {
     // The most rows one histogram workgroup adds up: k_hist spreads a leaf over at most hist_cap workgroups in
     // multiples of 64 rows (at least HIST_MIN_ROWS each); a split step gives a workgroup at most
     // ceil(tiles / (step_target - JMAX)) tiles of a job, the step's tiles being at most rows / STEP_TILE + JMAX.
-    uint64_t max_workgroup_rows() const {
+    uint64_t max_workgroup_rows(const WorkgroupCounts &wc) const {
         const uint64_t n = std::max<uint64_t>(rows, 1);
-        const uint64_t hist = div_up(std::max<uint64_t>(div_up(n, hist_cap), HIST_MIN_ROWS), 64) * 64 + 64;
-        const uint64_t share = step_target > JMAX ? step_target - JMAX : 1;
+        const uint64_t hist = div_up(std::max<uint64_t>(div_up(n, wc.hist_cap), HIST_MIN_ROWS), 64) * 64 + 64;
+        const uint64_t share = wc.step_target > JMAX ? wc.step_target - JMAX : 1;
         const uint64_t step = div_up(div_up(n, STEP_TILE) + JMAX, share) * STEP_TILE;
         return std::max(hist, step);
     }
 
     // Quantized units a histogram can take: a packed word holds g as a signed 16-bit half and h as an unsigned one,
     // and a workgroup's sums of either are i32 (the reference's CPU sums are i64, cpu.rs:517-525), so
-    // max_q * max_workgroup_rows() must stay below 2^31.
+    // max_q * max_workgroup_rows() must stay below 2^31. Checked against the workgroup counts the mode for these
+    // units takes, before set_mode changes anything, so a refused quantization leaves the context as it was.
     static void check_unit_range(int64_t grad_max_q, int64_t hess_max_q) {
         if (grad_max_q < 1 || grad_max_q > 32767 || hess_max_q < 1 || hess_max_q > 65535)
             fail(SROCM_ERR_UNSUPPORTED, "quantized units must lie in 1..=32767 for gradients and 1..=65535 for hessians");
     }
+    bool q32_for(int64_t grad_max_q, int64_t hess_max_q) const {
+        return packed_flush_rows(grad_max_q, hess_max_q) < Q32_BELOW_FLUSH;
+    }
     void check_quant_units(int64_t grad_max_q, int64_t hess_max_q) const {
         check_unit_range(grad_max_q, hess_max_q);
-        const uint64_t wg = max_workgroup_rows();
+        const uint64_t wg = max_workgroup_rows(mode_counts(q32_for(grad_max_q, hess_max_q), std::max(grad_max_q, hess_max_q)));
         if (static_cast<uint64_t>(std::max(grad_max_q, hess_max_q)) * wg > 2147483647ull)
             fail(SROCM_ERR_UNSUPPORTED, "quantized units up to " + std::to_string(std::max(grad_max_q, hess_max_q)) + " over " +
                                             std::to_string(wg) + " rows per histogram workgroup could overflow its 32-bit sums");
@@ -1144,9 +1156,8 @@ struct Context {
 
     void quantize(const srocm_quant_spec &s) {
         require_loaded();
-        check_unit_range(s.grad_max_q, s.hess_max_q);
-        set_mode(packed_flush_rows(s.grad_max_q, s.hess_max_q) < Q32_BELOW_FLUSH, std::max(s.grad_max_q, s.hess_max_q));
         check_quant_units(s.grad_max_q, s.hess_max_q);
+        set_mode(q32_for(s.grad_max_q, s.hess_max_q), std::max(s.grad_max_q, s.hess_max_q));
         QuantDev q{s.inv_grad_scale, s.inv_hess_scale, s.grad_max_q, s.hess_max_q, s.constant_hessian, s.stochastic, s.seed, s.iteration};
         if (rows) {
             k_quantize<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, q);
@@ -2287,9 +2298,8 @@ static void feature_mask(const std::vector<srocm_feature> &feats, double fractio
 uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t count, srocm_grown_tree *trees) {
     require_loaded();
     bool constant_hessian = objective == SROCM_OBJ_REGRESSION && !has_weight;  // objective/mod.rs:84-89
-    check_unit_range(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
-    set_mode(packed_flush_rows(p.num_grad_quant_bins / 2, p.num_grad_quant_bins) < Q32_BELOW_FLUSH, p.num_grad_quant_bins);
     check_quant_units(p.num_grad_quant_bins / 2, p.num_grad_quant_bins);
+    set_mode(q32_for(p.num_grad_quant_bins / 2, p.num_grad_quant_bins), p.num_grad_quant_bins);
     uint32_t done = 0;
     HostTree tree;
     std::vector<srocm_bin_split> splits;

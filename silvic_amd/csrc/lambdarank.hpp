@@ -45,6 +45,20 @@ struct Setup {
     std::vector<uint32_t> boundaries;     // num_queries + 1
 };
 
+// A label as Rust's `as` casts convert it (lambdarank.rs:172-188, :349): NaN to 0, values outside the target's range
+// to its nearest end, the rest truncated toward zero. A NaN label passes silvic's checks and takes label 0's gain.
+SRANK_HD inline int32_t label_as_i32(float l) {
+    if (!(l == l)) return 0;
+    if (l <= -2147483648.0f) return INT32_MIN;
+    if (l >= 2147483648.0f) return INT32_MAX;
+    return static_cast<int32_t>(l);
+}
+SRANK_HD inline uint64_t label_as_index(float l) {
+    if (!(l > 0.0f)) return 0;  // NaN, zero and negative labels
+    if (l >= 18446744073709551616.0f) return UINT64_MAX;
+    return static_cast<uint64_t>(l);
+}
+
 // A key whose ascending order is the score's descending order; +0.0f folds -0 into 0 (equal under `>`).
 SRANK_HD inline uint32_t rank_key(float score) {
     float s = score + 0.0f;
@@ -127,7 +141,7 @@ public:
     // descending order, each weighted by its rank's discount, summed in rank order.
     double max_dcg_at_k(size_t k, const float *labels, size_t n) const {
         std::vector<size_t> count(setup_.label_gain.size(), 0);
-        for (size_t i = 0; i < n; ++i) count[static_cast<size_t>(labels[i])] += 1;
+        for (size_t i = 0; i < n; ++i) count[label_as_index(labels[i])] += 1;
         size_t top = count.size() - 1;
         double dcg = 0.0;
         for (size_t j = 0; j < std::min(k, n); ++j) {
@@ -218,7 +232,7 @@ private:
             sc.row[k] = r;
             sc.score[k] = static_cast<double>(scores[b + r]);
             sc.lab[k] = label[b + r];
-            sc.gain[k] = setup_.label_gain[static_cast<size_t>(sc.lab[k])];
+            sc.gain[k] = setup_.label_gain[label_as_index(sc.lab[k])];
             sc.disc[k] = discount(k);
         }
         // -inf scores rank last; the lowest score skips one trailing -inf (lambdarank.rs:333-340)

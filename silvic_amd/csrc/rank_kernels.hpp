@@ -110,7 +110,7 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
             row[m] = r;
             sc[m] = static_cast<double>(a.scores[b + r]);
             lb[m] = a.label[b + r];
-            gn[m] = a.label_gain[static_cast<uint32_t>(lb[m])];
+            gn[m] = a.label_gain[srocm_rank::label_as_index(lb[m])];
             dc[m] = a.discount[k];
             if (sc[m] == -__builtin_inf() && k < first_inf) first_inf = k;
         }

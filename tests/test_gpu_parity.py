@@ -543,13 +543,17 @@ def test_lambdarank_gradients_match_the_oracle():
 # few), a query of 500 rows (the 512-row kernel); and the host path (a query of more than 512 rows sends every query
 # to the host), both against the oracle bit for bit.
 @pytest.mark.parametrize("case", ["no norm, truncation 5", "weights, sigmoid 2", "uniform labels",
-                                  "one query of 500 rows, uniform labels", "one query of 700 rows"])
+                                  "one query of 500 rows, uniform labels", "one query of 700 rows", "NaN labels"])
 def test_lambdarank_gradient_paths_match_the_oracle(case):
     say("lambdarank gradients", case)
     data = silvic_amd.synthetic(3, rows=60_000, seed=9)
     kw = {}
     if "uniform labels" in case:
         data.label = np.random.default_rng(4).integers(0, 5, data.num_rows).astype(np.float32)
+    if case == "NaN labels":  # Rust's `as` casts: a NaN label passes silvic's checks and takes label 0's gain
+        data.label = data.label.copy()
+        data.label[np.random.default_rng(6).random(data.num_rows) < 0.05] = np.nan
+        assert oracle.check_labels(data.label, 31) == 0
     if case.startswith("no norm"):
         kw = dict(lambdarank_norm=False, lambdarank_truncation_level=5)
     elif case.startswith("weights"):
@@ -579,6 +583,20 @@ def test_lambdarank_gradient_paths_match_the_oracle(case):
             t.step(1)
     finally:
         t.backend.close()
+
+
+def test_lambdarank_labels_are_checked_as_the_reference_checks_them():
+    # lambdarank.rs:172-188 with Rust's saturating casts: 3e9 saturates to i32::MAX and fails the integer check,
+    # -1 fails the sign check, 31 the gain check (31 default gains); the oracle's restatement agrees on each
+    say("lambdarank label checks")
+    for bad, code, text in ((3e9, 1, "int type"), (-1.0, 2, "non-negative"), (31.0, 3, "label mappings")):
+        data = silvic_amd.synthetic(3, rows=5_000, seed=9)
+        data.label = data.label.copy()
+        data.label[17] = bad
+        assert oracle.check_labels(data.label, 31) == code
+        with pytest.raises(_abi.SilvicError) as e:
+            silvic_amd.Trainer(dict(objective="lambdarank", num_leaves=7, device_type="rocm"), data)
+        assert e.value.kind == "data" and text in str(e.value), (bad, str(e.value))
 
 
 @pytest.mark.parametrize("rows,params,rounds", [

@@ -229,3 +229,23 @@ def test_max_dcg_follows_lightgbm():
         3.0 * discount(2)
     assert oracle.max_dcg_at_k(3, [0.0, 0.0], gain) == 0.0
     assert oracle.max_dcg_at_k(10, [1.0], gain) == 1.0
+
+
+def test_label_checks_follow_rusts_saturating_casts():
+    # check_labels (lambdarank.rs:172-188) converts with Rust's `as`: NaN -> 0 and out-of-range values saturate, so a
+    # NaN label passes all three checks (and takes label 0's gain), 3e9 saturates to i32::MAX and fails the integer
+    # check, and -inf and +inf fail it too
+    nan = float("nan")
+    assert oracle.check_labels([0, 1, 4, 2], 5) == 0
+    assert oracle.check_labels([0, nan, 3], 5) == 0
+    assert oracle.check_labels([3e9], 5) == 1
+    assert oracle.check_labels([float("-inf")], 5) == 1
+    assert oracle.check_labels([float("inf")], 5) == 1
+    assert oracle.check_labels([1.5], 5) == 1
+    assert oracle.check_labels([-2.0], 5) == 2
+    assert oracle.check_labels([5.0], 5) == 3
+    assert oracle.check_labels([2.0e9], 5) == 3  # an integer in i32 range, past the gains
+    # a NaN label takes label 0's gain (lambdarank.rs:349) and its pairs compare as NaN (:391-396): finite gradients
+    scores = np.array([0.5, -1.0, 2.0, 0.1], np.float32)
+    gn, hn = oracle.lambdarank_query(scores, [nan, 2, 1, 3], [0.0, 1.0, 3.0, 7.0], 0.1)
+    assert np.isfinite(gn).all() and np.isfinite(hn).all()

@@ -1,6 +1,7 @@
-"""srocm_histogram_noalloc (the entry point that allocates nothing) against srocm_histogram, through the C ABI: two
-calls in a row, the second on a smaller leaf, each bit for bit equal to the allocating entry point's histogram.
-The device output buffer comes from the HIP runtime the library itself links (ctypes), not from torch."""
+"""srocm_histogram_noalloc (the entry point that allocates nothing) against srocm_histogram, through the C ABI: calls
+in a row, each on a smaller leaf, each bit for bit equal to the allocating entry point's histogram, with and without
+waiting; and the device's free memory unchanged over many calls. The device output buffer comes from the HIP runtime
+the library itself links (ctypes), not from torch."""
 
 import ctypes as C
 
@@ -19,12 +20,22 @@ def _hip():
     hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
     hip.hipFree.argtypes = [C.c_void_p]
     hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
     return hip
 
 
-def _noalloc(rocm, hip, dbuf, leaf, n):
-    rc = rocm._lib.srocm_histogram_noalloc(rocm._h, _abi.LeafRange(*leaf), dbuf, n, 1)
+def _free_bytes(hip):
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipDeviceSynchronize() == 0
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def _noalloc(rocm, hip, dbuf, leaf, n, wait=1):
+    rc = rocm._lib.srocm_histogram_noalloc(rocm._h, _abi.LeafRange(*leaf), dbuf, n, wait)
     rocm._check(rc)
+    if not wait:
+        assert hip.hipDeviceSynchronize() == 0
     out = np.empty(n, np.int64)
     assert hip.hipMemcpy(out.ctypes.data, dbuf, n * 8, 2) == 0  # hipMemcpyDeviceToHost
     return out
@@ -55,6 +66,16 @@ def test_noalloc_histogram_matches_the_allocating_one():
             assert np.array_equal(got.astype(np.float64), want), leaf
         # an empty leaf is zeros, as the allocating entry point's
         assert not _noalloc(rocm, hip, dbuf, (5, 0), n).any()
+        # without waiting: the result is there once the device has finished
+        want = rocm.histogram((left, rows - left))
+        assert np.array_equal(_noalloc(rocm, hip, dbuf, (left, rows - left), n, wait=0).astype(np.float64), want)
+        # no device memory is taken by the calls: the free bytes do not move over many of them, waiting or not
+        before = _free_bytes(hip)
+        for k in range(24):
+            leaf = (0, rows) if k % 3 == 0 else (left, rows - left) if k % 3 == 1 else (17, 4000 + k)
+            rc = rocm._lib.srocm_histogram_noalloc(rocm._h, _abi.LeafRange(*leaf), dbuf, n, k % 2)
+            rocm._check(rc)
+        assert _free_bytes(hip) == before
     finally:
         rocm.close()
         hip.hipFree(dbuf)
