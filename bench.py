@@ -227,6 +227,42 @@ def trace_summary(args):
         print(f"| `{k}` | {n / args.steps:.2f} | {us / args.steps:.1f} | {us / n:.1f} | {us / busy:.1%} |")
 
 
+def sector_floor(v, layout, args, trees):
+    """The HBM bytes per tree k_step_rows cannot avoid with this layout, from the device's sector counts (srocm_profile
+    mode 2) over the repeated iterations: 32 bytes per distinct sector its gathers touch (the split bins of the
+    parent rows, the packed gradients of the built rows), every built row's slab row whole, the row ids read and
+    written once, and the partials as written. Also the split-bin bytes if jobs that split on the same feature in a
+    step shared their sectors."""
+    prow, psec, brow, bsec, shared, partials, packed = v
+    trees = max(trees, 1)
+    first = layout[0] if layout else {"width": 128, "row_bytes": 128}
+    slab_sectors = -(-first["row_bytes"] // 32)
+    pbytes = 256 * first["width"] * 4
+    parts = {
+        "split_bins": 32.0 * psec, "gradients": 32.0 * bsec, "slab_rows": 32.0 * slab_sectors * brow,
+        "row_ids_read": 4.0 * prow, "row_ids_written": 4.0 * prow,
+        "partials": pbytes * packed + 2 * pbytes * (partials - packed),
+    }
+    floor = sum(parts.values())
+    algorithmic = 9.0 * prow + brow * (first["width"] + 4.0)
+    out = {k + "_per_tree": b / trees for k, b in parts.items()}
+    out.update({
+        "floor_bytes_per_tree": floor / trees,
+        "floor_over_algorithmic": floor / algorithmic if algorithmic else None,
+        "parent_rows_per_tree": prow / trees, "built_rows_per_tree": brow / trees,
+        "split_bin_sectors_per_parent_row": psec / prow if prow else None,
+        "gradient_sectors_per_built_row": bsec / brow if brow else None,
+        "split_bins_shared_per_step_per_tree": 32.0 * shared / trees,
+        "note": "one slab; 32-byte sectors; the first slab's partials (packed: 256 x width x 4 B, pairs twice that)",
+    })
+    log(f"sector model per tree: {prow / trees:.3g} parent rows ({psec / max(prow, 1):.3f} split-bin sectors a row), "
+        f"{brow / trees:.3g} built rows ({bsec / max(brow, 1):.3f} gradient sectors a row); floor "
+        f"{floor / trees / 1e9:.2f} GB = {out['floor_over_algorithmic']:.2f} x algorithmic; split bins "
+        f"{parts['split_bins'] / trees / 1e9:.2f} GB per job, {32.0 * shared / trees / 1e9:.2f} GB if a step's jobs "
+        f"shared sectors")
+    return out
+
+
 def copy_calibration(nbytes):
     """Four device-to-device copies of `nbytes` through the HIP runtime (its copy kernel reads and writes each byte
     once): the reference point for FETCH_SIZE / WRITE_SIZE counters."""
@@ -269,6 +305,10 @@ def main():
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="no GPU: summarize rocprofv3 --pmc runs of this script (FETCH_SIZE dir, WRITE_SIZE dir, and "
                          "optionally an LDS-counter dir) over its timed iterations (--warmup, --steps as in the run)")
+    ap.add_argument("--sector-model", action="store_true",
+                    help="in the repeat with kernel events, also count the distinct 32-byte sectors each split step's "
+                         "gathers touch (kernels between the steps; the timed iterations are unaffected) and report "
+                         "the traffic floor they set for k_step_rows")
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="no GPU: per-iteration kernel times of a rocprofv3 --kernel-trace run of this script over "
                          "its timed iterations (--warmup, --steps as in the run)")
@@ -327,19 +367,20 @@ def main():
     trainer = silvic_amd.Trainer(params, data)
     lib, h = trainer.backend._lib, trainer.backend._h
     trainer.step(args.warmup)
-    trainer.backend._check(lib.srocm_profile(h, 1))
+    trainer.backend._check(lib.srocm_profile(h, 2 if args.sector_model else 1))
     t1 = time.perf_counter()
     profiled = trainer.step(args.steps)
     elapsed_profiled = time.perf_counter() - t1
-    prof = (C.c_double * 15)()
-    trainer.backend._check(lib.srocm_profile_read(h, prof, 15))
+    prof = (C.c_double * 22)()
+    trainer.backend._check(lib.srocm_profile_read(h, prof, 22))
     trainer.backend._check(lib.srocm_profile(h, 0))
     same_trees = all(np.array_equal(a["split_feature"], b["split_feature"]) and
                      np.array_equal(a["threshold_bin"], b["threshold_bin"]) for a, b in zip(gpu_trees, trainer.trees))
     if not same_trees:
         log("the repeated iterations grew different trees")
     (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
-     part_rows, _, _, grow_steps, expansions, kept) = list(prof)
+     part_rows, _, _, grow_steps, expansions, kept) = list(prof)[:15]
+    sector_model = sector_floor(list(prof)[15:], layout, args, len(profiled)) if args.sector_model else None
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
     psteps = max(len(profiled), 1)
@@ -436,6 +477,8 @@ def main():
                                      "avg_launch_us": hist_ms / hist_launches * 1e3 if hist_launches else None}},
         "cpu_baseline": cpu,
     }
+    if sector_model:
+        out["roofline"]["sector_model"] = sector_model
     print(json.dumps(out), flush=True)
     trainer.backend.close()
 

@@ -386,7 +386,9 @@ int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
 int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size_t len, int wait);
 
 /* Per-kernel timing with HIP events on the backend's stream, and algorithmic byte counts; no counterpart in the
- * reference (a measurement hook). srocm_profile: enable (1) or disable (0); either resets the counters.
+ * reference (a measurement hook). srocm_profile: enable (1), enable with the sector model (2: after every split
+ * step's k_step_rows launches, kernels that count the sectors its gathers touch, values [15]-[21]), or disable (0);
+ * each resets the counters.
  * srocm_profile_read writes min(len, SROCM_PROFILE_VALUES) values:
  *   [0] k_hist launches (root and trait histograms, one per slab)   [1] their ms   [2] their algorithmic bytes
  *   [3] k_step_rows launches (split steps: partition + built-child histogram)   [4] their ms
@@ -394,9 +396,14 @@ int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size
  *   [6] histogram builds   [7] rows histogrammed   [8] rows x used columns   [9] rows partitioned
  *   [10] trait partition launches   [11] their ms (count + scatter + copy back)
  *   [12] device-growth split steps   [13] leaves they expanded   [14] of those, splits the trees kept
+ *   sector model (mode 2; split steps, the first slab): [15] parent rows partitioned   [16] distinct 32-byte sectors
+ *   of the column-major split-feature bins they lie in, per job   [17] built-child rows histogrammed   [18] distinct
+ *   sectors of the packed gradients they lie in   [19] split-bin sectors counted once per step over every job
+ *   splitting on the same feature   [20] partials written   [21] of those, packed (256 x slab width x 4 bytes; the
+ *   others {g, h} pairs, twice that)
  * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
  * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
-#define SROCM_PROFILE_VALUES 15
+#define SROCM_PROFILE_VALUES 22
 int srocm_profile(void *ctx, int enable);
 int srocm_profile_read(void *ctx, double *out, uint32_t len);
 

@@ -316,11 +316,19 @@ struct Profile {
     double builds = 0, rows = 0, bins = 0, part_rows = 0;
     double part_launches = 0, part_ms = 0;                  // trait partitions
     double steps = 0, expansions = 0, splits = 0;           // device growth: split steps, leaves expanded, kept
+    // the sector model of the split steps' gathers (srocm_profile mode 2; k_sector_model): parent rows, their
+    // split-bin sectors, built rows, their gradient sectors, split-bin sectors shared over each step's jobs,
+    // partials written, of those packed
+    bool sectors = false;
+    DevBuf<unsigned long long> sector_counts;
+    DevBuf<uint32_t> sector_bits;
+    double sector[7] = {0, 0, 0, 0, 0, 0, 0};
     std::vector<hipEvent_t> pool;
     void reset() {
         hist_launches = hist_ms = hist_bytes = step_launches = step_ms = step_bytes = 0;
         builds = rows = bins = part_rows = part_launches = part_ms = 0;
         steps = expansions = splits = 0;
+        for (double &v : sector) v = 0;
     }
 };
 
@@ -1865,10 +1873,36 @@ struct Context {
     void profile(int enable) {
         settle_profile();
         prof.on = enable != 0;
+        prof.sectors = enable == 2;
         prof.reset();
+        if (prof.sectors) {
+            prof.sector_counts.alloc(8);
+            hip_check(hipMemsetAsync(prof.sector_counts.p, 0, 8 * sizeof(unsigned long long), stream), "zero sectors");
+            const uint64_t words = sector_bit_words();
+            prof.sector_bits.alloc(words);
+            hip_check(hipMemsetAsync(prof.sector_bits.p, 0, words * 4, stream), "zero sector bits");
+        }
+    }
+    uint64_t sectors_per_col() const { return div_up(std::max<uint64_t>(rows, 1), col16 ? 16 : 32); }
+    uint64_t sector_bit_words() const { return div_up(static_cast<uint64_t>(nt_feat.size()) * sectors_per_col(), 32); }
+    // after a split step's k_step_rows launches: the distinct sectors its gathers touch (measurement only)
+    void sector_model(uint32_t parity) {
+        if (!prof.sectors) return;
+        k_sector_model<<<dim3(64, JMAX), 256, 0, stream>>>(d_plans.p + parity, part.p, part2.p, col16, prof.sector_bits.p,
+                                                          sectors_per_col(), d_fmt.p, prof.sector_counts.p);
+        launch_check("k_sector_model");
+        k_sector_bits<<<std::min<uint64_t>(div_up(sector_bit_words(), 256), cus * 4), 256, 0, stream>>>(
+            prof.sector_bits.p, sector_bit_words(), prof.sector_counts.p);
+        launch_check("k_sector_bits");
     }
     void settle_profile() {
         sync();
+        if (prof.sectors && prof.sector_counts.p) {
+            unsigned long long c[8];
+            hip_check(hipMemcpy(c, prof.sector_counts.p, sizeof(c), hipMemcpyDeviceToHost), "read sectors");
+            for (int k = 0; k < 7; ++k) prof.sector[k] += static_cast<double>(c[k]);
+            hip_check(hipMemset(prof.sector_counts.p, 0, sizeof(c)), "zero sectors");
+        }
         auto settle = [&](std::vector<std::pair<hipEvent_t, hipEvent_t>> &events, double &total) {
             for (auto &e : events) {
                 float ms = 0;
@@ -2051,6 +2085,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     hip_check(hipEventRecord(e1, stream), "event");
                     prof.step_events.emplace_back(e0, e1);
                     prof.step_launches += static_cast<double>(launches);
+                    sector_model(parity);
                 }
                 ReduceStepArgs ra{step_partial.p, d_fmt.p, d_cgs.p, d_plans.p + parity, slab_slot_flat.p};
                 k_step_reduce<<<reduce_blocks(), 256, 0, stream>>>(g, ra);
@@ -2208,12 +2243,25 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
             hip_check(hipMemcpyAsync(d_merges.p, h_fix.p + rb, mb, hipMemcpyHostToDevice, stream), "upload merges");
             hip_check(hipMemcpyAsync(d_starts.p, h_fix.p + rb + mb, sb, hipMemcpyHostToDevice, stream), "upload merges");
             longest = 1;
-            for (const MergeJob &m : merges) longest = std::max(longest, m.count);
-            dim3 grid(std::min<uint32_t>(div_up(longest, 256 * 4), 64), static_cast<uint32_t>(merges.size()));
-            k_merge_runs<<<grid, 256, 0, stream>>>(d_merges.p, d_starts.p, part.p, part2.p);
-            launch_check("k_merge_runs");
-            k_copy_back<<<grid, 256, 0, stream>>>(d_merges.p, part2.p, part.p);
-            launch_check("k_copy_back");
+            uint32_t most = 1;
+            for (const MergeJob &m : merges) {
+                longest = std::max(longest, m.count);
+                most = std::max(most, m.runs);
+            }
+            dim3 grid(std::min<uint32_t>(div_up(longest, 256 * 4), 256), static_cast<uint32_t>(merges.size()));
+            // pairwise rounds between the two buffers, every leaf's rows moved in each; an odd count leaves the
+            // result in the second buffer
+            uint32_t rounds = 0;
+            while ((1u << rounds) < most) ++rounds;
+            for (uint32_t t = 0; t < rounds; ++t) {
+                const bool even = (t & 1u) == 0;
+                k_merge_round<<<grid, 256, 0, stream>>>(d_merges.p, d_starts.p, t, even ? part.p : part2.p, even ? part2.p : part.p);
+                launch_check("k_merge_round");
+            }
+            if (rounds & 1u) {
+                k_copy_back<<<grid, 256, 0, stream>>>(d_merges.p, part2.p, part.p);
+                launch_check("k_copy_back");
+            }
         }
     }
     if (prof.on && root_searched) {  // the root histogram was counted by launch_hist
@@ -2754,7 +2802,8 @@ int srocm_profile_read(void *ctx, double *out, uint32_t len) {
         const Profile &p = c.prof;
         double v[SROCM_PROFILE_VALUES] = {p.hist_launches, p.hist_ms, p.hist_bytes, p.step_launches, p.step_ms, p.step_bytes,
                                           p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms,
-                                          p.steps, p.expansions, p.splits};
+                                          p.steps, p.expansions, p.splits, p.sector[0], p.sector[1], p.sector[2],
+                                          p.sector[3], p.sector[4], p.sector[5], p.sector[6]};
         if (out) std::copy(v, v + std::min<uint32_t>(len, SROCM_PROFILE_VALUES), out);
     });
 }

@@ -2368,35 +2368,45 @@ __global__ void k_consolidate(const RowRun *__restrict__ runs, const uint32_t *_
     }
 }
 
-// A leaf whose expansion was dropped holds its rows as ascending runs (its speculative descendants' rows). Each
-// row's place in the leaf is its place in its run plus the rows below it in every other run (binary searches,
-// the rows of a leaf being distinct). Writes the merged leaf into the second buffer. grid: (x, leaves).
+// A leaf whose expansion was dropped holds its rows as ascending runs (its speculative descendants' rows), which
+// pairwise merge rounds bring back into one ascending run: in round t, runs 2m and 2m + 1 of the level-t runs (each
+// the merge of 2^t consecutive original runs, its start starts[min(p << t, runs)]) become one, a row's place being
+// its place in its run plus the rows below it in the partner run (a binary search; the rows of a leaf are distinct).
+// ceil(log2(runs)) rounds, each moving every row once from `src` to `dst`, so a leaf costs its rows times the rounds,
+// not times its runs. grid: (x, leaves).
 struct MergeJob {
     uint32_t begin, count;
     uint32_t first, runs;  // the runs' starts (relative to begin) are starts[first, first + runs], then `count`
 };
 
-__global__ void k_merge_runs(const MergeJob *__restrict__ jobs, const uint32_t *__restrict__ starts,
-                             const uint32_t *__restrict__ buf0, uint32_t *__restrict__ buf1) {
+__global__ void k_merge_round(const MergeJob *__restrict__ jobs, const uint32_t *__restrict__ starts, uint32_t t,
+                              const uint32_t *__restrict__ src, uint32_t *__restrict__ dst) {
     const MergeJob m = jobs[blockIdx.y];
     const uint32_t *s = starts + m.first;
-    const uint32_t *leaf = buf0 + m.begin;
+    const uint32_t *leaf = src + m.begin;
+    const uint32_t nr = (m.runs + (1u << t) - 1u) >> t;  // level-t runs
+    auto start = [&](uint32_t p) { return s[min(p << t, m.runs)]; };
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < m.count; i += gridDim.x * blockDim.x) {
-        uint32_t p = 0;
-        while (p + 1 < m.runs && s[p + 1] <= i) ++p;
-        const uint32_t v = leaf[i];
-        uint32_t rank = i - s[p];
-        for (uint32_t q = 0; q < m.runs; ++q) {
-            if (q == p) continue;
-            uint32_t lo = s[q], hi = s[q + 1];  // rows of run q below v: the first position in it holding more
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (leaf[mid] < v) lo = mid + 1;
-                else hi = mid;
-            }
-            rank += lo - s[q];
+        uint32_t lo = 0, hi = nr;  // the run holding i: the last p with start(p) <= i
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (start(mid) <= i) lo = mid;
+            else hi = mid;
         }
-        buf1[m.begin + rank] = v;
+        const uint32_t p = lo, q = p ^ 1u;
+        const uint32_t v = leaf[i];
+        uint32_t pos = i;
+        if (q < nr) {
+            uint32_t a = start(q), b = start(q + 1);  // rows of run q below v: the first position holding more
+            const uint32_t base = a;
+            while (a < b) {
+                const uint32_t mid = (a + b) >> 1;
+                if (leaf[mid] < v) a = mid + 1;
+                else b = mid;
+            }
+            pos = start(p & ~1u) + (i - start(p)) + (a - base);
+        }
+        dst[m.begin + pos] = v;
     }
 }
 
@@ -2508,7 +2518,8 @@ struct AdvShared {
     uint16_t cx[MAXL];                    // commit c: the leaf id split
     int16_t cpn[MAXL];                    // commit c: the split leaf's node above
     uint8_t cleft[MAXL];                  // commit c: the split leaf was its node's left child
-    uint64_t ckey[CAND];                  // speculation candidates' keys: higher gain (as f32), then lower leaf
+    uint64_t ckey[CAND];                  // speculation candidates' keys (higher bound, gain, then lower leaf);
+                                          // before them, frontier_bounds' parent links
     uint32_t crank[CAND];                 // and their ranks
     uint16_t cand[CAND];                  // speculation candidates
     uint16_t job_t[JMAX];
@@ -2977,6 +2988,76 @@ __device__ void apply_commits(const GrowState &g, const AdvShared<MAXL> &s, uint
     }
 }
 
+// Each speculative leaf's bound after the replay: the smallest gain (as f32) on its path from the committed leaf
+// above it (that leaf included) down to it, the order in which best_leaf would reach it (a leaf is committed before
+// another whose bound is lower, since every leaf on its path must be committed first and each is the largest gain
+// when it is). Into the .x half of each leaf's s.gain word (the replay's exact gains are no longer read), the leaf's
+// gain as f32 in .y; leaves not below a committed leaf (the committed tree's nodes) get -1. Pointer jumping over
+// parent links kept in the s.ckey words: a leaf's link is its parent until it meets a committed leaf, each round
+// takes the minimum with its link's and doubles the link's reach, so ceil(log2(depth)) + 1 rounds end it (at most
+// 16, which covers any tree of the sizes here). Block-wide.
+template <uint32_t MAXL>
+__device__ void frontier_bounds(AdvShared<MAXL> &s, uint32_t ntent, uint32_t n) {
+    constexpr uint32_t PER = (AdvShared<MAXL>::TCAP + 511) / 512;  // leaves a thread (blocks of at least 512)
+    constexpr uint32_t NONE = 0xffffu, UNDER = 1u << 16;             // link: bits 0-15; bit 16: below a committed leaf
+    static_assert(AdvShared<MAXL>::TCAP < NONE, "leaf links fit 16 bits");
+    static_assert(sizeof(s.ckey) >= sizeof(uint32_t) * AdvShared<MAXL>::TCAP, "the links fit the key words");
+    uint32_t *link = reinterpret_cast<uint32_t *>(s.ckey);
+    float2 *bw = reinterpret_cast<float2 *>(s.gain);
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    for (uint32_t k = tid; k < ntent; k += nt) link[k] = NONE;
+    __syncthreads();
+    for (uint32_t k = tid; k < ntent; k += nt) {
+        const uint32_t m = s.meta[k];
+        const double gk = s.gain[k];
+        if (((m >> 1) & 3u) != T_LEAF && (m >> 3) != 0u) {  // expanded or planned: its children are kid, kid + 1
+            const uint32_t kid = (m >> 3) - 1u;
+            link[kid] = k;
+            link[kid + 1] = k;
+        }
+        const float gf = (m & 1u) && gk == gk ? static_cast<float>(gk) : -1.0f;
+        bw[k] = make_float2(gf, gf);  // read after the barrier below
+    }
+    __syncthreads();
+    for (uint32_t id = tid; id < n; id += nt) link[s.leaf_t[id]] = UNDER | NONE;  // the committed leaves: the path's top
+    __syncthreads();
+    for (int round = 0; round < 16; ++round) {
+        uint32_t nl[PER];
+        float nb[PER];
+        bool moved = false;
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) {
+            const uint32_t k = tid + nt * i;
+            nl[i] = NONE;
+            nb[i] = 0.0f;
+            if (k >= ntent) continue;
+            const uint32_t l = link[k];
+            nl[i] = l;
+            nb[i] = bw[k].x;
+            if ((l & NONE) != NONE) {
+                const uint32_t u = l & NONE, lu = link[u];
+                nb[i] = fminf(nb[i], bw[u].x);
+                nl[i] = (l & UNDER) | (lu & UNDER) | (lu & NONE);
+                moved = true;
+            }
+        }
+        const bool any = __syncthreads_or(moved ? 1 : 0) != 0;
+#pragma unroll
+        for (uint32_t i = 0; i < PER; ++i) {
+            const uint32_t k = tid + nt * i;
+            if (k < ntent) {
+                link[k] = nl[i];
+                bw[k].x = nb[i];
+            }
+        }
+        __syncthreads();
+        if (!any) break;
+    }
+    for (uint32_t k = tid; k < ntent; k += nt)
+        if (!(link[k] & UNDER)) bw[k].x = -1.0f;
+    __syncthreads();
+}
+
 template <uint32_t MAXL>
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     AdvShared<MAXL> &s = *reinterpret_cast<AdvShared<MAXL> *>(scratch);
@@ -3027,16 +3108,21 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         return;
     }
 
-    // -- speculation candidates: unexpanded leaves with a positive gain, the blocker aside
+    // -- speculation candidates: unexpanded leaves with a positive gain, the blocker aside, in the order best_leaf
+    // would reach them: by bound (frontier_bounds), then gain, then lower leaf
     const uint32_t blocker = s.blocker;
+    frontier_bounds<MAXL>(s, ntent, n);
+    const float2 *bw = reinterpret_cast<const float2 *>(s.gain);
     for (uint32_t k = tid; k < ntent; k += nt) {
         const uint32_t m = s.meta[k];
-        const double gk = s.gain[k];
-        if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && gk > 0.0 && k != blocker) {
+        const float2 b = bw[k];
+        if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && b.y > 0.0f && b.x > 0.0f && k != blocker) {
             const uint32_t at = atomicAdd(&s.ncand, 1u);
             s.cand[at] = static_cast<uint16_t>(k);
-            // a positive f32's bits order as the value: the key orders by gain to f32 precision, then lower leaf
-            s.ckey[at] = (static_cast<uint64_t>(__float_as_uint(static_cast<float>(gk))) << 32) | (0xffffffffu - k);
+            // positive f32 bits order as the values: bound, then the top 19 bits of the gain below the sign, then
+            // the lower leaf (13 bits: leaf ids are below 8192)
+            s.ckey[at] = (static_cast<uint64_t>(__float_as_uint(b.x)) << 32) |
+                         (static_cast<uint64_t>(__float_as_uint(b.y) >> 12) << 13) | (8191u - k);
             s.crank[at] = 0;
         }
     }
@@ -3788,6 +3874,80 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     }
     flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
     if (tid == 0) R.fmt[wg] = 0u;
+}
+
+// Measurement only (profile mode): the distinct 32-byte sectors a split step's gathers must touch, from the step's
+// own plan and partition buffers, right after its k_step_rows launches. Per job, over the parent's rows (ascending in
+// row id, whatever order they are stored in): the sectors of the column-major split-feature array their bins lie in
+// (32 rows a sector, 16 for two-byte bins) and, over the built child's rows (sorted too), the sectors of the packed
+// gradient array (8 rows a sector). A sorted run of rows touches as many sectors as it has distinct row / rows-per-
+// sector values, so each is a count of the positions where that value changes. `shared`, when set, is one bit per
+// (column-major feature, split-bin sector), or-ed over every job of the step: the sectors the step would touch if
+// jobs that split on the same feature shared them. counters: [0] parent rows, [1] their split-bin sectors, [2]
+// built rows, [3] their gradient sectors, [5] partials written (the first slab's workgroups of histogrammed jobs),
+// [6] of those, packed ones (`fmt`: the first slab's partial formats). grid: (x, JMAX).
+__global__ __launch_bounds__(256) void k_sector_model(const StepPlan *plan, const uint32_t *buf0, const uint32_t *buf1,
+                                                      uint32_t col16, uint32_t *shared, uint64_t sectors_per_col,
+                                                      const uint32_t *fmt, unsigned long long *counters) {
+    __shared__ unsigned long long part[4];
+    const StepPlan &P = *plan;
+    const uint32_t j = blockIdx.y;
+    if (threadIdx.x < 4) part[threadIdx.x] = 0;
+    if (j < P.njobs && blockIdx.x == 0 && threadIdx.x == 0 && P.jobs[j].hist) {
+        const JobPlan &J = P.jobs[j];
+        unsigned long long packed = 0;
+        for (uint32_t k = 0; k < J.groups; ++k) packed += fmt[J.group_base + k] ? 1ull : 0ull;
+        atomicAdd(counters + 5, static_cast<unsigned long long>(J.groups));
+        atomicAdd(counters + 6, packed);
+    }
+    __syncthreads();
+    if (j < P.njobs) {
+        const JobPlan &J = P.jobs[j];
+        const uint32_t *src = J.src_buf ? buf1 : buf0, *dst = J.src_buf ? buf0 : buf1;
+        const uint32_t sshift = col16 ? 4u : 5u;
+        unsigned long long prow = 0, psec = 0, brow = 0, bsec = 0;
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < J.count; i += gridDim.x * blockDim.x) {
+            const uint32_t at = J.src_rev ? J.begin + J.count - 1 - i : J.begin + i;
+            const uint32_t r = src[at];
+            ++prow;
+            if (i == 0 || (src[J.src_rev ? at + 1 : at - 1] >> sshift) != (r >> sshift)) ++psec;
+            if (shared) {
+                const uint64_t bit = static_cast<uint64_t>(J.col) * sectors_per_col + (r >> sshift);
+                atomicOr(shared + (bit >> 5), 1u << (bit & 31u));
+            }
+        }
+        if (J.hist) {
+            // the built child: the left one first-first at begin, the right one last-first after the left rows
+            const uint32_t b = J.built_side == 0 ? J.begin : J.begin + J.left;
+            const uint32_t n = J.built_side == 0 ? J.left : J.count - J.left;
+            for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+                const uint32_t r = dst[b + i];
+                ++brow;
+                if (i == 0 || (dst[b + i - 1] >> 3) != (r >> 3)) ++bsec;
+            }
+        }
+        atomicAdd(&part[0], prow);
+        atomicAdd(&part[1], psec);
+        atomicAdd(&part[2], brow);
+        atomicAdd(&part[3], bsec);
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 && part[threadIdx.x]) atomicAdd(counters + threadIdx.x, part[threadIdx.x]);
+}
+
+// Measurement only: the set bits of k_sector_model's shared-sector bitmap into counters[4], the bitmap cleared.
+__global__ __launch_bounds__(256) void k_sector_bits(uint32_t *bits, uint64_t words, unsigned long long *counters) {
+    unsigned long long c = 0;
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < words;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint32_t w = bits[i];
+        if (w) {
+            c += static_cast<unsigned long long>(__popc(w));
+            bits[i] = 0;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) c += static_cast<unsigned long long>(__shfl_xor(static_cast<long long>(c), o));
+    if ((threadIdx.x & 63u) == 0 && c) atomicAdd(counters + 4, c);
 }
 
 // Four columns of one slab: a work unit of k_step_reduce and k_step_scan.
