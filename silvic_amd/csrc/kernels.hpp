@@ -2193,7 +2193,6 @@ __device__ __forceinline__ uint32_t wave_excl_sum(uint32_t v) { return wave_incl
 __device__ __forceinline__ uint32_t wave_total(uint32_t v) { return __shfl(wave_incl_sum(v), 63); }
 
 constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
-constexpr uint32_t SPEC_FLOOR = 4;         // speculative expansions a step may add whatever the budget
 constexpr uint32_t SPEC_FEW = 8;           // at most this many: picked by repeated wave maxima (top_few)
 constexpr uint32_t GROW_MAX_LEAVES = 2048;  // num_leaves of a device-grown tree at most
 // Speculative leaves of a tree of num_leaves: 4 per leaf up to 512 leaves, then 2 per further leaf (the expansions
@@ -2525,7 +2524,7 @@ struct AdvShared {
     uint16_t job_t[JMAX];
     uint64_t skey[JMAX];                  // select_top: the selected candidates' keys
     uint16_t scand[JMAX];                 // and leaves
-    uint32_t ncand, ncommit, n, blocker, done, njobs, band, above, nsel;
+    uint32_t ncand, ncommit, n, blocker, done, njobs, band, above, nsel, neligible;
 };
 
 __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
@@ -3058,6 +3057,60 @@ __device__ void frontier_bounds(AdvShared<MAXL> &s, uint32_t ntent, uint32_t n) 
     __syncthreads();
 }
 
+// The bits of the R-th highest bound (frontier_bounds, positive f32 bits order as the values) among the leaves the
+// tree may still commit: the unexpanded leaves with a split and a positive gain (the blocker among them) and the
+// expanded ones not yet committed; 0 when there are fewer than R of them. best_leaf commits a leaf before any of
+// lower bound, so a leaf below this bound is not among the next R commits and expanding it now is wasted. A radix
+// selection over the bound bits, 8 at a time from the top (s.crank: 256 counts). Block-wide.
+template <uint32_t MAXL>
+__device__ uint32_t pool_threshold(AdvShared<MAXL> &s, uint32_t ntent, uint32_t R) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, nt = blockDim.x;
+    const float2 *bw = reinterpret_cast<const float2 *>(s.gain);
+    uint32_t *count = s.crank;
+    auto bound_bits = [&](uint32_t k) -> uint32_t {  // 0: not in the pool
+        const uint32_t m = s.meta[k], st = (m >> 1) & 3u;
+        const float2 b = bw[k];
+        const bool in = b.x > 0.0f && (st == T_EXPANDED || (st == T_LEAF && (m & 1u) && b.y > 0.0f));
+        return in ? __float_as_uint(b.x) : 0u;
+    };
+    uint32_t prefix = 0, mask = 0, above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (uint32_t i = tid; i < 256u; i += nt) count[i] = 0;
+        __syncthreads();
+        for (uint32_t k = tid; k < ntent; k += nt) {
+            const uint32_t v = bound_bits(k);
+            if (v && (v & mask) == prefix) atomicAdd(&count[(v >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {  // lane l: buckets 255 - 4 l down to 252 - 4 l
+            uint32_t c = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) c += count[255u - 4u * lane - static_cast<uint32_t>(q)];
+            const uint32_t incl = wave_incl_sum(c), before = incl - c;
+            const unsigned long long hit = __ballot(above + incl >= R);
+            if (!hit) {
+                if (lane == 0) s.band = 256u;  // fewer than R in the pool
+            } else if (lane == static_cast<uint32_t>(__builtin_ctzll(hit))) {
+                uint32_t acc = above + before, b = 255u - 4u * lane;
+                for (int q = 0; q < 4; ++q, --b) {
+                    if (acc + count[b] >= R) break;
+                    acc += count[b];
+                }
+                s.band = b;
+                s.above = acc;
+            }
+        }
+        __syncthreads();
+        const uint32_t b = s.band;
+        if (b == 256u) return 0u;  // uniform
+        above = s.above;
+        prefix |= b << shift;
+        mask |= 255u << shift;
+        __syncthreads();  // the counts are read before the next round clears them
+    }
+    return prefix;
+}
+
 template <uint32_t MAXL>
 __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     AdvShared<MAXL> &s = *reinterpret_cast<AdvShared<MAXL> *>(scratch);
@@ -3112,11 +3165,16 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     // would reach them: by bound (frontier_bounds), then gain, then lower leaf
     const uint32_t blocker = s.blocker;
     frontier_bounds<MAXL>(s, ntent, n);
+    const uint32_t R = L - n;  // splits left, this step's blocker included
+    const uint32_t cut = pool_threshold<MAXL>(s, ntent, R);
+    if (tid == 0) s.neligible = 0;
+    __syncthreads();
     const float2 *bw = reinterpret_cast<const float2 *>(s.gain);
     for (uint32_t k = tid; k < ntent; k += nt) {
         const uint32_t m = s.meta[k];
         const float2 b = bw[k];
         if ((m & 1u) && ((m >> 1) & 3u) == T_LEAF && b.y > 0.0f && b.x > 0.0f && k != blocker) {
+            if (__float_as_uint(b.x) >= cut) atomicAdd(&s.neligible, 1u);
             const uint32_t at = atomicAdd(&s.ncand, 1u);
             s.cand[at] = static_cast<uint16_t>(k);
             // positive f32 bits order as the values: bound, then the top 19 bits of the gain below the sign, then
@@ -3128,9 +3186,10 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     }
     __syncthreads();
     const uint32_t ncand = s.ncand;
-    const uint32_t R = L - n;  // splits left, this step's blocker included
     const uint32_t pending = pending0 - nc;
-    uint32_t spec = R > pending + 1u + SPEC_FLOOR ? R - pending - 1u : SPEC_FLOOR;
+    // the candidates among the R leaves of highest bound (pool_threshold), at most JMAX - 1; being the highest keys,
+    // the ones the selection below takes are exactly those
+    uint32_t spec = s.neligible;
     if (spec > JMAX - 1) spec = JMAX - 1;
     // room for this step and every later blocker (each commits, so at most R of them in all)
     const uint32_t free_t = g.tcap - ntent, free_s = g.nslots - slot0;
