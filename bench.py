@@ -82,14 +82,16 @@ def timed_window(rows, warmup, steps):
     return rows[begin(warmup):begin(warmup + steps)]
 
 
-def step_kernels(layout):
+def step_kernels(layout, quant_bins):
     """The k_step_rows instances the backend launches for a slab layout (RocmBackend.slab_layout()), with their
-    slab counts."""
+    slab counts: the last parameter says the built rows' gradients travel as one-byte codes beside the row ids
+    (units of at most 7 and 15, i.e. num_grad_quant_bins up to 14, and no separate counters)."""
     out = {}
     for sl in layout:
         dp = (4 if sl["row_bytes"] <= 1024 else 8) if sl["dense"] else 0
+        codes = not sl["q32"] and quant_bins <= 14
         k = (f"k_step_rows<{sl['width']}, {'true' if sl['wide'] else 'false'}, {max(sl['pack'], 1)}, "
-             f"{'true' if sl['q32'] else 'false'}, {dp}>")
+             f"{'true' if sl['q32'] else 'false'}, {dp}, {'true' if codes else 'false'}>")
         out[k] = out.get(k, 0) + 1
     return ", ".join(f"{k} x{n}" for k, n in out.items())
 
@@ -121,6 +123,7 @@ def pmc_summary(args):
     fetch_dir, write_dir = args.pmc_summary[:2]
     lds_dir = args.pmc_summary[2] if len(args.pmc_summary) > 2 else None
     out = []
+    extra = []
     per_tree = {}
     launches = {}
     scale = {}
@@ -162,6 +165,43 @@ def pmc_summary(args):
             lpt = launches.get(k, 0) / args.steps
             out.append(f"traffic_bytes_per_tree {k}: {t:.0f}")
             out.append(f"traffic_bytes_per_launch {k}: {t / lpt if lpt else 0:.0f}")
+    if args.pmc_sizes:
+        # the read requests by size: true bytes 32 / 64 / 128 a request, beside FETCH_SIZE scaled by the copy (which
+        # reads 128-byte requests, so its scale fits 128-byte traffic only)
+        order, vals = read_counters(args.pmc_sizes)
+        first_load = next((i for i, r in enumerate(order) if "k_repack" in r["Kernel_Name"]), len(order))
+        names = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_sum")
+        copies = [vals[int(r["Dispatch_Id"])] for r in order[:first_load] if "copyBuffer" in r["Kernel_Name"]][:4]
+        sizes = {}
+        for r in timed_window(order, args.warmup, args.steps):
+            k = kernel_key(r["Kernel_Name"])
+            a = sizes.setdefault(k, dict.fromkeys(names, 0.0))
+            for c in names:
+                a[c] += vals[int(r["Dispatch_Id"])].get(c, 0.0) / args.steps
+        out.append("")
+        out.append("Read requests by size (`TCC_EA0_RDREQ_32B/64B/128B`, all of `TCC_EA0_RDREQ`), per tree; bytes = 32, "
+                   "64 and 128 a request:")
+        out.append("")
+        if copies:
+            c = copies[0]
+            n32, n64, n128 = (c.get(x, 0.0) for x in names[:3])
+            out.append(f"- calibration copy of {args.calibrate_copy} MiB: {n32:.0f} x 32 B + {n64:.0f} x 64 B + {n128:.0f} "
+                       f"x 128 B = {(32 * n32 + 64 * n64 + 128 * n128) / 2**20:.1f} MiB read")
+        out.append("")
+        out.append("| kernel | 32 B requests | 64 B requests | 128 B requests | all requests | read MB by request size | "
+                   "FETCH_SIZE x copy scale, MB |")
+        out.append("|---|---:|---:|---:|---:|---:|---:|")
+        for k in rank[:8]:
+            a = sizes.get(k)
+            if not a:
+                continue
+            b = 32 * a[names[0]] + 64 * a[names[1]] + 128 * a[names[2]]
+            out.append(f"| `{k}` | {a[names[0]]:.3g} | {a[names[1]]:.3g} | {a[names[2]]:.3g} | {a[names[3]]:.3g} | "
+                       f"{b / 1e6:.1f} | {per_tree[k].get('FETCH_SIZE', 0.0) / 1e6:.1f} |")
+            if k.startswith("k_step_rows") or k.startswith("k_hist<"):
+                extra.append(f"read_bytes_by_request_size_per_tree {k}: {b:.0f}")
+        out.append("")
+        out.extend(extra)
     if lds_dir:
         order, vals = read_counters(lds_dir)
         win = timed_window(order, args.warmup, args.steps)
@@ -227,39 +267,44 @@ def trace_summary(args):
         print(f"| `{k}` | {n / args.steps:.2f} | {us / args.steps:.1f} | {us / n:.1f} | {us / busy:.1%} |")
 
 
-def sector_floor(v, layout, args, trees):
-    """The HBM bytes per tree k_step_rows cannot avoid with this layout, from the device's sector counts (srocm_profile
-    mode 2) over the repeated iterations: 32 bytes per distinct sector its gathers touch (the split bins of the
-    parent rows, the packed gradients of the built rows), every built row's slab row whole, the row ids read and
+def line_floor(v, layout, args, trees):
+    """The HBM bytes per tree k_step_rows cannot avoid with this layout, from the device's line counts (srocm_profile
+    mode 2) over the repeated iterations: every L2 miss fetches a 128-byte line (the request-size counters show no
+    other size), so 128 bytes per distinct line its gathers touch (the split bins of the parent rows, the packed
+    gradients of the built rows), every built row's slab row whole, the row ids read once (whole lines) and
     written once, and the partials as written. Also the split-bin bytes if jobs that split on the same feature in a
-    step shared their sectors."""
-    prow, psec, brow, bsec, shared, partials, packed = v
+    step shared their lines, and the sparse jobs' share (fewer than two parent rows a split-bin line)."""
+    prow, plines, brow, blines, shared, partials, packed, sp_rows, sp_lines, sp_built = v
     trees = max(trees, 1)
     first = layout[0] if layout else {"width": 128, "row_bytes": 128}
-    slab_sectors = -(-first["row_bytes"] // 32)
+    slab_lines = -(-first["row_bytes"] // 128)
     pbytes = 256 * first["width"] * 4
     parts = {
-        "split_bins": 32.0 * psec, "gradients": 32.0 * bsec, "slab_rows": 32.0 * slab_sectors * brow,
+        "split_bins": 128.0 * plines, "gradients": 128.0 * blines, "slab_rows": 128.0 * slab_lines * brow,
         "row_ids_read": 4.0 * prow, "row_ids_written": 4.0 * prow,
         "partials": pbytes * packed + 2 * pbytes * (partials - packed),
     }
     floor = sum(parts.values())
+    reads = parts["split_bins"] + parts["gradients"] + parts["slab_rows"] + parts["row_ids_read"]
     algorithmic = 9.0 * prow + brow * (first["width"] + 4.0)
     out = {k + "_per_tree": b / trees for k, b in parts.items()}
     out.update({
-        "floor_bytes_per_tree": floor / trees,
+        "floor_bytes_per_tree": floor / trees, "floor_read_bytes_per_tree": reads / trees,
         "floor_over_algorithmic": floor / algorithmic if algorithmic else None,
         "parent_rows_per_tree": prow / trees, "built_rows_per_tree": brow / trees,
-        "split_bin_sectors_per_parent_row": psec / prow if prow else None,
-        "gradient_sectors_per_built_row": bsec / brow if brow else None,
-        "split_bins_shared_per_step_per_tree": 32.0 * shared / trees,
-        "note": "one slab; 32-byte sectors; the first slab's partials (packed: 256 x width x 4 B, pairs twice that)",
+        "split_bin_lines_per_parent_row": plines / prow if prow else None,
+        "gradient_lines_per_built_row": blines / brow if brow else None,
+        "split_bins_shared_per_step_per_tree": 128.0 * shared / trees,
+        "sparse_jobs": {"parent_rows_per_tree": sp_rows / trees, "split_bin_lines_per_tree": sp_lines / trees,
+                        "built_rows_per_tree": sp_built / trees},
+        "note": "one slab; 128-byte lines; the first slab's partials (packed: 256 x width x 4 B, pairs twice that)",
     })
-    log(f"sector model per tree: {prow / trees:.3g} parent rows ({psec / max(prow, 1):.3f} split-bin sectors a row), "
-        f"{brow / trees:.3g} built rows ({bsec / max(brow, 1):.3f} gradient sectors a row); floor "
-        f"{floor / trees / 1e9:.2f} GB = {out['floor_over_algorithmic']:.2f} x algorithmic; split bins "
-        f"{parts['split_bins'] / trees / 1e9:.2f} GB per job, {32.0 * shared / trees / 1e9:.2f} GB if a step's jobs "
-        f"shared sectors")
+    log(f"line model per tree: {prow / trees:.3g} parent rows ({plines / max(prow, 1):.3f} split-bin lines a row), "
+        f"{brow / trees:.3g} built rows ({blines / max(brow, 1):.3f} gradient lines a row); floor "
+        f"{floor / trees / 1e9:.2f} GB ({reads / trees / 1e9:.2f} GB read) = {out['floor_over_algorithmic']:.2f} x "
+        f"algorithmic; split bins {parts['split_bins'] / trees / 1e9:.2f} GB per job, {128.0 * shared / trees / 1e9:.2f} "
+        f"GB if a step's jobs shared lines; sparse jobs: {sp_rows / trees:.3g} parent rows, {sp_lines / trees:.3g} "
+        f"lines, {sp_built / trees:.3g} built rows")
     return out
 
 
@@ -305,10 +350,13 @@ def main():
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="no GPU: summarize rocprofv3 --pmc runs of this script (FETCH_SIZE dir, WRITE_SIZE dir, and "
                          "optionally an LDS-counter dir) over its timed iterations (--warmup, --steps as in the run)")
-    ap.add_argument("--sector-model", action="store_true",
-                    help="in the repeat with kernel events, also count the distinct 32-byte sectors each split step's "
+    ap.add_argument("--line-model", action="store_true",
+                    help="in the repeat with kernel events, also count the distinct 128-byte lines each split step's "
                          "gathers touch (kernels between the steps; the timed iterations are unaffected) and report "
                          "the traffic floor they set for k_step_rows")
+    ap.add_argument("--pmc-sizes", metavar="DIR",
+                    help="with --pmc-summary: a rocprofv3 --pmc run of TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_64B_sum "
+                         "TCC_EA0_RDREQ_128B_sum TCC_EA0_RDREQ_sum, for the read bytes by request size")
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="no GPU: per-iteration kernel times of a rocprofv3 --kernel-trace run of this script over "
                          "its timed iterations (--warmup, --steps as in the run)")
@@ -353,7 +401,7 @@ def main():
     warm = trainer.step(args.warmup)
     log(f"warmup {len(warm)} iterations done")
     layout = trainer.backend.slab_layout()  # as the boosting loop left it (the quantization picks the counters)
-    log(f"slabs: {step_kernels(layout)}")
+    log(f"slabs: {step_kernels(layout, args.quant_bins)}")
     # The timed iterations run without the per-kernel events (each event is a marker in the stream that idles the
     # GPU for a few microseconds). Training is deterministic, so a second trainer repeats the same warm-up and the
     # same iterations with the events on: the kernel times and work counts are those of the timed trees.
@@ -367,12 +415,12 @@ def main():
     trainer = silvic_amd.Trainer(params, data)
     lib, h = trainer.backend._lib, trainer.backend._h
     trainer.step(args.warmup)
-    trainer.backend._check(lib.srocm_profile(h, 2 if args.sector_model else 1))
+    trainer.backend._check(lib.srocm_profile(h, 2 if args.line_model else 1))
     t1 = time.perf_counter()
     profiled = trainer.step(args.steps)
     elapsed_profiled = time.perf_counter() - t1
-    prof = (C.c_double * 22)()
-    trainer.backend._check(lib.srocm_profile_read(h, prof, 22))
+    prof = (C.c_double * 25)()
+    trainer.backend._check(lib.srocm_profile_read(h, prof, 25))
     trainer.backend._check(lib.srocm_profile(h, 0))
     same_trees = all(np.array_equal(a["split_feature"], b["split_feature"]) and
                      np.array_equal(a["threshold_bin"], b["threshold_bin"]) for a, b in zip(gpu_trees, trainer.trees))
@@ -380,7 +428,7 @@ def main():
         log("the repeated iterations grew different trees")
     (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
      part_rows, _, _, grow_steps, expansions, kept) = list(prof)[:15]
-    sector_model = sector_floor(list(prof)[15:], layout, args, len(profiled)) if args.sector_model else None
+    line_model = line_floor(list(prof)[15:], layout, args, len(profiled)) if args.line_model else None
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
     psteps = max(len(profiled), 1)
@@ -440,7 +488,7 @@ def main():
                "trees_identical": f"{same}/{compared}", "seconds": cpu_elapsed}
 
     describe = wl["describe"].format(rows=args.rows, cols=args.cols, leaves=args.leaves, bins=args.quant_bins)
-    slab = step_kernels(layout)
+    slab = step_kernels(layout, args.quant_bins)
     out = {
         "metric": METRIC if args.workload == "binary" and args.quant_bins == 4 else
                   f"boosting iters/s, {args.workload} workload at num_grad_quant_bins={args.quant_bins}; % HBM peak",
@@ -477,8 +525,8 @@ def main():
                                      "avg_launch_us": hist_ms / hist_launches * 1e3 if hist_launches else None}},
         "cpu_baseline": cpu,
     }
-    if sector_model:
-        out["roofline"]["sector_model"] = sector_model
+    if line_model:
+        out["roofline"]["line_model"] = line_model
     print(json.dumps(out), flush=True)
     trainer.backend.close()
 

@@ -316,13 +316,13 @@ struct Profile {
     double builds = 0, rows = 0, bins = 0, part_rows = 0;
     double part_launches = 0, part_ms = 0;                  // trait partitions
     double steps = 0, expansions = 0, splits = 0;           // device growth: split steps, leaves expanded, kept
-    // the sector model of the split steps' gathers (srocm_profile mode 2; k_sector_model): parent rows, their
-    // split-bin sectors, built rows, their gradient sectors, split-bin sectors shared over each step's jobs,
-    // partials written, of those packed
+    // the line model of the split steps' gathers (srocm_profile mode 2; k_sector_model): parent rows, their
+    // split-bin lines, built rows, their gradient lines, split-bin lines shared over each step's jobs, partials
+    // written, of those packed, and the sparse jobs' parent rows, split-bin lines and built rows
     bool sectors = false;
     DevBuf<unsigned long long> sector_counts;
     DevBuf<uint32_t> sector_bits;
-    double sector[7] = {0, 0, 0, 0, 0, 0, 0};
+    double sector[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     std::vector<hipEvent_t> pool;
     void reset() {
         hist_launches = hist_ms = hist_bytes = step_launches = step_ms = step_bytes = 0;
@@ -381,6 +381,7 @@ struct Context {
     std::vector<float> h_label_v, h_weight_v;
     DevBuf<int32_t> packed, partial;
     DevBuf<uint32_t> part, part2, block_left, scalars;
+    DevBuf<uint8_t> codes0, codes1;  // grown trees: each row's gradient code beside its id in part / part2
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
     DevBuf<uint32_t> d_fmt;  // per slab and k_step_rows workgroup: the format of its partial (1 packed, 0 pairs)
@@ -1876,20 +1877,20 @@ struct Context {
         prof.sectors = enable == 2;
         prof.reset();
         if (prof.sectors) {
-            prof.sector_counts.alloc(8);
-            hip_check(hipMemsetAsync(prof.sector_counts.p, 0, 8 * sizeof(unsigned long long), stream), "zero sectors");
+            prof.sector_counts.alloc(10);
+            hip_check(hipMemsetAsync(prof.sector_counts.p, 0, 10 * sizeof(unsigned long long), stream), "zero sectors");
             const uint64_t words = sector_bit_words();
             prof.sector_bits.alloc(words);
             hip_check(hipMemsetAsync(prof.sector_bits.p, 0, words * 4, stream), "zero sector bits");
         }
     }
-    uint64_t sectors_per_col() const { return div_up(std::max<uint64_t>(rows, 1), col16 ? 16 : 32); }
+    uint64_t sectors_per_col() const { return div_up(std::max<uint64_t>(rows, 1), col16 ? 64 : 128); }
     uint64_t sector_bit_words() const { return div_up(static_cast<uint64_t>(nt_feat.size()) * sectors_per_col(), 32); }
     // after a split step's k_step_rows launches: the distinct sectors its gathers touch (measurement only)
     void sector_model(uint32_t parity) {
         if (!prof.sectors) return;
-        k_sector_model<<<dim3(64, JMAX), 256, 0, stream>>>(d_plans.p + parity, part.p, part2.p, col16, prof.sector_bits.p,
-                                                          sectors_per_col(), d_fmt.p, prof.sector_counts.p);
+        k_sector_model<<<dim3(1, JMAX), 256, 0, stream>>>(d_plans.p + parity, part.p, part2.p, col16, prof.sector_bits.p,
+                                                         sectors_per_col(), d_fmt.p, prof.sector_counts.p);
         launch_check("k_sector_model");
         k_sector_bits<<<std::min<uint64_t>(div_up(sector_bit_words(), 256), cus * 4), 256, 0, stream>>>(
             prof.sector_bits.p, sector_bit_words(), prof.sector_counts.p);
@@ -1898,9 +1899,9 @@ struct Context {
     void settle_profile() {
         sync();
         if (prof.sectors && prof.sector_counts.p) {
-            unsigned long long c[8];
+            unsigned long long c[10];
             hip_check(hipMemcpy(c, prof.sector_counts.p, sizeof(c), hipMemcpyDeviceToHost), "read sectors");
-            for (int k = 0; k < 7; ++k) prof.sector[k] += static_cast<double>(c[k]);
+            for (int k = 0; k < 10; ++k) prof.sector[k] += static_cast<double>(c[k]);
             hip_check(hipMemset(prof.sector_counts.p, 0, sizeof(c)), "zero sectors");
         }
         auto settle = [&](std::vector<std::pair<hipEvent_t, hipEvent_t>> &events, double &total) {
@@ -2004,6 +2005,16 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     hip_check(hipMemcpyAsync(d_mask.p, h_stage.p, nf, hipMemcpyHostToDevice, stream), "upload mask");
     k_grow_init<<<1, 64, 0, stream>>>(g, spec.root.begin, spec.root.count, spec.root_count, root_searched ? 1u : 0u);
     launch_check("k_grow_init");
+    // small units travel beside the row ids as one-byte codes (packed_code), so the split steps' histograms read them
+    // with the rows instead of gathering the packed words
+    const bool codes = !q32 && max_gq <= CODE_MAX_G && max_hq <= CODE_MAX_H && root_searched && spec.root.count;
+    if (codes) {
+        codes0.alloc(rows);
+        codes1.alloc(rows);
+        k_gh_codes<<<std::min<uint32_t>(div_up(spec.root.count, 256), cus * 8), 256, 0, stream>>>(
+            part.p, packed.p, spec.root.begin, spec.root.count, codes0.p);
+        launch_check("k_gh_codes");
+    }
     uint64_t used_root = 0;
     for (uint32_t f = 0; f < nf; ++f)
         if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
@@ -2055,22 +2066,29 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     StepArgs sa{slab_bins.p + sl.bins_off, slab_stride(sl), step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
                                 slab_col_bins.p + sl.col_bins_off, slab_pos_word.p + sl.pos_off, sl.row_bytes() / 4, k1_groups(), packed.p,
                                 train.col.p, col16, rows, part.p, part2.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(),
-                                si == 0 ? 1u : 0u};
+                                si == 0 ? 1u : 0u, codes ? codes0.p : nullptr, codes ? codes1.p : nullptr};
                     const uint32_t grid = k1_groups() * static_cast<uint32_t>(sj - si);
+                    // the instance with carried gradient codes when the units fit them (never with separate counters)
+#define SROCM_STEP_CASE(id, W, WIDE, PACK, DP)                                                                    \
+    case id:                                                                                                      \
+        if (codes) k_step_rows<W, WIDE, PACK, false, DP, true><<<grid, 1024, 0, stream>>>(sa);                    \
+        else k_step_rows<W, WIDE, PACK, false, DP, false><<<grid, 1024, 0, stream>>>(sa);                         \
+        break;
                     switch (slabs[si].kernel()) {
-                    case 32: k_step_rows<32><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 64: k_step_rows<64><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 128: k_step_rows<128><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 33: k_step_rows<32, true><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 65: k_step_rows<64, true><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 129: k_step_rows<128, true><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 36: k_step_rows<32, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 68: k_step_rows<64, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 34: k_step_rows<32, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 66: k_step_rows<64, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 130: k_step_rows<128, false, 2><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 3004: k_step_rows<128, false, 1, false, 4><<<grid, 1024, 0, stream>>>(sa); break;
-                    case 3008: k_step_rows<128, false, 1, false, 8><<<grid, 1024, 0, stream>>>(sa); break;
+                    SROCM_STEP_CASE(32, 32, false, 1, 0)
+                    SROCM_STEP_CASE(64, 64, false, 1, 0)
+                    SROCM_STEP_CASE(128, 128, false, 1, 0)
+                    SROCM_STEP_CASE(33, 32, true, 1, 0)
+                    SROCM_STEP_CASE(65, 64, true, 1, 0)
+                    SROCM_STEP_CASE(129, 128, true, 1, 0)
+                    SROCM_STEP_CASE(36, 32, false, 4, 0)
+                    SROCM_STEP_CASE(68, 64, false, 4, 0)
+                    SROCM_STEP_CASE(34, 32, false, 2, 0)
+                    SROCM_STEP_CASE(66, 64, false, 2, 0)
+                    SROCM_STEP_CASE(130, 128, false, 2, 0)
+                    SROCM_STEP_CASE(3004, 128, false, 1, 4)
+                    SROCM_STEP_CASE(3008, 128, false, 1, 8)
+#undef SROCM_STEP_CASE
                     case 1032: k_step_rows<32, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
                     case 1064: k_step_rows<64, false, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
                     case 1033: k_step_rows<32, true, 1, true><<<grid, 1024, 0, stream>>>(sa); break;
@@ -2803,7 +2821,8 @@ int srocm_profile_read(void *ctx, double *out, uint32_t len) {
         double v[SROCM_PROFILE_VALUES] = {p.hist_launches, p.hist_ms, p.hist_bytes, p.step_launches, p.step_ms, p.step_bytes,
                                           p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms,
                                           p.steps, p.expansions, p.splits, p.sector[0], p.sector[1], p.sector[2],
-                                          p.sector[3], p.sector[4], p.sector[5], p.sector[6]};
+                                          p.sector[3], p.sector[4], p.sector[5], p.sector[6], p.sector[7],
+                                          p.sector[8], p.sector[9]};
         if (out) std::copy(v, v + std::min<uint32_t>(len, SROCM_PROFILE_VALUES), out);
     });
 }

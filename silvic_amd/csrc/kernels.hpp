@@ -401,11 +401,11 @@ __device__ __forceinline__ void dense_lanes(const uint32_t *pos_word, uint32_t l
 
 // The rows list[c0 .. c1) of a dense slab into the LDS, UNROLL rows a wave at a time over NW waves (`wave` among
 // them); dwords past the row (dw_row) read as 0, i.e. bin 0 of spare positions.
-template <int W, int DP, int UNROLL, int NW = 16>
+template <int W, int DP, int UNROLL, int NW = 16, bool CODES = false>
 __device__ __forceinline__ void hist_list_dense(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1,
                                                 const int32_t *gh, const uint32_t *bins32, uint32_t dw_row,
                                                 const uint32_t (&xs)[4], const uint32_t (&cols)[DP][4],
-                                                uint32_t wave = threadIdx.x >> 6) {
+                                                uint32_t wave = threadIdx.x >> 6, const uint8_t *codes = nullptr) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t last = c1 - 1;
     for (uint32_t base = c0 + wave * UNROLL; base < c1; base += NW * UNROLL) {
@@ -416,7 +416,8 @@ __device__ __forceinline__ void hist_list_dense(int32_t *lds, const uint32_t *li
         uint32_t dw[UNROLL][DP];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            gq[u] = gh[r[u]];
+            if constexpr (CODES) gq[u] = code_word(codes[min(base + u, last)]);
+            else gq[u] = gh[r[u]];
 #pragma unroll
             for (int p = 0; p < DP; ++p) {
                 const uint32_t d = 64u * p + lane;
@@ -3425,6 +3426,8 @@ struct StepArgs {
     GrowCtl *ctl;
     uint32_t flush_rows;
     uint32_t partition;          // 1: this launch partitions (the first slab's alone); 0: histogram only
+    uint8_t *codes0, *codes1;    // each row's one-byte gradient code beside its id in buf0 / buf1 (packed_code), or
+                                 // null: the histograms gather the packed words
 };
 
 __device__ __forceinline__ unsigned long long status_word(uint32_t epoch, uint32_t flag, uint32_t value) {
@@ -3513,10 +3516,13 @@ struct StepView {
     uint32_t wide;        // the split is a wide feature's numerical rule
     uint32_t built_left;  // 1: the left child is histogrammed
     uint32_t epoch;
+    const uint8_t *csrc;  // the rows' gradient codes beside src, and beside dst (CODES)
+    uint8_t *cdst;
 };
 
 struct StepShared {
     uint32_t list[STEP_TILE];  // the tile's rows of the built child
+    uint8_t codes[STEP_TILE];  // and their gradient codes (CODES)
     uint32_t wl[TILE_RPT][16];  // left counts per (sub-tile, wave)
     uint32_t left_bins[8];     // the split's bins that go left
     uint32_t tile, tile2, prefix;
@@ -3530,15 +3536,21 @@ struct StepShared {
 // listed rows.
 struct TileRows {
     uint32_t row[TILE_RPT], bin[TILE_RPT];
+    uint32_t codes;  // CODES: row j's gradient code in byte j
 };
 
+template <bool CODES>
 __device__ __forceinline__ void tile_rows(const StepView &v, uint32_t t, TileRows &r) {
     const uint32_t t0 = t * STEP_TILE;
+    static_assert(TILE_RPT <= 4, "a tile's codes fit one word a thread");
+    if constexpr (CODES) r.codes = 0;
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
         const uint32_t i = t0 + j * 1024 + threadIdx.x;
         const uint32_t ic = i < v.count ? i : v.count - 1;
-        r.row[j] = v.src[v.rev ? v.begin + v.count - 1 - ic : v.begin + ic];
+        const uint32_t at = v.rev ? v.begin + v.count - 1 - ic : v.begin + ic;
+        r.row[j] = v.src[at];
+        if constexpr (CODES) r.codes |= static_cast<uint32_t>(v.csrc[at]) << (8 * j);
     }
 }
 
@@ -3549,17 +3561,20 @@ __device__ __forceinline__ void tile_bins(const StepView &v, TileRows &r) {
 
 struct TileState {
     uint32_t row[TILE_RPT], lrank[TILE_RPT];  // lrank: lefts before the row in the tile
+    uint32_t codes;                           // CODES: row j's gradient code in byte j
     bool ok[TILE_RPT], left[TILE_RPT];
     uint32_t tile_left;
 };
 
 // Returns the rows listed. Block-wide; the list is complete on return.
+template <bool CODES>
 __device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, const TileRows &r, TileState &st,
                                                StepShared &sh) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint64_t below_mask = (1ull << lane) - 1ull;
     const uint32_t t0 = t * STEP_TILE;
     const uint32_t valid = v.count - t0 < STEP_TILE ? v.count - t0 : STEP_TILE;
+    if constexpr (CODES) st.codes = r.codes;
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
         st.ok[j] = t0 + j * 1024 + tid < v.count;
@@ -3599,8 +3614,11 @@ __device__ __forceinline__ uint32_t tile_front(const StepView &v, uint32_t t, co
 #pragma unroll
         for (int j = 0; j < TILE_RPT; ++j) {
             uint32_t pos = j * 1024 + tid;
-            if (st.ok[j] && (st.left[j] ? 1u : 0u) == v.built_left)
-                sh.list[v.built_left ? st.lrank[j] : pos - st.lrank[j]] = st.row[j];
+            if (st.ok[j] && (st.left[j] ? 1u : 0u) == v.built_left) {
+                const uint32_t at = v.built_left ? st.lrank[j] : pos - st.lrank[j];
+                sh.list[at] = st.row[j];
+                if constexpr (CODES) sh.codes[at] = static_cast<uint8_t>(st.codes >> (8 * j));
+            }
         }
     }
     __syncthreads();  // the list is complete
@@ -3621,28 +3639,35 @@ __device__ __forceinline__ void tile_lookback(const StepView &v, const StepArgs 
 }
 
 // The tile's rows written from the offset in sh.prefix (after a barrier that follows tile_lookback).
+template <bool CODES>
 __device__ __forceinline__ void tile_scatter(const StepView &v, uint32_t t, const TileState &st, const StepShared &sh) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lp = sh.prefix, rp = t * STEP_TILE - lp;  // lefts and rights before the tile
 #pragma unroll
     for (int j = 0; j < TILE_RPT; ++j) {
         if (!st.ok[j]) continue;
+        uint32_t at;
         if (st.left[j]) {
-            uint32_t k = lp + st.lrank[j];
-            if (k < v.count) v.dst[v.begin + k] = st.row[j];
+            const uint32_t k = lp + st.lrank[j];
+            if (k >= v.count) continue;
+            at = v.begin + k;
         } else {
-            uint32_t k = rp + (j * 1024 + tid - st.lrank[j]);
-            if (k < v.count) v.dst[v.begin + v.count - 1 - k] = st.row[j];
+            const uint32_t k = rp + (j * 1024 + tid - st.lrank[j]);
+            if (k >= v.count) continue;
+            at = v.begin + v.count - 1 - k;
         }
+        v.dst[at] = st.row[j];
+        if constexpr (CODES) v.cdst[at] = static_cast<uint8_t>(st.codes >> (8 * j));
     }
 }
 
 // The histogram of rows list[c0, c1) into the packed LDS words: a wave covers RPW = 64 / (W/4) rows per step, a
 // lane one dword (4 columns) of a row, with the conflict-free byte rotation of k_hist. Loads are branch-free. NW
 // waves take part; `wave` is this one's index among them.
-template <int W, bool WIDE, int PACK, bool Q32, int UNROLL, int NW = 16>
+template <int W, bool WIDE, int PACK, bool Q32, int UNROLL, int NW = 16, bool CODES = false>
 __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
-                                          const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6) {
+                                          const uint32_t *bins32, uint32_t wave = threadIdx.x >> 6,
+                                          const uint8_t *codes = nullptr) {
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
     constexpr uint32_t STEP = NW * RPW * UNROLL;
@@ -3660,7 +3685,8 @@ __device__ __forceinline__ void hist_list(int32_t *lds, const uint32_t *list, ui
         int32_t gq[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            gq[u] = gh[r[u]];
+            if constexpr (CODES) gq[u] = code_word(codes[min(base + u * RPW + rsub, last)]);
+            else gq[u] = gh[r[u]];
             dw[u] = bins32[static_cast<size_t>(r[u]) * DW + d];
         }
 #pragma unroll
@@ -3720,9 +3746,10 @@ __device__ __forceinline__ void store_packed_partial(const int32_t *lds, int32_t
 // row, so that its k-th add takes byte (k + rot) % 8 (column 8d + (k + rot) % 8). The LDS serves an instruction a
 // half-wave (32 lanes, two rows) at a time; with rot = d / 4 + 4 * (row % 2) the 8 lanes of a half-wave whose
 // columns share a bank group (d % 4 alike) take 8 different bytes, so no two of its lanes meet in a bank.
-template <int UNROLL, int NW = 16>
+template <int UNROLL, int NW = 16, bool CODES = false>
 __device__ __forceinline__ void hist_list_pairs(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1,
-                                                const int32_t *gh, const uint32_t *bins32, uint32_t wave) {
+                                                const int32_t *gh, const uint32_t *bins32, uint32_t wave,
+                                                const uint8_t *codes = nullptr) {
     constexpr uint32_t W = 128, RPW = 4;
     constexpr uint32_t STEP = NW * RPW * UNROLL;
     const uint32_t lane = threadIdx.x & 63u, d = lane & 15u, rsub = lane >> 4;
@@ -3742,7 +3769,8 @@ __device__ __forceinline__ void hist_list_pairs(int32_t *lds, const uint32_t *li
         int32_t gq[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            gq[u] = gh[r[u]];
+            if constexpr (CODES) gq[u] = code_word(codes[min(base + u * RPW + rsub, last)]);
+            else gq[u] = gh[r[u]];
             v[u] = rows2[static_cast<size_t>(r[u]) * (W / 8) + d];
         }
 #pragma unroll
@@ -3759,28 +3787,43 @@ __device__ __forceinline__ void hist_list_pairs(int32_t *lds, const uint32_t *li
 }
 
 // A split step's histogram of list[c0 .. c1): hist_list, or hist_list_dense for a dense slab (DP passes).
-template <int W, bool WIDE, int PACK, bool Q32, int DP, int UNROLL, int NW = 16>
+template <int W, bool WIDE, int PACK, bool Q32, int DP, int UNROLL, int NW = 16, bool CODES = false>
 __device__ __forceinline__ void step_hist(int32_t *lds, const uint32_t *list, uint32_t c0, uint32_t c1, const int32_t *gh,
                                           const uint32_t *bins32, uint32_t dw_row, const uint32_t (&xs)[4],
-                                          const uint32_t (&dcols)[DP ? DP : 1][4], uint32_t wave = threadIdx.x >> 6) {
-    if constexpr (DP > 0) hist_list_dense<W, DP, DP <= 4 ? 2 : 1, NW>(lds, list, c0, c1, gh, bins32, dw_row, xs, dcols, wave);
-    else if constexpr (W == 128 && !WIDE && PACK == 1 && !Q32) hist_list_pairs<UNROLL * 3 / 4, NW>(lds, list, c0, c1, gh, bins32, wave);
-    else hist_list<W, WIDE, PACK, Q32, UNROLL, NW>(lds, list, c0, c1, gh, bins32, wave);
+                                          const uint32_t (&dcols)[DP ? DP : 1][4], uint32_t wave = threadIdx.x >> 6,
+                                          const uint8_t *codes = nullptr) {
+    if constexpr (DP > 0)
+        hist_list_dense<W, DP, DP <= 4 ? 2 : 1, NW, CODES>(lds, list, c0, c1, gh, bins32, dw_row, xs, dcols, wave, codes);
+    else if constexpr (W == 128 && !WIDE && PACK == 1 && !Q32)
+        hist_list_pairs<UNROLL * 3 / 4, NW, CODES>(lds, list, c0, c1, gh, bins32, wave, codes);
+    else hist_list<W, WIDE, PACK, Q32, UNROLL, NW, CODES>(lds, list, c0, c1, gh, bins32, wave, codes);
 }
 
-template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false, int DP = 0>
-__global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
+// The one-byte gradient codes of a tree's root rows, beside their ids: codes[i] = packed_code(gh[part[i]]) for i in
+// [begin, begin + count). The split steps then move each code with its row.
+__global__ void k_gh_codes(const uint32_t *__restrict__ part, const int32_t *__restrict__ gh, uint32_t begin,
+                           uint32_t count, uint8_t *__restrict__ codes) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+        codes[begin + i] = packed_code(gh[part[begin + i]]);
+}
+
+// The LDS words of a k_step_rows instance: the histogram (twice for separate counters) and a dense slab's spare row.
+template <int W, bool Q32, int DP>
+constexpr int step_lds_words() { return (Q32 ? 2 : 1) * 256 * W + (DP ? W : 0); }
+
+// k_step_rows' work, with the built rows' gradients read from their carried codes (CODES) or gathered.
+template <int W, bool WIDE, int PACK, bool Q32, int DP, bool CODES>
+__device__ __forceinline__ void step_rows_body(const StepArgs &a, int32_t *lds, StepShared &sh) {
     static_assert(PACK == 1 || (!WIDE && W * PACK <= 256), "a packed row is at most 64 dwords");
     static_assert(!Q32 || W <= 64, "separate g and h counters take twice the LDS");
     static_assert(DP == 0 || (W == 128 && !WIDE && PACK == 1 && !Q32), "a dense slab has 128 byte columns");
+    static_assert(!(CODES && Q32), "codes hold small units only");
     constexpr int DW = WIDE ? W / 8 : W * PACK / 4;
     constexpr int RPW = WAVE / DW;
     // rows per lane in multi-tile workgroups (16 at W = 32 with packed columns spills)
     constexpr int UNROLL = (W == 128 || (W == 32 && PACK > 1)) ? 8 : (64 / RPW < 16 ? 64 / RPW : 16);
     constexpr int SLOTS = 256 * W / 1024;
-    constexpr int LDS_WORDS = (Q32 ? 2 : 1) * 256 * W + (DP ? W : 0);  // a dense slab's spare row
-    __shared__ int32_t lds[LDS_WORDS];
-    __shared__ StepShared sh;
+    constexpr int LDS_WORDS = step_lds_words<W, Q32, DP>();
 
     // a launch of histogram-only slabs takes k1 workgroups a slab: wg is the workgroup within its slab
     const uint32_t sl = blockIdx.x / a.k1, wg = blockIdx.x - sl * a.k1;
@@ -3816,6 +3859,8 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     v.col = a.colbase + static_cast<size_t>(J.col) * a.rows * (a.col16 ? 2u : 1u);
     v.built_left = J.built_side == 0 ? 1u : 0u;
     v.epoch = P.epoch;
+    v.csrc = J.src_buf ? a.codes1 : a.codes0;
+    v.cdst = J.src_buf ? a.codes0 : a.codes1;
     const uint32_t tid = threadIdx.x;
     if (tid < 8) sh.left_bins[tid] = J.left_bins[tid];  // visible after the first barrier below
     const uint32_t *bins32 = reinterpret_cast<const uint32_t *>(R.bins);
@@ -3830,20 +3875,20 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         __syncthreads();
         const uint32_t t = sh.tile;
         TileRows r;
-        tile_rows(v, t, r);
+        tile_rows<CODES>(v, t, r);
         tile_bins(v, r);
         TileState st;
-        const uint32_t nb = tile_front(v, t, r, st, sh);
+        const uint32_t nb = tile_front<CODES>(v, t, r, st, sh);
         // wave 0 resolves the tile's offset while the other waves histogram it (wv: the wave, uniform)
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (v.hist) step_hist<W, WIDE, PACK, Q32, DP, 16, 15>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1);
+            else if (v.hist) step_hist<W, WIDE, PACK, Q32, DP, 16, 15, CODES>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1, sh.codes);
         } else if (v.hist) {
-            step_hist<W, WIDE, PACK, Q32, DP, 16>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols);
+            step_hist<W, WIDE, PACK, Q32, DP, 16, 16, CODES>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, threadIdx.x >> 6, sh.codes);
         }
         __syncthreads();  // the offset and the histogram are complete
-        if (v.partition) tile_scatter(v, t, st, sh);
+        if (v.partition) tile_scatter<CODES>(v, t, st, sh);
         if (!v.hist) return;
         if constexpr (Q32) {  // the counters as a {g, h} pair partial
             int2 *pairs = reinterpret_cast<int2 *>(R.partial) + static_cast<size_t>(wg) * step_partial_stride(W);
@@ -3878,16 +3923,16 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     uint32_t next = gi + 2 * v.groups;
     TileRows r;
     if (t < v.ntiles) {
-        tile_rows(v, t, r);
+        tile_rows<CODES>(v, t, r);
         tile_bins(v, r);
     }
     while (t < v.ntiles) {
         TileState st;
-        const uint32_t nb = tile_front(v, t, r, st, sh);
+        const uint32_t nb = tile_front<CODES>(v, t, r, st, sh);
         uint32_t ticket = next;
         if (v.partition && tid == 0) ticket = atomicAdd(&J.ticket, 1u);
         next += v.groups;
-        if (tn < v.ntiles) tile_rows(v, tn, r);
+        if (tn < v.ntiles) tile_rows<CODES>(v, tn, r);
         // a tile that takes the packed words past flush_rows rows is histogrammed by all waves around the flushes
         // (block-wide); otherwise wave 0 resolves the tile's offset while the other waves histogram it
         const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -3902,7 +3947,7 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
                 }
                 uint32_t room = a.flush_rows - pending;
                 uint32_t c1 = nb - c0 < room ? nb : c0 + room;
-                step_hist<W, WIDE, PACK, Q32, DP, UNROLL>(lds, sh.list, c0, c1, a.gh, bins32, a.dw_row, dxs, dcols);
+                step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 16, CODES>(lds, sh.list, c0, c1, a.gh, bins32, a.dw_row, dxs, dcols, threadIdx.x >> 6, sh.codes);
                 pending += c1 - c0;
                 c0 = c1;
             }
@@ -3910,11 +3955,11 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
         }
         if (v.partition) {
             if (wv == 0) tile_lookback(v, a, t, st, sh);
-            else if (!hist_done) step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 15>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1);
+            else if (!hist_done) step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 15, CODES>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, wv - 1, sh.codes);
             __syncthreads();  // the offset is in sh.prefix
-            tile_scatter(v, t, st, sh);
+            tile_scatter<CODES>(v, t, st, sh);
         } else if (!hist_done) {
-            step_hist<W, WIDE, PACK, Q32, DP, UNROLL>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols);
+            step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 16, CODES>(lds, sh.list, 0, nb, a.gh, bins32, a.dw_row, dxs, dcols, threadIdx.x >> 6, sh.codes);
         }
         if (!hist_done) pending += nb;
         if (tn < v.ntiles) tile_bins(v, r);
@@ -3935,18 +3980,29 @@ __global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
     if (tid == 0) R.fmt[wg] = 0u;
 }
 
-// Measurement only (profile mode): the distinct 32-byte sectors a split step's gathers must touch, from the step's
-// own plan and partition buffers, right after its k_step_rows launches. Per job, over the parent's rows (ascending in
-// row id, whatever order they are stored in): the sectors of the column-major split-feature array their bins lie in
-// (32 rows a sector, 16 for two-byte bins) and, over the built child's rows (sorted too), the sectors of the packed
-// gradient array (8 rows a sector). A sorted run of rows touches as many sectors as it has distinct row / rows-per-
-// sector values, so each is a count of the positions where that value changes. `shared`, when set, is one bit per
-// (column-major feature, split-bin sector), or-ed over every job of the step: the sectors the step would touch if
-// jobs that split on the same feature shared them. counters: [0] parent rows, [1] their split-bin sectors, [2]
-// built rows, [3] their gradient sectors, [5] partials written (the first slab's workgroups of histogrammed jobs),
-// [6] of those, packed ones (`fmt`: the first slab's partial formats). grid: (x, JMAX).
+// CODES: the built rows' gradients come from the codes beside their ids (a.codes0 / a.codes1), else gathered. The
+// two are separate instances: in one kernel behind a branch, the register allocator spilled both.
+template <int W, bool WIDE = false, int PACK = 1, bool Q32 = false, int DP = 0, bool CODES = false>
+__global__ __launch_bounds__(1024) void k_step_rows(StepArgs a) {
+    __shared__ int32_t lds[step_lds_words<W, Q32, DP>()];
+    __shared__ StepShared sh;
+    step_rows_body<W, WIDE, PACK, Q32, DP, CODES>(a, lds, sh);
+}
+
+// Measurement only (profile mode): the distinct 128-byte lines (the size of every L2 miss's request to memory) a
+// split step's gathers must touch, from the step's own plan and partition buffers, right after its k_step_rows
+// launches. Per job, over the parent's rows (ascending in row id, whatever order they are stored in): the lines of
+// the column-major split-feature array their bins lie in (128 rows a line, 64 for two-byte bins) and, over the built
+// child's rows (sorted too), the lines of the packed gradient array (32 rows a line). A sorted run of rows touches as
+// many lines as it has distinct row / rows-per-line values, so each is a count of the positions where that value
+// changes. `shared`, when set, is one bit per (column-major feature, split-bin line), or-ed over every job of the
+// step: the lines the step would touch if jobs that split on the same feature shared them. counters: [0] parent
+// rows, [1] their split-bin lines, [2] built rows, [3] their gradient lines, [5] partials written (the first slab's
+// workgroups of histogrammed jobs), [6] of those, packed (`fmt`: the first slab's partial formats), [7]-[9] parent
+// rows, split-bin lines and built rows of the sparse jobs (fewer than two parent rows a split-bin line). grid: (x,
+// JMAX); one block per job when `sparse_split` is needed (x = 1).
 __global__ __launch_bounds__(256) void k_sector_model(const StepPlan *plan, const uint32_t *buf0, const uint32_t *buf1,
-                                                      uint32_t col16, uint32_t *shared, uint64_t sectors_per_col,
+                                                      uint32_t col16, uint32_t *shared, uint64_t lines_per_col,
                                                       const uint32_t *fmt, unsigned long long *counters) {
     __shared__ unsigned long long part[4];
     const StepPlan &P = *plan;
@@ -3963,15 +4019,15 @@ __global__ __launch_bounds__(256) void k_sector_model(const StepPlan *plan, cons
     if (j < P.njobs) {
         const JobPlan &J = P.jobs[j];
         const uint32_t *src = J.src_buf ? buf1 : buf0, *dst = J.src_buf ? buf0 : buf1;
-        const uint32_t sshift = col16 ? 4u : 5u;
+        const uint32_t sshift = col16 ? 6u : 7u;
         unsigned long long prow = 0, psec = 0, brow = 0, bsec = 0;
-        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < J.count; i += gridDim.x * blockDim.x) {
+        for (uint32_t i = threadIdx.x; i < J.count; i += blockDim.x) {
             const uint32_t at = J.src_rev ? J.begin + J.count - 1 - i : J.begin + i;
             const uint32_t r = src[at];
             ++prow;
             if (i == 0 || (src[J.src_rev ? at + 1 : at - 1] >> sshift) != (r >> sshift)) ++psec;
             if (shared) {
-                const uint64_t bit = static_cast<uint64_t>(J.col) * sectors_per_col + (r >> sshift);
+                const uint64_t bit = static_cast<uint64_t>(J.col) * lines_per_col + (r >> sshift);
                 atomicOr(shared + (bit >> 5), 1u << (bit & 31u));
             }
         }
@@ -3979,10 +4035,10 @@ __global__ __launch_bounds__(256) void k_sector_model(const StepPlan *plan, cons
             // the built child: the left one first-first at begin, the right one last-first after the left rows
             const uint32_t b = J.built_side == 0 ? J.begin : J.begin + J.left;
             const uint32_t n = J.built_side == 0 ? J.left : J.count - J.left;
-            for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
                 const uint32_t r = dst[b + i];
                 ++brow;
-                if (i == 0 || (dst[b + i - 1] >> 3) != (r >> 3)) ++bsec;
+                if (i == 0 || (dst[b + i - 1] >> 5) != (r >> 5)) ++bsec;
             }
         }
         atomicAdd(&part[0], prow);
@@ -3992,9 +4048,14 @@ __global__ __launch_bounds__(256) void k_sector_model(const StepPlan *plan, cons
     }
     __syncthreads();
     if (threadIdx.x < 4 && part[threadIdx.x]) atomicAdd(counters + threadIdx.x, part[threadIdx.x]);
+    if (threadIdx.x == 0 && part[1] * 2 > part[0]) {  // a sparse job (one block a job)
+        atomicAdd(counters + 7, part[0]);
+        atomicAdd(counters + 8, part[1]);
+        atomicAdd(counters + 9, part[2]);
+    }
 }
 
-// Measurement only: the set bits of k_sector_model's shared-sector bitmap into counters[4], the bitmap cleared.
+// Measurement only: the set bits of k_sector_model's shared-line bitmap into counters[4], the bitmap cleared.
 __global__ __launch_bounds__(256) void k_sector_bits(uint32_t *bits, uint64_t words, unsigned long long *counters) {
     unsigned long long c = 0;
     for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < words;

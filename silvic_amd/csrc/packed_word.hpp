@@ -26,4 +26,16 @@ SROCM_PACKED_HD int32_t packed_h(int32_t word, int32_t g) {
     return static_cast<int32_t>((static_cast<uint32_t>(word) - static_cast<uint32_t>(g)) >> 16);
 }
 
+// A row's packed word in one byte, for units of at most 7 gradient and 15 hessian units (num_grad_quant_bins of at
+// most 14): g + 8 in the low four bits, h in the high four. The split steps carry it beside each row id, so that
+// the histogram of a built child reads it with the row instead of gathering the packed word.
+constexpr int32_t CODE_MAX_G = 7, CODE_MAX_H = 15;
+SROCM_PACKED_HD uint8_t packed_code(int32_t word) {
+    const int32_t g = packed_g(word);
+    return static_cast<uint8_t>((g + 8) | (packed_h(word, g) << 4));
+}
+SROCM_PACKED_HD int32_t code_word(uint32_t code) {
+    return static_cast<int32_t>((code >> 4) << 16) + static_cast<int32_t>(code & 15u) - 8;
+}
+
 }  // namespace srocm

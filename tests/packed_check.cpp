@@ -1,5 +1,6 @@
 // Unpacks every (g, h) with g in -32767..32767 and h in a sweep of 0..65535 that includes the upper half
-// (h >= 32768) from the word the 32-bit wrapping sums form, with silvic_amd/csrc/packed_word.hpp built for the host.
+// (h >= 32768) from the word the 32-bit wrapping sums form, with silvic_amd/csrc/packed_word.hpp built for the host,
+// and round-trips every small-unit word through its one-byte code.
 // Built with -fsanitize=undefined, so a signed overflow in the unpacking aborts. Prints the mismatches.
 #include <cstdio>
 #include <cstdint>
@@ -19,6 +20,15 @@ int main() {
             ++n;
         }
     }
-    std::printf("%ld %ld\n", bad, n);
+    // the one-byte code of a row's word for small units (g in -7..7, h in 0..15) gives the word back
+    long code_bad = 0, codes = 0;
+    for (int32_t h = 0; h <= srocm::CODE_MAX_H; ++h) {
+        for (int32_t g = -srocm::CODE_MAX_G; g <= srocm::CODE_MAX_G; ++g) {
+            const int32_t word = h * 65536 + g;
+            code_bad += srocm::code_word(srocm::packed_code(word)) != word;
+            ++codes;
+        }
+    }
+    std::printf("%ld %ld %ld %ld\n", bad, n, code_bad, codes);
     return 0;
 }
