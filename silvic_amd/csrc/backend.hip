@@ -261,7 +261,7 @@ struct HostTree {
 // The context
 // ---------------------------------------------------------------------------------------------------------
 
-constexpr uint32_t RANK_DEVICE_MAX = 512;  // rows of the largest query k_rank_pairs takes
+constexpr uint32_t RANK_DEVICE_MAX = 512;  // rows of the largest query k_rank_pairs takes (longer ones: the host's)
 constexpr uint32_t HIST_MIN_ROWS = 2048;   // rows per histogram workgroup before another one is used
 constexpr uint64_t ROW_BLOCK = 256;
 
@@ -426,12 +426,16 @@ struct Context {
 
     srocm_rank::Ranker ranker;  // lambdarank: the setup, the sigmoid and discount tables
     Pinned<float> h_rank_scores, h_rank_grad, h_rank_hess;
-    // lambdarank on the device (k_rank_pairs): the power of two its queries fit, 0 when a query has more rows than
-    // RANK_DEVICE_MAX (then the host computes every query); the setup, the tables and the per-row / per-query sums
+    // lambdarank: the queries of at most RANK_DEVICE_MAX rows run on the device (k_rank_pairs, one wave a query,
+    // largest first so that the launch's tail is short), the longer ones on the host's threads. rank_nmax: the power
+    // of two the device's queries fit (0: none); the setup, the tables and the per-row / per-query sums
     uint32_t rank_nmax = 0;
-    DevBuf<uint32_t> d_rank_bounds;
+    std::vector<uint32_t> rank_dev_q, rank_host_q;  // the device's queries (largest first) and the host's
+    DevBuf<uint32_t> d_rank_bounds, d_rank_queries;
     DevBuf<double> d_rank_imd, d_rank_gain, d_rank_table, d_rank_disc, d_rank_lam, d_rank_hes, d_rank_qsum, d_rank_factor;
     Pinned<double> h_rank_qsum, h_rank_factor;
+    std::unique_ptr<srocm_rank::WorkPool> rank_pool;  // host threads for the factors and the host's queries
+    hipEvent_t rank_event = nullptr;                   // the host's queries' scores have arrived
 
     Profile prof;
     int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
@@ -439,6 +443,7 @@ struct Context {
     ~Context() {
         if (tree_event) (void)hipEventDestroy(tree_event);
         if (steps_event) (void)hipEventDestroy(steps_event);
+        if (rank_event) (void)hipEventDestroy(rank_event);
         for (auto &e : prof.hist_events) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
@@ -453,7 +458,6 @@ struct Context {
         }
         for (auto e : prof.pool) (void)hipEventDestroy(e);
         if (copy_stream) (void)hipStreamDestroy(copy_stream);
-        if (steps_event) (void)hipEventDestroy(steps_event);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -508,16 +512,34 @@ struct Context {
         if (!obj->inverse_max_dcg) ranker.derive_inverse_max_dcg(t->label);
     }
 
-    // The device's copy of the lambdarank setup, when every query fits k_rank_pairs (at most RANK_DEVICE_MAX rows).
+    // The split of the queries between the device (at most RANK_DEVICE_MAX rows, largest first) and the host, and the
+    // device's copy of the lambdarank setup.
     void upload_ranking() {
         const srocm_rank::Setup &st = ranker.setup();
         const uint64_t nq = st.boundaries.size() - 1;
+        rank_dev_q.clear();
+        rank_host_q.clear();
         uint32_t biggest = 0;
-        for (uint64_t q = 0; q < nq; ++q) biggest = std::max(biggest, st.boundaries[q + 1] - st.boundaries[q]);
+        for (uint64_t q = 0; q < nq; ++q) {
+            const uint32_t n = st.boundaries[q + 1] - st.boundaries[q];
+            if (n > RANK_DEVICE_MAX) {
+                rank_host_q.push_back(static_cast<uint32_t>(q));
+            } else {
+                rank_dev_q.push_back(static_cast<uint32_t>(q));
+                biggest = std::max(biggest, n);
+            }
+        }
+        std::stable_sort(rank_dev_q.begin(), rank_dev_q.end(), [&](uint32_t a, uint32_t b) {
+            return st.boundaries[a + 1] - st.boundaries[a] > st.boundaries[b + 1] - st.boundaries[b];
+        });
+        if (!rank_pool) rank_pool = std::make_unique<srocm_rank::WorkPool>(std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+        if (!rank_event) hip_check(hipEventCreateWithFlags(&rank_event, hipEventDisableTiming), "hipEventCreate");
         rank_nmax = 0;
-        if (biggest > RANK_DEVICE_MAX) return;
+        if (rank_dev_q.empty()) return;
         rank_nmax = 64;
         while (rank_nmax < biggest) rank_nmax <<= 1;
+        d_rank_queries.alloc(rank_dev_q.size());
+        hip_check(hipMemcpy(d_rank_queries.p, rank_dev_q.data(), rank_dev_q.size() * 4, hipMemcpyHostToDevice), "upload queries");
         d_rank_bounds.alloc(nq + 1);
         d_rank_imd.alloc(nq);
         d_rank_gain.alloc(st.label_gain.size());
@@ -538,53 +560,84 @@ struct Context {
                   "upload discounts");
     }
 
-    // lambdarank gradients (lambdarank.rs:190-420). On the device when the queries fit k_rank_pairs: the pair sums,
-    // then the per-query normalization factors log2(1 + s) / s on the host (one log2 a query; the sums come back and
-    // the factors go out, so this waits for the stream), then k_rank_scale. Otherwise the scores come to the host and
-    // the gradients are computed there (f64, every host thread) and go back. The maxima are taken on the device.
+    // lambdarank gradients (lambdarank.rs:190-420). The device's queries: the pair sums (k_rank_pairs), then the
+    // per-query normalization factors log2(1 + s) / s on the host's pool (the C library's log2; the sums come back
+    // and the factors go out, so this waits for the stream), then k_rank_scale. The host's queries (more rows than
+    // k_rank_pairs takes): their scores come back first and their gradients are computed on the pool (f64) while the
+    // device works on its own, then go out. The maxima are taken on the device over every row.
     void ranking_gradients() {
+        const srocm_rank::Setup &st = ranker.setup();
+        const uint32_t nq = static_cast<uint32_t>(st.boundaries.size() - 1);
+        const uint32_t *qb = st.boundaries.data();
+        const bool host = !rank_host_q.empty();
+        // the host's queries' rows in few copies: query by query when they are few, else every row at once
+        const bool by_query = rank_host_q.size() <= 64;
+        auto each_host_range = [&](auto &&f) {
+            if (!by_query) {
+                f(0u, static_cast<uint32_t>(rows));
+                return;
+            }
+            for (uint32_t q : rank_host_q) f(qb[q], qb[q + 1] - qb[q]);
+        };
+        if (host) {
+            h_rank_scores.alloc(rows);
+            h_rank_grad.alloc(rows);
+            h_rank_hess.alloc(rows);
+            each_host_range([&](uint32_t b, uint32_t n) {
+                hip_check(hipMemcpyAsync(h_rank_scores.p + b, train.scores.p + b, static_cast<size_t>(n) * 4,
+                                         hipMemcpyDeviceToHost, stream), "read scores");
+            });
+            hip_check(hipEventRecord(rank_event, stream), "event");
+        }
         if (rank_nmax) {
-            const srocm_rank::Setup &st = ranker.setup();
-            const uint32_t nq = static_cast<uint32_t>(st.boundaries.size() - 1);
             RankArgs ra{train.scores.p, label.p, d_rank_bounds.p, d_rank_imd.p, d_rank_gain.p, d_rank_table.p,
                         d_rank_disc.p, st.sigmoid, st.sigmoid * st.sigmoid, ranker.min_input(), ranker.max_input(),
                         ranker.idx_factor(), st.norm ? 1u : 0u, st.truncation_level, d_rank_lam.p, d_rank_hes.p,
-                        d_rank_qsum.p};
+                        d_rank_qsum.p, d_rank_queries.p};
+            const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
             switch (rank_nmax) {
-            case 64: k_rank_pairs<64><<<nq, 64, 0, stream>>>(ra); break;
-            case 128: k_rank_pairs<128><<<nq, 64, 0, stream>>>(ra); break;
-            case 256: k_rank_pairs<256><<<nq, 64, 0, stream>>>(ra); break;
-            default: k_rank_pairs<512><<<nq, 64, 0, stream>>>(ra); break;
+            case 64: k_rank_pairs<64><<<nd, 64, 0, stream>>>(ra); break;
+            case 128: k_rank_pairs<128><<<nd, 64, 0, stream>>>(ra); break;
+            case 256: k_rank_pairs<256><<<nd, 64, 0, stream>>>(ra); break;
+            default: k_rank_pairs<512><<<nd, 64, 0, stream>>>(ra); break;
             }
             launch_check("k_rank_pairs");
+            if (st.norm) hip_check(hipMemcpyAsync(h_rank_qsum.p, d_rank_qsum.p, static_cast<size_t>(nq) * 8,
+                                                  hipMemcpyDeviceToHost, stream), "read sums");
+        }
+        if (host) {  // while the device ranks its queries
+            hip_check(hipEventSynchronize(rank_event), "event synchronize");
+            ranker.gradients(rank_host_q.data(), rank_host_q.size(), h_rank_scores.p, h_label_v.data(),
+                             has_weight ? h_weight_v.data() : nullptr, h_rank_grad.p, h_rank_hess.p, *rank_pool);
+            each_host_range([&](uint32_t b, uint32_t n) {
+                hip_check(hipMemcpyAsync(grad.p + b, h_rank_grad.p + b, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice,
+                                         stream), "upload grad");
+                hip_check(hipMemcpyAsync(hess.p + b, h_rank_hess.p + b, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice,
+                                         stream), "upload hess");
+            });
+        }
+        if (rank_nmax) {
             const double *factor = nullptr;
             if (st.norm) {
-                hip_check(hipMemcpyAsync(h_rank_qsum.p, d_rank_qsum.p, nq * 8, hipMemcpyDeviceToHost, stream), "read sums");
                 sync();
-                for (uint32_t q = 0; q < nq; ++q) {  // lambdarank.rs:287-300, as srocm_rank::Ranker takes it
-                    const double sl = h_rank_qsum.p[q];
-                    h_rank_factor.p[q] = sl > 0.0 ? std::log2(1.0 + sl) / sl : 1.0;
-                }
-                hip_check(hipMemcpyAsync(d_rank_factor.p, h_rank_factor.p, nq * 8, hipMemcpyHostToDevice, stream), "upload factors");
+                const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
+                const uint32_t per = (nd + rank_pool->size() - 1) / rank_pool->size();
+                rank_pool->run([&](unsigned w) {  // lambdarank.rs:287-300, as srocm_rank::Ranker takes it
+                    for (uint32_t k = w * per; k < std::min(nd, (w + 1) * per); ++k) {
+                        const uint32_t q = rank_dev_q[k];
+                        h_rank_factor.p[q] = srocm_rank::norm_factor(true, h_rank_qsum.p[q]);
+                    }
+                });
+                hip_check(hipMemcpyAsync(d_rank_factor.p, h_rank_factor.p, static_cast<size_t>(nq) * 8, hipMemcpyHostToDevice,
+                                         stream), "upload factors");
                 factor = d_rank_factor.p;
             }
-            k_rank_scale<<<nq, 64, 0, stream>>>(d_rank_bounds.p, d_rank_lam.p, d_rank_hes.p, factor,
-                                                has_weight ? weight.p : nullptr, grad.p, hess.p);
+            // the host's rows (uploaded above, from buffers that outlive the copies) are not written here
+            k_rank_scale<<<static_cast<uint32_t>(rank_dev_q.size()), 64, 0, stream>>>(
+                d_rank_bounds.p, d_rank_queries.p, d_rank_lam.p, d_rank_hes.p, factor, has_weight ? weight.p : nullptr,
+                grad.p, hess.p);
             launch_check("k_rank_scale");
-            k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, scalars.p + 1);
-            launch_check("k_max_abs");
-            return;
         }
-        h_rank_scores.alloc(rows);
-        h_rank_grad.alloc(rows);
-        h_rank_hess.alloc(rows);
-        hip_check(hipMemcpyAsync(h_rank_scores.p, train.scores.p, rows * 4, hipMemcpyDeviceToHost, stream), "read scores");
-        sync();
-        const unsigned threads = std::max(1u, std::min(64u, std::thread::hardware_concurrency()));
-        ranker.gradients(h_rank_scores.p, h_label_v.data(), has_weight ? h_weight_v.data() : nullptr, h_rank_grad.p,
-                         h_rank_hess.p, threads);
-        hip_check(hipMemcpyAsync(grad.p, h_rank_grad.p, rows * 4, hipMemcpyHostToDevice, stream), "upload grad");
-        hip_check(hipMemcpyAsync(hess.p, h_rank_hess.p, rows * 4, hipMemcpyHostToDevice, stream), "upload hess");
         k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, scalars.p + 1);
         launch_check("k_max_abs");
     }

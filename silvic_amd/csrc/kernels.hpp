@@ -3869,6 +3869,42 @@ __device__ __forceinline__ void step_rows_body(const StepArgs &a, int32_t *lds, 
     uint32_t dxs[4], dcols[DP ? DP : 1][4];
     if constexpr (DP > 0) dense_lanes<DP>(R.pos_word, tid & 63u, dxs, dcols);
 
+    if (!v.partition) {
+        // A later slab: the built child's rows as the partition launch (an earlier kernel) left them in dst, the left
+        // child first-first from begin, the right one after the left rows (any order sums alike), a workgroup
+        // taking an equal share; no tile is ranked again. Whenever flush_rows rows have gone into the packed words
+        // they are added into the partial as {g, h} pairs; a workgroup that never flushes stores them packed.
+        const uint32_t nb = v.built_left ? J.left : v.count - J.left;
+        const uint32_t b0 = v.begin + (v.built_left ? 0u : J.left);
+        const uint32_t per = (nb + v.groups - 1) / v.groups;
+        const uint32_t c0 = min(nb, gi * per), c1 = min(nb, c0 + per);
+        const uint32_t *list = v.dst + b0;
+        const uint8_t *codes = CODES ? v.cdst + b0 : nullptr;
+        int2 *pairs = reinterpret_cast<int2 *>(R.partial) + static_cast<size_t>(wg) * step_partial_stride(W);
+        const uint32_t col_bins = (PACK > 1 || DP > 0) ? 256u : R.col_bins[tid % W];
+        __syncthreads();  // the LDS histogram is zeroed
+        bool flushed = false;
+        for (uint32_t ca = c0; ca < c1;) {
+            const uint32_t cb = c1 - ca < a.flush_rows ? c1 : ca + a.flush_rows;
+            if (ca > c0) {
+                flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
+                flushed = true;
+            }
+            step_hist<W, WIDE, PACK, Q32, DP, UNROLL, 16, CODES>(lds, list, ca, cb, a.gh, bins32, a.dw_row, dxs, dcols,
+                                                                threadIdx.x >> 6, codes);
+            ca = cb;
+        }
+        if (!flushed && !Q32) {
+            __syncthreads();
+            store_packed_partial<W>(lds, R.partial + 2 * static_cast<size_t>(wg) * step_partial_stride(W));
+            if (tid == 0) R.fmt[wg] = 1u;
+            return;
+        }
+        flush_pairs<W, Q32>(lds, pairs, col_bins, flushed);
+        if (tid == 0) R.fmt[wg] = 0u;
+        return;
+    }
+
     if (packed) {  // one tile; the partial is the LDS words themselves
         __syncthreads();
         if (tid == 0) sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;

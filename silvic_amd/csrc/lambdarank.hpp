@@ -17,8 +17,11 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
 #include <limits>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -58,6 +61,70 @@ SRANK_HD inline uint64_t label_as_index(float l) {
     if (l >= 18446744073709551616.0f) return UINT64_MAX;
     return static_cast<uint64_t>(l);
 }
+
+// Host threads started once that run one job at a time: run(fn) calls fn(w) on every worker w in 0 .. size() - 1,
+// the calling thread being worker 0, and returns when every call has returned. Workers sleep between jobs, so a job
+// costs one wake-up instead of starting threads.
+class WorkPool {
+public:
+    explicit WorkPool(unsigned threads) : n_(std::max(1u, threads)) {
+        for (unsigned w = 1; w < n_; ++w) threads_.emplace_back([this, w] { loop(w); });
+    }
+    ~WorkPool() {
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            stop_ = true;
+        }
+        start_.notify_all();
+        for (auto &t : threads_) t.join();
+    }
+    WorkPool(const WorkPool &) = delete;
+    WorkPool &operator=(const WorkPool &) = delete;
+    unsigned size() const { return n_; }
+    void run(const std::function<void(unsigned)> &fn) {
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            job_ = &fn;
+            pending_ = n_ - 1;
+            ++gen_;
+        }
+        start_.notify_all();
+        fn(0);
+        std::unique_lock<std::mutex> lock(mu_);
+        done_.wait(lock, [this] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+
+private:
+    void loop(unsigned w) {
+        uint64_t seen = 0;
+        for (;;) {
+            const std::function<void(unsigned)> *job;
+            {
+                std::unique_lock<std::mutex> lock(mu_);
+                start_.wait(lock, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+                job = job_;
+            }
+            (*job)(w);
+            std::lock_guard<std::mutex> lock(mu_);
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    const unsigned n_;
+    std::vector<std::thread> threads_;
+    std::mutex mu_;
+    std::condition_variable start_, done_;
+    const std::function<void(unsigned)> *job_ = nullptr;
+    uint64_t gen_ = 0;
+    unsigned pending_ = 0;
+    bool stop_ = false;
+};
+
+// The normalization factor of a query with lambda sum s (lambdarank.rs:287-300): log2(1 + s) / s when normalizing
+// and s > 0, else 1; the C library's log2, as silvic's f64::log2.
+inline double norm_factor(bool norm, double s) { return norm && s > 0.0 ? std::log2(1.0 + s) / s : 1.0; }
 
 // A key whose ascending order is the score's descending order; +0.0f folds -0 into 0 (equal under `>`).
 SRANK_HD inline uint32_t rank_key(float score) {
@@ -163,25 +230,20 @@ public:
         }
     }
 
-    // grad/hess of every row from scores, labels and optional weights.
-    void gradients(const float *scores, const float *label, const float *weight, float *grad, float *hess,
-                   unsigned threads) const {
-        const size_t nq = setup_.boundaries.empty() ? 0 : setup_.boundaries.size() - 1;
+    // grad/hess of the rows of the listed queries (every query when `queries` is null: nq of them) from scores,
+    // labels and optional weights, the queries shared out over the pool's threads.
+    void gradients(const uint32_t *queries, size_t nq, const float *scores, const float *label, const float *weight,
+                   float *grad, float *hess, WorkPool &pool) const {
         std::atomic<size_t> next{0};
-        auto work = [&]() {
+        pool.run([&](unsigned) {
             Scratch sc;
             for (;;) {
                 const size_t q0 = next.fetch_add(QUERIES_PER_CLAIM);
                 if (q0 >= nq) break;
                 const size_t q1 = std::min(nq, q0 + QUERIES_PER_CLAIM);
-                for (size_t q = q0; q < q1; ++q) one_query(q, scores, label, weight, grad, hess, sc);
+                for (size_t k = q0; k < q1; ++k) one_query(queries ? queries[k] : k, scores, label, weight, grad, hess, sc);
             }
-        };
-        threads = std::max(1u, threads);
-        std::vector<std::thread> pool;
-        for (unsigned t = 1; t < threads; ++t) pool.emplace_back(work);
-        work();
-        for (auto &t : pool) t.join();
+        });
     }
 
 private:
@@ -267,7 +329,7 @@ private:
             sc.lambda[i] = lam_i;
             sc.hessian[i] = hes_i;
         }
-        const double factor = setup_.norm && sum_lambdas > 0.0 ? std::log2(1.0 + sum_lambdas) / sum_lambdas : 1.0;
+        const double factor = norm_factor(setup_.norm, sum_lambdas);
         for (size_t k = 0; k < n; ++k) {
             const size_t row = b + sc.row[k];
             float g = static_cast<float>(sc.lambda[k] * factor);

@@ -32,6 +32,7 @@ struct RankArgs {
     uint32_t norm, truncation;
     double *lam, *hes;             // per row: the unscaled lambda and hessian sums
     double *qsum;                  // per query: the lambda sum
+    const uint32_t *queries;       // the queries this launch takes, one a block (blockIdx.x's is queries[blockIdx.x])
 };
 
 // The value of a per-rank register array at rank k (lane k % 64, slot k / 64), on every lane; k is the same on all.
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
     constexpr uint32_t STRIDE = NMAX + 4;  // the three term lists 32 bytes apart in the banks
     __shared__ __align__(16) double lds[3 * STRIDE];  // the sort's keys, then row i's terms in j order
     uint64_t *keys = reinterpret_cast<uint64_t *>(lds);
-    const uint32_t q = blockIdx.x, lane = threadIdx.x;
+    const uint32_t q = a.queries[blockIdx.x], lane = threadIdx.x;
     const uint32_t b = a.bounds[q], n = a.bounds[q + 1] - b;
     if (n == 0) {
         if (lane == 0) a.qsum[q] = 0.0;
@@ -227,11 +228,11 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
 
 // The gradients from the sums (lambdarank.rs:287-300, 405-415): g = f32(lambda * factor), h = f32(hessian *
 // factor), each times the row's weight; the factor is the query's (1 without normalization). A block per query.
-__global__ __launch_bounds__(64) void k_rank_scale(const uint32_t *__restrict__ bounds, const double *__restrict__ lam,
-                                                   const double *__restrict__ hes, const double *__restrict__ factor,
-                                                   const float *__restrict__ weight, float *__restrict__ grad,
-                                                   float *__restrict__ hess) {
-    const uint32_t q = blockIdx.x, b = bounds[q], e = bounds[q + 1];
+__global__ __launch_bounds__(64) void k_rank_scale(const uint32_t *__restrict__ bounds, const uint32_t *__restrict__ queries,
+                                                   const double *__restrict__ lam, const double *__restrict__ hes,
+                                                   const double *__restrict__ factor, const float *__restrict__ weight,
+                                                   float *__restrict__ grad, float *__restrict__ hess) {
+    const uint32_t q = queries[blockIdx.x], b = bounds[q], e = bounds[q + 1];
     const double f = factor ? factor[q] : 1.0;
     for (uint32_t r = b + threadIdx.x; r < e; r += 64) {
         float g = static_cast<float>(lam[r] * f);

@@ -540,10 +540,11 @@ def test_lambdarank_gradients_match_the_oracle():
 
 # The device path (k_rank_pairs: every query of at most 512 rows) under other settings: no normalization, a short
 # truncation, row weights, sigmoid 2, labels drawn uniformly (most pairs taken, where the synthetic queries take
-# few), a query of 500 rows (the 512-row kernel); and the host path (a query of more than 512 rows sends every query
-# to the host), both against the oracle bit for bit.
+# few), a query of 500 rows (the 512-row kernel); and queries of more than 512 rows on the host's threads beside the
+# device's (one such query, copied by itself; 70, with every row's scores copied), against the oracle bit for bit.
 @pytest.mark.parametrize("case", ["no norm, truncation 5", "weights, sigmoid 2", "uniform labels",
-                                  "one query of 500 rows, uniform labels", "one query of 700 rows", "NaN labels"])
+                                  "one query of 500 rows, uniform labels", "one query of 700 rows", "NaN labels",
+                                  "70 queries of 600 rows", "70 queries of 600 rows, no norm, weights"])
 def test_lambdarank_gradient_paths_match_the_oracle(case):
     say("lambdarank gradients", case)
     data = silvic_amd.synthetic(3, rows=60_000, seed=9)
@@ -568,7 +569,17 @@ def test_lambdarank_gradient_paths_match_the_oracle(case):
         qb = data.query_boundaries
         k = int(np.searchsorted(qb, 700))
         data.query_boundaries = np.concatenate([[0], qb[k:]]).astype(qb.dtype)  # rows 0..qb[k] become one query
-        assert np.diff(data.query_boundaries).max() > 512
+        sizes = np.diff(data.query_boundaries)
+        assert sizes.max() > 512 and (sizes > 512).sum() == 1  # that one on the host, every other on the device
+    elif case.startswith("70 queries of 600"):  # more host queries than are copied one at a time
+        qb = data.query_boundaries
+        k = int(np.searchsorted(qb, 42_000))
+        data.query_boundaries = np.concatenate([np.arange(0, 42_000, 600), qb[k:]]).astype(qb.dtype)
+        sizes = np.diff(data.query_boundaries)
+        assert (sizes > 512).sum() >= 70 and (sizes <= 512).sum() > 100
+        if "no norm" in case:
+            data.weight = np.random.default_rng(3).uniform(0.5, 2.0, data.num_rows).astype(np.float32)
+            kw = dict(lambdarank_norm=False)
     p = oracle.default_params(objective=_abi.OBJ_LAMBDARANK, **kw)
     t = silvic_amd.Trainer(dict(objective="lambdarank", num_leaves=31, device_type="rocm", **kw), data)
     try:
