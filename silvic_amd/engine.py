@@ -67,8 +67,9 @@ def resolve_params(params):
         out[ALIASES.get(k, k)] = v
     if out["objective"] not in OBJECTIVES:
         raise _abi.SilvicError("unsupported", f"objective {out['objective']!r} does not run on the rocm device")
-    if not out["use_quantized_grad"]:
-        raise _abi.SilvicError("unsupported", "the rocm device trains with quantized gradients only")
+    if not out["use_quantized_grad"]:  # float training stays on the CPU backend (a config error, not a device one)
+        raise _abi.SilvicError("config", "device_type=rocm trains with quantized gradients only "
+                                         "(use_quantized_grad=true), or use device_type=cpu")
     # the reference takes 2..=64 (config.rs:416-421); up to 32766 (16-bit units) is this backend's extension
     if not 2 <= int(out["num_grad_quant_bins"]) <= 32766 or int(out["num_grad_quant_bins"]) % 2:
         raise _abi.SilvicError("config", "num_grad_quant_bins must be even and in 2..=32766")

@@ -80,3 +80,17 @@ def test_oracle_is_not_linked_by_the_product():
     assert "oracle_" not in out
     deps = subprocess.run(["ldd", _abi.ROCM_LIB], capture_output=True, text=True).stdout
     assert "oracle" not in deps
+
+
+def test_float_training_is_refused_at_device_selection():
+    # the backend serves quantized histograms only; float training (use_quantized_grad=false) is refused when the
+    # parameters are resolved, before any device is touched, as the binding's choose_device refuses it
+    import pytest
+
+    from silvic_amd import _abi
+    from silvic_amd.engine import resolve_params
+
+    with pytest.raises(_abi.SilvicError) as e:
+        resolve_params({"objective": "binary", "use_quantized_grad": False, "device_type": "rocm"})
+    assert e.value.kind == "config" and "quantized gradients only" in str(e.value)
+    assert resolve_params({"objective": "binary"})["use_quantized_grad"]
