@@ -3074,6 +3074,16 @@ __device__ uint32_t pool_threshold(AdvShared<MAXL> &s, uint32_t ntent, uint32_t 
         const bool in = b.x > 0.0f && (st == T_EXPANDED || (st == T_LEAF && (m & 1u) && b.y > 0.0f));
         return in ? __float_as_uint(b.x) : 0u;
     };
+    // fewer than R in the pool (early in a tree): every candidate may be committed
+    if (tid == 0) s.band = 0;
+    __syncthreads();
+    uint32_t mine = 0;
+    for (uint32_t k = tid; k < ntent; k += nt) mine += bound_bits(k) ? 1u : 0u;
+    mine = wave_total(mine);
+    if (lane == 0 && mine) atomicAdd(&s.band, mine);
+    __syncthreads();
+    if (s.band < R) return 0u;  // uniform
+    __syncthreads();  // s.band is read before the rounds below set it
     uint32_t prefix = 0, mask = 0, above = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (uint32_t i = tid; i < 256u; i += nt) count[i] = 0;
