@@ -270,22 +270,27 @@ def trace_summary(args):
 def line_floor(v, layout, args, trees):
     """The HBM bytes per tree k_step_rows cannot avoid with this layout, from the device's line counts (srocm_profile
     mode 2) over the repeated iterations: every L2 miss fetches a 128-byte line (the request-size counters show no
-    other size), so 128 bytes per distinct line its gathers touch (the split bins of the parent rows, the packed
-    gradients of the built rows), every built row's slab row whole, the row ids read once (whole lines) and
-    written once, and the partials as written. Also the split-bin bytes if jobs that split on the same feature in a
+    other size), so 128 bytes per distinct line its gathers touch (the split bins of the parent rows; the packed
+    gradients of the built rows, unless they travel as one-byte codes beside the row ids), every built row's slab
+    row whole, the row ids read once (whole lines) and written once, and the partials as written. Also the split-bin bytes if jobs that split on the same feature in a
     step shared their lines, and the sparse jobs' share (fewer than two parent rows a split-bin line)."""
     prow, plines, brow, blines, shared, partials, packed, sp_rows, sp_lines, sp_built = v
     trees = max(trees, 1)
-    first = layout[0] if layout else {"width": 128, "row_bytes": 128}
+    first = layout[0] if layout else {"width": 128, "row_bytes": 128, "q32": False}
     slab_lines = -(-first["row_bytes"] // 128)
     pbytes = 256 * first["width"] * 4
+    # small units travel as one-byte codes beside the row ids (read and written with every partitioned row);
+    # otherwise every built row gathers its packed word
+    codes = not first.get("q32", False) and args.quant_bins <= 14
     parts = {
-        "split_bins": 128.0 * plines, "gradients": 128.0 * blines, "slab_rows": 128.0 * slab_lines * brow,
+        "split_bins": 128.0 * plines, "gradients": 2.0 * prow if codes else 128.0 * blines,
+        "slab_rows": 128.0 * slab_lines * brow,
         "row_ids_read": 4.0 * prow, "row_ids_written": 4.0 * prow,
         "partials": pbytes * packed + 2 * pbytes * (partials - packed),
     }
     floor = sum(parts.values())
-    reads = parts["split_bins"] + parts["gradients"] + parts["slab_rows"] + parts["row_ids_read"]
+    reads = (parts["split_bins"] + parts["gradients"] / (2.0 if codes else 1.0) + parts["slab_rows"] +
+             parts["row_ids_read"])
     algorithmic = 9.0 * prow + brow * (first["width"] + 4.0)
     out = {k + "_per_tree": b / trees for k, b in parts.items()}
     out.update({
@@ -293,7 +298,7 @@ def line_floor(v, layout, args, trees):
         "floor_over_algorithmic": floor / algorithmic if algorithmic else None,
         "parent_rows_per_tree": prow / trees, "built_rows_per_tree": brow / trees,
         "split_bin_lines_per_parent_row": plines / prow if prow else None,
-        "gradient_lines_per_built_row": blines / brow if brow else None,
+        "gradient_lines_per_built_row": blines / brow if brow else None, "gradients_carried_as_codes": codes,
         "split_bins_shared_per_step_per_tree": 128.0 * shared / trees,
         "sparse_jobs": {"parent_rows_per_tree": sp_rows / trees, "split_bin_lines_per_tree": sp_lines / trees,
                         "built_rows_per_tree": sp_built / trees},

@@ -644,6 +644,7 @@ struct Context {
 
     void load(const srocm_dataset *t, const srocm_dataset *const *v, uint32_t nv, const srocm_objective *obj) {
         if (!t || !obj) fail(SROCM_ERR_DATA, "load needs a training set and an objective");
+        pending_order.on = false;
         if (t->num_rows > 0xFFFFFFFFull) fail(SROCM_ERR_UNSUPPORTED, std::to_string(t->num_rows) + " rows on one rank; the limit is 2^32 - 1");
         if (obj->kind == SROCM_OBJ_LAMBDARANK) {
             load_ranking(t, obj);
@@ -1232,6 +1233,7 @@ struct Context {
 
     uint32_t reset_partition(const srocm_bag &bag) {
         require_loaded();
+        pending_order.on = false;  // the partition is rewritten
         if (rows == 0) {
             part_len = 0;
             return 0;
@@ -1359,6 +1361,7 @@ struct Context {
     void histogram(srocm_leaf_range leaf, int quantized, double *out, size_t len) {
         require_loaded();
         check_range(leaf);
+        ensure_order();
         if (!quantized) fail(SROCM_ERR_UNSUPPORTED, "float-mode histograms run on the cpu backend only");
         if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
         if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
@@ -1380,6 +1383,7 @@ struct Context {
     void histogram_noalloc(srocm_leaf_range leaf, int64_t *d_out, size_t len, int wait) {
         require_loaded();
         check_range(leaf);
+        ensure_order();  // after a boosting call: its buffers are preallocated, so this allocates nothing either
         if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
         if (!d_out) fail(SROCM_ERR_DEVICE, "null histogram buffer");
         if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
@@ -1463,6 +1467,7 @@ struct Context {
     uint32_t partition(srocm_leaf_range leaf, const srocm_bin_split &split) {
         require_loaded();
         check_range(leaf);
+        ensure_order();
         enqueue_partition(leaf, split);
         hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
         sync();
@@ -1473,6 +1478,7 @@ struct Context {
                                      double *out, size_t len) {
         require_loaded();
         check_range(leaf);
+        ensure_order();
         if (!quantized) fail(SROCM_ERR_UNSUPPORTED, "float-mode histograms run on the cpu backend only");
         if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
         if (side > 1) fail(SROCM_ERR_DEVICE, "bad side");
@@ -1495,6 +1501,7 @@ struct Context {
     void leaf_sums(const srocm_leaf_range *leaves, uint32_t n, float gs, float hs, int64_t *out) {
         require_loaded();
         for (uint32_t i = 0; i < n; ++i) check_range(leaves[i]);
+        ensure_order();
         if (n == 0) return;
         std::vector<LeafJob> jobs(n);
         uint32_t maxc = 0;
@@ -1821,6 +1828,9 @@ struct Context {
         // host staging at its largest, so that no tree allocates pinned memory
         h_result.alloc(((static_cast<size_t>(grow_tcap(L)) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7)) + tree_layout.bytes);
         h_fix.alloc(static_cast<size_t>(grow_tcap(L)) * (sizeof(RowRun) + sizeof(MergeJob) + 8) + 64);
+        d_runs.alloc(grow_tcap(L));  // the row-order restore's device lists at their largest too
+        d_merges.alloc(L);
+        d_starts.alloc(static_cast<size_t>(grow_tcap(L)) + L);
         h_nodes.alloc(L);
         h_lv.alloc(L);
         h_sums.alloc(2 * static_cast<size_t>(L));
@@ -1886,6 +1896,21 @@ struct Context {
     // `after_steps` (when set) is called after each batch of split steps is launched, before the host waits on it.
     void grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<srocm_bin_split> &splits, std::vector<GrowLeaf> &leaves,
               bool final_order = true, const std::function<void(const GrowState &)> *after_steps = nullptr);
+    void restore_order(uint32_t n, uint32_t ntent, const int32_t *lt);
+    // The boosting loop's last tree leaves its row order to be restored by the first call that reads the partition
+    // (ensure_order; a reset of the partition drops it), so a loop run an iteration at a time does not pay for it.
+    struct PendingOrder {
+        bool on = false;
+        uint32_t n = 0, ntent = 0;
+        std::vector<int32_t> lt;
+    };
+    bool defer_order = false;
+    PendingOrder pending_order;
+    void ensure_order() {
+        if (!pending_order.on) return;
+        pending_order.on = false;
+        restore_order(pending_order.n, pending_order.ntent, pending_order.lt.data());
+    }
 
     void copy_tree(const HostTree &t, const std::vector<GrowLeaf> &leaves, srocm_grown_tree *out) const {
         if (out->capacity_leaves < t.num_leaves) fail(SROCM_ERR_DEVICE, "grown tree has more leaves than the output holds");
@@ -2034,6 +2059,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     require_loaded();
     if (!quantized_once) fail(SROCM_ERR_DEVICE, "grow before quantize");
     check_range(spec.root);
+    ensure_order();
     if (spec.num_leaves < 1) fail(SROCM_ERR_CONFIG, "num_leaves must be positive");
     if (spec.num_leaves > GROW_MAX_LEAVES)
         fail(SROCM_ERR_UNSUPPORTED, "device growth takes num_leaves up to " + std::to_string(GROW_MAX_LEAVES));
@@ -2259,81 +2285,10 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
         bs.column = m.column;
     }
 
-    // the final row order (cpu.rs:556-599 keeps every leaf ascending): each unexpanded speculative leaf's rows into
-    // the first buffer in ascending order, then each leaf whose expansion was dropped merged from its runs
-    const TLeaf *tl = reinterpret_cast<const TLeaf *>(h_result.p);
+    // the final row order: now, or (the boosting loop's last tree) when a call next reads the partition
     if (final_order && root_searched) {
-        hip_check(hipMemcpyAsync(h_result.p, d_tl.p, static_cast<size_t>(ntent) * sizeof(TLeaf), hipMemcpyDeviceToHost, stream), "read leaves");
-        sync();
-    }
-    std::vector<RowRun> runs;
-    for (uint32_t k = 0; k < ntent && final_order && root_searched; ++k)
-        if (tl[k].state == T_LEAF && tl[k].count && (tl[k].buf || tl[k].rev))
-            runs.push_back(RowRun{tl[k].begin, tl[k].count, tl[k].buf, tl[k].rev});
-    std::vector<MergeJob> merges;
-    std::vector<uint32_t> starts;
-    for (uint32_t i = 0; i < n && final_order && root_searched; ++i) {
-        const uint32_t k = static_cast<uint32_t>(lt[i]);
-        if (tl[k].state != T_EXPANDED) continue;
-        MergeJob m{tl[k].begin, tl[k].count, static_cast<uint32_t>(starts.size()), 0};
-        std::vector<uint32_t> stack{k};  // the unexpanded leaves below k, in row order (left child first)
-        while (!stack.empty()) {
-            const uint32_t x = stack.back();
-            stack.pop_back();
-            if (x >= ntent) fail(SROCM_ERR_INTERNAL, "device learner lost a leaf");
-            if (tl[x].state == T_EXPANDED) {
-                stack.push_back(static_cast<uint32_t>(tl[x].kid) + 1);
-                stack.push_back(static_cast<uint32_t>(tl[x].kid));
-            } else if (tl[x].count) {
-                starts.push_back(tl[x].begin - m.begin);
-                ++m.runs;
-            }
-        }
-        starts.push_back(m.count);
-        if (m.runs > 1) merges.push_back(m);
-        else starts.resize(m.first);
-    }
-    if (!runs.empty() || !merges.empty()) {
-        const size_t rb = runs.size() * sizeof(RowRun), mb = merges.size() * sizeof(MergeJob), sb = starts.size() * 4;
-        h_fix.alloc(rb + mb + sb + 64);
-        std::memcpy(h_fix.p, runs.data(), rb);
-        std::memcpy(h_fix.p + rb, merges.data(), mb);
-        std::memcpy(h_fix.p + rb + mb, starts.data(), sb);
-        uint32_t longest = 1;
-        if (!runs.empty()) {
-            d_runs.alloc(runs.size());
-            hip_check(hipMemcpyAsync(d_runs.p, h_fix.p, rb, hipMemcpyHostToDevice, stream), "upload runs");
-            for (const RowRun &r : runs) longest = std::max(longest, r.count);
-            k_consolidate<<<dim3(std::min<uint32_t>(div_up(longest, 256 * 4), 64), static_cast<uint32_t>(runs.size())), 256, 0, stream>>>(
-                d_runs.p, part2.p, part.p);
-            launch_check("k_consolidate");
-        }
-        if (!merges.empty()) {
-            d_merges.alloc(merges.size());
-            d_starts.alloc(starts.size());
-            hip_check(hipMemcpyAsync(d_merges.p, h_fix.p + rb, mb, hipMemcpyHostToDevice, stream), "upload merges");
-            hip_check(hipMemcpyAsync(d_starts.p, h_fix.p + rb + mb, sb, hipMemcpyHostToDevice, stream), "upload merges");
-            longest = 1;
-            uint32_t most = 1;
-            for (const MergeJob &m : merges) {
-                longest = std::max(longest, m.count);
-                most = std::max(most, m.runs);
-            }
-            dim3 grid(std::min<uint32_t>(div_up(longest, 256 * 4), 256), static_cast<uint32_t>(merges.size()));
-            // pairwise rounds between the two buffers, every leaf's rows moved in each; an odd count leaves the
-            // result in the second buffer
-            uint32_t rounds = 0;
-            while ((1u << rounds) < most) ++rounds;
-            for (uint32_t t = 0; t < rounds; ++t) {
-                const bool even = (t & 1u) == 0;
-                k_merge_round<<<grid, 256, 0, stream>>>(d_merges.p, d_starts.p, t, even ? part.p : part2.p, even ? part2.p : part.p);
-                launch_check("k_merge_round");
-            }
-            if (rounds & 1u) {
-                k_copy_back<<<grid, 256, 0, stream>>>(d_merges.p, part2.p, part.p);
-                launch_check("k_copy_back");
-            }
-        }
+        if (defer_order) pending_order = PendingOrder{true, n, ntent, std::vector<int32_t>(lt, lt + n)};
+        else restore_order(n, ntent, lt);
     }
     if (prof.on && root_searched) {  // the root histogram was counted by launch_hist
         prof.builds += hc.hist_builds;
@@ -2411,6 +2366,88 @@ static void feature_mask(const std::vector<srocm_feature> &feats, double fractio
         return a.second < b.second;
     });
     for (size_t i = 0; i < count && i < keyed.size(); ++i) mask[keyed[i].second] = 1;
+}
+
+// The reference's row order after a grown tree (cpu.rs:556-599 keeps every leaf ascending), from the speculative
+// leaves the tree's steps left on the device (d_tl, `ntent` of them) and `lt`, each of the `n` committed leaves'
+// speculative leaf: each unexpanded speculative leaf's rows into the first buffer in ascending order, then each
+// committed leaf whose expansion was dropped merged from its runs. Its buffers are sized by ensure_grow, so it
+// allocates nothing.
+void Context::restore_order(uint32_t n, uint32_t ntent, const int32_t *lt) {
+    // the final row order (cpu.rs:556-599 keeps every leaf ascending): each unexpanded speculative leaf's rows into
+    // the first buffer in ascending order, then each leaf whose expansion was dropped merged from its runs
+    const TLeaf *tl = reinterpret_cast<const TLeaf *>(h_result.p);
+    hip_check(hipMemcpyAsync(h_result.p, d_tl.p, static_cast<size_t>(ntent) * sizeof(TLeaf), hipMemcpyDeviceToHost, stream), "read leaves");
+    sync();
+    std::vector<RowRun> runs;
+    for (uint32_t k = 0; k < ntent; ++k)
+        if (tl[k].state == T_LEAF && tl[k].count && (tl[k].buf || tl[k].rev))
+            runs.push_back(RowRun{tl[k].begin, tl[k].count, tl[k].buf, tl[k].rev});
+    std::vector<MergeJob> merges;
+    std::vector<uint32_t> starts;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t k = static_cast<uint32_t>(lt[i]);
+        if (tl[k].state != T_EXPANDED) continue;
+        MergeJob m{tl[k].begin, tl[k].count, static_cast<uint32_t>(starts.size()), 0};
+        std::vector<uint32_t> stack{k};  // the unexpanded leaves below k, in row order (left child first)
+        while (!stack.empty()) {
+            const uint32_t x = stack.back();
+            stack.pop_back();
+            if (x >= ntent) fail(SROCM_ERR_INTERNAL, "device learner lost a leaf");
+            if (tl[x].state == T_EXPANDED) {
+                stack.push_back(static_cast<uint32_t>(tl[x].kid) + 1);
+                stack.push_back(static_cast<uint32_t>(tl[x].kid));
+            } else if (tl[x].count) {
+                starts.push_back(tl[x].begin - m.begin);
+                ++m.runs;
+            }
+        }
+        starts.push_back(m.count);
+        if (m.runs > 1) merges.push_back(m);
+        else starts.resize(m.first);
+    }
+    if (!runs.empty() || !merges.empty()) {
+        const size_t rb = runs.size() * sizeof(RowRun), mb = merges.size() * sizeof(MergeJob), sb = starts.size() * 4;
+        h_fix.alloc(rb + mb + sb + 64);
+        std::memcpy(h_fix.p, runs.data(), rb);
+        std::memcpy(h_fix.p + rb, merges.data(), mb);
+        std::memcpy(h_fix.p + rb + mb, starts.data(), sb);
+        uint32_t longest = 1;
+        if (!runs.empty()) {
+            d_runs.alloc(runs.size());
+            hip_check(hipMemcpyAsync(d_runs.p, h_fix.p, rb, hipMemcpyHostToDevice, stream), "upload runs");
+            for (const RowRun &r : runs) longest = std::max(longest, r.count);
+            k_consolidate<<<dim3(std::min<uint32_t>(div_up(longest, 256 * 4), 64), static_cast<uint32_t>(runs.size())), 256, 0, stream>>>(
+                d_runs.p, part2.p, part.p);
+            launch_check("k_consolidate");
+        }
+        if (!merges.empty()) {
+            d_merges.alloc(merges.size());
+            d_starts.alloc(starts.size());
+            hip_check(hipMemcpyAsync(d_merges.p, h_fix.p + rb, mb, hipMemcpyHostToDevice, stream), "upload merges");
+            hip_check(hipMemcpyAsync(d_starts.p, h_fix.p + rb + mb, sb, hipMemcpyHostToDevice, stream), "upload merges");
+            longest = 1;
+            uint32_t most = 1;
+            for (const MergeJob &m : merges) {
+                longest = std::max(longest, m.count);
+                most = std::max(most, m.runs);
+            }
+            dim3 grid(std::min<uint32_t>(div_up(longest, 256 * 4), 256), static_cast<uint32_t>(merges.size()));
+            // pairwise rounds between the two buffers, every leaf's rows moved in each; an odd count leaves the
+            // result in the second buffer
+            uint32_t rounds = 0;
+            while ((1u << rounds) < most) ++rounds;
+            for (uint32_t t = 0; t < rounds; ++t) {
+                const bool even = (t & 1u) == 0;
+                k_merge_round<<<grid, 256, 0, stream>>>(d_merges.p, d_starts.p, t, even ? part.p : part2.p, even ? part2.p : part.p);
+                launch_check("k_merge_round");
+            }
+            if (rounds & 1u) {
+                k_copy_back<<<grid, 256, 0, stream>>>(d_merges.p, part2.p, part.p);
+                launch_check("k_copy_back");
+            }
+        }
+    }
 }
 
 // boosting.rs:227-324 train_one_iter / add, `count` times
@@ -2530,6 +2567,12 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             ScalesFromDevice(const DevScales *&s, const DevScales *v) : slot(s) { slot = v; }
             ~ScalesFromDevice() { slot = nullptr; }
         } from_device(grow_dsc, d_scales.p);
+        // the last tree's row order waits for the first call that reads the partition
+        struct Defer {
+            bool &flag;
+            Defer(bool &f, bool on) : flag(f) { flag = on; }
+            ~Defer() { flag = false; }
+        } defer(defer_order, last);
         grow(gs, tree, splits, leaves, last, renew ? &renew_on_device : nullptr);
         finalize();  // the grown tree's readback came after the last tree's leaf values
         if (tree.num_leaves == 1) {  // boosting.rs:301-310
@@ -2747,6 +2790,7 @@ int srocm_partition_rows(void *ctx, uint32_t *out, size_t len) {
         c.require_loaded();
         if (len > c.rows) fail(SROCM_ERR_DEVICE, "partition read of " + std::to_string(len) + " rows, the training set has " + std::to_string(c.rows));
         if (len && !out) fail(SROCM_ERR_DEVICE, "null output");
+        c.ensure_order();
         if (len) hip_check(hipMemcpyAsync(out, c.part.p, len * 4, hipMemcpyDeviceToHost, c.stream), "read partition");
         c.sync();
     });
