@@ -386,8 +386,8 @@ int srocm_partition_rows(void *ctx, uint32_t *out, size_t len);
 int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size_t len, int wait);
 
 /* Per-kernel timing with HIP events on the backend's stream, and algorithmic byte counts; no counterpart in the
- * reference (a measurement hook). srocm_profile: enable (1), enable with the sector model (2: after every split
- * step's k_step_rows launches, kernels that count the sectors its gathers touch, values [15]-[21]), or disable (0);
+ * reference (a measurement hook). srocm_profile: enable (1), enable with the line model (2: after every split
+ * step's k_step_rows launches, kernels that count the memory lines its gathers touch, values [15]-[24]), or disable (0);
  * each resets the counters.
  * srocm_profile_read writes min(len, SROCM_PROFILE_VALUES) values:
  *   [0] k_hist launches (root and trait histograms, one per slab)   [1] their ms   [2] their algorithmic bytes
@@ -396,14 +396,15 @@ int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size
  *   [6] histogram builds   [7] rows histogrammed   [8] rows x used columns   [9] rows partitioned
  *   [10] trait partition launches   [11] their ms (count + scatter + copy back)
  *   [12] device-growth split steps   [13] leaves they expanded   [14] of those, splits the trees kept
- *   sector model (mode 2; split steps, the first slab): [15] parent rows partitioned   [16] distinct 32-byte sectors
+ *   line model (mode 2; split steps, the first slab): [15] parent rows partitioned   [16] distinct 128-byte lines
  *   of the column-major split-feature bins they lie in, per job   [17] built-child rows histogrammed   [18] distinct
- *   sectors of the packed gradients they lie in   [19] split-bin sectors counted once per step over every job
- *   splitting on the same feature   [20] partials written   [21] of those, packed (256 x slab width x 4 bytes; the
- *   others {g, h} pairs, twice that)
+ *   lines of the packed gradients they lie in   [19] split-bin lines counted once per step over every job splitting
+ *   on the same feature   [20] partials written   [21] of those, packed (256 x slab width x 4 bytes; the others
+ *   {g, h} pairs, twice that)   [22]-[24] the sparse jobs' (fewer than two parent rows a split-bin line) parent rows,
+ *   split-bin lines and built rows
  * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
  * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
-#define SROCM_PROFILE_VALUES 22
+#define SROCM_PROFILE_VALUES 25
 int srocm_profile(void *ctx, int enable);
 int srocm_profile_read(void *ctx, double *out, uint32_t len);
 
