@@ -244,8 +244,8 @@ def trace_summary(args):
         rows += list(csv.DictReader(open(f)))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     win = timed_window(rows, args.warmup, args.steps)
-    agg, gaps = {}, 0.0
-    prev = None
+    agg, gaps, where = {}, 0.0, {}
+    prev, prev_k = None, None
     for r in win:
         s, e = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
         k = kernel_key(r["Kernel_Name"])
@@ -254,7 +254,11 @@ def trace_summary(args):
         a[1] += (e - s) / 1e3
         if prev is not None and s > prev:
             gaps += (s - prev) / 1e3
-        prev = max(prev or 0, e)
+            w = where.setdefault((prev_k, k), [0, 0.0])
+            w[0] += 1
+            w[1] += (s - prev) / 1e3
+        if prev is None or e >= prev:
+            prev, prev_k = e, k
     span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e3
     print(f"{args.steps} iterations, {span / args.steps:.1f} us per iteration from the first dispatch of the window "
           f"to the last; busy {sum(v[1] for v in agg.values()) / args.steps:.1f} us, idle between dispatches "
@@ -265,6 +269,13 @@ def trace_summary(args):
     busy = sum(v[1] for v in agg.values())
     for k, (n, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         print(f"| `{k}` | {n / args.steps:.2f} | {us / args.steps:.1f} | {us / n:.1f} | {us / busy:.1%} |")
+    print()
+    print("Where the idle time falls (the dispatch that ended last, then the next one to start):")
+    print()
+    print("| after | before | gaps per iteration | idle us per iteration |")
+    print("|---|---|---:|---:|")
+    for (k0, k1), (n, us) in sorted(where.items(), key=lambda kv: -kv[1][1])[:6]:
+        print(f"| `{k0}` | `{k1}` | {n / args.steps:.2f} | {us / args.steps:.1f} |")
 
 
 def line_floor(v, layout, args, trees):

@@ -381,6 +381,7 @@ struct Context {
     std::vector<float> h_label_v, h_weight_v;
     DevBuf<int32_t> packed, partial;
     DevBuf<uint32_t> part, part2, block_left, scalars;
+    DevBuf<uint32_t> maxima;  // the gradient maxima, MAX_SLOTS pairs
     DevBuf<uint8_t> codes0, codes1;  // grown trees: each row's gradient code beside its id in part / part2
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
@@ -638,7 +639,7 @@ struct Context {
                 grad.p, hess.p);
             launch_check("k_rank_scale");
         }
-        k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, scalars.p + 1);
+        k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, maxima.p);
         launch_check("k_max_abs");
     }
 
@@ -712,6 +713,7 @@ struct Context {
         build_slabs();
         // device buffers
         scalars.alloc(16);
+        maxima.alloc(2 * MAX_SLOTS);
         hip_check(hipMemsetAsync(scalars.p + 15, 0, 4, stream), "zero bin check");
         train = DevData{};
         upload_bins(t, train, true);
@@ -1163,11 +1165,16 @@ struct Context {
     // ------------------------------------------------------------------------------------------------
 
     std::pair<double, double> read_maxima() {
-        hip_check(hipMemcpyAsync(h_u32.p, scalars.p + 1, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream), "read maxima");
+        hip_check(hipMemcpyAsync(h_u32.p, maxima.p, 8 * MAX_SLOTS, hipMemcpyDeviceToHost, stream), "read maxima");
         sync();
+        uint32_t ug = 0, uh = 0;
+        for (uint32_t k = 0; k < MAX_SLOTS; ++k) {
+            ug = std::max(ug, h_u32.p[2 * k]);
+            uh = std::max(uh, h_u32.p[2 * k + 1]);
+        }
         float g, h;
-        std::memcpy(&g, &h_u32.p[0], 4);
-        std::memcpy(&h, &h_u32.p[1], 4);
+        std::memcpy(&g, &ug, 4);
+        std::memcpy(&h, &uh, 4);
         return {static_cast<double>(g), static_cast<double>(h)};
     }
 
@@ -1181,8 +1188,8 @@ struct Context {
         if (n != rows) fail(SROCM_ERR_DEVICE, "gradient arrays of " + std::to_string(n) + " rows, expected " + std::to_string(rows));
         hip_check(hipMemcpyAsync(grad.p, g, n * 4, hipMemcpyHostToDevice, stream), "upload grad");
         hip_check(hipMemcpyAsync(hess.p, h, n * 4, hipMemcpyHostToDevice, stream), "upload hess");
-        hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
-        k_max_abs<<<grid_rows(n), 256, 0, stream>>>(grad.p, hess.p, n, scalars.p + 1);
+        hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
+        k_max_abs<<<grid_rows(n), 256, 0, stream>>>(grad.p, hess.p, n, maxima.p);
         launch_check("k_max_abs");
         return read_maxima();
     }
@@ -2036,15 +2043,15 @@ std::pair<double, double> Context::compute_gradients() {
 
 void Context::launch_gradients() {
     require_loaded();
-    hip_check(hipMemsetAsync(scalars.p + 1, 0, 8, stream), "zero maxima");
+    hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
     if (rows && objective == SROCM_OBJ_LAMBDARANK) {
         ranking_gradients();
     } else if (rows) {
         const float *w = has_weight ? weight.p : nullptr;
         if (objective == SROCM_OBJ_REGRESSION)
-            k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, scalars.p + 1);
+            k_grad_regression<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, maxima.p);
         else
-            k_grad_binary<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, sigmoid, scalars.p + 1);
+            k_grad_binary<<<grid_rows(rows), 256, 0, stream>>>(train.scores.p, label.p, w, grad.p, hess.p, rows, sigmoid, maxima.p);
         launch_check("k_grad");
     }
 }
@@ -2488,7 +2495,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         // quantize.rs:56-84 on the device: nothing waits for the gradient maxima
         launch_gradients();
         d_scales.alloc(1);
-        k_quant_spec<<<1, 64, 0, stream>>>(scalars.p + 1, d_scales.p, p.num_grad_quant_bins, constant_hessian ? 1u : 0u, 1.0,
+        k_quant_spec<<<1, MAX_SLOTS, 0, stream>>>(maxima.p, d_scales.p, p.num_grad_quant_bins, constant_hessian ? 1u : 0u, 1.0,
                                            p.stochastic_rounding != 0 ? 1u : 0u, p.data_random_seed, it);
         launch_check("k_quant_spec");
         if (rows) {
@@ -2691,7 +2698,7 @@ int srocm_create(int ordinal, void **out) {
         c->scratch_at = scratch_address(dev);
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "create stream");
         hip_check(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking), "create stream");
-        c->h_u32.alloc(64);
+        c->h_u32.alloc(2 * MAX_SLOTS);
         *out = c.release();
         g_create_error.clear();
         return SROCM_OK;

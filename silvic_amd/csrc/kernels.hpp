@@ -102,6 +102,11 @@ __global__ void k_quantize(const float *__restrict__ grad, const float *__restri
         packed[r] = quantize_row(spec, grad[r], hess[r], row_offset + r);
 }
 
+// The gradient maxima live in MAX_SLOTS pairs of words: block b adds its own to pair b mod MAX_SLOTS, so at most
+// ceil(blocks / MAX_SLOTS) atomics meet at one address (atomics on one address are served one at a time, about
+// 11 ns each: 2048 blocks on one pair took 49 us where the loads took 4), and readers take the largest pair-wise.
+constexpr uint32_t MAX_SLOTS = 64;
+
 // An iteration's quantization made on the device from the gradient maxima, so the boosting loop never waits for
 // them: the scales of quantize.rs:56-84 and the fixed-point scales of quantize.rs:153-159, in the host's double
 // operations (ceil(log2 x) from the exponent: exact for the float maxima these are).
@@ -124,8 +129,16 @@ __device__ __forceinline__ float fixed_point_scale_d(double max_abs) {
 
 __global__ void k_quant_spec(const uint32_t *maxima, DevScales *out, uint32_t num_bins, uint32_t constant_hessian,
                              double constant, uint32_t stochastic, uint32_t seed, uint32_t iteration) {
+    // one wave (launched with MAX_SLOTS threads): lane l reads slot pair l of the maxima
+    uint32_t ug = maxima[2u * threadIdx.x], uh = maxima[2u * threadIdx.x + 1u];
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t x = __shfl_xor(ug, o), y = __shfl_xor(uh, o);
+        ug = ug > x ? ug : x;
+        uh = uh > y ? uh : y;
+    }
+    static_assert(MAX_SLOTS == 64, "one slot pair a lane");
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const double mg = static_cast<double>(__uint_as_float(maxima[0])), mh = static_cast<double>(__uint_as_float(maxima[1]));
+    const double mg = static_cast<double>(__uint_as_float(ug)), mh = static_cast<double>(__uint_as_float(uh));
     DevScales d;
     d.q.grad_max_q = static_cast<int32_t>(num_bins / 2);
     d.q.hess_max_q = static_cast<int32_t>(num_bins);
@@ -159,7 +172,7 @@ __device__ __forceinline__ uint32_t abs_bits(float v) {
     return (a != a) ? 0u : __float_as_uint(a);
 }
 
-// Block-wide max of two per-thread values, one atomicMax each per block (blockDim 256).
+// Block-wide max of two per-thread values, one atomicMax each per block into its slot pair (blockDim 256).
 __device__ __forceinline__ void block_max2(uint32_t a, uint32_t b, uint32_t *out) {
     __shared__ uint32_t sa[4], sb[4];
     for (int o = 32; o >= 1; o >>= 1) {
@@ -177,8 +190,9 @@ __device__ __forceinline__ void block_max2(uint32_t a, uint32_t b, uint32_t *out
             a = a > sa[w] ? a : sa[w];
             b = b > sb[w] ? b : sb[w];
         }
-        atomicMax(out, a);
-        atomicMax(out + 1, b);
+        uint32_t *slot = out + 2u * (blockIdx.x % MAX_SLOTS);
+        atomicMax(slot, a);
+        atomicMax(slot + 1, b);
     }
 }
 
