@@ -435,8 +435,8 @@ def main():
     t1 = time.perf_counter()
     profiled = trainer.step(args.steps)
     elapsed_profiled = time.perf_counter() - t1
-    prof = (C.c_double * 25)()
-    trainer.backend._check(lib.srocm_profile_read(h, prof, 25))
+    prof = (C.c_double * 26)()
+    trainer.backend._check(lib.srocm_profile_read(h, prof, 26))
     trainer.backend._check(lib.srocm_profile(h, 0))
     same_trees = all(np.array_equal(a["split_feature"], b["split_feature"]) and
                      np.array_equal(a["threshold_bin"], b["threshold_bin"]) for a, b in zip(gpu_trees, trainer.trees))
@@ -543,6 +543,8 @@ def main():
     }
     if line_model:
         out["roofline"]["line_model"] = line_model
+    if args.workload == "lambdarank":  # iterations of the repeat taken again with the host's normalization factors
+        out["lambdarank_host_factor_redos"] = list(prof)[25]
     print(json.dumps(out), flush=True)
     trainer.backend.close()
 

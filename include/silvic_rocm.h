@@ -95,8 +95,11 @@ typedef struct srocm_dataset {
 /* ObjectiveSetup (crates/silvic-core/src/backend/mod.rs:56-71), the fields of its LambdaRank variant included.
  * Lambdarank gradients (objective/lambdarank.rs:190-420) are computed by srocm_compute_gradients and by the
  * boosting loop, bit-identical to silvic's f64 CPU path either way: on the device (k_rank_pairs) for queries of at
- * most 512 rows, on the library's host threads in f64 for longer ones. They need the training set's
- * query_boundaries. */
+ * most 512 rows, on the library's host threads in f64 for longer ones. The normalization factor log2(1 + s) / s
+ * of a device query is made on the device from the two doubles around log2(1 + s), one of which is the C library's;
+ * when some row's f32 gradient could depend on which, the gradients are made again with the host's factors (the
+ * boosting loop then takes that iteration again; nothing of the first attempt reaches the scores). They need the
+ * training set's query_boundaries. */
 enum { SROCM_OBJ_REGRESSION = 0, SROCM_OBJ_BINARY = 1, SROCM_OBJ_LAMBDARANK = 2 };
 typedef struct srocm_objective {
     uint32_t kind;                  /* SROCM_OBJ_* */
@@ -402,9 +405,12 @@ int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size
  *   on the same feature   [20] partials written   [21] of those, packed (256 x slab width x 4 bytes; the others
  *   {g, h} pairs, twice that)   [22]-[24] the sparse jobs' (fewer than two parent rows a split-bin line) parent rows,
  *   split-bin lines and built rows
+ *   [25] lambdarank gradient computations whose device-made normalization factors were flagged (some row's f32
+ *   gradient could depend on the last bit of the C library's log2) and made again with the host's (counted in every
+ *   mode; normally 0)
  * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
  * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
-#define SROCM_PROFILE_VALUES 25
+#define SROCM_PROFILE_VALUES 26
 int srocm_profile(void *ctx, int enable);
 int srocm_profile_read(void *ctx, double *out, uint32_t len);
 

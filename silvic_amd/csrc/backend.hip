@@ -323,12 +323,14 @@ struct Profile {
     DevBuf<unsigned long long> sector_counts;
     DevBuf<uint32_t> sector_bits;
     double sector[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    double rank_redos = 0;  // lambdarank gradients whose device factors were flagged and made again by the host
     std::vector<hipEvent_t> pool;
     void reset() {
         hist_launches = hist_ms = hist_bytes = step_launches = step_ms = step_bytes = 0;
         builds = rows = bins = part_rows = part_launches = part_ms = 0;
         steps = expansions = splits = 0;
         for (double &v : sector) v = 0;
+        rank_redos = 0;
     }
 };
 
@@ -411,14 +413,16 @@ struct Context {
     DevBuf<DevNode> d_nodes;
     Pinned<DevNode> h_nodes;
     Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
-    DevBuf<double> d_leaf_vw;           // a boosted tree's renewed leaf values, then (from GROW_MAX_LEAVES) weights
+    DevBuf<double> d_leaf_vw[2];        // a boosted tree's renewed leaf values, then (from GROW_MAX_LEAVES) weights
+                                        // (alternate trees, as h_leaf_vw)
     DevBuf<uint32_t> d_gate;            // the boosted tree's leaves once it is complete with a split (k_tree_nodes)
     DevBuf<DevScales> d_scales;         // the boosting loop's quantization, made on the device (k_quant_spec)
     const DevScales *grow_dsc = nullptr;  // set while the boosting loop grows: the scales of GrowState
     hipEvent_t tree_event = nullptr;    // a grown tree's readback has landed
     hipEvent_t steps_event = nullptr;   // a batch of split steps has ended (the readback waits for it)
     Pinned<double> h_leaf_vw[2];        // and on their way to the host (alternate trees, so one lands while the
-                                        // host still reads the other)
+                                        // host still reads the other), on the copy stream
+    hipEvent_t vw_ready[2] = {nullptr, nullptr}, vw_landed[2] = {nullptr, nullptr};  // made; copied to the host
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
@@ -437,14 +441,25 @@ struct Context {
     Pinned<double> h_rank_qsum, h_rank_factor;
     std::unique_ptr<srocm_rank::WorkPool> rank_pool;  // host threads for the factors and the host's queries
     hipEvent_t rank_event = nullptr;                   // the host's queries' scores have arrived
+    // The device's factors (k_rank_scale, RANK_FACTOR_DEVICE): its flag that some query's could differ from the
+    // host's comes back on the copy stream; while `rank_flag_pending`, the last gradients wait for that verdict
+    // (rank_factors_vetoed). SROCM_TEST_RANK_FALLBACK=1 at load makes every query raise it (a test of the fallback).
+    DevBuf<uint32_t> d_rank_flag;
+    DevBuf<double> d_rank_pair;  // per query: the device's factors from both ends of the log2 bracket
+    Pinned<uint32_t> h_rank_flag;
+    hipEvent_t rank_flag_event = nullptr;
+    bool rank_flag_pending = false, rank_force_fallback = false;
 
     Profile prof;
     int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
 
     ~Context() {
         if (tree_event) (void)hipEventDestroy(tree_event);
+        for (hipEvent_t e : {vw_ready[0], vw_ready[1], vw_landed[0], vw_landed[1]})
+            if (e) (void)hipEventDestroy(e);
         if (steps_event) (void)hipEventDestroy(steps_event);
         if (rank_event) (void)hipEventDestroy(rank_event);
+        if (rank_flag_event) (void)hipEventDestroy(rank_flag_event);
         for (auto &e : prof.hist_events) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
@@ -477,6 +492,17 @@ struct Context {
         hipEvent_t e;
         hip_check(hipEventCreate(&e), "hipEventCreate");
         return e;
+    }
+
+    // Whether the last gradients' device factors were flagged (some query's could differ from the host's): then the
+    // gradients are made again with the host's factors. Waits for the flag's copy, not for the stream.
+    bool rank_factors_vetoed() {
+        if (!rank_flag_pending) return false;
+        hip_check(hipEventSynchronize(rank_flag_event), "event synchronize");
+        rank_flag_pending = false;
+        if (h_rank_flag.p[0] == 0u) return false;
+        prof.rank_redos += 1;  // counted whether or not profiling is on
+        return true;
     }
 
     // ------------------------------------------------------------------------------------------------
@@ -535,6 +561,12 @@ struct Context {
         });
         if (!rank_pool) rank_pool = std::make_unique<srocm_rank::WorkPool>(std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
         if (!rank_event) hip_check(hipEventCreateWithFlags(&rank_event, hipEventDisableTiming), "hipEventCreate");
+        if (!rank_flag_event) hip_check(hipEventCreateWithFlags(&rank_flag_event, hipEventDisableTiming), "hipEventCreate");
+        d_rank_flag.alloc(1);
+        h_rank_flag.alloc(1);
+        rank_flag_pending = false;
+        const char *fb = std::getenv("SROCM_TEST_RANK_FALLBACK");
+        rank_force_fallback = fb && fb[0] == '1';
         rank_nmax = 0;
         if (rank_dev_q.empty()) return;
         rank_nmax = 64;
@@ -550,6 +582,7 @@ struct Context {
         d_rank_hes.alloc(std::max<uint64_t>(rows, 1));
         d_rank_qsum.alloc(nq);
         d_rank_factor.alloc(nq);
+        d_rank_pair.alloc(2 * static_cast<size_t>(nq));
         h_rank_qsum.alloc(nq);
         h_rank_factor.alloc(nq);
         hip_check(hipMemcpy(d_rank_bounds.p, st.boundaries.data(), (nq + 1) * 4, hipMemcpyHostToDevice), "upload queries");
@@ -561,12 +594,14 @@ struct Context {
                   "upload discounts");
     }
 
-    // lambdarank gradients (lambdarank.rs:190-420). The device's queries: the pair sums (k_rank_pairs), then the
-    // per-query normalization factors log2(1 + s) / s on the host's pool (the C library's log2; the sums come back
-    // and the factors go out, so this waits for the stream), then k_rank_scale. The host's queries (more rows than
-    // k_rank_pairs takes): their scores come back first and their gradients are computed on the pool (f64) while the
-    // device works on its own, then go out. The maxima are taken on the device over every row.
-    void ranking_gradients() {
+    // lambdarank gradients (lambdarank.rs:190-420). The device's queries: the pair sums (k_rank_pairs), then
+    // k_rank_scale with the per-query normalization factors log2(1 + s) / s made on the device, whose flag comes back
+    // on the copy stream (rank_factors_vetoed); with `host_factors` (the flag was raised), the factors are made on
+    // the host's pool with the C library's log2 instead (the sums come back and the factors go out, so this waits for
+    // the stream). The host's queries (more rows than k_rank_pairs takes): their scores come back first and their
+    // gradients are computed on the pool (f64) while the device works on its own, then go out. The maxima are taken
+    // on the device over every row.
+    void ranking_gradients(bool host_factors) {
         const srocm_rank::Setup &st = ranker.setup();
         const uint32_t nq = static_cast<uint32_t>(st.boundaries.size() - 1);
         const uint32_t *qb = st.boundaries.data();
@@ -603,8 +638,9 @@ struct Context {
             default: k_rank_pairs<512><<<nd, 64, 0, stream>>>(ra); break;
             }
             launch_check("k_rank_pairs");
-            if (st.norm) hip_check(hipMemcpyAsync(h_rank_qsum.p, d_rank_qsum.p, static_cast<size_t>(nq) * 8,
-                                                  hipMemcpyDeviceToHost, stream), "read sums");
+            if (st.norm && host_factors)
+                hip_check(hipMemcpyAsync(h_rank_qsum.p, d_rank_qsum.p, static_cast<size_t>(nq) * 8, hipMemcpyDeviceToHost,
+                                         stream), "read sums");
         }
         if (host) {  // while the device ranks its queries
             hip_check(hipEventSynchronize(rank_event), "event synchronize");
@@ -617,11 +653,20 @@ struct Context {
                                          stream), "upload hess");
             });
         }
+        rank_flag_pending = false;
         if (rank_nmax) {
             const double *factor = nullptr;
-            if (st.norm) {
+            uint32_t mode = RANK_FACTOR_ONE;
+            const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
+            if (st.norm && !host_factors) {
+                mode = rank_force_fallback ? RANK_FACTOR_DEVICE_CHECKED : RANK_FACTOR_DEVICE;
+                hip_check(hipMemsetAsync(d_rank_flag.p, 0, 4, stream), "zero rank flag");
+                k_rank_factor<<<div_up(nd, 256), 256, 0, stream>>>(d_rank_queries.p, nd, d_rank_qsum.p, mode, d_rank_pair.p,
+                                                                  d_rank_flag.p);
+                launch_check("k_rank_factor");
+            } else if (st.norm) {
+                mode = RANK_FACTOR_HOST;
                 sync();
-                const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
                 const uint32_t per = (nd + rank_pool->size() - 1) / rank_pool->size();
                 rank_pool->run([&](unsigned w) {  // lambdarank.rs:287-300, as srocm_rank::Ranker takes it
                     for (uint32_t k = w * per; k < std::min(nd, (w + 1) * per); ++k) {
@@ -635,12 +680,19 @@ struct Context {
             }
             // the host's rows (uploaded above, from buffers that outlive the copies) are not written here
             k_rank_scale<<<static_cast<uint32_t>(rank_dev_q.size()), 64, 0, stream>>>(
-                d_rank_bounds.p, d_rank_queries.p, d_rank_lam.p, d_rank_hes.p, factor, has_weight ? weight.p : nullptr,
-                grad.p, hess.p);
+                d_rank_bounds.p, d_rank_queries.p, d_rank_lam.p, d_rank_hes.p, factor, d_rank_pair.p, mode,
+                has_weight ? weight.p : nullptr, grad.p, hess.p, d_rank_flag.p);
             launch_check("k_rank_scale");
+            rank_flag_pending = mode >= RANK_FACTOR_DEVICE;
         }
         k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, maxima.p);
         launch_check("k_max_abs");
+        if (rank_flag_pending) {  // the flag follows on the copy stream (after the maxima); nothing waits for it here
+            hip_check(hipEventRecord(rank_event, stream), "event");
+            hip_check(hipStreamWaitEvent(copy_stream, rank_event, 0), "stream wait");
+            hip_check(hipMemcpyAsync(h_rank_flag.p, d_rank_flag.p, 4, hipMemcpyDeviceToHost, copy_stream), "read rank flag");
+            hip_check(hipEventRecord(rank_flag_event, copy_stream), "event");
+        }
     }
 
     void load(const srocm_dataset *t, const srocm_dataset *const *v, uint32_t nv, const srocm_objective *obj) {
@@ -1181,7 +1233,7 @@ struct Context {
     uint32_t grid_rows(uint64_t n) const { return static_cast<uint32_t>(std::min<uint64_t>(std::max<uint64_t>(div_up(n, 256), 1), cus * 8ull)); }
 
     std::pair<double, double> compute_gradients();
-    void launch_gradients();  // the gradients and their maxima, without waiting for them
+    void launch_gradients(bool host_factors);  // the gradients and their maxima, without waiting for them
 
     std::pair<double, double> set_gradients(const float *g, const float *h, uint64_t n) {
         require_loaded();
@@ -2037,15 +2089,17 @@ void Context::repack(const uint8_t *src, uint32_t stride, uint32_t column, uint3
 
 // objective/regression.rs:70-93 and objective/binary.rs:27-50 on the device; maxima as cpu.rs:774-778.
 std::pair<double, double> Context::compute_gradients() {
-    launch_gradients();
+    launch_gradients(false);
+    if (rank_factors_vetoed()) launch_gradients(true);
     return read_maxima();
 }
 
-void Context::launch_gradients() {
+void Context::launch_gradients(bool host_factors) {
     require_loaded();
+    rank_flag_pending = false;
     hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
     if (rows && objective == SROCM_OBJ_LAMBDARANK) {
-        ranking_gradients();
+        ranking_gradients(host_factors);
     } else if (rows) {
         const float *w = has_weight ? weight.p : nullptr;
         if (objective == SROCM_OBJ_REGRESSION)
@@ -2468,8 +2522,8 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     std::vector<srocm_bin_split> splits;
     std::vector<GrowLeaf> leaves;
     std::vector<uint8_t> mask;
-    // A renewed tree's leaf values are made on the device and come back with the next wait on the stream (the
-    // next iteration's gradient maxima, or the end): its copy into `trees` waits for them.
+    // A renewed tree's leaf values are made on the device and come back on the copy stream (so the next iteration's
+    // kernels do not queue behind the copy): its copy into `trees` waits for them.
     struct Pending {
         bool on = false;
         HostTree tree;
@@ -2481,6 +2535,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     auto finalize = [&]() {
         if (!pend.on) return;
         const uint32_t nl = pend.tree.num_leaves;
+        hip_check(hipEventSynchronize(vw_landed[pend.buf]), "event synchronize");
         const double *vw = h_leaf_vw[pend.buf].p;
         // the leaves k_tree_nodes let through (after the tree's readback, so checked here)
         if (vw[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
@@ -2492,8 +2547,12 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         pend.on = false;
     };
     for (uint32_t it = first; it < first + count; ++it) {
+        // lambdarank: an iteration whose device factors were flagged is taken again with the host's (the flag also
+        // closed its leaf-renewal gate, so nothing of it reached the scores)
+        bool host_factors = false;
+    again:
         // quantize.rs:56-84 on the device: nothing waits for the gradient maxima
-        launch_gradients();
+        launch_gradients(host_factors);
         d_scales.alloc(1);
         k_quant_spec<<<1, MAX_SLOTS, 0, stream>>>(maxima.p, d_scales.p, p.num_grad_quant_bins, constant_hessian ? 1u : 0u, 1.0,
                                            p.stochastic_rounding != 0 ? 1u : 0u, p.data_random_seed, it);
@@ -2534,11 +2593,18 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             d_nodes.alloc(L);
             d_leaf_out.alloc(2 * L);
             d_leaf_values.alloc(L);
-            d_leaf_vw.alloc(2 * L + 1);
+            DevBuf<double> &dvw = d_leaf_vw[vw_buf];
+            dvw.alloc(2 * L + 1);
             h_leaf_vw[vw_buf].alloc(2 * L + 1);
+            for (hipEvent_t *e : {&vw_ready[vw_buf], &vw_landed[vw_buf]})
+                if (!*e) hip_check(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate");
+            // this buffer's last copy to the host has landed before the kernels below write it again (an iteration
+            // taken again reuses the buffer at once)
+            hip_check(hipStreamWaitEvent(stream, vw_landed[vw_buf], 0), "stream wait");
             d_gate.alloc(1);
             leaf_of.alloc(rows);
-            k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, d_leaf_vw.p + 2 * L);
+            k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, dvw.p + 2 * L,
+                                                rank_flag_pending ? d_rank_flag.p : nullptr);
             launch_check("k_tree_nodes");
             TreeLeavesArgs a{};
             a.colbins = train.col.p;
@@ -2558,7 +2624,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             a.gate = d_gate.p;
             launch_tree_leaves(a, p.num_leaves);
             LeafValueArgs la{d_leaf_out.p, d_gate.p, d_scales.p, 0u, bias ? 1u : 0u, 1.0f, 1.0f, p.cfg.lambda_l1, p.cfg.lambda_l2,
-                             p.learning_rate, init_score_value, d_leaf_vw.p, d_leaf_vw.p + L, d_leaf_values.p};
+                             p.learning_rate, init_score_value, dvw.p, dvw.p + L, d_leaf_values.p};
             k_leaf_values<<<1, 512, 0, stream>>>(la);
             launch_check("k_leaf_values");
             if (train.rows)
@@ -2566,8 +2632,11 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             for (auto &v : valid)
                 if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, col16, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
             launch_check("k_add_tree");
-            hip_check(hipMemcpyAsync(h_leaf_vw[vw_buf].p, d_leaf_vw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost,
-                                     stream), "read leaf values");
+            hip_check(hipEventRecord(vw_ready[vw_buf], stream), "event");
+            hip_check(hipStreamWaitEvent(copy_stream, vw_ready[vw_buf], 0), "stream wait");
+            hip_check(hipMemcpyAsync(h_leaf_vw[vw_buf].p, dvw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost,
+                                     copy_stream), "read leaf values");
+            hip_check(hipEventRecord(vw_landed[vw_buf], copy_stream), "event");
         };
         struct ScalesFromDevice {  // GrowState takes the device's scales while this tree grows
             const DevScales *&slot;
@@ -2582,6 +2651,10 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         } defer(defer_order, last);
         grow(gs, tree, splits, leaves, last, renew ? &renew_on_device : nullptr);
         finalize();  // the grown tree's readback came after the last tree's leaf values
+        if (!host_factors && rank_factors_vetoed()) {
+            host_factors = true;
+            goto again;
+        }
         if (tree.num_leaves == 1) {  // boosting.rs:301-310
             if (trees_added == 0) {
                 HostTree c;
@@ -2926,7 +2999,7 @@ int srocm_profile_read(void *ctx, double *out, uint32_t len) {
                                           p.builds, p.rows, p.bins, p.part_rows, p.part_launches, p.part_ms,
                                           p.steps, p.expansions, p.splits, p.sector[0], p.sector[1], p.sector[2],
                                           p.sector[3], p.sector[4], p.sector[5], p.sector[6], p.sector[7],
-                                          p.sector[8], p.sector[9]};
+                                          p.sector[8], p.sector[9], p.rank_redos};
         if (out) std::copy(v, v + std::min<uint32_t>(len, SROCM_PROFILE_VALUES), out);
     });
 }

@@ -3358,11 +3358,13 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
 // the children), its leaf sums zeroed, and *gate = its leaves; *gate = 0 otherwise (an unfinished tree or one
 // that never split: the gated kernels after it do nothing). Every node is checked as the host checks an uploaded
 // tree (a known feature; an internal child after its parent, a leaf child among the leaves), so the walks over it
-// end; a malformed tree flags ctl->error = 6 and closes the gate. *gate_out: the gate, for the host. One block.
-__global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *sums, uint32_t *gate, double *gate_out) {
+// end; a malformed tree flags ctl->error = 6 and closes the gate. *gate_out: the gate, for the host. A nonzero
+// *veto (when given: the iteration's gradients are to be made again) closes the gate too. One block.
+__global__ void k_tree_nodes(GrowState g, DevNode *nodes, unsigned long long *sums, uint32_t *gate, double *gate_out,
+                             const uint32_t *veto) {
     __shared__ uint32_t bad;
     GrowCtl *ctl = g.ctl;
-    const uint32_t n = ctl->done && !ctl->error ? ctl->num_leaves : 0u;
+    const uint32_t n = ctl->done && !ctl->error && !(veto && *veto) ? ctl->num_leaves : 0u;
     const uint32_t nl = n > 1u && n <= GROW_MAX_LEAVES ? n : 0u, nn = nl ? nl - 1u : 0u;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();

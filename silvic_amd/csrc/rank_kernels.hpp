@@ -10,12 +10,15 @@
 // lanes (lambda, hessian, lambda sum) each add up their list, so every sum has the host's operation sequence. The
 // table reads of row i + 1 are issued before row i is added up, so their latency hides behind that serial sum.
 //
-// The unscaled sums go to per-row f64 buffers and the lambda sum to a per-query buffer. The normalization factor
-// log2(1 + s) / s takes the host's log2 (one call per query, on the host, between k_rank_pairs and k_rank_scale), so
-// the scaled f32 gradients equal the host's to the last bit.
+// The unscaled sums go to per-row f64 buffers and the lambda sum to a per-query buffer. k_rank_factor makes each
+// query's normalization factor log2(1 + s) / s from both doubles around log2(1 + s) (log2_dd.hpp: the C library's
+// log2, which the host takes, is one of them), and k_rank_scale keeps it where both give every row of the query the
+// same f32 gradient and hessian, so the scaled gradients equal the host's to the last bit; a query where they could
+// differ raises a flag, and the host then makes the iteration's factors itself.
 #pragma once
 
 #include "lambdarank.hpp"
+#include "log2_dd.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -226,17 +229,60 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
     if (lane == 2) a.qsum[q] = acc;
 }
 
+// The normalization factors' modes: 1 without normalization (RANK_FACTOR_ONE), the host's (RANK_FACTOR_HOST, made
+// with the C library's log2 on the host), or made on the device from the lambda sums (RANK_FACTOR_DEVICE; and
+// RANK_FACTOR_DEVICE_CHECKED, which flags every query: a host-forced test of the fallback).
+constexpr uint32_t RANK_FACTOR_ONE = 0, RANK_FACTOR_HOST = 1, RANK_FACTOR_DEVICE = 2, RANK_FACTOR_DEVICE_CHECKED = 3;
+
+// The device's factors of the `nq` listed queries, a thread each (norm_factor: log2(1 + s) / s for a lambda sum
+// s > 0, else 1): pair[2q] from the round-down end of the log2 bracket, pair[2q + 1] from the round-up end (the same
+// when log2(1 + s) is a double). An undecided bracket, or the checked mode, sets *flag.
+__global__ __launch_bounds__(256) void k_rank_factor(const uint32_t *__restrict__ queries, uint32_t nq,
+                                                     const double *__restrict__ qsum, uint32_t mode,
+                                                     double *__restrict__ pair, uint32_t *__restrict__ flag) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    bool unsure = false;
+    if (i < nq) {
+        const uint32_t q = queries[i];
+        const double s = qsum[q];
+        double f0 = 1.0, f1 = 1.0;
+        if (s > 0.0) {
+            double lo, hi;
+            const int st = srocm_log2::log2_bracket(1.0 + s, lo, hi);
+            f0 = lo / s;
+            f1 = hi / s;
+            unsure = st == 2 || mode == RANK_FACTOR_DEVICE_CHECKED;
+        }
+        pair[2 * static_cast<size_t>(q)] = f0;
+        pair[2 * static_cast<size_t>(q) + 1] = f1;
+    }
+    if (__ballot(unsure) && (threadIdx.x & 63u) == 0) atomicOr(flag, 1u);
+}
+
 // The gradients from the sums (lambdarank.rs:287-300, 405-415): g = f32(lambda * factor), h = f32(hessian *
-// factor), each times the row's weight; the factor is the query's (1 without normalization). A block per query.
+// factor), each times the row's weight; the factor is the query's in `mode`: 1, the host's (`factor`), or the
+// device's pair (`pair`, k_rank_factor), where a row whose f32 gradient or hessian differs between the pair's two
+// factors sets *flag (the rows keep the first factor's values, and the host takes the iteration again with its own
+// factors). A block (one wave) per query.
 __global__ __launch_bounds__(64) void k_rank_scale(const uint32_t *__restrict__ bounds, const uint32_t *__restrict__ queries,
                                                    const double *__restrict__ lam, const double *__restrict__ hes,
-                                                   const double *__restrict__ factor, const float *__restrict__ weight,
-                                                   float *__restrict__ grad, float *__restrict__ hess) {
+                                                   const double *__restrict__ factor, const double *__restrict__ pair,
+                                                   uint32_t mode, const float *__restrict__ weight, float *__restrict__ grad,
+                                                   float *__restrict__ hess, uint32_t *__restrict__ flag) {
     const uint32_t q = queries[blockIdx.x], b = bounds[q], e = bounds[q + 1];
-    const double f = factor ? factor[q] : 1.0;
+    double f0 = 1.0, f1 = 1.0;
+    if (mode == RANK_FACTOR_HOST) {
+        f0 = f1 = factor[q];
+    } else if (mode >= RANK_FACTOR_DEVICE) {
+        f0 = pair[2 * static_cast<size_t>(q)];
+        f1 = pair[2 * static_cast<size_t>(q) + 1];
+    }
+    bool unsure = false;
     for (uint32_t r = b + threadIdx.x; r < e; r += 64) {
-        float g = static_cast<float>(lam[r] * f);
-        float h = static_cast<float>(hes[r] * f);
+        float g = static_cast<float>(lam[r] * f0);
+        float h = static_cast<float>(hes[r] * f0);
+        if (f1 != f0)
+            unsure = unsure || static_cast<float>(lam[r] * f1) != g || static_cast<float>(hes[r] * f1) != h;
         if (weight) {
             g *= weight[r];
             h *= weight[r];
@@ -244,6 +290,7 @@ __global__ __launch_bounds__(64) void k_rank_scale(const uint32_t *__restrict__ 
         grad[r] = g;
         hess[r] = h;
     }
+    if (__ballot(unsure) && threadIdx.x == 0) atomicOr(flag, 1u);
 }
 
 }  // namespace srocm

@@ -627,6 +627,44 @@ def test_lambdarank_boosting_matches_the_oracle(rows, params, rounds):
     t.backend.close()
 
 
+# The fallback of the device-made lambdarank normalization factors (SROCM_TEST_RANK_FALLBACK=1 at load makes every
+# device query raise the flag that some row's f32 gradient could depend on the last bit of the C library's log2): the
+# gradients are made again with the host's factors, and each boosting iteration is taken again after its first
+# attempt was kept from the scores (by the leaf-renewal gate; without renewal the host never applies it). Gradients,
+# trees and scores equal the oracle's, and the profile counts one redo per gradient computation.
+@pytest.mark.parametrize("renew", [1, 0])
+def test_lambdarank_host_factor_fallback_matches_the_oracle(monkeypatch, renew):
+    say("lambdarank host-factor fallback", renew)
+    monkeypatch.setenv("SROCM_TEST_RANK_FALLBACK", "1")
+    data = silvic_amd.synthetic(3, rows=60_000, seed=13)
+    prof = (C.c_double * 26)()
+    p = oracle.default_params(objective=_abi.OBJ_LAMBDARANK)
+    t = silvic_amd.Trainer(dict(objective="lambdarank", num_leaves=31, device_type="rocm"), data)
+    try:
+        t.backend._check(t.backend._lib.srocm_profile(t.backend._h, 0))  # the counters from zero
+        scores = t.backend.scores(0)
+        mg, mh = t.backend.compute_gradients()
+        g, h = t.backend.gradients()
+        og, oh = oracle.lambdarank_gradients(data, p, scores)
+        assert np.array_equal(g, og) and np.array_equal(h, oh)
+        assert mg == float(np.abs(og).max()) and mh == float(oh.max())
+        t.backend._check(t.backend._lib.srocm_profile_read(t.backend._h, prof, 26))
+        assert prof[25] == 1
+    finally:
+        t.backend.close()
+    rounds = 4
+    o, t = boost_both(data, dict(objective=_abi.OBJ_LAMBDARANK, num_leaves=31, quant_train_renew_leaf=renew), rounds)
+    try:
+        assert len(t.trees) == len(o.trees) == rounds
+        for i, (d, ot) in enumerate(zip(t.trees, o.trees)):
+            compare_trees(d, ot, f"tree {i}", exact_values=False)
+        assert np.array_equal(t.backend.scores(0), o.scores)
+        t.backend._check(t.backend._lib.srocm_profile_read(t.backend._h, prof, 26))
+        assert prof[25] == rounds
+    finally:
+        t.backend.close()
+
+
 # Validation sets (Backend::load's `valid`, cpu.rs:707-728; scores(1), cpu.rs:929): two sets binned with the
 # training set's layout; after boosting, their scores equal the oracle's trees replayed onto their rows with its
 # add_tree (cpu.rs:605-695), the initial score first and the first tree's values without it (replay.rs:38-40).
