@@ -408,7 +408,8 @@ int srocm_histogram_noalloc(void *ctx, srocm_leaf_range leaf, int64_t *out, size
  *   [25] lambdarank gradient computations whose device-made normalization factors were flagged (some row's f32
  *   gradient could depend on the last bit of the C library's log2) and made again with the host's (counted in every
  *   mode; normally 0)
- * Algorithmic bytes of a k_hist build: rows x (used columns + 4 B gradients + 4 B row id) + 16 B x total_bins.
+ * Algorithmic bytes of a k_hist build: rows x (the used features' bin bytes, two for a two-byte bin, + 4 B gradients
+ * + 4 B row id) + 2 x 4 B x the used features' bins (the output).
  * Builds whose row count only the device knows (partition_and_histogram) add launches and time but no rows. */
 #define SROCM_PROFILE_VALUES 26
 int srocm_profile(void *ctx, int enable);

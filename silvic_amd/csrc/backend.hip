@@ -126,6 +126,10 @@ struct Pinned {
 
 uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
 
+// A histogrammed row's k_step_rows work in partitioned rows: the split steps' planner gives a job workgroups in
+// proportion to its tiles plus this much for each tile's worth of built-child rows.
+constexpr float STEP_HIST_WEIGHT = 3.0f;
+
 // ---------------------------------------------------------------------------------------------------------
 // Host restatements the driver needs (quantize.rs, split.rs, tree.rs)
 // ---------------------------------------------------------------------------------------------------------
@@ -1337,14 +1341,31 @@ struct Context {
 
     // The histogram of rows part[begin..+count] (or the `side` child of that range split at *dev_left) into
     // `out` (i64 {g,h} per bin), and parent -= out when `parent` is set.
+    // The features a histogram build evaluates: their columns, their bin bytes a row (two for a feature of
+    // two-byte bins) and their bins (for the algorithmic byte counts of srocm_profile).
+    struct HistUse {
+        uint64_t columns = 0, bin_bytes = 0, bins = 0;
+    };
+    template <class Keep>
+    HistUse hist_use(Keep &&keep) const {
+        HistUse u;
+        for (uint32_t f = 0; f < nf; ++f)
+            if (keep(f) && feats[f].num_bins) {
+                ++u.columns;
+                u.bin_bytes += group_bits[feats[f].group] == 16 ? 2u : 1u;
+                u.bins += feats[f].num_bins;
+            }
+        return u;
+    }
+
     void launch_hist(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
-                     int64_t *parent, uint64_t bins_used) {
-        launch_hist_into(begin, count, dev_left, side, out, parent, bins_used, partial.p, hist_groups(count), prof.on);
+                     int64_t *parent, const HistUse &use) {
+        launch_hist_into(begin, count, dev_left, side, out, parent, use, partial.p, hist_groups(count), prof.on);
     }
 
     // launch_hist with the partials in `partials` (grid * 256 * max_width {g, h} pairs) over `grid` workgroups
     void launch_hist_into(uint32_t begin, uint32_t count, const uint32_t *dev_left, uint32_t side, int64_t *out,
-                          int64_t *parent, uint64_t bins_used, int32_t *partials, uint32_t grid, bool profiled) {
+                          int64_t *parent, const HistUse &use, int32_t *partials, uint32_t grid, bool profiled) {
         for (auto &s : slabs) {
             HistArgs a{slab_bins.p + s.bins_off, part.p, packed.p, partials, dev_left, begin, count, side, flush_rows(), grid, HIST_MIN_ROWS,
                        slab_pos_word.p + s.pos_off, s.row_bytes() / 4};
@@ -1387,21 +1408,18 @@ struct Context {
         }
         if (profiled) {
             prof.builds += 1;
-            if (!dev_left) {  // rows known on the host: rows x (used bins + 4 B gradients + 4 B row id) + the output
-                // (with any two-byte group, every bin counts two bytes)
+            if (!dev_left) {  // rows known on the host: rows x (the used features' bin bytes + 4 B gradients + 4 B
+                // row id) + the output, 2 x 4 B a bin of the used features
                 prof.rows += count;
-                prof.bins += static_cast<double>(count) * static_cast<double>(bins_used);
-                prof.hist_bytes += static_cast<double>(count) * (static_cast<double>(bins_used) * (col16 ? 2.0 : 1.0) + 8.0) +
-                                   16.0 * static_cast<double>(total_bins);
+                prof.bins += static_cast<double>(count) * static_cast<double>(use.columns);
+                prof.hist_bytes += static_cast<double>(count) * (static_cast<double>(use.bin_bytes) + 8.0) +
+                                   8.0 * static_cast<double>(use.bins);
             }
         }
     }
 
-    uint64_t used_columns() const {
-        uint64_t n = 0;
-        for (uint32_t f = 0; f < nf; ++f)
-            if (used[f] && feats[f].num_bins) ++n;
-        return n;
+    HistUse used_columns() const {
+        return hist_use([&](uint32_t f) { return used[f] != 0; });
     }
 
     void check_range(srocm_leaf_range leaf) const {
@@ -1947,6 +1965,10 @@ struct Context {
         g.ncg = ncg;
         g.nsg = nsg;
         g.flush_rows = flush_rows();
+        // a workgroup's i32 sums take at most (2^31 - 1) / max_q rows
+        const uint64_t mq = static_cast<uint64_t>(std::max<int64_t>(std::max(max_gq, max_hq), 1));
+        g.tile_cap = static_cast<uint32_t>(std::max<uint64_t>(std::min<uint64_t>((2147483647ull / mq) / STEP_TILE, 1u << 30), 1));
+        g.hist_weight = STEP_HIST_WEIGHT;
         return g;
     }
 
@@ -2155,9 +2177,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
             part.p, packed.p, spec.root.begin, spec.root.count, codes0.p);
         launch_check("k_gh_codes");
     }
-    uint64_t used_root = 0;
-    for (uint32_t f = 0; f < nf; ++f)
-        if ((mask[f] || static_cast<int32_t>(f) == sums_feature) && feats[f].num_bins) ++used_root;
+    const HistUse used_root = hist_use([&](uint32_t f) { return mask[f] || static_cast<int32_t>(f) == sums_feature; });
     // the tree block comes back with every check for the end of the tree
     const TreeLayout &lay = tree_layout;
     const size_t tl_max = (static_cast<size_t>(grow_tcap(L)) * sizeof(TLeaf) + 7) & ~static_cast<size_t>(7);

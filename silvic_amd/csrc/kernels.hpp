@@ -2206,6 +2206,11 @@ __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_excl_sum(uint32_t v) { return wave_incl_sum(v) - v; }
 __device__ __forceinline__ uint32_t wave_total(uint32_t v) { return __shfl(wave_incl_sum(v), 63); }
+__device__ __forceinline__ float wave_total_f32(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
 
 constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
 constexpr uint32_t SPEC_FEW = 8;           // at most this many: picked by repeated wave maxima (top_few)
@@ -2352,7 +2357,8 @@ struct GrowState {
     uint32_t ncg;             // column groups of k_step_reduce
     uint32_t nsg;             // scan units of k_step_scan (a wave per unit and child)
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
-    uint32_t pad_;
+    uint32_t tile_cap;        // k_step_rows tiles a workgroup may take (its i32 sums of the quantized units)
+    float hist_weight;        // a histogrammed row's k_step_rows work in partitioned rows (the planner's cost)
 };
 
 __device__ __forceinline__ double grow_sg(const GrowState &g) { return g.dsc ? g.dsc->sg : g.sg; }
@@ -3266,6 +3272,7 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const bool on = lane < njobs;
         JobPlan J = {};
         uint32_t hist = 0, ntiles = 0;
+        float cost = 0.0f;
         if (on) {
             const uint32_t tt = s.job_t[lane];
             const TLeaf &l = g.tl[tt];
@@ -3285,6 +3292,11 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             J.src_rev = l.rev;
             ntiles = (l.count + STEP_TILE - 1) / STEP_TILE;
             J.ntiles = ntiles;
+            // the job's k_step_rows work in tiles: every tile partitions, and the built child's share of its rows is
+            // histogrammed besides (hist_weight tiles' worth a tile of built rows)
+            const double lc = static_cast<double>(info.left_count), rc = static_cast<double>(info.right_count);
+            const double built = hist && lc + rc > 0.0 ? (lc <= rc ? lc : rc) / (lc + rc) : 0.0;
+            cost = static_cast<float>(ntiles) * (1.0f + g.hist_weight * static_cast<float>(built));
             J.parent_count = l.cnt;
             J.child_ug[0] = info.left_grad;
             J.child_uh[0] = info.left_hess;
@@ -3296,13 +3308,22 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         const uint32_t hist_before = wave_excl_sum(hist);
         const uint32_t tiles_before = wave_excl_sum(ntiles);
         const uint32_t total_tiles = wave_total(ntiles);
+        const float total_cost = wave_total_f32(cost);
         uint32_t groups = 0;
-        if (on) {  // at most `per` tiles a workgroup in every job, so no job's workgroups run long; the rounding up in
-            // each job costs at most one workgroup a job, so with target - njobs per share the step fits in one
-            // round of workgroups (one per compute unit)
+        if (on) {  // workgroups in proportion to the jobs' work (a job's tiles go to its workgroups by ticket), so that
+            // no job's workgroups run long; the rounding up in each job costs at most one workgroup a job, so with
+            // target - njobs for the shares the step fits in one round of workgroups (one per compute unit). At most
+            // tile_cap tiles a workgroup (its i32 sums), and no more workgroups than tiles.
             const uint32_t share = g.target_groups > njobs ? g.target_groups - njobs : 1u;
-            const uint32_t per = total_tiles > g.target_groups ? (total_tiles + share - 1) / share : 1u;
-            groups = (ntiles + per - 1) / per;
+            if (total_tiles <= g.target_groups) {
+                groups = ntiles;
+            } else {
+                const float per_cost = total_cost / static_cast<float>(share);
+                groups = static_cast<uint32_t>(__builtin_ceilf(cost / per_cost));
+                const uint32_t least = (ntiles + g.tile_cap - 1) / g.tile_cap;
+                groups = groups < least ? least : groups;
+                groups = groups > ntiles ? ntiles : groups;
+            }
             if (groups == 0) groups = 1;
         }
         const uint32_t groups_before = wave_excl_sum(groups);
@@ -4334,7 +4355,18 @@ __global__ __launch_bounds__(256) void k_step_reduce(GrowState g, ReduceStepArgs
         const uint32_t j = job_of(P.red_base, P.njobs, item);
         const JobPlan &J = P.jobs[j];
         const uint32_t ways = J.ways, groups = J.groups;
-        const uint32_t r = item - J.red_base, cgi = r / ways, sub = r - cgi * ways;
+        const uint32_t r = item - J.red_base;
+        uint32_t cgi, sub;
+        if ((g.ncg & 15u) == 0u) {
+            // column groups 2p and 2p + 1 (one 128-byte line of a packed partial) 8 items apart, so on one XCD (blocks
+            // go to the 8 XCDs in turn): the second reads the line from that XCD's L2
+            const uint32_t w = r & 15u, pi = (r >> 4) * 8u + (w & 7u), pair = pi / ways;
+            sub = pi - pair * ways;
+            cgi = 2u * pair + (w >> 3);
+        } else {
+            cgi = r / ways;
+            sub = r - cgi * ways;
+        }
         const ColGroup &cg = a.cgs[cgi];  // read in place: a column is picked per thread
         int64_t *built = g.pool + static_cast<size_t>(J.built_slot) * g.slot_stride;
         int64_t *parent = g.pool + static_cast<size_t>(J.parent_slot) * g.slot_stride;
