@@ -2226,7 +2226,7 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     StepArgs sa{slab_bins.p + sl.bins_off, slab_stride(sl), step_partial.p + 2 * sl.step_partial_off, d_fmt.p + si * k1_groups(),
                                 slab_col_bins.p + sl.col_bins_off, slab_pos_word.p + sl.pos_off, sl.row_bytes() / 4, k1_groups(), packed.p,
                                 train.col.p, col16, rows, part.p, part2.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(),
-                                si == 0 ? 1u : 0u, codes ? codes0.p : nullptr, codes ? codes1.p : nullptr};
+                                si == 0 ? 1u : 0u, g.tile_cap, codes ? codes0.p : nullptr, codes ? codes1.p : nullptr};
                     const uint32_t grid = k1_groups() * static_cast<uint32_t>(sj - si);
                     // the instance with carried gradient codes when the units fit them (never with separate counters)
 #define SROCM_STEP_CASE(id, W, WIDE, PACK, DP)                                                                    \

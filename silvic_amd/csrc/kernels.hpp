@@ -3473,6 +3473,7 @@ struct StepArgs {
     GrowCtl *ctl;
     uint32_t flush_rows;
     uint32_t partition;          // 1: this launch partitions (the first slab's alone); 0: histogram only
+    uint32_t tile_cap;           // tiles a workgroup takes at most (its i32 sums of the quantized units)
     uint8_t *codes0, *codes1;    // each row's one-byte gradient code beside its id in buf0 / buf1 (packed_code), or
                                  // null: the histograms gather the packed words
 };
@@ -3996,10 +3997,14 @@ __device__ __forceinline__ void step_rows_body(const StepArgs &a, int32_t *lds, 
     // take tiles gi, gi + groups, ...
     // A workgroup holds the tickets of its current and next tiles, and loads the next tile's rows while it
     // histograms the current one (their split bins after it).
+    // At most a.tile_cap tickets a workgroup, whatever the others' pace (its i32 sums; the planner gives every job
+    // enough workgroups for its tiles at that many each).
     __syncthreads();  // the LDS histogram is zeroed
+    uint32_t taken = 0;  // tickets this workgroup drew (thread 0's count)
     if (tid == 0) {
         sh.tile = v.partition ? atomicAdd(&J.ticket, 1u) : gi;
-        sh.tile2 = v.partition ? atomicAdd(&J.ticket, 1u) : gi + v.groups;
+        sh.tile2 = v.partition ? (a.tile_cap > 1u ? atomicAdd(&J.ticket, 1u) : v.ntiles) : gi + v.groups;
+        taken = a.tile_cap > 1u ? 2u : 1u;
     }
     __syncthreads();
     uint32_t t = sh.tile, tn = sh.tile2;
@@ -4013,7 +4018,10 @@ __device__ __forceinline__ void step_rows_body(const StepArgs &a, int32_t *lds, 
         TileState st;
         const uint32_t nb = tile_front<CODES>(v, t, r, st, sh);
         uint32_t ticket = next;
-        if (v.partition && tid == 0) ticket = atomicAdd(&J.ticket, 1u);
+        if (v.partition && tid == 0) {
+            ticket = taken < a.tile_cap ? atomicAdd(&J.ticket, 1u) : v.ntiles;
+            ++taken;
+        }
         next += v.groups;
         if (tn < v.ntiles) tile_rows<CODES>(v, tn, r);
         // a tile that takes the packed words past flush_rows rows is histogrammed by all waves around the flushes
