@@ -2358,7 +2358,8 @@ struct GrowState {
     uint32_t nsg;             // scan units of k_step_scan (a wave per unit and child)
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
     uint32_t tile_cap;        // k_step_rows tiles a workgroup may take (its i32 sums of the quantized units)
-    float hist_weight;        // a histogrammed row's k_step_rows work in partitioned rows (the planner's cost)
+    float hist_weight;        // the planner's cost of a tile of histogrammed rows, in partitioned tiles of a dense
+    float sparse_weight;      // leaf, and the most a tile of a sparse leaf costs more
 };
 
 __device__ __forceinline__ double grow_sg(const GrowState &g) { return g.dsc ? g.dsc->sg : g.sg; }
@@ -3292,11 +3293,14 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
             J.src_rev = l.rev;
             ntiles = (l.count + STEP_TILE - 1) / STEP_TILE;
             J.ntiles = ntiles;
-            // the job's k_step_rows work in tiles: every tile partitions, and the built child's share of its rows is
-            // histogrammed besides (hist_weight tiles' worth a tile of built rows)
+            // the job's k_step_rows work in tiles: every tile partitions, its rows' split bins costing more the sparser
+            // the leaf's rows lie (a line a row once they are sparser than one in 128: sparse_weight at most), and the
+            // built child's share of its rows is histogrammed besides (hist_weight a tile of built rows)
             const double lc = static_cast<double>(info.left_count), rc = static_cast<double>(info.right_count);
             const double built = hist && lc + rc > 0.0 ? (lc <= rc ? lc : rc) / (lc + rc) : 0.0;
-            cost = static_cast<float>(ntiles) * (1.0f + g.hist_weight * static_cast<float>(built));
+            const double spread = static_cast<double>(g.tl[0].count) / (128.0 * static_cast<double>(l.count ? l.count : 1u));
+            cost = static_cast<float>(ntiles) * (1.0f + g.sparse_weight * static_cast<float>(spread < 1.0 ? spread : 1.0) +
+                                                 g.hist_weight * static_cast<float>(built));
             J.parent_count = l.cnt;
             J.child_ug[0] = info.left_grad;
             J.child_uh[0] = info.left_hess;
