@@ -444,7 +444,7 @@ def main():
         log("the repeated iterations grew different trees")
     (hist_launches, hist_ms, hist_bytes, step_launches, step_ms, step_bytes, builds, hist_rows, hist_bins,
      part_rows, _, _, grow_steps, expansions, kept) = list(prof)[:15]
-    line_model = line_floor(list(prof)[15:], layout, args, len(profiled)) if args.line_model else None
+    line_model = line_floor(list(prof)[15:25], layout, args, len(profiled)) if args.line_model else None
     steps = max(len(timed), 1)
     iters_per_s = steps / elapsed
     psteps = max(len(profiled), 1)

@@ -419,16 +419,14 @@ struct Context {
     DevBuf<DevNode> d_nodes;
     Pinned<DevNode> h_nodes;
     Pinned<unsigned long long> h_sums;  // leaf sums on their way to the host
-    DevBuf<double> d_leaf_vw[2];        // a boosted tree's renewed leaf values, then (from GROW_MAX_LEAVES) weights
-                                        // (alternate trees, as h_leaf_vw)
+    DevBuf<double> d_leaf_vw;           // per tree of a boosting call (2 GROW_MAX_LEAVES + 1 each): its renewed leaf
+                                        // values, then (from GROW_MAX_LEAVES) weights, then the gate
     DevBuf<uint32_t> d_gate;            // the boosted tree's leaves once it is complete with a split (k_tree_nodes)
     DevBuf<DevScales> d_scales;         // the boosting loop's quantization, made on the device (k_quant_spec)
     const DevScales *grow_dsc = nullptr;  // set while the boosting loop grows: the scales of GrowState
     hipEvent_t tree_event = nullptr;    // a grown tree's readback has landed
     hipEvent_t steps_event = nullptr;   // a batch of split steps has ended (the readback waits for it)
-    Pinned<double> h_leaf_vw[2];        // and on their way to the host (alternate trees, so one lands while the
-                                        // host still reads the other), on the copy stream
-    hipEvent_t vw_ready[2] = {nullptr, nullptr}, vw_landed[2] = {nullptr, nullptr};  // made; copied to the host
+    Pinned<double> h_leaf_vw;           // and on the host, copied once at the end of the call
     Pinned<float> h_lv;
     DevBuf<uint16_t> leaf_of;  // each training row's leaf in the last tree (k_tree_leaves)
     DevBuf<float> d_leaf_values;
@@ -454,15 +452,13 @@ struct Context {
     DevBuf<double> d_rank_pair;  // per query: the device's factors from both ends of the log2 bracket
     Pinned<uint32_t> h_rank_flag;
     hipEvent_t rank_flag_event = nullptr;
-    bool rank_flag_pending = false, rank_force_fallback = false;
+    bool rank_flag_pending = false, rank_flag_queued = false, rank_force_fallback = false;
 
     Profile prof;
     int2 *scratch_at = nullptr;  // this device's copy of `scratch` (srocm_histogram_noalloc)
 
     ~Context() {
         if (tree_event) (void)hipEventDestroy(tree_event);
-        for (hipEvent_t e : {vw_ready[0], vw_ready[1], vw_landed[0], vw_landed[1]})
-            if (e) (void)hipEventDestroy(e);
         if (steps_event) (void)hipEventDestroy(steps_event);
         if (rank_event) (void)hipEventDestroy(rank_event);
         if (rank_flag_event) (void)hipEventDestroy(rank_flag_event);
@@ -504,6 +500,7 @@ struct Context {
     // gradients are made again with the host's factors. Waits for the flag's copy, not for the stream.
     bool rank_factors_vetoed() {
         if (!rank_flag_pending) return false;
+        queue_rank_flag();
         hip_check(hipEventSynchronize(rank_flag_event), "event synchronize");
         rank_flag_pending = false;
         if (h_rank_flag.p[0] == 0u) return false;
@@ -693,12 +690,18 @@ struct Context {
         }
         k_max_abs<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, rows, maxima.p);
         launch_check("k_max_abs");
-        if (rank_flag_pending) {  // the flag follows on the copy stream (after the maxima); nothing waits for it here
-            hip_check(hipEventRecord(rank_event, stream), "event");
-            hip_check(hipStreamWaitEvent(copy_stream, rank_event, 0), "stream wait");
-            hip_check(hipMemcpyAsync(h_rank_flag.p, d_rank_flag.p, 4, hipMemcpyDeviceToHost, copy_stream), "read rank flag");
-            hip_check(hipEventRecord(rank_flag_event, copy_stream), "event");
-        }
+        rank_flag_queued = false;  // queue_rank_flag copies it, once the kernels after these are queued
+    }
+
+    // The device factors' flag, copied on the copy stream behind the kernels queued so far (the boosting loop calls
+    // this once the iteration's quantization is queued, so the API calls leave no gap between its kernels).
+    void queue_rank_flag() {
+        if (!rank_flag_pending || rank_flag_queued) return;
+        hip_check(hipEventRecord(rank_event, stream), "event");
+        hip_check(hipStreamWaitEvent(copy_stream, rank_event, 0), "stream wait");
+        hip_check(hipMemcpyAsync(h_rank_flag.p, d_rank_flag.p, 4, hipMemcpyDeviceToHost, copy_stream), "read rank flag");
+        hip_check(hipEventRecord(rank_flag_event, copy_stream), "event");
+        rank_flag_queued = true;
     }
 
     void load(const srocm_dataset *t, const srocm_dataset *const *v, uint32_t nv, const srocm_objective *obj) {
@@ -2545,29 +2548,35 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
     std::vector<srocm_bin_split> splits;
     std::vector<GrowLeaf> leaves;
     std::vector<uint8_t> mask;
-    // A renewed tree's leaf values are made on the device and come back on the copy stream (so the next iteration's
-    // kernels do not queue behind the copy): its copy into `trees` waits for them.
+    // A renewed tree's leaf values are made on the device, in the tree's own slot of d_leaf_vw, and come back with
+    // every other tree's of the call in one copy at its end (a copy after each tree idled the GPU between
+    // iterations); the trees' copies into `trees` wait for them.
     struct Pending {
-        bool on = false;
         HostTree tree;
         std::vector<GrowLeaf> leaves;
-        uint32_t index = 0;
-        uint32_t buf = 0;  // h_leaf_vw[buf]
-    } pend;
-    uint32_t vw_buf = 0;  // the h_leaf_vw the next renewed tree lands in
+        uint32_t index = 0;  // the tree's index in the call, and its slot
+    };
+    std::vector<Pending> pends;
+    const size_t VW = 2 * static_cast<size_t>(GROW_MAX_LEAVES) + 1;
+    if (p.quant_train_renew_leaf != 0) d_leaf_vw.alloc(static_cast<size_t>(count) * VW);
     auto finalize = [&]() {
-        if (!pend.on) return;
-        const uint32_t nl = pend.tree.num_leaves;
-        hip_check(hipEventSynchronize(vw_landed[pend.buf]), "event synchronize");
-        const double *vw = h_leaf_vw[pend.buf].p;
-        // the leaves k_tree_nodes let through (after the tree's readback, so checked here)
-        if (vw[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
-        for (uint32_t l = 0; l < nl; ++l) {
-            pend.tree.leaf_value[l] = vw[l];
-            pend.tree.leaf_weight[l] = vw[GROW_MAX_LEAVES + l];
+        if (pends.empty()) return;
+        const size_t n = (static_cast<size_t>(pends.back().index) + 1) * VW;
+        h_leaf_vw.alloc(n);
+        hip_check(hipMemcpyAsync(h_leaf_vw.p, d_leaf_vw.p, n * sizeof(double), hipMemcpyDeviceToHost, stream), "read leaf values");
+        sync();
+        for (Pending &pd : pends) {
+            const uint32_t nl = pd.tree.num_leaves;
+            const double *vw = h_leaf_vw.p + static_cast<size_t>(pd.index) * VW;
+            // the leaves k_tree_nodes let through (after the tree's readback, so checked here)
+            if (vw[2 * GROW_MAX_LEAVES] != static_cast<double>(nl)) fail(SROCM_ERR_INTERNAL, "malformed device tree");
+            for (uint32_t l = 0; l < nl; ++l) {
+                pd.tree.leaf_value[l] = vw[l];
+                pd.tree.leaf_weight[l] = vw[GROW_MAX_LEAVES + l];
+            }
+            if (trees) copy_tree(pd.tree, pd.leaves, &trees[pd.index]);
         }
-        if (trees) copy_tree(pend.tree, pend.leaves, &trees[pend.index]);
-        pend.on = false;
+        pends.clear();
     };
     for (uint32_t it = first; it < first + count; ++it) {
         // lambdarank: an iteration whose device factors were flagged is taken again with the host's (the flag also
@@ -2584,6 +2593,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             k_quantize_dev<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, d_scales.p);
             launch_check("k_quantize");
         }
+        queue_rank_flag();
         max_gq = static_cast<int64_t>(p.num_grad_quant_bins / 2);
         max_hq = static_cast<int64_t>(p.num_grad_quant_bins);
         quantized_once = true;
@@ -2616,17 +2626,11 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             d_nodes.alloc(L);
             d_leaf_out.alloc(2 * L);
             d_leaf_values.alloc(L);
-            DevBuf<double> &dvw = d_leaf_vw[vw_buf];
-            dvw.alloc(2 * L + 1);
-            h_leaf_vw[vw_buf].alloc(2 * L + 1);
-            for (hipEvent_t *e : {&vw_ready[vw_buf], &vw_landed[vw_buf]})
-                if (!*e) hip_check(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate");
-            // this buffer's last copy to the host has landed before the kernels below write it again (an iteration
-            // taken again reuses the buffer at once)
-            hip_check(hipStreamWaitEvent(stream, vw_landed[vw_buf], 0), "stream wait");
+            double *dvw = d_leaf_vw.p + static_cast<size_t>(done) * VW;  // this tree's slot (an iteration taken
+                                                                          // again writes it again)
             d_gate.alloc(1);
             leaf_of.alloc(rows);
-            k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, dvw.p + 2 * L,
+            k_tree_nodes<<<1, 512, 0, stream>>>(gst, d_nodes.p, d_leaf_out.p, d_gate.p, dvw + 2 * L,
                                                 rank_flag_pending ? d_rank_flag.p : nullptr);
             launch_check("k_tree_nodes");
             TreeLeavesArgs a{};
@@ -2647,7 +2651,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             a.gate = d_gate.p;
             launch_tree_leaves(a, p.num_leaves);
             LeafValueArgs la{d_leaf_out.p, d_gate.p, d_scales.p, 0u, bias ? 1u : 0u, 1.0f, 1.0f, p.cfg.lambda_l1, p.cfg.lambda_l2,
-                             p.learning_rate, init_score_value, dvw.p, dvw.p + L, d_leaf_values.p};
+                             p.learning_rate, init_score_value, dvw, dvw + L, d_leaf_values.p};
             k_leaf_values<<<1, 512, 0, stream>>>(la);
             launch_check("k_leaf_values");
             if (train.rows)
@@ -2655,11 +2659,6 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             for (auto &v : valid)
                 if (v.rows) k_add_tree<<<grid_rows(v.rows), 256, 0, stream>>>(v.col.p, col16, v.rows, d_nodes.p, d_leaf_values.p, v.scores.p, d_gate.p);
             launch_check("k_add_tree");
-            hip_check(hipEventRecord(vw_ready[vw_buf], stream), "event");
-            hip_check(hipStreamWaitEvent(copy_stream, vw_ready[vw_buf], 0), "stream wait");
-            hip_check(hipMemcpyAsync(h_leaf_vw[vw_buf].p, dvw.p, (2 * L + 1) * sizeof(double), hipMemcpyDeviceToHost,
-                                     copy_stream), "read leaf values");
-            hip_check(hipEventRecord(vw_landed[vw_buf], copy_stream), "event");
         };
         struct ScalesFromDevice {  // GrowState takes the device's scales while this tree grows
             const DevScales *&slot;
@@ -2673,7 +2672,6 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
             ~Defer() { flag = false; }
         } defer(defer_order, last);
         grow(gs, tree, splits, leaves, last, renew ? &renew_on_device : nullptr);
-        finalize();  // the grown tree's readback came after the last tree's leaf values
         if (!host_factors && rank_factors_vetoed()) {
             host_factors = true;
             goto again;
@@ -2690,15 +2688,10 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         }
         if (renew) {
             // the scores and leaf values were queued behind the tree's steps (renew_on_device); the values reach
-            // the host with the next wait
+            // the host at the end of the call
             tree.shrink(p.learning_rate);  // the internal values (the leaf values are replaced on arrival)
             if (bias) tree.add_bias(init_score_value);
-            pend.on = true;
-            pend.tree = tree;
-            pend.leaves = leaves;
-            pend.index = done;
-            pend.buf = vw_buf;
-            vw_buf ^= 1u;
+            pends.push_back(Pending{tree, leaves, done});
             ++done;
             ++trees_added;
             continue;
@@ -2726,10 +2719,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         ++done;
         ++trees_added;
     }
-    if (pend.on) {
-        sync();
-        finalize();
-    }
+    finalize();
     return done;
 }
 
