@@ -1656,13 +1656,33 @@ struct Context {
         sync();  // the staging is rewritten by the next call
     }
 
+    // k_tree_leaves<MAXL, COL16> on as many blocks as the compute units hold at once (the runtime's occupancy for the
+    // kernel), or fewer when the rows take fewer
+    template <uint32_t MAXL, bool COL16>
+    void launch_tree_leaves(const TreeLeavesArgs &a) {
+        constexpr uint32_t threads = tl_threads<MAXL>();
+        static const int per_cu = [] {
+            int n = 0;
+            hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_tree_leaves<MAXL, COL16>, threads, 0), "occupancy");
+            return n > 0 ? n : 1;
+        }();
+        const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(static_cast<uint64_t>(per_cu) * cus,
+                                                                        div_up(rows, static_cast<uint64_t>(tl_rows<MAXL>()) * threads)));
+        k_tree_leaves<MAXL, COL16><<<grid, threads, 0, stream>>>(a);
+    }
+
     // k_tree_leaves for trees of up to max_leaves leaves (the gate, when set, holds the actual count)
     void launch_tree_leaves(const TreeLeavesArgs &a, uint32_t max_leaves) {
-        const uint32_t grid = std::min<uint32_t>(4 * cus, div_up(rows, static_cast<uint64_t>(TL_RPT) * TL_THREADS));
-        if (max_leaves <= LEAVES_SMALL) k_tree_leaves<LEAVES_SMALL><<<grid, TL_THREADS, 0, stream>>>(a);
-        else if (max_leaves <= GROW_MAX_LEAVES) k_tree_leaves<GROW_MAX_LEAVES><<<grid, TL_THREADS, 0, stream>>>(a);
-        else fail(SROCM_ERR_UNSUPPORTED, "a tree of " + std::to_string(max_leaves) + " leaves; the row walk takes up to " +
-                                              std::to_string(GROW_MAX_LEAVES));
+        if (max_leaves <= LEAVES_SMALL) {
+            if (a.col16) launch_tree_leaves<LEAVES_SMALL, true>(a);
+            else launch_tree_leaves<LEAVES_SMALL, false>(a);
+        } else if (max_leaves <= GROW_MAX_LEAVES) {
+            if (a.col16) launch_tree_leaves<GROW_MAX_LEAVES, true>(a);
+            else launch_tree_leaves<GROW_MAX_LEAVES, false>(a);
+        } else {
+            fail(SROCM_ERR_UNSUPPORTED, "a tree of " + std::to_string(max_leaves) + " leaves; the row walk takes up to " +
+                                            std::to_string(GROW_MAX_LEAVES));
+        }
         launch_check("k_tree_leaves");
     }
 

@@ -814,7 +814,7 @@ __global__ void k_add_tree(const uint8_t *__restrict__ colbins, uint32_t col16, 
 // Each row's leaf from a walk down the tree (nodes in LDS; several rows per thread in flight: the walk is a chain
 // of dependent gathers), in row order, and the leaves' exact fixed-point sums rint(v * scale) of the in-bag rows'
 // gradients: the sums k_leaf_sums makes over the final partition (integers, so the order does not matter;
-// cpu.rs:886-908). grid: any, TL_THREADS threads.
+// cpu.rs:886-908). grid: any, tl_threads<MAXL>() threads.
 struct TreeLeavesArgs {
     const uint8_t *colbins;            // column-major bins [feature][rows]
     uint32_t col16;                    // two bytes per bin
@@ -831,18 +831,27 @@ struct TreeLeavesArgs {
     const uint32_t *gate;              // when set: the leaves (nn, nl from it), 0 for no tree (k_tree_nodes)
     const DevScales *dsc;              // when set: gs and hs are its fixed-point scales
 };
-// Instantiated for trees of up to 512 leaves (33 KiB of LDS: several blocks per compute unit) and up to 2048 (131 KiB:
-// one block).
+// Instantiated for trees of up to 512 leaves (28 KiB of LDS: several blocks per compute unit) and up to 2048 (112 KiB:
+// one block per compute unit, of 1024 threads, so that 16 waves walk at once). The walk is a chain of dependent
+// LDS reads and gathers; its rate is set by the rows in flight, which the register file bounds: 8 rows a thread
+// keeps the 512-leaf kernel at 70 registers (7 waves a SIMD), 12 the 2048-leaf one at 124 (4 waves a SIMD, which
+// its one block a compute unit fills).
 constexpr uint32_t LEAVES_SMALL = 512;
-constexpr int TL_RPT = 8;
-constexpr uint32_t TL_THREADS = 512;
+template <uint32_t MAXL> constexpr uint32_t tl_threads() { return MAXL > LEAVES_SMALL ? 1024u : 512u; }
+template <uint32_t MAXL> constexpr int tl_rows() { return MAXL > LEAVES_SMALL ? 12 : 8; }
 
-template <uint32_t MAXL>
-__global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
-    // rows per thread in flight: a tree of more than 512 leaves takes one block per compute unit (its nodes fill the
-    // LDS) and is deeper, so each thread walks more rows at once
-    constexpr int RPT = MAXL > LEAVES_SMALL ? 4 * TL_RPT : TL_RPT;
-    __shared__ DevNode sn[MAXL - 1];
+// COL16: two-byte column-major bins (the only kind with numerical rules, `wide`).
+template <uint32_t MAXL, bool COL16>
+__global__ __launch_bounds__(tl_threads<MAXL>()) void k_tree_leaves(TreeLeavesArgs a) {
+    constexpr int RPT = tl_rows<MAXL>();
+    constexpr uint32_t NN = MAXL - 1;
+    // A level of the walk is branch-free over a thread's RPT rows, so that their LDS reads and gathers issue back to
+    // back and each kind waits once: every row reads its node's head (x: its feature's column, bit 31 set for a
+    // numerical rule; y: its left and right children as two i16, a leaf l as ~l), gathers its bin, then reads the
+    // rule word the bin selects. A row already at its leaf reads node 0 and row 0 and keeps its leaf. The rule words
+    // are word-major (word w of node n at w * NN + n).
+    __shared__ uint2 head[NN];
+    __shared__ uint32_t rule[8 * NN];
     __shared__ unsigned long long ls[MAXL][2];
     uint32_t nn = a.nn, nl = a.nl;
     const float gs = a.dsc ? a.dsc->gsc : a.gs, hs = a.dsc ? a.dsc->hsc : a.hs;
@@ -851,37 +860,60 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_leaves(TreeLeavesArgs a) {
         if (nl == 0u || nl > MAXL) return;
         nn = nl - 1u;
     }
-    for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) sn[k] = a.nodes[k];
+    for (uint32_t k = threadIdx.x; k < nn; k += blockDim.x) {
+        const DevNode &x = a.nodes[k];
+        head[k] = make_uint2(x.feature | (x.wide ? 0x80000000u : 0u),
+                             (static_cast<uint32_t>(x.left) & 0xffffu) | (static_cast<uint32_t>(x.right) << 16));
+#pragma unroll
+        for (int w = 0; w < 8; ++w) rule[w * NN + k] = x.left_bins[w];
+    }
     if (a.grad)
         for (uint32_t l = threadIdx.x; l < nl; l += blockDim.x) ls[l][0] = ls[l][1] = 0ull;
     __syncthreads();
-    const uint64_t stride = static_cast<uint64_t>(RPT) * gridDim.x * blockDim.x;
-    for (uint64_t base = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; base < a.rows; base += stride) {
-        uint64_t r[RPT];
+    const uint32_t rows = static_cast<uint32_t>(a.rows);  // rows < 2^32 (row ids are u32)
+    const uint32_t step = gridDim.x * blockDim.x;
+    for (uint64_t base = blockIdx.x * blockDim.x + threadIdx.x; base < rows; base += static_cast<uint64_t>(RPT) * step) {
+        uint32_t r[RPT];
         int32_t nd[RPT];
 #pragma unroll
         for (int k = 0; k < RPT; ++k) {
-            r[k] = base + static_cast<uint64_t>(k) * gridDim.x * blockDim.x;
-            nd[k] = r[k] < a.rows ? 0 : -1;
+            const uint64_t row = base + static_cast<uint64_t>(k) * step;
+            r[k] = row < rows ? static_cast<uint32_t>(row) : 0u;
+            nd[k] = row < rows ? 0 : -1;
         }
         for (;;) {
+            uint2 h[RPT];
+#pragma unroll
+            for (int k = 0; k < RPT; ++k) h[k] = head[nd[k] < 0 ? 0 : nd[k]];
             uint32_t b[RPT];
 #pragma unroll
-            for (int k = 0; k < RPT; ++k)
-                b[k] = nd[k] >= 0 ? col_bin(a.colbins, a.col16, static_cast<size_t>(sn[nd[k]].feature) * a.rows + r[k]) : 0u;
+            for (int k = 0; k < RPT; ++k) {
+                const size_t i = static_cast<size_t>(h[k].x & 0x7fffffffu) * rows + (nd[k] < 0 ? 0u : r[k]);
+                b[k] = COL16 ? static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(a.colbins)[i]) : static_cast<uint32_t>(a.colbins[i]);
+            }
+            uint32_t m0[RPT], m1[RPT];
+#pragma unroll
+            for (int k = 0; k < RPT; ++k) {
+                const uint32_t n = nd[k] < 0 ? 0u : static_cast<uint32_t>(nd[k]);
+                const uint32_t w = COL16 ? (h[k].x >> 31 ? 0u : min(b[k] >> 5, 7u)) : b[k] >> 5;
+                m0[k] = rule[w * NN + n];
+                if (COL16) m1[k] = rule[NN + n];
+            }
             bool any = false;
 #pragma unroll
             for (int k = 0; k < RPT; ++k) {
-                if (nd[k] < 0) continue;
-                const DevNode &x = sn[nd[k]];
-                nd[k] = rule_left(x.left_bins, x.wide, b[k]) ? x.left : x.right;
+                bool left = ((m0[k] >> (b[k] & 31u)) & 1u) != 0u;
+                // rule_left's numerical rule: word 0 the threshold, word 1 the NaN bin + 1 or 0
+                if (COL16 && (h[k].x >> 31)) left = b[k] <= m0[k] || (m1[k] != 0u && b[k] == m1[k] - 1u);
+                const int32_t c = static_cast<int32_t>(static_cast<int16_t>(left ? h[k].y & 0xffffu : h[k].y >> 16));
+                nd[k] = nd[k] < 0 ? nd[k] : c;
                 any = any || nd[k] >= 0;
             }
             if (!any) break;
         }
 #pragma unroll
         for (int k = 0; k < RPT; ++k) {
-            if (r[k] >= a.rows) continue;
+            if (base + static_cast<uint64_t>(k) * step >= rows) continue;
             const uint32_t leaf = static_cast<uint32_t>(~nd[k]);
             a.leaf_of[r[k]] = static_cast<uint16_t>(leaf);
             if (!a.grad) continue;
