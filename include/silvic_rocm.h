@@ -331,6 +331,34 @@ int srocm_find_best_split(void *ctx, const double *hist, size_t len, const srocm
                           double hess_scale, const srocm_split_config *cfg, srocm_split_info *out,
                           uint8_t *splittable);
 
+/* Histogram slots: the learner's histograms kept on the device, for a binding that grows trees split by split over
+ * the calls above (learner.rs:121-352; trees of more leaves than srocm_grow takes). They replace the host copies of
+ * Learner's histograms and its subtraction (learner.rs:356-371): each slot holds 2 * total_bins int64 units in
+ * srocm_histogram's order. */
+
+/* Sets up `num_slots` slots on the loaded dataset (earlier slots and their contents are dropped). */
+int srocm_hist_slots(void *ctx, uint32_t num_slots);
+
+/* Backend::histogram (mod.rs:147-149, quantized mode) into slot `slot`; nothing comes back to the host. */
+int srocm_histogram_slot(void *ctx, srocm_leaf_range leaf, uint32_t slot);
+
+/* Backend::partition_and_histogram (mod.rs:154-168, quantized mode) with the `side` child's histogram into slot
+ * `slot`; *left as srocm_partition_and_histogram returns it. */
+int srocm_partition_and_histogram_slot(void *ctx, srocm_leaf_range leaf, const srocm_bin_split *split, uint32_t side,
+                                       uint32_t slot, uint32_t *left);
+
+/* learner.rs:365-367 on the device: slot `parent_slot` -= slot `child_slot`, so the parent's slot holds the other
+ * child's histogram (exact integer units). */
+int srocm_subtract(void *ctx, uint32_t parent_slot, uint32_t child_slot);
+
+/* srocm_find_best_split over slot `slot` instead of a host histogram. */
+int srocm_find_best_split_slot(void *ctx, uint32_t slot, const srocm_feature *features, uint32_t num_features,
+                               const uint8_t *evaluate, const srocm_sums *sums, double grad_scale, double hess_scale,
+                               const srocm_split_config *cfg, srocm_split_info *out, uint8_t *splittable);
+
+/* Slot `slot` as 2 * total_bins doubles (what srocm_histogram would have returned). */
+int srocm_read_slot(void *ctx, uint32_t slot, double *out, size_t len);
+
 /* Learner::grow (crates/silvic-core/src/learner.rs:121-169) with every histogram, subtraction, split search
  * and partition on the device and one readback of the finished tree. Quantized mode only. */
 int srocm_grow(void *ctx, const srocm_grow_spec *spec, srocm_grown_tree *out);

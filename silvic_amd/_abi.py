@@ -166,6 +166,15 @@ _SIGNATURES = {
                                         C.POINTER(C.c_uint8),
                                         C.POINTER(Sums), C.c_double, C.c_double, C.POINTER(SplitConfig),
                                         C.POINTER(SplitInfo), C.POINTER(C.c_uint8)]),
+    "srocm_hist_slots": (C.c_int, [_P, C.c_uint32]),
+    "srocm_histogram_slot": (C.c_int, [_P, LeafRange, C.c_uint32]),
+    "srocm_partition_and_histogram_slot": (C.c_int, [_P, LeafRange, C.POINTER(BinSplit), C.c_uint32, C.c_uint32,
+                                                     C.POINTER(C.c_uint32)]),
+    "srocm_subtract": (C.c_int, [_P, C.c_uint32, C.c_uint32]),
+    "srocm_find_best_split_slot": (C.c_int, [_P, C.c_uint32, C.POINTER(Feature), C.c_uint32, C.POINTER(C.c_uint8),
+                                             C.POINTER(Sums), C.c_double, C.c_double, C.POINTER(SplitConfig),
+                                             C.POINTER(SplitInfo), C.POINTER(C.c_uint8)]),
+    "srocm_read_slot": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_double), C.c_size_t]),
     "srocm_grow": (C.c_int, [_P, C.POINTER(GrowSpec), C.POINTER(GrownTree)]),
     "srocm_boost_init": (C.c_int, [_P, C.POINTER(TrainParams), C.POINTER(C.c_double)]),
     "srocm_boost": (C.c_int, [_P, C.POINTER(TrainParams), C.c_uint32, C.c_uint32, C.POINTER(GrownTree),

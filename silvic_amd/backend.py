@@ -183,6 +183,41 @@ class RocmBackend:
 
     # -- device-side extension ----------------------------------------------------------------------
 
+    # Histogram slots: the learner's histograms kept on the device (srocm_hist_slots and the calls after it).
+    def hist_slots(self, n):
+        self._check(self._lib.srocm_hist_slots(self._h, n))
+
+    def histogram_slot(self, leaf, slot):
+        self._check(self._lib.srocm_histogram_slot(self._h, LeafRange(*leaf), slot))
+
+    def partition_and_histogram_slot(self, leaf, split, side, slot):
+        left = C.c_uint32()
+        self._check(self._lib.srocm_partition_and_histogram_slot(self._h, LeafRange(*leaf), C.byref(split), side, slot,
+                                                                 C.byref(left)))
+        return left.value
+
+    def subtract(self, parent_slot, child_slot):
+        """learner.rs:365-367 on the device: the parent's slot becomes parent - child."""
+        self._check(self._lib.srocm_subtract(self._h, parent_slot, child_slot))
+
+    def read_slot(self, slot):
+        out = np.zeros(2 * self.total_bins, np.float64)
+        self._check(self._lib.srocm_read_slot(self._h, slot, _p(out, C.c_double), len(out)))
+        return out
+
+    def find_best_split_slot(self, slot, features, evaluate, sums, grad_scale, hess_scale, cfg):
+        ev = np.ascontiguousarray(evaluate, dtype=np.uint8)
+        feats = (_abi.Feature * max(1, len(features)))()
+        for i, f in enumerate(features):
+            feats[i] = _abi.Feature(f.num_bins, f.group, f.column, f.hist_offset, f.kind, int(bool(f.nan_bin)))
+        out = _abi.SplitInfo()
+        spl = np.zeros(len(features), np.uint8)
+        s = _abi.Sums(*sums)
+        self._check(self._lib.srocm_find_best_split_slot(self._h, slot, feats, len(features), _p(ev, C.c_uint8),
+                                                         C.byref(s), grad_scale, hess_scale, C.byref(cfg),
+                                                         C.byref(out), _p(spl, C.c_uint8)))
+        return out, spl.astype(bool)
+
     def find_best_split(self, hist, features, evaluate, sums, grad_scale, hess_scale, cfg):
         """``split::find_best_split`` (split.rs:919-961) on the device: returns (SplitInfo, splittable bools)."""
         hist = np.ascontiguousarray(hist, dtype=np.float64)

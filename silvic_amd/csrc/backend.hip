@@ -1753,10 +1753,92 @@ struct Context {
                            c.max_cat_to_onehot, c.max_cat_threshold, c.cat_l2, c.cat_smooth, c.min_data_per_group};
     }
 
+    // ------------------------------------------------------------------------------------------------
+    // histogram slots: the learner's histograms kept on the device (learner.rs:121-352 over the trait calls, with
+    // the subtraction of learner.rs:356-371 and the split search reading them where they are)
+    DevBuf<int64_t> hslots;   // num_hslots histograms of 2 * total_bins int64 units
+    uint32_t num_hslots = 0;
+
+    int64_t *slot_ptr(uint32_t slot) {
+        if (slot >= num_hslots)
+            fail(SROCM_ERR_DEVICE, "histogram slot " + std::to_string(slot) + " of " + std::to_string(num_hslots));
+        return hslots.p + static_cast<size_t>(slot) * 2 * total_bins;
+    }
+
+    void hist_slots(uint32_t n) {
+        require_loaded();
+        hslots.alloc(static_cast<size_t>(std::max<uint32_t>(n, 1)) * 2 * total_bins);
+        num_hslots = n;
+    }
+
+    void histogram_slot(srocm_leaf_range leaf, uint32_t slot) {
+        require_loaded();
+        check_range(leaf);
+        ensure_order();
+        if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
+        int64_t *d = slot_ptr(slot);
+        if (leaf.count) launch_hist(leaf.begin, leaf.count, nullptr, 0, d, nullptr, used_columns());
+        else hip_check(hipMemsetAsync(d, 0, 2 * total_bins * 8, stream), "zero histogram");
+    }
+
+    uint32_t partition_and_histogram_slot(srocm_leaf_range leaf, const srocm_bin_split &split, uint32_t side, uint32_t slot) {
+        require_loaded();
+        check_range(leaf);
+        ensure_order();
+        if (side > 1) fail(SROCM_ERR_DEVICE, "bad side");
+        if (!quantized_once) fail(SROCM_ERR_DEVICE, "histogram before quantize");
+        int64_t *d = slot_ptr(slot);
+        enqueue_partition(leaf, split);
+        if (leaf.count) launch_hist(leaf.begin, leaf.count, scalars.p, side, d, nullptr, used_columns());
+        else hip_check(hipMemsetAsync(d, 0, 2 * total_bins * 8, stream), "zero histogram");
+        hip_check(hipMemcpyAsync(h_u32.p, scalars.p, 4, hipMemcpyDeviceToHost, stream), "read left count");
+        sync();
+        return h_u32.p[0];
+    }
+
+    // learner.rs:365-367: the parent's slot becomes parent - built, the other child's histogram (exact integers)
+    void subtract(uint32_t parent, uint32_t child) {
+        require_loaded();
+        if (parent == child) fail(SROCM_ERR_DEVICE, "a slot subtracted from itself");
+        int64_t *p = slot_ptr(parent);
+        const int64_t *c = slot_ptr(child);
+        k_sub_i64<<<grid_rows(2 * total_bins), 256, 0, stream>>>(p, c, 2 * total_bins);
+        launch_check("k_sub_i64");
+    }
+
+    void read_slot(uint32_t slot, double *out, size_t len) {
+        require_loaded();
+        if (len != 2 * total_bins) fail(SROCM_ERR_DEVICE, "histogram buffer of " + std::to_string(len) + " values, expected " + std::to_string(2 * total_bins));
+        const int64_t *d = slot_ptr(slot);
+        h_hist.alloc(2 * total_bins);
+        hip_check(hipMemcpyAsync(h_hist.p, d, 2 * total_bins * 8, hipMemcpyDeviceToHost, stream), "read histogram slot");
+        sync();
+        for (size_t i = 0; i < len; ++i) out[i] = static_cast<double>(h_hist.p[i]);
+    }
+
+    void find_best_split_slot(uint32_t slot, const srocm_feature *features, uint32_t num_features, const uint8_t *evaluate,
+                              const srocm_sums &sums, double sg, double sh, const srocm_split_config &cfg,
+                              srocm_split_info *out, uint8_t *splittable) {
+        require_loaded();
+        find_best_split_dev(slot_ptr(slot), 2 * total_bins, features, num_features, evaluate, sums, sg, sh, cfg, out, splittable);
+    }
+
     // split.rs:919-961 on a host histogram over an explicit feature table (no loaded dataset needed)
     void find_best_split(const double *hist, size_t len, const srocm_feature *features, uint32_t num_features,
                          const uint8_t *evaluate, const srocm_sums &sums, double sg, double sh,
                          const srocm_split_config &cfg, srocm_split_info *out, uint8_t *splittable) {
+        std::vector<int64_t> units(len);
+        for (size_t i = 0; i < len; ++i) units[i] = static_cast<int64_t>(hist[i]);
+        DevBuf<int64_t> dh;
+        dh.alloc(std::max<size_t>(len, 1));
+        if (len) hip_check(hipMemcpyAsync(dh.p, units.data(), len * 8, hipMemcpyHostToDevice, stream), "upload histogram");
+        find_best_split_dev(dh.p, len, features, num_features, evaluate, sums, sg, sh, cfg, out, splittable);
+    }
+
+    // find_best_split over `len` int64 units on the device (an uploaded host histogram, or a histogram slot)
+    void find_best_split_dev(const int64_t *dh, size_t len, const srocm_feature *features, uint32_t num_features,
+                             const uint8_t *evaluate, const srocm_sums &sums, double sg, double sh,
+                             const srocm_split_config &cfg, srocm_split_info *out, uint8_t *splittable) {
         std::vector<FeatDev> fd(num_features);
         for (uint32_t f = 0; f < num_features; ++f) {
             const srocm_feature &m = features[f];
@@ -1766,28 +1848,23 @@ struct Context {
                 fail(SROCM_ERR_DEVICE, "feature " + std::to_string(f) + " lies outside the histogram");
             fd[f] = FeatDev{m.num_bins, m.hist_offset, m.kind, m.nan_bin, 0u, m.num_bins > 256 ? 1u : 0u};
         }
-        std::vector<int64_t> units(len);
-        for (size_t i = 0; i < len; ++i) units[i] = static_cast<int64_t>(hist[i]);
-        DevBuf<int64_t> dh;
         DevBuf<FeatDev> dfd;
         DevBuf<ScanJob> dj;
         DevBuf<FeatCand> dc;
         DevBuf<SplitOut> dso;
         DevBuf<uint8_t> dsp, dev, dorder;
         dorder.alloc(static_cast<size_t>(std::max<uint32_t>(num_features, 1)) * 256);
-        dh.alloc(std::max<size_t>(len, 1));
         dfd.alloc(std::max<uint32_t>(num_features, 1));
         dj.alloc(1);
         dc.alloc(std::max<uint32_t>(num_features, 1));
         dso.alloc(1);
         dsp.alloc(std::max<uint32_t>(num_features, 1));
         dev.alloc(std::max<uint32_t>(num_features, 1));
-        if (len) hip_check(hipMemcpyAsync(dh.p, units.data(), len * 8, hipMemcpyHostToDevice, stream), "upload histogram");
         if (num_features) {
             hip_check(hipMemcpyAsync(dfd.p, fd.data(), num_features * sizeof(FeatDev), hipMemcpyHostToDevice, stream), "upload features");
             hip_check(hipMemcpyAsync(dev.p, evaluate, num_features, hipMemcpyHostToDevice, stream), "upload evaluate");
         }
-        ScanJob job{dh.p, sums.grad, sums.hess, sums.count, dc.p};
+        ScanJob job{dh, sums.grad, sums.hess, sums.count, dc.p};
         hip_check(hipMemcpyAsync(dj.p, &job, sizeof(job), hipMemcpyHostToDevice, stream), "upload job");
         if (num_features) {
             // numerical byte features of 2..64 bins go in scan units of several (k_split_scan_seg), as in a tree
@@ -2977,6 +3054,45 @@ int srocm_find_best_split(void *ctx, const double *hist, size_t len, const srocm
             (!splittable && num_features))
             fail(SROCM_ERR_DEVICE, "null argument");
         c.find_best_split(hist, len, features, num_features, evaluate, *sums, grad_scale, hess_scale, *cfg, out, splittable);
+    });
+}
+
+int srocm_hist_slots(void *ctx, uint32_t num_slots) {
+    return guard(ctx, [&](Context &c) { c.hist_slots(num_slots); });
+}
+
+int srocm_histogram_slot(void *ctx, srocm_leaf_range leaf, uint32_t slot) {
+    return guard(ctx, [&](Context &c) { c.histogram_slot(leaf, slot); });
+}
+
+int srocm_partition_and_histogram_slot(void *ctx, srocm_leaf_range leaf, const srocm_bin_split *split, uint32_t side,
+                                       uint32_t slot, uint32_t *left) {
+    return guard(ctx, [&](Context &c) {
+        if (!split) fail(SROCM_ERR_DEVICE, "null split");
+        uint32_t l = c.partition_and_histogram_slot(leaf, *split, side, slot);
+        if (left) *left = l;
+    });
+}
+
+int srocm_subtract(void *ctx, uint32_t parent_slot, uint32_t child_slot) {
+    return guard(ctx, [&](Context &c) { c.subtract(parent_slot, child_slot); });
+}
+
+int srocm_read_slot(void *ctx, uint32_t slot, double *out, size_t len) {
+    return guard(ctx, [&](Context &c) {
+        if (!out && len) fail(SROCM_ERR_DEVICE, "null argument");
+        c.read_slot(slot, out, len);
+    });
+}
+
+int srocm_find_best_split_slot(void *ctx, uint32_t slot, const srocm_feature *features, uint32_t num_features,
+                               const uint8_t *evaluate, const srocm_sums *sums, double grad_scale, double hess_scale,
+                               const srocm_split_config *cfg, srocm_split_info *out, uint8_t *splittable) {
+    return guard(ctx, [&](Context &c) {
+        if ((!features && num_features) || (!evaluate && num_features) || !sums || !cfg || !out ||
+            (!splittable && num_features))
+            fail(SROCM_ERR_DEVICE, "null argument");
+        c.find_best_split_slot(slot, features, num_features, evaluate, *sums, grad_scale, hess_scale, *cfg, out, splittable);
     });
 }
 

@@ -938,6 +938,12 @@ __global__ void k_add_leaf_values(const uint16_t *__restrict__ leaf_of, const fl
         scores[r] += leaf_values[leaf_of[r]];
 }
 
+// a -= b over n int64 values (a histogram slot minus another, learner.rs:365-367)
+__global__ void k_sub_i64(int64_t *__restrict__ a, const int64_t *__restrict__ b, uint64_t n) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        a[i] -= b[i];
+}
+
 __global__ void k_add_const(float *__restrict__ scores, uint64_t rows, float v) {
     for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
         scores[r] += v;

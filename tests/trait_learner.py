@@ -1,6 +1,7 @@
 """A learner over the trait calls alone: Learner::grow / split_leaf / best_leaf / find_split (learner.rs:121-352,
 418-452) driving Backend::histogram, partition, partition_and_histogram and the device split search one split at a
-time, with the sibling's histogram by subtraction on the host (learner.rs:356-371). It is how a binding grows trees
+time, with the sibling's histogram by subtraction on the host (learner.rs:356-371), or (SlotBackend) with every
+histogram, the subtraction and the split search on the device over histogram slots. It is how a binding grows trees
 of more leaves than srocm_grow takes (2048; silvic takes up to 131072, config.rs:389-391), so a test grows such a
 tree with it and checks it against the oracle's learner. Test infrastructure: it restates the reference's learner
 in Python, as the oracle restates it in C++.
@@ -165,6 +166,57 @@ def grow(backend, data, params, feature_mask, grad_scale, hess_scale, root, root
             find_split(b_leaf, built, evaluate)
             find_split(o_leaf, other_hist, evaluate)
     return tree.arrays(), np.array([l.range for l in leaves], np.int64)
+
+
+class SlotHist:
+    """A histogram in a device slot (srocm_hist_slots). `parent - built` subtracts on the device, so the parent's slot
+    becomes the other child's histogram (learner.rs:365-367); indexing reads the slot to the host once."""
+
+    def __init__(self, backend, slot):
+        self.backend, self.slot, self._host = backend, slot, None
+
+    def __sub__(self, built):
+        self.backend.rocm.subtract(self.slot, built.slot)
+        return SlotHist(self.backend, self.slot)
+
+    def __getitem__(self, i):
+        if self._host is None:
+            self._host = self.backend.rocm.read_slot(self.slot)
+        return self._host[i]
+
+
+class SlotBackend:
+    """The device backend with every histogram grow() makes kept in a device slot: the slot calls for the histogram,
+    the fused partition and histogram, the subtraction and the split search, so no histogram crosses to the host
+    (the root's, read once for its sums, aside). A histogram takes the next slot; a sibling reuses its parent's."""
+
+    def __init__(self, rocm, num_slots):
+        self.rocm, self.num_slots, self.used = rocm, num_slots, 0
+        rocm.hist_slots(num_slots)
+
+    def _slot(self):
+        assert self.used < self.num_slots, "out of histogram slots"
+        self.used += 1
+        return self.used - 1
+
+    def set_histogram_features(self, used):
+        self.rocm.set_histogram_features(used)
+
+    def histogram(self, leaf):
+        slot = self._slot()
+        self.rocm.histogram_slot(leaf, slot)
+        return SlotHist(self, slot)
+
+    def partition(self, leaf, split):
+        return self.rocm.partition(leaf, split)
+
+    def partition_and_histogram(self, leaf, split, side):
+        slot = self._slot()
+        left = self.rocm.partition_and_histogram_slot(leaf, split, side, slot)
+        return left, SlotHist(self, slot)
+
+    def find_best_split(self, hist, features, evaluate, sums, grad_scale, hess_scale, cfg):
+        return self.rocm.find_best_split_slot(hist.slot, features, evaluate, sums, grad_scale, hess_scale, cfg)
 
 
 class OracleBackend:
