@@ -390,6 +390,7 @@ struct Context {
     DevBuf<int32_t> packed, partial;
     DevBuf<uint32_t> part, part2, block_left, scalars;
     DevBuf<uint32_t> maxima;  // the gradient maxima, MAX_SLOTS pairs
+    bool maxima_clear = false; // maxima holds zeros on the stream (k_quant_spec cleared it after reading)
     DevBuf<uint8_t> codes0, codes1;  // grown trees: each row's gradient code beside its id in part / part2
     DevBuf<FeatDev> dfeats;
     DevBuf<ColGroup> d_cgs;
@@ -632,7 +633,7 @@ struct Context {
             RankArgs ra{train.scores.p, label.p, d_rank_bounds.p, d_rank_imd.p, d_rank_gain.p, d_rank_table.p,
                         d_rank_disc.p, st.sigmoid, st.sigmoid * st.sigmoid, ranker.min_input(), ranker.max_input(),
                         ranker.idx_factor(), st.norm ? 1u : 0u, st.truncation_level, d_rank_lam.p, d_rank_hes.p,
-                        d_rank_qsum.p, d_rank_queries.p};
+                        d_rank_qsum.p, d_rank_queries.p, d_rank_flag.p};
             const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
             switch (rank_nmax) {
             case 64: k_rank_pairs<64><<<nd, 64, 0, stream>>>(ra); break;
@@ -662,8 +663,7 @@ struct Context {
             uint32_t mode = RANK_FACTOR_ONE;
             const uint32_t nd = static_cast<uint32_t>(rank_dev_q.size());
             if (st.norm && !host_factors) {
-                mode = rank_force_fallback ? RANK_FACTOR_DEVICE_CHECKED : RANK_FACTOR_DEVICE;
-                hip_check(hipMemsetAsync(d_rank_flag.p, 0, 4, stream), "zero rank flag");
+                mode = rank_force_fallback ? RANK_FACTOR_DEVICE_CHECKED : RANK_FACTOR_DEVICE;  // flag cleared by k_rank_pairs
                 k_rank_factor<<<div_up(nd, 256), 256, 0, stream>>>(d_rank_queries.p, nd, d_rank_qsum.p, mode, d_rank_pair.p,
                                                                   d_rank_flag.p);
                 launch_check("k_rank_factor");
@@ -775,6 +775,7 @@ struct Context {
         // device buffers
         scalars.alloc(16);
         maxima.alloc(2 * MAX_SLOTS);
+        maxima_clear = false;
         hip_check(hipMemsetAsync(scalars.p + 15, 0, 4, stream), "zero bin check");
         train = DevData{};
         upload_bins(t, train, true);
@@ -1250,6 +1251,7 @@ struct Context {
         hip_check(hipMemcpyAsync(grad.p, g, n * 4, hipMemcpyHostToDevice, stream), "upload grad");
         hip_check(hipMemcpyAsync(hess.p, h, n * 4, hipMemcpyHostToDevice, stream), "upload hess");
         hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
+        maxima_clear = false;
         k_max_abs<<<grid_rows(n), 256, 0, stream>>>(grad.p, hess.p, n, maxima.p);
         launch_check("k_max_abs");
         return read_maxima();
@@ -2222,7 +2224,8 @@ std::pair<double, double> Context::compute_gradients() {
 void Context::launch_gradients(bool host_factors) {
     require_loaded();
     rank_flag_pending = false;
-    hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
+    if (!maxima_clear) hip_check(hipMemsetAsync(maxima.p, 0, 8 * MAX_SLOTS, stream), "zero maxima");
+    maxima_clear = false;
     if (rows && objective == SROCM_OBJ_LAMBDARANK) {
         ranking_gradients(host_factors);
     } else if (rows) {
@@ -2686,6 +2689,7 @@ uint32_t Context::boost(const srocm_train_params &p, uint32_t first, uint32_t co
         k_quant_spec<<<1, MAX_SLOTS, 0, stream>>>(maxima.p, d_scales.p, p.num_grad_quant_bins, constant_hessian ? 1u : 0u, 1.0,
                                            p.stochastic_rounding != 0 ? 1u : 0u, p.data_random_seed, it);
         launch_check("k_quant_spec");
+        maxima_clear = true;
         if (rows) {
             k_quantize_dev<<<grid_rows(rows), 256, 0, stream>>>(grad.p, hess.p, packed.p, rows, row_offset, d_scales.p);
             launch_check("k_quantize");

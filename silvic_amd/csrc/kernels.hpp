@@ -127,10 +127,13 @@ __device__ __forceinline__ float fixed_point_scale_d(double max_abs) {
     return __builtin_ldexpf(1.0f, e);
 }
 
-__global__ void k_quant_spec(const uint32_t *maxima, DevScales *out, uint32_t num_bins, uint32_t constant_hessian,
+// One wave (launched with MAX_SLOTS threads): lane l reads slot pair l of the maxima and clears it, so the next
+// gradients' maxima start from zero without a fill of their own.
+__global__ void k_quant_spec(uint32_t *maxima, DevScales *out, uint32_t num_bins, uint32_t constant_hessian,
                              double constant, uint32_t stochastic, uint32_t seed, uint32_t iteration) {
-    // one wave (launched with MAX_SLOTS threads): lane l reads slot pair l of the maxima
     uint32_t ug = maxima[2u * threadIdx.x], uh = maxima[2u * threadIdx.x + 1u];
+    maxima[2u * threadIdx.x] = 0u;
+    maxima[2u * threadIdx.x + 1u] = 0u;
     for (int o = 32; o >= 1; o >>= 1) {
         const uint32_t x = __shfl_xor(ug, o), y = __shfl_xor(uh, o);
         ug = ug > x ? ug : x;

@@ -36,6 +36,7 @@ struct RankArgs {
     double *lam, *hes;             // per row: the unscaled lambda and hessian sums
     double *qsum;                  // per query: the lambda sum
     const uint32_t *queries;       // the queries this launch takes, one a block (blockIdx.x's is queries[blockIdx.x])
+    uint32_t *flag;                // when set, cleared here for k_rank_factor and k_rank_scale, which run after
 };
 
 // The value of a per-rank register array at rank k (lane k % 64, slot k / 64), on every lane; k is the same on all.
@@ -73,6 +74,7 @@ __global__ __launch_bounds__(64) void k_rank_pairs(RankArgs a) {
     __shared__ __align__(16) double lds[3 * STRIDE];  // the sort's keys, then row i's terms in j order
     uint64_t *keys = reinterpret_cast<uint64_t *>(lds);
     const uint32_t q = a.queries[blockIdx.x], lane = threadIdx.x;
+    if (a.flag && blockIdx.x == 0 && lane == 0) *a.flag = 0u;
     const uint32_t b = a.bounds[q], n = a.bounds[q + 1] - b;
     if (n == 0) {
         if (lane == 0) a.qsum[q] = 0.0;
