@@ -1956,6 +1956,7 @@ struct Context {
     DevBuf<TKey> d_tk;
     DevBuf<uint8_t> d_leaf_left;
     DevBuf<uint8_t> d_splittable, d_eval, d_mask;
+    std::vector<uint8_t> d_mask_host;  // what d_mask holds (empty: unknown), so an unchanged mask is not uploaded again
     DevBuf<ScanJob> d_jobs;
     DevBuf<FeatCand> d_cands;
     DevBuf<RowRun> d_runs;            // end of a tree: runs of rows to bring into ascending order
@@ -2002,6 +2003,7 @@ struct Context {
         d_splittable.alloc(static_cast<size_t>(tcap) * nf);
         d_eval.alloc(nf);
         d_mask.alloc(nf);
+        d_mask_host.clear();
         d_jobs.alloc(1);
         d_cands.alloc(static_cast<size_t>(JMAX) * 2 * nf);
         tree_layout = TreeLayout(L);
@@ -2268,9 +2270,12 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
     g.sums_feature = sums_feature < 0 ? 0u : static_cast<uint32_t>(sums_feature);
     if (epochs_used + L > (1ull << 29)) reset_step_state();  // tile status epochs are 30 bits wide
     epochs_used += L;
-    h_stage.alloc(nf + 64);
-    std::memcpy(h_stage.p, mask.data(), nf);
-    hip_check(hipMemcpyAsync(d_mask.p, h_stage.p, nf, hipMemcpyHostToDevice, stream), "upload mask");
+    if (mask != d_mask_host) {  // (feature_fraction 1 keeps one mask for every tree)
+        h_stage.alloc(nf + 64);
+        std::memcpy(h_stage.p, mask.data(), nf);
+        hip_check(hipMemcpyAsync(d_mask.p, h_stage.p, nf, hipMemcpyHostToDevice, stream), "upload mask");
+        d_mask_host = mask;
+    }
     k_grow_init<<<1, 64, 0, stream>>>(g, spec.root.begin, spec.root.count, spec.root_count, root_searched ? 1u : 0u);
     launch_check("k_grow_init");
     // small units travel beside the row ids as one-byte codes (packed_code), so the split steps' histograms read them
