@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "exp_f64.hpp"
 #include "packed_word.hpp"
 
@@ -1215,6 +1217,25 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = dpp_max_u32_step<DPP_ROW_BCAST15, 0xa>(v);
     v = dpp_max_u32_step<DPP_ROW_BCAST31, 0xc>(v);
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, ROW_MASK, 0xf, false));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, ROW_MASK, 0xf, false));
+    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = dpp_max_u64_step<DPP_ROW_SHR1, 0xf>(v);
+    v = dpp_max_u64_step<DPP_ROW_SHR2, 0xf>(v);
+    v = dpp_max_u64_step<DPP_ROW_SHR4, 0xf>(v);
+    v = dpp_max_u64_step<DPP_ROW_SHR8, 0xf>(v);
+    v = dpp_max_u64_step<DPP_ROW_BCAST15, 0xa>(v);
+    v = dpp_max_u64_step<DPP_ROW_BCAST31, 0xc>(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 // A feature candidate as held by lane `owner`, broadcast to the wave.
@@ -2575,7 +2596,9 @@ struct AdvShared {
     int16_t pnode[MAXL];                  // committed leaf -> the internal node above it (-1: the root)
     uint8_t is_left[MAXL];                // committed leaf is its node's left child
     uint8_t touched[MAXL];                // committed leaf changed by this replay
-    uint32_t key[MAXL];                   // committed leaf's replay key (0: none)
+    // committed leaf's replay key (0: none): replay_key64 in trees of more than 512 leaves, where 32-bit keys meet
+    // the winner's gain prefix often; replay_key<11> in the others, where its u32 wave max is the cheaper
+    std::conditional_t<(MAXL > LEAVES_SMALL), uint64_t, uint32_t> key[MAXL];
     uint16_t ck[MAXL];                    // commit c: the speculative leaf split (node n0 - 1 + c)
     uint16_t cx[MAXL];                    // commit c: the leaf id split
     int16_t cpn[MAXL];                    // commit c: the split leaf's node above
@@ -2606,10 +2629,21 @@ __device__ __forceinline__ uint32_t replay_key(double gain, uint32_t meta, uint3
     return (p << IDB) | ((1u << IDB) - 1u - id);
 }
 
+// replay_key in 64 bits for trees of up to 2048 leaves (replay_lds): the positive gain's bits without their low 11
+// (its exponent and 41 bits of mantissa) above 2047 - leaf id. Two gains share that prefix only when they agree to
+// about 5e-13 (32-bit keys kept 21 bits, and at 2047 leaves a third of the commits met a leaf with the winner's
+// prefix, each settled by an exact f64 argmax).
+__device__ __forceinline__ uint64_t replay_key64(double gain, uint32_t meta, uint32_t id) {
+    if (!(meta & 1u) || !(gain > 0.0)) return 0ull;
+    uint64_t p = __builtin_bit_cast(uint64_t, gain) >> 11;
+    p = p ? p : 1ull;
+    return (p << 11) | (2047u - id);
+}
+
 // The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave. Lane l owns committed
 // leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves); their state is in LDS (speculative leaf, node above,
 // left and changed flags, and the replay key in s.key) and only the lane's largest key is in a register. A commit is
-// one u32 wave max of those (the reference's argmax only matters while the best gain is positive: otherwise the tree
+// one wave max of those (the reference's argmax only matters while the best gain is positive: otherwise the tree
 // stops), with an exact f64 argmax only when two leaves share the winner's gain prefix: a lane other than the
 // winner's holds such a key exactly when its largest key has the prefix, and the winner's own other keys, like its
 // new largest key after the commit, are read from s.key by NPL lanes at once. The rule that the first leaf with a
@@ -2619,18 +2653,29 @@ template <int NPL, typename S>
 __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     constexpr int IDB = 11;
     static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 64, "leaf ids fit");
-    constexpr uint32_t IDM = (1u << IDB) - 1u;
+    constexpr uint64_t IDM = (1u << IDB) - 1u;
+    using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
+    constexpr bool K64 = sizeof(Key) == 8;
+    auto key_of = [](double gain, uint32_t meta, uint32_t id) -> Key {
+        if constexpr (K64) return replay_key64(gain, meta, id);
+        else return replay_key<IDB>(gain, meta, id);
+    };
+    auto wave_max_key = [](Key v) -> Key {
+        if constexpr (K64) return wave_max_u64(v);
+        else return wave_max_u32(v);
+    };
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t lk = 0, nan_lane = 0;
+    Key lk = 0;
+    uint32_t nan_lane = 0;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const uint32_t id = lane + 64u * j;
-        uint32_t key = 0;
+        Key key = 0;
         if (id < n0) {
             const uint32_t t = s.leaf_t[id];
             const double gj = s.gain[t];
             const uint32_t m = s.meta[t];
-            key = replay_key<IDB>(gj, m, id);
+            key = key_of(gj, m, id);
             nan_lane += (m & 1u) && gj != gj ? 1u : 0u;
         }
         s.key[id] = key;
@@ -2660,17 +2705,18 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
                 break;
             }
         }
-        const uint32_t best = wave_max_u32(lk);
+        const Key best = wave_max_key(lk);
         if (best == 0u) {
             done = true;
             break;
         }
-        uint32_t x = IDM - (best & IDM);
+        uint32_t x = static_cast<uint32_t>(IDM - (best & IDM));
         {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
-            const uint32_t bp = best >> IDB, lw = x & 63u;
+            const Key bp = best >> IDB;
+            const uint32_t lw = x & 63u;
             bool other = lane != lw && (lk >> IDB) == bp;
             if (lane < static_cast<uint32_t>(NPL)) {  // the winner's lane's keys (0 past the leaves)
-                const uint32_t kk = s.key[lw + 64u * lane];
+                const Key kk = s.key[lw + 64u * lane];
                 other = other || ((kk >> IDB) == bp && kk != best);
             }
             if (__ballot(other)) {
@@ -2700,7 +2746,7 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         const uint32_t kid = (m >> 3) - 1u;
         const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
         const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
-        const uint32_t k0 = replay_key<IDB>(g0, m0, x), k1 = replay_key<IDB>(g1, m1, n);
+        const Key k0 = key_of(g0, m0, x), k1 = key_of(g1, m1, n);
         // leaf x becomes the left child, leaf n the right one, both under node n - 1
         const int32_t node = static_cast<int32_t>(n) - 1;
         if (lane == 0) {
@@ -2722,8 +2768,8 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
         nan_leaves += ((m0 & 1u) && g0 != g0 ? 1u : 0u) + ((m1 & 1u) && g1 != g1 ? 1u : 0u);
         // the lanes' largest keys: x's lane (its largest was x's old key) from its keys, n's lane takes k1 as well
         const uint32_t lx = x & 63u, ln = n & 63u;
-        const uint32_t kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : 0u;
-        const uint32_t mx = wave_max_u32(kk);
+        const Key kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : Key{0};
+        const Key mx = wave_max_key(kk);
         if (lane == lx) lk = mx;
         else if (lane == ln) lk = k1 > lk ? k1 : lk;
         ++nc;
