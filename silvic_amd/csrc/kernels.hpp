@@ -2611,6 +2611,7 @@ struct AdvShared {
     uint64_t skey[JMAX];                  // select_top: the selected candidates' keys
     uint16_t scand[JMAX];                 // and leaves
     uint32_t ncand, ncommit, n, blocker, done, njobs, band, above, nsel, neligible;
+    uint32_t nnan;                        // committed leaves whose best gain is NaN (replay_lds)
 };
 
 __device__ __forceinline__ uint32_t key_meta(const TKey &k) {
@@ -2640,6 +2641,13 @@ __device__ __forceinline__ uint64_t replay_key64(double gain, uint32_t meta, uin
     return (p << 11) | (2047u - id);
 }
 
+// replay_lds's key of a leaf, in the width of the key array (Key)
+template <class Key>
+__device__ __forceinline__ Key leaf_key(double gain, uint32_t meta, uint32_t id) {
+    if constexpr (sizeof(Key) == 8) return replay_key64(gain, meta, id);
+    else return replay_key<11>(gain, meta, id);
+}
+
 // The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave. Lane l owns committed
 // leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves); their state is in LDS (speculative leaf, node above,
 // left and changed flags, and the replay key in s.key) and only the lane's largest key is in a register. A commit is
@@ -2656,32 +2664,20 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     constexpr uint64_t IDM = (1u << IDB) - 1u;
     using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
     constexpr bool K64 = sizeof(Key) == 8;
-    auto key_of = [](double gain, uint32_t meta, uint32_t id) -> Key {
-        if constexpr (K64) return replay_key64(gain, meta, id);
-        else return replay_key<IDB>(gain, meta, id);
-    };
+    auto key_of = [](double gain, uint32_t meta, uint32_t id) -> Key { return leaf_key<Key>(gain, meta, id); };
     auto wave_max_key = [](Key v) -> Key {
         if constexpr (K64) return wave_max_u64(v);
         else return wave_max_u32(v);
     };
     const uint32_t lane = threadIdx.x & 63u;
+    // the keys (0 past the committed leaves) and the NaN count were made by the whole block (advance)
     Key lk = 0;
-    uint32_t nan_lane = 0;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
-        const uint32_t id = lane + 64u * j;
-        Key key = 0;
-        if (id < n0) {
-            const uint32_t t = s.leaf_t[id];
-            const double gj = s.gain[t];
-            const uint32_t m = s.meta[t];
-            key = key_of(gj, m, id);
-            nan_lane += (m & 1u) && gj != gj ? 1u : 0u;
-        }
-        s.key[id] = key;
+        const Key key = s.key[lane + 64u * j];
         lk = key > lk ? key : lk;
     }
-    uint32_t nan_leaves = wave_total(nan_lane);
+    uint32_t nan_leaves = s.nnan;
     uint32_t n = n0, nc = 0, blocker = 0;
     bool done = false;
     for (;;) {
@@ -3251,8 +3247,27 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         s.is_left[id] = g.leaf_left[id];
         s.touched[id] = 0;
     }
-    if (tid == 0) s.ncand = 0;
+    if (tid == 0) {
+        s.ncand = 0;
+        s.nnan = 0;
+    }
     __syncthreads();
+    // the replay keys of the committed leaves for replay_lds (trees of more than 128 leaves), by the whole block
+    if (MAXL > LEAVES_SMALL || L > 128) {
+        using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
+        for (uint32_t id = tid; id < MAXL; id += nt) {
+            Key key = 0;
+            if (id < n0) {
+                const uint32_t t = s.leaf_t[id];
+                const double gj = s.gain[t];
+                const uint32_t m = s.meta[t];
+                key = leaf_key<Key>(gj, m, id);
+                if ((m & 1u) && gj != gj) atomicAdd(&s.nnan, 1u);
+            }
+            s.key[id] = key;
+        }
+        __syncthreads();
+    }
 
     // -- the replay, one wave, with as few leaves per lane as the tree needs
     if (tid < 64) {
