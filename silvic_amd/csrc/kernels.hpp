@@ -3300,7 +3300,10 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     const uint32_t blocker = s.blocker;
     frontier_bounds<MAXL>(s, ntent, n);
     const uint32_t R = L - n;  // splits left, this step's blocker included
-    const uint32_t cut = pool_threshold<MAXL>(s, ntent, R);
+    // The pool holds the candidates, the blocker and the expanded leaves not yet committed (pending0 - nc). With
+    // R >= that last count + JMAX, fewer than R of them lie above the (JMAX - 1)-th highest candidate's bound, so the
+    // R-th highest bound cannot leave out any of the candidates a step takes: no selection is needed.
+    const uint32_t cut = R >= pending0 - nc + JMAX ? 0u : pool_threshold<MAXL>(s, ntent, R);
     if (tid == 0) s.neligible = 0;
     __syncthreads();
     const float2 *bw = reinterpret_cast<const float2 *>(s.gain);
