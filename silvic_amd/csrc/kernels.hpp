@@ -2599,6 +2599,10 @@ struct AdvShared {
     // committed leaf's replay key (0: none): replay_key64 in trees of more than 512 leaves, where 32-bit keys meet
     // the winner's gain prefix often; replay_key<11> in the others, where its u32 wave max is the cheaper
     std::conditional_t<(MAXL > LEAVES_SMALL), uint64_t, uint32_t> key[MAXL];
+    // trees of up to 512 leaves (replay_reg): an expanded speculative leaf's children, left then right, as their
+    // replay_key<11> without the id bits (0: no key), bit 0 set when the child has a split and a NaN gain
+    uint2 crec[MAXL > LEAVES_SMALL ? 1 : TCAP];
+    uint32_t leaf_m[MAXL > LEAVES_SMALL ? MAXL : 1];  // trees of more than 512 leaves: committed leaf's s.meta word
     uint16_t ck[MAXL];                    // commit c: the speculative leaf split (node n0 - 1 + c)
     uint16_t cx[MAXL];                    // commit c: the leaf id split
     int16_t cpn[MAXL];                    // commit c: the split leaf's node above
@@ -2650,18 +2654,20 @@ __device__ __forceinline__ Key leaf_key(double gain, uint32_t meta, uint32_t id)
 
 // The replay of advance (learner.rs:158-163 with best_leaf, learner.rs:418-429) on one wave. Lane l owns committed
 // leaves l, l + 64, ... (NPL of them, NPL * 64 >= num_leaves); their state is in LDS (speculative leaf, node above,
-// left and changed flags, and the replay key in s.key) and only the lane's largest key is in a register. A commit is
-// one wave max of those (the reference's argmax only matters while the best gain is positive: otherwise the tree
-// stops), with an exact f64 argmax only when two leaves share the winner's gain prefix: a lane other than the
-// winner's holds such a key exactly when its largest key has the prefix, and the winner's own other keys, like its
-// new largest key after the commit, are read from s.key by NPL lanes at once. The rule that the first leaf with a
-// split decides when its gain is NaN takes a wave minimum, only while some leaf has a NaN gain (they are counted).
-// Leaves the commits, the committed-leaf arrays and the outcome in `s`.
+// its state word, left and changed flags, and the replay key in s.key) and only the lane's largest key is in a
+// register. A commit is one wave max of those (the reference's argmax only matters while the best gain is positive:
+// otherwise the tree stops), with an exact f64 argmax only when two leaves share the winner's gain prefix: a lane
+// other than the winner's holds such a key exactly when its largest key has the prefix, and the winner's own keys
+// are read from s.key by NPL lanes at once, with the winner's state, and serve again for that lane's new largest key
+// after the commit. So a commit waits on two LDS reads: those, then its children's gains and state words. The rule
+// that the first leaf with a split decides when its gain is NaN takes a wave minimum, only while some leaf has a NaN
+// gain (they are counted). Leaves the commits, the committed-leaf arrays and the outcome in `s`.
 template <int NPL, typename S>
 __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     constexpr int IDB = 11;
     static_assert(NPL * 64 <= (1 << IDB) && NPL * 64 <= static_cast<int>(GROW_MAX_LEAVES) && NPL <= 64, "leaf ids fit");
     constexpr uint64_t IDM = (1u << IDB) - 1u;
+    static_assert(sizeof(s.leaf_m) >= sizeof(uint32_t) * NPL * 64, "the committed leaves' state words");
     using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
     constexpr bool K64 = sizeof(Key) == 8;
     auto key_of = [](double gain, uint32_t meta, uint32_t id) -> Key { return leaf_key<Key>(gain, meta, id); };
@@ -2707,14 +2713,14 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             break;
         }
         uint32_t x = static_cast<uint32_t>(IDM - (best & IDM));
+        // the winner's lane's keys (0 past the leaves) and the winner's state, read together
+        Key kk = lane < static_cast<uint32_t>(NPL) ? s.key[(x & 63u) + 64u * lane] : Key{0};
+        uint32_t k = s.leaf_t[x], m = s.leaf_m[x];
+        int32_t pn = s.pnode[x];
+        uint32_t xl = s.is_left[x];
         {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
             const Key bp = best >> IDB;
-            const uint32_t lw = x & 63u;
-            bool other = lane != lw && (lk >> IDB) == bp;
-            if (lane < static_cast<uint32_t>(NPL)) {  // the winner's lane's keys (0 past the leaves)
-                const Key kk = s.key[lw + 64u * lane];
-                other = other || ((kk >> IDB) == bp && kk != best);
-            }
+            const bool other = (lane != (x & 63u) && (lk >> IDB) == bp) || ((kk >> IDB) == bp && kk != best);
             if (__ballot(other)) {
                 double kg = 0.0;
                 int ki = -1;
@@ -2729,16 +2735,17 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
                 }
                 wave_argmax(kg, ki);
                 x = static_cast<uint32_t>(ki);
+                kk = lane < static_cast<uint32_t>(NPL) ? s.key[(x & 63u) + 64u * lane] : Key{0};
+                k = s.leaf_t[x];
+                m = s.leaf_m[x];
+                pn = s.pnode[x];
+                xl = s.is_left[x];
             }
         }
-        const uint32_t k = s.leaf_t[x];  // x is wave-uniform: broadcast reads
-        const uint32_t m = s.meta[k];
         if (((m >> 1) & 3u) != T_EXPANDED) {
             blocker = k;
             break;
         }
-        const int32_t pn = s.pnode[x];
-        const uint32_t xl = s.is_left[x];
         const uint32_t kid = (m >> 3) - 1u;
         const double g0 = s.gain[kid], g1 = s.gain[kid + 1];
         const uint32_t m0 = s.meta[kid], m1 = s.meta[kid + 1];
@@ -2751,23 +2758,160 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
             s.cpn[nc] = static_cast<int16_t>(pn);
             s.cleft[nc] = static_cast<uint8_t>(xl);
             s.leaf_t[x] = static_cast<uint16_t>(kid);
+            s.leaf_m[x] = m0;
             s.pnode[x] = static_cast<int16_t>(node);
             s.is_left[x] = 1;
             s.touched[x] = 1;
             s.key[x] = k0;
             s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
+            s.leaf_m[n] = m1;
             s.pnode[n] = static_cast<int16_t>(node);
             s.is_left[n] = 0;
             s.touched[n] = 1;
             s.key[n] = k1;
         }
         nan_leaves += ((m0 & 1u) && g0 != g0 ? 1u : 0u) + ((m1 & 1u) && g1 != g1 ? 1u : 0u);
-        // the lanes' largest keys: x's lane (its largest was x's old key) from its keys, n's lane takes k1 as well
+        // the lanes' largest keys: x's lane (its largest was x's old key) from its keys as read, with x's key now k0
+        // (and n's k1 when n is in that lane); n's lane takes k1 as well
         const uint32_t lx = x & 63u, ln = n & 63u;
-        const Key kk = lane < static_cast<uint32_t>(NPL) ? s.key[lx + 64u * lane] : Key{0};
-        const Key mx = wave_max_key(kk);
+        Key kv = lane == (x >> 6) ? k0 : kk;
+        kv = ln == lx && lane == (n >> 6) ? k1 : kv;
+        const Key mx = wave_max_key(kv);
         if (lane == lx) lk = mx;
         else if (lane == ln) lk = k1 > lk ? k1 : lk;
+        ++nc;
+        ++n;
+    }
+    if (lane == 0) {
+        s.ncommit = nc;
+        s.n = n;
+        s.done = done ? 1u : 0u;
+        s.blocker = blocker;
+    }
+}
+
+// replay_lds for trees of up to 512 leaves (NPL 4 or 8) with the replay keys and speculative leaves of lane l's
+// committed leaves (l, l + 64, ...) in its registers: the test for another leaf with the winner's gain prefix
+// needs no LDS, the winner's speculative leaf is a read of its lane, and its children's keys come from one read
+// of s.crec (their key prefixes, made by the whole block), so a commit waits on one LDS read (that record with the
+// state word) where replay_lds waits on five. Lane 0 keeps the committed-leaf arrays in LDS up to date for
+// apply_commits and the NaN rule, which reads them; s.key is left as the block made it.
+template <int NPL, typename S>
+__device__ __forceinline__ void replay_reg(S &s, uint32_t n0, uint32_t L) {
+    constexpr int IDB = 11;
+    static_assert(NPL * 64 <= static_cast<int>(LEAVES_SMALL) && sizeof(s.key[0]) == 4, "u32 keys of 512 leaves at most");
+    constexpr uint32_t IDM = (1u << IDB) - 1u;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t rk[NPL], rt[NPL], lk = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {  // keys are 0 past the committed leaves, whose speculative leaf is then unused
+        const uint32_t id = lane + 64u * j;
+        rk[j] = s.key[id];
+        rt[j] = s.leaf_t[id];
+        lk = rk[j] > lk ? rk[j] : lk;
+    }
+    uint32_t nan_leaves = s.nnan;
+    uint32_t n = n0, nc = 0, blocker = 0;
+    bool done = false;
+    for (;;) {
+        if (n >= L) {
+            done = true;
+            break;
+        }
+        // best_leaf: the first leaf with a split decides when its gain is NaN (nothing beats NaN under `>`)
+        if (nan_leaves) {
+            int lfirst = 1 << 30;
+            for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is the one kept
+                const uint32_t id = lane + 64u * j;
+                if (id >= n) continue;
+                const uint32_t t = s.leaf_t[id];
+                const double gj = s.gain[t];
+                if (s.meta[t] & 1u) lfirst = 2 * static_cast<int>(id) + (gj != gj ? 1 : 0);
+            }
+            const int first = wave_min_i32(lfirst);
+            if (first < (1 << 30) && (first & 1)) {
+                done = true;
+                break;
+            }
+        }
+        const uint32_t best = wave_max_u32(lk);
+        if (best == 0u) {
+            done = true;
+            break;
+        }
+        uint32_t x = IDM - (best & IDM);
+        {  // another leaf with the winner's gain prefix: the exact gains decide (then the lower id)
+            const uint32_t bp = best >> IDB;
+            bool other = false;
+            if (lane == (x & 63u)) {
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) other = other || (rk[j] != best && (rk[j] >> IDB) == bp);
+            } else {
+                other = (lk >> IDB) == bp;
+            }
+            if (__ballot(other)) {
+                double kg = 0.0;
+                int ki = -1;
+#pragma unroll
+                for (int j = NPL - 1; j >= 0; --j) {  // descending, so the lowest id is kept on equal gains
+                    if ((rk[j] >> IDB) != bp) continue;
+                    const double gj = s.gain[rt[j]];
+                    if (ki < 0 || gj >= kg) {
+                        kg = gj;
+                        ki = static_cast<int>(lane + 64u * j);
+                    }
+                }
+                wave_argmax(kg, ki);
+                x = static_cast<uint32_t>(ki);
+            }
+        }
+        const uint32_t jx = x >> 6, lx = x & 63u, jn = n >> 6, ln = n & 63u;
+        uint32_t tv = rt[0];
+#pragma unroll
+        for (int j = 1; j < NPL; ++j) tv = jx == static_cast<uint32_t>(j) ? rt[j] : tv;
+        const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(tv), static_cast<int>(lx)));
+        const uint32_t m = s.meta[k];
+        const uint2 c = s.crec[k];
+        const int32_t pn = s.pnode[x];
+        const uint32_t xl = s.is_left[x];
+        if (((m >> 1) & 3u) != T_EXPANDED) {
+            blocker = k;
+            break;
+        }
+        const uint32_t kid = (m >> 3) - 1u;
+        const uint32_t k0 = (c.x >> IDB) ? ((c.x & ~IDM) | (IDM - x)) : 0u;
+        const uint32_t k1 = (c.y >> IDB) ? ((c.y & ~IDM) | (IDM - n)) : 0u;
+        // leaf x becomes the left child, leaf n the right one, both under node n - 1
+        const int32_t node = static_cast<int32_t>(n) - 1;
+        if (lane == 0) {
+            s.ck[nc] = static_cast<uint16_t>(k);
+            s.cx[nc] = static_cast<uint16_t>(x);
+            s.cpn[nc] = static_cast<int16_t>(pn);
+            s.cleft[nc] = static_cast<uint8_t>(xl);
+            s.leaf_t[x] = static_cast<uint16_t>(kid);
+            s.pnode[x] = static_cast<int16_t>(node);
+            s.is_left[x] = 1;
+            s.touched[x] = 1;
+            s.leaf_t[n] = static_cast<uint16_t>(kid + 1);
+            s.pnode[n] = static_cast<int16_t>(node);
+            s.is_left[n] = 0;
+            s.touched[n] = 1;
+        }
+        nan_leaves += (c.x & 1u) + (c.y & 1u);
+        uint32_t nk = 0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            if (jx == static_cast<uint32_t>(j) && lane == lx) {
+                rk[j] = k0;
+                rt[j] = kid;
+            }
+            if (jn == static_cast<uint32_t>(j) && lane == ln) {
+                rk[j] = k1;
+                rt[j] = kid + 1u;
+            }
+            nk = rk[j] > nk ? rk[j] : nk;
+        }
+        lk = nk;
         ++nc;
         ++n;
     }
@@ -3252,7 +3396,8 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         s.nnan = 0;
     }
     __syncthreads();
-    // the replay keys of the committed leaves for replay_lds (trees of more than 128 leaves), by the whole block
+    // the replay keys of the committed leaves for replay_lds and replay_reg (trees of more than 128 leaves), by the
+    // whole block
     if (MAXL > LEAVES_SMALL || L > 128) {
         using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
         for (uint32_t id = tid; id < MAXL; id += nt) {
@@ -3263,8 +3408,24 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
                 const uint32_t m = s.meta[t];
                 key = leaf_key<Key>(gj, m, id);
                 if ((m & 1u) && gj != gj) atomicAdd(&s.nnan, 1u);
+                if constexpr (MAXL > LEAVES_SMALL) s.leaf_m[id] = m;
             }
             s.key[id] = key;
+        }
+        if constexpr (MAXL <= LEAVES_SMALL) {  // replay_reg's records of the expanded speculative leaves
+            for (uint32_t k = tid; k < ntent; k += nt) {
+                const uint32_t m = s.meta[k];
+                if (((m >> 1) & 3u) != T_EXPANDED) continue;
+                const uint32_t kid = (m >> 3) - 1u;
+                uint32_t c[2];
+#pragma unroll
+                for (uint32_t i = 0; i < 2; ++i) {
+                    const double gc = s.gain[kid + i];
+                    const uint32_t mc = s.meta[kid + i];
+                    c[i] = (replay_key<11>(gc, mc, 0) & ~2047u) | ((mc & 1u) && gc != gc ? 1u : 0u);
+                }
+                s.crec[k] = make_uint2(c[0], c[1]);
+            }
         }
         __syncthreads();
     }
@@ -3274,8 +3435,8 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
         if constexpr (MAXL <= LEAVES_SMALL) {
             if (L <= 64) replay<1>(s, n0, L);
             else if (L <= 128) replay<2>(s, n0, L);
-            else if (L <= 256) replay_lds<4>(s, n0, L);
-            else replay_lds<LEAVES_SMALL / 64>(s, n0, L);
+            else if (L <= 256) replay_reg<4>(s, n0, L);
+            else replay_reg<LEAVES_SMALL / 64>(s, n0, L);
         } else {
             if (L <= 1024) replay_lds<16>(s, n0, L);
             else replay_lds<MAXL / 64>(s, n0, L);
