@@ -2068,6 +2068,7 @@ struct Context {
         g.sh = spec.hess_scale;
         g.dsc = grow_dsc;
         g.target_groups = step_target;
+        g.jcap = grow_jcap(spec.num_leaves);
         g.ncg = ncg;
         g.nsg = nsg;
         g.flush_rows = flush_rows();
@@ -2338,7 +2339,9 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                                 slab_col_bins.p + sl.col_bins_off, slab_pos_word.p + sl.pos_off, sl.row_bytes() / 4, k1_groups(), packed.p,
                                 train.col.p, col16, rows, part.p, part2.p, tile_status.p, d_plans.p + parity, g.ctl, flush_rows(),
                                 si == 0 ? 1u : 0u, g.tile_cap, codes ? codes0.p : nullptr, codes ? codes1.p : nullptr};
-                    const uint32_t grid = k1_groups() * static_cast<uint32_t>(sj - si);
+                    // a launch of one slab stops at the workgroups a step of jcap jobs can use (the plan's rounding
+                    // takes at most one more a job); one of several slabs takes k1 a slab
+                    const uint32_t grid = sj - si == 1 ? step_target + g.jcap : k1_groups() * static_cast<uint32_t>(sj - si);
                     // the instance with carried gradient codes when the units fit them (never with separate counters)
 #define SROCM_STEP_CASE(id, W, WIDE, PACK, DP)                                                                    \
     case id:                                                                                                      \
@@ -2389,8 +2392,8 @@ void Context::grow(const srocm_grow_spec &spec, HostTree &tree, std::vector<sroc
                     launch_check("k_step_cat");
                 }
                 SelectArgs sa2{fin_counts.p, d_plans.p + parity, d_plans.p + (parity ^ 1u)};
-                if (L <= LEAVES_SMALL) k_step_select<LEAVES_SMALL><<<JMAX, 512, 0, stream>>>(g, sa2);
-                else k_step_select<GROW_MAX_LEAVES><<<JMAX, 512, 0, stream>>>(g, sa2);
+                if (L <= LEAVES_SMALL) k_step_select<LEAVES_SMALL><<<g.jcap, 512, 0, stream>>>(g, sa2);
+                else k_step_select<GROW_MAX_LEAVES><<<g.jcap, 512, 0, stream>>>(g, sa2);
                 launch_check("k_step_select");
             }
             if (after_steps) {

@@ -2274,7 +2274,10 @@ __device__ __forceinline__ float wave_total_f32(float v) {
     return v;
 }
 
-constexpr uint32_t JMAX = 32;              // leaves expanded by one step at most
+constexpr uint32_t JMAX = 64;              // leaves expanded by one step at most (the plan's capacity)
+// a step's jobs at most (GrowState::jcap): trees of up to LEAVES_SMALL leaves take 32, where a longer speculation
+// mostly expands leaves the tree commits late or never; larger trees take JMAX, their steps being bound by the job count
+__host__ __device__ constexpr uint32_t grow_jcap(uint32_t num_leaves) { return num_leaves <= LEAVES_SMALL ? 32u : JMAX; }
 constexpr uint32_t SPEC_FEW = 8;           // at most this many: picked by repeated wave maxima (top_few)
 constexpr uint32_t GROW_MAX_LEAVES = 2048;  // num_leaves of a device-grown tree at most
 // Speculative leaves of a tree of num_leaves: 4 per leaf up to 512 leaves, then 2 per further leaf (the expansions
@@ -2364,13 +2367,18 @@ struct StepPlan {
 };
 
 // The job whose range of work holds x: the last whose first element (bases[k]) is at or below it. The bases are read
-// as one unrolled run, so the search is one round of loads.
-__device__ __forceinline__ uint32_t job_of(const uint32_t (&bases)[JMAX], uint32_t njobs, uint32_t x) {
+// as one unrolled run, so the search is one round of loads: of the first 32 when the step has no more jobs (the
+// whole run cost the latency-bound k_step_reduce 15% in such steps).
+template <uint32_t N>
+__device__ __forceinline__ uint32_t job_search(const uint32_t (&bases)[JMAX], uint32_t njobs, uint32_t x) {
     uint32_t j = 0;
 #pragma unroll
-    for (uint32_t k = 1; k < JMAX; ++k)
+    for (uint32_t k = 1; k < N; ++k)
         if (k < njobs && x >= bases[k]) j = k;
     return j;
+}
+__device__ __forceinline__ uint32_t job_of(const uint32_t (&bases)[JMAX], uint32_t njobs, uint32_t x) {
+    return njobs <= 32u ? job_search<32>(bases, njobs, x) : job_search<JMAX>(bases, njobs, x);
 }
 
 struct GrowCtl {
@@ -2416,6 +2424,7 @@ struct GrowState {
     double sg, sh;
     const struct DevScales *dsc;  // when set, the scales are these (made on the device), not sg and sh
     uint32_t target_groups;   // k_step_rows workgroups a step is spread over
+    uint32_t jcap;            // jobs a step at most: grow_jcap(num_leaves)
     uint32_t ncg;             // column groups of k_step_reduce
     uint32_t nsg;             // scan units of k_step_scan (a wave per unit and child)
     uint32_t flush_rows;      // rows a packed 16/16 LDS word can take
@@ -3462,9 +3471,9 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     frontier_bounds<MAXL>(s, ntent, n);
     const uint32_t R = L - n;  // splits left, this step's blocker included
     // The pool holds the candidates, the blocker and the expanded leaves not yet committed (pending0 - nc). With
-    // R >= that last count + JMAX, fewer than R of them lie above the (JMAX - 1)-th highest candidate's bound, so the
+    // R >= that last count + jcap, fewer than R of them lie above the (jcap - 1)-th highest candidate's bound, so the
     // R-th highest bound cannot leave out any of the candidates a step takes: no selection is needed.
-    const uint32_t cut = R >= pending0 - nc + JMAX ? 0u : pool_threshold<MAXL>(s, ntent, R);
+    const uint32_t cut = R >= pending0 - nc + g.jcap ? 0u : pool_threshold<MAXL>(s, ntent, R);
     if (tid == 0) s.neligible = 0;
     __syncthreads();
     const float2 *bw = reinterpret_cast<const float2 *>(s.gain);
@@ -3485,10 +3494,10 @@ __device__ void advance(const GrowState &g, StepPlan &next, void *scratch) {
     __syncthreads();
     const uint32_t ncand = s.ncand;
     const uint32_t pending = pending0 - nc;
-    // the candidates among the R leaves of highest bound (pool_threshold), at most JMAX - 1; being the highest keys,
+    // the candidates among the R leaves of highest bound (pool_threshold), at most jcap - 1; being the highest keys,
     // the ones the selection below takes are exactly those
     uint32_t spec = s.neligible;
-    if (spec > JMAX - 1) spec = JMAX - 1;
+    if (spec > g.jcap - 1) spec = g.jcap - 1;
     // room for this step and every later blocker (each commits, so at most R of them in all)
     const uint32_t free_t = g.tcap - ntent, free_s = g.nslots - slot0;
     const uint32_t room_t = free_t >= 2 * R ? (free_t - 2 * R) / 2 : 0u, room_s = free_s >= R ? free_s - R : 0u;
@@ -4828,7 +4837,7 @@ __global__ __launch_bounds__(256) void k_step_cat(GrowState g, ScanStepArgs a) {
     }
 }
 
-// Block j selects both children of job j (job_select); the last block to finish runs advance. grid: JMAX blocks.
+// Block j selects both children of job j (job_select); the last block to finish runs advance. grid: jcap blocks.
 template <uint32_t MAXL>
 __global__ __launch_bounds__(512) void k_step_select(GrowState g, SelectArgs a) {
     __shared__ __align__(16) uint8_t scratch[sizeof(AdvShared<MAXL>)];
