@@ -1237,6 +1237,18 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
+// wave_max_u64 by the high words first: their u32 maximum, then the low word of the one lane holding it, or the low
+// words' maximum over the lanes holding it when several do (half the DPP work of wave_max_u64 when the high words
+// rarely tie). All lanes active.
+__device__ __forceinline__ uint64_t wave_max_u64_hi(uint64_t v) {
+    const uint32_t hi = static_cast<uint32_t>(v >> 32), lo = static_cast<uint32_t>(v);
+    const uint32_t mh = wave_max_u32(hi);
+    const unsigned long long at = __ballot(hi == mh);
+    const uint32_t ml = (at & (at - 1ull)) == 0ull
+                            ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), static_cast<int>(__builtin_ctzll(at))))
+                            : wave_max_u32(hi == mh ? lo : 0u);
+    return (static_cast<uint64_t>(mh) << 32) | ml;
+}
 
 // A feature candidate as held by lane `owner`, broadcast to the wave.
 __device__ __forceinline__ FeatCand readlane_cand(const FeatCand &c, uint32_t owner) {
@@ -2680,8 +2692,8 @@ __device__ __forceinline__ void replay_lds(S &s, uint32_t n0, uint32_t L) {
     using Key = std::remove_cv_t<std::remove_reference_t<decltype(s.key[0])>>;
     constexpr bool K64 = sizeof(Key) == 8;
     auto key_of = [](double gain, uint32_t meta, uint32_t id) -> Key { return leaf_key<Key>(gain, meta, id); };
-    auto wave_max_key = [](Key v) -> Key {
-        if constexpr (K64) return wave_max_u64(v);
+    auto wave_max_key = [](Key v) -> Key {  // 64-bit keys: two gains share the high word when within about 1e-6
+        if constexpr (K64) return wave_max_u64_hi(v);
         else return wave_max_u32(v);
     };
     const uint32_t lane = threadIdx.x & 63u;
