@@ -4139,11 +4139,22 @@ __device__ __forceinline__ void step_hist(int32_t *lds, const uint32_t *list, ui
 }
 
 // The one-byte gradient codes of a tree's root rows, beside their ids: codes[i] = packed_code(gh[part[i]]) for i in
-// [begin, begin + count). The split steps then move each code with its row.
+// [begin, begin + count). The split steps then move each code with its row. Four rows a thread, their loads issued
+// together (one row a thread waited on two dependent loads a row).
 __global__ void k_gh_codes(const uint32_t *__restrict__ part, const int32_t *__restrict__ gh, uint32_t begin,
                            uint32_t count, uint8_t *__restrict__ codes) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
-        codes[begin + i] = packed_code(gh[part[begin + i]]);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < count; i += 4u * stride) {
+        uint32_t r[4];
+        int32_t w[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) r[k] = i + k * stride < count ? part[begin + i + k * stride] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) w[k] = i + k * stride < count ? gh[r[k]] : 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k)
+            if (i + k * stride < count) codes[begin + i + k * stride] = packed_code(w[k]);
+    }
 }
 
 // The LDS words of a k_step_rows instance: the histogram (twice for separate counters) and a dense slab's spare row.
