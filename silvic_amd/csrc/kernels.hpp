@@ -935,12 +935,32 @@ __global__ __launch_bounds__(tl_threads<MAXL>()) void k_tree_leaves(TreeLeavesAr
     }
 }
 
-// scores[r] += the value of row r's leaf: the f32 add of k_add_tree, in row order.
+// scores[r] += the value of row r's leaf: the f32 add of k_add_tree, in row order. Four rows of the grid-stride loop
+// at once, their loads (then their leaves' values) issued together: one row an iteration waited on its loads and then
+// on its leaf's value (21.0 -> 18.4 us at 10M rows; the gradient kernels, bound by their f64 arithmetic, were slower
+// so).
 __global__ void k_add_leaf_values(const uint16_t *__restrict__ leaf_of, const float *__restrict__ leaf_values,
                                   float *__restrict__ scores, uint64_t rows, const uint32_t *gate) {
+    constexpr int RA = 4;
     if (gate && *gate == 0u) return;
-    for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < rows; r += (uint64_t)gridDim.x * blockDim.x)
-        scores[r] += leaf_values[leaf_of[r]];
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t r0 = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r0 < rows; r0 += RA * stride) {
+        uint32_t l[RA];
+        float s[RA], v[RA];
+#pragma unroll
+        for (int k = 0; k < RA; ++k) {
+            const uint64_t r = r0 + k * stride;
+            l[k] = r < rows ? leaf_of[r] : 0u;
+            s[k] = r < rows ? scores[r] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < RA; ++k) v[k] = r0 + k * stride < rows ? leaf_values[l[k]] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < RA; ++k) {
+            const uint64_t r = r0 + k * stride;
+            if (r < rows) scores[r] = s[k] + v[k];
+        }
+    }
 }
 
 // a -= b over n int64 values (a histogram slot minus another, learner.rs:365-367)
