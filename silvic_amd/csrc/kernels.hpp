@@ -4545,10 +4545,12 @@ struct ReduceStepArgs {
 };
 
 // The end of job j, by one block (learner.rs:294-352): both children's best splits from their per-feature
-// candidates (split.rs:866-880; half the block's waves a child, each over a share of the features, their bests then
-// merged: the (gain, feature) order is total, so any split of the features gives the same winner; every wave counts a
-// share of the job's evaluated features), then their leaves in the speculative tree and the job's leaf marked
-// expanded (thread 0). One wave a child took 2000 features in 32 rounds of dependent loads.
+// candidates (split.rs:866-880), then their leaves in the speculative tree and the job's leaf marked expanded (thread
+// 0). Up to 256 features, waves 0 and 1 take a child each while wave 2 counts the job's evaluated features; beyond,
+// half the block's waves take a child, each over a share of the features, and their bests are merged (the (gain,
+// feature) order is total, so any split of the features gives the same winner), every wave counting a share of the
+// evaluated features: one wave a child took 2000 features in 32 rounds of dependent loads, and the merge's extra
+// barrier costs small feature counts 1 us a step.
 __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
     __shared__ SplitOut s_out[2];
     __shared__ uint32_t s_used;
@@ -4571,58 +4573,97 @@ __device__ void job_select(const GrowState &g, const JobPlan &J, uint32_t j) {
     const int32_t depth = g.tl[J.t].depth + 1;
     const int64_t min_pair = 2 * g.cfg.min_data_in_leaf;
     const bool searched = J.hist && depth_allows(g, depth) && (left >= min_pair || right >= min_pair);
-    // the job's evaluated features (learner.rs:262-265), for the byte count, a share a wave
-    const uint32_t nw = blockDim.x >> 6, wpc = nw >= 4u ? (nw >> 1 < 8u ? nw >> 1 : 8u) : 1u;  // waves a child
-    if (threadIdx.x == 0) s_used = 0;
-    __syncthreads();
-    {
-        const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
-        uint32_t used = 0;
-        for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) used += g.mask[f] != 0 && prow[f] != 0 ? 1u : 0u;
-        used = wave_total(used);
-        if (lane == 0 && used) atomicAdd(&s_used, used);
-    }
-    // waves c wpc .. c wpc + wpc - 1: child c's best over features sub 64 + lane, + 64 wpc, ...
-    if (wave < 2u * wpc && searched) {
-        const uint32_t ch = wave / wpc, sub = wave - ch * wpc;
-        const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
-        uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
-        double best = 0.0;
-        int bf = -1;
-        for (uint32_t f = sub * 64u + lane; f < g.nf; f += 64u * wpc) {
-            const FeatCand &c = cands[f];
-            row[f] = static_cast<uint8_t>(c.splittable);
-            if (!c.found) continue;
-            const double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
-            if (cand_better(gv, static_cast<int>(f), best, bf)) {
-                best = gv;
-                bf = static_cast<int>(f);
-            }
-        }
-        wave_best(best, bf);
-        if (lane == 0) {
-            s_wb[ch][sub] = best;
-            s_wf[ch][sub] = bf;
-        }
-    }
-    __syncthreads();
-    // waves 0 and 1: the left and the right child's winner over its waves' bests
-    if (wave < 2) {
-        const uint32_t ch = wave;
-        SplitOut out = {};
-        if (searched) {
-            double wb = lane < wpc ? s_wb[ch][lane] : 0.0;
-            int wf = lane < wpc ? s_wf[ch][lane] : -1;
-            wave_best(wb, wf);
-            if (wf >= 0) {  // the winner, read once more where the scans left it
+    const uint32_t nw = blockDim.x >> 6;
+    if (g.nf <= 256u || nw < 4u) {  // uniform
+        // waves 0 and 1: the best split of the left and the right child; wave 2: the job's evaluated features
+        // (learner.rs:262-265), for the byte count
+        if (wave == 2) {
+            const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
+            uint32_t used = 0;
+            for (uint32_t f = lane; f < g.nf; f += 64u)
+                used += static_cast<uint32_t>(__popcll(__ballot(g.mask[f] != 0 && prow[f] != 0)));
+            if (lane == 0) s_used = used;
+        } else if (wave < 2) {
+            const uint32_t ch = wave;
+            SplitOut out = {};
+            if (searched) {
                 const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
-                const int64_t cnt = ch == 0 ? left : right;
-                out = split_out(cands[wf], wf, make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
+                double best = 0.0;
+                int bf = -1;
+                for (uint32_t f = lane; f < g.nf; f += 64u) {
+                    const FeatCand &c = cands[f];
+                    row[f] = static_cast<uint8_t>(c.splittable);
+                    if (!c.found) continue;
+                    const double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+                    if (cand_better(gv, static_cast<int>(f), best, bf)) {
+                        best = gv;
+                        bf = static_cast<int>(f);
+                    }
+                }
+                wave_best(best, bf);
+                if (bf >= 0) {  // the winner, read once more where the scans left it
+                    const int64_t cnt = ch == 0 ? left : right;
+                    out = split_out(cands[bf], bf, make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                }
+            }
+            if (lane == 0) s_out[ch] = out;
+        }
+        __syncthreads();
+    } else {
+        // the job's evaluated features (learner.rs:262-265), for the byte count, a share a wave
+        const uint32_t wpc = nw >> 1 < 8u ? nw >> 1 : 8u;  // waves a child
+        if (threadIdx.x == 0) s_used = 0;
+        __syncthreads();
+        {
+            const uint8_t *prow = g.splittable + static_cast<size_t>(J.t) * g.nf;
+            uint32_t used = 0;
+            for (uint32_t f = threadIdx.x; f < g.nf; f += blockDim.x) used += g.mask[f] != 0 && prow[f] != 0 ? 1u : 0u;
+            used = wave_total(used);
+            if (lane == 0 && used) atomicAdd(&s_used, used);
+        }
+        // waves c wpc .. c wpc + wpc - 1: child c's best over features sub 64 + lane, + 64 wpc, ...
+        if (wave < 2u * wpc && searched) {
+            const uint32_t ch = wave / wpc, sub = wave - ch * wpc;
+            const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
+            uint8_t *row = g.splittable + static_cast<size_t>(kid + static_cast<int32_t>(ch)) * g.nf;
+            double best = 0.0;
+            int bf = -1;
+            for (uint32_t f = sub * 64u + lane; f < g.nf; f += 64u * wpc) {
+                const FeatCand &c = cands[f];
+                row[f] = static_cast<uint8_t>(c.splittable);
+                if (!c.found) continue;
+                const double gv = (c.gain != c.gain) ? -__builtin_inf() : c.gain;
+                if (cand_better(gv, static_cast<int>(f), best, bf)) {
+                    best = gv;
+                    bf = static_cast<int>(f);
+                }
+            }
+            wave_best(best, bf);
+            if (lane == 0) {
+                s_wb[ch][sub] = best;
+                s_wf[ch][sub] = bf;
             }
         }
-        if (lane == 0) s_out[ch] = out;
+        __syncthreads();
+        // waves 0 and 1: the left and the right child's winner over its waves' bests
+        if (wave < 2) {
+            const uint32_t ch = wave;
+            SplitOut out = {};
+            if (searched) {
+                double wb = lane < wpc ? s_wb[ch][lane] : 0.0;
+                int wf = lane < wpc ? s_wf[ch][lane] : -1;
+                wave_best(wb, wf);
+                if (wf >= 0) {  // the winner, read once more where the scans left it
+                    const FeatCand *cands = g.cands + (static_cast<size_t>(j) * 2 + ch) * g.nf;
+                    const int64_t cnt = ch == 0 ? left : right;
+                    out = split_out(cands[wf], wf, make_ctx(g.cfg, grow_sg(g), grow_sh(g), J.child_ug[ch], J.child_uh[ch], cnt), g.cfg);
+                }
+            }
+            if (lane == 0) s_out[ch] = out;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     // the children's best splits, copied a dword a thread (no child-sized copy through one thread's stack)
     static_assert(sizeof(SplitOut) % 4 == 0 && sizeof(SplitOut) / 4 <= 64, "a split copies in one wave");
     if (threadIdx.x < 128) {
